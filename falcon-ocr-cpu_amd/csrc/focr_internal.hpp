@@ -1,0 +1,129 @@
+// Internal declarations of the focr_hip library (gfx950 only).
+//
+// Build flags (falcon-ocr-cpu_amd/Makefile): -ffp-contract=off, so every fused
+// multiply-add in device code is an explicit __builtin_fmaf and every other
+// product/sum rounds on its own, as the reference's Rust arithmetic does;
+// IEEE division and square root (__fdiv_rn, __fsqrt_rn); FP32 denormals kept.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "../../include/focr_hip.h"
+
+namespace focr {
+
+// ---- errors --------------------------------------------------------------
+int set_error(int code, const std::string &message);
+#define FOCR_HIP_CHECK(expr)                                                              \
+  do {                                                                                    \
+    hipError_t focr_err_ = (expr);                                                        \
+    if (focr_err_ != hipSuccess)                                                          \
+      return ::focr::set_error(FOCR_E_HIP, std::string(#expr) + ": " +                    \
+                                               hipGetErrorString(focr_err_));             \
+  } while (0)
+#define FOCR_REQUIRE(cond, code, msg)                                                     \
+  do {                                                                                    \
+    if (!(cond)) return ::focr::set_error((code), (msg));                                 \
+  } while (0)
+
+// ---- context ---------------------------------------------------------------
+struct Ctx {
+  int device = 0;
+  hipStream_t own = nullptr;
+  hipStream_t stream = nullptr;  // own, or a caller's stream
+  // Scratch owned by the context, grown on demand (INT16 activation codes).
+  void *scratch = nullptr;
+  size_t scratch_bytes = 0;
+  uint32_t *argmax_dev = nullptr;  // [2 * rows] result words for focr_argmax
+  size_t argmax_rows = 0;
+};
+
+// Grows the context scratch to at least `bytes` (hipMalloc on growth only).
+int ensure_scratch(Ctx *ctx, size_t bytes);
+
+// ---- device-resident matrix ---------------------------------------------
+// Decode GEMV layout (built at upload): wave tiles of kGemvChannels output
+// channels; lane (half h, phase p) of a wave owns phase p of channels
+// 2h, 2h+1 of the tile; each step is one 16-byte load per lane covering S
+// consecutive 32-blocks, so every wave load is one contiguous 1 KB chunk.
+constexpr int kGemvChannels = 4;  // per wave tile (2 per lane half)
+
+struct Linear {
+  int bits = 8;  // 8, 16 or 32
+  size_t n = 0, k = 0, group = 64, groups = 0, n_exc = 0;
+  // Row-major copies (dequantization, GEMM operands, GEMV tails).
+  void *codes = nullptr;   // [n][k] int8 / int16 / float
+  float *scales = nullptr; // [n][groups] (bits 8/16)
+  int32_t *exc_cols = nullptr;  // [n_exc]
+  float *exc_vals = nullptr;    // [n][n_exc]
+  int16_t *exc_index = nullptr; // [k]: exception number of a column, or -1
+  // GEMV tiles.
+  void *gemv_codes = nullptr;    // [tiles][steps][64 lanes][16 B]
+  float *gemv_scales = nullptr;  // [tiles][steps][2 halves][2 ch][sps]
+  size_t gemv_tiles = 0, gemv_steps = 0, gemv_sps = 0, gemv_blocks = 0;
+  // INT16-panel operands (bits 8, group 64): B tiles in MFMA lane order and
+  // per-(group, column) weight sums times 128.
+  int8_t *i16_b = nullptr;      // [groups][n/16][64 lanes][16 B]
+  int32_t *i16_wsum = nullptr;  // [groups][n]  (128 * sum of the group's codes)
+  float *i16_sw = nullptr;      // [groups][n]  scales, group-major
+  size_t device_bytes = 0;
+};
+
+// ---- launchers (each validates its launch shape on the host) -------------
+int launch_gemv(Ctx *ctx, const Linear *lin, const float *x, size_t rows, float *out, bool glu);
+int launch_dequantize(Ctx *ctx, const Linear *lin, float *out);
+int launch_row_scales(Ctx *ctx, const float *h, size_t rows, size_t width, float eps, float *out);
+int launch_prefill_f32(Ctx *ctx, const Linear *lin, const float *x, size_t rows,
+                       const float *row_scale, int epilogue, float *out);
+int launch_prefill_chain(Ctx *ctx, const Linear *lin, const float *x, size_t rows,
+                         const float *row_scale, int epilogue, float *out);
+int launch_prefill_i16(Ctx *ctx, const Linear *lin, const float *x, size_t rows,
+                       const float *row_scale, int epilogue, float *out);
+int launch_attention(Ctx *ctx, const float *q, const float *prefix_k, const float *generated_k,
+                     const float *v, size_t query_len, size_t prefix_len, size_t total_len,
+                     size_t n_heads, size_t n_kv_heads, size_t query_offset, size_t image_start,
+                     size_t image_end, const float *sinks, int softmax, int exp_mode, float *out);
+int launch_argmax(Ctx *ctx, const float *logits, size_t rows, size_t vocab, uint32_t *result_dev);
+
+// ---- device helpers ---------------------------------------------------------
+__device__ __forceinline__ float fmaf_(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
+
+// squared_relu_glu, src/kernels/mod.rs:567-572.
+__device__ __forceinline__ float squared_relu_glu(float gate, float up) {
+  float relu = gate > 0.0f ? gate : 0.0f;
+  return (relu * relu) * up;
+}
+
+// exp_poly_unchecked / exp_poly, src/kernels/exp.rs:232-277 (Cephes expf:
+// the reference's literal constants, digit for digit).
+__device__ __forceinline__ float exp_poly_unchecked(float x) {
+  const float n = __builtin_rintf(x * 1.44269504088896340735992468100189214f);
+  float r = fmaf_(n, -0.6933594f, x);
+  r = fmaf_(n, 2.1219444e-4f, r);
+  float p = 1.9875691e-4f;
+  p = fmaf_(p, r, 1.3981999e-3f);
+  p = fmaf_(p, r, 8.333452e-3f);
+  p = fmaf_(p, r, 4.1665796e-2f);
+  p = fmaf_(p, r, 0.16666665f);
+  p = fmaf_(p, r, 0.5f);
+  const float y = fmaf_(p, r * r, r) + 1.0f;
+  return y * __uint_as_float(static_cast<uint32_t>(static_cast<int32_t>(n) + 127) << 23);
+}
+
+// The device libm exp and log (ExpMode::Exact, and the sink's exp/ln):
+// accurate to about 1 ulp, not bitwise the host libm.
+__device__ __forceinline__ float expf_acc(float x) { return ::expf(x); }
+__device__ __forceinline__ float logf_acc(float x) { return ::logf(x); }
+
+__device__ __forceinline__ float exp_poly(float x) {
+  if (__builtin_isnan(x)) return x;
+  if (x < -87.0f) return 0.0f;
+  if (x > 88.376f) return __builtin_inff();
+  return exp_poly_unchecked(x);
+}
+
+}  // namespace focr

@@ -1,0 +1,195 @@
+// Element-wise and per-row kernels of the hot path: weight dequantization
+// (A1), RMS row scales (A6) and greedy argmax (A9). All HBM-bound.
+#include "focr_internal.hpp"
+
+namespace focr {
+namespace {
+
+// dequantize_row for every row (src/quant/linear.rs:246-262, dot.rs:25-29):
+// w = fl(code * scale), exception columns replaced by their FP32 weights.
+template <typename T>
+__global__ __launch_bounds__(256) void dequantize_kernel(const T *__restrict__ codes, const float *__restrict__ scales,
+                                                         const int16_t *__restrict__ exc_index,
+                                                         const float *__restrict__ exc_vals, int n_exc, size_t n,
+                                                         size_t k, size_t group, size_t groups, float *__restrict__ out) {
+  const size_t total = n * k;
+  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < total;
+       i += static_cast<size_t>(gridDim.x) * blockDim.x) {
+    const size_t row = i / k, col = i % k;
+    float w = static_cast<float>(static_cast<int32_t>(codes[i])) * scales[row * groups + col / group];
+    if (exc_index) {
+      const int e = exc_index[col];
+      if (e >= 0) w = exc_vals[row * n_exc + e];
+    }
+    out[i] = w;
+  }
+}
+
+// One 32-element leaf of sum_squares_pairwise (src/kernels/mod.rs:546-552):
+// squares into 32 zero-padded slots, then partial[i] += partial[i + w] for
+// w = 16, 8, 4, 2, 1.
+__device__ float leaf_sum(const float *x, int len) {
+  float part[32];
+#pragma unroll
+  for (int i = 0; i < 32; i++) part[i] = i < len ? x[i] * x[i] : 0.0f;
+#pragma unroll
+  for (int w = 16; w >= 1; w /= 2)
+#pragma unroll
+    for (int i = 0; i < w; i++) part[i] = part[i] + part[i + w];
+  return part[0];
+}
+
+__device__ __forceinline__ int split_point(int len) { return ((len / 2 + 31) / 32) * 32; }
+
+constexpr int kMaxLeaves = 1024;  // widths up to 16384 (leaves <= 2 * width / 32)
+
+// rms_scale (src/kernels/mod.rs:531-553): one wave per row. Lane 0 walks the
+// recursive halving tree (split at (len/2).next_multiple_of(32)) to list the
+// leaves left to right, the wave sums the leaves in parallel, and lane 0
+// adds them back up the same tree: left + right at every node.
+__global__ __launch_bounds__(64) void row_scales_kernel(const float *__restrict__ h, int width, float eps,
+                                                        float *__restrict__ out) {
+  __shared__ int leaf_start[kMaxLeaves];
+  __shared__ int leaf_len[kMaxLeaves];
+  __shared__ float leaf_val[kMaxLeaves];
+  __shared__ int leaf_count;
+  const float *row = h + static_cast<size_t>(blockIdx.x) * width;
+  if (threadIdx.x == 0) {
+    int stack_start[40], stack_len[40], sp = 0, count = 0;
+    stack_start[sp] = 0;
+    stack_len[sp++] = width;
+    while (sp > 0) {
+      const int s = stack_start[--sp], len = stack_len[sp];
+      if (len > 32) {
+        const int m = split_point(len);
+        stack_start[sp] = s + m;  // right, visited after left
+        stack_len[sp++] = len - m;
+        stack_start[sp] = s;
+        stack_len[sp++] = m;
+      } else {
+        leaf_start[count] = s;
+        leaf_len[count++] = len;
+      }
+    }
+    leaf_count = count;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < leaf_count; i += 64) leaf_val[i] = leaf_sum(row + leaf_start[i], leaf_len[i]);
+  __syncthreads();
+  if (threadIdx.x != 0) return;
+  // Post-order evaluation: frame state 0 = descend left, 1 = descend right, 2 = add.
+  int f_len[40], f_state[40], sp = 0, next_leaf = 0;
+  float f_left[40], ret = 0.0f;
+  f_len[0] = width;
+  f_state[0] = 0;
+  sp = 1;
+  while (sp > 0) {
+    const int top = sp - 1, len = f_len[top];
+    if (len <= 32) {
+      ret = leaf_val[next_leaf++];
+      sp--;
+      continue;
+    }
+    const int m = split_point(len);
+    if (f_state[top] == 0) {
+      f_state[top] = 1;
+      f_len[sp] = m;
+      f_state[sp++] = 0;
+    } else if (f_state[top] == 1) {
+      f_left[top] = ret;
+      f_state[top] = 2;
+      f_len[sp] = len - m;
+      f_state[sp++] = 0;
+    } else {
+      ret = f_left[top] + ret;
+      sp--;
+    }
+  }
+  // (sum / width + eps).sqrt().recip(): IEEE division and square root.
+  out[blockIdx.x] = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ret, static_cast<float>(width)) + eps));
+}
+
+// argmax (src/runner/mod.rs:916-930): first index of the maximum, and a flag
+// when any value is non-finite. One workgroup per row.
+__global__ __launch_bounds__(256) void argmax_kernel(const float *__restrict__ logits, int vocab,
+                                                     uint32_t *__restrict__ result) {
+  const float *row = logits + static_cast<size_t>(blockIdx.x) * vocab;
+  float best = -__builtin_inff();
+  int best_i = -1;
+  int nonfinite = 0;
+  for (int i = threadIdx.x; i < vocab; i += blockDim.x) {
+    const float v = row[i];
+    nonfinite |= !__builtin_isfinite(v);
+    if (best_i < 0 || v > best) {
+      best = v;
+      best_i = i;
+    }
+  }
+  __shared__ float s_val[256];
+  __shared__ int s_idx[256];
+  __shared__ int s_bad[256];
+  s_val[threadIdx.x] = best;
+  s_idx[threadIdx.x] = best_i;
+  s_bad[threadIdx.x] = nonfinite;
+  __syncthreads();
+  for (int stride = 128; stride > 0; stride /= 2) {
+    if (threadIdx.x < stride) {
+      const int o = threadIdx.x + stride;
+      const float a = s_val[threadIdx.x], b = s_val[o];
+      const int ia = s_idx[threadIdx.x], ib = s_idx[o];
+      if (ib >= 0 && (ia < 0 || b > a || (b == a && ib < ia))) {
+        s_val[threadIdx.x] = b;
+        s_idx[threadIdx.x] = ib;
+      }
+      s_bad[threadIdx.x] |= s_bad[o];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    result[2 * blockIdx.x] = static_cast<uint32_t>(s_idx[0]);
+    result[2 * blockIdx.x + 1] = static_cast<uint32_t>(s_bad[0]);
+  }
+}
+
+}  // namespace
+
+int launch_dequantize(Ctx *ctx, const Linear *lin, float *out) {
+  FOCR_HIP_CHECK(hipSetDevice(ctx->device));
+  const size_t total = lin->n * lin->k;
+  if (lin->bits == 32) {
+    FOCR_HIP_CHECK(hipMemcpyAsync(out, lin->codes, total * sizeof(float), hipMemcpyDeviceToDevice, ctx->stream));
+    return FOCR_OK;
+  }
+  const size_t want = (total + 255) / 256;
+  const int blocks = static_cast<int>(want < 65536 ? want : 65536);
+  if (lin->bits == 8)
+    hipLaunchKernelGGL(dequantize_kernel<int8_t>, dim3(blocks), dim3(256), 0, ctx->stream,
+                       static_cast<const int8_t *>(lin->codes), lin->scales, lin->exc_index, lin->exc_vals,
+                       static_cast<int>(lin->n_exc), lin->n, lin->k, lin->group, lin->groups, out);
+  else
+    hipLaunchKernelGGL(dequantize_kernel<int16_t>, dim3(blocks), dim3(256), 0, ctx->stream,
+                       static_cast<const int16_t *>(lin->codes), lin->scales, lin->exc_index, lin->exc_vals,
+                       static_cast<int>(lin->n_exc), lin->n, lin->k, lin->group, lin->groups, out);
+  FOCR_HIP_CHECK(hipGetLastError());
+  return FOCR_OK;
+}
+
+int launch_row_scales(Ctx *ctx, const float *h, size_t rows, size_t width, float eps, float *out) {
+  FOCR_REQUIRE(width <= 16384, FOCR_E_SHAPE, "focr_row_scales: width above 16384");
+  FOCR_REQUIRE(rows < (size_t(1) << 31), FOCR_E_SHAPE, "focr_row_scales: too many rows");
+  FOCR_HIP_CHECK(hipSetDevice(ctx->device));
+  hipLaunchKernelGGL(row_scales_kernel, dim3(static_cast<unsigned>(rows)), dim3(64), 0, ctx->stream, h,
+                     static_cast<int>(width), eps, out);
+  FOCR_HIP_CHECK(hipGetLastError());
+  return FOCR_OK;
+}
+
+int launch_argmax(Ctx *ctx, const float *logits, size_t rows, size_t vocab, uint32_t *result_dev) {
+  FOCR_REQUIRE(rows < (size_t(1) << 31), FOCR_E_SHAPE, "focr_argmax: too many rows");
+  hipLaunchKernelGGL(argmax_kernel, dim3(static_cast<unsigned>(rows)), dim3(256), 0, ctx->stream, logits,
+                     static_cast<int>(vocab), result_dev);
+  FOCR_HIP_CHECK(hipGetLastError());
+  return FOCR_OK;
+}
+
+}  // namespace focr

@@ -1,0 +1,365 @@
+"""Python host mirror of the Falcon-OCR runner's operator interface, over the
+``focr_hip`` C ABI (include/focr_hip.h, lib/libfocr_hip.so built for gfx950).
+
+Names and argument meanings follow the reference (amazingvince/falcon-ocr-cpu):
+
+  QuantLinear            src/quant/linear.rs:123-130 (codes, scales, exceptions)
+    .from_parts          from_parts          (linear.rs:318-358)
+    .with_exceptions     with_exceptions     (linear.rs:366-390)
+    .linear              linear, 1..=8 rows  (linear.rs:497-549)
+    .linear_glu          linear_glu          (linear.rs:555-625)
+    .prefill             prefill             (linear.rs:634-707)
+    .dequantize          dequantize_row x n  (linear.rs:246-262)
+  Linear.from_f32        kernels::linear_with_simd's FP32 weights (kernels/mod.rs:387)
+  Epilogue               panel::Epilogue     (kernels/panels/panel.rs:26-33)
+  PrefillProjection      kernels::PrefillProjection (kernels/mod.rs:71-84), `hip` kinds
+  Geometry, CompactKv    kernels::attention  (kernels/attention/mod.rs:40-196)
+  PrefillOptions         (attention/mod.rs:205-221)
+  attention_with         (attention/mod.rs:256-311)
+  row_scales / rms_scale (model/rope.rs:147-152, kernels/mod.rs:531-533)
+  argmax                 (runner/mod.rs:916-930)
+
+Tensors are torch CUDA tensors (device memory and streams come from torch;
+the arithmetic runs in the HIP library). Errors raise ``FocrError``, the
+counterpart of the reference's ``anyhow`` errors and shape assertions. There
+is no CPU fallback: without the built library or a GPU this module raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import enum
+from dataclasses import dataclass
+from pathlib import Path
+from typing import Optional
+
+import numpy as np
+
+_ROOT = Path(__file__).resolve().parents[1]
+LIBRARY = _ROOT / "lib" / "libfocr_hip.so"
+HEADER = _ROOT.parent / "include" / "focr_hip.h"
+
+FOCR_OK = 0
+ERRORS = {-1: "FOCR_E_ARG", -2: "FOCR_E_SHAPE", -3: "FOCR_E_UNSUPPORTED", -4: "FOCR_E_HIP",
+          -5: "FOCR_E_VALUE", -6: "FOCR_E_NONFINITE"}
+
+# Every entry point of include/focr_hip.h, with its ctypes signature.
+_P, _Z, _I, _F = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_float
+SIGNATURES = {
+    "focr_ctx_create": (_I, [_I, ctypes.POINTER(_P)]),
+    "focr_ctx_destroy": (_I, [_P]),
+    "focr_ctx_set_stream": (_I, [_P, _P]),
+    "focr_ctx_stream": (_P, [_P]),
+    "focr_ctx_sync": (_I, [_P]),
+    "focr_last_error": (ctypes.c_char_p, []),
+    "focr_malloc": (_I, [_P, _Z, ctypes.POINTER(_P)]),
+    "focr_free": (_I, [_P, _P]),
+    "focr_memcpy_h2d": (_I, [_P, _P, _P, _Z]),
+    "focr_memcpy_d2h": (_I, [_P, _P, _P, _Z]),
+    "focr_linear_upload": (_I, [_P, _I, _Z, _Z, _Z, _P, _P, _P, _P, _Z, ctypes.POINTER(_P)]),
+    "focr_linear_free": (_I, [_P]),
+    "focr_linear_info": (_I, [_P, ctypes.POINTER(_I), ctypes.POINTER(_Z), ctypes.POINTER(_Z),
+                              ctypes.POINTER(_Z), ctypes.POINTER(_Z), ctypes.POINTER(_Z)]),
+    "focr_linear_dequantize": (_I, [_P, _P, _P]),
+    "focr_linear_decode": (_I, [_P, _P, _P, _Z, _P]),
+    "focr_linear_decode_glu": (_I, [_P, _P, _P, _Z, _P]),
+    "focr_linear_prefill": (_I, [_P, _P, _P, _Z, _P, _I, _I, _P]),
+    "focr_row_scales": (_I, [_P, _P, _Z, _Z, _F, _P]),
+    "focr_attention_prefill": (_I, [_P, _P, _P, _P, _P, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _P, _I, _I, _P]),
+    "focr_argmax": (_I, [_P, _P, _Z, _Z, _P]),
+}
+
+
+class FocrError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(f"{ERRORS.get(code, code)}: {message}")
+        self.code = code
+
+
+def load_library(path: Path = LIBRARY) -> ctypes.CDLL:
+    """Load lib/libfocr_hip.so and bind every declared symbol (raises if absent)."""
+    if not path.exists():
+        raise FocrError(-3, f"{path} is not built; run __graft_entry__.build()")
+    lib = ctypes.CDLL(str(path))
+    for name, (restype, argtypes) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    return lib
+
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        _lib = load_library()
+    return _lib
+
+
+def _check(rc: int) -> None:
+    if rc != FOCR_OK:
+        raise FocrError(rc, lib().focr_last_error().decode())
+
+
+def _torch():
+    import torch
+
+    return torch
+
+
+def _dev(t) -> Optional[int]:
+    """Device pointer of a CUDA tensor (None passes NULL)."""
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise FocrError(-1, "expected a CUDA tensor")
+    if not t.is_contiguous():
+        raise FocrError(-2, "expected a contiguous tensor")
+    return t.data_ptr()
+
+
+class Context:
+    """A focr_ctx bound to torch's current stream on `device`."""
+
+    def __init__(self, device: int = 0):
+        torch = _torch()
+        handle = ctypes.c_void_p()
+        _check(lib().focr_ctx_create(device, ctypes.byref(handle)))
+        self.handle = handle
+        self.device = device
+        with torch.cuda.device(device):
+            stream = torch.cuda.current_stream(device)
+        _check(lib().focr_ctx_set_stream(self.handle, ctypes.c_void_p(stream.cuda_stream)))
+
+    def use_stream(self, stream) -> None:
+        _check(lib().focr_ctx_set_stream(self.handle, ctypes.c_void_p(stream.cuda_stream if stream else 0)))
+
+    def sync(self) -> None:
+        _check(lib().focr_ctx_sync(self.handle))
+
+    def close(self) -> None:
+        if self.handle:
+            _check(lib().focr_ctx_destroy(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+_default: Optional[Context] = None
+
+
+def default_context() -> Context:
+    global _default
+    if _default is None:
+        _default = Context(0)
+    return _default
+
+
+class Epilogue(enum.IntEnum):
+    """Where a finished tile goes (panel.rs:26-33)."""
+
+    STORE = 0
+    GLU = 1
+    ADD = 2
+
+
+class PrefillProjection(enum.IntEnum):
+    """The `hip` backend's prefill projection kernels."""
+
+    F32_MFMA = 0  # FP32 matrix cores, within FP32 tolerance of the panels
+    F32_CHAIN = 1  # bitwise the FP32 panels (PanelAvx2)
+    I16 = 2  # bitwise the INT16 panels (PanelI16Vnni / PanelI16Avx2)
+
+
+class Linear:
+    """A device-resident matrix (focr_linear): 8/16-bit codes or FP32 weights."""
+
+    def __init__(self, bits, codes, scales, group, exc_cols=None, exc_vals=None, ctx: Optional[Context] = None):
+        self.ctx = ctx or default_context()
+        codes = np.ascontiguousarray(codes)
+        n, k = codes.shape
+        dtype = {8: np.int8, 16: np.int16, 32: np.float32}[bits]
+        codes = codes.astype(dtype, copy=False)
+        sc = None if scales is None else np.ascontiguousarray(scales, dtype=np.float32)
+        cols = vals = None
+        n_exc = 0
+        if exc_cols is not None and len(exc_cols):
+            cols = np.ascontiguousarray(exc_cols, dtype=np.int32)
+            vals = np.ascontiguousarray(exc_vals, dtype=np.float32)
+            n_exc = len(cols)
+        handle = ctypes.c_void_p()
+        ptr = lambda a: None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+        _check(lib().focr_linear_upload(self.ctx.handle, bits, n, k, group if bits != 32 else 0, ptr(codes), ptr(sc),
+                                        ptr(cols), ptr(vals), n_exc, ctypes.byref(handle)))
+        self.handle = handle
+        self.out_dim, self.in_dim, self.group, self._bits, self.n_exc = n, k, group, bits, n_exc
+
+    @classmethod
+    def from_f32(cls, weights, ctx: Optional[Context] = None) -> "Linear":
+        return cls(32, np.asarray(weights, dtype=np.float32), None, 32, ctx=ctx)
+
+    def dimensions(self):
+        return self.out_dim, self.in_dim
+
+    def bits(self) -> int:
+        return self._bits
+
+    def device_bytes(self) -> int:
+        out = ctypes.c_size_t()
+        _check(lib().focr_linear_info(self.handle, None, None, None, None, None, ctypes.byref(out)))
+        return out.value
+
+    def free(self) -> None:
+        if getattr(self, "handle", None):
+            _check(lib().focr_linear_free(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+    # -- operators ---------------------------------------------------------
+    def dequantize(self):
+        torch = _torch()
+        out = torch.empty((self.out_dim, self.in_dim), dtype=torch.float32, device=f"cuda:{self.ctx.device}")
+        _check(lib().focr_linear_dequantize(self.ctx.handle, self.handle, _dev(out)))
+        return out
+
+    def linear(self, input, rows: int, output=None):
+        """`QuantLinear::linear` for 1..=8 rows: returns [rows][out]."""
+        torch = _torch()
+        if input.numel() != rows * self.in_dim:
+            raise FocrError(-2, "W8 input shape")
+        if output is None:
+            output = torch.empty((rows, self.out_dim), dtype=torch.float32, device=input.device)
+        elif output.numel() != rows * self.out_dim:
+            raise FocrError(-2, "W8 output shape")
+        _check(lib().focr_linear_decode(self.ctx.handle, self.handle, _dev(input), rows, _dev(output)))
+        return output
+
+    def linear_glu(self, input, rows: int, gated=None):
+        """`QuantLinear::linear_glu`: squared-ReLU GLU of interleaved gate/up rows."""
+        torch = _torch()
+        if input.numel() != rows * self.in_dim:
+            raise FocrError(-2, "W8 input shape")
+        if gated is None:
+            gated = torch.empty((rows, self.out_dim // 2), dtype=torch.float32, device=input.device)
+        _check(lib().focr_linear_decode_glu(self.ctx.handle, self.handle, _dev(input), rows, _dev(gated)))
+        return gated
+
+    def prefill(self, input, rows: int, row_scale=None, epilogue: Epilogue = Epilogue.STORE, out=None,
+                kernel: PrefillProjection = PrefillProjection.F32_MFMA):
+        """`QuantLinear::prefill`: out = epilogue(A' W^T), A' = input * row_scale per row.
+
+        For Epilogue.ADD, `out` holds the residual and is updated in place."""
+        torch = _torch()
+        if input.numel() != rows * self.in_dim:
+            raise FocrError(-2, "prefill input shape")
+        width = self.out_dim // 2 if epilogue == Epilogue.GLU else self.out_dim
+        if out is None:
+            if epilogue == Epilogue.ADD:
+                raise FocrError(-1, "Epilogue.ADD needs the residual `out`")
+            out = torch.empty((rows, width), dtype=torch.float32, device=input.device)
+        _check(lib().focr_linear_prefill(self.ctx.handle, self.handle, _dev(input), rows, _dev(row_scale),
+                                         int(epilogue), int(kernel), _dev(out)))
+        return out
+
+
+class QuantLinear(Linear):
+    """A quantized matrix with 8- or 16-bit codes (src/quant/linear.rs:123-130)."""
+
+    @classmethod
+    def from_parts(cls, out_dim, in_dim, group_size, codes, scales, ctx: Optional[Context] = None) -> "QuantLinear":
+        codes = np.asarray(codes).reshape(out_dim, in_dim)
+        bits = 8 if codes.dtype == np.int8 else 16
+        return cls(bits, codes, np.asarray(scales, dtype=np.float32).reshape(out_dim, -1), group_size, ctx=ctx)
+
+    def with_exceptions(self, columns, values) -> "QuantLinear":
+        raise FocrError(-3, "pass exc_cols/exc_vals to the constructor (the device copy is immutable)")
+
+
+@dataclass(frozen=True)
+class Geometry:
+    """Masking geometry (attention/mod.rs:40-76)."""
+
+    query_offset: int
+    image_start: int
+    image_end: int
+
+
+@dataclass
+class CompactKv:
+    """Compact KV cache (attention/mod.rs:78-151); tensors on the GPU."""
+
+    prefix_k: object
+    generated_k: object
+    v: object
+    prefix_len: int
+    total_len: int
+    n_heads: int
+    n_kv_heads: int
+    head_dim: int
+
+    @classmethod
+    def prefill(cls, k, v, total, n_heads, n_kv_heads, head_dim=64) -> "CompactKv":
+        return cls(k, None, v, total, total, n_heads, n_kv_heads, head_dim)
+
+
+class Softmax(enum.IntEnum):
+    ONLINE = 0
+    STATIC = 1
+
+
+class ExpMode(enum.IntEnum):
+    FAST = 0
+    EXACT = 1
+
+
+@dataclass(frozen=True)
+class PrefillOptions:
+    exp: ExpMode = ExpMode.FAST
+    fp32_softmax: Softmax = Softmax.ONLINE
+
+
+def attention_with(q, kv: CompactKv, query_len: int, geometry: Geometry, sinks, options: PrefillOptions = PrefillOptions(),
+                   output=None, ctx: Optional[Context] = None):
+    """`kernels::attention_with` for a prefill: returns [query_len][n_heads][64]."""
+    torch = _torch()
+    ctx = ctx or default_context()
+    if output is None:
+        output = torch.empty_like(q)
+    _check(lib().focr_attention_prefill(ctx.handle, _dev(q), _dev(kv.prefix_k), _dev(kv.generated_k), _dev(kv.v),
+                                        query_len, kv.prefix_len, kv.total_len, kv.n_heads, kv.n_kv_heads,
+                                        kv.head_dim, geometry.query_offset, geometry.image_start,
+                                        geometry.image_end, _dev(sinks), int(options.fp32_softmax),
+                                        int(options.exp), _dev(output)))
+    return output
+
+
+F32_EPSILON = float(np.finfo(np.float32).eps)
+
+
+def row_scales(h, width: int, eps: float = F32_EPSILON, out=None, ctx: Optional[Context] = None):
+    """`rms_norm`'s factor of every width-wide row (eps f32::EPSILON by default)."""
+    torch = _torch()
+    ctx = ctx or default_context()
+    rows = h.numel() // width
+    if out is None:
+        out = torch.empty(rows, dtype=torch.float32, device=h.device)
+    _check(lib().focr_row_scales(ctx.handle, _dev(h), rows, width, eps, _dev(out)))
+    return out
+
+
+def argmax(logits, rows: int, vocab: int, ctx: Optional[Context] = None):
+    """Greedy tokens of `rows` rows; FocrError(FOCR_E_NONFINITE) on NaN/inf."""
+    ctx = ctx or default_context()
+    tokens = (ctypes.c_uint32 * rows)()
+    _check(lib().focr_argmax(ctx.handle, _dev(logits), rows, vocab, ctypes.cast(tokens, ctypes.c_void_p)))
+    return list(tokens)

@@ -1,0 +1,167 @@
+/*
+ * focr_hip.h — C ABI of the MI355X (gfx950) backend for the Falcon-OCR
+ * runner's projection linears and prefill attention.
+ *
+ * The reference (amazingvince/falcon-ocr-cpu) is a Rust crate with no C ABI;
+ * each entry point below replaces one of its operator interfaces, cited by
+ * file:line. A Rust `extern "C"` crate binds these declarations as a new
+ * `hip` backend next to avx2|scalar|neon (src/config.rs:19-35).
+ *
+ * Conventions
+ *  - Every function returns FOCR_OK (0) or a negative FOCR_E_* code and never
+ *    aborts; focr_last_error() returns the message of the calling thread's
+ *    last failure. Shape misuse that the reference asserts on
+ *    (src/kernels/panels/driver.rs:66-78, src/quant/linear.rs:654-662) is an
+ *    FOCR_E_SHAPE error here.
+ *  - Pointers named *_dev are device (HBM) addresses; everything else is a
+ *    host address. Compute calls are asynchronous on the context's stream;
+ *    focr_ctx_sync() waits for them. One context serves one thread at a time;
+ *    two contexts may run concurrently (the reference's prefill pool and
+ *    decode team, src/runner/pipeline.rs:1-4).
+ *  - Results never depend on launch configuration: every output has one
+ *    fixed operation sequence.
+ */
+#ifndef FOCR_HIP_H
+#define FOCR_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------ */
+#define FOCR_OK 0
+#define FOCR_E_ARG (-1)         /* null pointer or invalid enum value */
+#define FOCR_E_SHAPE (-2)       /* shapes that do not fit the operator */
+#define FOCR_E_UNSUPPORTED (-3) /* valid, but not supported by this backend */
+#define FOCR_E_HIP (-4)         /* a HIP runtime error */
+#define FOCR_E_VALUE (-5)       /* invalid data (e.g. a W8 code of -128) */
+#define FOCR_E_NONFINITE (-6)   /* non-finite logits (argmax) */
+
+/* ---- enums --------------------------------------------------------------- */
+/* Epilogue, src/kernels/panels/panel.rs:26-33. */
+#define FOCR_EPI_STORE 0 /* out[m][n] = C */
+#define FOCR_EPI_GLU 1   /* out[m][i] = squared_relu_glu(C[m][2i], C[m][2i+1]) */
+#define FOCR_EPI_ADD 2   /* out[m][n] += C (residual add) */
+
+/* Prefill projection kernel, the `hip` counterparts of PrefillProjection
+ * (src/kernels/mod.rs:71-84). */
+#define FOCR_PROJ_F32_MFMA 0  /* FP32 weights or fl(code*scale), FP32 matrix cores
+                                 (tolerance-matched to the FP32 panels) */
+#define FOCR_PROJ_F32_CHAIN 1 /* FP32 panels' exact order: one ascending-k FMA
+                                 chain per output (bitwise PanelAvx2) */
+#define FOCR_PROJ_I16 2       /* INT16 activations x INT8 codes, exact INT32 group
+                                 sums (bitwise PanelI16Vnni/PanelI16Avx2) */
+
+/* Prefill softmax (src/config.rs PrefillSoftmax) and exp (ExpMode). */
+#define FOCR_SOFTMAX_ONLINE 0
+#define FOCR_SOFTMAX_STATIC 1
+#define FOCR_EXP_FAST 0  /* exp_poly, src/kernels/exp.rs:232-277 */
+#define FOCR_EXP_EXACT 1 /* the device libm expf */
+
+typedef struct focr_ctx focr_ctx;
+typedef struct focr_linear focr_linear;
+
+/* ---- context ------------------------------------------------------------ */
+/* No reference counterpart (the CPU runner needs no device state); the
+ * Rust backend creates one per Rayon pool / decode team. */
+int focr_ctx_create(int device, focr_ctx **out);
+int focr_ctx_destroy(focr_ctx *ctx);
+/* Run on an existing hipStream_t (e.g. a framework's stream) instead of the
+ * context's own; NULL restores the context's stream. */
+int focr_ctx_set_stream(focr_ctx *ctx, void *hip_stream);
+void *focr_ctx_stream(const focr_ctx *ctx);
+int focr_ctx_sync(focr_ctx *ctx);
+/* Message of the calling thread's last failure ("" if none). */
+const char *focr_last_error(void);
+/* Device memory helpers for callers without HIP headers. */
+int focr_malloc(focr_ctx *ctx, size_t bytes, void **out_dev);
+int focr_free(focr_ctx *ctx, void *dev);
+int focr_memcpy_h2d(focr_ctx *ctx, void *dst_dev, const void *src, size_t bytes);
+int focr_memcpy_d2h(focr_ctx *ctx, void *dst, const void *src_dev, size_t bytes);
+
+/* ---- A1: quantized linear storage --------------------------------------- */
+/* Upload one matrix into a device handle, the device side of
+ * QuantLinear::from_parts / from_mapped / with_exceptions
+ * (src/quant/linear.rs:318-358,392-455) and of the FP32 weight slices of
+ * kernels::linear_with_simd (src/kernels/mod.rs:387-398).
+ *   bits 8: codes int8 [out][in] (W8 rules of from_parts are checked:
+ *           no -128, finite non-negative scales, zero codes in zero-scale
+ *           groups); bits 16: codes int16 [out][in]; bits 32: FP32 weights
+ *           [out][in], scales NULL, group ignored.
+ *   scales: FP32 [out][ceil(in/group)], group 32, 64 or 128.
+ *   exc_cols/exc_vals: optional exception columns (sorted, unique, < in)
+ *           and their FP32 weights [out][n_exc]; codes there must be zero.
+ * Host pointers; the call copies them and returns when the upload is done. */
+int focr_linear_upload(focr_ctx *ctx, int bits, size_t out_dim, size_t in_dim, size_t group,
+                       const void *codes, const float *scales, const int32_t *exc_cols,
+                       const float *exc_vals, size_t n_exc, focr_linear **out);
+int focr_linear_free(focr_linear *lin);
+int focr_linear_info(const focr_linear *lin, int *bits, size_t *out_dim, size_t *in_dim,
+                     size_t *group, size_t *n_exc, size_t *device_bytes);
+/* fl(code * scale) for every weight, exception columns in place:
+ * QuantLinear::dequantize_row for all rows (src/quant/linear.rs:246-262).
+ * out_dev: FP32 [out][in]. Bit-exact. */
+int focr_linear_dequantize(focr_ctx *ctx, const focr_linear *lin, float *out_dev);
+
+/* ---- A4 / A5: decode and draft-verify GEMV ------------------------------ */
+/* QuantLinear::linear for 1..=8 rows (src/quant/linear.rs:497-549,783-817),
+ * and kernels::linear_with_simd rows <= 8 for bits 32
+ * (src/kernels/mod.rs:407-432). x_dev [rows][in], out_dev [rows][out].
+ * Bitwise equal to the reference's AVX2/NEON/portable dot_q / dot order. */
+int focr_linear_decode(focr_ctx *ctx, const focr_linear *lin, const float *x_dev, size_t rows,
+                       float *out_dev);
+/* QuantLinear::linear_glu / kernels::linear_glu_with_simd for 1..=8 rows
+ * (src/quant/linear.rs:555-625, src/kernels/mod.rs:580-615): gated_dev
+ * [rows][out/2] from interleaved [gate, up] rows. Bitwise. */
+int focr_linear_decode_glu(focr_ctx *ctx, const focr_linear *lin, const float *x_dev,
+                           size_t rows, float *gated_dev);
+
+/* ---- A2 / A3: prefill projection ---------------------------------------- */
+/* QuantLinear::prefill (src/quant/linear.rs:634-707) and its FP32 panel
+ * and INT16 panel kernels (src/kernels/panels/{panel,panel_i16}.rs).
+ *   x_dev [rows][in]; row_scale_dev optional [rows] (an RMS norm folded
+ *   into packing); epilogue FOCR_EPI_*; kernel FOCR_PROJ_*.
+ *   out_dev [rows][out] (STORE, ADD) or [rows][out/2] (GLU).
+ * FOCR_PROJ_I16 needs 8-bit codes, group 64, out % 32 == 0, in % 64 == 0
+ * (fits_i16_panels, src/quant/linear.rs:29-31); it uses a scratch buffer the
+ * context owns and grows. */
+int focr_linear_prefill(focr_ctx *ctx, const focr_linear *lin, const float *x_dev, size_t rows,
+                        const float *row_scale_dev, int epilogue, int kernel, float *out_dev);
+
+/* ---- A6: RMS row scales -------------------------------------------------- */
+/* rms_scale of every width-wide row (src/kernels/mod.rs:531-553, row_scales
+ * src/model/rope.rs:147-152): 1/sqrt(pairwise_sum_squares/width + eps).
+ * Bitwise. */
+int focr_row_scales(focr_ctx *ctx, const float *h_dev, size_t rows, size_t width, float eps,
+                    float *out_dev);
+
+/* ---- A7: prefill attention ---------------------------------------------- */
+/* kernels::attention_with for a prefill (src/kernels/attention/mod.rs:256-311)
+ * over a compact cache (CompactKv, 85-196), head_dim 64:
+ *   q_dev [query_len][n_heads][64]; prefix_k_dev [prefix_len][n_heads][64];
+ *   generated_k_dev [total_len - prefix_len][n_kv_heads][64] (NULL when
+ *   prefix_len == total_len); v_dev [total_len][n_kv_heads][64];
+ *   Geometry (query_offset, image_start, image_end); sinks_dev [n_heads];
+ *   softmax FOCR_SOFTMAX_*; exp FOCR_EXP_*; out_dev like q.
+ * FP32 matrix cores: within the FP32 tolerance of the reference tiles. */
+int focr_attention_prefill(focr_ctx *ctx, const float *q_dev, const float *prefix_k_dev,
+                           const float *generated_k_dev, const float *v_dev, size_t query_len,
+                           size_t prefix_len, size_t total_len, size_t n_heads,
+                           size_t n_kv_heads, size_t head_dim, size_t query_offset,
+                           size_t image_start, size_t image_end, const float *sinks_dev,
+                           int softmax, int exp_mode, float *out_dev);
+
+/* ---- A9: greedy selection ------------------------------------------------ */
+/* argmax of each row (src/runner/mod.rs:916-939): first index of the
+ * maximum; FOCR_E_NONFINITE if any value of a row is NaN or infinite.
+ * logits_dev [rows][vocab]; tokens (host) [rows]. Synchronous. */
+int focr_argmax(focr_ctx *ctx, const float *logits_dev, size_t rows, size_t vocab,
+                uint32_t *tokens);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,119 @@
+/*
+ * CPU oracle for the Falcon-OCR projection/attention hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY. This is a plain-C restatement of the reference
+ * operators (amazingvince/falcon-ocr-cpu, Rust), operation for operation, used
+ * to check the HIP library and as the reported CPU baseline. Nothing in the
+ * product links or calls it. Every function cites the reference file:line it
+ * follows. Built with -ffp-contract=off: every fused multiply-add is an
+ * explicit fmaf(), every other product and sum rounds on its own, as in Rust.
+ */
+#ifndef FOCR_ORACLE_H
+#define FOCR_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Epilogues of the panel GEMMs (src/kernels/panels/panel.rs:26-33). */
+enum { ORC_STORE = 0, ORC_GLU = 1, ORC_ADD = 2 };
+
+/* src/kernels/exp.rs:232-277 */
+float orc_exp_poly(float x);
+float orc_exp_poly_unchecked(float x);
+/* src/kernels/mod.rs:567-572 */
+float orc_squared_relu_glu(float gate, float up);
+
+/* ---- A1: quantized storage ------------------------------------------- */
+/* RTN quantizer, src/quant/linear.rs:140-201. codes_out is int8_t (bits 8)
+ * or int16_t (bits 16). Returns 0, or a negative code for the reference's
+ * error cases (-1 bits, -2 shape/group, -3 nonfinite weight, -4 overflow). */
+int orc_quantize_bits(const float *w, size_t n, size_t k, size_t group, int bits,
+                      void *codes_out, float *scales_out);
+/* dequantize_row for every row, src/quant/linear.rs:246-262 + dot.rs:25-29.
+ * bits 8/16; exception columns replace the weight in place. */
+void orc_dequantize(int bits, const void *codes, const float *scales, size_t n, size_t k,
+                    size_t group, const int32_t *exc_cols, const float *exc_vals, size_t n_exc,
+                    float *out);
+/* QuantLinear::from_parts W8 validation, src/quant/linear.rs:318-358.
+ * 0 ok; negative on the first failing rule. */
+int orc_validate_w8(size_t n, size_t k, size_t group, const int8_t *codes, const float *scales);
+
+/* ---- A4 / A5: decode GEMV -------------------------------------------- */
+/* simd::dot (src/simd.rs:749-777), Portable/Avx2 tree. */
+float orc_dot(const float *a, const float *b, size_t len);
+/* simd::dot_q (src/simd.rs:821-857). bits 8/16. */
+float orc_dot_q(int bits, const float *x, const void *codes, const float *scales, size_t len,
+                size_t group);
+/* QuantLinear::linear small-M (src/quant/linear.rs:497-549,745-817) with
+ * exception FMAs (84-118). bits 8/16; bits 32 = kernels::linear_with_simd
+ * rows <= 8 over FP32 weights (src/kernels/mod.rs:407-432), scales unused. */
+void orc_linear_decode(int bits, const void *codes, const float *scales, size_t n, size_t k,
+                       size_t group, const int32_t *exc_cols, const float *exc_vals, size_t n_exc,
+                       const float *x, size_t rows, float *out);
+/* linear_glu (src/quant/linear.rs:555-625) / linear_glu_with_simd
+ * (src/kernels/mod.rs:580-615): gated [rows][n/2]. */
+void orc_linear_decode_glu(int bits, const void *codes, const float *scales, size_t n, size_t k,
+                           size_t group, const int32_t *exc_cols, const float *exc_vals,
+                           size_t n_exc, const float *x, size_t rows, float *gated);
+
+/* ---- A6: RMS row scale ------------------------------------------------ */
+/* rms_scale + sum_squares_pairwise, src/kernels/mod.rs:531-553. */
+float orc_rms_scale(const float *row, size_t width, float eps);
+void orc_row_scales(const float *h, size_t rows, size_t width, float eps, float *out);
+
+/* ---- A2: FP32 panel GEMM ---------------------------------------------- */
+/* panel::gemm + driver::tiled_gemm (src/kernels/panels/panel.rs:79-172,
+ * driver.rs:57-140): ascending-k FMA chain from +0 per output. w is the
+ * dequantized [n][k] matrix. out is [m][n] (or [m][n/2] for GLU). */
+void orc_panel_gemm(const float *a, size_t m, size_t k, const float *w, size_t n,
+                    const float *row_scale, int epilogue, float *out);
+
+/* ---- A3: INT16-activation x INT8-code panel GEMM ----------------------- */
+/* quantize_group, src/kernels/panels/panel_i16.rs:233-266. Returns the step. */
+float orc_i16_quantize_group(const float *x, int16_t *q);
+/* pack_rows + kernel_scalar + exception_tile + epilogue
+ * (src/kernels/panels/panel_i16.rs:187-213,275-369). */
+void orc_i16_gemm(const float *a, size_t m, size_t k, const int8_t *codes, const float *scales,
+                  size_t n, const int32_t *exc_cols, const float *exc_vals, size_t n_exc,
+                  const float *row_scale, int epilogue, float *out);
+/* The activation quantization alone (pack_rows): codes [m][k] i16, steps
+ * [m][k/64] (times row_scale), exception inputs [m][n_exc]. */
+void orc_i16_quantize_rows(const float *a, size_t m, size_t k, const int32_t *exc_cols,
+                           size_t n_exc, const float *row_scale, int16_t *codes, float *steps,
+                           float *exc_inputs);
+
+/* ---- A7: FP32 prefill attention --------------------------------------- */
+/* compact_prefill / tile_head (src/kernels/attention/prefill64.rs:149-480),
+ * head_dim 64. generated_k may be NULL when prefix_len == total_len.
+ * static_softmax: static_shift tiles (prefill64/static_shift.rs:135-196).
+ * exp_fast: ExpMode::Fast (exp_poly); else platform expf. */
+void orc_attention_prefill(const float *q, const float *prefix_k, const float *generated_k,
+                           const float *v, size_t query_len, size_t prefix_len, size_t total_len,
+                           size_t n_heads, size_t n_kv_heads, size_t query_offset,
+                           size_t image_start, size_t image_end, const float *sinks,
+                           int static_softmax, int exp_fast, float *out);
+/* The same over a subset of (query tile, head) tasks, for bounded CPU
+ * baseline samples: tiles [tile_begin, tile_end) of every head. */
+void orc_attention_prefill_tiles(const float *q, const float *prefix_k, const float *generated_k,
+                                 const float *v, size_t query_len, size_t prefix_len,
+                                 size_t total_len, size_t n_heads, size_t n_kv_heads,
+                                 size_t query_offset, size_t image_start, size_t image_end,
+                                 const float *sinks, int static_softmax, int exp_fast,
+                                 size_t tile_begin, size_t tile_end, float *out);
+
+/* ---- A9: greedy selection --------------------------------------------- */
+/* argmax, src/runner/mod.rs:916-930. 0 ok, -1 on non-finite/empty. */
+int orc_argmax(const float *logits, size_t n, uint32_t *out);
+
+/* Threads the oracle uses for its parallel loops (1 = scalar). */
+void orc_set_threads(int threads);
+int orc_get_threads(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,267 @@
+"""ctypes loader for the C oracle (oracle/focr_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, by ``__graft_entry__.smoke()``
+as the checker, and by bench.py's ``cpu_baseline`` leg. The product library
+never loads it. Each wrapper names the reference function its C body follows
+(see the C file for file:line citations).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import numpy as np
+
+_HERE = Path(__file__).resolve().parent
+_BUILD = _HERE / "_build"
+
+STORE, GLU, ADD = 0, 1, 2
+
+
+def _cpu_has_v3() -> bool:
+    try:
+        flags = Path("/proc/cpuinfo").read_text().split("flags", 2)[1].split("\n", 1)[0].split()
+    except (OSError, IndexError):
+        return False
+    return all(f in flags for f in ("avx2", "fma", "bmi2", "movbe"))
+
+
+def build() -> None:
+    """Compile the oracle (gcc, oracle/Makefile)."""
+    import subprocess
+
+    subprocess.run(["make", "-s", "-C", str(_HERE)], check=True)
+
+
+def _load() -> ctypes.CDLL:
+    name = "liboracle_v3.so" if _cpu_has_v3() else "liboracle_generic.so"
+    path = _BUILD / name
+    if not path.exists():
+        build()
+    return ctypes.CDLL(str(path))
+
+
+_lib = _load()
+_P = ctypes.c_void_p
+_Z = ctypes.c_size_t
+_I = ctypes.c_int
+_F = ctypes.c_float
+
+
+def _sig(name, restype, *args):
+    fn = getattr(_lib, name)
+    fn.restype = restype
+    fn.argtypes = list(args)
+    return fn
+
+
+_sig("orc_exp_poly", _F, _F)
+_sig("orc_exp_poly_unchecked", _F, _F)
+_sig("orc_squared_relu_glu", _F, _F, _F)
+_sig("orc_quantize_bits", _I, _P, _Z, _Z, _Z, _I, _P, _P)
+_sig("orc_dequantize", None, _I, _P, _P, _Z, _Z, _Z, _P, _P, _Z, _P)
+_sig("orc_validate_w8", _I, _Z, _Z, _Z, _P, _P)
+_sig("orc_dot", _F, _P, _P, _Z)
+_sig("orc_dot_q", _F, _I, _P, _P, _P, _Z, _Z)
+_sig("orc_linear_decode", None, _I, _P, _P, _Z, _Z, _Z, _P, _P, _Z, _P, _Z, _P)
+_sig("orc_linear_decode_glu", None, _I, _P, _P, _Z, _Z, _Z, _P, _P, _Z, _P, _Z, _P)
+_sig("orc_rms_scale", _F, _P, _Z, _F)
+_sig("orc_row_scales", None, _P, _Z, _Z, _F, _P)
+_sig("orc_panel_gemm", None, _P, _Z, _Z, _P, _Z, _P, _I, _P)
+_sig("orc_i16_quantize_group", _F, _P, _P)
+_sig("orc_i16_quantize_rows", None, _P, _Z, _Z, _P, _Z, _P, _P, _P, _P)
+_sig("orc_i16_gemm", None, _P, _Z, _Z, _P, _P, _Z, _P, _P, _Z, _P, _I, _P)
+_sig("orc_attention_prefill", None, _P, _P, _P, _P, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _P, _I, _I, _P)
+_sig("orc_attention_prefill_tiles", None, _P, _P, _P, _P, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _P, _I, _I, _Z, _Z, _P)
+_sig("orc_argmax", _I, _P, _Z, _P)
+_sig("orc_set_threads", None, _I)
+_sig("orc_get_threads", _I)
+
+
+def _ptr(a):
+    if a is None:
+        return None
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def set_threads(n: int) -> None:
+    _lib.orc_set_threads(int(n))
+
+
+def threads() -> int:
+    return _lib.orc_get_threads()
+
+
+set_threads(1)
+
+
+def exp_poly(x: float) -> float:
+    return _lib.orc_exp_poly(x)
+
+
+def exp_poly_unchecked(x: float) -> float:
+    return _lib.orc_exp_poly_unchecked(x)
+
+
+def squared_relu_glu(gate: float, up: float) -> float:
+    return _lib.orc_squared_relu_glu(gate, up)
+
+
+def quantize_bits(w, n, k, group, bits):
+    """QuantLinear::quantize_bits (src/quant/linear.rs:140-201) -> (codes, scales) or error code."""
+    w = _f32(w)
+    codes = np.zeros(n * k, dtype=np.int8 if bits == 8 else np.int16)
+    scales = np.zeros(n * ((k + group - 1) // group), dtype=np.float32)
+    rc = _lib.orc_quantize_bits(_ptr(w), n, k, group, bits, _ptr(codes), _ptr(scales))
+    if rc != 0:
+        return rc
+    return codes.reshape(n, k), scales.reshape(n, -1)
+
+
+def _exc(exc_cols, exc_vals):
+    if exc_cols is None or len(exc_cols) == 0:
+        return None, None, 0
+    cols = np.ascontiguousarray(exc_cols, dtype=np.int32)
+    vals = _f32(exc_vals)
+    return cols, vals, len(cols)
+
+
+def dequantize(bits, codes, scales, n, k, group, exc_cols=None, exc_vals=None):
+    """dequantize_row for every row (src/quant/linear.rs:246-262)."""
+    codes = np.ascontiguousarray(codes)
+    scales = _f32(scales)
+    cols, vals, ne = _exc(exc_cols, exc_vals)
+    out = np.zeros((n, k), dtype=np.float32)
+    _lib.orc_dequantize(bits, _ptr(codes), _ptr(scales), n, k, group, _ptr(cols), _ptr(vals), ne, _ptr(out))
+    return out
+
+
+def validate_w8(n, k, group, codes, scales) -> int:
+    codes = np.ascontiguousarray(codes, dtype=np.int8)
+    scales = _f32(scales)
+    return _lib.orc_validate_w8(n, k, group, _ptr(codes), _ptr(scales))
+
+
+def dot(a, b) -> float:
+    a, b = _f32(a), _f32(b)
+    return _lib.orc_dot(_ptr(a), _ptr(b), a.size)
+
+
+def dot_q(bits, x, codes, scales, group) -> float:
+    x, scales, codes = _f32(x), _f32(scales), np.ascontiguousarray(codes)
+    return _lib.orc_dot_q(bits, _ptr(x), _ptr(codes), _ptr(scales), x.size, group)
+
+
+def linear_decode(bits, codes, scales, n, k, group, x, rows, exc_cols=None, exc_vals=None):
+    """QuantLinear::linear small-M (bits 8/16) or linear_with_simd rows<=8 (bits 32)."""
+    codes = np.ascontiguousarray(codes)
+    scales = _f32(scales) if scales is not None else np.zeros(1, np.float32)
+    x = _f32(x)
+    cols, vals, ne = _exc(exc_cols, exc_vals)
+    out = np.zeros((rows, n), dtype=np.float32)
+    _lib.orc_linear_decode(bits, _ptr(codes), _ptr(scales), n, k, group, _ptr(cols), _ptr(vals), ne, _ptr(x), rows, _ptr(out))
+    return out
+
+
+def linear_decode_glu(bits, codes, scales, n, k, group, x, rows, exc_cols=None, exc_vals=None):
+    codes = np.ascontiguousarray(codes)
+    scales = _f32(scales) if scales is not None else np.zeros(1, np.float32)
+    x = _f32(x)
+    cols, vals, ne = _exc(exc_cols, exc_vals)
+    out = np.zeros((rows, n // 2), dtype=np.float32)
+    _lib.orc_linear_decode_glu(bits, _ptr(codes), _ptr(scales), n, k, group, _ptr(cols), _ptr(vals), ne, _ptr(x), rows, _ptr(out))
+    return out
+
+
+def rms_scale(row, eps=float(np.finfo(np.float32).eps)) -> float:
+    row = _f32(row)
+    return _lib.orc_rms_scale(_ptr(row), row.size, eps)
+
+
+def row_scales(h, width, eps=float(np.finfo(np.float32).eps)):
+    h = _f32(h)
+    rows = h.size // width
+    out = np.zeros(rows, dtype=np.float32)
+    _lib.orc_row_scales(_ptr(h), rows, width, eps, _ptr(out))
+    return out
+
+
+def panel_gemm(a, m, k, w, n, row_scale=None, epilogue=STORE, out=None):
+    """FP32 panel GEMM (src/kernels/panels/panel.rs:118-172) on dequantized w [n][k]."""
+    a, w = _f32(a), _f32(w)
+    rs = _f32(row_scale) if row_scale is not None else None
+    width = n // 2 if epilogue == GLU else n
+    if out is None:
+        out = np.zeros((m, width), dtype=np.float32)
+    else:
+        out = _f32(out).copy()
+    _lib.orc_panel_gemm(_ptr(a), m, k, _ptr(w), n, _ptr(rs), epilogue, _ptr(out))
+    return out
+
+
+def i16_quantize_group(x):
+    x = _f32(x)
+    assert x.size == 64
+    q = np.zeros(64, dtype=np.int16)
+    step = _lib.orc_i16_quantize_group(_ptr(x), _ptr(q))
+    return np.float32(step), q
+
+
+def i16_quantize_rows(a, m, k, row_scale=None, exc_cols=None):
+    a = _f32(a)
+    rs = _f32(row_scale) if row_scale is not None else None
+    cols = np.ascontiguousarray(exc_cols, dtype=np.int32) if exc_cols is not None and len(exc_cols) else None
+    ne = 0 if cols is None else len(cols)
+    codes = np.zeros((m, k), dtype=np.int16)
+    steps = np.zeros((m, k // 64), dtype=np.float32)
+    xe = np.zeros((m, max(ne, 1)), dtype=np.float32)
+    _lib.orc_i16_quantize_rows(_ptr(a), m, k, _ptr(cols), ne, _ptr(rs), _ptr(codes), _ptr(steps), _ptr(xe))
+    return codes, steps, xe[:, :ne]
+
+
+def i16_gemm(a, m, k, codes, scales, n, row_scale=None, epilogue=STORE, exc_cols=None, exc_vals=None, out=None):
+    """INT16-activation panel GEMM (src/kernels/panels/panel_i16.rs:133-369)."""
+    a = _f32(a)
+    codes = np.ascontiguousarray(codes, dtype=np.int8)
+    scales = _f32(scales)
+    rs = _f32(row_scale) if row_scale is not None else None
+    cols, vals, ne = _exc(exc_cols, exc_vals)
+    width = n // 2 if epilogue == GLU else n
+    if out is None:
+        out = np.zeros((m, width), dtype=np.float32)
+    else:
+        out = _f32(out).copy()
+    _lib.orc_i16_gemm(_ptr(a), m, k, _ptr(codes), _ptr(scales), n, _ptr(cols), _ptr(vals), ne, _ptr(rs), epilogue, _ptr(out))
+    return out
+
+
+def attention_prefill(q, prefix_k, v, query_len, prefix_len, total_len, n_heads, n_kv_heads,
+                      query_offset, image_start, image_end, sinks, static=False, exp_fast=True,
+                      generated_k=None, tiles=None):
+    """compact_prefill (src/kernels/attention/prefill64.rs:149-480), head_dim 64."""
+    q, prefix_k, v, sinks = _f32(q), _f32(prefix_k), _f32(v), _f32(sinks)
+    gk = _f32(generated_k) if generated_k is not None else None
+    out = np.zeros(query_len * n_heads * 64, dtype=np.float32)
+    if tiles is None:
+        _lib.orc_attention_prefill(_ptr(q), _ptr(prefix_k), _ptr(gk), _ptr(v), query_len, prefix_len, total_len,
+                                   n_heads, n_kv_heads, query_offset, image_start, image_end, _ptr(sinks),
+                                   int(static), int(exp_fast), _ptr(out))
+    else:
+        _lib.orc_attention_prefill_tiles(_ptr(q), _ptr(prefix_k), _ptr(gk), _ptr(v), query_len, prefix_len,
+                                         total_len, n_heads, n_kv_heads, query_offset, image_start, image_end,
+                                         _ptr(sinks), int(static), int(exp_fast), tiles[0], tiles[1], _ptr(out))
+    return out.reshape(query_len, n_heads, 64)
+
+
+def argmax(logits):
+    logits = _f32(logits)
+    out = ctypes.c_uint32(0)
+    rc = _lib.orc_argmax(_ptr(logits), logits.size, ctypes.byref(out))
+    if rc != 0:
+        raise ValueError("nonfinite or empty logits")
+    return int(out.value)

@@ -1,0 +1,90 @@
+"""Prefill attention on the GPU against the oracle within the FP32 tolerance
+(src/kernels/attention/prefill64/tests.rs:36-84, static_shift/tests.rs)."""
+import numpy as np
+import pytest
+
+import gen
+import oracle
+from gpu_util import host, max_rel, to_dev
+
+pytestmark = pytest.mark.gpu
+
+CASES = [(70, 3, 65), (300, 5, 262), (257, 0, 257), (160, 16, 144), (129, 1, 128), (40, 0, 3), (95, 10, 90), (600, 0, 0)]
+
+
+@pytest.fixture(scope="module")
+def fh():
+    import focr_hip
+
+    return focr_hip
+
+
+def close(got, want):
+    # The reference's own FP32 attention tolerance (prefill64/tests.rs:76-81)
+    # and the north-star metric max|d| / max|ref| <= 1e-5.
+    assert np.all(np.abs(got - want) <= 1e-5 * (1.0 + np.abs(want))), float(np.max(np.abs(got - want)))
+    assert max_rel(got, want) <= 1e-5
+
+
+def run(fh, q, k, v, sinks, L, geometry, options, prefix=None, total=None, generated=None, n_heads=16, n_kv=8):
+    prefix = L if prefix is None else prefix
+    total = L if total is None else total
+    kv = fh.CompactKv(to_dev(k), None if generated is None else to_dev(generated), to_dev(v), prefix, total,
+                      n_heads, n_kv, 64)
+    out = fh.attention_with(to_dev(q), kv, L, fh.Geometry(*geometry), to_dev(sinks), options)
+    return host(out)
+
+
+@pytest.mark.parametrize("L,image_start,image_end", CASES)
+@pytest.mark.parametrize("exp", ["fast", "exact"])
+def test_online_prefill(fh, L, image_start, image_end, exp):
+    q = gen.att_values(L * 16 * 64, 17 + L, 3.0)
+    k = gen.att_values(L * 16 * 64, 19 + L, 3.0)
+    v = gen.att_values(L * 8 * 64, 23 + L, 3.0)
+    sinks = gen.att_values(16, 29, 2.0)
+    opts = fh.PrefillOptions(exp=fh.ExpMode.FAST if exp == "fast" else fh.ExpMode.EXACT)
+    got = run(fh, q, k, v, sinks, L, (0, image_start, image_end), opts)
+    want = oracle.attention_prefill(q, k, v, L, L, L, 16, 8, 0, image_start, image_end, sinks, exp_fast=exp == "fast")
+    close(got, want)
+
+
+@pytest.mark.parametrize("L,image_start,image_end", CASES[:4])
+def test_static_prefill(fh, L, image_start, image_end):
+    q = gen.normalized(L * 16 * 64, 17 + L)
+    k = gen.normalized(L * 16 * 64, 19 + L)
+    v = gen.values(L * 8 * 64, 23 + L, 3.0)
+    sinks = gen.values(16, 29, 2.0)
+    got = run(fh, q, k, v, sinks, L, (0, image_start, image_end), fh.PrefillOptions(fp32_softmax=fh.Softmax.STATIC))
+    want = oracle.attention_prefill(q, k, v, L, L, L, 16, 8, 0, image_start, image_end, sinks, static=True)
+    close(got, want)
+
+
+@pytest.mark.parametrize("L,prefix,total,offset,image", [(4, 137, 141, 137, (1, 129)), (9, 128, 137, 128, (1, 129)),
+                                                         (33, 100, 133, 100, (1, 90)), (40, 3, 43, 3, (1, 3)),
+                                                         (5, 250, 300, 295, (0, 0))])
+def test_generated_keys(fh, L, prefix, total, offset, image):
+    # prefill64/tests.rs:89-153 (mixed caches)
+    q = gen.att_values(L * 16 * 64, 71, 3.0)
+    pk = gen.att_values(prefix * 16 * 64, 83, 3.0)
+    gk = gen.att_values((total - prefix) * 8 * 64, 37, 3.0)
+    v = gen.att_values(total * 8 * 64, 117, 3.0)
+    sinks = gen.att_values(16, 29, 2.0)
+    got = run(fh, q, pk, v, sinks, L, (offset, *image), fh.PrefillOptions(), prefix=prefix, total=total, generated=gk)
+    want = oracle.attention_prefill(q, pk, v, L, prefix, total, 16, 8, offset, image[0], image[1], sinks, generated_k=gk)
+    close(got, want)
+
+
+def test_config4_full_page(fh):
+    # 6,544 tokens, 16 heads x 64, image prefix 4,096, Q/K/V ~ N(0,1).
+    L, image_end = 6544, 4096
+    q = gen.normal(L * 16 * 64, 1.0, 20)
+    k = gen.normal(L * 16 * 64, 1.0, 21)
+    v = gen.normal(L * 8 * 64, 1.0, 22)
+    sinks = gen.uniform(16, -2.0, 2.0, 23)
+    got = run(fh, q, k, v, sinks, L, (0, 0, image_end), fh.PrefillOptions())
+    assert np.all(np.isfinite(got))
+    # Oracle on sample query tiles: image-only, straddling, causal, last.
+    for t0, t1 in ((0, 2), (127, 129), (170, 172), (203, 205)):
+        want = oracle.attention_prefill(q, k, v, L, L, L, 16, 8, 0, 0, image_end, sinks, tiles=(t0, t1))
+        sl = slice(t0 * 32, min(t1 * 32, L))
+        close(got[sl], want[sl])

@@ -1,0 +1,155 @@
+"""Decode/verify GEMV and dequantization on the GPU against the oracle, bitwise
+(src/quant/linear/integrated_tests.rs, src/kernels/tests.rs)."""
+import math
+
+import numpy as np
+import pytest
+
+import gen
+import oracle
+from gpu_util import F32, assert_bitwise, host, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def fh():
+    import focr_hip
+
+    return focr_hip
+
+
+def quantized(bits, n, k, group, seed, exc=None):
+    """Matrix codes as quantize_bits makes them, with exception columns zeroed."""
+    w = ((np.arange(n * k) * 7919 % 2003).astype(np.float32) - F32(1001.0)) / F32(977.0)
+    w = (w * (gen.values(n * k, seed) + F32(1.5))).astype(np.float32).reshape(n, k)
+    vals = None
+    if exc:
+        vals = w[:, exc].copy() * F32(300.0)
+        w[:, exc] = 0.0
+    codes, scales = oracle.quantize_bits(w, n, k, group, bits)
+    return codes, scales, vals
+
+
+@pytest.mark.parametrize("bits", [8, 16])
+@pytest.mark.parametrize("k,group", [(768, 64), (1024, 64), (2304, 64), (65, 64), (31, 32), (100, 32), (768, 128), (520, 64)])
+def test_decode_is_bitwise_the_reference_dot(fh, bits, k, group):
+    n = 37
+    codes, scales, _ = quantized(bits, n, k, group, 3)
+    lin = fh.QuantLinear(bits, codes, scales, group)
+    for rows in range(1, 9):
+        x = ((np.arange(rows * k) * 104729 % 1009).astype(np.float32) - F32(504.0)) / F32(311.0)
+        got = host(lin.linear(to_dev(x), rows))
+        want = oracle.linear_decode(bits, codes, scales, n, k, group, x, rows)
+        assert_bitwise(got, want, f"bits {bits} k {k} g {group} rows {rows}")
+
+
+@pytest.mark.parametrize("bits", [8, 16])
+@pytest.mark.parametrize("n,k,group,columns", [(37, 768, 64, [0]), (5, 1024, 64, [3, 511, 1023]),
+                                              (3, 2304, 64, [17, 18, 1500, 2303]), (4, 65, 64, [64]),
+                                              (2, 31, 32, [0, 30]), (37, 768, 32, [100, 700])])
+def test_decode_exception_columns_in_ascending_order(fh, bits, n, k, group, columns):
+    # integrated_tests.rs:195-252
+    codes, scales, vals = quantized(bits, n, k, group, 5, exc=columns)
+    lin = fh.QuantLinear(bits, codes, scales, group, exc_cols=columns, exc_vals=vals)
+    for rows in (1, 3, 8):
+        x = ((np.arange(rows * k) * 104729 % 1009).astype(np.float32) - F32(504.0)) / F32(311.0)
+        got = host(lin.linear(to_dev(x), rows))
+        want = oracle.linear_decode(bits, codes, scales, n, k, group, x, rows, exc_cols=columns, exc_vals=vals)
+        assert_bitwise(got, want, f"exceptions bits {bits} rows {rows}")
+
+
+@pytest.mark.parametrize("in_dim,ffn", [(768, 2304), (65, 19), (1, 1), (1024, 64)])
+def test_fp32_decode_and_glu(fh, in_dim, ffn):
+    # src/kernels/tests.rs:48-82 (NaN, signed zeros, negatives in the weights)
+    w = gen.values(2 * ffn * in_dim, 7)
+    idx = np.arange(0, w.size, 97)
+    w[idx] = np.array([math.nan, 0.0, -0.0, -3.0], np.float32)[idx % 4]
+    w = w.reshape(2 * ffn, in_dim)
+    lin = fh.Linear.from_f32(w)
+    for rows in range(1, 9):
+        x = gen.values(rows * in_dim, 11 + rows)
+        packed = host(lin.linear(to_dev(x), rows))
+        assert_bitwise(packed, oracle.linear_decode(32, w, None, 2 * ffn, in_dim, 32, x, rows), f"fp32 rows {rows}")
+        fused = host(lin.linear_glu(to_dev(x), rows))
+        assert_bitwise(fused, oracle.linear_decode_glu(32, w, None, 2 * ffn, in_dim, 32, x, rows), f"glu rows {rows}")
+
+
+def test_fp32_linear_kat(fh):
+    # src/kernels/tests.rs:109-117
+    lin = fh.Linear.from_f32(np.array([[1, 10, 100], [-1, -2, -3]], np.float32))
+    out = host(lin.linear(to_dev(np.array([1, 2, 3, 4, 5, 6], np.float32)), 2))
+    assert out.ravel().tolist() == [321.0, -14.0, 654.0, -32.0]
+
+
+@pytest.mark.parametrize("bits", [8, 16])
+def test_quantized_glu(fh, bits):
+    n, k = 2 * 96, 768
+    codes, scales, vals = quantized(bits, n, k, 64, 9, exc=[5, 700])
+    lin = fh.QuantLinear(bits, codes, scales, 64, exc_cols=[5, 700], exc_vals=vals)
+    for rows in (1, 5, 8):
+        x = gen.values(rows * k, 13 + rows) * F32(2.0)
+        got = host(lin.linear_glu(to_dev(x), rows))
+        want = oracle.linear_decode_glu(bits, codes, scales, n, k, 64, x, rows, exc_cols=[5, 700], exc_vals=vals)
+        assert_bitwise(got, want, f"glu bits {bits} rows {rows}")
+
+
+@pytest.mark.parametrize("rows", [1, 5])
+def test_config2_int16_gemv_full_size(fh, rows):
+    # W[4096 x 1024] int16 over [-32768, 32767], scales U(1e-6, 4e-6).
+    n, k = 4096, 1024
+    codes = gen.codes_uniform((n, k), -32768, 32767, np.int16, 1)
+    scales = gen.uniform((n, k // 64), 1e-6, 4e-6, 2)
+    x = gen.normal((rows, k), 1.0, 3)
+    lin = fh.QuantLinear(16, codes, scales, 64)
+    got = host(lin.linear(to_dev(x), rows))
+    assert_bitwise(got, oracle.linear_decode(16, codes, scales, n, k, 64, x, rows), f"config 2 rows {rows}")
+
+
+def test_config3_int8_gemv_full_size(fh):
+    n, k = 4096, 1024
+    codes = gen.codes_uniform((n, k), -127, 127, np.int8, 4)
+    scales = gen.uniform((n, k // 64), 1e-4, 4e-4, 5)
+    x = gen.normal((1, k), 1.0, 6)
+    lin = fh.QuantLinear(8, codes, scales, 64)
+    got = host(lin.linear(to_dev(x), 1))
+    assert_bitwise(got, oracle.linear_decode(8, codes, scales, n, k, 64, x, 1), "config 3 GEMV")
+
+
+@pytest.mark.parametrize("bits,group", [(8, 64), (16, 64), (8, 32), (16, 128)])
+def test_dequantize_is_bit_exact(fh, bits, group):
+    n, k = 48, 300
+    codes, scales, vals = quantized(bits, n, k, group, 11, exc=[0, 299])
+    scales = scales.copy()
+    scales[0, 0] = np.float32(3e-39)  # subnormal scale
+    lin = fh.QuantLinear(bits, codes, scales, group, exc_cols=[0, 299], exc_vals=vals)
+    got = host(lin.dequantize())
+    assert_bitwise(got, oracle.dequantize(bits, codes, scales, n, k, group, [0, 299], vals), "dequant")
+
+
+def test_w8_validation(fh):
+    # src/quant/linear/integrated_tests.rs:455-460
+    with pytest.raises(fh.FocrError, match="-128"):
+        fh.QuantLinear.from_parts(1, 1, 64, np.array([-128], np.int8), [1.0])
+    with pytest.raises(fh.FocrError):
+        fh.QuantLinear.from_parts(1, 1, 64, np.array([1], np.int8), [0.0])
+    with pytest.raises(fh.FocrError):
+        fh.QuantLinear.from_parts(1, 1, 64, np.array([0], np.int8), [math.nan])
+    with pytest.raises(fh.FocrError, match="sorted"):
+        fh.QuantLinear(8, np.zeros((2, 64), np.int8), np.ones((2, 1), np.float32), 64, exc_cols=[5, 3],
+                       exc_vals=np.zeros((2, 2), np.float32))
+    with pytest.raises(fh.FocrError, match="nonzero code"):
+        fh.QuantLinear(8, np.ones((2, 64), np.int8), np.ones((2, 1), np.float32), 64, exc_cols=[3],
+                       exc_vals=np.zeros((2, 1), np.float32))
+
+
+def test_shape_errors(fh):
+    import torch
+
+    lin = fh.QuantLinear(8, np.ones((32, 64), np.int8), np.ones((32, 1), np.float32), 64)
+    x = torch.zeros(9 * 64, device="cuda:0")
+    with pytest.raises(fh.FocrError):
+        lin.linear(x, 9)  # decode takes 1..=8 rows
+    odd = fh.QuantLinear(8, np.ones((3, 64), np.int8), np.ones((3, 1), np.float32), 64)
+    with pytest.raises(fh.FocrError, match="GLU"):
+        odd.linear_glu(torch.zeros(64, device="cuda:0"), 1)

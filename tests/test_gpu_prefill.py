@@ -1,0 +1,170 @@
+"""Prefill projections on the GPU against the oracle:
+INT16 panels bitwise (src/kernels/panels/panel_i16/tests.rs), FP32 exact-order
+panels bitwise and FP32 matrix cores within the FP32 tolerance
+(src/kernels/panels/panel.rs:243-299)."""
+import numpy as np
+import pytest
+
+import gen
+import oracle
+from gpu_util import EPS, F32, assert_bitwise, host, max_rel, to_dev
+
+pytestmark = pytest.mark.gpu
+
+I16_SHAPES = [(1, 64, 32), (13, 768, 64), (97, 1024, 32), (50, 2304, 64), (7, 128, 96), (200, 768, 160), (130, 256, 416)]
+
+
+@pytest.fixture(scope="module")
+def fh():
+    import focr_hip
+
+    return focr_hip
+
+
+def run_prefill(fh, lin, a, m, rs, epi, kernel, base=None):
+    out = None if base is None else to_dev(base)
+    got = lin.prefill(to_dev(a), m, row_scale=None if rs is None else to_dev(rs), epilogue=epi, out=out, kernel=kernel)
+    return host(got)
+
+
+@pytest.mark.parametrize("m,k,n", I16_SHAPES)
+def test_i16_panels_bitwise_every_epilogue(fh, m, k, n):
+    a = gen.i16_activations(m, k)
+    codes, scales = gen.i16_weights(n, k)
+    rs = (F32(0.25) + np.arange(m, dtype=np.float32) / F32(9.0)).astype(np.float32)
+    base = ((np.arange(m * n) % 13).astype(np.float32) - F32(6.0)).reshape(m, n)
+    lin = fh.QuantLinear(8, codes, scales, 64)
+    I16 = fh.PrefillProjection.I16
+    assert_bitwise(run_prefill(fh, lin, a, m, rs, fh.Epilogue.STORE, I16),
+                   oracle.i16_gemm(a, m, k, codes, scales, n, row_scale=rs), "store")
+    assert_bitwise(run_prefill(fh, lin, a, m, None, fh.Epilogue.GLU, I16),
+                   oracle.i16_gemm(a, m, k, codes, scales, n, epilogue=oracle.GLU), "glu")
+    assert_bitwise(run_prefill(fh, lin, a, m, rs, fh.Epilogue.ADD, I16, base=base),
+                   oracle.i16_gemm(a, m, k, codes, scales, n, row_scale=rs, epilogue=oracle.ADD, out=base), "add")
+
+
+@pytest.mark.parametrize("m,k,n", [(13, 768, 64), (50, 2304, 64), (97, 1024, 32)])
+def test_i16_exception_columns(fh, m, k, n):
+    # panel_i16/tests.rs:156-227: two pairs share a group; huge inputs there.
+    columns = [0, 1, k // 2, k // 2 + 1, k - 1]
+    vals = (gen.noise(np.arange(n * len(columns), dtype=np.uint64), 4) * F32(0.1)).reshape(n, len(columns))
+    a = gen.i16_activations(m, k).reshape(m, k)
+    codes, scales = gen.i16_weights(n, k)
+    codes = codes.copy()
+    codes[:, columns] = 0
+    for c in columns:
+        a[:, c] = F32(100000.0) * (F32(1.0) + gen.noise(np.array([c], np.uint64), 5)[0])
+    rs = (F32(0.25) + np.arange(m, dtype=np.float32) / F32(9.0)).astype(np.float32)
+    lin = fh.QuantLinear(8, codes, scales, 64, exc_cols=columns, exc_vals=vals)
+    I16 = fh.PrefillProjection.I16
+    for epi, o_epi, r in ((fh.Epilogue.STORE, oracle.STORE, rs), (fh.Epilogue.GLU, oracle.GLU, None)):
+        got = run_prefill(fh, lin, a, m, r, epi, I16)
+        want = oracle.i16_gemm(a, m, k, codes, scales, n, row_scale=r, epilogue=o_epi, exc_cols=columns, exc_vals=vals)
+        assert_bitwise(got, want, f"exceptions {epi.name}")
+
+
+def test_i16_nonfinite_zero_and_tiny_rows(fh):
+    # panel_i16/tests.rs:307-355
+    m, k, n = 8, 128, 32
+    a = gen.i16_activations(m, k)
+    a[5] = np.nan
+    a[k + 70] = np.inf
+    a[3 * k:4 * k] = 0.0
+    for row, mag in enumerate([1e-35, 1e-37, 1e-38, np.array([1], np.uint32).view(np.float32)[0]]):
+        a[(row + 4) * k:(row + 5) * k] = mag
+    codes, scales = gen.i16_weights(n, k)
+    lin = fh.QuantLinear(8, codes, scales, 64)
+    got = run_prefill(fh, lin, a, m, None, fh.Epilogue.STORE, fh.PrefillProjection.I16)
+    want = oracle.i16_gemm(a, m, k, codes, scales, n)
+    assert_bitwise(got, want, "edge rows")
+    assert np.all(np.isnan(got[0])) and np.all(got[3].view(np.uint32) == 0) and np.all(got[7] == 0)
+    tiny = a[4 * k:]
+    rs = np.array([1.0, 2.0, 1024.0, 1e6], np.float32)
+    got = run_prefill(fh, lin, tiny, 4, rs, fh.Epilogue.STORE, fh.PrefillProjection.I16)
+    assert_bitwise(got, oracle.i16_gemm(tiny, 4, k, codes, scales, n, row_scale=rs), "tiny rows scaled")
+
+
+def test_i16_rejects_matrices_the_panels_cannot_hold(fh):
+    import torch
+
+    lin = fh.QuantLinear(16, np.zeros((32, 64), np.int16), np.ones((32, 1), np.float32), 64)
+    with pytest.raises(fh.FocrError, match="fits_i16_panels"):
+        lin.prefill(torch.zeros(9 * 64, device="cuda:0"), 9, kernel=fh.PrefillProjection.I16)
+
+
+def test_config3_int8_prefill_full_size(fh):
+    # BASELINE config 3 (literal shape): X[6544 x 1024] ~ N(0,1), W 4096 x 1024 int8, scales U(1e-4, 4e-4).
+    m, k, n = 6544, 1024, 4096
+    a = gen.normal((m, k), 1.0, 7)
+    codes = gen.codes_uniform((n, k), -127, 127, np.int8, 8)
+    scales = gen.uniform((n, k // 64), 1e-4, 4e-4, 9)
+    lin = fh.QuantLinear(8, codes, scales, 64)
+    got = run_prefill(fh, lin, a, m, None, fh.Epilogue.STORE, fh.PrefillProjection.I16)
+    # Bitwise on a row sample (the oracle takes seconds per 100 rows).
+    rows = np.r_[0:64, 3000:3040, m - 64:m]
+    want = oracle.i16_gemm(a[rows], len(rows), k, codes, scales, n)
+    assert_bitwise(got[rows], want, "config 3 sample rows")
+    assert np.all(np.isfinite(got))
+
+
+F32_SHAPES = [(1, 64, 16), (13, 768, 48), (97, 1024, 32), (200, 2304, 64), (9, 7, 16), (130, 300, 160)]
+
+
+@pytest.mark.parametrize("bits", [32, 16, 8])
+@pytest.mark.parametrize("m,k,n", F32_SHAPES)
+def test_f32_chain_is_bitwise_the_panels(fh, bits, m, k, n):
+    a = gen.matrix(m * k, 1).reshape(m, k)
+    w = gen.matrix(n * k, 2).reshape(n, k)
+    if bits == 32:
+        lin, dense = fh.Linear.from_f32(w), w
+    else:
+        codes, scales = oracle.quantize_bits(w, n, k, 64, bits)
+        lin = fh.QuantLinear(bits, codes, scales, 64)
+        dense = oracle.dequantize(bits, codes, scales, n, k, 64)
+    rs = (F32(0.5) + np.arange(m, dtype=np.float32) / F32(7.0)).astype(np.float32)
+    base = ((np.arange(m * n) % 17).astype(np.float32) - F32(8.0)).reshape(m, n)
+    CH = fh.PrefillProjection.F32_CHAIN
+    assert_bitwise(run_prefill(fh, lin, a, m, rs, fh.Epilogue.STORE, CH), oracle.panel_gemm(a, m, k, dense, n, row_scale=rs), "store")
+    assert_bitwise(run_prefill(fh, lin, a, m, None, fh.Epilogue.GLU, CH),
+                   oracle.panel_gemm(a, m, k, dense, n, epilogue=oracle.GLU), "glu")
+    assert_bitwise(run_prefill(fh, lin, a, m, None, fh.Epilogue.ADD, CH, base=base),
+                   oracle.panel_gemm(a, m, k, dense, n, epilogue=oracle.ADD, out=base), "add")
+
+
+@pytest.mark.parametrize("bits", [32, 16, 8])
+@pytest.mark.parametrize("m,k,n", F32_SHAPES)
+def test_f32_mfma_within_fp32_tolerance(fh, bits, m, k, n):
+    a = gen.matrix(m * k, 3).reshape(m, k)
+    w = gen.matrix(n * k, 4).reshape(n, k)
+    if bits == 32:
+        lin, dense = fh.Linear.from_f32(w), w
+    else:
+        codes, scales = oracle.quantize_bits(w, n, k, 64, bits)
+        lin = fh.QuantLinear(bits, codes, scales, 64)
+        dense = oracle.dequantize(bits, codes, scales, n, k, 64)
+    rs = (F32(0.5) + np.arange(m, dtype=np.float32) / F32(7.0)).astype(np.float32)
+    got = run_prefill(fh, lin, a, m, rs, fh.Epilogue.STORE, fh.PrefillProjection.F32_MFMA)
+    want = oracle.panel_gemm(a, m, k, dense, n, row_scale=rs)
+    ad = (a * rs[:, None]).astype(np.float32).astype(np.float64)
+    mag = np.abs(ad) @ np.abs(dense.astype(np.float64)).T
+    # Both orders are within (k-1) eps sum|a w| of the exact product.
+    assert np.all(np.abs(got.astype(np.float64) - want) <= 2 * k * EPS * mag + 1e-30)
+    assert max_rel(got, want) <= 1e-5
+    glu = run_prefill(fh, lin, a, m, rs, fh.Epilogue.GLU, fh.PrefillProjection.F32_MFMA)
+    g, u = got[:, 0::2], got[:, 1::2]
+    assert_bitwise(glu, (np.where(g > 0, g, F32(0)) ** 2 * u).astype(np.float32), "glu of store")
+
+
+@pytest.mark.parametrize("name,k,n,epi", [("qkv", 768, 2048, 0), ("wo", 1024, 768, 2), ("w13", 768, 4608, 1),
+                                          ("w2", 2304, 768, 2), ("literal", 1024, 4096, 0)])
+def test_config1_fp32_gemm_checkpoint_shapes(fh, name, k, n, epi):
+    # X ~ N(0,1), W ~ N(0, 0.02), m = 6544; tolerance on a row sample.
+    m = 6544
+    a = gen.normal((m, k), 1.0, 10)
+    w = gen.normal((n, k), 0.02, 11)
+    lin = fh.Linear.from_f32(w)
+    base = gen.normal((m, n), 1.0, 12) if epi == 2 else None
+    got = run_prefill(fh, lin, a, m, None, fh.Epilogue(epi), fh.PrefillProjection.F32_MFMA, base=base)
+    rows = np.r_[0:32, m - 32:m]
+    want = oracle.panel_gemm(a[rows], len(rows), k, w, n, epilogue=epi, out=None if base is None else base[rows])
+    assert max_rel(got[rows], want) <= 1e-5, name

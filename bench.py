@@ -1,0 +1,314 @@
+#!/usr/bin/env python3
+"""Benchmark of the hip backend's hot path on one MI355X.
+
+Headline: the near-exact INT16 group-64 decode GEMV,
+W[4096 x 1024] int16 codes uniform over [-32768, 32767], one FP32 scale per 64
+inputs ~ U(1e-6, 4e-6), X[1 x 1024] ~ N(0, 1). A step is one GEMV over one
+matrix; steps rotate through a pool of distinct device copies (> 512 MB, twice
+the 256 MB Infinity Cache) so every step streams its weights from HBM. The K
+timed steps are replayed from a HIP graph (captured launches of the C ABI),
+and `value` is algorithmic bytes / wall time over those K steps.
+
+`roofline` describes the GEMV kernel: algorithmic bytes per launch divided by
+the average launch duration, i.e. the HIP-event time of the K replayed launches
+(events recorded on the stream the kernels run on) divided by K. `per_op` reports the other BASELINE configurations on the
+same box (FP32 prefill GEMM, INT16-activation x INT8 prefill GEMM, INT8 GEMV,
+attention prefill). `cpu_baseline` times the C oracle (a restatement of the
+reference's CPU operator) on the host cores for a bounded sample.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--ops a,b] [--no-cpu]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for p in (ROOT / "falcon-ocr-cpu_amd", ROOT / "tests", ROOT / "oracle"):
+    sys.path.insert(0, str(p))
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
+FP32_MFMA_PEAK = 157.3  # TFLOP/s dense
+INT8_MFMA_PEAK = 5000.0  # TOP/s dense
+POOL_BYTES = 600 << 20  # > 2 x 256 MB Infinity Cache
+
+
+def gemv_bytes(n, k, rows, code_bytes, group=64):
+    """Algorithmic bytes of one decode GEMV: codes + scales + inputs + outputs."""
+    return n * k * code_bytes + 4 * n * (k // group) + 4 * rows * k + 4 * rows * n
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+class Timer:
+    """Per-launch HIP event pairs on torch's current stream (the stream the
+    library's context launches on)."""
+
+    def __init__(self, torch):
+        self.torch = torch
+
+    def per_launch_ms(self, fn, reps):
+        torch = self.torch
+        starts = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+        ends = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+        for i in range(reps):
+            starts[i].record()
+            fn(i)
+            ends[i].record()
+        torch.cuda.synchronize()
+        times = sorted(s.elapsed_time(e) for s, e in zip(starts, ends))
+        return sum(times) / len(times), times[len(times) // 2]
+
+
+def make_pool(fh, gen, np, bits, n, k, count_bytes, seed):
+    code_bytes = {8: 1, 16: 2}[bits]
+    lo, hi, dt = (-32768, 32767, np.int16) if bits == 16 else (-127, 127, np.int8)
+    codes = gen.codes_uniform((n, k), lo, hi, dt, seed)
+    scales = gen.uniform((n, k // 64), 1e-6, 4e-6, seed + 1) if bits == 16 else gen.uniform((n, k // 64), 1e-4, 4e-4, seed + 1)
+    per = n * k * code_bytes
+    copies = max(2, -(-count_bytes // per))
+    return codes, scales, [fh.QuantLinear(bits, codes, scales, 64) for _ in range(copies)]
+
+
+def bench_gemv(torch, fh, gen, np, bits, rows, steps, warmup, graph=True):
+    """Decode GEMV over a rotating pool; returns whole-job and per-launch numbers."""
+    n, k = 4096, 1024
+    codes, scales, pool = make_pool(fh, gen, np, bits, n, k, POOL_BYTES, 1 if bits == 16 else 4)
+    x = torch.from_numpy(gen.normal((rows, k), 1.0, 3)).cuda()
+    out = torch.empty((rows, n), device="cuda")
+    nbytes = gemv_bytes(n, k, rows, 2 if bits == 16 else 1)
+    step = lambda i: pool[i % len(pool)].linear(x, rows, out)
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    # Whole job: K steps replayed from a HIP graph (or launched directly).
+    ctx = fh.default_context()
+    stream = torch.cuda.current_stream()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    if graph:
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(stream)
+        with torch.cuda.stream(s):
+            ctx.use_stream(s)
+            with torch.cuda.graph(g, stream=s):
+                ctx.use_stream(torch.cuda.current_stream())
+                for i in range(steps):
+                    step(i)
+        stream.wait_stream(s)
+        ctx.use_stream(stream)
+        g.replay()
+        torch.cuda.synchronize()
+        run = g.replay
+    else:
+        def run():
+            for i in range(steps):
+                step(i)
+    # Timed region: barrier, events on the launch stream around the K steps.
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    run()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    avg_ms = ev0.elapsed_time(ev1) / steps
+    return {"bytes": nbytes, "wall_s": wall, "steps": steps, "avg_launch_ms": avg_ms,
+            "pool_copies": len(pool), "codes": codes, "scales": scales, "x": x}
+
+
+def bench_gemm(torch, fh, gen, np, reps):
+    """BASELINE config 1 (FP32, m = 6544) on the checkpoint shapes and the literal shape."""
+    m = 6544
+    shapes = [("qkv", 768, 2048, fh.Epilogue.STORE), ("wo", 1024, 768, fh.Epilogue.ADD),
+              ("w13", 768, 4608, fh.Epilogue.GLU), ("w2", 2304, 768, fh.Epilogue.ADD),
+              ("literal", 1024, 4096, fh.Epilogue.STORE)]
+    timer = Timer(torch)
+    res = {}
+    for name, k, n, epi in shapes:
+        a = torch.from_numpy(gen.normal((m, k), 1.0, 10)).cuda()
+        w = gen.normal((n, k), 0.02, 11)
+        lin = fh.Linear.from_f32(w)
+        width = n // 2 if epi == fh.Epilogue.GLU else n
+        out = torch.zeros((m, width), device="cuda")
+        for kern in (fh.PrefillProjection.F32_MFMA, fh.PrefillProjection.F32_CHAIN):
+            fn = lambda i: lin.prefill(a, m, epilogue=epi, out=out, kernel=kern)
+            for i in range(2):
+                fn(i)
+            avg, med = timer.per_launch_ms(fn, reps)
+            flops = 2.0 * m * k * n
+            tag = "mfma" if kern == fh.PrefillProjection.F32_MFMA else "chain"
+            res[f"{name}_{tag}"] = {"ms": round(avg, 4), "tflops": round(flops / (avg * 1e-3) / 1e12, 2)}
+        lin.free()
+    return res
+
+
+def bench_i16(torch, fh, gen, np, reps):
+    """BASELINE config 3 prefill: X[6544 x k] FP32 -> INT16 activations x INT8 codes."""
+    m = 6544
+    shapes = [("literal", 1024, 4096, fh.Epilogue.STORE), ("qkv", 768, 2048, fh.Epilogue.STORE),
+              ("wo", 1024, 768, fh.Epilogue.ADD), ("w13", 768, 4608, fh.Epilogue.GLU),
+              ("w2", 2304, 768, fh.Epilogue.ADD)]
+    timer = Timer(torch)
+    res = {}
+    for name, k, n, epi in shapes:
+        a = torch.from_numpy(gen.normal((m, k), 1.0, 7)).cuda()
+        codes = gen.codes_uniform((n, k), -127, 127, np.int8, 8)
+        scales = gen.uniform((n, k // 64), 1e-4, 4e-4, 9)
+        lin = fh.QuantLinear(8, codes, scales, 64)
+        width = n // 2 if epi == fh.Epilogue.GLU else n
+        out = torch.zeros((m, width), device="cuda")
+        fn = lambda i: lin.prefill(a, m, epilogue=epi, out=out, kernel=fh.PrefillProjection.I16)
+        for i in range(2):
+            fn(i)
+        avg, med = timer.per_launch_ms(fn, reps)
+        ops = 2.0 * m * k * n
+        res[name] = {"ms": round(avg, 4), "tops": round(ops / (avg * 1e-3) / 1e12, 2)}
+        lin.free()
+    return res
+
+
+def bench_attention(torch, fh, gen, np, reps):
+    """6,544 tokens, 16 heads x 64 (8 KV heads), image prefix 4,096."""
+    L, img = 6544, 4096
+    q = torch.from_numpy(gen.normal(L * 16 * 64, 1.0, 20)).cuda()
+    k = torch.from_numpy(gen.normal(L * 16 * 64, 1.0, 21)).cuda()
+    v = torch.from_numpy(gen.normal(L * 8 * 64, 1.0, 22)).cuda()
+    sinks = torch.from_numpy(gen.uniform(16, -2.0, 2.0, 23)).cuda()
+    out = torch.empty_like(q)
+    kv = fh.CompactKv.prefill(k, v, L, 16, 8)
+    visible = img * img + sum(qq + 1 for qq in range(img, L))
+    flops = 4.0 * 64 * visible * 16
+    res = {"visible_pairs_per_head": visible, "gflop": round(flops / 1e9, 2)}
+    timer = Timer(torch)
+    for name, opts in (("online_fast", fh.PrefillOptions()), ("static", fh.PrefillOptions(fp32_softmax=fh.Softmax.STATIC))):
+        fn = lambda i: fh.attention_with(q, kv, L, fh.Geometry(0, 0, img), sinks, opts, output=out)
+        for i in range(2):
+            fn(i)
+        avg, med = timer.per_launch_ms(fn, reps)
+        res[name] = {"ms": round(avg, 4), "tflops": round(flops / (avg * 1e-3) / 1e12, 2)}
+    return res
+
+
+def bench_copy(torch, reps):
+    """A plain device copy of known size (calibrates rocprofv3 FETCH/WRITE_SIZE)."""
+    n = 256 << 20
+    src = torch.empty(n // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+    dst = torch.empty_like(src)
+    fn = lambda i: dst.copy_(src)
+    avg, med = Timer(torch).per_launch_ms(fn, reps)
+    return {"bytes_read": n, "bytes_written": n, "ms": round(avg, 4), "gbs": round(2 * n / (avg * 1e-3) / 1e9, 1)}
+
+
+def cpu_baseline(np, gen, seconds=10.0):
+    """The oracle's INT16 GEMV (reference dot_q order) on the host cores, on the
+    headline matrix. Like the GPU side, calls rotate through a pool of copies
+    (1 GiB, above any host last-level cache) so weights stream from DRAM."""
+    import oracle
+
+    threads = min(os.cpu_count() or 1, 16)
+    oracle.set_threads(threads)
+    n, k = 4096, 1024
+    codes = gen.codes_uniform((n, k), -32768, 32767, np.int16, 1)
+    scales = gen.uniform((n, k // 64), 1e-6, 4e-6, 2)
+    x = gen.normal((1, k), 1.0, 3)
+    pool = [(codes.copy(), scales.copy()) for _ in range(max(2, (1 << 30) // codes.nbytes))]
+    oracle.linear_decode(16, codes, scales, n, k, 64, x, 1)
+    times = []
+    t_end = time.perf_counter() + seconds
+    i = 0
+    while time.perf_counter() < t_end or len(times) < 5:
+        c, sc = pool[i % len(pool)]
+        t0 = time.perf_counter()
+        oracle.linear_decode(16, c, sc, n, k, 64, x, 1)
+        times.append(time.perf_counter() - t0)
+        i += 1
+    times.sort()
+    med = times[len(times) // 2]
+    oracle.set_threads(1)
+    return {"value": round(gemv_bytes(n, k, 1, 2) / med / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"INT16 g64 GEMV W[4096x1024] M=1 over a {len(pool)}-copy pool (1 GiB), median of {len(times)} "
+                      f"calls in ~{seconds:.0f} s (oracle/focr_oracle.c, OpenMP {threads} threads)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--ops", default="gemv,gemm,i16,attention,copy")
+    ap.add_argument("--reps", type=int, default=20, help="timed launches per secondary op")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-graph", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (see DESIGN.md, 'Sharding').", file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    import focr_hip as fh
+    import gen
+
+    ops = set(args.ops.split(","))
+    torch.cuda.init()
+    fh.default_context()
+    log(f"device: {torch.cuda.get_device_name(0)}")
+    head = bench_gemv(torch, fh, gen, np, 16, 1, args.steps, args.warmup, graph=not args.no_graph)
+    log(f"gemv16 M=1: wall {head['wall_s'] * 1e3:.2f} ms / {args.steps} steps, launch {head['avg_launch_ms'] * 1e3:.2f} us")
+    ms_per_step = head["wall_s"] * 1e3 / args.steps
+    value = head["bytes"] / (head["wall_s"] / args.steps) / 1e9
+    achieved = head["bytes"] / (head["avg_launch_ms"] * 1e-3) / 1e9
+    per_op = {"gemv_i16_m1": {"bytes": head["bytes"], "launch_us": round(head["avg_launch_ms"] * 1e3, 3),
+                              "gbs_per_launch": round(achieved, 1), "gbs_whole_job": round(value, 1),
+                              "pool_copies": head["pool_copies"]}}
+    if "gemv" in ops:
+        for bits, rows in ((16, 5), (8, 1), (8, 5)):
+            r = bench_gemv(torch, fh, gen, np, bits, rows, max(200, args.steps // 4), 10, graph=not args.no_graph)
+            key = f"gemv_i{bits}_m{rows}"
+            per_op[key] = {"bytes": r["bytes"], "launch_us": round(r["avg_launch_ms"] * 1e3, 3),
+                           "gbs_per_launch": round(r["bytes"] / (r["avg_launch_ms"] * 1e-3) / 1e9, 1),
+                           "gbs_whole_job": round(r["bytes"] / (r["wall_s"] / r["steps"]) / 1e9, 1),
+                           "frac_hbm_per_launch": round(r["bytes"] / (r["avg_launch_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 3)}
+            log(f"{key}: {per_op[key]}")
+    if "gemm" in ops:
+        per_op["prefill_f32"] = bench_gemm(torch, fh, gen, np, args.reps)
+        log(f"prefill_f32: {per_op['prefill_f32']}")
+    if "i16" in ops:
+        per_op["prefill_i16xi8"] = bench_i16(torch, fh, gen, np, args.reps)
+        log(f"prefill_i16xi8: {per_op['prefill_i16xi8']}")
+    if "attention" in ops:
+        per_op["attention_prefill"] = bench_attention(torch, fh, gen, np, max(5, args.reps // 2))
+        log(f"attention: {per_op['attention_prefill']}")
+    if "copy" in ops:
+        per_op["copy_256MiB"] = bench_copy(torch, 10)
+    cpu = None if args.no_cpu else cpu_baseline(np, gen)
+    line = {
+        "metric": "decode GEMV HBM GB/s (INT16 group-64, W 4096x1024, M=1)",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "i16xf32",
+        "data": "synthetic (seeded PCG64: codes uniform [-32768,32767], scales U(1e-6,4e-6), x ~ N(0,1))",
+        "config": {"workload": "BASELINE configs[1]: near-exact INT16 g64 decode GEMV, W[4096x1024], M=1",
+                   "pool_copies": head["pool_copies"], "graph_replay": not args.no_graph},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+        "per_op": per_op,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -142,7 +142,14 @@ int focr_ctx_destroy(focr_ctx *handle) {
 int focr_ctx_set_stream(focr_ctx *handle, void *stream) {
   Ctx *ctx = reinterpret_cast<Ctx *>(handle);
   FOCR_REQUIRE(ctx, FOCR_E_ARG, "focr_ctx_set_stream: null context");
-  ctx->stream = stream ? static_cast<hipStream_t>(stream) : ctx->own;
+  ctx->stream = static_cast<hipStream_t>(stream);
+  return FOCR_OK;
+}
+
+int focr_ctx_use_own_stream(focr_ctx *handle) {
+  Ctx *ctx = reinterpret_cast<Ctx *>(handle);
+  FOCR_REQUIRE(ctx, FOCR_E_ARG, "focr_ctx_use_own_stream: null context");
+  ctx->stream = ctx->own;
   return FOCR_OK;
 }
 

@@ -3,7 +3,8 @@
 // Build flags (falcon-ocr-cpu_amd/Makefile): -ffp-contract=off, so every fused
 // multiply-add in device code is an explicit __builtin_fmaf and every other
 // product/sum rounds on its own, as the reference's Rust arithmetic does;
-// IEEE division and square root (__fdiv_rn, __fsqrt_rn); FP32 denormals kept.
+// IEEE division (__fdiv_rn) and square root (__builtin_sqrtf, which lowers to the
+// FMA-corrected sequence; __fsqrt_rn lowers to the 1-ulp v_sqrt_f32); FP32 denormals kept.
 #pragma once
 
 #include <hip/hip_runtime.h>

@@ -32,6 +32,40 @@ __device__ __forceinline__ float to_f32(float v) { return v; }
 // pairing; IEEE addition is commutative, so operand order is immaterial).
 __device__ __forceinline__ float add_down(float v, int delta) { return v + __shfl_down(v, delta, 32); }
 
+// Loads of one step's scales for this lane's two channels (2 * SPS floats,
+// identical across the 32 lanes of a half: the memory pipeline broadcasts).
+template <int NS>
+struct Scales {
+  float v[NS > 0 ? NS : 1];
+};
+template <int NS>
+__device__ __forceinline__ Scales<NS> load_scales(const float *p) {
+  Scales<NS> s;
+  if constexpr (NS >= 4) {
+#pragma unroll
+    for (int i = 0; i < NS / 4; i++) {
+      const float4 f = reinterpret_cast<const float4 *>(p)[i];
+      s.v[4 * i] = f.x;
+      s.v[4 * i + 1] = f.y;
+      s.v[4 * i + 2] = f.z;
+      s.v[4 * i + 3] = f.w;
+    }
+  } else if constexpr (NS == 2) {
+    const float2 f = *reinterpret_cast<const float2 *>(p);
+    s.v[0] = f.x;
+    s.v[1] = f.y;
+  }
+  return s;
+}
+
+// Steps of weights kept in flight per lane: a rolling window of 16-byte code
+// loads (and their scales) issued before x is staged and refilled as soon as a
+// slot is consumed, so a wave streams several KB at once.
+template <int SPS>
+constexpr int window() {
+  return SPS >= 4 ? 4 : 8;
+}
+
 // T: code type; M: rows; SPS: scales per lane-channel per step (0 for FP32).
 template <typename T, int M, int SPS>
 __global__ __launch_bounds__(256) void gemv_kernel(
@@ -41,14 +75,29 @@ __global__ __launch_bounds__(256) void gemv_kernel(
     int groups, int nb, int steps, int tiles_total, int glu, float *__restrict__ out) {
   constexpr int B = sizeof(T);
   constexpr int S = 16 / (2 * B);  // 32-blocks per step
+  constexpr int NS = 2 * SPS;      // scales per lane per step
+  constexpr int W = window<SPS>();
   extern __shared__ float xs[];    // [M][k]
-  for (int i = threadIdx.x; i < M * k; i += blockDim.x) xs[i] = x[i];
-  __syncthreads();
 
   const int lane = threadIdx.x & 63;
   const int h = lane >> 5, p = lane & 31;
   const int tile = blockIdx.x * kWaves + (threadIdx.x >> 6);
-  if (tile >= tiles_total) return;
+  const bool active = tile < tiles_total;
+  const int my_tile = active ? tile : 0;
+
+  const uint4 *src = tiles + static_cast<size_t>(my_tile) * steps * 64 + lane;
+  const float *sc_src = tile_scales + (static_cast<size_t>(my_tile) * steps * 2 + h) * (NS > 0 ? NS : 1);
+  uint4 cbuf[W];
+  Scales<NS> sbuf[W];
+#pragma unroll
+  for (int j = 0; j < W; j++)
+    if (j < steps) {
+      cbuf[j] = src[static_cast<size_t>(j) * 64];
+      if constexpr (NS > 0) sbuf[j] = load_scales<NS>(sc_src + static_cast<size_t>(j) * 2 * NS);
+    }
+  for (int i = threadIdx.x; i < M * k; i += blockDim.x) xs[i] = x[i];
+  __syncthreads();
+  if (!active) return;
 
   float acc[2][M];
 #pragma unroll
@@ -56,35 +105,33 @@ __global__ __launch_bounds__(256) void gemv_kernel(
 #pragma unroll
     for (int r = 0; r < M; r++) acc[c][r] = 0.0f;
 
-  const uint4 *src = tiles + static_cast<size_t>(tile) * steps * 64 + lane;
-  const float *sc_src = tile_scales + (static_cast<size_t>(tile) * steps * 2 + h) * 2 * (SPS > 0 ? SPS : 1);
-  uint4 next = src[0];
-  for (int t = 0; t < steps; t++) {
-    const uint4 raw = next;
-    if (t + 1 < steps) next = src[static_cast<size_t>(t + 1) * 64];
-    float sc[2][SPS > 0 ? SPS : 1];
-    if constexpr (SPS > 0) {
-      const float *sp = sc_src + static_cast<size_t>(t) * 4 * SPS;
+  for (int base = 0; base < steps; base += W) {
 #pragma unroll
-      for (int c = 0; c < 2; c++)
+    for (int j = 0; j < W; j++) {
+      const int t = base + j;
+      if (t >= steps) break;
+      const uint4 raw = cbuf[j];
+      const Scales<NS> sc = sbuf[j];
+      if (t + W < steps) {
+        cbuf[j] = src[static_cast<size_t>(t + W) * 64];
+        if constexpr (NS > 0) sbuf[j] = load_scales<NS>(sc_src + static_cast<size_t>(t + W) * 2 * NS);
+      }
+      T vals[S][2];
+      __builtin_memcpy(vals, &raw, 16);
 #pragma unroll
-        for (int g = 0; g < SPS; g++) sc[c][g] = sp[c * SPS + g];
-    }
-    T vals[S][2];
-    __builtin_memcpy(vals, &raw, 16);
+      for (int s = 0; s < S; s++) {
+        const int b = t * S + s;
+        if (b >= nb) break;
+        float xv[M];
 #pragma unroll
-    for (int s = 0; s < S; s++) {
-      const int b = t * S + s;
-      if (b >= nb) break;
-      float xv[M];
+        for (int r = 0; r < M; r++) xv[r] = xs[r * k + 32 * b + p];
 #pragma unroll
-      for (int r = 0; r < M; r++) xv[r] = xs[r * k + 32 * b + p];
+        for (int c = 0; c < 2; c++) {
+          float w = to_f32(vals[s][c]);
+          if constexpr (SPS > 0) w = w * sc.v[c * SPS + s / (S / SPS)];
 #pragma unroll
-      for (int c = 0; c < 2; c++) {
-        float w = to_f32(vals[s][c]);
-        if constexpr (SPS > 0) w = w * sc[c][s / (S / SPS)];
-#pragma unroll
-        for (int r = 0; r < M; r++) acc[c][r] = fmaf_(xv[r], w, acc[c][r]);
+          for (int r = 0; r < M; r++) acc[c][r] = fmaf_(xv[r], w, acc[c][r]);
+        }
       }
     }
   }

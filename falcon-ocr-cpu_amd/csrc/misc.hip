@@ -106,7 +106,7 @@ __global__ __launch_bounds__(64) void row_scales_kernel(const float *__restrict_
     }
   }
   // (sum / width + eps).sqrt().recip(): IEEE division and square root.
-  out[blockIdx.x] = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(ret, static_cast<float>(width)) + eps));
+  out[blockIdx.x] = __fdiv_rn(1.0f, __builtin_sqrtf(__fdiv_rn(ret, static_cast<float>(width)) + eps));
 }
 
 // argmax (src/runner/mod.rs:916-930): first index of the maximum, and a flag

@@ -48,6 +48,7 @@ SIGNATURES = {
     "focr_ctx_create": (_I, [_I, ctypes.POINTER(_P)]),
     "focr_ctx_destroy": (_I, [_P]),
     "focr_ctx_set_stream": (_I, [_P, _P]),
+    "focr_ctx_use_own_stream": (_I, [_P]),
     "focr_ctx_stream": (_P, [_P]),
     "focr_ctx_sync": (_I, [_P]),
     "focr_last_error": (ctypes.c_char_p, []),
@@ -133,7 +134,11 @@ class Context:
         _check(lib().focr_ctx_set_stream(self.handle, ctypes.c_void_p(stream.cuda_stream)))
 
     def use_stream(self, stream) -> None:
-        _check(lib().focr_ctx_set_stream(self.handle, ctypes.c_void_p(stream.cuda_stream if stream else 0)))
+        """Run on a torch stream (None: the context's own stream)."""
+        if stream is None:
+            _check(lib().focr_ctx_use_own_stream(self.handle))
+        else:
+            _check(lib().focr_ctx_set_stream(self.handle, ctypes.c_void_p(stream.cuda_stream)))
 
     def sync(self) -> None:
         _check(lib().focr_ctx_sync(self.handle))

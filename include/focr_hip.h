@@ -70,8 +70,10 @@ typedef struct focr_linear focr_linear;
 int focr_ctx_create(int device, focr_ctx **out);
 int focr_ctx_destroy(focr_ctx *ctx);
 /* Run on an existing hipStream_t (e.g. a framework's stream) instead of the
- * context's own; NULL restores the context's stream. */
+ * context's own; NULL selects the device's default (null) stream. */
 int focr_ctx_set_stream(focr_ctx *ctx, void *hip_stream);
+/* Return to the context's own stream. */
+int focr_ctx_use_own_stream(focr_ctx *ctx);
 void *focr_ctx_stream(const focr_ctx *ctx);
 int focr_ctx_sync(focr_ctx *ctx);
 /* Message of the calling thread's last failure ("" if none). */

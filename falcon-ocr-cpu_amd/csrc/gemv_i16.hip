@@ -1,0 +1,16 @@
+// Decode GEMV instantiations for i16 weights (kernel: gemv_kernel.hpp).
+#include "gemv_kernel.hpp"
+
+namespace focr {
+namespace gemv {
+
+int launch_i16(Ctx *ctx, const Linear *lin, const float *x, size_t rows, float *out, bool glu) {
+  switch (lin->group) {
+    case 32: return launch_rows<int16_t, 4>(ctx, lin, x, rows, out, glu);
+    case 64: return launch_rows<int16_t, 2>(ctx, lin, x, rows, out, glu);
+    default: return launch_rows<int16_t, 1>(ctx, lin, x, rows, out, glu);
+  }
+}
+
+}  // namespace gemv
+}  // namespace focr

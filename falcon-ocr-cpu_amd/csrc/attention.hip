@@ -3,18 +3,27 @@
 // (src/kernels/attention/prefill64.rs:149-480, static_shift.rs:135-196).
 //
 // Per workgroup: one query head and 128 consecutive queries (4 waves x 32).
-// Key tiles of 64 keys are staged in LDS (K for this head, V for its KV head).
+// Key tiles of 32 keys (K rows of this head, V rows of its KV head) are copied
+// HBM -> LDS by the DMA path (global_load_lds, 16 bytes per lane), double
+// buffered in two separate LDS arrays so the copy of tile t + 1 overlaps the
+// math on tile t. A K row (256 bytes) is stored as 16 float4 chunks in the
+// order c ^ (row % 16), so the 32 lanes that read one chunk of 32 different
+// rows hit distinct banks; V rows are stored as they are (a lane half reads
+// 32 consecutive floats of one row).
 // Each wave computes S^T = K Q^T with v_mfma_f32_32x32x2f32, so lane l holds
-// the scores of query l % 32 (16 keys per 32-key block in each lane half):
-// the running max, the denominator and the probabilities of a query stay in
-// that query's two lanes, and O^T = V^T P^T takes the probabilities straight
-// from the registers that hold them as the B operand. Scores are scale * dot
-// with scale = 1/8, masked by the reference rule (key > query unless both are
-// image tokens), softmax per query as in softmax_lanes (rescale by
-// exp(old_max - new_max), p = exp(s - new_max), den = den * r + sum p), and
-// the sink at the end: out = (o / den) * 1 / (1 + exp(sink - lse)).
-// The matrix cores sum in their own order, so outputs match the reference
-// within FP32 rounding, not bitwise.
+// the scores of query l % 32 (16 keys in each lane half): the running max,
+// the denominator and the probabilities of a query stay in that query's two
+// lanes, and O^T = V^T P^T takes the probabilities straight from the
+// registers that hold them as the B operand. Scores are scale * dot with
+// scale = 1/8 (folded into Q: a power of two, so exact), masked by the
+// reference rule (key > query unless both are image tokens) on the tiles
+// where some key is hidden from some query of the wave, softmax per query as
+// in softmax_lanes (rescale by exp(old_max - new_max), p = exp(s - new_max),
+// den = den * r + sum p), and the sink at the end:
+// out = (o / den) * 1 / (1 + exp(sink - lse)).
+// The matrix cores sum in their own order, and the online max is taken per
+// 32-key tile rather than per 128 keys, so outputs match the reference within
+// FP32 rounding, not bitwise.
 //
 // Roofline: FP32 matrix cores. FLOPs = 4 * 64 * visible (query, key) pairs
 // per head (122.07 GFLOP at 6,544 tokens, 16 heads, 4,096 image tokens).
@@ -24,10 +33,11 @@ namespace focr {
 namespace {
 
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) const void global_void;
 
 constexpr int kQueries = 128;  // per workgroup (4 waves x 32)
-constexpr int kKeys = 64;      // per LDS key tile
-constexpr int kPitch = 64 + 4; // floats per LDS row
+constexpr int kKeys = 32;      // per LDS key tile
 
 struct AttnArgs {
   const float *q, *prefix_k, *generated_k, *v, *sinks;
@@ -36,21 +46,186 @@ struct AttnArgs {
   int query_offset, image_start, image_end;
 };
 
+// One buffered key tile: [0] = K, [1] = V; 32 rows of 16 swizzled float4.
+struct KvTile {
+  float4 rows[2][kKeys][16];
+};
+
 __device__ __forceinline__ const float *key_row(const AttnArgs &a, int position, int head) {
   if (position < a.prefix_len) return a.prefix_k + (static_cast<size_t>(position) * a.n_heads + head) * 64;
   const int repeat = a.n_heads / a.n_kv_heads;
   return a.generated_k + (static_cast<size_t>(position - a.prefix_len) * a.n_kv_heads + head / repeat) * 64;
 }
 
+__device__ __forceinline__ int chunk(int logical, int row) { return logical ^ (row & 15); }
+
+// x[l % 32] op x[l % 32 + 32] in every lane l (a query's two lane halves),
+// with v_permlane32_swap: the first result holds the low half of x in both
+// halves, the second the high half.
+__device__ __forceinline__ float halves_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float halves_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const float lo = __uint_as_float(r[0]), hi = __uint_as_float(r[1]);
+  return hi > lo ? hi : lo;
+}
+
+// exp_poly for x <= 0 or NaN (an online-softmax exponent s - max), where its
+// x > 88.376 case cannot occur. Below -87 the polynomial runs on -87 and the
+// result is multiplied by 0 (the polynomial is finite there), so no branch
+// is formed; NaN passes through the polynomial as NaN.
+__device__ __forceinline__ float exp_poly_nonpositive(float x) {
+  const bool under = x < -87.0f;
+  return exp_poly_unchecked(under ? -87.0f : x) * (under ? 0.0f : 1.0f);
+}
+
+// exp_poly_unchecked with masked scores (-inf) mapped to +0 the same way.
+__device__ __forceinline__ float exp_unchecked_masked(float s) {
+  const bool masked = s == -__builtin_inff();
+  return exp_poly_unchecked(masked ? 0.0f : s) * (masked ? 0.0f : 1.0f);
+}
+
+// Copies the key tile starting at kstart into t: each wave moves rows
+// 4w..4w+3 and 16+4w..16+4w+3 of K and of V, lane l -> row 4w + l / 16 (+16),
+// stored chunk l % 16 (holding K chunk (l % 16) ^ (row % 16), V chunk l % 16).
+// Rows at or past visible_end repeat the last visible row (in bounds); their
+// scores are masked and their V rows cleared later.
+__device__ __forceinline__ void copy_tile(const AttnArgs &a, KvTile &t, int kstart, int visible_end, int head,
+                                          int kv_head, int wave, int lane) {
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int row = 16 * j + 4 * wave + (lane >> 4);
+    const int logical = chunk(lane & 15, row);
+    int pos = kstart + row;
+    pos = pos < visible_end ? pos : visible_end - 1;
+    const float *k_src = key_row(a, pos, head) + 4 * logical;
+    const float *v_src = a.v + (static_cast<size_t>(pos) * a.n_kv_heads + kv_head) * 64 + 4 * (lane & 15);
+    __builtin_amdgcn_global_load_lds((global_void *)(k_src),
+                                     (lds_void *)(&t.rows[0][16 * j + 4 * wave][0]), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((global_void *)(v_src),
+                                     (lds_void *)(&t.rows[1][16 * j + 4 * wave][0]), 16, 0, 0);
+  }
+}
+
+struct WaveState {
+  float qv[32];  // Q^T operand, pre-scaled by 1/8: q[query][32 h + s]
+  v16f o[2];     // O^T, dims 32 d + 8(r/4) + 4h + r%4 of query l32
+  float run_max, den;
+};
+
+// One 32-key tile of one wave (prefill64.rs:328-480 per key tile).
 template <bool STATIC, bool FAST>
-__global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
-  __shared__ float ks[kKeys][kPitch];
-  __shared__ float vs[kKeys][kPitch];
+__device__ __forceinline__ void tile_step(const AttnArgs &a, const KvTile &t, WaveState &w, int kstart, int keys,
+                                          bool need_mask, int h, int l32, int my_abs, bool my_image) {
+  // S^T = K Q^T: step s uses dims s (lanes 0-31) and 32 + s (lanes 32-63).
+  v16f st;
+#pragma unroll
+  for (int r = 0; r < 16; r++) st[r] = 0.0f;
+  // Each K chunk is read one chunk ahead of the four products that use it.
+  float4 next = t.rows[0][l32][chunk(8 * h, l32)];
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const float4 kf = next;
+    if (i < 7) next = t.rows[0][l32][chunk(8 * h + i + 1, l32)];
+    st = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.x, w.qv[4 * i], st, 0, 0, 0);
+    st = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.y, w.qv[4 * i + 1], st, 0, 0, 0);
+    st = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.z, w.qv[4 * i + 2], st, 0, 0, 0);
+    st = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.w, w.qv[4 * i + 3], st, 0, 0, 0);
+  }
+  // Register r holds key kstart + 8(r/4) + 4h + r%4.
+  if (need_mask) {
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int key = kstart + 8 * (r / 4) + 4 * h + (r % 4);
+      const bool hidden = key >= kstart + keys ||
+                          (key > my_abs && !(my_image && key >= a.image_start && key < a.image_end));
+      st[r] = hidden ? -__builtin_inff() : st[r];
+    }
+  }
+  if constexpr (STATIC) {
+    // p = exp_poly_unchecked(s), masked keys +0 (static_shift.rs:135-160).
+    float psum = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const float s = st[r];
+      const float p = exp_unchecked_masked(s);
+      st[r] = p;
+      psum = psum + p;
+    }
+    w.den = w.den + halves_sum(psum);
+  } else {
+    // Online step (softmax_lanes, prefill64.rs:574-652) over both halves.
+    float tile_max = st[0];
+#pragma unroll
+    for (int r = 1; r < 16; r++) tile_max = st[r] > tile_max ? st[r] : tile_max;
+    tile_max = halves_max(tile_max);
+    const float new_max = tile_max > w.run_max ? tile_max : w.run_max;
+    const bool skip = new_max == -__builtin_inff();
+    const bool first = w.run_max == -__builtin_inff();
+    float rescale = FAST ? exp_poly_nonpositive(w.run_max - new_max) : expf_acc(w.run_max - new_max);
+    rescale = first ? 0.0f : rescale;
+    rescale = skip ? 1.0f : rescale;
+    // A skipped tile (every key hidden) has s = -inf everywhere: subtracting
+    // 0 instead of -inf gives p = exp(-inf) = +0, the reference's no-op.
+    const float shift = skip ? 0.0f : new_max;
+    float psum = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const float x = st[r] - shift;
+      const float p = FAST ? exp_poly_nonpositive(x) : expf_acc(x);
+      st[r] = p;
+      psum = psum + p;
+    }
+    w.den = w.den * rescale + halves_sum(psum);
+    w.run_max = skip ? w.run_max : new_max;
+    // Multiplying by 1 is exact, so the wave rescales when any lane needs it.
+    if (__builtin_amdgcn_ballot_w64(rescale != 1.0f)) {
+#pragma unroll
+      for (int d = 0; d < 2; d++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) w.o[d][r] = w.o[d][r] * rescale;
+    }
+  }
+  // O^T += V^T P^T: step s uses key 8(s/4) + 4h + s%4 (the score register s);
+  // the V operands are read two steps ahead of their products.
+  const float *vbase = reinterpret_cast<const float *>(t.rows[1]) + 4 * h * 64 + l32;
+  float v_now[2], v_next[2], v_far[2];
+#pragma unroll
+  for (int d = 0; d < 2; d++) {
+    v_now[d] = vbase[0 * 64 + 32 * d];
+    v_next[d] = vbase[1 * 64 + 32 * d];
+  }
+#pragma unroll
+  for (int s = 0; s < 16; s++) {
+    if (s + 2 < 16) {
+      const int row = 8 * ((s + 2) / 4) + (s + 2) % 4;
+#pragma unroll
+      for (int d = 0; d < 2; d++) v_far[d] = vbase[row * 64 + 32 * d];
+    }
+#pragma unroll
+    for (int d = 0; d < 2; d++) w.o[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(v_now[d], st[s], w.o[d], 0, 0, 0);
+#pragma unroll
+    for (int d = 0; d < 2; d++) {
+      v_now[d] = v_next[d];
+      v_next[d] = v_far[d];
+    }
+  }
+}
+
+template <bool STATIC, bool FAST>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void attention_kernel(AttnArgs a) {
+  __shared__ KvTile tile0;
+  __shared__ KvTile tile1;
   const int head = blockIdx.y;
   const int kv_head = head / (a.n_heads / a.n_kv_heads);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int h = lane >> 5, l32 = lane & 31;
-  const int first_query = blockIdx.x * kQueries;
+  // Query tiles are dispatched last-first: later (text) tiles see the most
+  // keys, so the longest workgroups start first.
+  const int first_query = (gridDim.x - 1 - blockIdx.x) * kQueries;
   const int wq0 = first_query + wave * 32;  // this wave's first query row
   const int my_query = wq0 + l32;
   const int my_abs = a.query_offset + my_query;
@@ -63,148 +238,75 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
   const int last_abs = first_abs + wg_queries - 1;
   const bool intersects = first_abs < a.image_end && last_abs >= a.image_start;
   const int visible_end = intersects ? (last_abs + 1 > a.image_end ? last_abs + 1 : a.image_end) : last_abs + 1;
-  // This wave's own span, for skipping tiles that are masked for all its rows.
+  // This wave's own span: tiles past it are skipped, tiles before w_first
+  // (and image tiles of an all-image wave) need no mask.
   const int w_queries = a.query_len - wq0 < 32 ? a.query_len - wq0 : 32;
   const int w_first = a.query_offset + wq0, w_last = w_first + (w_queries > 0 ? w_queries : 1) - 1;
   const bool w_intersects = w_queries > 0 && w_first < a.image_end && w_last >= a.image_start;
   const int w_visible = w_queries <= 0 ? 0 : (w_intersects ? (w_last + 1 > a.image_end ? w_last + 1 : a.image_end) : w_last + 1);
+  const bool w_all_image = w_first >= a.image_start && w_last < a.image_end;
 
-  // Q^T operand: lane holds q[my_query][32 h .. 32 h + 32).
-  float qv[32];
+  WaveState w;
   {
     const float *src = a.q + (static_cast<size_t>(my_valid ? my_query : 0) * a.n_heads + head) * 64 + 32 * h;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
       const float4 f = reinterpret_cast<const float4 *>(src)[i];
-      qv[4 * i] = my_valid ? f.x : 0.0f;
-      qv[4 * i + 1] = my_valid ? f.y : 0.0f;
-      qv[4 * i + 2] = my_valid ? f.z : 0.0f;
-      qv[4 * i + 3] = my_valid ? f.w : 0.0f;
+      w.qv[4 * i] = my_valid ? 0.125f * f.x : 0.0f;
+      w.qv[4 * i + 1] = my_valid ? 0.125f * f.y : 0.0f;
+      w.qv[4 * i + 2] = my_valid ? 0.125f * f.z : 0.0f;
+      w.qv[4 * i + 3] = my_valid ? 0.125f * f.w : 0.0f;
     }
   }
-  v16f o[2];
 #pragma unroll
   for (int d = 0; d < 2; d++)
 #pragma unroll
-    for (int r = 0; r < 16; r++) o[d][r] = 0.0f;
-  float run_max = -__builtin_inff();
-  float den = 0.0f;
+    for (int r = 0; r < 16; r++) w.o[d][r] = 0.0f;
+  w.run_max = -__builtin_inff();
+  w.den = 0.0f;
 
-  for (int kstart = 0; kstart < visible_end; kstart += kKeys) {
+  // Tile t is computed from tile0 (t even) or tile1 (t odd) while tile t + 1
+  // is copied into the other array.
+  auto step = [&](KvTile &cur, KvTile &next, int kstart) __attribute__((always_inline)) {
     const int keys = visible_end - kstart < kKeys ? visible_end - kstart : kKeys;
+    // This wave's copies into cur have landed; after the barrier every
+    // wave's have, and no wave still reads next (the previous tile).
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
     __syncthreads();
-    // Stage K (this head) and V (its KV head); rows past `keys` are zero.
-    for (int idx = tid; idx < kKeys * 16; idx += 256) {
-      const int r = idx >> 4, c4 = idx & 15;
-      float4 kf = make_float4(0.f, 0.f, 0.f, 0.f), vf = kf;
-      if (r < keys) {
-        kf = reinterpret_cast<const float4 *>(key_row(a, kstart + r, head))[c4];
-        vf = reinterpret_cast<const float4 *>(a.v + (static_cast<size_t>(kstart + r) * a.n_kv_heads + kv_head) * 64)[c4];
-      }
-      *reinterpret_cast<float4 *>(&ks[r][4 * c4]) = kf;
-      *reinterpret_cast<float4 *>(&vs[r][4 * c4]) = vf;
+    if (keys < kKeys) {
+      // Last tile: clear the V rows past the visible keys (p = 0 there, and
+      // 0 * V must stay finite).
+      for (int idx = tid; idx < (kKeys - keys) * 16; idx += 256)
+        cur.rows[1][keys + (idx >> 4)][idx & 15] = make_float4(0.f, 0.f, 0.f, 0.f);
+      __syncthreads();
     }
-    __syncthreads();
-    // Tiles that are masked for every query of the wave add nothing.
-    if (w_queries <= 0 || kstart >= w_visible) continue;
-
-    // S^T = K Q^T for two 32-key blocks; step s uses d = s + 32 h.
-    v16f st[2];
-#pragma unroll
-    for (int kb = 0; kb < 2; kb++) {
-#pragma unroll
-      for (int r = 0; r < 16; r++) st[kb][r] = 0.0f;
-      const float4 *krow = reinterpret_cast<const float4 *>(&ks[kb * 32 + l32][32 * h]);
-#pragma unroll
-      for (int i = 0; i < 8; i++) {
-        const float4 kf = krow[i];
-        st[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.x, qv[4 * i], st[kb], 0, 0, 0);
-        st[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.y, qv[4 * i + 1], st[kb], 0, 0, 0);
-        st[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.z, qv[4 * i + 2], st[kb], 0, 0, 0);
-        st[kb] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.w, qv[4 * i + 3], st[kb], 0, 0, 0);
-      }
+    if (kstart + kKeys < visible_end) copy_tile(a, next, kstart + kKeys, visible_end, head, kv_head, wave, lane);
+    if (w_queries > 0 && kstart < w_visible) {
+      const bool full = keys == kKeys && (kstart + kKeys <= w_first + 1 ||
+                                          (w_all_image && kstart >= a.image_start && kstart + kKeys <= a.image_end));
+      tile_step<STATIC, FAST>(a, cur, w, kstart, keys, !full, h, l32, my_abs, my_image);
     }
-    // Scale and mask. Register r of block kb holds key kb*32 + 8(r/4) + 4h + r%4.
-    float tile_max = -__builtin_inff();
-#pragma unroll
-    for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int key = kstart + kb * 32 + 8 * (r / 4) + 4 * h + (r % 4);
-        float s = 0.125f * st[kb][r];
-        const bool hidden = key >= kstart + keys ||
-                            (key > my_abs && !(my_image && key >= a.image_start && key < a.image_end));
-        s = hidden ? -__builtin_inff() : s;
-        st[kb][r] = s;
-        tile_max = s > tile_max ? s : tile_max;
-      }
-    float rescale = 1.0f;
-    if constexpr (STATIC) {
-      // p = exp_poly_unchecked(s), masked keys +0 (static_shift.rs:135-160).
-      float psum = 0.0f;
-#pragma unroll
-      for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-          const float s = st[kb][r];
-          const float p = s == -__builtin_inff() ? 0.0f : exp_poly_unchecked(s);
-          st[kb][r] = p;
-          psum = psum + p;
-        }
-      den = den + (psum + __shfl_xor(psum, 32));
-    } else {
-      // Online step (softmax_lanes, prefill64.rs:574-652) over both halves.
-      const float other = __shfl_xor(tile_max, 32);
-      tile_max = other > tile_max ? other : tile_max;
-      const float new_max = tile_max > run_max ? tile_max : run_max;
-      const bool skip = new_max == -__builtin_inff();
-      const bool first = run_max == -__builtin_inff();
-      rescale = FAST ? exp_poly(run_max - new_max) : expf_acc(run_max - new_max);
-      rescale = first ? 0.0f : rescale;
-      rescale = skip ? 1.0f : rescale;
-      float psum = 0.0f;
-#pragma unroll
-      for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-          const float x = st[kb][r] - new_max;
-          const float p = skip ? 0.0f : (FAST ? exp_poly(x) : expf_acc(x));
-          st[kb][r] = p;
-          psum = psum + p;
-        }
-      den = den * rescale + (psum + __shfl_xor(psum, 32));
-      run_max = skip ? run_max : new_max;
-      if (rescale != 1.0f) {
-#pragma unroll
-        for (int d = 0; d < 2; d++)
-#pragma unroll
-          for (int r = 0; r < 16; r++) o[d][r] = o[d][r] * rescale;
-      }
-    }
-    // O^T += V^T P^T: step t of block kb uses key kb*32 + 8(t/4) + 4h + t%4.
-#pragma unroll
-    for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-      for (int t = 0; t < 16; t++) {
-        const int key = kb * 32 + 8 * (t / 4) + 4 * h + (t % 4);
-#pragma unroll
-        for (int d = 0; d < 2; d++)
-          o[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(vs[key][d * 32 + l32], st[kb][t], o[d], 0, 0, 0);
-      }
+  };
+  copy_tile(a, tile0, 0, visible_end, head, kv_head, wave, lane);
+  for (int kstart = 0; kstart < visible_end; kstart += 2 * kKeys) {
+    step(tile0, tile1, kstart);
+    if (kstart + kKeys < visible_end) step(tile1, tile0, kstart + kKeys);
   }
+
   // Normalize and apply the sink (prefill64.rs:468-479).
-  const float lse = STATIC ? logf_acc(den) : run_max + logf_acc(den);
+  const float lse = STATIC ? logf_acc(w.den) : w.run_max + logf_acc(w.den);
   const float sink_scale = __fdiv_rn(1.0f, 1.0f + expf_acc(a.sinks[head] - lse));
   __syncthreads();
-  // Transpose through LDS: o[d][r] is output d = 32 d_blk + 8(r/4) + 4h + r%4 of
-  // query l32; write rows contiguously.
-  float(*stage)[kPitch] = wave < 2 ? ks + wave * 32 : vs + (wave - 2) * 32;
+  // Transpose through LDS (8 KB per wave, swizzled like the key tiles):
+  // o[d][r] is output dim 32 d + 8(r/4) + 4h + r%4 of query l32.
+  float4(*stage)[16] = wave == 0 ? tile0.rows[0] : wave == 1 ? tile0.rows[1] : wave == 2 ? tile1.rows[0] : tile1.rows[1];
 #pragma unroll
   for (int d = 0; d < 2; d++)
 #pragma unroll
     for (int r = 0; r < 16; r++) {
       const int dim = d * 32 + 8 * (r / 4) + 4 * h + (r % 4);
-      stage[l32][dim] = __fmul_rn(__fdiv_rn(o[d][r], den), sink_scale);
+      reinterpret_cast<float *>(&stage[l32][chunk(dim >> 2, l32)])[dim & 3] =
+          __fmul_rn(__fdiv_rn(w.o[d][r], w.den), sink_scale);
     }
   __syncthreads();
   for (int idx = lane; idx < 32 * 16; idx += 64) {
@@ -212,7 +314,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
     const int row = wq0 + r;
     if (row < a.query_len)
       reinterpret_cast<float4 *>(a.out + (static_cast<size_t>(row) * a.n_heads + head) * 64)[c4] =
-          *reinterpret_cast<const float4 *>(&stage[r][4 * c4]);
+          stage[r][chunk(c4, r)];
   }
 }
 

@@ -120,11 +120,13 @@ __device__ __forceinline__ float exp_poly_unchecked(float x) {
 __device__ __forceinline__ float expf_acc(float x) { return ::expf(x); }
 __device__ __forceinline__ float logf_acc(float x) { return ::logf(x); }
 
+// Branch-free: the polynomial runs on the clamped input (the identity inside
+// the range) and the out-of-range and NaN results are selected afterwards.
 __device__ __forceinline__ float exp_poly(float x) {
-  if (__builtin_isnan(x)) return x;
-  if (x < -87.0f) return 0.0f;
-  if (x > 88.376f) return __builtin_inff();
-  return exp_poly_unchecked(x);
+  const float inside = exp_poly_unchecked(__builtin_fminf(__builtin_fmaxf(x, -87.0f), 88.376f));
+  float y = x < -87.0f ? 0.0f : inside;
+  y = x > 88.376f ? __builtin_inff() : y;
+  return __builtin_isnan(x) ? x : y;
 }
 
 }  // namespace focr

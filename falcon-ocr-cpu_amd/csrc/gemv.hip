@@ -4,21 +4,23 @@
 
 namespace focr {
 
-// Largest row count whose x fits the 64 KB of LDS a workgroup may take (x is
-// staged in LDS for three or more rows).
-static size_t rows_per_launch(size_t k) {
-  const size_t fit = (64 * 1024) / (k * sizeof(float));
-  return fit < 2 ? 2 : (fit < 8 ? fit : 8);
+// Largest row count whose x fits the 64 KB of LDS a workgroup may take
+// (x is staged in LDS, padded to whole steps).
+static size_t rows_per_launch(const Linear *lin) {
+  const size_t scales = gemv::scale_lds_bytes(lin);
+  const size_t fit = scales >= gemv::kLdsBudget ? 0 : (gemv::kLdsBudget - scales) / gemv::x_row_bytes(lin);
+  return fit < 8 ? fit : 8;
 }
 
 int launch_gemv(Ctx *ctx, const Linear *lin, const float *x, size_t rows, float *out, bool glu) {
   FOCR_HIP_CHECK(hipSetDevice(ctx->device));
-  const size_t chunk = rows_per_launch(lin->k);
+  const size_t chunk = rows_per_launch(lin);
+  FOCR_REQUIRE(chunk >= 1, FOCR_E_SHAPE, "GEMV: in_dim too large for one row of x in LDS");
   const size_t width = glu ? lin->n / 2 : lin->n;
   // Rows are independent (each output row is its single-row dot, bitwise), so
   // a call whose inputs exceed the LDS budget runs as several launches.
   for (size_t r0 = 0; r0 < rows; r0 += chunk) {
-    const size_t m = rows - r0 < chunk ? rows - r0 : chunk;  // m <= 2 or m * k floats fit LDS
+    const size_t m = rows - r0 < chunk ? rows - r0 : chunk;
     const float *xr = x + r0 * lin->k;
     float *orow = out + r0 * width;
     int rc;

@@ -15,11 +15,14 @@
 // phase for its two channels. Dequantization fl(code * scale) happens in
 // registers; FP32 weights are never materialized.
 //
-// Latency structure: a wave issues every load it needs for up to W steps
-// (weights, scales and, for 1-2 rows, its own x values) before any compute,
-// all unconditional with in-bounds clamped indices, and only then consumes
-// them in order; register arrays are indexed statically so nothing is
-// spilled. With three or more rows x is staged once per workgroup in LDS.
+// Latency structure. Every thread first loads its share of x, then issues
+// the scale loads and the weight loads of up to W steps, all unconditional
+// with in-bounds clamped indices. It waits only for the x loads (the oldest:
+// vmcnt counts down in issue order) to store x in LDS, meets the other waves
+// at one barrier, and then consumes step t as soon as its own weights have
+// arrived, while the later steps are still in flight. x sits in LDS as [row][32 * S * steps]
+// with the blocks past the last full one zeroed; the tile layout holds zero
+// codes there, so the padded products are fma(0, 0, acc) = acc exactly.
 //
 // Roofline: HBM. Bytes per call = codes + scales (+ x, out), e.g. 4,476,928 B
 // for an INT8 4096x1024 matrix at one row.
@@ -36,9 +39,29 @@ __device__ __forceinline__ float to_f32(int8_t v) { return static_cast<float>(st
 __device__ __forceinline__ float to_f32(int16_t v) { return static_cast<float>(static_cast<int32_t>(v)); }
 __device__ __forceinline__ float to_f32(float v) { return v; }
 
-// Sum of lane and lane + delta within a 32-lane half (the reference's lane
-// pairing; IEEE addition is commutative, so operand order is immaterial).
-__device__ __forceinline__ float add_down(float v, int delta) { return v + __shfl_down(v, delta, 32); }
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// Lane p < 8 of each 32-lane half: (v[p] + v[p+8]) + (v[p+16] + v[p+24]), the
+// reference's (a0 + a1) + (a2 + a3) (IEEE addition is commutative, so operand
+// order is immaterial). row_ror:8 pairs p with p + 8 (= p - 8 mod 16) inside a 16-lane row;
+// v_permlane16_swap then pairs the two rows of each half.
+__device__ __forceinline__ float fold_32_to_8(float v) {
+  const float t = v + dpp<0x128>(v);
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(t), __float_as_uint(t), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Lane 0 of each half: ((v0 + v4) + (v1 + v5)) + ((v2 + v6) + (v3 + v7)):
+// row_ror:12 (lane i reads lane i + 4 of its row; row_ror:n reads lane
+// i - n), then quad_perm [1,0,3,2], then quad_perm [2,3,0,1].
+__device__ __forceinline__ float fold_8_to_1(float v) {
+  const float u = v + dpp<0x12C>(v);
+  const float w = u + dpp<0xB1>(u);
+  return w + dpp<0x4E>(w);
+}
 
 // One step's scales for this lane's two channels (2 * SPS floats, identical
 // across the 32 lanes of a half).
@@ -46,6 +69,10 @@ template <int NS>
 struct Scales {
   float v[NS > 0 ? NS : 1];
 };
+template <int NS>
+constexpr int scale_loads() {
+  return NS >= 4 ? NS / 4 : (NS == 2 ? 1 : 0);
+}
 template <int NS>
 __device__ __forceinline__ Scales<NS> load_scales(const float *p) {
   Scales<NS> s;
@@ -79,51 +106,111 @@ struct Args {
   float *out;
 };
 
+// Floats per LDS row of x: every block a step can touch.
+__host__ __device__ inline int x_pitch(int steps, int S) { return 32 * S * steps; }
+
 // T: code type; M: rows; SPS: scales per lane-channel per step (0 for FP32
-// weights); W: steps held in registers (all of them when steps <= W).
-template <typename T, int M, int SPS, int W>
+// weights); W: steps held in registers; ROLL: steps > W, so the window is
+// refilled as it is consumed (a separate instantiation, so that code common
+// to both paths cannot be hoisted above the first step's wait).
+template <typename T, int M, int SPS, int W, bool ROLL>
 __global__ __launch_bounds__(256) void kernel(Args a) {
   constexpr int B = sizeof(T);
-  constexpr int S = 16 / (2 * B);   // 32-blocks per step
-  constexpr int NS = 2 * SPS;       // scales per lane per step
-  constexpr bool XREG = M <= 2;     // x straight to registers (else LDS)
-  extern __shared__ float xs[];     // [M][k] when !XREG
+  constexpr int S = 16 / (2 * B);  // 32-blocks per step
+  constexpr int NS = 2 * SPS;      // scales per lane per step
+  extern __shared__ float xs[];    // [M][x_pitch], then scales [kWaves][steps][2][NS]
 
-  const int lane = threadIdx.x & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = lane >> 5, p = lane & 31;
-  const int tile = blockIdx.x * kWaves + (threadIdx.x >> 6);
+  const int tile = blockIdx.x * kWaves + wave;
   const bool active = tile < a.tiles_total;
-  const int my_tile = active ? tile : 0;
+  const int my_tile = active ? tile : a.tiles_total - 1;
   const int k = a.k, nb = a.nb, steps = a.steps;
+  const int pitch = x_pitch(steps, S);
   const T *codes = static_cast<const T *>(a.codes);
+  float *ss = xs + M * pitch;
 
+  // Operands staged per workgroup: x (the 32 * nb floats of the full blocks
+  // of each row) and the scales of the workgroup's tiles (contiguous in the
+  // tile layout: kWaves * steps * 2 * NS floats from the first tile).
+  const int cols = 32 * nb;
+  const int cols4 = cols / 4;
+  const bool x_vec = k % 4 == 0;
+  const int sc_total4 = a.tiles_total * steps * 2 * NS / 4;
+  const int sc_base4 = blockIdx.x * kWaves * steps * 2 * NS / 4;
+  const int sc_count4 = kWaves * steps * 2 * NS / 4;
+  // x[r][4i .. 4i + 3], every index clamped into the row (k >= 1; with
+  // 16-byte rows k % 4 == 0 means k >= 4 whenever a float4 is read).
+  auto x_load = [&](int r, int i) {
+    const float *row = a.x + static_cast<size_t>(r) * k;
+    if (x_vec) return reinterpret_cast<const float4 *>(row)[i * 4 + 3 < k ? i : 0];
+    auto at = [&](int c) { return row[c < k ? c : k - 1]; };
+    return make_float4(at(4 * i), at(4 * i + 1), at(4 * i + 2), at(4 * i + 3));
+  };
+  auto sc_load = [&](int i) {
+    const int g = sc_base4 + i;
+    return reinterpret_cast<const float4 *>(a.tile_scales)[g < sc_total4 ? g : sc_total4 - 1];
+  };
+
+  // 1. Without ROLL: x and scales go to registers first (clamped, in bounds)
+  // and to LDS only after the weight loads are issued, so their stores wait
+  // for the x and scale loads only (the oldest: vmcnt counts down in issue
+  // order). (The LDS-DMA path would save the registers, but a read of
+  // DMA-written LDS makes the compiler wait for every load in flight.)
+  constexpr int XJ = ROLL ? 1 : (8 * S * W + 255) / 256;       // float4 per thread per row
+  constexpr int SJ = ROLL || NS == 0 ? 1 : (2 * W * NS + 255) / 256;  // float4 per thread
+  float4 xv[M][XJ], sv[SJ];
+  if constexpr (!ROLL) {
+#pragma unroll
+    for (int r = 0; r < M; r++)
+#pragma unroll
+      for (int j = 0; j < XJ; j++) {
+        const int i = tid + 256 * j;
+        xv[r][j] = x_load(r, i < cols4 ? i : (cols4 > 0 ? cols4 - 1 : 0));  // cols4 = 0 when k < 32
+      }
+    if constexpr (NS > 0)
+#pragma unroll
+      for (int j = 0; j < SJ; j++) sv[j] = sc_load(tid + 256 * j < sc_count4 ? tid + 256 * j : sc_count4 - 1);
+  } else {
+    // Rows longer than the window: stage directly (the weights wait).
+    for (int r = 0; r < M; r++)
+      for (int i = tid; i < cols4; i += 256) *reinterpret_cast<float4 *>(xs + r * pitch + 4 * i) = x_load(r, i);
+    if constexpr (NS > 0)
+      for (int i = tid; i < sc_count4; i += 256) reinterpret_cast<float4 *>(ss)[i] = sc_load(i);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 2. Weights of the first W steps (clamped, in bounds).
   const uint4 *src = a.tiles + static_cast<size_t>(my_tile) * steps * 64 + lane;
-  const float *sc_src = a.tile_scales + (static_cast<size_t>(my_tile) * steps * 2 + h) * (NS > 0 ? NS : 1);
-  // x of block b for this lane's phase; blocks past the last are clamped
-  // (in bounds, never used).
-  auto x_at = [&](int r, int b) { return a.x[r * k + 32 * (b < nb ? b : (nb > 0 ? nb - 1 : 0)) + p]; };
-
   uint4 cbuf[W];
-  Scales<NS> sbuf[W];
-  float xw[XREG ? W : 1][XREG ? S : 1][XREG ? M : 1];
 #pragma unroll
-  for (int j = 0; j < W; j++) {
-    const int t = j < steps ? j : steps - 1;
-    cbuf[j] = src[static_cast<size_t>(t) * 64];
-    if constexpr (NS > 0) sbuf[j] = load_scales<NS>(sc_src + static_cast<size_t>(t) * 2 * NS);
-    if constexpr (XREG)
+  for (int j = 0; j < W; j++) cbuf[j] = src[static_cast<size_t>(j < steps ? j : steps - 1) * 64];
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 3. Store x and the scales, zero the padded blocks, and meet the other
+  // waves (a plain s_barrier: __syncthreads' release fence would also wait
+  // for the weight loads).
+  if constexpr (!ROLL) {
 #pragma unroll
-      for (int s = 0; s < S; s++)
+    for (int r = 0; r < M; r++)
 #pragma unroll
-        for (int r = 0; r < M; r++) xw[j][s][r] = x_at(r, t * S + s);
+      for (int j = 0; j < XJ; j++) {
+        const int i = tid + 256 * j;
+        if (i < cols4) *reinterpret_cast<float4 *>(xs + r * pitch + 4 * i) = xv[r][j];
+      }
+    if constexpr (NS > 0)
+#pragma unroll
+      for (int j = 0; j < SJ; j++)
+        if (tid + 256 * j < sc_count4) reinterpret_cast<float4 *>(ss)[tid + 256 * j] = sv[j];
   }
-  if constexpr (!XREG) {
-    for (int i = threadIdx.x; i < M * k; i += blockDim.x) xs[i] = a.x[i];
-    __syncthreads();
+  for (int i = tid; i < M * (pitch - cols); i += 64 * kWaves) {
+    const int r = i / (pitch - cols), c = cols + i % (pitch - cols);
+    xs[r * pitch + c] = 0.0f;
   }
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   if (!active) return;
-  // x for the tails and exceptions (any column).
-  auto x_col = [&](int r, int i) { return XREG ? a.x[r * k + i] : xs[r * k + i]; };
+  const float *my_scales = ss + (wave * steps * 2 + h) * NS;  // + t * 2 * NS for step t
 
   float acc[2][M];
 #pragma unroll
@@ -131,21 +218,17 @@ __global__ __launch_bounds__(256) void kernel(Args a) {
 #pragma unroll
     for (int r = 0; r < M; r++) acc[c][r] = 0.0f;
 
-  const int ch0 = tile * kGemvChannels + h * 2;
-  // A full step: S blocks of this lane's phase for both channels.
-  auto step_full = [&](int t, const uint4 &raw, const Scales<NS> &sc, const float (&xv)[XREG ? S : 1][XREG ? M : 1]) {
+  // Step t: S blocks of this lane's phase for both channels.
+  auto step = [&](int t, const uint4 &raw) {
     T vals[S][2];
     __builtin_memcpy(vals, &raw, 16);
+    Scales<NS> sc;
+    if constexpr (NS > 0) sc = load_scales<NS>(my_scales + t * 2 * NS);
 #pragma unroll
     for (int s = 0; s < S; s++) {
       float xr[M];
 #pragma unroll
-      for (int r = 0; r < M; r++) {
-        if constexpr (XREG)
-          xr[r] = xv[s][r];
-        else
-          xr[r] = xs[r * k + 32 * (t * S + s) + p];
-      }
+      for (int r = 0; r < M; r++) xr[r] = xs[r * pitch + 32 * (t * S + s) + p];
 #pragma unroll
       for (int c = 0; c < 2; c++) {
         float w = to_f32(vals[s][c]);
@@ -155,60 +238,33 @@ __global__ __launch_bounds__(256) void kernel(Args a) {
       }
     }
   };
-  // The last step when k/32 is not a multiple of S (odd widths only): read
-  // the row-major codes directly (no register arrays indexed at run time).
-  auto step_partial = [&](int t) {
-    for (int b = t * S; b < nb; b++)
+  if constexpr (!ROLL) {
 #pragma unroll
-      for (int c = 0; c < 2; c++) {
-        const int ch = ch0 + c < a.n ? ch0 + c : a.n - 1;
-        float w = to_f32(codes[static_cast<size_t>(ch) * k + 32 * b + p]);
-        if constexpr (SPS > 0) w = w * a.scales[static_cast<size_t>(ch) * a.groups + (32 * b) / a.group];
-#pragma unroll
-        for (int r = 0; r < M; r++) acc[c][r] = fmaf_(x_col(r, 32 * b + p), w, acc[c][r]);
-      }
-  };
-  const int full = nb / S;  // steps whose S blocks all exist
-  if (steps <= W) {
-#pragma unroll
-    for (int t = 0; t < W; t++) {
-      if (t < full)
-        step_full(t, cbuf[t], sbuf[t], xw[XREG ? t : 0]);
-      else if (t < steps)
-        step_partial(t);
-    }
+    for (int t = 0; t < W; t++)
+      if (t < steps) step(t, cbuf[t]);
   } else {
     for (int base = 0; base < steps; base += W) {
 #pragma unroll
       for (int j = 0; j < W; j++) {
         const int t = base + j;
-        if (t < full)
-          step_full(t, cbuf[j], sbuf[j], xw[XREG ? j : 0]);
-        else if (t < steps)
-          step_partial(t);
+        if (t < steps) step(t, cbuf[j]);
         const int tn = t + W < steps ? t + W : steps - 1;
         cbuf[j] = src[static_cast<size_t>(tn) * 64];
-        if constexpr (NS > 0) sbuf[j] = load_scales<NS>(sc_src + static_cast<size_t>(tn) * 2 * NS);
-        if constexpr (XREG)
-#pragma unroll
-          for (int s = 0; s < S; s++)
-#pragma unroll
-            for (int r = 0; r < M; r++) xw[j][s][r] = x_at(r, tn * S + s);
       }
     }
   }
 
-  // (a0 + a1) + (a2 + a3) lane-wise: lane p < 8 ends up with the combined
-  // accumulator lane p of the reference.
+  const int ch0 = tile * kGemvChannels + h * 2;
+  auto x_col = [&](int r, int i) { return a.x[static_cast<size_t>(r) * k + i]; };
 #pragma unroll
   for (int c = 0; c < 2; c++)
 #pragma unroll
-    for (int r = 0; r < M; r++) acc[c][r] = add_down(add_down(acc[c][r], 8), 16);
+    for (int r = 0; r < M; r++) acc[c][r] = fold_32_to_8(acc[c][r]);
 
   // 8-wide tail (k % 32 >= 8): one more FMA per combined lane and chunk.
-  const int tail8 = (k - 32 * nb) / 8;
+  const int tail8 = (k - cols) / 8;
   for (int ci = 0; ci < tail8; ci++) {
-    const int i = 32 * nb + 8 * ci;
+    const int i = cols + 8 * ci;
     if (p < 8) {
 #pragma unroll
       for (int c = 0; c < 2; c++) {
@@ -220,11 +276,10 @@ __global__ __launch_bounds__(256) void kernel(Args a) {
       }
     }
   }
-  // ((v0+v4)+(v1+v5))+((v2+v6)+(v3+v7)) on lanes 0..7.
 #pragma unroll
   for (int c = 0; c < 2; c++)
 #pragma unroll
-    for (int r = 0; r < M; r++) acc[c][r] = add_down(add_down(add_down(acc[c][r], 4), 1), 2);
+    for (int r = 0; r < M; r++) acc[c][r] = fold_8_to_1(acc[c][r]);
 
   if (p != 0) return;
   float total[2][M];
@@ -235,7 +290,7 @@ __global__ __launch_bounds__(256) void kernel(Args a) {
     for (int r = 0; r < M; r++) total[c][r] = acc[c][r];
     if (ch >= a.n) continue;
     // Scalar tail: total += x * fl(code * scale), unfused.
-    for (int i = 32 * nb + 8 * tail8; i < k; i++) {
+    for (int i = cols + 8 * tail8; i < k; i++) {
       float w = to_f32(codes[static_cast<size_t>(ch) * k + i]);
       if constexpr (SPS > 0) w = w * a.scales[static_cast<size_t>(ch) * a.groups + i / a.group];
 #pragma unroll
@@ -265,9 +320,18 @@ __global__ __launch_bounds__(256) void kernel(Args a) {
   }
 }
 
-template <typename T, int M, int SPS, int W>
+// LDS bytes of one row of x, and of the workgroup's scales.
+inline size_t x_row_bytes(const Linear *lin) {
+  const int S = 16 / (2 * (lin->bits / 8));
+  return static_cast<size_t>(x_pitch(static_cast<int>(lin->gemv_steps), S)) * sizeof(float);
+}
+inline size_t scale_lds_bytes(const Linear *lin) { return kWaves * lin->gemv_steps * 2 * 2 * lin->gemv_sps * sizeof(float); }
+constexpr size_t kLdsBudget = 64 * 1024;
+
+template <typename T, int M, int SPS, int W, bool ROLL = false>
 int launch_typed(Ctx *ctx, const Linear *lin, const float *x, float *out, bool glu) {
-  const size_t lds = M <= 2 ? 0 : static_cast<size_t>(M) * lin->k * sizeof(float);
+  const size_t lds = M * x_row_bytes(lin) + scale_lds_bytes(lin);
+  FOCR_REQUIRE(lds <= kLdsBudget, FOCR_E_SHAPE, "GEMV: x rows exceed the LDS budget");
   const int blocks = static_cast<int>((lin->gemv_tiles + kWaves - 1) / kWaves);
   Args a;
   a.tiles = static_cast<const uint4 *>(lin->gemv_codes);
@@ -287,23 +351,25 @@ int launch_typed(Ctx *ctx, const Linear *lin, const float *x, float *out, bool g
   a.tiles_total = static_cast<int>(lin->gemv_tiles);
   a.glu = glu ? 1 : 0;
   a.out = out;
-  hipLaunchKernelGGL((kernel<T, M, SPS, W>), dim3(blocks), dim3(64 * kWaves), lds, ctx->stream, a);
+  hipLaunchKernelGGL((kernel<T, M, SPS, W, ROLL>), dim3(blocks), dim3(64 * kWaves), lds, ctx->stream, a);
   FOCR_HIP_CHECK(hipGetLastError());
   return FOCR_OK;
 }
 
-// Window buckets: all steps in registers up to 20 steps (36 for FP32
-// weights), which covers every matrix of the model; longer rows refill.
+// Window buckets: every step in registers up to 20 steps (FP32: 36), which
+// covers every matrix of the model; longer rows refill a 20 (36) step window.
 template <typename T, int M, int SPS>
 int launch_window(Ctx *ctx, const Linear *lin, const float *x, float *out, bool glu) {
   const size_t steps = lin->gemv_steps;
   if (steps <= 4) return launch_typed<T, M, SPS, 4>(ctx, lin, x, out, glu);
   if (steps <= 8) return launch_typed<T, M, SPS, 8>(ctx, lin, x, out, glu);
+  if (steps <= 12) return launch_typed<T, M, SPS, 12>(ctx, lin, x, out, glu);
+  if (steps <= 20) return launch_typed<T, M, SPS, 20>(ctx, lin, x, out, glu);
   if constexpr (SPS == 0) {
-    if (steps <= 20) return launch_typed<T, M, SPS, 20>(ctx, lin, x, out, glu);
-    return launch_typed<T, M, SPS, 36>(ctx, lin, x, out, glu);
+    if (steps <= 36) return launch_typed<T, M, SPS, 36>(ctx, lin, x, out, glu);
+    return launch_typed<T, M, SPS, 36, true>(ctx, lin, x, out, glu);
   } else {
-    return launch_typed<T, M, SPS, 20>(ctx, lin, x, out, glu);
+    return launch_typed<T, M, SPS, 20, true>(ctx, lin, x, out, glu);
   }
 }
 

@@ -30,6 +30,10 @@ for p in (ROOT / "falcon-ocr-cpu_amd", ROOT / "tests", ROOT / "oracle"):
     sys.path.insert(0, str(p))
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
+# HBM bytes per launch of the headline kernel, from rocprofv3 FETCH_SIZE and
+# WRITE_SIZE runs scaled by the same counters on a copy of known size (the
+# file records the commands and the scaling).
+TRAFFIC_FILE = ROOT / "profiles" / "gemv_i16_m1_traffic.md"
 FP32_MFMA_PEAK = 157.3  # TFLOP/s dense
 INT8_MFMA_PEAK = 5000.0  # TOP/s dense
 POOL_BYTES = 600 << 20  # > 2 x 256 MB Infinity Cache
@@ -235,6 +239,17 @@ def cpu_baseline(np, gen, seconds=10.0):
                       f"calls in ~{seconds:.0f} s (oracle/focr_oracle.c, OpenMP {threads} threads)"}
 
 
+def measured_traffic():
+    """traffic_bytes_per_launch from the committed PMC summary, or None."""
+    import re
+
+    try:
+        m = re.search(r"traffic_bytes_per_launch\s*=\s*(\d+)", TRAFFIC_FILE.read_text())
+    except OSError:
+        return None
+    return int(m.group(1)) if m else None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -303,7 +318,7 @@ def main():
         "config": {"workload": "BASELINE configs[1]: near-exact INT16 g64 decode GEMV, W[4096x1024], M=1",
                    "pool_copies": head["pool_copies"], "graph_replay": not args.no_graph},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic()},
         "cpu_baseline": cpu,
         "per_op": per_op,
     }

@@ -195,6 +195,14 @@ def bench_attention(torch, fh, gen, np, reps):
             fn(i)
         avg, med = timer.per_launch_ms(fn, reps)
         res[name] = {"ms": round(avg, 4), "tflops": round(flops / (avg * 1e-3) / 1e12, 2)}
+    # A8: the BF16 kernels (K/V conversion included in the timed launch).
+    for name, sm in (("bf16_online", fh.Softmax.ONLINE), ("bf16_static", fh.Softmax.STATIC)):
+        opts = fh.PrefillOptions(softmax=sm)
+        fn = lambda i: fh.attention_prefill_bf16(q, kv, L, fh.Geometry(0, 0, img), sinks, out, opts)
+        for i in range(2):
+            fn(i)
+        avg, med = timer.per_launch_ms(fn, reps)
+        res[name] = {"ms": round(avg, 4), "tflops": round(flops / (avg * 1e-3) / 1e12, 2)}
     return res
 
 

@@ -443,6 +443,27 @@ int focr_attention_prefill(focr_ctx *handle, const float *q, const float *prefix
                           n_kv_heads, query_offset, image_start, image_end, sinks, softmax, exp_mode, out);
 }
 
+int focr_attention_prefill_bf16(focr_ctx *handle, const float *q, const float *k, const float *v, size_t query_len,
+                                size_t n_heads, size_t n_kv_heads, size_t head_dim, size_t image_start,
+                                size_t image_end, const float *sinks, int softmax, int exp_mode, float *out) {
+  Ctx *ctx = reinterpret_cast<Ctx *>(handle);
+  FOCR_REQUIRE(ctx, FOCR_E_ARG, "focr_attention_prefill_bf16: null context");
+  // CompactKv::validate (src/kernels/attention/mod.rs:157-195) for a pure prefill.
+  FOCR_REQUIRE(head_dim > 0 && n_heads > 0 && n_kv_heads > 0, FOCR_E_SHAPE, "attention head dimensions must be positive");
+  FOCR_REQUIRE(n_heads % n_kv_heads == 0, FOCR_E_SHAPE, "attention GQA grouping");
+  FOCR_REQUIRE(image_start <= image_end && image_end <= query_len, FOCR_E_SHAPE, "attention image must be inside the prefix");
+  FOCR_REQUIRE(softmax == FOCR_SOFTMAX_ONLINE || softmax == FOCR_SOFTMAX_STATIC, FOCR_E_ARG, "unknown softmax");
+  FOCR_REQUIRE(exp_mode == FOCR_EXP_FAST || exp_mode == FOCR_EXP_EXACT, FOCR_E_ARG, "unknown exp mode");
+  // attention_prefill_bf16 (mod.rs:320-352) runs only these shapes and
+  // otherwise returns false: here FOCR_E_UNSUPPORTED, nothing written.
+  FOCR_REQUIRE(query_len >= 4 && head_dim == 64, FOCR_E_UNSUPPORTED,
+               "the BF16 attention takes pure prefills of at least 4 queries with head_dim 64");
+  FOCR_REQUIRE(q && k && v && sinks && out, FOCR_E_ARG, "focr_attention_prefill_bf16: null buffer");
+  FOCR_HIP_CHECK(hipSetDevice(ctx->device));
+  return launch_attention_bf16(ctx, q, k, v, query_len, n_heads, n_kv_heads, image_start, image_end, sinks, softmax,
+                               out);
+}
+
 int focr_argmax(focr_ctx *handle, const float *logits, size_t rows, size_t vocab, uint32_t *tokens) {
   Ctx *ctx = reinterpret_cast<Ctx *>(handle);
   FOCR_REQUIRE(ctx, FOCR_E_ARG, "focr_argmax: null context");

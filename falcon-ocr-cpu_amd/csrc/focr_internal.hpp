@@ -88,6 +88,9 @@ int launch_attention(Ctx *ctx, const float *q, const float *prefix_k, const floa
                      const float *v, size_t query_len, size_t prefix_len, size_t total_len,
                      size_t n_heads, size_t n_kv_heads, size_t query_offset, size_t image_start,
                      size_t image_end, const float *sinks, int softmax, int exp_mode, float *out);
+int launch_attention_bf16(Ctx *ctx, const float *q, const float *k, const float *v, size_t query_len,
+                          size_t n_heads, size_t n_kv_heads, size_t image_start, size_t image_end,
+                          const float *sinks, int softmax, float *out);
 int launch_argmax(Ctx *ctx, const float *logits, size_t rows, size_t vocab, uint32_t *result_dev);
 
 // ---- device helpers ---------------------------------------------------------

@@ -39,6 +39,7 @@ LIBRARY = _ROOT / "lib" / "libfocr_hip.so"
 HEADER = _ROOT.parent / "include" / "focr_hip.h"
 
 FOCR_OK = 0
+FOCR_E_UNSUPPORTED = -3
 ERRORS = {-1: "FOCR_E_ARG", -2: "FOCR_E_SHAPE", -3: "FOCR_E_UNSUPPORTED", -4: "FOCR_E_HIP",
           -5: "FOCR_E_VALUE", -6: "FOCR_E_NONFINITE"}
 
@@ -66,6 +67,7 @@ SIGNATURES = {
     "focr_linear_prefill": (_I, [_P, _P, _P, _Z, _P, _I, _I, _P]),
     "focr_row_scales": (_I, [_P, _P, _Z, _Z, _F, _P]),
     "focr_attention_prefill": (_I, [_P, _P, _P, _P, _P, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _P, _I, _I, _P]),
+    "focr_attention_prefill_bf16": (_I, [_P, _P, _P, _P, _Z, _Z, _Z, _Z, _Z, _Z, _P, _I, _I, _P]),
     "focr_argmax": (_I, [_P, _P, _Z, _Z, _P]),
 }
 
@@ -329,8 +331,13 @@ class ExpMode(enum.IntEnum):
 
 @dataclass(frozen=True)
 class PrefillOptions:
+    """attention/mod.rs:205-221: `softmax` is the BF16 kernels' softmax
+    (static shift by default, as the reference's PrefillSoftmax), and
+    `fp32_softmax` the FP32 tiles' one."""
+
     exp: ExpMode = ExpMode.FAST
     fp32_softmax: Softmax = Softmax.ONLINE
+    softmax: Softmax = Softmax.STATIC
 
 
 def attention_with(q, kv: CompactKv, query_len: int, geometry: Geometry, sinks, options: PrefillOptions = PrefillOptions(),
@@ -346,6 +353,23 @@ def attention_with(q, kv: CompactKv, query_len: int, geometry: Geometry, sinks, 
                                         geometry.image_end, _dev(sinks), int(options.fp32_softmax),
                                         int(options.exp), _dev(output)))
     return output
+
+
+def attention_prefill_bf16(q, kv: CompactKv, query_len: int, geometry: Geometry, sinks, output,
+                           options: PrefillOptions = PrefillOptions(), ctx: Optional[Context] = None) -> bool:
+    """`kernels::attention_prefill_bf16` (attention/mod.rs:320-352): the BF16
+    prefill into `output`; False (nothing written) where the reference's
+    returns false: not a pure prefill, fewer than 4 queries, head_dim != 64."""
+    ctx = ctx or default_context()
+    if geometry.query_offset != 0 or kv.prefix_len != kv.total_len or query_len != kv.total_len:
+        return False
+    rc = lib().focr_attention_prefill_bf16(ctx.handle, _dev(q), _dev(kv.prefix_k), _dev(kv.v), query_len, kv.n_heads,
+                                           kv.n_kv_heads, kv.head_dim, geometry.image_start, geometry.image_end,
+                                           _dev(sinks), int(options.softmax), int(options.exp), _dev(output))
+    if rc == FOCR_E_UNSUPPORTED:
+        return False
+    _check(rc)
+    return True
 
 
 F32_EPSILON = float(np.finfo(np.float32).eps)

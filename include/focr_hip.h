@@ -156,6 +156,25 @@ int focr_attention_prefill(focr_ctx *ctx, const float *q_dev, const float *prefi
                            size_t image_start, size_t image_end, const float *sinks_dev,
                            int softmax, int exp_mode, float *out_dev);
 
+/* ---- A8: BF16 prefill attention ----------------------------------------- */
+/* kernels::attention_prefill_bf16 (src/kernels/attention/mod.rs:320-352) ->
+ * prefill64::bf16::compact_prefill (prefill64/bf16.rs:70-175, plans Bf16 /
+ * Bf16Static): a pure prefill (query_offset 0, every key a prefix key),
+ * q_dev / k_dev [query_len][n_heads][64], v_dev [query_len][n_kv_heads][64].
+ * Q, K, V and the probabilities are rounded to BF16; products accumulate in
+ * FP32 on the BF16 matrix cores; softmax FOCR_SOFTMAX_ONLINE or _STATIC
+ * (the static shift needs scores bounded, as the reference's does). exp_mode
+ * is accepted for the interface; both use the hardware exp2 (the result is
+ * within the BF16 tolerance, 2e-3, of either reference exp). Where the
+ * reference returns false (query_len < 4, head_dim != 64) this returns
+ * FOCR_E_UNSUPPORTED and writes nothing. Converts K and V into the context
+ * scratch first. */
+int focr_attention_prefill_bf16(focr_ctx *ctx, const float *q_dev, const float *k_dev,
+                                const float *v_dev, size_t query_len, size_t n_heads,
+                                size_t n_kv_heads, size_t head_dim, size_t image_start,
+                                size_t image_end, const float *sinks_dev, int softmax,
+                                int exp_mode, float *out_dev);
+
 /* ---- A9: greedy selection ------------------------------------------------ */
 /* argmax of each row (src/runner/mod.rs:916-939): first index of the
  * maximum; FOCR_E_NONFINITE if any value of a row is NaN or infinite.

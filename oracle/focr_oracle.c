@@ -27,6 +27,11 @@
  *    by the tile-independence identities; the reference's short "gemm crate"
  *    tiles (q*k <= 256, k < 3 or q < 2) are parity unpinned bitwise (the
  *    gemm crate 0.19.0 order is not available here) and pinned to tolerance.
+ *  - orc_attention_prefill_bf16_tiles: pinned by the reference's f64 bound on
+ *    BF16-rounded operands (bf16.rs matches_bf16_operand_reference: |d| <=
+ *    3 * 2^-9 + 2e-3), the static variant's exp2 polynomial by its scalar
+ *    restatement and 7.6e-5 bound, and hand checks of the BF16 rounding and
+ *    the vdpbf16ps pair order; short online tiles as for orc_attention_prefill.
  *  - orc_argmax: pinned (KAT).
  */
 #include "focr_oracle.h"
@@ -634,6 +639,209 @@ void orc_attention_prefill(const float *q, const float *prefix_k, const float *g
                                 n_heads, n_kv_heads, query_offset, image_start, image_end, sinks,
                                 static_softmax, exp_fast, 0, (size_t)-1, out);
 }
+
+/* ---- A8: BF16 prefill attention (src/kernels/attention/prefill64/bf16.rs) -- */
+
+/* BF16 round to nearest even. `daz` follows vcvtneps2bf16 (denormal inputs
+ * are zero); without it, half::bf16::from_f32 (used for the queries,
+ * bf16.rs:256-268). NaN stays a quiet NaN. */
+static inline float bf16_round(float x, int daz) {
+    uint32_t u = f2u(x);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return u2f((u | 0x00400000u) & 0xffff0000u);
+    if (daz && (u & 0x7f800000u) == 0) return u2f(u & 0x80000000u);
+    return u2f((u + 0x7fffu + ((u >> 16) & 1u)) & 0xffff0000u);
+}
+static inline float flush(float x) { return (f2u(x) & 0x7f800000u) == 0 ? u2f(f2u(x) & 0x80000000u) : x; }
+
+/* One vdpbf16ps lane step: acc += a1*b1, then acc += a0*b0 (the odd element
+ * first), each product exact in FP32, denormal results flushed. */
+static inline float dpbf16(float acc, float a0, float a1, float b0, float b1) {
+    acc = flush(acc + flush(a1 * b1));
+    return flush(acc + flush(a0 * b0));
+}
+
+/* exp2_lanes / exp2_scalar (bf16/static_shift.rs:277-289, tests.rs:19-24):
+ * the reference's degree-3 minimax coefficients, digit for digit. */
+static const float EXP2_C[4] = {0.99992806f, 0.69326097f, 0.24261113f, 0.05517167f};
+float orc_exp2_minimax(float t) {
+    float n = nearbyintf(t);
+    float f = t - n;
+    float p = fmaf(fmaf(fmaf(EXP2_C[3], f, EXP2_C[2]), f, EXP2_C[1]), f, EXP2_C[0]);
+    return ldexpf(p, (int)n);
+}
+
+/* One (query tile, head) of compact_prefill (bf16.rs:70-175) for a pure
+ * prefill (query_offset 0, every key a prefix key): tile_head (bf16.rs:
+ * 271-398) for the online softmax, static_shift::tile_head
+ * (bf16/static_shift.rs:100-168) for the static one. */
+static void bf16_tile_head(const float *q, const float *k, const float *v, size_t total, size_t n_heads,
+                           size_t n_kv_heads, size_t image_start, size_t image_end, size_t tile,
+                           size_t queries, size_t head, const float *sinks, int is_static, ExpFn exp_fn,
+                           float *output) {
+    const size_t qw = n_heads * HD, kvw = n_kv_heads * HD;
+    const size_t kv_head = head / (n_heads / n_kv_heads);
+    const float scale = 0.125f;
+    const float escale = 1.44269504088896340736f * scale; /* exponent_scale: LOG2_E * scale */
+    size_t first_query = tile * QT;
+    size_t first_absolute = first_query, last_absolute = first_absolute + queries - 1;
+    int intersects = first_absolute < image_end && last_absolute >= image_start;
+    size_t visible_end = intersects ? (last_absolute + 1 > image_end ? last_absolute + 1 : image_end) : last_absolute + 1;
+    int all_image = first_absolute >= image_start && last_absolute < image_end;
+
+    float qb[QT][HD], qf[HD][QT];
+    memset(qb, 0, sizeof qb);
+    memset(qf, 0, sizeof qf);
+    for (size_t r = 0; r < queries; r++)
+        for (int d = 0; d < HD; d++) {
+            float x = q[(first_query + r) * qw + head * HD + d];
+            qb[r][d] = bf16_round(x, 0); /* query_pairs: half::bf16 */
+            qf[d][r] = x;
+        }
+    float maxima[QT], den[QT], out[QT][HD];
+    for (int r = 0; r < QT; r++) {
+        maxima[r] = -INFINITY;
+        den[r] = 0.0f;
+    }
+    memset(out, 0, sizeof out);
+    static __thread float st[KT][QT], kb[KT][HD], vb[KT][HD];
+
+    for (size_t key_start = 0; key_start < visible_end; key_start += KT) {
+        size_t keys = visible_end - key_start < KT ? visible_end - key_start : KT;
+        int main_path = queries * keys > 256 && keys >= 3 && queries >= 2;
+        if (is_static || main_path) {
+            for (size_t j = 0; j < KT; j++)
+                for (int d = 0; d < HD; d++) {
+                    kb[j][d] = j < keys ? bf16_round(k[(key_start + j) * qw + head * HD + d], 1) : 0.0f;
+                    vb[j][d] = j < keys ? bf16_round(v[(key_start + j) * kvw + kv_head * HD + d], 1) : 0.0f;
+                }
+            /* qk_keys (bf16.rs:563-596): pairs p = 0..31, odd element first. */
+            for (size_t j = 0; j < keys; j++)
+                for (int r = 0; r < QT; r++) {
+                    float acc = 0.0f;
+                    for (int pr = 0; pr < HD / 2; pr++)
+                        acc = dpbf16(acc, qb[r][2 * pr], qb[r][2 * pr + 1], kb[j][2 * pr], kb[j][2 * pr + 1]);
+                    st[j][r] = (is_static ? escale : scale) * acc;
+                }
+            if (is_static) {
+                /* qk_exp_lanes epilogue: 2^t on visible lanes, +0 elsewhere;
+                 * denominators add the BF16-rounded values in key order. */
+                for (size_t j = 0; j < keys; j++)
+                    for (size_t r = 0; r < queries; r++) {
+                        size_t key = key_start + j;
+                        int visible = all_image || !masked(first_absolute + r, key, image_start, image_end);
+                        float p = visible ? orc_exp2_minimax(st[j][r]) : 0.0f;
+                        st[j][r] = p;
+                        den[r] = den[r] + bf16_round(p, 1);
+                    }
+            } else {
+                if (!all_image)
+                    for (size_t r = 0; r < queries; r++)
+                        for (size_t j = 0; j < keys; j++)
+                            if (masked(first_absolute + r, key_start + j, image_start, image_end)) st[j][r] = -INFINITY;
+                /* softmax_pairs / softmax_lanes (bf16.rs:409-473): the FP32
+                 * online step; the denominators add the unrounded p. */
+                for (size_t r = 0; r < queries; r++) {
+                    float block_max = -INFINITY;
+                    for (size_t j = 0; j < keys; j++) block_max = st[j][r] > block_max ? st[j][r] : block_max;
+                    float old_max = maxima[r];
+                    float new_max = block_max > old_max ? block_max : old_max;
+                    int skip = new_max == -INFINITY, first = old_max == -INFINITY;
+                    float rescale = exp_fn(old_max - new_max);
+                    if (first) rescale = 0.0f;
+                    if (skip) rescale = 1.0f;
+                    if (!skip && rescale != 1.0f)
+                        for (int d = 0; d < HD; d++) out[r][d] *= rescale;
+                    float denominator = den[r] * rescale;
+                    for (size_t j = 0; j < keys; j++) {
+                        float p = skip ? 0.0f : exp_fn(st[j][r] - new_max);
+                        denominator = denominator + p;
+                        st[j][r] = p;
+                    }
+                    den[r] = denominator;
+                    maxima[r] = skip ? old_max : new_max;
+                }
+            }
+            /* pv_rows (bf16.rs:627-657): per key pair, odd key first, from
+             * +0; then + out. Probabilities round to BF16 first. */
+            for (size_t r = 0; r < queries; r++) {
+                float acc[HD];
+                for (int d = 0; d < HD; d++) acc[d] = 0.0f;
+                for (size_t kp = 0; kp < (keys + 1) / 2; kp++) {
+                    float p0 = bf16_round(st[2 * kp][r], 1);
+                    float p1 = 2 * kp + 1 < keys ? bf16_round(st[2 * kp + 1][r], 1) : 0.0f;
+                    for (int d = 0; d < HD; d++) acc[d] = dpbf16(acc[d], vb[2 * kp][d], vb[2 * kp + 1][d], p0, p1);
+                }
+                for (int d = 0; d < HD; d++) out[r][d] = acc[d] + out[r][d];
+            }
+        } else {
+            /* Short tiles: the parent's FP32 reference path on the FP32
+             * operands (bf16.rs:368-393), as in the FP32 oracle. */
+            for (size_t r = 0; r < queries; r++) {
+                size_t absolute = first_absolute + r;
+                float scores[KT];
+                float block_max = -INFINITY;
+                for (size_t j = 0; j < keys; j++) {
+                    float acc = 0.0f;
+                    const float *kr = k + (key_start + j) * qw + head * HD;
+                    for (int d = 0; d < HD; d++) acc = fmaf(qf[d][r], kr[d], acc);
+                    float s = scale * acc;
+                    if (masked(absolute, key_start + j, image_start, image_end)) s = -INFINITY;
+                    scores[j] = s;
+                    block_max = fmaxf(block_max, s);
+                }
+                float new_max = fmaxf(maxima[r], block_max);
+                if (new_max == -INFINITY) {
+                    for (size_t j = 0; j < keys; j++) st[j][r] = 0.0f;
+                    continue;
+                }
+                float rescale = maxima[r] == -INFINITY ? 0.0f : expf(maxima[r] - new_max);
+                for (int d = 0; d < HD; d++) out[r][d] *= rescale;
+                den[r] *= rescale;
+                for (size_t j = 0; j < keys; j++) {
+                    float p = expf(scores[j] - new_max);
+                    st[j][r] = p;
+                    den[r] += p;
+                }
+                maxima[r] = new_max;
+            }
+            for (size_t r = 0; r < queries; r++) {
+                float acc[HD];
+                for (int d = 0; d < HD; d++) acc[d] = 0.0f;
+                for (size_t j = 0; j < keys; j++) {
+                    const float *vr = v + (key_start + j) * kvw + kv_head * HD;
+                    for (int d = 0; d < HD; d++) acc[d] = fmaf(st[j][r], vr[d], acc[d]);
+                }
+                for (int d = 0; d < HD; d++) out[r][d] = out[r][d] + acc[d];
+            }
+        }
+    }
+    for (size_t r = 0; r < queries; r++) {
+        float lse = is_static ? logf(den[r]) : maxima[r] + logf(den[r]);
+        float sink_scale = 1.0f / (1.0f + expf(sinks[head] - lse));
+        float *dst = output + (first_query + r) * qw + head * HD;
+        for (int d = 0; d < HD; d++) dst[d] = (out[r][d] / den[r]) * sink_scale;
+    }
+}
+
+void orc_attention_prefill_bf16_tiles(const float *q, const float *k, const float *v, size_t query_len,
+                                      size_t n_heads, size_t n_kv_heads, size_t image_start,
+                                      size_t image_end, const float *sinks, int static_softmax,
+                                      int exp_fast, size_t tile_begin, size_t tile_end, float *out) {
+    size_t tiles = (query_len + QT - 1) / QT;
+    if (tile_end > tiles) tile_end = tiles;
+    if (tile_begin >= tile_end) return;
+    size_t span = tile_end - tile_begin;
+    ExpFn exp_fn = exp_fast ? orc_exp_poly : platform_exp;
+#pragma omp parallel for schedule(dynamic, 1)
+    for (long task = 0; task < (long)(span * n_heads); task++) {
+        size_t tile = tile_begin + (size_t)task / n_heads, head = (size_t)task % n_heads;
+        size_t queries = query_len - tile * QT < QT ? query_len - tile * QT : QT;
+        bf16_tile_head(q, k, v, query_len, n_heads, n_kv_heads, image_start, image_end, tile, queries, head,
+                       sinks, static_softmax, exp_fn, out);
+    }
+}
+
+float orc_bf16_round(float x) { return bf16_round(x, 0); }
 
 /* ---- A9 ------------------------------------------------------------------ */
 int orc_argmax(const float *logits, size_t n, uint32_t *out) {

@@ -86,6 +86,22 @@ void orc_i16_quantize_rows(const float *a, size_t m, size_t k, const int32_t *ex
                            size_t n_exc, const float *row_scale, int16_t *codes, float *steps,
                            float *exc_inputs);
 
+/* ---- A8: BF16 prefill attention ---------------------------------------- */
+/* compact_prefill (src/kernels/attention/prefill64/bf16.rs:70-175) for a pure
+ * prefill (query_offset 0, query_len == total == prefix): Q, K, V rounded to
+ * BF16, vdpbf16ps products (odd element first, FP32 accumulation), FP32
+ * online softmax with probabilities rounded to BF16 before PV; the static
+ * variant (bf16/static_shift.rs) uses 2^t with the degree-3 minimax and
+ * sums the rounded probabilities. Query tiles [tile_begin, tile_end). */
+void orc_attention_prefill_bf16_tiles(const float *q, const float *k, const float *v, size_t query_len,
+                                      size_t n_heads, size_t n_kv_heads, size_t image_start,
+                                      size_t image_end, const float *sinks, int static_softmax,
+                                      int exp_fast, size_t tile_begin, size_t tile_end, float *out);
+/* exp2_scalar (bf16/static_shift/tests.rs:19-24). */
+float orc_exp2_minimax(float t);
+/* half::bf16::from_f32(x).to_f32(). */
+float orc_bf16_round(float x);
+
 /* ---- A7: FP32 prefill attention --------------------------------------- */
 /* compact_prefill / tile_head (src/kernels/attention/prefill64.rs:149-480),
  * head_dim 64. generated_k may be NULL when prefix_len == total_len.

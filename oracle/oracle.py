@@ -74,6 +74,9 @@ _sig("orc_i16_quantize_rows", None, _P, _Z, _Z, _P, _Z, _P, _P, _P, _P)
 _sig("orc_i16_gemm", None, _P, _Z, _Z, _P, _P, _Z, _P, _P, _Z, _P, _I, _P)
 _sig("orc_attention_prefill", None, _P, _P, _P, _P, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _P, _I, _I, _P)
 _sig("orc_attention_prefill_tiles", None, _P, _P, _P, _P, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _P, _I, _I, _Z, _Z, _P)
+_sig("orc_attention_prefill_bf16_tiles", None, _P, _P, _P, _Z, _Z, _Z, _Z, _Z, _P, _I, _I, _Z, _Z, _P)
+_sig("orc_exp2_minimax", _F, _F)
+_sig("orc_bf16_round", _F, _F)
 _sig("orc_argmax", _I, _P, _Z, _P)
 _sig("orc_set_threads", None, _I)
 _sig("orc_get_threads", _I)
@@ -256,6 +259,31 @@ def attention_prefill(q, prefix_k, v, query_len, prefix_len, total_len, n_heads,
                                          total_len, n_heads, n_kv_heads, query_offset, image_start, image_end,
                                          _ptr(sinks), int(static), int(exp_fast), tiles[0], tiles[1], _ptr(out))
     return out.reshape(query_len, n_heads, 64)
+
+
+def attention_prefill_bf16(q, k, v, query_len, n_heads, n_kv_heads, image_start, image_end, sinks,
+                           static=False, exp_fast=True, tiles=None):
+    """BF16 compact_prefill (src/kernels/attention/prefill64/bf16.rs:70-175), pure prefill."""
+    q, k, v, sinks = _f32(q), _f32(k), _f32(v), _f32(sinks)
+    out = np.zeros(query_len * n_heads * 64, dtype=np.float32)
+    lo, hi = (0, (query_len + 31) // 32) if tiles is None else tiles
+    _lib.orc_attention_prefill_bf16_tiles(_ptr(q), _ptr(k), _ptr(v), query_len, n_heads, n_kv_heads, image_start,
+                                          image_end, _ptr(sinks), int(static), int(exp_fast), lo, hi, _ptr(out))
+    return out.reshape(query_len, n_heads, 64)
+
+
+def exp2_minimax(t):
+    return np.float32(_lib.orc_exp2_minimax(float(t)))
+
+
+def bf16_round(x):
+    """half::bf16::from_f32(x).to_f32(), elementwise."""
+    x = _f32(x)
+    u = x.view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7fffffff) > 0x7f800000
+    r = ((u + 0x7fff + ((u >> 16) & 1)) & 0xffff0000).astype(np.uint32)
+    r = np.where(nan, (u.astype(np.uint32) | 0x00400000) & 0xffff0000, r).astype(np.uint32)
+    return r.view(np.float32)
 
 
 def argmax(logits):

@@ -1,0 +1,121 @@
+"""BF16 prefill attention (A8) on the GPU against the oracle, within the BF16
+tolerance: max|d| / max|ref| <= 2e-3, and within the reference's own f64
+bound on BF16-rounded operands (prefill64/bf16.rs matches_bf16_operand_reference,
+bf16/static_shift/tests.rs)."""
+import numpy as np
+import pytest
+
+import gen
+import oracle
+from gpu_util import host, max_rel, to_dev
+from test_oracle_bf16 import CASES, f64_attention
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def fh():
+    import focr_hip
+
+    return focr_hip
+
+
+def run(fh, q, k, v, sinks, L, image, softmax, heads=16, kv_heads=8):
+    import torch
+
+    out = torch.full((L * heads * 64,), float("nan"), device="cuda")
+    kv = fh.CompactKv.prefill(to_dev(k), to_dev(v), L, heads, kv_heads)
+    ran = fh.attention_prefill_bf16(to_dev(q), kv, L, fh.Geometry(0, *image), to_dev(sinks), out,
+                                    fh.PrefillOptions(softmax=softmax))
+    assert ran
+    return host(out).reshape(L, heads, 64)
+
+
+@pytest.mark.parametrize("L,image_start,image_end", CASES + [(600, 0, 0), (33, 0, 33)])
+def test_online_bf16(fh, L, image_start, image_end):
+    r = oracle.bf16_round
+    q = r(gen.values(L * 16 * 64, 17 + L, 3.0))
+    k = r(gen.values(L * 16 * 64, 19 + L, 3.0))
+    v = r(gen.values(L * 8 * 64, 23 + L, 3.0))
+    sinks = gen.values(16, 29, 2.0)
+    got = run(fh, q, k, v, sinks, L, (image_start, image_end), fh.Softmax.ONLINE)
+    want = oracle.attention_prefill_bf16(q, k, v, L, 16, 8, image_start, image_end, sinks, static=False)
+    assert np.all(np.isfinite(got))
+    assert max_rel(got, want) <= 2e-3
+    exact = f64_attention(q, k, v, L, 16, 8, image_start, image_end, sinks)
+    assert np.abs(got - exact).max() <= 3.0 * 2.0 ** -9 + 2e-3
+
+
+@pytest.mark.parametrize("L,image_start,image_end", CASES + [(600, 0, 0)])
+def test_static_bf16(fh, L, image_start, image_end):
+    r = oracle.bf16_round
+    q = r(gen.normalized(L * 16 * 64, 17 + L))
+    k = r(gen.normalized(L * 16 * 64, 19 + L))
+    v = r(gen.values(L * 8 * 64, 23 + L, 3.0))
+    sinks = gen.values(16, 29, 2.0)
+    got = run(fh, q, k, v, sinks, L, (image_start, image_end), fh.Softmax.STATIC)
+    want = oracle.attention_prefill_bf16(q, k, v, L, 16, 8, image_start, image_end, sinks, static=True)
+    assert np.all(np.isfinite(got))
+    assert max_rel(got, want) <= 2e-3
+    exact = f64_attention(q, k, v, L, 16, 8, image_start, image_end, sinks, shift=False)
+    assert np.abs(got - exact).max() <= 3.0 * 2.0 * (2.0 ** -8 + 7.5e-5) + 1e-4
+
+
+@pytest.mark.parametrize("L,image", [(130, (2, 100)), (97, (0, 40)), (66, (3, 65)), (33, (0, 0)), (300, (5, 262)),
+                                     (259, (0, 257)), (6, (0, 3))])
+def test_unrounded_operands_online(fh, L, image):
+    # FP32 operands: the kernel rounds Q, K, V itself, like the reference, and
+    # the reference's short key tiles (and rows of a last one- or two-query
+    # tile) take the FP32 path on the unrounded values.
+    q = gen.values(L * 16 * 64, 3 + L, 3.0)
+    k = gen.values(L * 16 * 64, 4 + L, 3.0)
+    v = gen.values(L * 8 * 64, 5 + L, 3.0)
+    sinks = gen.values(16, 29, 2.0)
+    got = run(fh, q, k, v, sinks, L, image, fh.Softmax.ONLINE)
+    want = oracle.attention_prefill_bf16(q, k, v, L, 16, 8, image[0], image[1], sinks, static=False)
+    assert np.all(np.isfinite(got))
+    assert max_rel(got, want) <= 2e-3
+
+
+@pytest.mark.parametrize("L,image", [(130, (2, 100)), (66, (3, 65))])
+def test_unrounded_operands_static(fh, L, image):
+    q = gen.normalized(L * 16 * 64, 3 + L)
+    k = gen.normalized(L * 16 * 64, 4 + L)
+    v = gen.values(L * 8 * 64, 5 + L, 3.0)
+    sinks = gen.values(16, 29, 2.0)
+    got = run(fh, q, k, v, sinks, L, image, fh.Softmax.STATIC)
+    want = oracle.attention_prefill_bf16(q, k, v, L, 16, 8, image[0], image[1], sinks, static=True)
+    assert max_rel(got, want) <= 2e-3
+
+
+def test_unsupported_shapes_write_nothing(fh):
+    import torch
+
+    L = 3
+    q = to_dev(gen.values(L * 16 * 64, 1))
+    v = to_dev(gen.values(L * 8 * 64, 2))
+    out = torch.full((L * 16 * 64,), 7.0, device="cuda")
+    kv = fh.CompactKv.prefill(q, v, L, 16, 8)
+    assert not fh.attention_prefill_bf16(q, kv, L, fh.Geometry(0, 0, 0), to_dev(gen.values(16, 3)), out)
+    mixed = fh.CompactKv(q, q, v, 2, 3, 16, 8, 64)
+    assert not fh.attention_prefill_bf16(q, mixed, L, fh.Geometry(0, 0, 0), to_dev(gen.values(16, 3)), out)
+    assert bool(torch.all(out == 7.0))
+
+
+@pytest.mark.parametrize("softmax", ["online", "static"])
+def test_config4_full_page_bf16(fh, softmax):
+    # BASELINE config 4 shape (6,544 tokens, image prefix 4,096), Q/K/V ~ N(0,1),
+    # checked against the oracle on query tiles that span the image end.
+    L, image_end = 6544, 4096
+    q = gen.normal(L * 16 * 64, 1.0, 20)
+    k = gen.normal(L * 16 * 64, 1.0, 21)
+    v = gen.normal(L * 8 * 64, 1.0, 22)
+    sinks = gen.uniform(16, -2.0, 2.0, 23)
+    sm = fh.Softmax.ONLINE if softmax == "online" else fh.Softmax.STATIC
+    got = run(fh, q, k, v, sinks, L, (0, image_end), sm)
+    assert np.all(np.isfinite(got))
+    for lo, hi in ((0, 2), (127, 129), (203, 205)):
+        want = oracle.attention_prefill_bf16(q, k, v, L, 16, 8, 0, image_end, sinks, static=softmax == "static",
+                                             tiles=(lo, hi))
+        rows = slice(32 * lo, 32 * hi)
+        assert max_rel(got[rows], want[rows]) <= 2e-3

@@ -18,6 +18,10 @@
 // matrix core gives the same S, and every output matches kernel_scalar bit
 // for bit.
 //
+// Each group's A and B tiles, activation steps, column sums and scales are
+// copied HBM -> LDS by the LDS-DMA path into one of two buffers while the
+// previous group is computed from the other.
+//
 // Roofline: the i8 matrix cores do 2 x 64 MACs per output and group; the
 // FP32 group epilogue (4 VALU ops per output and group) bounds it in practice.
 #include "focr_internal.hpp"
@@ -145,19 +149,65 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float *__restrict__
   if (lane < 16) steps[static_cast<size_t>(g) * m_pad + row] = step * scale;
 }
 
+// One group's operands in LDS, filled by the LDS-DMA path (25.5 KB; two
+// buffers).
+struct GroupTile {
+  uint4 a[kBM / 16 * 2 * 64];  // [8 row blocks][hi, lo][64 lanes] x 16 B
+  uint4 b[kBN / 16 * 64];      // [8 column blocks][64 lanes] x 16 B
+  float steps[kBM];            // activation steps of the tile's rows
+  int32_t wsum[kBN];           // 128 * sum of the group's codes per column
+  float sw[kBN];               // weight scales per column
+};
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) const void global_void;
+
 template <int EPI>
 __global__ __launch_bounds__(256) void gemm_kernel(const int8_t *__restrict__ a_tiles, const float *__restrict__ steps,
                                                    const float *__restrict__ exc_inputs, const int8_t *__restrict__ b_tiles,
                                                    const int32_t *__restrict__ wsum, const float *__restrict__ sw,
                                                    const float *__restrict__ exc_vals, int n_exc, int m, int n,
                                                    int groups, int row_blocks, int m_pad, float *__restrict__ out) {
-  __shared__ uint4 lds_a[kBM / 16 * 2 * 64];  // [8 row blocks][hi, lo][64 lanes] x 16 B
-  __shared__ uint4 lds_b[kBN / 16 * 64];      // [8 col blocks][64 lanes] x 16 B
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  __shared__ GroupTile buf0;
+  __shared__ GroupTile buf1;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
   const int mb0 = blockIdx.x * (kBM / 16);
   const int nb0 = blockIdx.y * (kBN / 16);
   const int col_blocks = n / 16;
+
+  // Group g -> t by DMA (16 B per lane; sources clamped into their arrays,
+  // columns past n are computed and discarded): A 4 and B 2 instructions per
+  // thread; the steps, column sums and scales by lanes 0-31 of waves 0-2.
+  auto copy_group = [&](GroupTile &t, int g) {
+    const char *ga = reinterpret_cast<const char *>(a_tiles) + (static_cast<size_t>(g) * row_blocks + mb0) * 2048;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      __builtin_amdgcn_global_load_lds((global_void *)(ga + 16 * (tid + 256 * i)), (lds_void *)(&t.a[64 * wave + 256 * i]),
+                                       16, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const int idx = tid + 256 * i;
+      int blk = nb0 + idx / 64;
+      blk = blk < col_blocks ? blk : col_blocks - 1;
+      const char *gb = reinterpret_cast<const char *>(b_tiles) + ((static_cast<size_t>(g) * col_blocks + blk) * 64 + (idx & 63)) * 16;
+      __builtin_amdgcn_global_load_lds((global_void *)gb, (lds_void *)(&t.b[64 * wave + 256 * i]), 16, 0, 0);
+    }
+    if (lane < 32) {
+      if (wave == 0) {
+        __builtin_amdgcn_global_load_lds((global_void *)(steps + static_cast<size_t>(g) * m_pad + mb0 * 16 + 4 * lane),
+                                         (lds_void *)(&t.steps[0]), 16, 0, 0);
+      } else if (wave < 3) {
+        int col = nb0 * 16 + 4 * lane;
+        col = col < n ? col : n - 4;
+        const void *src = wave == 1 ? static_cast<const void *>(wsum + static_cast<size_t>(g) * n + col)
+                                    : static_cast<const void *>(sw + static_cast<size_t>(g) * n + col);
+        __builtin_amdgcn_global_load_lds((global_void *)src, wave == 1 ? (lds_void *)(&t.wsum[0]) : (lds_void *)(&t.sw[0]),
+                                         16, 0, 0);
+      }
+    }
+  };
 
   float acc[4][4][4];
 #pragma unroll
@@ -168,51 +218,40 @@ __global__ __launch_bounds__(256) void gemm_kernel(const int8_t *__restrict__ a_
       for (int r = 0; r < 4; r++) acc[i][j][r] = 0.0f;
 
   const int quad = lane >> 4, col_in = lane & 15;
-  for (int g = 0; g < groups; g++) {
-    // Stage this group's operands: A 16 KB (contiguous), B up to 8 KB.
-    const uint4 *ga = reinterpret_cast<const uint4 *>(a_tiles + (static_cast<size_t>(g) * row_blocks + mb0) * 2048);
-#pragma unroll
-    for (int i = 0; i < 4; i++) lds_a[tid + 256 * i] = ga[tid + 256 * i];
-    const uint4 *gb = reinterpret_cast<const uint4 *>(b_tiles + (static_cast<size_t>(g) * col_blocks + nb0) * 1024);
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-      const int idx = tid + 256 * i;
-      if (nb0 + idx / 64 < col_blocks) lds_b[idx] = gb[idx];
-    }
-    __syncthreads();
+  // Group g is read from one buffer while g + 1 is copied into the other.
+  auto step = [&](GroupTile &cur, GroupTile &next, int g) __attribute__((always_inline)) {
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's copies of cur
+    __syncthreads();                     // everyone's; nobody still reads next
+    if (g + 1 < groups) copy_group(next, g + 1);
     v4i ahi[4], alo[4], b[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const int rb = wm * 4 + i;
-      const uint4 h = lds_a[(rb * 2) * 64 + lane], l = lds_a[(rb * 2 + 1) * 64 + lane];
-      ahi[i] = v4i{static_cast<int>(h.x), static_cast<int>(h.y), static_cast<int>(h.z), static_cast<int>(h.w)};
-      alo[i] = v4i{static_cast<int>(l.x), static_cast<int>(l.y), static_cast<int>(l.z), static_cast<int>(l.w)};
+      const uint4 hv = cur.a[(rb * 2) * 64 + lane], lv = cur.a[(rb * 2 + 1) * 64 + lane];
+      ahi[i] = v4i{static_cast<int>(hv.x), static_cast<int>(hv.y), static_cast<int>(hv.z), static_cast<int>(hv.w)};
+      alo[i] = v4i{static_cast<int>(lv.x), static_cast<int>(lv.y), static_cast<int>(lv.z), static_cast<int>(lv.w)};
     }
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-      const uint4 w = lds_b[(wn * 4 + j) * 64 + lane];
+      const uint4 w = cur.b[(wn * 4 + j) * 64 + lane];
       b[j] = v4i{static_cast<int>(w.x), static_cast<int>(w.y), static_cast<int>(w.z), static_cast<int>(w.w)};
     }
-    __syncthreads();
-    // Per-column weight terms and per-row activation steps of this group.
     int32_t ws[4];
     float swv[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-      const int col = (nb0 + wn * 4 + j) * 16 + col_in;
-      const int c = col < n ? col : n - 1;
-      ws[j] = wsum[static_cast<size_t>(g) * n + c];
-      swv[j] = sw[static_cast<size_t>(g) * n + c];
+      const int c = (wn * 4 + j) * 16 + col_in;
+      ws[j] = cur.wsum[c];
+      swv[j] = cur.sw[c];
     }
     float sa[4][4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      const int row = (mb0 + wm * 4 + i) * 16 + 4 * quad;
-      const float4 s = *reinterpret_cast<const float4 *>(steps + static_cast<size_t>(g) * m_pad + row);
-      sa[i][0] = s.x;
-      sa[i][1] = s.y;
-      sa[i][2] = s.z;
-      sa[i][3] = s.w;
+      const float4 sv = *reinterpret_cast<const float4 *>(&cur.steps[(wm * 4 + i) * 16 + 4 * quad]);
+      sa[i][0] = sv.x;
+      sa[i][1] = sv.y;
+      sa[i][2] = sv.z;
+      sa[i][3] = sv.w;
     }
 #pragma unroll
     for (int i = 0; i < 4; i++)
@@ -223,13 +262,18 @@ __global__ __launch_bounds__(256) void gemm_kernel(const int8_t *__restrict__ a_
         v4i c;
 #pragma unroll
         for (int r = 0; r < 4; r++) c[r] = (hsum[r] << 8) + ws[j];
-        const v4i s = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo[i], b[j], c, 0, 0, 0);
+        const v4i sum = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo[i], b[j], c, 0, 0, 0);
 #pragma unroll
         for (int r = 0; r < 4; r++) {
           const float scale = swv[j] * sa[i][r];
-          acc[i][j][r] = fmaf_(static_cast<float>(s[r]), scale, acc[i][j][r]);
+          acc[i][j][r] = fmaf_(static_cast<float>(sum[r]), scale, acc[i][j][r]);
         }
       }
+  };
+  copy_group(buf0, 0);
+  for (int g = 0; g < groups; g += 2) {
+    step(buf0, buf1, g);
+    if (g + 1 < groups) step(buf1, buf0, g + 1);
   }
 
   // Exception FMAs (ascending columns), then the epilogue.

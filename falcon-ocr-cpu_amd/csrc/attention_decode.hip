@@ -1,0 +1,292 @@
+// Decode and draft-verify attention (1..=8 query rows) over a compact KV cache,
+// head_dim 64: kernels::attention_with for query_len < 4 and decode64
+// (src/kernels/attention/mod.rs:256-311, online.rs:96-150, decode64.rs:22-33).
+//
+// The reference walks each query head's visible keys serially: 128-key tiles,
+// score = dot(q, k) * (1/8), running max, rescale by exp(old - new),
+// p = exp(s - max), den += p, out = fma(p, v, out), then
+// out = (out / den) * 1 / (1 + exp(sink - (max + ln den))). Here the keys of
+// a head are split across many waves (split-K): every wave runs that online
+// softmax over its own 64 (or 32) keys, and a second kernel merges the
+// partial states (max, denominator, unnormalized output) with the usual
+// exp(m_c - M) weights before the sink step. The sums run in a different
+// order than the reference's serial loop, so outputs agree within FP32
+// rounding, not bitwise; exp and ln are the device libm's.
+//
+// Wave task = (query head h, key chunk c). Lane group lg = lane / 16 takes the
+// chunk's keys 4i + lg; lane lp = lane % 16 holds dims 4lp..4lp+3 of the
+// query, the key, the value and the output. Every key and value load is one
+// float4 per lane (a wave instruction reads four 256-byte rows), all issued
+// before the first score. Dot products reduce over the 16 lanes of a group
+// with DPP (quad_perm, row_half_mirror, row_mirror: every lane ends with the
+// same sum). Consecutive tasks are the query heads of one KV head on the same
+// chunk, so their value rows are read together.
+//
+// Roofline: HBM. Bytes per call = keys (prefix keys per query head, generated
+// keys per KV head) + values per KV head over the visible keys, + q, out and
+// the partial states.
+#include "focr_internal.hpp"
+
+namespace focr {
+namespace {
+
+constexpr int kWaves = 4;
+
+struct DecArgs {
+  const float *q, *prefix_k, *generated_k, *v;
+  float *part_o, *part_md;  // [rows * n_heads][chunks][64], [rows * n_heads][chunks][2]
+  int prefix_len, total_len, n_heads, n_kv_heads, query_offset, image_start, image_end;
+  int chunks, tasks;
+};
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over the 16 lanes of a DPP row; every lane of the row gets the same
+// value (each step adds a value and its mirror image, so partners agree).
+__device__ __forceinline__ float row_sum16(float v) {
+  v = v + dpp<0xB1>(v);   // quad_perm [1,0,3,2]
+  v = v + dpp<0x4E>(v);   // quad_perm [2,3,0,1]
+  v = v + dpp<0x141>(v);  // row_half_mirror
+  return v + dpp<0x140>(v);  // row_mirror
+}
+
+__device__ __forceinline__ float xor_lane(float x, int mask) {
+  const int lane = threadIdx.x & 63;
+  return __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, __float_as_int(x)));
+}
+
+__device__ __forceinline__ float4 ld4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
+
+// Merge two online-softmax states (max m, denominator d, output o); both
+// partners compute the same bits (products identical, sums commutative).
+__device__ __forceinline__ void merge(float &m, float &d, float4 &o, float m2, float d2, float4 o2) {
+  const float mn = m > m2 ? m : m2;
+  if (mn == -__builtin_inff()) return;  // both empty
+  const float f1 = m == -__builtin_inff() ? 0.0f : expf_acc(m - mn);
+  const float f2 = m2 == -__builtin_inff() ? 0.0f : expf_acc(m2 - mn);
+  d = d * f1 + d2 * f2;
+  o = make_float4(o.x * f1 + o2.x * f2, o.y * f1 + o2.y * f2, o.z * f1 + o2.z * f2, o.w * f1 + o2.w * f2);
+  m = mn;
+}
+
+// M: query rows; KPL: keys per lane group (chunk = 4 * KPL keys).
+template <int M, int KPL>
+__global__ __launch_bounds__(256) void decode_partial_kernel(DecArgs a) {
+  constexpr int KW = 4 * KPL;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lg = lane >> 4, lp = lane & 15;
+  const int task = blockIdx.x * kWaves + wave;
+  if (task >= a.tasks) return;
+  const int repeat = a.n_heads / a.n_kv_heads;
+  const int t = task % repeat, gc = task / repeat;
+  const int c = gc % a.chunks, g = gc / a.chunks;
+  const int h = g * repeat + t;
+  const int key0 = c * KW;
+
+  // Geometry::visible_end per row (attention/mod.rs:60-67).
+  int vis[M], limit = 0;
+#pragma unroll
+  for (int r = 0; r < M; r++) {
+    const int abs = a.query_offset + r;
+    vis[r] = abs >= a.image_start && abs < a.image_end ? a.image_end : abs + 1;
+    limit = vis[r] > limit ? vis[r] : limit;
+  }
+  const int end = key0 + KW < limit ? key0 + KW : limit;
+
+  // Every key and value of the chunk, in flight before the first score.
+  float4 kb[KPL], vb[KPL];
+#pragma unroll
+  for (int i = 0; i < KPL; i++) {
+    const int j = key0 + 4 * i + lg;
+    const int jj = j < end ? j : 0;
+    const float *krow = jj < a.prefix_len
+                            ? a.prefix_k + (static_cast<size_t>(jj) * a.n_heads + h) * 64
+                            : a.generated_k + (static_cast<size_t>(jj - a.prefix_len) * a.n_kv_heads + g) * 64;
+    kb[i] = ld4(krow + 4 * lp);
+    vb[i] = ld4(a.v + (static_cast<size_t>(jj) * a.n_kv_heads + g) * 64 + 4 * lp);
+  }
+  float4 qv[M];
+#pragma unroll
+  for (int r = 0; r < M; r++) qv[r] = ld4(a.q + (static_cast<size_t>(r) * a.n_heads + h) * 64 + 4 * lp);
+
+  const float ninf = -__builtin_inff();
+  float m[M], den[M];
+  float4 o[M];
+#pragma unroll
+  for (int r = 0; r < M; r++) {
+    m[r] = ninf;
+    den[r] = 0.0f;
+    o[r] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
+  // Online softmax of this lane group's keys, four at a time.
+#pragma unroll
+  for (int b = 0; b < KPL / 4; b++) {
+    float s[4][M];
+#pragma unroll
+    for (int kk = 0; kk < 4; kk++) {
+      const int i = 4 * b + kk;
+      const int j = key0 + 4 * i + lg;
+      const float4 k = kb[i];
+#pragma unroll
+      for (int r = 0; r < M; r++) {
+        float d = qv[r].x * k.x;
+        d = fmaf_(qv[r].y, k.y, d);
+        d = fmaf_(qv[r].z, k.z, d);
+        d = fmaf_(qv[r].w, k.w, d);
+        d = row_sum16(d) * 0.125f;
+        s[kk][r] = j < end && j < vis[r] ? d : ninf;
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < M; r++) {
+      float bmax = s[0][r];
+#pragma unroll
+      for (int kk = 1; kk < 4; kk++) bmax = s[kk][r] > bmax ? s[kk][r] : bmax;
+      const float mn = bmax > m[r] ? bmax : m[r];
+      if (mn == ninf) continue;
+      const float rs = m[r] == ninf ? 0.0f : expf_acc(m[r] - mn);
+      den[r] = den[r] * rs;
+      o[r] = make_float4(o[r].x * rs, o[r].y * rs, o[r].z * rs, o[r].w * rs);
+      m[r] = mn;
+#pragma unroll
+      for (int kk = 0; kk < 4; kk++) {
+        const float p = s[kk][r] == ninf ? 0.0f : expf_acc(s[kk][r] - mn);
+        const float4 v = vb[4 * b + kk];
+        den[r] = den[r] + p;
+        o[r] = make_float4(fmaf_(p, v.x, o[r].x), fmaf_(p, v.y, o[r].y), fmaf_(p, v.z, o[r].z),
+                           fmaf_(p, v.w, o[r].w));
+      }
+    }
+  }
+  // Merge the four lane groups (lanes 16 and 32 apart), then store.
+#pragma unroll
+  for (int r = 0; r < M; r++) {
+#pragma unroll
+    for (int mask = 16; mask <= 32; mask *= 2) {
+      const float m2 = xor_lane(m[r], mask), d2 = xor_lane(den[r], mask);
+      const float4 o2 = make_float4(xor_lane(o[r].x, mask), xor_lane(o[r].y, mask), xor_lane(o[r].z, mask),
+                                    xor_lane(o[r].w, mask));
+      merge(m[r], den[r], o[r], m2, d2, o2);
+    }
+    const size_t slot = (static_cast<size_t>(r) * a.n_heads + h) * a.chunks + c;
+    if (lg == 0) *reinterpret_cast<float4 *>(a.part_o + slot * 64 + 4 * lp) = o[r];
+    if (lane == 0) *reinterpret_cast<float2 *>(a.part_md + slot * 2) = make_float2(m[r], den[r]);
+  }
+}
+
+struct CombineArgs {
+  const float *part_o, *part_md, *sinks;
+  float *out;
+  int n_heads, chunks;
+};
+
+// One workgroup per (row, head): lane = dim; the 4 waves take every 4th
+// chunk, and their sums are added in a fixed order. Final step as online.rs
+// head (lines 144-149): lse = max + ln(den), out = (o / den) * 1/(1 + exp(sink - lse)).
+__global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgs a) {
+  __shared__ float s_max[kWaves], s_den[kWaves], s_o[kWaves][64];
+  const int rh = blockIdx.x, h = rh % a.n_heads;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const float *md = a.part_md + static_cast<size_t>(rh) * a.chunks * 2;
+  const float *po = a.part_o + static_cast<size_t>(rh) * a.chunks * 64;
+  const float ninf = -__builtin_inff();
+  float mx = ninf;
+  for (int c = wave; c < a.chunks; c += kWaves) {
+    const float mc = md[2 * c];
+    mx = mc > mx ? mc : mx;
+  }
+  if (lane == 0) s_max[wave] = mx;
+  __syncthreads();
+  float big = s_max[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; w++) big = s_max[w] > big ? s_max[w] : big;
+  float den = 0.0f, o = 0.0f;
+  if (big != ninf)
+    for (int c = wave; c < a.chunks; c += kWaves) {
+      const float mc = md[2 * c];
+      const float f = mc == ninf ? 0.0f : expf_acc(mc - big);
+      den = den + md[2 * c + 1] * f;
+      o = o + po[static_cast<size_t>(c) * 64 + lane] * f;
+    }
+  if (lane == 0) s_den[wave] = den;
+  s_o[wave][lane] = o;
+  __syncthreads();
+  if (wave != 0) return;
+  const float d = (s_den[0] + s_den[1]) + (s_den[2] + s_den[3]);
+  const float total = (s_o[0][lane] + s_o[1][lane]) + (s_o[2][lane] + s_o[3][lane]);
+  const float lse = big + logf_acc(d);
+  const float sink_scale = __fdiv_rn(1.0f, 1.0f + expf_acc(a.sinks[h] - lse));
+  a.out[static_cast<size_t>(rh) * 64 + lane] = __fdiv_rn(total, d) * sink_scale;
+}
+
+template <int M>
+int launch_rows(Ctx *ctx, DecArgs a, int limit, const float *sinks, float *out, size_t rows) {
+  constexpr int KPL = M <= 4 ? 16 : 8;
+  a.chunks = (limit + 4 * KPL - 1) / (4 * KPL);
+  a.tasks = a.n_heads * a.chunks;
+  const size_t slots = rows * static_cast<size_t>(a.n_heads) * a.chunks;
+  const size_t bytes = slots * 66 * sizeof(float);
+  int rc = ensure_scratch(ctx, bytes);
+  if (rc != FOCR_OK) return rc;
+  a.part_o = static_cast<float *>(ctx->scratch);
+  a.part_md = a.part_o + slots * 64;
+  const unsigned blocks = static_cast<unsigned>((a.tasks + kWaves - 1) / kWaves);
+  hipLaunchKernelGGL((decode_partial_kernel<M, KPL>), dim3(blocks), dim3(64 * kWaves), 0, ctx->stream, a);
+  FOCR_HIP_CHECK(hipGetLastError());
+  CombineArgs c;
+  c.part_o = a.part_o;
+  c.part_md = a.part_md;
+  c.sinks = sinks;
+  c.out = out;
+  c.n_heads = a.n_heads;
+  c.chunks = a.chunks;
+  hipLaunchKernelGGL(decode_combine_kernel, dim3(static_cast<unsigned>(rows * a.n_heads)), dim3(64 * kWaves), 0,
+                     ctx->stream, c);
+  FOCR_HIP_CHECK(hipGetLastError());
+  return FOCR_OK;
+}
+
+}  // namespace
+
+int launch_attention_decode(Ctx *ctx, const float *q, const float *prefix_k, const float *generated_k, const float *v,
+                            size_t query_len, size_t prefix_len, size_t total_len, size_t n_heads, size_t n_kv_heads,
+                            size_t query_offset, size_t image_start, size_t image_end, const float *sinks,
+                            float *out) {
+  FOCR_REQUIRE(total_len < (size_t(1) << 30) && n_heads <= 4096, FOCR_E_SHAPE, "decode attention: shape too large");
+  DecArgs a;
+  a.q = q;
+  a.prefix_k = prefix_k;
+  a.generated_k = generated_k;
+  a.v = v;
+  a.prefix_len = static_cast<int>(prefix_len);
+  a.total_len = static_cast<int>(total_len);
+  a.n_heads = static_cast<int>(n_heads);
+  a.n_kv_heads = static_cast<int>(n_kv_heads);
+  a.query_offset = static_cast<int>(query_offset);
+  a.image_start = static_cast<int>(image_start);
+  a.image_end = static_cast<int>(image_end);
+  // The largest visible end over the rows bounds the keys read (validated:
+  // query_offset + query_len <= total_len and image_end <= prefix_len).
+  size_t limit = 0;
+  for (size_t r = 0; r < query_len; r++) {
+    const size_t abs = query_offset + r;
+    const size_t vis = abs >= image_start && abs < image_end ? image_end : abs + 1;
+    limit = vis > limit ? vis : limit;
+  }
+  switch (query_len) {
+    case 1: return launch_rows<1>(ctx, a, static_cast<int>(limit), sinks, out, query_len);
+    case 2: return launch_rows<2>(ctx, a, static_cast<int>(limit), sinks, out, query_len);
+    case 3: return launch_rows<3>(ctx, a, static_cast<int>(limit), sinks, out, query_len);
+    case 4: return launch_rows<4>(ctx, a, static_cast<int>(limit), sinks, out, query_len);
+    case 5: return launch_rows<5>(ctx, a, static_cast<int>(limit), sinks, out, query_len);
+    case 6: return launch_rows<6>(ctx, a, static_cast<int>(limit), sinks, out, query_len);
+    case 7: return launch_rows<7>(ctx, a, static_cast<int>(limit), sinks, out, query_len);
+    case 8: return launch_rows<8>(ctx, a, static_cast<int>(limit), sinks, out, query_len);
+    default: return set_error(FOCR_E_SHAPE, "decode attention takes 1..=8 query rows");
+  }
+}
+
+}  // namespace focr

@@ -367,7 +367,7 @@ int focr_linear_decode(focr_ctx *handle, const focr_linear *lh, const float *x, 
   FOCR_REQUIRE(rows <= 8, FOCR_E_SHAPE, "focr_linear_decode: 1..=8 rows (decode and draft verification)");
   if (rows == 0) return FOCR_OK;
   FOCR_REQUIRE(x && out, FOCR_E_ARG, "focr_linear_decode: null buffer");
-  return launch_gemv(ctx, lin, x, rows, out, false);
+  return launch_gemv(ctx, lin, x, rows, nullptr, FOCR_EPI_STORE, out);
 }
 
 int focr_linear_decode_glu(focr_ctx *handle, const focr_linear *lh, const float *x, size_t rows, float *gated) {
@@ -378,7 +378,21 @@ int focr_linear_decode_glu(focr_ctx *handle, const focr_linear *lh, const float 
   FOCR_REQUIRE(rows <= 8, FOCR_E_SHAPE, "focr_linear_decode_glu: 1..=8 rows");
   if (rows == 0) return FOCR_OK;
   FOCR_REQUIRE(x && gated, FOCR_E_ARG, "focr_linear_decode_glu: null buffer");
-  return launch_gemv(ctx, lin, x, rows, gated, true);
+  return launch_gemv(ctx, lin, x, rows, nullptr, FOCR_EPI_GLU, gated);
+}
+
+int focr_linear_decode_ex(focr_ctx *handle, const focr_linear *lh, const float *x, size_t rows,
+                          const float *row_scale, int epilogue, float *out) {
+  Ctx *ctx = reinterpret_cast<Ctx *>(handle);
+  const Linear *lin = reinterpret_cast<const Linear *>(lh);
+  FOCR_REQUIRE(ctx && lin, FOCR_E_ARG, "focr_linear_decode_ex: null argument");
+  FOCR_REQUIRE(epilogue == FOCR_EPI_STORE || epilogue == FOCR_EPI_GLU || epilogue == FOCR_EPI_ADD, FOCR_E_ARG,
+               "focr_linear_decode_ex: unknown epilogue");
+  FOCR_REQUIRE(epilogue != FOCR_EPI_GLU || lin->n % 2 == 0, FOCR_E_SHAPE, "GLU needs interleaved gate/up rows");
+  FOCR_REQUIRE(rows <= 8, FOCR_E_SHAPE, "focr_linear_decode_ex: 1..=8 rows (decode and draft verification)");
+  if (rows == 0) return FOCR_OK;
+  FOCR_REQUIRE(x && out, FOCR_E_ARG, "focr_linear_decode_ex: null buffer");
+  return launch_gemv(ctx, lin, x, rows, row_scale, epilogue, out);
 }
 
 int focr_linear_prefill(focr_ctx *handle, const focr_linear *lh, const float *x, size_t rows,
@@ -462,6 +476,45 @@ int focr_attention_prefill_bf16(focr_ctx *handle, const float *q, const float *k
   FOCR_HIP_CHECK(hipSetDevice(ctx->device));
   return launch_attention_bf16(ctx, q, k, v, query_len, n_heads, n_kv_heads, image_start, image_end, sinks, softmax,
                                out);
+}
+
+int focr_qkv_rows(focr_ctx *handle, const float *qkv, size_t rows, const float *rope, size_t n_heads,
+                  size_t n_kv_heads, size_t head_dim, size_t prefix_rows, float *q, float *prefix_k,
+                  float *generated_k, float *v) {
+  Ctx *ctx = reinterpret_cast<Ctx *>(handle);
+  FOCR_REQUIRE(ctx, FOCR_E_ARG, "focr_qkv_rows: null context");
+  FOCR_REQUIRE(n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0, FOCR_E_SHAPE, "qkv rows: GQA grouping");
+  FOCR_REQUIRE(head_dim == 64, FOCR_E_UNSUPPORTED, "the hip QKV row kernel takes head_dim 64");
+  FOCR_REQUIRE(prefix_rows <= rows, FOCR_E_SHAPE, "qkv rows: more prefix rows than rows");
+  if (rows == 0) return FOCR_OK;
+  FOCR_REQUIRE(qkv && rope && q && v, FOCR_E_ARG, "focr_qkv_rows: null buffer");
+  FOCR_REQUIRE(prefix_rows == 0 || prefix_k, FOCR_E_ARG, "focr_qkv_rows: prefix keys missing");
+  FOCR_REQUIRE(prefix_rows == rows || generated_k, FOCR_E_ARG, "focr_qkv_rows: generated keys missing");
+  FOCR_HIP_CHECK(hipSetDevice(ctx->device));
+  return launch_qkv_rows(ctx, qkv, rows, rope, n_heads, n_kv_heads, prefix_rows, q, prefix_k, generated_k, v);
+}
+
+int focr_attention_decode(focr_ctx *handle, const float *q, const float *prefix_k, const float *generated_k,
+                          const float *v, size_t query_len, size_t prefix_len, size_t total_len, size_t n_heads,
+                          size_t n_kv_heads, size_t head_dim, size_t query_offset, size_t image_start,
+                          size_t image_end, const float *sinks, float *out) {
+  Ctx *ctx = reinterpret_cast<Ctx *>(handle);
+  FOCR_REQUIRE(ctx, FOCR_E_ARG, "focr_attention_decode: null context");
+  // CompactKv::validate (src/kernels/attention/mod.rs:157-195).
+  FOCR_REQUIRE(head_dim > 0 && n_heads > 0 && n_kv_heads > 0, FOCR_E_SHAPE, "attention head dimensions must be positive");
+  FOCR_REQUIRE(head_dim == 64, FOCR_E_UNSUPPORTED, "the hip decode attention takes head_dim 64");
+  FOCR_REQUIRE(n_heads % n_kv_heads == 0, FOCR_E_SHAPE, "attention GQA grouping");
+  FOCR_REQUIRE(prefix_len <= total_len, FOCR_E_SHAPE, "attention prefix length");
+  FOCR_REQUIRE(image_start <= image_end && image_end <= prefix_len, FOCR_E_SHAPE, "attention image must be inside the prefix");
+  FOCR_REQUIRE(query_offset + query_len <= total_len, FOCR_E_SHAPE, "attention query interval");
+  FOCR_REQUIRE(query_len <= 8, FOCR_E_SHAPE, "decode attention takes 1..=8 query rows");
+  if (query_len == 0) return FOCR_OK;
+  FOCR_REQUIRE(q && v && sinks && out, FOCR_E_ARG, "focr_attention_decode: null buffer");
+  FOCR_REQUIRE(prefix_len == 0 || prefix_k, FOCR_E_ARG, "prefix keys missing");
+  FOCR_REQUIRE(prefix_len == total_len || generated_k, FOCR_E_ARG, "generated keys missing");
+  FOCR_HIP_CHECK(hipSetDevice(ctx->device));
+  return launch_attention_decode(ctx, q, prefix_k, generated_k, v, query_len, prefix_len, total_len, n_heads,
+                                 n_kv_heads, query_offset, image_start, image_end, sinks, out);
 }
 
 int focr_argmax(focr_ctx *handle, const float *logits, size_t rows, size_t vocab, uint32_t *tokens) {

@@ -75,7 +75,8 @@ struct Linear {
 };
 
 // ---- launchers (each validates its launch shape on the host) -------------
-int launch_gemv(Ctx *ctx, const Linear *lin, const float *x, size_t rows, float *out, bool glu);
+int launch_gemv(Ctx *ctx, const Linear *lin, const float *x, size_t rows, const float *row_scale, int epilogue,
+                float *out);
 int launch_dequantize(Ctx *ctx, const Linear *lin, float *out);
 int launch_row_scales(Ctx *ctx, const float *h, size_t rows, size_t width, float eps, float *out);
 int launch_prefill_f32(Ctx *ctx, const Linear *lin, const float *x, size_t rows,
@@ -92,6 +93,12 @@ int launch_attention_bf16(Ctx *ctx, const float *q, const float *k, const float 
                           size_t n_heads, size_t n_kv_heads, size_t image_start, size_t image_end,
                           const float *sinks, int softmax, float *out);
 int launch_argmax(Ctx *ctx, const float *logits, size_t rows, size_t vocab, uint32_t *result_dev);
+int launch_qkv_rows(Ctx *ctx, const float *qkv, size_t rows, const float *rope, size_t n_heads, size_t n_kv_heads,
+                    size_t prefix_rows, float *q, float *prefix_k, float *generated_k, float *v);
+int launch_attention_decode(Ctx *ctx, const float *q, const float *prefix_k, const float *generated_k, const float *v,
+                            size_t query_len, size_t prefix_len, size_t total_len, size_t n_heads, size_t n_kv_heads,
+                            size_t query_offset, size_t image_start, size_t image_end, const float *sinks,
+                            float *out);
 
 // ---- device helpers ---------------------------------------------------------
 __device__ __forceinline__ float fmaf_(float a, float b, float c) { return __builtin_fmaf(a, b, c); }

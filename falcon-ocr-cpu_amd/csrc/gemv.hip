@@ -12,24 +12,26 @@ static size_t rows_per_launch(const Linear *lin) {
   return fit < 8 ? fit : 8;
 }
 
-int launch_gemv(Ctx *ctx, const Linear *lin, const float *x, size_t rows, float *out, bool glu) {
+int launch_gemv(Ctx *ctx, const Linear *lin, const float *x, size_t rows, const float *row_scale, int epilogue,
+                float *out) {
   FOCR_HIP_CHECK(hipSetDevice(ctx->device));
   const size_t chunk = rows_per_launch(lin);
   FOCR_REQUIRE(chunk >= 1, FOCR_E_SHAPE, "GEMV: in_dim too large for one row of x in LDS");
-  const size_t width = glu ? lin->n / 2 : lin->n;
+  const size_t width = epilogue == FOCR_EPI_GLU ? lin->n / 2 : lin->n;
   // Rows are independent (each output row is its single-row dot, bitwise), so
   // a call whose inputs exceed the LDS budget runs as several launches.
   for (size_t r0 = 0; r0 < rows; r0 += chunk) {
     const size_t m = rows - r0 < chunk ? rows - r0 : chunk;
     const float *xr = x + r0 * lin->k;
+    const float *rs = row_scale ? row_scale + r0 : nullptr;
     float *orow = out + r0 * width;
     int rc;
     if (lin->bits == 8)
-      rc = gemv::launch_i8(ctx, lin, xr, m, orow, glu);
+      rc = gemv::launch_i8(ctx, lin, xr, rs, m, orow, epilogue);
     else if (lin->bits == 16)
-      rc = gemv::launch_i16(ctx, lin, xr, m, orow, glu);
+      rc = gemv::launch_i16(ctx, lin, xr, rs, m, orow, epilogue);
     else
-      rc = gemv::launch_f32(ctx, lin, xr, m, orow, glu);
+      rc = gemv::launch_f32(ctx, lin, xr, rs, m, orow, epilogue);
     if (rc != FOCR_OK) return rc;
   }
   return FOCR_OK;

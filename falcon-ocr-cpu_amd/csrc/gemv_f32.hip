@@ -4,8 +4,8 @@
 namespace focr {
 namespace gemv {
 
-int launch_f32(Ctx *ctx, const Linear *lin, const float *x, size_t rows, float *out, bool glu) {
-  return launch_rows<float, 0>(ctx, lin, x, rows, out, glu);
+int launch_f32(Ctx *ctx, const Linear *lin, const float *x, const float *rs, size_t rows, float *out, int epi) {
+  return launch_rows<float, 0>(ctx, lin, x, rs, rows, out, epi);
 }
 
 }  // namespace gemv

@@ -4,11 +4,11 @@
 namespace focr {
 namespace gemv {
 
-int launch_i16(Ctx *ctx, const Linear *lin, const float *x, size_t rows, float *out, bool glu) {
+int launch_i16(Ctx *ctx, const Linear *lin, const float *x, const float *rs, size_t rows, float *out, int epi) {
   switch (lin->group) {
-    case 32: return launch_rows<int16_t, 4>(ctx, lin, x, rows, out, glu);
-    case 64: return launch_rows<int16_t, 2>(ctx, lin, x, rows, out, glu);
-    default: return launch_rows<int16_t, 1>(ctx, lin, x, rows, out, glu);
+    case 32: return launch_rows<int16_t, 4>(ctx, lin, x, rs, rows, out, epi);
+    case 64: return launch_rows<int16_t, 2>(ctx, lin, x, rs, rows, out, epi);
+    default: return launch_rows<int16_t, 1>(ctx, lin, x, rs, rows, out, epi);
   }
 }
 

@@ -102,7 +102,8 @@ struct Args {
   const float *exc_vals;
   int n_exc;
   const float *x;
-  int n, k, group, groups, nb, steps, tiles_total, glu;
+  const float *row_scale;  // optional [rows]: x rows enter as fl(x * row_scale)
+  int n, k, group, groups, nb, steps, tiles_total, glu, add;
   float *out;
 };
 
@@ -142,11 +143,22 @@ __global__ __launch_bounds__(256) void kernel(Args a) {
   const int sc_count4 = kWaves * steps * 2 * NS / 4;
   // x[r][4i .. 4i + 3], every index clamped into the row (k >= 1; with
   // 16-byte rows k % 4 == 0 means k >= 4 whenever a float4 is read).
+  // rms_norm folded in: every x element used below is fl(x * row_scale[r])
+  // (rms_norm_row's `*y = *x * scale`, src/kernels/mod.rs:509-512).
   auto x_load = [&](int r, int i) {
     const float *row = a.x + static_cast<size_t>(r) * k;
-    if (x_vec) return reinterpret_cast<const float4 *>(row)[i * 4 + 3 < k ? i : 0];
-    auto at = [&](int c) { return row[c < k ? c : k - 1]; };
-    return make_float4(at(4 * i), at(4 * i + 1), at(4 * i + 2), at(4 * i + 3));
+    float4 v;
+    if (x_vec) {
+      v = reinterpret_cast<const float4 *>(row)[i * 4 + 3 < k ? i : 0];
+    } else {
+      auto at = [&](int c) { return row[c < k ? c : k - 1]; };
+      v = make_float4(at(4 * i), at(4 * i + 1), at(4 * i + 2), at(4 * i + 3));
+    }
+    if (a.row_scale) {
+      const float rs = a.row_scale[r];
+      v = make_float4(v.x * rs, v.y * rs, v.z * rs, v.w * rs);
+    }
+    return v;
   };
   auto sc_load = [&](int i) {
     const int g = sc_base4 + i;
@@ -255,7 +267,10 @@ __global__ __launch_bounds__(256) void kernel(Args a) {
   }
 
   const int ch0 = tile * kGemvChannels + h * 2;
-  auto x_col = [&](int r, int i) { return a.x[static_cast<size_t>(r) * k + i]; };
+  auto x_col = [&](int r, int i) {
+    const float v = a.x[static_cast<size_t>(r) * k + i];
+    return a.row_scale ? v * a.row_scale[r] : v;
+  };
 #pragma unroll
   for (int c = 0; c < 2; c++)
 #pragma unroll
@@ -311,6 +326,16 @@ __global__ __launch_bounds__(256) void kernel(Args a) {
 #pragma unroll
       for (int r = 0; r < M; r++) a.out[static_cast<size_t>(r) * ffn + i] = squared_relu_glu(total[0][r], total[1][r]);
     }
+  } else if (a.add) {
+    // add_residual (src/model/rope.rs:155-169): h += projected.
+#pragma unroll
+    for (int c = 0; c < 2; c++)
+      if (ch0 + c < a.n)
+#pragma unroll
+        for (int r = 0; r < M; r++) {
+          float *o = a.out + static_cast<size_t>(r) * a.n + ch0 + c;
+          *o = *o + total[c][r];
+        }
   } else {
 #pragma unroll
     for (int c = 0; c < 2; c++)
@@ -329,7 +354,7 @@ inline size_t scale_lds_bytes(const Linear *lin) { return kWaves * lin->gemv_ste
 constexpr size_t kLdsBudget = 64 * 1024;
 
 template <typename T, int M, int SPS, int W, bool ROLL = false>
-int launch_typed(Ctx *ctx, const Linear *lin, const float *x, float *out, bool glu) {
+int launch_typed(Ctx *ctx, const Linear *lin, const float *x, const float *rs, float *out, int epi) {
   const size_t lds = M * x_row_bytes(lin) + scale_lds_bytes(lin);
   FOCR_REQUIRE(lds <= kLdsBudget, FOCR_E_SHAPE, "GEMV: x rows exceed the LDS budget");
   const int blocks = static_cast<int>((lin->gemv_tiles + kWaves - 1) / kWaves);
@@ -342,6 +367,7 @@ int launch_typed(Ctx *ctx, const Linear *lin, const float *x, float *out, bool g
   a.exc_vals = lin->exc_vals;
   a.n_exc = static_cast<int>(lin->n_exc);
   a.x = x;
+  a.row_scale = rs;
   a.n = static_cast<int>(lin->n);
   a.k = static_cast<int>(lin->k);
   a.group = static_cast<int>(lin->group);
@@ -349,7 +375,8 @@ int launch_typed(Ctx *ctx, const Linear *lin, const float *x, float *out, bool g
   a.nb = static_cast<int>(lin->gemv_blocks);
   a.steps = static_cast<int>(lin->gemv_steps);
   a.tiles_total = static_cast<int>(lin->gemv_tiles);
-  a.glu = glu ? 1 : 0;
+  a.glu = epi == FOCR_EPI_GLU ? 1 : 0;
+  a.add = epi == FOCR_EPI_ADD ? 1 : 0;
   a.out = out;
   hipLaunchKernelGGL((kernel<T, M, SPS, W, ROLL>), dim3(blocks), dim3(64 * kWaves), lds, ctx->stream, a);
   FOCR_HIP_CHECK(hipGetLastError());
@@ -359,39 +386,39 @@ int launch_typed(Ctx *ctx, const Linear *lin, const float *x, float *out, bool g
 // Window buckets: every step in registers up to 20 steps (FP32: 36), which
 // covers every matrix of the model; longer rows refill a 20 (36) step window.
 template <typename T, int M, int SPS>
-int launch_window(Ctx *ctx, const Linear *lin, const float *x, float *out, bool glu) {
+int launch_window(Ctx *ctx, const Linear *lin, const float *x, const float *rs, float *out, int epi) {
   const size_t steps = lin->gemv_steps;
-  if (steps <= 4) return launch_typed<T, M, SPS, 4>(ctx, lin, x, out, glu);
-  if (steps <= 8) return launch_typed<T, M, SPS, 8>(ctx, lin, x, out, glu);
-  if (steps <= 12) return launch_typed<T, M, SPS, 12>(ctx, lin, x, out, glu);
-  if (steps <= 20) return launch_typed<T, M, SPS, 20>(ctx, lin, x, out, glu);
+  if (steps <= 4) return launch_typed<T, M, SPS, 4>(ctx, lin, x, rs, out, epi);
+  if (steps <= 8) return launch_typed<T, M, SPS, 8>(ctx, lin, x, rs, out, epi);
+  if (steps <= 12) return launch_typed<T, M, SPS, 12>(ctx, lin, x, rs, out, epi);
+  if (steps <= 20) return launch_typed<T, M, SPS, 20>(ctx, lin, x, rs, out, epi);
   if constexpr (SPS == 0) {
-    if (steps <= 36) return launch_typed<T, M, SPS, 36>(ctx, lin, x, out, glu);
-    return launch_typed<T, M, SPS, 36, true>(ctx, lin, x, out, glu);
+    if (steps <= 36) return launch_typed<T, M, SPS, 36>(ctx, lin, x, rs, out, epi);
+    return launch_typed<T, M, SPS, 36, true>(ctx, lin, x, rs, out, epi);
   } else {
-    return launch_typed<T, M, SPS, 20, true>(ctx, lin, x, out, glu);
+    return launch_typed<T, M, SPS, 20, true>(ctx, lin, x, rs, out, epi);
   }
 }
 
 template <typename T, int SPS>
-int launch_rows(Ctx *ctx, const Linear *lin, const float *x, size_t rows, float *out, bool glu) {
+int launch_rows(Ctx *ctx, const Linear *lin, const float *x, const float *rs, size_t rows, float *out, int epi) {
   switch (rows) {
-    case 1: return launch_window<T, 1, SPS>(ctx, lin, x, out, glu);
-    case 2: return launch_window<T, 2, SPS>(ctx, lin, x, out, glu);
-    case 3: return launch_window<T, 3, SPS>(ctx, lin, x, out, glu);
-    case 4: return launch_window<T, 4, SPS>(ctx, lin, x, out, glu);
-    case 5: return launch_window<T, 5, SPS>(ctx, lin, x, out, glu);
-    case 6: return launch_window<T, 6, SPS>(ctx, lin, x, out, glu);
-    case 7: return launch_window<T, 7, SPS>(ctx, lin, x, out, glu);
-    case 8: return launch_window<T, 8, SPS>(ctx, lin, x, out, glu);
+    case 1: return launch_window<T, 1, SPS>(ctx, lin, x, rs, out, epi);
+    case 2: return launch_window<T, 2, SPS>(ctx, lin, x, rs, out, epi);
+    case 3: return launch_window<T, 3, SPS>(ctx, lin, x, rs, out, epi);
+    case 4: return launch_window<T, 4, SPS>(ctx, lin, x, rs, out, epi);
+    case 5: return launch_window<T, 5, SPS>(ctx, lin, x, rs, out, epi);
+    case 6: return launch_window<T, 6, SPS>(ctx, lin, x, rs, out, epi);
+    case 7: return launch_window<T, 7, SPS>(ctx, lin, x, rs, out, epi);
+    case 8: return launch_window<T, 8, SPS>(ctx, lin, x, rs, out, epi);
     default: return set_error(FOCR_E_SHAPE, "GEMV rows must be 1..=8");
   }
 }
 
 // Per-code-type dispatch (one translation unit each, compiled in parallel).
-int launch_i8(Ctx *ctx, const Linear *lin, const float *x, size_t rows, float *out, bool glu);
-int launch_i16(Ctx *ctx, const Linear *lin, const float *x, size_t rows, float *out, bool glu);
-int launch_f32(Ctx *ctx, const Linear *lin, const float *x, size_t rows, float *out, bool glu);
+int launch_i8(Ctx *ctx, const Linear *lin, const float *x, const float *rs, size_t rows, float *out, int epi);
+int launch_i16(Ctx *ctx, const Linear *lin, const float *x, const float *rs, size_t rows, float *out, int epi);
+int launch_f32(Ctx *ctx, const Linear *lin, const float *x, const float *rs, size_t rows, float *out, int epi);
 
 }  // namespace gemv
 }  // namespace focr

@@ -1,0 +1,113 @@
+// The row step between the QKV projection and attention: split the fused QKV
+// row into heads, RMS-normalize each 64-wide query and key head (unit weight,
+// eps f32::EPSILON), rotate with the row's RoPE factors, and append the keys
+// and values to the compact cache.
+//
+// Prefill rows follow fused_prefix_rows / fused_row (src/model/fused.rs:17-123):
+// keys are stored for every query head (prefix keys, the GQA-expanded head
+// h / (n_heads / n_kv_heads) normalized and rotated with head h's factors).
+// Rows past the prefix follow split_norm_rope (src/model/rope.rs:14-86) and
+// LayerCache::append's append_unique_heads (src/model/cache.rs:117-140,
+// 202-216): one key per KV head, the expanded head g * repeat. Values are the
+// KV heads' slices, copied. Every element sees the reference's operations:
+//   scale = 1 / sqrt(sum_squares_pairwise(x) / 64 + eps)   (IEEE div, sqrt)
+//   y = x * scale
+//   out[2i] = y[2i] * cos - y[2i+1] * sin, out[2i+1] = y[2i] * sin + y[2i+1] * cos
+// with separate roundings (no contraction), so outputs are bitwise the
+// reference's.
+//
+// One workgroup of 4 waves per row; each wave normalizes and rotates whole
+// heads, lane = element. The 64-wide pairwise sum is two 32-leaves folded
+// 16-8-4-2-1 (xor butterflies: lane i < w adds lane i + w, the other lanes'
+// values are never read) and then leaf0 + leaf1.
+//
+// Roofline: HBM. Bytes per row = 4 * (qkv width + n_heads * 64 rope floats
+// + q + keys + values written).
+#include "focr_internal.hpp"
+
+namespace focr {
+namespace {
+
+struct RowArgs {
+  const float *qkv, *rope;
+  float *q, *prefix_k, *generated_k, *v;
+  int rows, prefix_rows, n_heads, n_kv_heads;
+};
+
+// x[lane ^ mask] with ds_swizzle-free cross-lane reads (ds_bpermute).
+__device__ __forceinline__ float xor_lane(float x, int mask) {
+  const int lane = threadIdx.x & 63;
+  return __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, __float_as_int(x)));
+}
+
+// rms_norm_row (width 64, no weight) then the pairwise rotation, for the
+// head whose element `lane` is x. Returns the rotated element.
+__device__ __forceinline__ float norm_rope(float x, float2 factor, int lane) {
+  float part = x * x;
+#pragma unroll
+  for (int w = 16; w >= 1; w /= 2) part = part + xor_lane(part, w);
+  // Lane 0 holds leaf(0..32), lane 32 leaf(32..64).
+  const float leaf0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 0));
+  const float leaf1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 32));
+  const float sum = leaf0 + leaf1;
+  const float scale = __fdiv_rn(1.0f, __builtin_sqrtf(__fdiv_rn(sum, 64.0f) + 1.1920929e-7f));
+  const float y = x * scale;
+  const float partner = xor_lane(y, 1);
+  const bool even = (lane & 1) == 0;
+  const float a = even ? y : partner, b = even ? partner : y;
+  return even ? a * factor.x - b * factor.y : a * factor.y + b * factor.x;
+}
+
+__global__ __launch_bounds__(256) void qkv_rows_kernel(RowArgs a) {
+  const int row = blockIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int qdim = a.n_heads * 64, kdim = a.n_kv_heads * 64;
+  const int repeat = a.n_heads / a.n_kv_heads;
+  const float *src = a.qkv + static_cast<size_t>(row) * (qdim + 2 * kdim);
+  const float2 *rope = reinterpret_cast<const float2 *>(a.rope) + static_cast<size_t>(row) * a.n_heads * 32;
+  const bool prefix = row < a.prefix_rows;
+  // Jobs: n_heads query heads, then the key heads (n_heads expanded ones for
+  // a prefix row, n_kv_heads unique ones for a generated row).
+  const int key_jobs = prefix ? a.n_heads : a.n_kv_heads;
+  const int jobs = a.n_heads + key_jobs;
+  for (int job = wave; job < jobs; job += 4) {
+    if (job < a.n_heads) {
+      const int h = job;
+      const float y = norm_rope(src[h * 64 + lane], rope[h * 32 + lane / 2], lane);
+      a.q[static_cast<size_t>(row) * qdim + h * 64 + lane] = y;
+    } else if (prefix) {
+      const int h = job - a.n_heads;  // expanded key head: KV head h / repeat
+      const float y = norm_rope(src[qdim + (h / repeat) * 64 + lane], rope[h * 32 + lane / 2], lane);
+      a.prefix_k[static_cast<size_t>(row) * qdim + h * 64 + lane] = y;
+    } else {
+      const int g = job - a.n_heads;  // unique key head g = expanded head g * repeat
+      const float y = norm_rope(src[qdim + g * 64 + lane], rope[g * repeat * 32 + lane / 2], lane);
+      a.generated_k[static_cast<size_t>(row - a.prefix_rows) * kdim + g * 64 + lane] = y;
+    }
+  }
+  // Values: the KV heads' slice of the row, copied.
+  for (int i = threadIdx.x; i < kdim; i += 256) a.v[static_cast<size_t>(row) * kdim + i] = src[qdim + kdim + i];
+}
+
+}  // namespace
+
+int launch_qkv_rows(Ctx *ctx, const float *qkv, size_t rows, const float *rope, size_t n_heads, size_t n_kv_heads,
+                    size_t prefix_rows, float *q, float *prefix_k, float *generated_k, float *v) {
+  FOCR_REQUIRE(rows < (size_t(1) << 31) && n_heads <= 1024, FOCR_E_SHAPE, "qkv rows: shape too large");
+  RowArgs a;
+  a.qkv = qkv;
+  a.rope = rope;
+  a.q = q;
+  a.prefix_k = prefix_k;
+  a.generated_k = generated_k;
+  a.v = v;
+  a.rows = static_cast<int>(rows);
+  a.prefix_rows = static_cast<int>(prefix_rows < rows ? prefix_rows : rows);
+  a.n_heads = static_cast<int>(n_heads);
+  a.n_kv_heads = static_cast<int>(n_kv_heads);
+  hipLaunchKernelGGL(qkv_rows_kernel, dim3(static_cast<unsigned>(rows)), dim3(256), 0, ctx->stream, a);
+  FOCR_HIP_CHECK(hipGetLastError());
+  return FOCR_OK;
+}
+
+}  // namespace focr

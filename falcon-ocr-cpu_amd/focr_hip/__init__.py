@@ -18,6 +18,10 @@ Names and argument meanings follow the reference (amazingvince/falcon-ocr-cpu):
   attention_with         (attention/mod.rs:256-311)
   row_scales / rms_scale (model/rope.rs:147-152, kernels/mod.rs:531-533)
   argmax                 (runner/mod.rs:916-930)
+  qkv_rows               fused_prefix_rows / split_norm_rope + LayerCache::append
+                         (model/fused.rs:17-123, model/rope.rs:14-86, model/cache.rs:117-216)
+  DecoderLayer           one layer of Model::forward_layers (model/mod.rs:513-691):
+                         prefill and decode steps over a device-resident compact cache
 
 Tensors are torch CUDA tensors (device memory and streams come from torch;
 the arithmetic runs in the HIP library). Errors raise ``FocrError``, the
@@ -64,11 +68,14 @@ SIGNATURES = {
     "focr_linear_dequantize": (_I, [_P, _P, _P]),
     "focr_linear_decode": (_I, [_P, _P, _P, _Z, _P]),
     "focr_linear_decode_glu": (_I, [_P, _P, _P, _Z, _P]),
+    "focr_linear_decode_ex": (_I, [_P, _P, _P, _Z, _P, _I, _P]),
     "focr_linear_prefill": (_I, [_P, _P, _P, _Z, _P, _I, _I, _P]),
     "focr_row_scales": (_I, [_P, _P, _Z, _Z, _F, _P]),
     "focr_attention_prefill": (_I, [_P, _P, _P, _P, _P, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _P, _I, _I, _P]),
     "focr_attention_prefill_bf16": (_I, [_P, _P, _P, _P, _Z, _Z, _Z, _Z, _Z, _Z, _P, _I, _I, _P]),
     "focr_argmax": (_I, [_P, _P, _Z, _Z, _P]),
+    "focr_qkv_rows": (_I, [_P, _P, _Z, _P, _Z, _Z, _Z, _Z, _P, _P, _P, _P]),
+    "focr_attention_decode": (_I, [_P, _P, _P, _P, _P, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _P, _P]),
 }
 
 
@@ -261,6 +268,25 @@ class Linear:
         _check(lib().focr_linear_decode_glu(self.ctx.handle, self.handle, _dev(input), rows, _dev(gated)))
         return gated
 
+    def linear_ex(self, input, rows: int, row_scale=None, epilogue: Epilogue = Epilogue.STORE, out=None):
+        """The decode step's projection with its neighbours folded in
+        (Model::project_qkv / attention_out_ffn, model/mod.rs:421-492):
+        input rows times `row_scale` (rms_norm), then `linear` (STORE),
+        `linear_glu` (GLU) or `linear` + `add_residual` into `out` (ADD)."""
+        torch = _torch()
+        if input.numel() != rows * self.in_dim:
+            raise FocrError(-2, "W8 input shape")
+        width = self.out_dim // 2 if epilogue == Epilogue.GLU else self.out_dim
+        if out is None:
+            if epilogue == Epilogue.ADD:
+                raise FocrError(-1, "Epilogue.ADD needs the residual `out`")
+            out = torch.empty((rows, width), dtype=torch.float32, device=input.device)
+        elif out.numel() != rows * width:
+            raise FocrError(-2, "W8 output shape")
+        _check(lib().focr_linear_decode_ex(self.ctx.handle, self.handle, _dev(input), rows, _dev(row_scale),
+                                           int(epilogue), _dev(out)))
+        return out
+
     def prefill(self, input, rows: int, row_scale=None, epilogue: Epilogue = Epilogue.STORE, out=None,
                 kernel: PrefillProjection = PrefillProjection.F32_MFMA):
         """`QuantLinear::prefill`: out = epilogue(A' W^T), A' = input * row_scale per row.
@@ -342,17 +368,53 @@ class PrefillOptions:
 
 def attention_with(q, kv: CompactKv, query_len: int, geometry: Geometry, sinks, options: PrefillOptions = PrefillOptions(),
                    output=None, ctx: Optional[Context] = None):
-    """`kernels::attention_with` for a prefill: returns [query_len][n_heads][64]."""
+    """`kernels::attention_with`: returns [query_len][n_heads][64].
+
+    As the reference dispatches (attention/mod.rs:271-311): fewer than 4
+    queries, or up to 8 over a cache with generated keys (decode and draft
+    verification), take the decode kernel; the rest the prefill tiles."""
     torch = _torch()
     ctx = ctx or default_context()
     if output is None:
         output = torch.empty_like(q)
+    if query_len < 4 or (query_len <= 8 and kv.total_len > kv.prefix_len):
+        return attention_decode(q, kv, query_len, geometry, sinks, output=output, ctx=ctx)
     _check(lib().focr_attention_prefill(ctx.handle, _dev(q), _dev(kv.prefix_k), _dev(kv.generated_k), _dev(kv.v),
                                         query_len, kv.prefix_len, kv.total_len, kv.n_heads, kv.n_kv_heads,
                                         kv.head_dim, geometry.query_offset, geometry.image_start,
                                         geometry.image_end, _dev(sinks), int(options.fp32_softmax),
                                         int(options.exp), _dev(output)))
     return output
+
+
+def attention_decode(q, kv: CompactKv, query_len: int, geometry: Geometry, sinks, output=None,
+                     ctx: Optional[Context] = None):
+    """Decode / draft-verify attention of 1..=8 query rows (online::head,
+    attention/online.rs:96-150, split over many waves): [query_len][n_heads][64]."""
+    torch = _torch()
+    ctx = ctx or default_context()
+    if output is None:
+        output = torch.empty_like(q)
+    _check(lib().focr_attention_decode(ctx.handle, _dev(q), _dev(kv.prefix_k), _dev(kv.generated_k), _dev(kv.v),
+                                       query_len, kv.prefix_len, kv.total_len, kv.n_heads, kv.n_kv_heads,
+                                       kv.head_dim, geometry.query_offset, geometry.image_start, geometry.image_end,
+                                       _dev(sinks), _dev(output)))
+    return output
+
+
+def qkv_rows(qkv, rows: int, rope, n_heads: int, n_kv_heads: int, prefix_rows: int, q=None, prefix_k=None,
+             generated_k=None, v=None, head_dim: int = 64, ctx: Optional[Context] = None):
+    """Split, per-head RMS norm, RoPE and cache append of `rows` QKV rows
+    (fused_prefix_rows for the first `prefix_rows`, split_norm_rope +
+    LayerCache::append after them). `prefix_k`, `generated_k` and `v` are the
+    cache slots of the first row; returns q [rows][n_heads][64]."""
+    torch = _torch()
+    ctx = ctx or default_context()
+    if q is None:
+        q = torch.empty((rows, n_heads, head_dim), dtype=torch.float32, device=qkv.device)
+    _check(lib().focr_qkv_rows(ctx.handle, _dev(qkv), rows, _dev(rope), n_heads, n_kv_heads, head_dim, prefix_rows,
+                               _dev(q), _dev(prefix_k), _dev(generated_k), _dev(v)))
+    return q
 
 
 def attention_prefill_bf16(q, kv: CompactKv, query_len: int, geometry: Geometry, sinks, output,
@@ -392,3 +454,5 @@ def argmax(logits, rows: int, vocab: int, ctx: Optional[Context] = None):
     tokens = (ctypes.c_uint32 * rows)()
     _check(lib().focr_argmax(ctx.handle, _dev(logits), rows, vocab, ctypes.cast(tokens, ctypes.c_void_p)))
     return list(tokens)
+
+from .layer import DecoderLayer  # noqa: E402,F401

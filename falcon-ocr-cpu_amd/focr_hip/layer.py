@@ -1,0 +1,137 @@
+"""One decoder layer of the Falcon-OCR runner on the `hip` backend.
+
+`DecoderLayer` strings the C ABI's operators together the way
+``Model::forward_layers`` does for one layer (src/model/mod.rs:513-691):
+
+prefill (rows > 8, a quantized body on the panel path, mod.rs:568,956-1007)::
+
+    row_scales(h)                          panel_qkv (rms norm folded into packing)
+    qkv.prefill(h, row_scale) -> qkv        Epilogue::Store
+    qkv_rows(qkv) -> q, prefix keys, values fused_prefix_rows (model/fused.rs:17-99)
+    attention_with(q, cache) -> attn        LayerCache::attention (model/cache.rs:142-197)
+    wo.prefill(attn) += h                   Epilogue::Add(h)
+    row_scales(h); w13.prefill(h) -> gated  Epilogue::Glu
+    w2.prefill(gated) += h                  Epilogue::Add(h)
+
+decode / draft verification (1..=8 rows, project_qkv + attention_out_ffn,
+mod.rs:421-492)::
+
+    rms_norm(h) . qkv -> qkv                focr_linear_decode_ex with the row scale
+    qkv_rows -> q, generated keys, values   split_norm_rope + LayerCache::append
+    attention over prefix + generated keys  (decode kernel)
+    wo(attn); add_residual                  Epilogue ADD
+    rms_norm(h) . w13 -> gated (GLU)
+    w2(gated); add_residual
+
+The compact cache (prefix keys per query head, generated keys and values per
+KV head) lives in device memory sized for `capacity` positions, as
+``Session::new`` sizes the reference's (model/cache.rs:364). RoPE factors
+come from the caller ([rows][n_heads][32][2] cos/sin pairs), as
+``rotary_factors`` provides them to the reference's row kernels.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+from . import (CompactKv, Context, Epilogue, FocrError, Geometry, PrefillOptions, PrefillProjection, attention_with,
+               default_context, qkv_rows, row_scales)
+
+
+class DecoderLayer:
+    def __init__(self, qkv, wo, w13, w2, sinks, capacity: int, n_heads: int = 16, n_kv_heads: int = 8,
+                 head_dim: int = 64, projection: PrefillProjection = PrefillProjection.I16,
+                 options: PrefillOptions = PrefillOptions(), ctx: Optional[Context] = None):
+        import torch
+
+        self.ctx = ctx or default_context()
+        self.qkv, self.wo, self.w13, self.w2 = qkv, wo, w13, w2
+        self.sinks = sinks
+        self.n_heads, self.n_kv_heads, self.head_dim = n_heads, n_kv_heads, head_dim
+        self.dim = qkv.in_dim
+        qdim, kdim = n_heads * head_dim, n_kv_heads * head_dim
+        if qkv.out_dim != qdim + 2 * kdim or wo.in_dim != qdim or wo.out_dim != self.dim:
+            raise FocrError(-2, "layer shapes: qkv [qdim + 2 kdim][dim], wo [dim][qdim]")
+        if w13.in_dim != self.dim or w2.in_dim != w13.out_dim // 2 or w2.out_dim != self.dim:
+            raise FocrError(-2, "layer shapes: w13 [2 ffn][dim], w2 [dim][ffn]")
+        self.projection, self.options = projection, options
+        self.capacity = capacity
+        dev = f"cuda:{self.ctx.device}"
+        f32 = torch.float32
+        self.prefix_k = torch.empty((capacity, n_heads, head_dim), dtype=f32, device=dev)
+        self.generated_k = torch.empty((capacity, n_kv_heads, head_dim), dtype=f32, device=dev)
+        self.v = torch.empty((capacity, n_kv_heads, head_dim), dtype=f32, device=dev)
+        self.len = 0
+        self.prefix_len = 0
+        self.image = (0, 0)
+        self._work = {}
+
+    def _buf(self, name: str, shape):
+        import torch
+
+        t = self._work.get(name)
+        n = 1
+        for s in shape:
+            n *= s
+        if t is None or t.numel() < n:
+            t = torch.empty(n, dtype=torch.float32, device=f"cuda:{self.ctx.device}")
+            self._work[name] = t
+        return t[:n].view(*shape)
+
+    def kv(self, total: int) -> CompactKv:
+        """The cache's first `total` positions as a CompactKv."""
+        p = self.prefix_len
+        gen = self.generated_k[: total - p] if total > p else None
+        return CompactKv(self.prefix_k[:p], gen, self.v[:total], p, total, self.n_heads, self.n_kv_heads,
+                         self.head_dim)
+
+    def prefill(self, h, rope, image_start: int, image_end: int):
+        """The whole prompt (offset 0): updates `h` [rows][dim] in place and
+        fills the prefix cache."""
+        rows = h.shape[0]
+        if self.len != 0:
+            raise FocrError(-2, "a prefill forwards the whole prefix first")
+        if rows > self.capacity:
+            raise FocrError(-2, "KV context exhausted")
+        if not (image_start <= image_end <= rows):
+            raise FocrError(-2, "attention image must be inside the prefix")
+        ctx, qdim = self.ctx, self.n_heads * self.head_dim
+        rs = row_scales(h, self.dim, out=self._buf("rs", (rows,)), ctx=ctx)
+        qkv = self.qkv.prefill(h, rows, row_scale=rs, epilogue=Epilogue.STORE, kernel=self.projection,
+                               out=self._buf("qkv", (rows, self.qkv.out_dim)))
+        self.prefix_len = rows
+        q = qkv_rows(qkv, rows, rope, self.n_heads, self.n_kv_heads, rows, q=self._buf("q", (rows, self.n_heads, 64)),
+                     prefix_k=self.prefix_k[:rows], v=self.v[:rows], ctx=ctx)
+        self.image = (image_start, image_end)
+        attn = attention_with(q, self.kv(rows), rows, Geometry(0, image_start, image_end), self.sinks, self.options,
+                              output=self._buf("attn", (rows, self.n_heads, 64)), ctx=ctx)
+        self.wo.prefill(attn, rows, epilogue=Epilogue.ADD, out=h, kernel=self.projection)
+        rs = row_scales(h, self.dim, out=rs, ctx=ctx)
+        gated = self.w13.prefill(h, rows, row_scale=rs, epilogue=Epilogue.GLU, kernel=self.projection,
+                                 out=self._buf("gated", (rows, self.w13.out_dim // 2)))
+        self.w2.prefill(gated, rows, epilogue=Epilogue.ADD, out=h, kernel=self.projection)
+        self.len = rows
+        return h
+
+    def decode(self, h, rope):
+        """1..=8 rows at positions len.. (a greedy step, or the last token plus
+        drafts): updates `h` [rows][dim] in place and appends to the cache."""
+        rows = h.shape[0]
+        if not 1 <= rows <= 8:
+            raise FocrError(-2, "decode takes 1..=8 rows")
+        if self.len + rows > self.capacity:
+            raise FocrError(-2, "KV context exhausted")
+        ctx, p, pos = self.ctx, self.prefix_len, self.len
+        rs = row_scales(h, self.dim, out=self._buf("drs", (rows,)), ctx=ctx)
+        qkv = self.qkv.linear_ex(h, rows, row_scale=rs, out=self._buf("dqkv", (rows, self.qkv.out_dim)))
+        q = qkv_rows(qkv, rows, rope, self.n_heads, self.n_kv_heads, 0, q=self._buf("dq", (rows, self.n_heads, 64)),
+                     generated_k=self.generated_k[pos - p: pos - p + rows], v=self.v[pos: pos + rows], ctx=ctx)
+        total = pos + rows
+        attn = attention_with(q, self.kv(total), rows, Geometry(pos, *self.image), self.sinks, self.options,
+                              output=self._buf("dattn", (rows, self.n_heads, 64)), ctx=ctx)
+        self.wo.linear_ex(attn, rows, epilogue=Epilogue.ADD, out=h)
+        rs = row_scales(h, self.dim, out=rs, ctx=ctx)
+        gated = self.w13.linear_ex(h, rows, row_scale=rs, epilogue=Epilogue.GLU,
+                                   out=self._buf("dgated", (rows, self.w13.out_dim // 2)))
+        self.w2.linear_ex(gated, rows, epilogue=Epilogue.ADD, out=h)
+        self.len = total
+        return h

@@ -121,6 +121,17 @@ int focr_linear_decode(focr_ctx *ctx, const focr_linear *lin, const float *x_dev
 int focr_linear_decode_glu(focr_ctx *ctx, const focr_linear *lin, const float *x_dev,
                            size_t rows, float *gated_dev);
 
+/* The decode step's projections with their neighbours folded in, as
+ * Model::project_qkv / attention_out_ffn call them for 1..=8 rows
+ * (src/model/mod.rs:421-492): row_scale_dev optional [rows] multiplies each
+ * input row first (rms_norm_row's `x * scale`, src/kernels/mod.rs:497-514,
+ * the factor from focr_row_scales); epilogue FOCR_EPI_STORE (linear),
+ * FOCR_EPI_GLU (linear_glu, out [rows][out/2]) or FOCR_EPI_ADD
+ * (add_residual, src/model/rope.rs:155-169: out += projection). Bitwise equal
+ * to the separate reference passes. */
+int focr_linear_decode_ex(focr_ctx *ctx, const focr_linear *lin, const float *x_dev, size_t rows,
+                          const float *row_scale_dev, int epilogue, float *out_dev);
+
 /* ---- A2 / A3: prefill projection ---------------------------------------- */
 /* QuantLinear::prefill (src/quant/linear.rs:634-707) and its FP32 panel
  * and INT16 panel kernels (src/kernels/panels/{panel,panel_i16}.rs).
@@ -174,6 +185,42 @@ int focr_attention_prefill_bf16(focr_ctx *ctx, const float *q_dev, const float *
                                 size_t n_kv_heads, size_t head_dim, size_t image_start,
                                 size_t image_end, const float *sinks_dev, int softmax,
                                 int exp_mode, float *out_dev);
+
+/* ---- the QKV row step (split, per-head RMS norm, RoPE, cache append) ---- */
+/* fused_prefix_rows / fused_row (src/model/fused.rs:17-123) for the first
+ * prefix_rows rows, and split_norm_rope + LayerCache::append
+ * (src/model/rope.rs:14-86, src/model/cache.rs:117-140,202-216) for the
+ * rest, head_dim 64:
+ *   qkv_dev [rows][n_heads*64 + 2*n_kv_heads*64] (the QKV projection rows);
+ *   rope_dev [rows][n_heads][32][2] ([cos, sin] per rotated pair, as
+ *   rotary_factors builds them, src/model/rope.rs:103-142);
+ *   q_dev [rows][n_heads][64] normalized and rotated queries;
+ *   prefix_k_dev [prefix_rows][n_heads][64] (keys of every query head: the
+ *   KV head h/(n_heads/n_kv_heads), rotated with head h's factors);
+ *   generated_k_dev [rows - prefix_rows][n_kv_heads][64] (one key per KV
+ *   head: the expanded head g*(n_heads/n_kv_heads));
+ *   v_dev [rows][n_kv_heads][64] (values, copied).
+ * Per head: y = x * (1/sqrt(pairwise_sum(x^2)/64 + f32::EPSILON)), then
+ * (a, b) -> (a*cos - b*sin, a*sin + b*cos). Bitwise. The output pointers
+ * are the cache slots of the first row (append = write at the end). */
+int focr_qkv_rows(focr_ctx *ctx, const float *qkv_dev, size_t rows, const float *rope_dev,
+                  size_t n_heads, size_t n_kv_heads, size_t head_dim, size_t prefix_rows,
+                  float *q_dev, float *prefix_k_dev, float *generated_k_dev, float *v_dev);
+
+/* ---- decode / draft-verify attention -------------------------------------- */
+/* kernels::attention_with for 1..=8 query rows over a compact cache with
+ * generated keys (src/kernels/attention/mod.rs:256-311 -> online::head,
+ * online.rs:96-150, and decode64, decode64.rs:22-33), head_dim 64; the
+ * arguments mean what they mean for focr_attention_prefill. The keys of each
+ * head are split over many waves and the partial softmax states merged, so
+ * the result is within FP32 rounding of the reference's serial loop; exp/ln
+ * are the device libm's (the reference uses the platform expf, ExpMode does
+ * not apply to decode). Uses the context scratch for the partial states. */
+int focr_attention_decode(focr_ctx *ctx, const float *q_dev, const float *prefix_k_dev,
+                          const float *generated_k_dev, const float *v_dev, size_t query_len,
+                          size_t prefix_len, size_t total_len, size_t n_heads, size_t n_kv_heads,
+                          size_t head_dim, size_t query_offset, size_t image_start,
+                          size_t image_end, const float *sinks_dev, float *out_dev);
 
 /* ---- A9: greedy selection ------------------------------------------------ */
 /* argmax of each row (src/runner/mod.rs:916-939): first index of the

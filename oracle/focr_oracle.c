@@ -36,6 +36,7 @@
  */
 #include "focr_oracle.h"
 
+#include <float.h>
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -855,4 +856,94 @@ int orc_argmax(const float *logits, size_t n, uint32_t *out) {
     if (!finite) return -1;
     *out = (uint32_t)best;
     return 0;
+}
+
+/* ---- the QKV row step ------------------------------------------------------ */
+/* rms_norm_row on one 64-wide head, no weight (src/kernels/mod.rs:497-514),
+ * then the pairwise rotation (src/model/fused.rs:109-120, the same products
+ * as split_norm_rope's, src/model/rope.rs:60-72). rope: [32][2] = [cos, sin]. */
+static void norm_rope_head(const float *x, const float *rope, float *out) {
+    float scale = orc_rms_scale(x, HD, FLT_EPSILON);
+    float y[HD];
+    for (int i = 0; i < HD; i++) y[i] = x[i] * scale;
+    for (int pair = 0; pair < HD / 2; pair++) {
+        float c = rope[2 * pair], s = rope[2 * pair + 1];
+        float a = y[2 * pair], b = y[2 * pair + 1];
+        out[2 * pair] = a * c - b * s;
+        out[2 * pair + 1] = a * s + b * c;
+    }
+}
+
+void orc_qkv_rows(const float *qkv, size_t rows, const float *rope, size_t n_heads, size_t n_kv_heads,
+                  size_t prefix_rows, float *q, float *prefix_k, float *generated_k, float *v) {
+    size_t qdim = n_heads * HD, kdim = n_kv_heads * HD, repeat = n_heads / n_kv_heads;
+#pragma omp parallel for schedule(static)
+    for (long r = 0; r < (long)rows; r++) {
+        const float *src = qkv + (size_t)r * (qdim + 2 * kdim);
+        const float *factors = rope + (size_t)r * n_heads * HD; /* n_heads * 32 pairs * 2 */
+        for (size_t h = 0; h < n_heads; h++)
+            norm_rope_head(src + h * HD, factors + h * HD, q + (size_t)r * qdim + h * HD);
+        if ((size_t)r < prefix_rows) {
+            /* fused_row: every query head's key (fused.rs:107-111). */
+            for (size_t h = 0; h < n_heads; h++)
+                norm_rope_head(src + qdim + (h / repeat) * HD, factors + h * HD, prefix_k + (size_t)r * qdim + h * HD);
+        } else {
+            /* split_norm_rope's expanded keys, then append_unique_heads keeps
+             * the first head of each group (cache.rs:202-216). */
+            for (size_t g = 0; g < n_kv_heads; g++)
+                norm_rope_head(src + qdim + g * HD, factors + g * repeat * HD,
+                               generated_k + ((size_t)r - prefix_rows) * kdim + g * HD);
+        }
+        memcpy(v + (size_t)r * kdim, src + qdim + kdim, kdim * sizeof(float));
+    }
+}
+
+/* ---- decode attention ----------------------------------------------------- */
+/* online::head (src/kernels/attention/online.rs:96-150) with the 64-wide
+ * simd::dot / simd::axpy (src/simd.rs:749-777,925-940) and the platform expf
+ * and logf, for query qh = query * n_heads + head. */
+static void decode_head(const float *q, const Cache *cache, size_t query_offset, size_t image_start,
+                        size_t image_end, size_t query, size_t head, const float *sinks, float *out) {
+    const float scale = 1.0f / sqrtf((float)HD);
+    size_t repeat = cache->n_heads / cache->n_kv_heads, kv_head = head / repeat;
+    size_t absolute = query_offset + query;
+    size_t visible_end = absolute >= image_start && absolute < image_end ? image_end : absolute + 1;
+    const float *qvec = q + (query * cache->n_heads + head) * HD;
+    for (int d = 0; d < HD; d++) out[d] = 0.0f;
+    float running_max = -INFINITY, denominator = 0.0f;
+    float logits[KT];
+    for (size_t start = 0; start < visible_end; start += KT) {
+        size_t len = visible_end - start < KT ? visible_end - start : KT;
+        float block_max = -INFINITY;
+        for (size_t j = 0; j < len; j++) {
+            logits[j] = orc_dot(qvec, cache_key(cache, start + j, head), HD) * scale;
+            block_max = fmaxf(block_max, logits[j]);
+        }
+        float new_max = fmaxf(running_max, block_max);
+        float rescale = running_max == -INFINITY ? 0.0f : expf(running_max - new_max);
+        for (int d = 0; d < HD; d++) out[d] *= rescale;
+        denominator *= rescale;
+        for (size_t j = 0; j < len; j++) logits[j] = expf(logits[j] - new_max);
+        for (size_t j = 0; j < len; j++) {
+            float p = logits[j];
+            const float *value = cache_value(cache, start + j, kv_head);
+            denominator += p;
+            for (int d = 0; d < HD; d++) out[d] = fmaf(p, value[d], out[d]);
+        }
+        running_max = new_max;
+    }
+    float logsumexp = running_max + logf(denominator);
+    float sink_scale = 1.0f / (1.0f + expf(sinks[head] - logsumexp));
+    for (int d = 0; d < HD; d++) out[d] = (out[d] / denominator) * sink_scale;
+}
+
+void orc_attention_decode(const float *q, const float *prefix_k, const float *generated_k, const float *v,
+                          size_t query_len, size_t prefix_len, size_t total_len, size_t n_heads,
+                          size_t n_kv_heads, size_t query_offset, size_t image_start, size_t image_end,
+                          const float *sinks, float *out) {
+    Cache cache = {prefix_k, generated_k, v, prefix_len, total_len, n_heads, n_kv_heads};
+#pragma omp parallel for schedule(static)
+    for (long qh = 0; qh < (long)(query_len * n_heads); qh++)
+        decode_head(q, &cache, query_offset, image_start, image_end, (size_t)qh / n_heads, (size_t)qh % n_heads,
+                    sinks, out + (size_t)qh * HD);
 }

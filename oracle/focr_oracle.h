@@ -121,6 +121,25 @@ void orc_attention_prefill_tiles(const float *q, const float *prefix_k, const fl
                                  const float *sinks, int static_softmax, int exp_fast,
                                  size_t tile_begin, size_t tile_end, float *out);
 
+/* ---- the QKV row step --------------------------------------------------- */
+/* fused_row (src/model/fused.rs:101-123) for rows < prefix_rows, and
+ * split_norm_rope + append_unique_heads (src/model/rope.rs:14-86,
+ * src/model/cache.rs:202-216) for the rest; head_dim 64. qkv
+ * [rows][qdim + 2 kdim]; rope [rows][n_heads][32][2]; q [rows][n_heads][64];
+ * prefix_k [prefix_rows][n_heads][64]; generated_k [rows-prefix_rows][n_kv][64];
+ * v [rows][n_kv][64]. */
+void orc_qkv_rows(const float *qkv, size_t rows, const float *rope, size_t n_heads, size_t n_kv_heads,
+                  size_t prefix_rows, float *q, float *prefix_k, float *generated_k, float *v);
+
+/* ---- decode attention --------------------------------------------------- */
+/* online::head (src/kernels/attention/online.rs:96-150) for every (query,
+ * head), as decode64 and online::attention run it (query_len 1..3 in the
+ * reference; any count here), platform expf/logf. */
+void orc_attention_decode(const float *q, const float *prefix_k, const float *generated_k, const float *v,
+                          size_t query_len, size_t prefix_len, size_t total_len, size_t n_heads,
+                          size_t n_kv_heads, size_t query_offset, size_t image_start, size_t image_end,
+                          const float *sinks, float *out);
+
 /* ---- A9: greedy selection --------------------------------------------- */
 /* argmax, src/runner/mod.rs:916-930. 0 ok, -1 on non-finite/empty. */
 int orc_argmax(const float *logits, size_t n, uint32_t *out);

@@ -78,6 +78,8 @@ _sig("orc_attention_prefill_bf16_tiles", None, _P, _P, _P, _Z, _Z, _Z, _Z, _Z, _
 _sig("orc_exp2_minimax", _F, _F)
 _sig("orc_bf16_round", _F, _F)
 _sig("orc_argmax", _I, _P, _Z, _P)
+_sig("orc_qkv_rows", None, _P, _Z, _P, _Z, _Z, _Z, _P, _P, _P, _P)
+_sig("orc_attention_decode", None, _P, _P, _P, _P, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _P, _P)
 _sig("orc_set_threads", None, _I)
 _sig("orc_get_threads", _I)
 
@@ -284,6 +286,33 @@ def bf16_round(x):
     r = ((u + 0x7fff + ((u >> 16) & 1)) & 0xffff0000).astype(np.uint32)
     r = np.where(nan, (u.astype(np.uint32) | 0x00400000) & 0xffff0000, r).astype(np.uint32)
     return r.view(np.float32)
+
+
+def qkv_rows(qkv, rows, rope, n_heads, n_kv_heads, prefix_rows):
+    """fused_row / split_norm_rope + append_unique_heads (src/model/fused.rs:101-123,
+    src/model/rope.rs:14-86, src/model/cache.rs:202-216): returns
+    (q [rows][n_heads][64], prefix_k [prefix_rows][n_heads][64],
+    generated_k [rows - prefix_rows][n_kv_heads][64], v [rows][n_kv_heads][64])."""
+    qkv, rope = _f32(qkv), _f32(rope)
+    q = np.zeros((rows, n_heads, 64), dtype=np.float32)
+    pk = np.zeros((prefix_rows, n_heads, 64), dtype=np.float32)
+    gk = np.zeros((rows - prefix_rows, n_kv_heads, 64), dtype=np.float32)
+    v = np.zeros((rows, n_kv_heads, 64), dtype=np.float32)
+    _lib.orc_qkv_rows(_ptr(qkv), rows, _ptr(rope), n_heads, n_kv_heads, prefix_rows, _ptr(q), _ptr(pk), _ptr(gk),
+                      _ptr(v))
+    return q, pk, gk, v
+
+
+def attention_decode(q, prefix_k, generated_k, v, query_len, prefix_len, total_len, n_heads, n_kv_heads,
+                     query_offset, image_start, image_end, sinks):
+    """online::head (src/kernels/attention/online.rs:96-150) for every (query, head)."""
+    q, v, sinks = _f32(q), _f32(v), _f32(sinks)
+    pk = _f32(prefix_k) if prefix_len else None
+    gk = _f32(generated_k) if total_len > prefix_len else None
+    out = np.zeros(query_len * n_heads * 64, dtype=np.float32)
+    _lib.orc_attention_decode(_ptr(q), _ptr(pk), _ptr(gk), _ptr(v), query_len, prefix_len, total_len, n_heads,
+                              n_kv_heads, query_offset, image_start, image_end, _ptr(sinks), _ptr(out))
+    return out.reshape(query_len, n_heads, 64)
 
 
 def argmax(logits):

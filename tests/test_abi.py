@@ -21,7 +21,8 @@ def declared_functions():
 def test_header_declares_the_boundary():
     names = declared_functions()
     for required in ("focr_linear_upload", "focr_linear_decode", "focr_linear_decode_glu", "focr_linear_prefill",
-                     "focr_linear_dequantize", "focr_row_scales", "focr_attention_prefill", "focr_argmax"):
+                     "focr_linear_dequantize", "focr_row_scales", "focr_attention_prefill", "focr_argmax",
+                     "focr_linear_decode_ex", "focr_qkv_rows", "focr_attention_decode"):
         assert required in names
 
 
@@ -44,6 +45,9 @@ def test_null_arguments_are_errors_not_crashes():
     assert lib.focr_linear_decode(None, None, None, 1, None) == -1
     assert lib.focr_linear_prefill(None, None, None, 1, None, 0, 0, None) == -1
     assert lib.focr_attention_prefill(None, *([None] * 4), *([0] * 9), None, 0, 0, None) == -1
+    assert lib.focr_linear_decode_ex(None, None, None, 1, None, 0, None) == -1
+    assert lib.focr_qkv_rows(None, None, 1, None, 16, 8, 64, 0, None, None, None, None) == -1
+    assert lib.focr_attention_decode(None, *([None] * 4), *([0] * 9), None, None) == -1
     assert lib.focr_ctx_destroy(None) == 0
     assert lib.focr_linear_free(None) == 0
 

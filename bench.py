@@ -206,6 +206,86 @@ def bench_attention(torch, fh, gen, np, reps):
     return res
 
 
+def bench_layer(torch, fh, gen, np, steps=64):
+    """one GPTQ INT8 g64 decoder layer (checkpoint shapes:
+    dim 768, QKV 768->2048, WO 1024->768, W13 768->4608 + GLU, W2 2304->768;
+    16 query / 8 KV heads of 64) prefilled over P = 16,320 rows (image
+    [0, 4096)), then `steps` greedy decode steps growing the cache to 16,384.
+    Prefill stages are timed with HIP events (the layer's phase marks); the
+    decode steps are captured into one HIP graph and replayed."""
+    P, img, dim, heads, kv = 16384 - steps, 4096, 768, 16, 8
+    qd, kd, ffn = heads * 64, kv * 64, 2304
+    shapes = {"qkv": (qd + 2 * kd, dim), "wo": (dim, qd), "w13": (2 * ffn, dim), "w2": (dim, ffn)}
+    lins = {}
+    for i, (name, (n, k)) in enumerate(shapes.items()):
+        codes = gen.codes_uniform((n, k), -127, 127, np.int8, 30 + 2 * i)
+        scales = gen.uniform((n, k // 64), 1e-4, 4e-4, 31 + 2 * i)
+        lins[name] = fh.QuantLinear(8, codes, scales, 64)
+    sinks = torch.from_numpy(gen.uniform(heads, -2.0, 2.0, 40)).cuda()
+    layer = fh.DecoderLayer(lins["qkv"], lins["wo"], lins["w13"], lins["w2"], sinks, capacity=P + steps)
+    ang = gen.uniform((P + steps, heads, 32), -3.14159, 3.14159, 41)
+    rope = torch.from_numpy(np.stack([np.cos(ang), np.sin(ang)], -1).astype(np.float32)).cuda()
+    h0 = torch.from_numpy(gen.normal((P, dim), 1.0, 42)).cuda()
+    xs = torch.from_numpy(gen.normal((steps, 1, dim), 1.0, 43)).cuda()
+    stream = torch.cuda.current_stream()
+    # Prefill: one untimed pass (allocates the workspace), then a timed one.
+    marks = []
+    clock = lambda stage: marks.append((stage, torch.cuda.Event(enable_timing=True))) or marks[-1][1].record(stream)
+    layer.prefill(h0.clone(), rope[:P], 0, img)
+    h = h0.clone()
+    layer.len = 0
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    layer.prefill(h, rope[:P], 0, img, clock=clock)
+    torch.cuda.synchronize()
+    stage_ms, prev = {}, start
+    for stage, ev in marks:
+        stage_ms[stage] = round(prev.elapsed_time(ev), 4)
+        prev = ev
+    prefill_ms = start.elapsed_time(marks[-1][1])
+    proj_flop = 2.0 * P * sum(n * k for n, k in shapes.values())
+    visible = img * img + sum(q + 1 for q in range(img, P))
+    attn_flop = 4.0 * 64 * visible * heads
+    # Decode: a warm step allocates the decode workspace; the cache is then
+    # rewound and the `steps` steps are captured and replayed once.
+    layer.decode(xs[0].clone(), rope[P:P + 1])
+    layer.len = P
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    ctx = fh.default_context()
+    cap = torch.cuda.Stream()
+    cap.wait_stream(stream)
+    with torch.cuda.stream(cap):
+        with torch.cuda.graph(g, stream=cap):
+            ctx.use_stream(torch.cuda.current_stream())
+            for t in range(steps):
+                layer.decode(xs[t], rope[P + t:P + t + 1])
+    stream.wait_stream(cap)
+    ctx.use_stream(stream)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    g.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    decode_ms = e0.elapsed_time(e1)
+    # Bytes per decode step: the four matrices' GEMV tiles and scales, the
+    # visible keys (prefix keys per query head, generated per KV head) and values.
+    w_bytes = sum(n * k + 4 * n * (k // 64) for n, k in shapes.values())
+    avg_total = P + (steps + 1) / 2.0
+    kv_bytes = 4 * 64 * (P * heads + (avg_total - P) * kv + avg_total * kv)
+    step_bytes = w_bytes + kv_bytes
+    for lin in lins.values():
+        lin.free()
+    return {"prefill_rows": P, "prefill_ms": round(prefill_ms, 3), "prefill_stage_ms": stage_ms,
+            "prefill_gflop": round((proj_flop + attn_flop) / 1e9, 2),
+            "prefill_tflops": round((proj_flop + attn_flop) / (prefill_ms * 1e-3) / 1e12, 2),
+            "decode_steps": steps, "decode_us_per_step": round(decode_ms * 1e3 / steps, 2),
+            "decode_bytes_per_step": int(step_bytes),
+            "decode_gbs": round(step_bytes / (decode_ms * 1e-3 / steps) / 1e9, 1)}
+
+
 def bench_copy(torch, reps):
     """A plain device copy of known size (calibrates rocprofv3 FETCH/WRITE_SIZE)."""
     n = 256 << 20
@@ -263,7 +343,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--ops", default="gemv,gemm,i16,attention,copy")
+    ap.add_argument("--ops", default="gemv,gemm,i16,attention,layer,copy")
     ap.add_argument("--reps", type=int, default=20, help="timed launches per secondary op")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
@@ -307,6 +387,9 @@ def main():
     if "attention" in ops:
         per_op["attention_prefill"] = bench_attention(torch, fh, gen, np, max(5, args.reps // 2))
         log(f"attention: {per_op['attention_prefill']}")
+    if "layer" in ops:
+        per_op["layer_int8_16k"] = bench_layer(torch, fh, gen, np)
+        log(f"layer: {per_op['layer_int8_16k']}")
     if "copy" in ops:
         per_op["copy_256MiB"] = bench_copy(torch, 10)
     cpu = None if args.no_cpu else cpu_baseline(np, gen)

@@ -7,7 +7,7 @@
 // p = exp(s - max), den += p, out = fma(p, v, out), then
 // out = (out / den) * 1 / (1 + exp(sink - (max + ln den))). Here the keys of
 // a head are split across many waves (split-K): every wave runs that online
-// softmax over its own 64 (or 32) keys, and a second kernel merges the
+// softmax over its own run of keys, and a second kernel merges the
 // partial states (max, denominator, unnormalized output) with the usual
 // exp(m_c - M) weights before the sink step. The sums run in a different
 // order than the reference's serial loop, so outputs agree within FP32
@@ -16,8 +16,8 @@
 // Wave task = (query head h, key chunk c). Lane group lg = lane / 16 takes the
 // chunk's keys 4i + lg; lane lp = lane % 16 holds dims 4lp..4lp+3 of the
 // query, the key, the value and the output. Every key and value load is one
-// float4 per lane (a wave instruction reads four 256-byte rows), all issued
-// before the first score. Dot products reduce over the 16 lanes of a group
+// float4 per lane (a wave instruction reads four 256-byte rows); the next 32
+// keys are in flight while the current 32 are scored. Dot products reduce over the 16 lanes of a group
 // with DPP (quad_perm, row_half_mirror, row_mirror: every lane ends with the
 // same sum). Consecutive tasks are the query heads of one KV head on the same
 // chunk, so their value rows are read together.
@@ -72,10 +72,14 @@ __device__ __forceinline__ void merge(float &m, float &d, float4 &o, float m2, f
   m = mn;
 }
 
-// M: query rows; KPL: keys per lane group (chunk = 4 * KPL keys).
-template <int M, int KPL>
-__global__ __launch_bounds__(256) void decode_partial_kernel(DecArgs a) {
-  constexpr int KW = 4 * KPL;
+// Keys per lane group per iteration (a wave takes 4 * kKpl = 32 keys per
+// iteration, double-buffered: the next iteration's keys and values are in
+// flight while the current ones are scored).
+constexpr int kKpl = 8;
+
+// M: query rows. A wave task covers `iters` iterations of 32 keys.
+template <int M>
+__global__ __launch_bounds__(256) void decode_partial_kernel(DecArgs a, int iters) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int lg = lane >> 4, lp = lane & 15;
   const int task = blockIdx.x * kWaves + wave;
@@ -84,7 +88,7 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(DecArgs a) {
   const int t = task % repeat, gc = task / repeat;
   const int c = gc % a.chunks, g = gc / a.chunks;
   const int h = g * repeat + t;
-  const int key0 = c * KW;
+  const int key0 = c * iters * 4 * kKpl;
 
   // Geometry::visible_end per row (attention/mod.rs:60-67).
   int vis[M], limit = 0;
@@ -94,20 +98,23 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(DecArgs a) {
     vis[r] = abs >= a.image_start && abs < a.image_end ? a.image_end : abs + 1;
     limit = vis[r] > limit ? vis[r] : limit;
   }
-  const int end = key0 + KW < limit ? key0 + KW : limit;
 
-  // Every key and value of the chunk, in flight before the first score.
-  float4 kb[KPL], vb[KPL];
+  // Keys key0 + 32 it + 4 i + lg of iteration `it` (clamped to key 0 past
+  // the visible keys; those are masked below).
+  auto load = [&](float4 (&kb)[kKpl], float4 (&vb)[kKpl], int it) {
 #pragma unroll
-  for (int i = 0; i < KPL; i++) {
-    const int j = key0 + 4 * i + lg;
-    const int jj = j < end ? j : 0;
-    const float *krow = jj < a.prefix_len
-                            ? a.prefix_k + (static_cast<size_t>(jj) * a.n_heads + h) * 64
-                            : a.generated_k + (static_cast<size_t>(jj - a.prefix_len) * a.n_kv_heads + g) * 64;
-    kb[i] = ld4(krow + 4 * lp);
-    vb[i] = ld4(a.v + (static_cast<size_t>(jj) * a.n_kv_heads + g) * 64 + 4 * lp);
-  }
+    for (int i = 0; i < kKpl; i++) {
+      const int j = key0 + 32 * it + 4 * i + lg;
+      const int jj = j < limit ? j : 0;
+      const float *krow = jj < a.prefix_len
+                              ? a.prefix_k + (static_cast<size_t>(jj) * a.n_heads + h) * 64
+                              : a.generated_k + (static_cast<size_t>(jj - a.prefix_len) * a.n_kv_heads + g) * 64;
+      kb[i] = ld4(krow + 4 * lp);
+      vb[i] = ld4(a.v + (static_cast<size_t>(jj) * a.n_kv_heads + g) * 64 + 4 * lp);
+    }
+  };
+  float4 ka[kKpl], va[kKpl], kb[kKpl], vb[kKpl];
+  load(ka, va, 0);
   float4 qv[M];
 #pragma unroll
   for (int r = 0; r < M; r++) qv[r] = ld4(a.q + (static_cast<size_t>(r) * a.n_heads + h) * 64 + 4 * lp);
@@ -121,44 +128,54 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(DecArgs a) {
     den[r] = 0.0f;
     o[r] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   }
-  // Online softmax of this lane group's keys, four at a time.
+  // Online softmax of this lane group's keys of one iteration, four at a time.
+  auto consume = [&](const float4 (&kk4)[kKpl], const float4 (&vv4)[kKpl], int it) {
 #pragma unroll
-  for (int b = 0; b < KPL / 4; b++) {
-    float s[4][M];
-#pragma unroll
-    for (int kk = 0; kk < 4; kk++) {
-      const int i = 4 * b + kk;
-      const int j = key0 + 4 * i + lg;
-      const float4 k = kb[i];
-#pragma unroll
-      for (int r = 0; r < M; r++) {
-        float d = qv[r].x * k.x;
-        d = fmaf_(qv[r].y, k.y, d);
-        d = fmaf_(qv[r].z, k.z, d);
-        d = fmaf_(qv[r].w, k.w, d);
-        d = row_sum16(d) * 0.125f;
-        s[kk][r] = j < end && j < vis[r] ? d : ninf;
-      }
-    }
-#pragma unroll
-    for (int r = 0; r < M; r++) {
-      float bmax = s[0][r];
-#pragma unroll
-      for (int kk = 1; kk < 4; kk++) bmax = s[kk][r] > bmax ? s[kk][r] : bmax;
-      const float mn = bmax > m[r] ? bmax : m[r];
-      if (mn == ninf) continue;
-      const float rs = m[r] == ninf ? 0.0f : expf_acc(m[r] - mn);
-      den[r] = den[r] * rs;
-      o[r] = make_float4(o[r].x * rs, o[r].y * rs, o[r].z * rs, o[r].w * rs);
-      m[r] = mn;
+    for (int b = 0; b < kKpl / 4; b++) {
+      float s[4][M];
 #pragma unroll
       for (int kk = 0; kk < 4; kk++) {
-        const float p = s[kk][r] == ninf ? 0.0f : expf_acc(s[kk][r] - mn);
-        const float4 v = vb[4 * b + kk];
-        den[r] = den[r] + p;
-        o[r] = make_float4(fmaf_(p, v.x, o[r].x), fmaf_(p, v.y, o[r].y), fmaf_(p, v.z, o[r].z),
-                           fmaf_(p, v.w, o[r].w));
+        const int i = 4 * b + kk;
+        const int j = key0 + 32 * it + 4 * i + lg;
+        const float4 k = kk4[i];
+#pragma unroll
+        for (int r = 0; r < M; r++) {
+          float d = qv[r].x * k.x;
+          d = fmaf_(qv[r].y, k.y, d);
+          d = fmaf_(qv[r].z, k.z, d);
+          d = fmaf_(qv[r].w, k.w, d);
+          d = row_sum16(d) * 0.125f;
+          s[kk][r] = j < vis[r] ? d : ninf;
+        }
       }
+#pragma unroll
+      for (int r = 0; r < M; r++) {
+        float bmax = s[0][r];
+#pragma unroll
+        for (int kk = 1; kk < 4; kk++) bmax = s[kk][r] > bmax ? s[kk][r] : bmax;
+        const float mn = bmax > m[r] ? bmax : m[r];
+        if (mn == ninf) continue;
+        const float rs = m[r] == ninf ? 0.0f : expf_acc(m[r] - mn);
+        den[r] = den[r] * rs;
+        o[r] = make_float4(o[r].x * rs, o[r].y * rs, o[r].z * rs, o[r].w * rs);
+        m[r] = mn;
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) {
+          const float p = s[kk][r] == ninf ? 0.0f : expf_acc(s[kk][r] - mn);
+          const float4 v = vv4[4 * b + kk];
+          den[r] = den[r] + p;
+          o[r] = make_float4(fmaf_(p, v.x, o[r].x), fmaf_(p, v.y, o[r].y), fmaf_(p, v.z, o[r].z),
+                             fmaf_(p, v.w, o[r].w));
+        }
+      }
+    }
+  };
+  for (int it = 0; it < iters; it += 2) {
+    if (it + 1 < iters) load(kb, vb, it + 1);
+    consume(ka, va, it);
+    if (it + 1 < iters) {
+      if (it + 2 < iters) load(ka, va, it + 2);
+      consume(kb, vb, it + 1);
     }
   }
   // Merge the four lane groups (lanes 16 and 32 apart), then store.
@@ -183,39 +200,73 @@ struct CombineArgs {
   int n_heads, chunks;
 };
 
-// One workgroup per (row, head): lane = dim; the 4 waves take every 4th
-// chunk, and their sums are added in a fixed order. Final step as online.rs
-// head (lines 144-149): lse = max + ln(den), out = (o / den) * 1/(1 + exp(sink - lse)).
+constexpr int kMaxChunks = 1024;
+
+// Sum over a wave in a fixed order (every lane gets the same value).
+__device__ __forceinline__ float wave_sum(float v) {
+  v = row_sum16(v);
+  v = v + xor_lane(v, 16);
+  return v + xor_lane(v, 32);
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int mask = 1; mask < 64; mask *= 2) {
+    const float o = xor_lane(v, mask);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+// One workgroup per (row, head). Thread t takes chunks t, t + 256, ... for
+// the maximum and the weights exp(m_c - M); then lane = dim and wave w sums
+// the outputs of chunks w, w + 4, ...; the partial sums are added in a fixed
+// order. Final step as online.rs head (lines 144-149):
+// lse = max + ln(den), out = (o / den) * 1/(1 + exp(sink - lse)).
 __global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgs a) {
-  __shared__ float s_max[kWaves], s_den[kWaves], s_o[kWaves][64];
+  __shared__ float s_f[kMaxChunks];
+  __shared__ float s_red[kWaves], s_o[kWaves][64];
   const int rh = blockIdx.x, h = rh % a.n_heads;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const float *md = a.part_md + static_cast<size_t>(rh) * a.chunks * 2;
   const float *po = a.part_o + static_cast<size_t>(rh) * a.chunks * 64;
   const float ninf = -__builtin_inff();
   float mx = ninf;
-  for (int c = wave; c < a.chunks; c += kWaves) {
+  for (int c = tid; c < a.chunks; c += 256) {
     const float mc = md[2 * c];
     mx = mc > mx ? mc : mx;
   }
-  if (lane == 0) s_max[wave] = mx;
+  mx = wave_max(mx);
+  if (lane == 0) s_red[wave] = mx;
   __syncthreads();
-  float big = s_max[0];
+  float big = s_red[0];
 #pragma unroll
-  for (int w = 1; w < kWaves; w++) big = s_max[w] > big ? s_max[w] : big;
-  float den = 0.0f, o = 0.0f;
-  if (big != ninf)
-    for (int c = wave; c < a.chunks; c += kWaves) {
-      const float mc = md[2 * c];
-      const float f = mc == ninf ? 0.0f : expf_acc(mc - big);
-      den = den + md[2 * c + 1] * f;
-      o = o + po[static_cast<size_t>(c) * 64 + lane] * f;
-    }
-  if (lane == 0) s_den[wave] = den;
+  for (int w = 1; w < kWaves; w++) big = s_red[w] > big ? s_red[w] : big;
+  __syncthreads();
+  float den = 0.0f;
+  for (int c = tid; c < a.chunks; c += 256) {
+    const float mc = md[2 * c];
+    const float f = mc == ninf || big == ninf ? 0.0f : expf_acc(mc - big);
+    s_f[c] = f;
+    den = den + md[2 * c + 1] * f;
+  }
+  den = wave_sum(den);
+  if (lane == 0) s_red[wave] = den;
+  __syncthreads();
+  float o = 0.0f;
+  int c = wave;
+  for (; c + 12 < a.chunks; c += 16) {
+    const float o0 = po[static_cast<size_t>(c) * 64 + lane], o1 = po[static_cast<size_t>(c + 4) * 64 + lane];
+    const float o2 = po[static_cast<size_t>(c + 8) * 64 + lane], o3 = po[static_cast<size_t>(c + 12) * 64 + lane];
+    o = fmaf_(o0, s_f[c], o);
+    o = fmaf_(o1, s_f[c + 4], o);
+    o = fmaf_(o2, s_f[c + 8], o);
+    o = fmaf_(o3, s_f[c + 12], o);
+  }
+  for (; c < a.chunks; c += 4) o = fmaf_(po[static_cast<size_t>(c) * 64 + lane], s_f[c], o);
   s_o[wave][lane] = o;
   __syncthreads();
   if (wave != 0) return;
-  const float d = (s_den[0] + s_den[1]) + (s_den[2] + s_den[3]);
+  const float d = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
   const float total = (s_o[0][lane] + s_o[1][lane]) + (s_o[2][lane] + s_o[3][lane]);
   const float lse = big + logf_acc(d);
   const float sink_scale = __fdiv_rn(1.0f, 1.0f + expf_acc(a.sinks[h] - lse));
@@ -224,8 +275,15 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgs a) {
 
 template <int M>
 int launch_rows(Ctx *ctx, DecArgs a, int limit, const float *sinks, float *out, size_t rows) {
-  constexpr int KPL = M <= 4 ? 16 : 8;
-  a.chunks = (limit + 4 * KPL - 1) / (4 * KPL);
+  // Keys per wave: enough waves to fill the chip (about 2048), at most
+  // kMaxChunks chunks per head, whole 32-key iterations.
+  const long want = (static_cast<long>(limit) * a.n_heads + 2047) / 2048;
+  long per_wave = ((want + 31) / 32) * 32;
+  const long min_per_wave = ((static_cast<long>(limit) + kMaxChunks - 1) / kMaxChunks + 31) / 32 * 32;
+  if (per_wave < min_per_wave) per_wave = min_per_wave;
+  if (per_wave < 32) per_wave = 32;
+  const int iters = static_cast<int>(per_wave / 32);
+  a.chunks = static_cast<int>((limit + per_wave - 1) / per_wave);
   a.tasks = a.n_heads * a.chunks;
   const size_t slots = rows * static_cast<size_t>(a.n_heads) * a.chunks;
   const size_t bytes = slots * 66 * sizeof(float);
@@ -234,7 +292,7 @@ int launch_rows(Ctx *ctx, DecArgs a, int limit, const float *sinks, float *out, 
   a.part_o = static_cast<float *>(ctx->scratch);
   a.part_md = a.part_o + slots * 64;
   const unsigned blocks = static_cast<unsigned>((a.tasks + kWaves - 1) / kWaves);
-  hipLaunchKernelGGL((decode_partial_kernel<M, KPL>), dim3(blocks), dim3(64 * kWaves), 0, ctx->stream, a);
+  hipLaunchKernelGGL((decode_partial_kernel<M>), dim3(blocks), dim3(64 * kWaves), 0, ctx->stream, a, iters);
   FOCR_HIP_CHECK(hipGetLastError());
   CombineArgs c;
   c.part_o = a.part_o;

@@ -123,6 +123,12 @@ int focr_ctx_create(int device, focr_ctx **out) {
     return set_error(FOCR_E_HIP, std::string("hipStreamCreate: ") + hipGetErrorString(err));
   }
   ctx->stream = ctx->own;
+  err = hipMalloc(&ctx->rms_dev, 8 * sizeof(float));
+  if (err != hipSuccess) {
+    (void)hipStreamDestroy(ctx->own);
+    delete ctx;
+    return set_error(FOCR_E_HIP, std::string("hipMalloc: ") + hipGetErrorString(err));
+  }
   *out = reinterpret_cast<focr_ctx *>(ctx);
   return FOCR_OK;
 }
@@ -134,6 +140,7 @@ int focr_ctx_destroy(focr_ctx *handle) {
   FOCR_HIP_CHECK(hipStreamSynchronize(ctx->stream));
   if (ctx->scratch) FOCR_HIP_CHECK(hipFree(ctx->scratch));
   if (ctx->argmax_dev) FOCR_HIP_CHECK(hipFree(ctx->argmax_dev));
+  if (ctx->rms_dev) FOCR_HIP_CHECK(hipFree(ctx->rms_dev));
   FOCR_HIP_CHECK(hipStreamDestroy(ctx->own));
   delete ctx;
   return FOCR_OK;
@@ -382,7 +389,7 @@ int focr_linear_decode_glu(focr_ctx *handle, const focr_linear *lh, const float 
 }
 
 int focr_linear_decode_ex(focr_ctx *handle, const focr_linear *lh, const float *x, size_t rows,
-                          const float *row_scale, int epilogue, float *out) {
+                          const float *row_scale, int rms_norm, int epilogue, float *out) {
   Ctx *ctx = reinterpret_cast<Ctx *>(handle);
   const Linear *lin = reinterpret_cast<const Linear *>(lh);
   FOCR_REQUIRE(ctx && lin, FOCR_E_ARG, "focr_linear_decode_ex: null argument");
@@ -390,9 +397,12 @@ int focr_linear_decode_ex(focr_ctx *handle, const focr_linear *lh, const float *
                "focr_linear_decode_ex: unknown epilogue");
   FOCR_REQUIRE(epilogue != FOCR_EPI_GLU || lin->n % 2 == 0, FOCR_E_SHAPE, "GLU needs interleaved gate/up rows");
   FOCR_REQUIRE(rows <= 8, FOCR_E_SHAPE, "focr_linear_decode_ex: 1..=8 rows (decode and draft verification)");
+  FOCR_REQUIRE(rms_norm == 0 || rms_norm == 1, FOCR_E_ARG, "focr_linear_decode_ex: rms_norm is 0 or 1");
+  FOCR_REQUIRE(!(rms_norm && row_scale), FOCR_E_ARG, "focr_linear_decode_ex: rms_norm and row_scale are exclusive");
   if (rows == 0) return FOCR_OK;
   FOCR_REQUIRE(x && out, FOCR_E_ARG, "focr_linear_decode_ex: null buffer");
-  return launch_gemv(ctx, lin, x, rows, row_scale, epilogue, out);
+  FOCR_HIP_CHECK(hipSetDevice(ctx->device));
+  return launch_gemv(ctx, lin, x, rows, row_scale, epilogue, out, rms_norm != 0);
 }
 
 int focr_linear_prefill(focr_ctx *handle, const focr_linear *lh, const float *x, size_t rows,

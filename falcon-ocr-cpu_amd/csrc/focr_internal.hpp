@@ -41,6 +41,7 @@ struct Ctx {
   size_t scratch_bytes = 0;
   uint32_t *argmax_dev = nullptr;  // [2 * rows] result words for focr_argmax
   size_t argmax_rows = 0;
+  float *rms_dev = nullptr;  // [8] row scales of a decode GEMV whose width has no in-kernel rms_norm
 };
 
 // Grows the context scratch to at least `bytes` (hipMalloc on growth only).
@@ -75,8 +76,11 @@ struct Linear {
 };
 
 // ---- launchers (each validates its launch shape on the host) -------------
+// Row-scale argument of the GEMV launchers that asks for the in-kernel
+// rms_norm instead of a precomputed factor.
+inline const float *const kRmsInKernel = reinterpret_cast<const float *>(uintptr_t(1));
 int launch_gemv(Ctx *ctx, const Linear *lin, const float *x, size_t rows, const float *row_scale, int epilogue,
-                float *out);
+                float *out, bool rms_norm = false);
 int launch_dequantize(Ctx *ctx, const Linear *lin, float *out);
 int launch_row_scales(Ctx *ctx, const float *h, size_t rows, size_t width, float eps, float *out);
 int launch_prefill_f32(Ctx *ctx, const Linear *lin, const float *x, size_t rows,

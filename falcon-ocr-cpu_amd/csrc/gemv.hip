@@ -13,7 +13,7 @@ static size_t rows_per_launch(const Linear *lin) {
 }
 
 int launch_gemv(Ctx *ctx, const Linear *lin, const float *x, size_t rows, const float *row_scale, int epilogue,
-                float *out) {
+                float *out, bool rms_norm) {
   FOCR_HIP_CHECK(hipSetDevice(ctx->device));
   const size_t chunk = rows_per_launch(lin);
   FOCR_REQUIRE(chunk >= 1, FOCR_E_SHAPE, "GEMV: in_dim too large for one row of x in LDS");
@@ -24,6 +24,14 @@ int launch_gemv(Ctx *ctx, const Linear *lin, const float *x, size_t rows, const 
     const size_t m = rows - r0 < chunk ? rows - r0 : chunk;
     const float *xr = x + r0 * lin->k;
     const float *rs = row_scale ? row_scale + r0 : nullptr;
+    if (rms_norm && lin->k == static_cast<size_t>(gemv::kRmsWidth)) {
+      rs = kRmsInKernel;
+    } else if (rms_norm) {
+      // Other widths: the row scales first, into the context's small buffer.
+      int rc = launch_row_scales(ctx, xr, m, lin->k, 1.1920929e-7f, ctx->rms_dev);
+      if (rc != FOCR_OK) return rc;
+      rs = ctx->rms_dev;
+    }
     float *orow = out + r0 * width;
     int rc;
     if (lin->bits == 8)

@@ -29,6 +29,7 @@
 #pragma once
 
 #include "focr_internal.hpp"
+#include "rms_tree.hpp"
 
 namespace focr {
 namespace gemv {
@@ -113,8 +114,11 @@ __host__ __device__ inline int x_pitch(int steps, int S) { return 32 * S * steps
 // T: code type; M: rows; SPS: scales per lane-channel per step (0 for FP32
 // weights); W: steps held in registers; ROLL: steps > W, so the window is
 // refilled as it is consumed (a separate instantiation, so that code common
-// to both paths cannot be hoisted above the first step's wait).
-template <typename T, int M, int SPS, int W, bool ROLL>
+// to both paths cannot be hoisted above the first step's wait). RMS: the row
+// width whose rms_norm (unit weight, eps f32::EPSILON) each wave computes
+// from the staged x while its weights are still arriving, then applies as
+// fl(x * scale) on every read (0: none).
+template <typename T, int M, int SPS, int W, bool ROLL, int RMS = 0>
 __global__ __launch_bounds__(256) void kernel(Args a) {
   constexpr int B = sizeof(T);
   constexpr int S = 16 / (2 * B);  // 32-blocks per step
@@ -222,6 +226,14 @@ __global__ __launch_bounds__(256) void kernel(Args a) {
   }
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   if (!active) return;
+  float rsc[M];
+#pragma unroll
+  for (int r = 0; r < M; r++) {
+    if constexpr (RMS > 0)
+      rsc[r] = rms_scale_wave<RMS>([&](int i) { return xs[r * pitch + i]; }, 1.1920929e-7f);
+    else
+      rsc[r] = 1.0f;
+  }
   const float *my_scales = ss + (wave * steps * 2 + h) * NS;  // + t * 2 * NS for step t
 
   float acc[2][M];
@@ -240,7 +252,10 @@ __global__ __launch_bounds__(256) void kernel(Args a) {
     for (int s = 0; s < S; s++) {
       float xr[M];
 #pragma unroll
-      for (int r = 0; r < M; r++) xr[r] = xs[r * pitch + 32 * (t * S + s) + p];
+      for (int r = 0; r < M; r++) {
+        xr[r] = xs[r * pitch + 32 * (t * S + s) + p];
+        if constexpr (RMS > 0) xr[r] = xr[r] * rsc[r];
+      }
 #pragma unroll
       for (int c = 0; c < 2; c++) {
         float w = to_f32(vals[s][c]);
@@ -269,6 +284,7 @@ __global__ __launch_bounds__(256) void kernel(Args a) {
   const int ch0 = tile * kGemvChannels + h * 2;
   auto x_col = [&](int r, int i) {
     const float v = a.x[static_cast<size_t>(r) * k + i];
+    if constexpr (RMS > 0) return v * rsc[r];
     return a.row_scale ? v * a.row_scale[r] : v;
   };
 #pragma unroll
@@ -353,7 +369,7 @@ inline size_t x_row_bytes(const Linear *lin) {
 inline size_t scale_lds_bytes(const Linear *lin) { return kWaves * lin->gemv_steps * 2 * 2 * lin->gemv_sps * sizeof(float); }
 constexpr size_t kLdsBudget = 64 * 1024;
 
-template <typename T, int M, int SPS, int W, bool ROLL = false>
+template <typename T, int M, int SPS, int W, bool ROLL = false, int RMS = 0>
 int launch_typed(Ctx *ctx, const Linear *lin, const float *x, const float *rs, float *out, int epi) {
   const size_t lds = M * x_row_bytes(lin) + scale_lds_bytes(lin);
   FOCR_REQUIRE(lds <= kLdsBudget, FOCR_E_SHAPE, "GEMV: x rows exceed the LDS budget");
@@ -378,16 +394,26 @@ int launch_typed(Ctx *ctx, const Linear *lin, const float *x, const float *rs, f
   a.glu = epi == FOCR_EPI_GLU ? 1 : 0;
   a.add = epi == FOCR_EPI_ADD ? 1 : 0;
   a.out = out;
-  hipLaunchKernelGGL((kernel<T, M, SPS, W, ROLL>), dim3(blocks), dim3(64 * kWaves), lds, ctx->stream, a);
+  hipLaunchKernelGGL((kernel<T, M, SPS, W, ROLL, RMS>), dim3(blocks), dim3(64 * kWaves), lds, ctx->stream, a);
   FOCR_HIP_CHECK(hipGetLastError());
   return FOCR_OK;
 }
 
+// The in-kernel rms_norm is instantiated for the model's hidden width.
+constexpr int kRmsWidth = 768;
+
 // Window buckets: every step in registers up to 20 steps (FP32: 36), which
 // covers every matrix of the model; longer rows refill a 20 (36) step window.
+// rs == kRmsInKernel selects the in-kernel rms_norm (in_dim == kRmsWidth).
 template <typename T, int M, int SPS>
 int launch_window(Ctx *ctx, const Linear *lin, const float *x, const float *rs, float *out, int epi) {
   const size_t steps = lin->gemv_steps;
+  if (rs == kRmsInKernel) {
+    constexpr int B = sizeof(T), S = 16 / (2 * B);
+    constexpr int RW = (kRmsWidth / 32 + S - 1) / S;  // steps of a kRmsWidth row
+    constexpr int WB = RW <= 4 ? 4 : RW <= 8 ? 8 : RW <= 12 ? 12 : 20;
+    return launch_typed<T, M, SPS, WB, false, kRmsWidth>(ctx, lin, x, nullptr, out, epi);
+  }
   if (steps <= 4) return launch_typed<T, M, SPS, 4>(ctx, lin, x, rs, out, epi);
   if (steps <= 8) return launch_typed<T, M, SPS, 8>(ctx, lin, x, rs, out, epi);
   if (steps <= 12) return launch_typed<T, M, SPS, 12>(ctx, lin, x, rs, out, epi);

@@ -1,6 +1,7 @@
 // Element-wise and per-row kernels of the hot path: weight dequantization
 // (A1), RMS row scales (A6) and greedy argmax (A9). All HBM-bound.
 #include "focr_internal.hpp"
+#include "rms_tree.hpp"
 
 namespace focr {
 namespace {
@@ -109,6 +110,18 @@ __global__ __launch_bounds__(64) void row_scales_kernel(const float *__restrict_
   out[blockIdx.x] = __fdiv_rn(1.0f, __builtin_sqrtf(__fdiv_rn(ret, static_cast<float>(width)) + eps));
 }
 
+// rms_scale for the model's widths: one wave per row, leaves in parallel and
+// the reference's addition order unrolled at compile time (rms_tree.hpp).
+template <int LEN>
+__global__ __launch_bounds__(256) void row_scales_fixed_kernel(const float *__restrict__ h, int rows, float eps,
+                                                               float *__restrict__ out) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const float *x = h + static_cast<size_t>(row) * LEN;
+  const float scale = rms_scale_wave<LEN>([&](int i) { return x[i]; }, eps);
+  if ((threadIdx.x & 63) == 0) out[row] = scale;
+}
+
 // argmax (src/runner/mod.rs:916-930): first index of the maximum, and a flag
 // when any value is non-finite. One workgroup per row.
 __global__ __launch_bounds__(256) void argmax_kernel(const float *__restrict__ logits, int vocab,
@@ -178,8 +191,19 @@ int launch_row_scales(Ctx *ctx, const float *h, size_t rows, size_t width, float
   FOCR_REQUIRE(width <= 16384, FOCR_E_SHAPE, "focr_row_scales: width above 16384");
   FOCR_REQUIRE(rows < (size_t(1) << 31), FOCR_E_SHAPE, "focr_row_scales: too many rows");
   FOCR_HIP_CHECK(hipSetDevice(ctx->device));
-  hipLaunchKernelGGL(row_scales_kernel, dim3(static_cast<unsigned>(rows)), dim3(64), 0, ctx->stream, h,
-                     static_cast<int>(width), eps, out);
+  const dim3 grid(static_cast<unsigned>((rows + 3) / 4)), block(256);
+  const int r = static_cast<int>(rows);
+  switch (width) {
+    case 64: hipLaunchKernelGGL(row_scales_fixed_kernel<64>, grid, block, 0, ctx->stream, h, r, eps, out); break;
+    case 768: hipLaunchKernelGGL(row_scales_fixed_kernel<768>, grid, block, 0, ctx->stream, h, r, eps, out); break;
+    case 1024: hipLaunchKernelGGL(row_scales_fixed_kernel<1024>, grid, block, 0, ctx->stream, h, r, eps, out); break;
+    case 2304: hipLaunchKernelGGL(row_scales_fixed_kernel<2304>, grid, block, 0, ctx->stream, h, r, eps, out); break;
+    case 4096: hipLaunchKernelGGL(row_scales_fixed_kernel<4096>, grid, block, 0, ctx->stream, h, r, eps, out); break;
+    default:
+      // Any other width: lane 0 walks the tree.
+      hipLaunchKernelGGL(row_scales_kernel, dim3(static_cast<unsigned>(rows)), dim3(64), 0, ctx->stream, h,
+                         static_cast<int>(width), eps, out);
+  }
   FOCR_HIP_CHECK(hipGetLastError());
   return FOCR_OK;
 }

@@ -68,7 +68,7 @@ SIGNATURES = {
     "focr_linear_dequantize": (_I, [_P, _P, _P]),
     "focr_linear_decode": (_I, [_P, _P, _P, _Z, _P]),
     "focr_linear_decode_glu": (_I, [_P, _P, _P, _Z, _P]),
-    "focr_linear_decode_ex": (_I, [_P, _P, _P, _Z, _P, _I, _P]),
+    "focr_linear_decode_ex": (_I, [_P, _P, _P, _Z, _P, _I, _I, _P]),
     "focr_linear_prefill": (_I, [_P, _P, _P, _Z, _P, _I, _I, _P]),
     "focr_row_scales": (_I, [_P, _P, _Z, _Z, _F, _P]),
     "focr_attention_prefill": (_I, [_P, _P, _P, _P, _P, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _P, _I, _I, _P]),
@@ -268,10 +268,12 @@ class Linear:
         _check(lib().focr_linear_decode_glu(self.ctx.handle, self.handle, _dev(input), rows, _dev(gated)))
         return gated
 
-    def linear_ex(self, input, rows: int, row_scale=None, epilogue: Epilogue = Epilogue.STORE, out=None):
+    def linear_ex(self, input, rows: int, row_scale=None, epilogue: Epilogue = Epilogue.STORE, out=None,
+                  rms_norm: bool = False):
         """The decode step's projection with its neighbours folded in
         (Model::project_qkv / attention_out_ffn, model/mod.rs:421-492):
-        input rows times `row_scale` (rms_norm), then `linear` (STORE),
+        input rows rms-normalized (`rms_norm=True`, computed in the kernel)
+        or times a precomputed `row_scale`, then `linear` (STORE),
         `linear_glu` (GLU) or `linear` + `add_residual` into `out` (ADD)."""
         torch = _torch()
         if input.numel() != rows * self.in_dim:
@@ -284,7 +286,7 @@ class Linear:
         elif out.numel() != rows * width:
             raise FocrError(-2, "W8 output shape")
         _check(lib().focr_linear_decode_ex(self.ctx.handle, self.handle, _dev(input), rows, _dev(row_scale),
-                                           int(epilogue), _dev(out)))
+                                           int(bool(rms_norm)), int(epilogue), _dev(out)))
         return out
 
     def prefill(self, input, rows: int, row_scale=None, epilogue: Epilogue = Epilogue.STORE, out=None,

@@ -16,7 +16,7 @@ prefill (rows > 8, a quantized body on the panel path, mod.rs:568,956-1007)::
 decode / draft verification (1..=8 rows, project_qkv + attention_out_ffn,
 mod.rs:421-492)::
 
-    rms_norm(h) . qkv -> qkv                focr_linear_decode_ex with the row scale
+    rms_norm(h) . qkv -> qkv                focr_linear_decode_ex, rms_norm in the GEMV
     qkv_rows -> q, generated keys, values   split_norm_rope + LayerCache::append
     attention over prefix + generated keys  (decode kernel)
     wo(attn); add_residual                  Epilogue ADD
@@ -28,6 +28,9 @@ KV head) lives in device memory sized for `capacity` positions, as
 ``Session::new`` sizes the reference's (model/cache.rs:364). RoPE factors
 come from the caller ([rows][n_heads][32][2] cos/sin pairs), as
 ``rotary_factors`` provides them to the reference's row kernels.
+
+`clock`, if given, is called with a stage name after each stage is
+enqueued, as the reference's PhaseClock marks phases (model/profile.rs:40-60).
 """
 from __future__ import annotations
 
@@ -84,7 +87,7 @@ class DecoderLayer:
         return CompactKv(self.prefix_k[:p], gen, self.v[:total], p, total, self.n_heads, self.n_kv_heads,
                          self.head_dim)
 
-    def prefill(self, h, rope, image_start: int, image_end: int):
+    def prefill(self, h, rope, image_start: int, image_end: int, clock=None):
         """The whole prompt (offset 0): updates `h` [rows][dim] in place and
         fills the prefix cache."""
         rows = h.shape[0]
@@ -94,25 +97,32 @@ class DecoderLayer:
             raise FocrError(-2, "KV context exhausted")
         if not (image_start <= image_end <= rows):
             raise FocrError(-2, "attention image must be inside the prefix")
-        ctx, qdim = self.ctx, self.n_heads * self.head_dim
+        ctx = self.ctx
+        mark = clock or (lambda stage: None)
         rs = row_scales(h, self.dim, out=self._buf("rs", (rows,)), ctx=ctx)
         qkv = self.qkv.prefill(h, rows, row_scale=rs, epilogue=Epilogue.STORE, kernel=self.projection,
                                out=self._buf("qkv", (rows, self.qkv.out_dim)))
+        mark("qkv")
         self.prefix_len = rows
         q = qkv_rows(qkv, rows, rope, self.n_heads, self.n_kv_heads, rows, q=self._buf("q", (rows, self.n_heads, 64)),
                      prefix_k=self.prefix_k[:rows], v=self.v[:rows], ctx=ctx)
+        mark("qkv_rows")
         self.image = (image_start, image_end)
         attn = attention_with(q, self.kv(rows), rows, Geometry(0, image_start, image_end), self.sinks, self.options,
                               output=self._buf("attn", (rows, self.n_heads, 64)), ctx=ctx)
+        mark("attention")
         self.wo.prefill(attn, rows, epilogue=Epilogue.ADD, out=h, kernel=self.projection)
+        mark("wo")
         rs = row_scales(h, self.dim, out=rs, ctx=ctx)
         gated = self.w13.prefill(h, rows, row_scale=rs, epilogue=Epilogue.GLU, kernel=self.projection,
                                  out=self._buf("gated", (rows, self.w13.out_dim // 2)))
+        mark("w13")
         self.w2.prefill(gated, rows, epilogue=Epilogue.ADD, out=h, kernel=self.projection)
+        mark("w2")
         self.len = rows
         return h
 
-    def decode(self, h, rope):
+    def decode(self, h, rope, clock=None):
         """1..=8 rows at positions len.. (a greedy step, or the last token plus
         drafts): updates `h` [rows][dim] in place and appends to the cache."""
         rows = h.shape[0]
@@ -121,17 +131,22 @@ class DecoderLayer:
         if self.len + rows > self.capacity:
             raise FocrError(-2, "KV context exhausted")
         ctx, p, pos = self.ctx, self.prefix_len, self.len
-        rs = row_scales(h, self.dim, out=self._buf("drs", (rows,)), ctx=ctx)
-        qkv = self.qkv.linear_ex(h, rows, row_scale=rs, out=self._buf("dqkv", (rows, self.qkv.out_dim)))
+        mark = clock or (lambda stage: None)
+        qkv = self.qkv.linear_ex(h, rows, rms_norm=True, out=self._buf("dqkv", (rows, self.qkv.out_dim)))
+        mark("qkv")
         q = qkv_rows(qkv, rows, rope, self.n_heads, self.n_kv_heads, 0, q=self._buf("dq", (rows, self.n_heads, 64)),
                      generated_k=self.generated_k[pos - p: pos - p + rows], v=self.v[pos: pos + rows], ctx=ctx)
+        mark("qkv_rows")
         total = pos + rows
         attn = attention_with(q, self.kv(total), rows, Geometry(pos, *self.image), self.sinks, self.options,
                               output=self._buf("dattn", (rows, self.n_heads, 64)), ctx=ctx)
+        mark("attention")
         self.wo.linear_ex(attn, rows, epilogue=Epilogue.ADD, out=h)
-        rs = row_scales(h, self.dim, out=rs, ctx=ctx)
-        gated = self.w13.linear_ex(h, rows, row_scale=rs, epilogue=Epilogue.GLU,
+        mark("wo")
+        gated = self.w13.linear_ex(h, rows, rms_norm=True, epilogue=Epilogue.GLU,
                                    out=self._buf("dgated", (rows, self.w13.out_dim // 2)))
+        mark("w13")
         self.w2.linear_ex(gated, rows, epilogue=Epilogue.ADD, out=h)
+        mark("w2")
         self.len = total
         return h

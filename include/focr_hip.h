@@ -123,14 +123,18 @@ int focr_linear_decode_glu(focr_ctx *ctx, const focr_linear *lin, const float *x
 
 /* The decode step's projections with their neighbours folded in, as
  * Model::project_qkv / attention_out_ffn call them for 1..=8 rows
- * (src/model/mod.rs:421-492): row_scale_dev optional [rows] multiplies each
- * input row first (rms_norm_row's `x * scale`, src/kernels/mod.rs:497-514,
- * the factor from focr_row_scales); epilogue FOCR_EPI_STORE (linear),
- * FOCR_EPI_GLU (linear_glu, out [rows][out/2]) or FOCR_EPI_ADD
- * (add_residual, src/model/rope.rs:155-169: out += projection). Bitwise equal
- * to the separate reference passes. */
+ * (src/model/mod.rs:421-492):
+ *   rms_norm 1: each input row is first rms-normalized (kernels::rms_norm,
+ *     unit weight, eps f32::EPSILON, src/kernels/mod.rs:481-533), computed
+ *     inside the GEMV; row_scale_dev must then be NULL;
+ *   row_scale_dev optional [rows]: a precomputed factor (focr_row_scales)
+ *     multiplied into each row instead (rms_norm_row's `x * scale`);
+ *   epilogue FOCR_EPI_STORE (linear), FOCR_EPI_GLU (linear_glu, out
+ *     [rows][out/2]) or FOCR_EPI_ADD (add_residual, src/model/rope.rs:155-169:
+ *     out += projection).
+ * Bitwise equal to the separate reference passes. */
 int focr_linear_decode_ex(focr_ctx *ctx, const focr_linear *lin, const float *x_dev, size_t rows,
-                          const float *row_scale_dev, int epilogue, float *out_dev);
+                          const float *row_scale_dev, int rms_norm, int epilogue, float *out_dev);
 
 /* ---- A2 / A3: prefill projection ---------------------------------------- */
 /* QuantLinear::prefill (src/quant/linear.rs:634-707) and its FP32 panel

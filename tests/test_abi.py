@@ -45,7 +45,7 @@ def test_null_arguments_are_errors_not_crashes():
     assert lib.focr_linear_decode(None, None, None, 1, None) == -1
     assert lib.focr_linear_prefill(None, None, None, 1, None, 0, 0, None) == -1
     assert lib.focr_attention_prefill(None, *([None] * 4), *([0] * 9), None, 0, 0, None) == -1
-    assert lib.focr_linear_decode_ex(None, None, None, 1, None, 0, None) == -1
+    assert lib.focr_linear_decode_ex(None, None, None, 1, None, 0, 0, None) == -1
     assert lib.focr_qkv_rows(None, None, 1, None, 16, 8, 64, 0, None, None, None, None) == -1
     assert lib.focr_attention_decode(None, *([None] * 4), *([0] * 9), None, None) == -1
     assert lib.focr_ctx_destroy(None) == 0

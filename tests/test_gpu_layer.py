@@ -81,6 +81,30 @@ def test_decode_ex_folds_row_scale_and_residual(fh, bits, rows):
     lin.free()
 
 
+@pytest.mark.parametrize("bits", [8, 16, 32])
+@pytest.mark.parametrize("rows", [1, 2, 5, 8])
+@pytest.mark.parametrize("k", [768, 1024])
+def test_decode_ex_rms_norm_in_kernel(fh, bits, rows, k):
+    # rms_norm(h) then linear / linear_glu (model/mod.rs:421-492): in the GEMV
+    # for the model width 768, through focr_row_scales for other widths.
+    n = 256
+    if bits == 32:
+        codes, scales = gen.normal((n, k), 0.02, 15), None
+    else:
+        lo, hi = (-127, 127) if bits == 8 else (-32767, 32767)
+        codes = gen.codes_uniform((n, k), lo, hi, np.int8 if bits == 8 else np.int16, 15)
+        scales = gen.uniform((n, k // 64), 1e-4, 4e-4, 16)
+    lin = fh.Linear(bits, codes, scales, 64)
+    h = gen.normal((rows, k), 3.0, 17)
+    h[0, :64] = 0.0
+    normalized = h * oracle.row_scales(h, k)[:, None]
+    got = host(lin.linear_ex(to_dev(h), rows, rms_norm=True))
+    assert_bitwise(got, oracle.linear_decode(bits, codes, scales, n, k, 64, normalized, rows), "rms store")
+    got = host(lin.linear_ex(to_dev(h), rows, rms_norm=True, epilogue=fh.Epilogue.GLU))
+    assert_bitwise(got, oracle.linear_decode_glu(bits, codes, scales, n, k, 64, normalized, rows), "rms glu")
+    lin.free()
+
+
 def close(got, want, tol=1e-5):
     assert np.all(np.isfinite(got))
     assert np.all(np.abs(got - want) <= tol * (1.0 + np.abs(want))), float(np.max(np.abs(got - want)))

@@ -18,7 +18,7 @@ def fh():
     return focr_hip
 
 
-@pytest.mark.parametrize("width", [768, 1024, 2304, 64, 96, 33, 1, 5000])
+@pytest.mark.parametrize("width", [768, 1024, 2304, 4096, 64, 96, 33, 1, 5000])
 def test_row_scales_bitwise(fh, width):
     rows = 37
     h = gen.values(rows * width, 9) * F32(3.0)

@@ -78,9 +78,8 @@ def make_pool(fh, gen, np, bits, n, k, count_bytes, seed):
     return codes, scales, [fh.QuantLinear(bits, codes, scales, 64) for _ in range(copies)]
 
 
-def bench_gemv(torch, fh, gen, np, bits, rows, steps, warmup, graph=True):
+def bench_gemv(torch, fh, gen, np, bits, rows, steps, warmup, graph=True, n=4096, k=1024):
     """Decode GEMV over a rotating pool; returns whole-job and per-launch numbers."""
-    n, k = 4096, 1024
     codes, scales, pool = make_pool(fh, gen, np, bits, n, k, POOL_BYTES, 1 if bits == 16 else 4)
     x = torch.from_numpy(gen.normal((rows, k), 1.0, 3)).cuda()
     out = torch.empty((rows, n), device="cuda")
@@ -376,6 +375,16 @@ def main():
             per_op[key] = {"bytes": r["bytes"], "launch_us": round(r["avg_launch_ms"] * 1e3, 3),
                            "gbs_per_launch": round(r["bytes"] / (r["avg_launch_ms"] * 1e-3) / 1e9, 1),
                            "gbs_whole_job": round(r["bytes"] / (r["wall_s"] / r["steps"]) / 1e9, 1),
+                           "frac_hbm_per_launch": round(r["bytes"] / (r["avg_launch_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 3)}
+            log(f"{key}: {per_op[key]}")
+        # The same INT8 kernel on larger single launches: the model's W13
+        # (4608 x 768), a 16384 x 1024 matrix and the 65,536 x 768 vocabulary
+        # head (the screened head's GEMV), each from a > 512 MB pool.
+        for n, k in ((4608, 768), (16384, 1024), (65536, 768)):
+            r = bench_gemv(torch, fh, gen, np, 8, 1, 200, 10, graph=not args.no_graph, n=n, k=k)
+            key = f"gemv_i8_m1_{n}x{k}"
+            per_op[key] = {"bytes": r["bytes"], "launch_us": round(r["avg_launch_ms"] * 1e3, 3),
+                           "gbs_per_launch": round(r["bytes"] / (r["avg_launch_ms"] * 1e-3) / 1e9, 1),
                            "frac_hbm_per_launch": round(r["bytes"] / (r["avg_launch_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 3)}
             log(f"{key}: {per_op[key]}")
     if "gemm" in ops:

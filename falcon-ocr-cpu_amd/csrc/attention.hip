@@ -21,9 +21,11 @@
 // in softmax_lanes (rescale by exp(old_max - new_max), p = exp(s - new_max),
 // den = den * r + sum p), and the sink at the end:
 // out = (o / den) * 1 / (1 + exp(sink - lse)).
-// The matrix cores sum in their own order, and the online max is taken per
-// 32-key tile rather than per 128 keys, so outputs match the reference within
-// FP32 rounding, not bitwise.
+// The matrix cores sum in their own order, the online max is taken per
+// 32-key tile rather than per 128 keys, and the softmax exponentials of the
+// Fast and static modes are the hardware exp2 of log2(e) * x (a few ulp from
+// the reference's Cephes exp_poly; ExpMode::Exact uses the device libm expf),
+// so outputs match the reference within FP32 rounding, not bitwise.
 //
 // Roofline: FP32 matrix cores. FLOPs = 4 * 64 * visible (query, key) pairs
 // per head (122.07 GFLOP at 6,544 tokens, 16 heads, 4,096 image tokens).
@@ -68,24 +70,15 @@ __device__ __forceinline__ float halves_sum(float x) {
 }
 __device__ __forceinline__ float halves_max(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  const float lo = __uint_as_float(r[0]), hi = __uint_as_float(r[1]);
-  return hi > lo ? hi : lo;
+  return __builtin_fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
-// exp_poly for x <= 0 or NaN (an online-softmax exponent s - max), where its
-// x > 88.376 case cannot occur. Below -87 the polynomial runs on -87 and the
-// result is multiplied by 0 (the polynomial is finite there), so no branch
-// is formed; NaN passes through the polynomial as NaN.
-__device__ __forceinline__ float exp_poly_nonpositive(float x) {
-  const bool under = x < -87.0f;
-  return exp_poly_unchecked(under ? -87.0f : x) * (under ? 0.0f : 1.0f);
-}
+constexpr float kLog2e = 1.44269504088896340736f;
 
-// exp_poly_unchecked with masked scores (-inf) mapped to +0 the same way.
-__device__ __forceinline__ float exp_unchecked_masked(float s) {
-  const bool masked = s == -__builtin_inff();
-  return exp_poly_unchecked(masked ? 0.0f : s) * (masked ? 0.0f : 1.0f);
-}
+// The hardware exp2 (v_exp_f32, 1 ulp) of log2(e) * x: e^x within a few ulp
+// of the reference's Cephes exp_poly, i.e. far inside the FP32 attention
+// tolerance, at 3 instructions instead of about 17. x = -inf gives +0.
+__device__ __forceinline__ float exp_hw(float x) { return __builtin_amdgcn_exp2f(kLog2e * x); }
 
 // Copies the key tile starting at kstart into t: each wave moves rows
 // 4w..4w+3 and 16+4w..16+4w+3 of K and of V, lane l -> row 4w + l / 16 (+16),
@@ -145,12 +138,12 @@ __device__ __forceinline__ void tile_step(const AttnArgs &a, const KvTile &t, Wa
     }
   }
   if constexpr (STATIC) {
-    // p = exp_poly_unchecked(s), masked keys +0 (static_shift.rs:135-160).
+    // p = exp(s) (the reference's exp_poly_unchecked), masked keys +0
+    // (static_shift.rs:135-160).
     float psum = 0.0f;
 #pragma unroll
     for (int r = 0; r < 16; r++) {
-      const float s = st[r];
-      const float p = exp_unchecked_masked(s);
+      const float p = exp_hw(st[r]);  // masked keys: exp(-inf) = +0
       st[r] = p;
       psum = psum + p;
     }
@@ -159,12 +152,12 @@ __device__ __forceinline__ void tile_step(const AttnArgs &a, const KvTile &t, Wa
     // Online step (softmax_lanes, prefill64.rs:574-652) over both halves.
     float tile_max = st[0];
 #pragma unroll
-    for (int r = 1; r < 16; r++) tile_max = st[r] > tile_max ? st[r] : tile_max;
+    for (int r = 1; r < 16; r++) tile_max = __builtin_fmaxf(tile_max, st[r]);
     tile_max = halves_max(tile_max);
-    const float new_max = tile_max > w.run_max ? tile_max : w.run_max;
+    const float new_max = __builtin_fmaxf(tile_max, w.run_max);
     const bool skip = new_max == -__builtin_inff();
     const bool first = w.run_max == -__builtin_inff();
-    float rescale = FAST ? exp_poly_nonpositive(w.run_max - new_max) : expf_acc(w.run_max - new_max);
+    float rescale = FAST ? exp_hw(w.run_max - new_max) : expf_acc(w.run_max - new_max);
     rescale = first ? 0.0f : rescale;
     rescale = skip ? 1.0f : rescale;
     // A skipped tile (every key hidden) has s = -inf everywhere: subtracting
@@ -174,7 +167,7 @@ __device__ __forceinline__ void tile_step(const AttnArgs &a, const KvTile &t, Wa
 #pragma unroll
     for (int r = 0; r < 16; r++) {
       const float x = st[r] - shift;
-      const float p = FAST ? exp_poly_nonpositive(x) : expf_acc(x);
+      const float p = FAST ? exp_hw(x) : expf_acc(x);
       st[r] = p;
       psum = psum + p;
     }

@@ -44,9 +44,34 @@ constexpr int kKeys = 32;      // per LDS key tile
 struct AttnArgs {
   const float *q, *prefix_k, *generated_k, *v, *sinks;
   float *out;
+  float *part;  // partial states of split tiles: [slot][head][128 rows][64] o, then [slot][head][128][2] (max, den)
   int query_len, prefix_len, total_len, n_heads, n_kv_heads;
   int query_offset, image_start, image_end;
+  int tiles, chunk_keys, slots;
 };
+
+// Work plan (computed on the host, passed by value): query tiles in dispatch
+// order i (tile tiles - 1 - i: the latest, longest tiles first), each split
+// into ceil(visible keys / chunk_keys) work items of equal size (rounded up
+// to whole 32-key tiles).
+constexpr int kMaxTiles = 256;
+constexpr long long kSplitItems = 3072;  // target work items per call (about 4 per slot)
+constexpr long long kMinChunkKeys = 1024;
+struct SplitPlan {
+  int first[kMaxTiles + 1];  // first work item of the i-th tile; first[tiles] = items
+  int slot[kMaxTiles];       // first partial slot of the i-th tile if it is split
+  int keys[kMaxTiles];       // keys per work item of the i-th tile (a multiple of 32)
+};
+
+// Keys [0, end) that query tile `tile` sees (tile_span, prefill64/span.rs:9-20).
+__host__ __device__ inline int tile_visible_end(int tile, int query_len, int query_offset, int image_start,
+                                                int image_end) {
+  const int first_query = tile * kQueries;
+  const int queries = query_len - first_query < kQueries ? query_len - first_query : kQueries;
+  const int first_abs = query_offset + first_query, last_abs = first_abs + queries - 1;
+  const bool intersects = first_abs < image_end && last_abs >= image_start;
+  return intersects ? (last_abs + 1 > image_end ? last_abs + 1 : image_end) : last_abs + 1;
+}
 
 // One buffered key tile: [0] = K, [1] = V; 32 rows of 16 swizzled float4.
 struct KvTile {
@@ -117,11 +142,15 @@ __device__ __forceinline__ void tile_step(const AttnArgs &a, const KvTile &t, Wa
 #pragma unroll
   for (int r = 0; r < 16; r++) st[r] = 0.0f;
   // Each K chunk is read one chunk ahead of the four products that use it.
-  float4 next = t.rows[0][l32][chunk(8 * h, l32)];
+  // All eight K chunks are read before the first product (the compiler
+  // would otherwise wait for each chunk right before its four products).
+  float4 kall[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) kall[i] = t.rows[0][l32][chunk(8 * h + i, l32)];
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int i = 0; i < 8; i++) {
-    const float4 kf = next;
-    if (i < 7) next = t.rows[0][l32][chunk(8 * h + i + 1, l32)];
+    const float4 kf = kall[i];
     st = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.x, w.qv[4 * i], st, 0, 0, 0);
     st = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.y, w.qv[4 * i + 1], st, 0, 0, 0);
     st = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.z, w.qv[4 * i + 2], st, 0, 0, 0);
@@ -208,7 +237,8 @@ __device__ __forceinline__ void tile_step(const AttnArgs &a, const KvTile &t, Wa
 }
 
 template <bool STATIC, bool FAST>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void attention_kernel(AttnArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void attention_kernel(AttnArgs a,
+                                                                                                SplitPlan plan) {
   __shared__ KvTile tile0;
   __shared__ KvTile tile1;
   const int head = blockIdx.y;
@@ -216,9 +246,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void a
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int h = lane >> 5, l32 = lane & 31;
-  // Query tiles are dispatched last-first: later (text) tiles see the most
-  // keys, so the longest workgroups start first.
-  const int first_query = (gridDim.x - 1 - blockIdx.x) * kQueries;
+  // This workgroup's work item: tile `order` of the plan, key chunk `part`.
+  const int item = blockIdx.x;
+  int lo = 0, hi = a.tiles - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (plan.first[mid] <= item) lo = mid; else hi = mid - 1;
+  }
+  const int order = lo;
+  const int part = item - plan.first[order];
+  const int parts = plan.first[order + 1] - plan.first[order];
+  const int first_query = (a.tiles - 1 - order) * kQueries;
   const int wq0 = first_query + wave * 32;  // this wave's first query row
   const int my_query = wq0 + l32;
   const int my_abs = a.query_offset + my_query;
@@ -230,7 +268,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void a
   const int first_abs = a.query_offset + first_query;
   const int last_abs = first_abs + wg_queries - 1;
   const bool intersects = first_abs < a.image_end && last_abs >= a.image_start;
-  const int visible_end = intersects ? (last_abs + 1 > a.image_end ? last_abs + 1 : a.image_end) : last_abs + 1;
+  const int tile_end = intersects ? (last_abs + 1 > a.image_end ? last_abs + 1 : a.image_end) : last_abs + 1;
+  // This item's keys: [key_begin, visible_end), a multiple of 32 from 0.
+  const int key_begin = part * plan.keys[order];
+  const int visible_end = key_begin + plan.keys[order] < tile_end ? key_begin + plan.keys[order] : tile_end;
   // This wave's own span: tiles past it are skipped, tiles before w_first
   // (and image tiles of an all-image wave) need no mask.
   const int w_queries = a.query_len - wq0 < 32 ? a.query_len - wq0 : 32;
@@ -280,15 +321,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void a
       tile_step<STATIC, FAST>(a, cur, w, kstart, keys, !full, h, l32, my_abs, my_image);
     }
   };
-  copy_tile(a, tile0, 0, visible_end, head, kv_head, wave, lane);
-  for (int kstart = 0; kstart < visible_end; kstart += 2 * kKeys) {
+  copy_tile(a, tile0, key_begin, visible_end, head, kv_head, wave, lane);
+  for (int kstart = key_begin; kstart < visible_end; kstart += 2 * kKeys) {
     step(tile0, tile1, kstart);
     if (kstart + kKeys < visible_end) step(tile1, tile0, kstart + kKeys);
   }
 
-  // Normalize and apply the sink (prefill64.rs:468-479).
+  // Normalize and apply the sink (prefill64.rs:468-479); a split tile
+  // stores its unnormalized state for attention_merge_kernel instead.
   const float lse = STATIC ? logf_acc(w.den) : w.run_max + logf_acc(w.den);
   const float sink_scale = __fdiv_rn(1.0f, 1.0f + expf_acc(a.sinks[head] - lse));
+  const bool split = parts > 1;
   __syncthreads();
   // Transpose through LDS (8 KB per wave, swizzled like the key tiles):
   // o[d][r] is output dim 32 d + 8(r/4) + 4h + r%4 of query l32.
@@ -299,16 +342,134 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void a
     for (int r = 0; r < 16; r++) {
       const int dim = d * 32 + 8 * (r / 4) + 4 * h + (r % 4);
       reinterpret_cast<float *>(&stage[l32][chunk(dim >> 2, l32)])[dim & 3] =
-          __fmul_rn(__fdiv_rn(w.o[d][r], w.den), sink_scale);
+          split ? w.o[d][r] : __fmul_rn(__fdiv_rn(w.o[d][r], w.den), sink_scale);
     }
   __syncthreads();
+  if (!split) {
+    for (int idx = lane; idx < 32 * 16; idx += 64) {
+      const int r = idx >> 4, c4 = idx & 15;
+      const int row = wq0 + r;
+      if (row < a.query_len)
+        reinterpret_cast<float4 *>(a.out + (static_cast<size_t>(row) * a.n_heads + head) * 64)[c4] =
+            stage[r][chunk(c4, r)];
+    }
+    return;
+  }
+  const size_t slot = static_cast<size_t>(plan.slot[order] + part) * a.n_heads + head;
+  float *po = a.part + slot * kQueries * 64 + wave * 32 * 64;
   for (int idx = lane; idx < 32 * 16; idx += 64) {
     const int r = idx >> 4, c4 = idx & 15;
-    const int row = wq0 + r;
-    if (row < a.query_len)
-      reinterpret_cast<float4 *>(a.out + (static_cast<size_t>(row) * a.n_heads + head) * 64)[c4] =
-          stage[r][chunk(c4, r)];
+    reinterpret_cast<float4 *>(po + r * 64)[c4] = stage[r][chunk(c4, r)];
   }
+  if (h == 0) {
+    float *pmd = a.part + static_cast<size_t>(a.slots) * a.n_heads * kQueries * 64 + slot * kQueries * 2;
+    // The static softmax has no shift: its parts merge with weight exp(0) = 1.
+    reinterpret_cast<float2 *>(pmd)[wave * 32 + l32] = make_float2(STATIC ? 0.0f : w.run_max, w.den);
+  }
+}
+
+// Merges the parts of the split tiles (one workgroup per tile and head; the
+// unsplit tiles exit): per query row, M = max of the parts' maxima,
+// den = sum den_p exp(m_p - M), o = sum o_p exp(m_p - M) in part order, then
+// the final step of prefill64.rs:468-479 with lse = M + ln(den).
+__global__ __launch_bounds__(256) void attention_merge_kernel(AttnArgs a, SplitPlan plan) {
+  const int order = blockIdx.x, head = blockIdx.y;
+  const int parts = plan.first[order + 1] - plan.first[order];
+  if (parts <= 1) return;
+  const int row_in_tile = threadIdx.x >> 1, half = threadIdx.x & 1;
+  const int row = (a.tiles - 1 - order) * kQueries + row_in_tile;
+  if (row >= a.query_len) return;
+  const float *pmd = a.part + static_cast<size_t>(a.slots) * a.n_heads * kQueries * 64;
+  const float ninf = -__builtin_inff();
+  float big = ninf;
+  for (int p = 0; p < parts; p++) {
+    const size_t slot = static_cast<size_t>(plan.slot[order] + p) * a.n_heads + head;
+    const float m = pmd[(slot * kQueries + row_in_tile) * 2];
+    big = __builtin_fmaxf(big, m);
+  }
+  float den = 0.0f;
+  float4 o[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) o[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int p = 0; p < parts; p++) {
+    const size_t slot = static_cast<size_t>(plan.slot[order] + p) * a.n_heads + head;
+    const float2 md = reinterpret_cast<const float2 *>(pmd)[slot * kQueries + row_in_tile];
+    const float f = md.x == ninf ? 0.0f : expf_acc(md.x - big);
+    den = den + md.y * f;
+    const float4 *src = reinterpret_cast<const float4 *>(a.part + (slot * kQueries + row_in_tile) * 64 + 32 * half);
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const float4 v = src[i];
+      o[i] = make_float4(fmaf_(v.x, f, o[i].x), fmaf_(v.y, f, o[i].y), fmaf_(v.z, f, o[i].z), fmaf_(v.w, f, o[i].w));
+    }
+  }
+  const float lse = big + logf_acc(den);
+  const float sink_scale = __fdiv_rn(1.0f, 1.0f + expf_acc(a.sinks[head] - lse));
+  float4 *dst = reinterpret_cast<float4 *>(a.out + (static_cast<size_t>(row) * a.n_heads + head) * 64 + 32 * half);
+#pragma unroll
+  for (int i = 0; i < 8; i++)
+    dst[i] = make_float4(__fmul_rn(__fdiv_rn(o[i].x, den), sink_scale), __fmul_rn(__fdiv_rn(o[i].y, den), sink_scale),
+                         __fmul_rn(__fdiv_rn(o[i].z, den), sink_scale), __fmul_rn(__fdiv_rn(o[i].w, den), sink_scale));
+}
+
+}  // namespace
+
+namespace {
+
+// One launch (plus the merge) for at most kMaxTiles query tiles.
+int launch_tiles(Ctx *ctx, AttnArgs a, int softmax, int exp_mode) {
+  // Split plan: query tiles whose visible keys exceed chunk_keys run as
+  // several work items of at most chunk_keys keys, so that every item costs
+  // about the same and about four rounds of items fill the chip (the
+  // causal tiles' costs differ up to fourfold at a 16K context).
+  const int tiles = (a.query_len + kQueries - 1) / kQueries;
+  SplitPlan plan;
+  long long total = 0;
+  int vis[kMaxTiles];
+  for (int t = 0; t < tiles; t++) {
+    vis[t] = tile_visible_end(t, a.query_len, a.query_offset, a.image_start, a.image_end);
+    total += vis[t];
+  }
+  const long long want = total * static_cast<long long>(a.n_heads) / kSplitItems;
+  const int chunk_keys =
+      static_cast<int>(((want > kMinChunkKeys ? want : kMinChunkKeys) + kKeys - 1) / kKeys * kKeys);
+  int items = 0, slots = 0;
+  for (int i = 0; i < tiles; i++) {
+    const int end = vis[tiles - 1 - i];
+    const int want_parts = (end + chunk_keys - 1) / chunk_keys;
+    const int per = ((end + want_parts - 1) / want_parts + kKeys - 1) / kKeys * kKeys;
+    const int parts = (end + per - 1) / per;  // every part starts before `end`
+    plan.first[i] = items;
+    plan.slot[i] = parts > 1 ? slots : -1;
+    plan.keys[i] = per;
+    items += parts;
+    slots += parts > 1 ? parts : 0;
+  }
+  plan.first[tiles] = items;
+  a.tiles = tiles;
+  a.chunk_keys = chunk_keys;
+  a.slots = slots;
+  a.part = nullptr;
+  if (slots > 0) {
+    const size_t bytes = static_cast<size_t>(slots) * a.n_heads * kQueries * 66 * sizeof(float);
+    int rc = ensure_scratch(ctx, bytes);
+    if (rc != FOCR_OK) return rc;
+    a.part = static_cast<float *>(ctx->scratch);
+  }
+  const dim3 grid(static_cast<unsigned>(items), static_cast<unsigned>(a.n_heads));
+  if (softmax == FOCR_SOFTMAX_STATIC)
+    hipLaunchKernelGGL((attention_kernel<true, true>), grid, dim3(256), 0, ctx->stream, a, plan);
+  else if (exp_mode == FOCR_EXP_FAST)
+    hipLaunchKernelGGL((attention_kernel<false, true>), grid, dim3(256), 0, ctx->stream, a, plan);
+  else
+    hipLaunchKernelGGL((attention_kernel<false, false>), grid, dim3(256), 0, ctx->stream, a, plan);
+  FOCR_HIP_CHECK(hipGetLastError());
+  if (slots > 0) {
+    hipLaunchKernelGGL(attention_merge_kernel, dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(a.n_heads)),
+                       dim3(256), 0, ctx->stream, a, plan);
+    FOCR_HIP_CHECK(hipGetLastError());
+  }
+  return FOCR_OK;
 }
 
 }  // namespace
@@ -319,28 +480,28 @@ int launch_attention(Ctx *ctx, const float *q, const float *prefix_k, const floa
                      int exp_mode, float *out) {
   FOCR_REQUIRE(total_len < (size_t(1) << 30) && n_heads < 65536, FOCR_E_SHAPE, "attention shape too large");
   AttnArgs a;
-  a.q = q;
   a.prefix_k = prefix_k;
   a.generated_k = generated_k;
   a.v = v;
   a.sinks = sinks;
-  a.out = out;
-  a.query_len = static_cast<int>(query_len);
   a.prefix_len = static_cast<int>(prefix_len);
   a.total_len = static_cast<int>(total_len);
   a.n_heads = static_cast<int>(n_heads);
   a.n_kv_heads = static_cast<int>(n_kv_heads);
-  a.query_offset = static_cast<int>(query_offset);
   a.image_start = static_cast<int>(image_start);
   a.image_end = static_cast<int>(image_end);
-  const dim3 grid(static_cast<unsigned>((query_len + kQueries - 1) / kQueries), static_cast<unsigned>(n_heads));
-  if (softmax == FOCR_SOFTMAX_STATIC)
-    hipLaunchKernelGGL((attention_kernel<true, true>), grid, dim3(256), 0, ctx->stream, a);
-  else if (exp_mode == FOCR_EXP_FAST)
-    hipLaunchKernelGGL((attention_kernel<false, true>), grid, dim3(256), 0, ctx->stream, a);
-  else
-    hipLaunchKernelGGL((attention_kernel<false, false>), grid, dim3(256), 0, ctx->stream, a);
-  FOCR_HIP_CHECK(hipGetLastError());
+  // Query rows are independent: longer calls run as several launches of at
+  // most kMaxTiles query tiles (the plan table's size).
+  const size_t per_launch = static_cast<size_t>(kMaxTiles) * kQueries;
+  for (size_t q0 = 0; q0 < query_len; q0 += per_launch) {
+    const size_t n = query_len - q0 < per_launch ? query_len - q0 : per_launch;
+    a.q = q + q0 * n_heads * 64;
+    a.out = out + q0 * n_heads * 64;
+    a.query_len = static_cast<int>(n);
+    a.query_offset = static_cast<int>(query_offset + q0);
+    const int rc = launch_tiles(ctx, a, softmax, exp_mode);
+    if (rc != FOCR_OK) return rc;
+  }
   return FOCR_OK;
 }
 

@@ -29,6 +29,7 @@
 //
 // Roofline: FP32 matrix cores. FLOPs = 4 * 64 * visible (query, key) pairs
 // per head (122.07 GFLOP at 6,544 tokens, 16 heads, 4,096 image tokens).
+#include "attention_split.hpp"
 #include "focr_internal.hpp"
 
 namespace focr {
@@ -44,34 +45,13 @@ constexpr int kKeys = 32;      // per LDS key tile
 struct AttnArgs {
   const float *q, *prefix_k, *generated_k, *v, *sinks;
   float *out;
-  float *part;  // partial states of split tiles: [slot][head][128 rows][64] o, then [slot][head][128][2] (max, den)
+  float *part;  // partial states of split tiles (attention_split.hpp)
   int query_len, prefix_len, total_len, n_heads, n_kv_heads;
   int query_offset, image_start, image_end;
-  int tiles, chunk_keys, slots;
+  int tiles, slots;
 };
-
-// Work plan (computed on the host, passed by value): query tiles in dispatch
-// order i (tile tiles - 1 - i: the latest, longest tiles first), each split
-// into ceil(visible keys / chunk_keys) work items of equal size (rounded up
-// to whole 32-key tiles).
-constexpr int kMaxTiles = 256;
-constexpr long long kSplitItems = 3072;  // target work items per call (about 4 per slot)
-constexpr long long kMinChunkKeys = 1024;
-struct SplitPlan {
-  int first[kMaxTiles + 1];  // first work item of the i-th tile; first[tiles] = items
-  int slot[kMaxTiles];       // first partial slot of the i-th tile if it is split
-  int keys[kMaxTiles];       // keys per work item of the i-th tile (a multiple of 32)
-};
-
-// Keys [0, end) that query tile `tile` sees (tile_span, prefill64/span.rs:9-20).
-__host__ __device__ inline int tile_visible_end(int tile, int query_len, int query_offset, int image_start,
-                                                int image_end) {
-  const int first_query = tile * kQueries;
-  const int queries = query_len - first_query < kQueries ? query_len - first_query : kQueries;
-  const int first_abs = query_offset + first_query, last_abs = first_abs + queries - 1;
-  const bool intersects = first_abs < image_end && last_abs >= image_start;
-  return intersects ? (last_abs + 1 > image_end ? last_abs + 1 : image_end) : last_abs + 1;
-}
+using split::kMaxTiles;
+static_assert(split::kQueries == kQueries, "one query tile per split plan entry");
 
 // One buffered key tile: [0] = K, [1] = V; 32 rows of 16 swizzled float4.
 struct KvTile {
@@ -238,7 +218,7 @@ __device__ __forceinline__ void tile_step(const AttnArgs &a, const KvTile &t, Wa
 
 template <bool STATIC, bool FAST>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void attention_kernel(AttnArgs a,
-                                                                                                SplitPlan plan) {
+                                                                                                split::Plan plan) {
   __shared__ KvTile tile0;
   __shared__ KvTile tile1;
   const int head = blockIdx.y;
@@ -246,16 +226,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void a
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int h = lane >> 5, l32 = lane & 31;
-  // This workgroup's work item: tile `order` of the plan, key chunk `part`.
-  const int item = blockIdx.x;
-  int lo = 0, hi = a.tiles - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (plan.first[mid] <= item) lo = mid; else hi = mid - 1;
-  }
-  const int order = lo;
-  const int part = item - plan.first[order];
-  const int parts = plan.first[order + 1] - plan.first[order];
+  // This workgroup's work item: part `it.part` of the tile `it.order` of the
+  // plan (heavy, late tiles first).
+  const split::Item it = split::find_item(plan, a.tiles, blockIdx.x);
+  const int order = it.order, part = it.part, parts = it.parts;
   const int first_query = (a.tiles - 1 - order) * kQueries;
   const int wq0 = first_query + wave * 32;  // this wave's first query row
   const int my_query = wq0 + l32;
@@ -270,8 +244,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void a
   const bool intersects = first_abs < a.image_end && last_abs >= a.image_start;
   const int tile_end = intersects ? (last_abs + 1 > a.image_end ? last_abs + 1 : a.image_end) : last_abs + 1;
   // This item's keys: [key_begin, visible_end), a multiple of 32 from 0.
-  const int key_begin = part * plan.keys[order];
-  const int visible_end = key_begin + plan.keys[order] < tile_end ? key_begin + plan.keys[order] : tile_end;
+  const int key_begin = it.key_begin;
+  const int visible_end = key_begin + it.keys < tile_end ? key_begin + it.keys : tile_end;
   // This wave's own span: tiles past it are skipped, tiles before w_first
   // (and image tiles of an all-image wave) need no mask.
   const int w_queries = a.query_len - wq0 < 32 ? a.query_len - wq0 : 32;
@@ -368,86 +342,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void a
   }
 }
 
-// Merges the parts of the split tiles (one workgroup per tile and head; the
-// unsplit tiles exit): per query row, M = max of the parts' maxima,
-// den = sum den_p exp(m_p - M), o = sum o_p exp(m_p - M) in part order, then
-// the final step of prefill64.rs:468-479 with lse = M + ln(den).
-__global__ __launch_bounds__(256) void attention_merge_kernel(AttnArgs a, SplitPlan plan) {
-  const int order = blockIdx.x, head = blockIdx.y;
-  const int parts = plan.first[order + 1] - plan.first[order];
-  if (parts <= 1) return;
-  const int row_in_tile = threadIdx.x >> 1, half = threadIdx.x & 1;
-  const int row = (a.tiles - 1 - order) * kQueries + row_in_tile;
-  if (row >= a.query_len) return;
-  const float *pmd = a.part + static_cast<size_t>(a.slots) * a.n_heads * kQueries * 64;
-  const float ninf = -__builtin_inff();
-  float big = ninf;
-  for (int p = 0; p < parts; p++) {
-    const size_t slot = static_cast<size_t>(plan.slot[order] + p) * a.n_heads + head;
-    const float m = pmd[(slot * kQueries + row_in_tile) * 2];
-    big = __builtin_fmaxf(big, m);
-  }
-  float den = 0.0f;
-  float4 o[8];
-#pragma unroll
-  for (int i = 0; i < 8; i++) o[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int p = 0; p < parts; p++) {
-    const size_t slot = static_cast<size_t>(plan.slot[order] + p) * a.n_heads + head;
-    const float2 md = reinterpret_cast<const float2 *>(pmd)[slot * kQueries + row_in_tile];
-    const float f = md.x == ninf ? 0.0f : expf_acc(md.x - big);
-    den = den + md.y * f;
-    const float4 *src = reinterpret_cast<const float4 *>(a.part + (slot * kQueries + row_in_tile) * 64 + 32 * half);
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const float4 v = src[i];
-      o[i] = make_float4(fmaf_(v.x, f, o[i].x), fmaf_(v.y, f, o[i].y), fmaf_(v.z, f, o[i].z), fmaf_(v.w, f, o[i].w));
-    }
-  }
-  const float lse = big + logf_acc(den);
-  const float sink_scale = __fdiv_rn(1.0f, 1.0f + expf_acc(a.sinks[head] - lse));
-  float4 *dst = reinterpret_cast<float4 *>(a.out + (static_cast<size_t>(row) * a.n_heads + head) * 64 + 32 * half);
-#pragma unroll
-  for (int i = 0; i < 8; i++)
-    dst[i] = make_float4(__fmul_rn(__fdiv_rn(o[i].x, den), sink_scale), __fmul_rn(__fdiv_rn(o[i].y, den), sink_scale),
-                         __fmul_rn(__fdiv_rn(o[i].z, den), sink_scale), __fmul_rn(__fdiv_rn(o[i].w, den), sink_scale));
-}
-
 }  // namespace
 
 namespace {
 
 // One launch (plus the merge) for at most kMaxTiles query tiles.
 int launch_tiles(Ctx *ctx, AttnArgs a, int softmax, int exp_mode) {
-  // Split plan: query tiles whose visible keys exceed chunk_keys run as
-  // several work items of at most chunk_keys keys, so that every item costs
-  // about the same and about four rounds of items fill the chip (the
-  // causal tiles' costs differ up to fourfold at a 16K context).
+  // Split plan (attention_split.hpp): parts of whole 32-key tiles.
   const int tiles = (a.query_len + kQueries - 1) / kQueries;
-  SplitPlan plan;
-  long long total = 0;
-  int vis[kMaxTiles];
-  for (int t = 0; t < tiles; t++) {
-    vis[t] = tile_visible_end(t, a.query_len, a.query_offset, a.image_start, a.image_end);
-    total += vis[t];
-  }
-  const long long want = total * static_cast<long long>(a.n_heads) / kSplitItems;
-  const int chunk_keys =
-      static_cast<int>(((want > kMinChunkKeys ? want : kMinChunkKeys) + kKeys - 1) / kKeys * kKeys);
-  int items = 0, slots = 0;
-  for (int i = 0; i < tiles; i++) {
-    const int end = vis[tiles - 1 - i];
-    const int want_parts = (end + chunk_keys - 1) / chunk_keys;
-    const int per = ((end + want_parts - 1) / want_parts + kKeys - 1) / kKeys * kKeys;
-    const int parts = (end + per - 1) / per;  // every part starts before `end`
-    plan.first[i] = items;
-    plan.slot[i] = parts > 1 ? slots : -1;
-    plan.keys[i] = per;
-    items += parts;
-    slots += parts > 1 ? parts : 0;
-  }
-  plan.first[tiles] = items;
+  split::Plan plan;
+  int slots = 0;
+  const int items = split::make_plan(plan, tiles, a.query_len, a.query_offset, a.image_start, a.image_end, a.n_heads,
+                                     kKeys, &slots);
   a.tiles = tiles;
-  a.chunk_keys = chunk_keys;
   a.slots = slots;
   a.part = nullptr;
   if (slots > 0) {
@@ -465,8 +372,17 @@ int launch_tiles(Ctx *ctx, AttnArgs a, int softmax, int exp_mode) {
     hipLaunchKernelGGL((attention_kernel<false, false>), grid, dim3(256), 0, ctx->stream, a, plan);
   FOCR_HIP_CHECK(hipGetLastError());
   if (slots > 0) {
-    hipLaunchKernelGGL(attention_merge_kernel, dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(a.n_heads)),
-                       dim3(256), 0, ctx->stream, a, plan);
+    split::Args m;
+    m.sinks = a.sinks;
+    m.out = a.out;
+    m.part = a.part;
+    m.query_len = a.query_len;
+    m.n_heads = a.n_heads;
+    m.tiles = tiles;
+    m.slots = slots;
+    m.merge_end = a.query_len;
+    hipLaunchKernelGGL(split::merge_kernel, dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(a.n_heads)),
+                       dim3(256), 0, ctx->stream, m, plan);
     FOCR_HIP_CHECK(hipGetLastError());
   }
   return FOCR_OK;

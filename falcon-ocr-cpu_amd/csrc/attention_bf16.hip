@@ -40,6 +40,7 @@
 // Roofline: BF16 matrix cores (2.5 PFLOP/s dense) for the products; the FP32
 // softmax (VALU, about 8-10 instructions per score) bounds it in practice.
 // FLOPs = 4 * 64 * visible pairs per head, as for FP32.
+#include "attention_split.hpp"
 #include "focr_internal.hpp"
 
 namespace focr {
@@ -120,7 +121,9 @@ struct Bf16Args {
   const float *q, *k, *v, *sinks;  // FP32 operands (the short tiles' path)
   const uint4 *kb, *vb;
   float *out;
+  float *part;  // partial states of split query tiles (attention_split.hpp)
   int query_len, n_heads, n_kv_heads, tiles, image_start, image_end;
+  int q_base, qtiles, slots;  // this launch's query tiles start at row q_base
 };
 
 // x[l % 32] op x[l % 32 + 32] in every lane (v_permlane32_swap).
@@ -283,13 +286,16 @@ __global__ __launch_bounds__(128) void short_rows_kernel(Bf16Args a, int first_r
   }
 }
 
+static_assert(split::kQueries == kQueries, "one query tile per split plan entry");
+
 struct KvLds {
   uint4 k[256];  // 32 keys x 8 chunks
   uint4 v[256];  // 64 dims x 4 chunks
 };
 
 template <bool STATIC>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void attention_bf16_kernel(Bf16Args a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void attention_bf16_kernel(Bf16Args a,
+                                                                                                     split::Plan plan) {
   __shared__ KvLds buf0;
   __shared__ KvLds buf1;
   const int head = blockIdx.y;
@@ -297,7 +303,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void a
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int h = lane >> 5, l32 = lane & 31;
-  const int first_query = (gridDim.x - 1 - blockIdx.x) * kQueries;  // heavy (late) tiles first
+  // This workgroup's work item: a part of the query tile it.order of the plan
+  // (heavy, late tiles first); parts are whole 128-key tiles of the reference.
+  const split::Item it = split::find_item(plan, a.qtiles, blockIdx.x);
+  const int first_query = a.q_base + (a.qtiles - 1 - it.order) * kQueries;
   const int wq0 = first_query + wave * 32;
   const int my_query = wq0 + l32;
   const bool my_valid = my_query < a.query_len;
@@ -307,7 +316,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void a
   const int wg_queries = a.query_len - first_query < kQueries ? a.query_len - first_query : kQueries;
   const int last_abs = first_query + wg_queries - 1;
   const bool intersects = first_query < a.image_end && last_abs >= a.image_start;
-  const int visible_end = intersects ? (last_abs + 1 > a.image_end ? last_abs + 1 : a.image_end) : last_abs + 1;
+  const int tile_end = intersects ? (last_abs + 1 > a.image_end ? last_abs + 1 : a.image_end) : last_abs + 1;
+  const int key_begin = it.key_begin;
+  const int visible_end = key_begin + it.keys < tile_end ? key_begin + it.keys : tile_end;
   const int w_queries = a.query_len - wq0 < 32 ? a.query_len - wq0 : 32;
   const int w_first = wq0, w_last = w_first + (w_queries > 0 ? w_queries : 1) - 1;
   const bool w_intersects = w_queries > 0 && w_first < a.image_end && w_last >= a.image_start;
@@ -437,17 +448,36 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void a
       }
   };
 
-  copy_tile(buf0, 0);
-  for (int kstart = 0; kstart < visible_end; kstart += 2 * kKeys) {
+  copy_tile(buf0, key_begin / kKeys);
+  for (int kstart = key_begin; kstart < visible_end; kstart += 2 * kKeys) {
     step(buf0, buf1, kstart);
     if (kstart + kKeys < visible_end) step(buf1, buf0, kstart + kKeys);
   }
 
+  // The short last key tile lies in one part (parts are whole 128-key tiles).
   if constexpr (!STATIC)
-    if (short_last) fp32_tail(a, head, kv_head, h, my_query, my_valid, my_image, last_tile, w_visible, o, run_max, den);
+    if (short_last && last_tile >= key_begin && last_tile < key_begin + it.keys)
+      fp32_tail(a, head, kv_head, h, my_query, my_valid, my_image, last_tile, w_visible, o, run_max, den);
+
+  if (!my_valid || short_rows) return;
+  if (it.parts > 1) {
+    // A split tile: the unnormalized state, for split::merge_kernel.
+    split::Args m;
+    m.part = a.part;
+    m.n_heads = a.n_heads;
+    m.slots = a.slots;
+    float *po = split::part_out(m, plan, it, head, my_query - first_query);
+#pragma unroll
+    for (int d = 0; d < 2; d++)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; q4++)
+        *reinterpret_cast<float4 *>(po + 32 * d + 8 * q4 + 4 * h) =
+            make_float4(o[d][4 * q4], o[d][4 * q4 + 1], o[d][4 * q4 + 2], o[d][4 * q4 + 3]);
+    if (h == 0) *split::part_md(m, plan, it, head, my_query - first_query) = make_float2(STATIC ? 0.0f : run_max, den);
+    return;
+  }
 
   // Normalize and apply the sink (bf16.rs:388-397, static_shift.rs:160-168).
-  if (!my_valid || short_rows) return;
   const float lse = STATIC ? logf_acc(den) : run_max + logf_acc(den);
   const float sink_scale = __fdiv_rn(1.0f, 1.0f + expf_acc(a.sinks[head] - lse));
   float *dst = a.out + (static_cast<size_t>(my_query) * a.n_heads + head) * 64;
@@ -495,11 +525,65 @@ int launch_attention_bf16(Ctx *ctx, const float *q, const float *k, const float 
   a.tiles = static_cast<int>(tiles);
   a.image_start = static_cast<int>(image_start);
   a.image_end = static_cast<int>(image_end);
-  const dim3 grid(static_cast<unsigned>((query_len + kQueries - 1) / kQueries), static_cast<unsigned>(n_heads));
-  if (softmax == FOCR_SOFTMAX_STATIC) {
-    hipLaunchKernelGGL(attention_bf16_kernel<true>, grid, dim3(256), 0, ctx->stream, a);
-  } else {
-    hipLaunchKernelGGL(attention_bf16_kernel<false>, grid, dim3(256), 0, ctx->stream, a);
+  // Query rows in launches of at most split::kMaxTiles tiles, each with its
+  // split plan (parts of whole 128-key tiles) and merge.
+  const int short_count = softmax == FOCR_SOFTMAX_STATIC ? 0 : static_cast<int>(query_len % 32);
+  const int merge_end = static_cast<int>(query_len) - (short_count == 1 || short_count == 2 ? short_count : 0);
+  const size_t per_launch = static_cast<size_t>(split::kMaxTiles) * kQueries;
+  for (size_t q0 = 0; q0 < query_len; q0 += per_launch) {
+    const int n = static_cast<int>(query_len - q0 < per_launch ? query_len - q0 : per_launch);
+    const int qtiles = (n + kQueries - 1) / kQueries;
+    split::Plan plan;
+    int slots = 0;
+    const int items = split::make_plan(plan, qtiles, n, static_cast<int>(q0), a.image_start, a.image_end,
+                                       a.n_heads, 128, &slots);
+    a.q_base = static_cast<int>(q0);
+    a.qtiles = qtiles;
+    a.slots = slots;
+    a.part = nullptr;
+    if (slots > 0) {
+      const size_t part_bytes = static_cast<size_t>(slots) * n_heads * kQueries * 66 * sizeof(float);
+      // The converted K/V stay at the front of the scratch; growing it would
+      // discard them, so grow first and convert again.
+      if (ctx->scratch_bytes < k_bytes + v_bytes + part_bytes) {
+        rc = ensure_scratch(ctx, k_bytes + v_bytes + part_bytes);
+        if (rc != FOCR_OK) return rc;
+        kb = static_cast<uint4 *>(ctx->scratch);
+        vb = reinterpret_cast<uint4 *>(static_cast<char *>(ctx->scratch) + k_bytes);
+        hipLaunchKernelGGL(convert_kv_kernel, dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(n_heads)),
+                           dim3(256), 0, ctx->stream, k, v, static_cast<int>(query_len), static_cast<int>(n_heads),
+                           static_cast<int>(n_kv_heads), static_cast<int>(tiles), kb, vb);
+        FOCR_HIP_CHECK(hipGetLastError());
+        a.kb = kb;
+        a.vb = vb;
+      }
+      a.part = reinterpret_cast<float *>(static_cast<char *>(ctx->scratch) + k_bytes + v_bytes);
+    }
+    const dim3 grid(static_cast<unsigned>(items), static_cast<unsigned>(n_heads));
+    if (softmax == FOCR_SOFTMAX_STATIC)
+      hipLaunchKernelGGL(attention_bf16_kernel<true>, grid, dim3(256), 0, ctx->stream, a, plan);
+    else
+      hipLaunchKernelGGL(attention_bf16_kernel<false>, grid, dim3(256), 0, ctx->stream, a, plan);
+    FOCR_HIP_CHECK(hipGetLastError());
+    if (slots > 0) {
+      split::Args m;
+      m.sinks = sinks;
+      m.out = out;
+      m.part = a.part;
+      m.query_len = static_cast<int>(query_len);
+      m.n_heads = static_cast<int>(n_heads);
+      m.tiles = qtiles;
+      m.slots = slots;
+      m.merge_end = merge_end;
+      // merge_kernel's rows are relative to the launch: offset the output.
+      m.out = out + q0 * n_heads * 64;
+      m.merge_end = merge_end - static_cast<int>(q0);
+      hipLaunchKernelGGL(split::merge_kernel, dim3(static_cast<unsigned>(qtiles), static_cast<unsigned>(n_heads)),
+                         dim3(256), 0, ctx->stream, m, plan);
+      FOCR_HIP_CHECK(hipGetLastError());
+    }
+  }
+  if (softmax != FOCR_SOFTMAX_STATIC) {
     // A last 32-query tile of one or two queries (the main kernel skips it).
     const size_t rows = query_len % 32;
     if (rows == 1 || rows == 2)

@@ -119,3 +119,22 @@ def test_config4_full_page_bf16(fh, softmax):
                                              tiles=(lo, hi))
         rows = slice(32 * lo, 32 * hi)
         assert max_rel(got[rows], want[rows]) <= 2e-3
+
+
+@pytest.mark.parametrize("softmax", ["online", "static"])
+@pytest.mark.parametrize("L,image", [(3001, (0, 1500)), (2562, (0, 0))])
+def test_split_key_ranges_bf16(fh, softmax, L, image):
+    # Query tiles with more than 1,024 visible keys run as several work items
+    # (whole 128-key tiles) merged afterwards; L % 32 = 1 or 2 keeps the
+    # short-rows kernel's rows out of the merge.
+    oracle.set_threads(8)
+    r = oracle.bf16_round
+    q = r(gen.normalized(L * 16 * 64, 401))
+    k = r(gen.normalized(L * 16 * 64, 402))
+    v = r(gen.values(L * 8 * 64, 403, 3.0))
+    sinks = gen.values(16, 29, 2.0)
+    sm = fh.Softmax.STATIC if softmax == "static" else fh.Softmax.ONLINE
+    got = run(fh, q, k, v, sinks, L, image, sm)
+    want = oracle.attention_prefill_bf16(q, k, v, L, 16, 8, *image, sinks, static=softmax == "static")
+    assert np.all(np.isfinite(got))
+    assert max_rel(got, want) <= 2e-3

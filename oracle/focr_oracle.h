@@ -72,6 +72,11 @@ void orc_row_scales(const float *h, size_t rows, size_t width, float eps, float 
 void orc_panel_gemm(const float *a, size_t m, size_t k, const float *w, size_t n,
                     const float *row_scale, int epilogue, float *out);
 
+/* The same product with the reference's AVX2 6x16 FMA micro-kernel
+ * (focr_cpu_panels.c): bitwise orc_panel_gemm, at CPU-baseline speed. */
+void orc_panel_gemm_fast(const float *a, size_t m, size_t k, const float *w, size_t n,
+                         const float *row_scale, int epilogue, float *out);
+
 /* ---- A3: INT16-activation x INT8-code panel GEMM ----------------------- */
 /* quantize_group, src/kernels/panels/panel_i16.rs:233-266. Returns the step. */
 float orc_i16_quantize_group(const float *x, int16_t *q);
@@ -120,6 +125,14 @@ void orc_attention_prefill_tiles(const float *q, const float *prefix_k, const fl
                                  size_t query_offset, size_t image_start, size_t image_end,
                                  const float *sinks, int static_softmax, int exp_fast,
                                  size_t tile_begin, size_t tile_end, float *out);
+
+/* orc_attention_prefill_tiles with exp_fast = 1, vectorized across the 32
+ * query lanes (focr_cpu_attention.c): bitwise the same, CPU-baseline speed. */
+void orc_attention_prefill_fast(const float *q, const float *prefix_k, const float *generated_k, const float *v,
+                                size_t query_len, size_t prefix_len, size_t total_len, size_t n_heads,
+                                size_t n_kv_heads, size_t query_offset, size_t image_start, size_t image_end,
+                                const float *sinks, int static_softmax, size_t tile_begin, size_t tile_end,
+                                float *out);
 
 /* ---- the QKV row step --------------------------------------------------- */
 /* fused_row (src/model/fused.rs:101-123) for rows < prefix_rows, and

@@ -69,6 +69,8 @@ _sig("orc_linear_decode_glu", None, _I, _P, _P, _Z, _Z, _Z, _P, _P, _Z, _P, _Z, 
 _sig("orc_rms_scale", _F, _P, _Z, _F)
 _sig("orc_row_scales", None, _P, _Z, _Z, _F, _P)
 _sig("orc_panel_gemm", None, _P, _Z, _Z, _P, _Z, _P, _I, _P)
+_sig("orc_panel_gemm_fast", None, _P, _Z, _Z, _P, _Z, _P, _I, _P)
+_sig("orc_attention_prefill_fast", None, _P, _P, _P, _P, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _P, _I, _Z, _Z, _P)
 _sig("orc_i16_quantize_group", _F, _P, _P)
 _sig("orc_i16_quantize_rows", None, _P, _Z, _Z, _P, _Z, _P, _P, _P, _P)
 _sig("orc_i16_gemm", None, _P, _Z, _Z, _P, _P, _Z, _P, _P, _Z, _P, _I, _P)
@@ -209,6 +211,20 @@ def panel_gemm(a, m, k, w, n, row_scale=None, epilogue=STORE, out=None):
     return out
 
 
+def panel_gemm_fast(a, m, k, w, n, row_scale=None, epilogue=STORE, out=None):
+    """The FP32 panel GEMM with the reference's AVX2 6x16 micro-kernel
+    (oracle/focr_cpu_panels.c): bitwise panel_gemm, CPU-baseline speed."""
+    a, w = _f32(a), _f32(w)
+    rs = _f32(row_scale) if row_scale is not None else None
+    width = n // 2 if epilogue == GLU else n
+    if out is None:
+        out = np.zeros((m, width), dtype=np.float32)
+    else:
+        out = _f32(out).copy()
+    _lib.orc_panel_gemm_fast(_ptr(a), m, k, _ptr(w), n, _ptr(rs), epilogue, _ptr(out))
+    return out
+
+
 def i16_quantize_group(x):
     x = _f32(x)
     assert x.size == 64
@@ -260,6 +276,21 @@ def attention_prefill(q, prefix_k, v, query_len, prefix_len, total_len, n_heads,
         _lib.orc_attention_prefill_tiles(_ptr(q), _ptr(prefix_k), _ptr(gk), _ptr(v), query_len, prefix_len,
                                          total_len, n_heads, n_kv_heads, query_offset, image_start, image_end,
                                          _ptr(sinks), int(static), int(exp_fast), tiles[0], tiles[1], _ptr(out))
+    return out.reshape(query_len, n_heads, 64)
+
+
+def attention_prefill_fast(q, prefix_k, v, query_len, prefix_len, total_len, n_heads, n_kv_heads, query_offset,
+                           image_start, image_end, sinks, static=False, generated_k=None, tiles=None, out=None):
+    """attention_prefill (Fast exp or static) vectorized over the query lanes:
+    bitwise the same outputs, at CPU-baseline speed (oracle/focr_cpu_attention.c)."""
+    q, prefix_k, v, sinks = _f32(q), _f32(prefix_k), _f32(v), _f32(sinks)
+    gk = _f32(generated_k) if generated_k is not None else None
+    if out is None:
+        out = np.zeros(query_len * n_heads * 64, dtype=np.float32)
+    lo, hi = (0, (query_len + 31) // 32) if tiles is None else tiles
+    _lib.orc_attention_prefill_fast(_ptr(q), _ptr(prefix_k), _ptr(gk), _ptr(v), query_len, prefix_len, total_len,
+                                    n_heads, n_kv_heads, query_offset, image_start, image_end, _ptr(sinks),
+                                    int(static), lo, hi, _ptr(out))
     return out.reshape(query_len, n_heads, 64)
 
 

@@ -326,6 +326,56 @@ def cpu_baseline(np, gen, seconds=10.0):
                       f"calls in ~{seconds:.0f} s (oracle/focr_oracle.c, OpenMP {threads} threads)"}
 
 
+def cpu_prefill_page(np, gen, gpu_gemm, gpu_attention, reps=2):
+    """The FP32 prefill of one 6,544-token page on the host cores against the
+    GPU's: the literal projection X[6544x1024] x W[1024x4096] and the four
+    checkpoint projections, each plus the config-4 attention (16 heads, image
+    prefix 4,096). The CPU side runs the reference's AVX2 panel micro-kernel
+    and the attention tile vectorized over the query lanes (bitwise the
+    oracle's results), over the whole page; best of `reps` calls each."""
+    import oracle
+
+    threads = min(os.cpu_count() or 1, 16)
+    oracle.set_threads(threads)
+    m = 6544
+
+    def best(fn):
+        t = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            t.append(time.perf_counter() - t0)
+        return min(t) * 1e3
+
+    cpu = {}
+    for name, k, n, epi in (("literal", 1024, 4096, oracle.STORE), ("qkv", 768, 2048, oracle.STORE),
+                            ("wo", 1024, 768, oracle.ADD), ("w13", 768, 4608, oracle.GLU),
+                            ("w2", 2304, 768, oracle.ADD)):
+        a = gen.normal((m, k), 1.0, 10)
+        w = gen.normal((n, k), 0.02, 11)
+        cpu[name] = best(lambda: oracle.panel_gemm_fast(a, m, k, w, n, epilogue=epi))
+        log(f"cpu {name} GEMM: {cpu[name]:.1f} ms")
+    L, img = 6544, 4096
+    q, k = gen.normal(L * 16 * 64, 1.0, 20), gen.normal(L * 16 * 64, 1.0, 21)
+    v, sinks = gen.normal(L * 8 * 64, 1.0, 22), gen.uniform(16, -2.0, 2.0, 23)
+    cpu["attention"] = best(lambda: oracle.attention_prefill_fast(q, k, v, L, L, L, 16, 8, 0, 0, img, sinks))
+    log(f"cpu attention: {cpu['attention']:.1f} ms")
+    oracle.set_threads(1)
+    layer = ("qkv", "wo", "w13", "w2")
+    gpu_literal = gpu_gemm["literal_mfma"]["ms"] + gpu_attention["online_fast"]["ms"]
+    gpu_layer = sum(gpu_gemm[f"{s}_mfma"]["ms"] for s in layer) + gpu_attention["online_fast"]["ms"]
+    cpu_literal = cpu["literal"] + cpu["attention"]
+    cpu_layer = sum(cpu[s] for s in layer) + cpu["attention"]
+    return {"cores": threads, "kind": "port",
+            "cpu_ms": {s: round(t, 2) for s, t in cpu.items()},
+            "literal_page": {"gpu_ms": round(gpu_literal, 4), "cpu_ms": round(cpu_literal, 1),
+                             "speedup": round(cpu_literal / gpu_literal, 1)},
+            "layer_page": {"gpu_ms": round(gpu_layer, 4), "cpu_ms": round(cpu_layer, 1),
+                           "speedup": round(cpu_layer / gpu_layer, 1)},
+            "sample": f"whole page, best of {reps} calls, OpenMP {threads} threads "
+                      "(oracle/focr_cpu_panels.c, oracle/focr_cpu_attention.c; online softmax, Fast exp)"}
+
+
 def measured_traffic():
     """traffic_bytes_per_launch from the committed PMC summary, or None."""
     import re
@@ -401,6 +451,9 @@ def main():
         log(f"layer: {per_op['layer_int8_16k']}")
     if "copy" in ops:
         per_op["copy_256MiB"] = bench_copy(torch, 10)
+    if not args.no_cpu and "prefill_f32" in per_op and "attention_prefill" in per_op:
+        per_op["prefill_page_vs_cpu"] = cpu_prefill_page(np, gen, per_op["prefill_f32"], per_op["attention_prefill"])
+        log(f"prefill page vs CPU: {per_op['prefill_page_vs_cpu']}")
     cpu = None if args.no_cpu else cpu_baseline(np, gen)
     line = {
         "metric": "decode GEMV HBM GB/s (INT16 group-64, W 4096x1024, M=1)",

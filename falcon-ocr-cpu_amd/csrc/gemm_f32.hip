@@ -221,49 +221,216 @@ __global__ __launch_bounds__(256) void mfma_kernel(GemmArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
 
-  const int stages = (a.k + kBK - 1) / kBK;
-  load_stage(0);
-  store_stage(0);
-  __syncthreads();
-  for (int st = 0; st < stages; st++) {
-    const int buf = st & 1;
-    if (st + 1 < stages) load_stage((st + 1) * kBK);
-    // Lane half h supplies k-slot h of each 32x32x2 step: k = 16 h + s.
-    float av[WM][16], bv[WN][16];
+  // Each stage's 16 k-steps run in two halves of 8. The LDS reads of one half
+  // are issued before the matrix-core work on the other, so their latency
+  // hides behind it: half 1 of stage s is read before half 0's products, and
+  // half 0 of stage s + 1 right after the barrier, before half 1's products.
+  float fa[2][WM][8], fb[2][WN][8];
+  auto read_half = [&](int buf, int half, float (*va)[8], float (*vb)[8]) {
 #pragma unroll
     for (int i = 0; i < WM; i++) {
-      const float4 *ar = reinterpret_cast<const float4 *>(&as[buf][wm * (BM / 2) + i * 32 + l32][16 * h]);
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const float4 x = ar[q];
-        av[i][4 * q] = x.x;
-        av[i][4 * q + 1] = x.y;
-        av[i][4 * q + 2] = x.z;
-        av[i][4 * q + 3] = x.w;
-      }
+      const float4 *ar =
+          reinterpret_cast<const float4 *>(&as[buf][wm * (BM / 2) + i * 32 + l32][16 * h + 8 * half]);
+      const float4 x0 = ar[0], x1 = ar[1];
+      va[i][0] = x0.x; va[i][1] = x0.y; va[i][2] = x0.z; va[i][3] = x0.w;
+      va[i][4] = x1.x; va[i][5] = x1.y; va[i][6] = x1.z; va[i][7] = x1.w;
     }
 #pragma unroll
     for (int j = 0; j < WN; j++) {
-      const float4 *br = reinterpret_cast<const float4 *>(&bs[buf][wn * (BN / 2) + j * 32 + l32][16 * h]);
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const float4 y = br[q];
-        bv[j][4 * q] = y.x;
-        bv[j][4 * q + 1] = y.y;
-        bv[j][4 * q + 2] = y.z;
-        bv[j][4 * q + 3] = y.w;
-      }
+      const float4 *br =
+          reinterpret_cast<const float4 *>(&bs[buf][wn * (BN / 2) + j * 32 + l32][16 * h + 8 * half]);
+      const float4 y0 = br[0], y1 = br[1];
+      vb[j][0] = y0.x; vb[j][1] = y0.y; vb[j][2] = y0.z; vb[j][3] = y0.w;
+      vb[j][4] = y1.x; vb[j][5] = y1.y; vb[j][6] = y1.z; vb[j][7] = y1.w;
     }
+  };
+  // Lane half h supplies k-slot h of each 32x32x2 step: k = 16 h + 8 half + s.
+  auto products = [&](float (*va)[8], float (*vb)[8]) {
 #pragma unroll
-    for (int s2 = 0; s2 < 16; s2++)
+    for (int s2 = 0; s2 < 8; s2++)
 #pragma unroll
       for (int i = 0; i < WM; i++)
 #pragma unroll
         for (int j = 0; j < WN; j++)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i][s2], bv[j][s2], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(va[i][s2], vb[j][s2], acc[i][j], 0, 0, 0);
+  };
+
+  const int stages = (a.k + kBK - 1) / kBK;
+  load_stage(0);
+  store_stage(0);
+  __syncthreads();
+  read_half(0, 0, fa[0], fb[0]);
+  for (int st = 0; st < stages; st++) {
+    const int buf = st & 1;
+    if (st + 1 < stages) load_stage((st + 1) * kBK);
+    read_half(buf, 1, fa[1], fb[1]);
+    products(fa[0], fb[0]);
     if (st + 1 < stages) store_stage(buf ^ 1);
+    // The barrier's LDS wait also retires this stage's half-1 reads before
+    // any wave overwrites this buffer (two stages on).
     __syncthreads();
+    if (st + 1 < stages) read_half(buf ^ 1, 0, fa[0], fb[0]);
+    products(fa[1], fb[1]);
   }
+  // D layout of 32x32: column = lane % 32, row = 8 (r / 4) + 4 (lane / 32) + r % 4.
+#pragma unroll
+  for (int i = 0; i < WM; i++)
+#pragma unroll
+    for (int j = 0; j < WN; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int row = m0 + wm * (BM / 2) + i * 32 + 8 * (r / 4) + 4 * h + (r % 4);
+        const int col = n0 + wn * (BN / 2) + j * 32 + l32;
+        const float v = acc[i][j][r];
+        const float partner = EPI == FOCR_EPI_GLU ? __shfl_xor(v, 1) : 0.0f;
+        emit<EPI>(a, row, col, v, partner);
+      }
+}
+
+// FP32 weights, k a multiple of 64: A and W stages of 16 k are copied
+// HBM -> LDS by the LDS-DMA path (global_load_lds, 16 bytes per lane) into a
+// ring of four stages, three stages ahead of the matrix cores, so the copies'
+// latency never stalls them and no registers stage the data. Rows of a stage
+// hold 16 floats as four 16-byte chunks, chunk c of row r stored at position
+// c ^ dma_swizzle(r) (conflict-free for the 32-row fragment reads). The row
+// scale is applied to the fragments as they are read (the same single
+// rounding fl(a * row_scale)). Rows past m or n repeat the last row (in
+// bounds); their outputs are not written.
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) const void global_void;
+
+constexpr int kDmaBK = 16;
+
+__device__ __forceinline__ int dma_swizzle(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+
+// Compiler-only ordering around the plain workgroup barrier: the waits are
+// explicit (a __syncthreads fence would wait for every copy in flight).
+__device__ __forceinline__ void plain_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+template <int EPI, int BN>
+__global__ __launch_bounds__(256) void dma_kernel(GemmArgs a) {
+  constexpr int BM = 128;
+  constexpr int WM = BM / 64, WN = BN / 64;
+  constexpr int AT = BM / 64, BT = BN / 64;  // copies of 1 KB per wave per stage
+  constexpr int PER = AT + BT;
+  __shared__ float4 la0[BM * 4], la1[BM * 4], la2[BM * 4], la3[BM * 4];
+  __shared__ float4 lb0[BN * 4], lb1[BN * 4], lb2[BN * 4], lb3[BN * 4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
+  const int h = lane >> 5, l32 = lane & 31;
+  const float *w = static_cast<const float *>(a.codes);
+
+  // Copy t of this wave fills LDS chunks [64 (wave + 4 t), +64): row
+  // 16 (wave + 4 t) + lane / 4, position lane % 4.
+  const float *asrc[AT];
+  const float *bsrc[BT];
+#pragma unroll
+  for (int t = 0; t < AT; t++) {
+    const int row = 16 * (wave + 4 * t) + (lane >> 2);
+    const int g = m0 + row < a.m ? m0 + row : a.m - 1;
+    asrc[t] = a.x + static_cast<size_t>(g) * a.k + 4 * ((lane & 3) ^ dma_swizzle(row));
+  }
+#pragma unroll
+  for (int t = 0; t < BT; t++) {
+    const int row = 16 * (wave + 4 * t) + (lane >> 2);
+    const int g = n0 + row < a.n ? n0 + row : a.n - 1;
+    bsrc[t] = w + static_cast<size_t>(g) * a.k + 4 * ((lane & 3) ^ dma_swizzle(row));
+  }
+  auto issue = [&](float4 *la, float4 *lb, int stage) {
+    const int off = stage * kDmaBK;
+#pragma unroll
+    for (int t = 0; t < AT; t++)
+      __builtin_amdgcn_global_load_lds((global_void *)(asrc[t] + off), (lds_void *)(la + 64 * (wave + 4 * t)), 16, 0, 0);
+#pragma unroll
+    for (int t = 0; t < BT; t++)
+      __builtin_amdgcn_global_load_lds((global_void *)(bsrc[t] + off), (lds_void *)(lb + 64 * (wave + 4 * t)), 16, 0, 0);
+  };
+
+  float rs[WM];
+#pragma unroll
+  for (int i = 0; i < WM; i++) {
+    const int r = m0 + wm * (BM / 2) + 32 * i + l32;
+    rs[i] = a.row_scale ? a.row_scale[r < a.m ? r : a.m - 1] : 1.0f;
+  }
+  const bool scaled = a.row_scale != nullptr;
+
+  // Lane half h holds k = 8 h .. 8 h + 7 of the stage (chunks 2h, 2h + 1).
+  auto read = [&](const float4 *la, const float4 *lb, float (*va)[8], float (*vb)[8]) {
+#pragma unroll
+    for (int i = 0; i < WM; i++) {
+      const int r = wm * (BM / 2) + 32 * i + l32;
+      const float4 x0 = la[4 * r + ((2 * h) ^ dma_swizzle(r))];
+      const float4 x1 = la[4 * r + ((2 * h + 1) ^ dma_swizzle(r))];
+      va[i][0] = x0.x; va[i][1] = x0.y; va[i][2] = x0.z; va[i][3] = x0.w;
+      va[i][4] = x1.x; va[i][5] = x1.y; va[i][6] = x1.z; va[i][7] = x1.w;
+    }
+#pragma unroll
+    for (int j = 0; j < WN; j++) {
+      const int r = wn * (BN / 2) + 32 * j + l32;
+      const float4 y0 = lb[4 * r + ((2 * h) ^ dma_swizzle(r))];
+      const float4 y1 = lb[4 * r + ((2 * h + 1) ^ dma_swizzle(r))];
+      vb[j][0] = y0.x; vb[j][1] = y0.y; vb[j][2] = y0.z; vb[j][3] = y0.w;
+      vb[j][4] = y1.x; vb[j][5] = y1.y; vb[j][6] = y1.z; vb[j][7] = y1.w;
+    }
+  };
+
+  v16f acc[WM][WN];
+#pragma unroll
+  for (int i = 0; i < WM; i++)
+#pragma unroll
+    for (int j = 0; j < WN; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+  auto products = [&](float (*va)[8], float (*vb)[8]) {
+    if (scaled) {
+#pragma unroll
+      for (int i = 0; i < WM; i++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) va[i][e] = va[i][e] * rs[i];
+    }
+#pragma unroll
+    for (int s2 = 0; s2 < 8; s2++)
+#pragma unroll
+      for (int i = 0; i < WM; i++)
+#pragma unroll
+        for (int j = 0; j < WN; j++)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(va[i][s2], vb[j][s2], acc[i][j], 0, 0, 0);
+  };
+
+  // Stage st sits in ring slot st % 4. Step st: wait for this wave's copies
+  // of stage st (and its reads of the previous slot), meet the other waves,
+  // start stage st + 3 into the previous stage's slot, read stage st's
+  // fragments, then run the products of stage st - 1 while they arrive.
+  const int stages = a.k / kDmaBK;  // a multiple of 4
+  float fa[2][WM][8], fb[2][WN][8];
+  issue(la0, lb0, 0);
+  issue(la1, lb1, 1);
+  issue(la2, lb2, 2);
+  auto step = [&](int st, const float4 *ca, const float4 *cb, float4 *na, float4 *nb, float (*ra)[8],
+                  float (*rb)[8], float (*pa)[8], float (*pb)[8]) __attribute__((always_inline)) {
+    __builtin_amdgcn_s_waitcnt((2 * PER) | 0x0070);  // vmcnt(2 PER) lgkmcnt(0)
+    plain_barrier();
+    // Past the last stage the copy repeats it into the free slot, so the
+    // count of copies in flight (and the wait above) stays the same.
+    issue(na, nb, st + 3 < stages ? st + 3 : stages - 1);
+    read(ca, cb, ra, rb);
+    if (st > 0) products(pa, pb);
+  };
+  for (int st = 0; st < stages; st += 4) {
+    step(st, la0, lb0, la3, lb3, fa[0], fb[0], fa[1], fb[1]);
+    step(st + 1, la1, lb1, la0, lb0, fa[1], fb[1], fa[0], fb[0]);
+    step(st + 2, la2, lb2, la1, lb1, fa[0], fb[0], fa[1], fb[1]);
+    step(st + 3, la3, lb3, la2, lb2, fa[1], fb[1], fa[0], fb[0]);
+  }
+  products(fa[1], fb[1]);
+  // The repeated copies must land before the workgroup's LDS is released.
+  __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
+
   // D layout of 32x32: column = lane % 32, row = 8 (r / 4) + 4 (lane / 32) + r % 4.
 #pragma unroll
   for (int i = 0; i < WM; i++)
@@ -347,11 +514,21 @@ void launch_one(bool chain, const GemmArgs &a, hipStream_t stream) {
     hipLaunchKernelGGL((chain_kernel<T, EPI>), grid, dim3(256), 0, stream, a);
     return;
   }
-  // Vector staging needs rows of whole float4 (and whole 32-stages of k).
-  const bool vec = a.k % kBK == 0;
   // A narrower N tile when 128 x 128 tiles would not give two waves of
   // workgroups over the 256 compute units.
   const long tiles128 = static_cast<long>((a.m + 127) / 128) * ((a.n + 127) / 128);
+  if constexpr (std::is_same<T, float>::value) {
+    const bool aligned = (reinterpret_cast<uintptr_t>(a.x) | reinterpret_cast<uintptr_t>(a.codes)) % 16 == 0;
+    if (a.k % (4 * kDmaBK) == 0 && aligned) {
+      if (tiles128 >= 512)
+        hipLaunchKernelGGL((dma_kernel<EPI, 128>), dim3((a.m + 127) / 128, (a.n + 127) / 128), dim3(256), 0, stream, a);
+      else
+        hipLaunchKernelGGL((dma_kernel<EPI, 64>), dim3((a.m + 127) / 128, (a.n + 63) / 64), dim3(256), 0, stream, a);
+      return;
+    }
+  }
+  // Vector staging needs rows of whole float4 (and whole 32-stages of k).
+  const bool vec = a.k % kBK == 0;
   if (tiles128 >= 512) {
     const dim3 grid((a.m + 127) / 128, (a.n + 127) / 128);
     if (vec)

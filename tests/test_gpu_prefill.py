@@ -107,7 +107,7 @@ def test_config3_int8_prefill_full_size(fh):
     assert np.all(np.isfinite(got))
 
 
-F32_SHAPES = [(1, 64, 16), (13, 768, 48), (97, 1024, 32), (200, 2304, 64), (9, 7, 16), (130, 300, 160)]
+F32_SHAPES = [(1, 64, 16), (13, 768, 48), (97, 1024, 32), (200, 2304, 64), (9, 7, 16), (130, 300, 160), (300, 192, 200)]
 
 
 @pytest.mark.parametrize("bits", [32, 16, 8])

@@ -107,6 +107,14 @@ __device__ __forceinline__ void copy_tile(const AttnArgs &a, KvTile &t, int ksta
   }
 }
 
+// Compiler-only ordering around the plain workgroup barrier: the waits are
+// explicit (a __syncthreads fence would wait for every copy in flight).
+__device__ __forceinline__ void plain_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 struct WaveState {
   float qv[32];  // Q^T operand, pre-scaled by 1/8: q[query][32 h + s]
   v16f o[2];     // O^T, dims 32 d + 8(r/4) + 4h + r%4 of query l32
@@ -221,6 +229,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void a
                                                                                                 split::Plan plan) {
   __shared__ KvTile tile0;
   __shared__ KvTile tile1;
+  __shared__ KvTile tile2;
   const int head = blockIdx.y;
   const int kv_head = head / (a.n_heads / a.n_kv_heads);
   const int tid = threadIdx.x, lane = tid & 63;
@@ -273,32 +282,43 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void a
   w.run_max = -__builtin_inff();
   w.den = 0.0f;
 
-  // Tile t is computed from tile0 (t even) or tile1 (t odd) while tile t + 1
-  // is copied into the other array.
-  auto step = [&](KvTile &cur, KvTile &next, int kstart) __attribute__((always_inline)) {
+  // Tile t sits in array t % 3; while it is computed, tiles t + 1 and t + 2
+  // are in flight. Past the last tile the copy repeats the last key into the
+  // free array, so every wave always has the copies of two tiles in flight.
+  auto step = [&](KvTile &cur, KvTile &ahead, int kstart) __attribute__((always_inline)) {
     const int keys = visible_end - kstart < kKeys ? visible_end - kstart : kKeys;
-    // This wave's copies into cur have landed; after the barrier every
-    // wave's have, and no wave still reads next (the previous tile).
-    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0)
-    __syncthreads();
-    if (keys < kKeys) {
+    // This wave's copies into cur have landed and its reads of the previous
+    // tile are done; after the barrier every wave's are, so the previous
+    // tile's array (ahead) is free.
+    __builtin_amdgcn_s_waitcnt(4 | 0x0070);  // vmcnt(4) lgkmcnt(0)
+    plain_barrier();
+    if (keys > 0 && keys < kKeys) {
       // Last tile: clear the V rows past the visible keys (p = 0 there, and
       // 0 * V must stay finite).
       for (int idx = tid; idx < (kKeys - keys) * 16; idx += 256)
         cur.rows[1][keys + (idx >> 4)][idx & 15] = make_float4(0.f, 0.f, 0.f, 0.f);
-      __syncthreads();
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+      plain_barrier();
     }
-    if (kstart + kKeys < visible_end) copy_tile(a, next, kstart + kKeys, visible_end, head, kv_head, wave, lane);
-    if (w_queries > 0 && kstart < w_visible) {
+    const int far = kstart + 2 * kKeys;
+    copy_tile(a, ahead, far < visible_end ? far : visible_end - 1, visible_end, head, kv_head, wave, lane);
+    if (keys > 0 && w_queries > 0 && kstart < w_visible) {
       const bool full = keys == kKeys && (kstart + kKeys <= w_first + 1 ||
                                           (w_all_image && kstart >= a.image_start && kstart + kKeys <= a.image_end));
       tile_step<STATIC, FAST>(a, cur, w, kstart, keys, !full, h, l32, my_abs, my_image);
     }
   };
   copy_tile(a, tile0, key_begin, visible_end, head, kv_head, wave, lane);
-  for (int kstart = key_begin; kstart < visible_end; kstart += 2 * kKeys) {
-    step(tile0, tile1, kstart);
-    if (kstart + kKeys < visible_end) step(tile1, tile0, kstart + kKeys);
+  copy_tile(a, tile1, key_begin + kKeys < visible_end ? key_begin + kKeys : visible_end - 1, visible_end, head,
+            kv_head, wave, lane);
+  // Whole rounds of three steps (a step past the last tile only waits, meets
+  // the other waves and repeats a copy): the same straight-line code for
+  // every round keeps the compiler's LDS-copy tracking exact, so it adds no
+  // wait for the copies in flight before the reads of a landed tile.
+  for (int kstart = key_begin; kstart < visible_end; kstart += 3 * kKeys) {
+    step(tile0, tile2, kstart);
+    step(tile1, tile0, kstart + kKeys);
+    step(tile2, tile1, kstart + 2 * kKeys);
   }
 
   // Normalize and apply the sink (prefill64.rs:468-479); a split tile

@@ -157,6 +157,26 @@ void orc_attention_decode(const float *q, const float *prefix_k, const float *ge
 /* argmax, src/runner/mod.rs:916-930. 0 ok, -1 on non-finite/empty. */
 int orc_argmax(const float *logits, size_t n, uint32_t *out);
 
+/* ---- INT8 screened vocabulary head (src/head_screen.rs) ------------------ */
+#define ORC_SCREEN_GROUP 64
+#define ORC_SCREEN_LIMIT 1024
+/* kappa of a dim-wide head (head_screen.rs:99-106), NaN if >= 0.53. */
+float orc_screen_kappa(size_t dim);
+/* ScreenedHead::build / quantize_row: codes [vocab][dim], scales
+ * [vocab][dim/64]; 0 ok, -1 on shape, non-finite weight or premise. */
+int orc_screen_build(const float *w, size_t vocab, size_t dim, int8_t *codes, float *scales,
+                     float *weight_abs_max, float *kappa);
+/* prepare: 1 with norms [dim/64], or 0 when the proof's assumptions fail. */
+int orc_screen_prepare(const float *x, size_t dim, float weight_abs_max, float *norms);
+/* screen_row in the AVX2 order: approximate logit q and S = sum s_g n_g. */
+void orc_screen_row(const float *x, const int8_t *codes, const float *scales, const float *norms,
+                    size_t dim, float *q, float *s);
+/* select: 1 = Token (*token, *candidates), 0 = Fallback (*candidates);
+ * upper [vocab] receives q + B. */
+int orc_screen_select(const float *x, const float *fp32, const int8_t *codes, const float *scales,
+                      size_t vocab, size_t dim, float weight_abs_max, float kappa, float *upper,
+                      uint32_t *token, uint32_t *candidates);
+
 /* Threads the oracle uses for its parallel loops (1 = scalar). */
 void orc_set_threads(int threads);
 int orc_get_threads(void);

@@ -80,6 +80,11 @@ _sig("orc_attention_prefill_bf16_tiles", None, _P, _P, _P, _Z, _Z, _Z, _Z, _Z, _
 _sig("orc_exp2_minimax", _F, _F)
 _sig("orc_bf16_round", _F, _F)
 _sig("orc_argmax", _I, _P, _Z, _P)
+_sig("orc_screen_kappa", _F, _Z)
+_sig("orc_screen_build", _I, _P, _Z, _Z, _P, _P, _P, _P)
+_sig("orc_screen_prepare", _I, _P, _Z, _F, _P)
+_sig("orc_screen_row", None, _P, _P, _P, _P, _Z, _P, _P)
+_sig("orc_screen_select", _I, _P, _P, _P, _P, _Z, _Z, _F, _F, _P, _P, _P)
 _sig("orc_qkv_rows", None, _P, _Z, _P, _Z, _Z, _Z, _P, _P, _P, _P)
 _sig("orc_attention_decode", None, _P, _P, _P, _P, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _P, _P)
 _sig("orc_set_threads", None, _I)
@@ -353,3 +358,52 @@ def argmax(logits):
     if rc != 0:
         raise ValueError("nonfinite or empty logits")
     return int(out.value)
+
+
+# ---- INT8 screened vocabulary head (src/head_screen.rs) -------------------
+SCREEN_LIMIT = 1024
+
+
+def screen_build(w, vocab, dim):
+    """ScreenedHead::build: (codes int8 [vocab][dim], scales [vocab][dim/64],
+    weight_abs_max, kappa); raises ValueError where the reference errors."""
+    w = _f32(w)
+    codes = np.zeros((vocab, dim), dtype=np.int8)
+    scales = np.zeros((vocab, max(dim // 64, 1)), dtype=np.float32)
+    wmax, kappa = ctypes.c_float(0), ctypes.c_float(0)
+    rc = _lib.orc_screen_build(_ptr(w), vocab, dim, _ptr(codes), _ptr(scales), ctypes.byref(wmax), ctypes.byref(kappa))
+    if rc != 0:
+        raise ValueError("screened head build rejected the weights")
+    return codes, scales, float(wmax.value), float(kappa.value)
+
+
+def screen_kappa(dim):
+    return float(_lib.orc_screen_kappa(dim))
+
+
+def screen_prepare(x, dim, weight_abs_max):
+    """(ok, norms) of prepare."""
+    x = _f32(x)
+    norms = np.zeros(max(dim // 64, 1), dtype=np.float32)
+    ok = _lib.orc_screen_prepare(_ptr(x), dim, weight_abs_max, _ptr(norms))
+    return bool(ok), norms
+
+
+def screen_row(x, codes, scales, norms, dim):
+    """(q, S) of screen_row for one screen row."""
+    x, scales, norms = _f32(x), _f32(scales), _f32(norms)
+    codes = np.ascontiguousarray(codes, dtype=np.int8)
+    q, s = ctypes.c_float(0), ctypes.c_float(0)
+    _lib.orc_screen_row(_ptr(x), _ptr(codes), _ptr(scales), _ptr(norms), dim, ctypes.byref(q), ctypes.byref(s))
+    return float(q.value), float(s.value)
+
+
+def screen_select(x, fp32, codes, scales, vocab, dim, weight_abs_max, kappa):
+    """ScreenedHead::select: (token or None for Fallback, candidates, upper [vocab])."""
+    x, fp32, scales = _f32(x), _f32(fp32), _f32(scales)
+    codes = np.ascontiguousarray(codes, dtype=np.int8)
+    upper = np.zeros(vocab, dtype=np.float32)
+    token, cand = ctypes.c_uint32(0), ctypes.c_uint32(0)
+    ok = _lib.orc_screen_select(_ptr(x), _ptr(fp32), _ptr(codes), _ptr(scales), vocab, dim, weight_abs_max, kappa,
+                                _ptr(upper), ctypes.byref(token), ctypes.byref(cand))
+    return (int(token.value) if ok else None), int(cand.value), upper

@@ -285,6 +285,43 @@ def bench_layer(torch, fh, gen, np, steps=64):
             "decode_gbs": round(step_bytes / (decode_ms * 1e-3 / steps) / 1e9, 1)}
 
 
+def bench_screen(torch, fh, gen, np, reps=50):
+    """The INT8 screened vocabulary head (65,536 x 768, FP32 head N(0, 0.02)):
+    one exact greedy selection per call (rows 1 and 5, synchronous, host wall
+    time) against the full FP32 head GEMV + argmax."""
+    vocab, dim = 65536, 768
+    head = gen.normal((vocab, dim), 0.02, 40)
+    screen = fh.ScreenedHead.build(head)
+    lin = fh.Linear.from_f32(head)
+    screen_bytes = vocab * (dim + 4 * (dim // 64))
+    res = {"vocab": vocab, "dim": dim, "screen_bytes": screen_bytes, "fp32_head_bytes": vocab * dim * 4}
+    for rows in (1, 5):
+        x = torch.from_numpy(gen.normal((rows, dim), 1.0, 41)).cuda()
+        out = torch.empty((rows, vocab), device="cuda")
+        for _ in range(3):
+            screen.select(x, rows, lin)
+        times = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            sel = screen.select(x, rows, lin)
+            times.append(time.perf_counter() - t0)
+        full = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            lin.linear(x, rows, out)
+            fh.argmax(out, rows, vocab)
+            full.append(time.perf_counter() - t0)
+        times.sort()
+        full.sort()
+        med, fmed = times[len(times) // 2], full[len(full) // 2]
+        res[f"rows{rows}"] = {"select_us": round(med * 1e6, 1), "full_head_us": round(fmed * 1e6, 1),
+                              "speedup": round(fmed / med, 2), "candidates": [c for _, c in sel],
+                              "screen_gbs": round(screen_bytes / med / 1e9, 1)}
+    screen.free()
+    lin.free()
+    return res
+
+
 def bench_copy(torch, reps):
     """A plain device copy of known size (calibrates rocprofv3 FETCH/WRITE_SIZE)."""
     n = 256 << 20
@@ -392,7 +429,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--ops", default="gemv,gemm,i16,attention,layer,copy")
+    ap.add_argument("--ops", default="gemv,gemm,i16,attention,layer,screen,copy")
     ap.add_argument("--reps", type=int, default=20, help="timed launches per secondary op")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
@@ -449,6 +486,9 @@ def main():
     if "layer" in ops:
         per_op["layer_int8_16k"] = bench_layer(torch, fh, gen, np)
         log(f"layer: {per_op['layer_int8_16k']}")
+    if "screen" in ops:
+        per_op["screened_head_65536x768"] = bench_screen(torch, fh, gen, np)
+        log(f"screened head: {per_op['screened_head_65536x768']}")
     if "copy" in ops:
         per_op["copy_256MiB"] = bench_copy(torch, 10)
     if not args.no_cpu and "prefill_f32" in per_op and "attention_prefill" in per_op:

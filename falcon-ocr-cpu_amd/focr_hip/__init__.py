@@ -74,6 +74,11 @@ SIGNATURES = {
     "focr_attention_prefill": (_I, [_P, _P, _P, _P, _P, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _P, _I, _I, _P]),
     "focr_attention_prefill_bf16": (_I, [_P, _P, _P, _P, _Z, _Z, _Z, _Z, _Z, _Z, _P, _I, _I, _P]),
     "focr_argmax": (_I, [_P, _P, _Z, _Z, _P]),
+    "focr_screen_build": (_I, [_P, _P, _Z, _Z, ctypes.POINTER(_P)]),
+    "focr_screen_upload": (_I, [_P, _P, _P, _Z, _Z, ctypes.c_float, ctypes.c_float, ctypes.POINTER(_P)]),
+    "focr_screen_free": (_I, [_P]),
+    "focr_screen_constants": (_I, [_P, _P, _P]),
+    "focr_screen_select": (_I, [_P, _P, _P, _P, _Z, _P, _P]),
     "focr_qkv_rows": (_I, [_P, _P, _Z, _P, _Z, _Z, _Z, _Z, _P, _P, _P, _P]),
     "focr_attention_decode": (_I, [_P, _P, _P, _P, _P, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _P, _P]),
 }
@@ -456,5 +461,68 @@ def argmax(logits, rows: int, vocab: int, ctx: Optional[Context] = None):
     tokens = (ctypes.c_uint32 * rows)()
     _check(lib().focr_argmax(ctx.handle, _dev(logits), rows, vocab, ctypes.cast(tokens, ctypes.c_void_p)))
     return list(tokens)
+
+
+SCREEN_LIMIT = 1024  # CANDIDATE_LIMIT (src/head_screen.rs:29)
+
+
+class ScreenedHead:
+    """`ScreenedHead` (src/head_screen.rs): an INT8 screen of the FP32
+    vocabulary head whose `select` returns the exact FP32 greedy token."""
+
+    def __init__(self, handle, vocab: int, dim: int, ctx: Context):
+        self.handle, self.vocab, self.dim, self.ctx = handle, vocab, dim, ctx
+
+    @classmethod
+    def build(cls, weights, ctx: Optional[Context] = None) -> "ScreenedHead":
+        """`ScreenedHead::build` from host FP32 weights [vocab][dim]."""
+        ctx = ctx or default_context()
+        w = np.ascontiguousarray(weights, dtype=np.float32)
+        vocab, dim = w.shape
+        handle = ctypes.c_void_p()
+        _check(lib().focr_screen_build(ctx.handle, w.ctypes.data_as(ctypes.c_void_p), vocab, dim, ctypes.byref(handle)))
+        return cls(handle, vocab, dim, ctx)
+
+    @classmethod
+    def from_parts(cls, codes, scales, weight_abs_max: float, kappa: float, ctx: Optional[Context] = None):
+        """`ScreenedHead::from_mapped`: a stored screen and its constants."""
+        ctx = ctx or default_context()
+        codes = np.ascontiguousarray(codes, dtype=np.int8)
+        scales = np.ascontiguousarray(scales, dtype=np.float32)
+        vocab, dim = codes.shape
+        handle = ctypes.c_void_p()
+        _check(lib().focr_screen_upload(ctx.handle, codes.ctypes.data_as(ctypes.c_void_p),
+                                        scales.ctypes.data_as(ctypes.c_void_p), vocab, dim, weight_abs_max, kappa,
+                                        ctypes.byref(handle)))
+        return cls(handle, vocab, dim, ctx)
+
+    def constants(self):
+        """(weight_abs_max, kappa)."""
+        wmax, kappa = ctypes.c_float(), ctypes.c_float()
+        _check(lib().focr_screen_constants(self.handle, ctypes.byref(wmax), ctypes.byref(kappa)))
+        return float(wmax.value), float(kappa.value)
+
+    def select(self, x, rows: int, head: "Linear"):
+        """`select_rows`: per input row, (token, candidates) for Screened::Token
+        or (None, candidates) for Screened::Fallback."""
+        if x.numel() != rows * self.dim:
+            raise FocrError(-2, "screened head input shape")
+        tokens = (ctypes.c_int32 * rows)()
+        cands = (ctypes.c_uint32 * rows)()
+        _check(lib().focr_screen_select(self.ctx.handle, self.handle, head.handle, _dev(x), rows,
+                                        ctypes.cast(tokens, ctypes.c_void_p), ctypes.cast(cands, ctypes.c_void_p)))
+        return [(None if t < 0 else int(t), int(c)) for t, c in zip(tokens, cands)]
+
+    def free(self) -> None:
+        if getattr(self, "handle", None):
+            _check(lib().focr_screen_free(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
 
 from .layer import DecoderLayer  # noqa: E402,F401

@@ -63,6 +63,7 @@ extern "C" {
 
 typedef struct focr_ctx focr_ctx;
 typedef struct focr_linear focr_linear;
+typedef struct focr_screen focr_screen;
 
 /* ---- context ------------------------------------------------------------ */
 /* No reference counterpart (the CPU runner needs no device state); the
@@ -232,6 +233,35 @@ int focr_attention_decode(focr_ctx *ctx, const float *q_dev, const float *prefix
  * logits_dev [rows][vocab]; tokens (host) [rows]. Synchronous. */
 int focr_argmax(focr_ctx *ctx, const float *logits_dev, size_t rows, size_t vocab,
                 uint32_t *tokens);
+
+/* ---- INT8 screened vocabulary head (src/head_screen.rs) ------------------ */
+/* ScreenedHead::build (src/head_screen.rs:84-118): quantizes the FP32 head
+ * weights_host [vocab][dim] into INT8 codes with one absmax/127 scale per 64
+ * channels (ties to even), verifies the bound's premises and uploads the
+ * screen. FOCR_E_SHAPE unless dim is a nonzero multiple of 64;
+ * FOCR_E_VALUE for a non-finite weight, a failed premise or dim whose bound
+ * constant reaches 0.53; FOCR_E_UNSUPPORTED for dim above 1024. */
+int focr_screen_build(focr_ctx *ctx, const float *weights_host, size_t vocab, size_t dim,
+                      focr_screen **out);
+/* ScreenedHead::from_mapped (src/head_screen.rs:122-145): a stored screen
+ * (host codes [vocab][dim], scales [vocab][dim/64] and its constants), as the
+ * packed model file holds it; the same checks on the constants. */
+int focr_screen_upload(focr_ctx *ctx, const int8_t *codes_host, const float *scales_host,
+                       size_t vocab, size_t dim, float weight_abs_max, float kappa,
+                       focr_screen **out);
+int focr_screen_free(focr_screen *screen);
+/* ScreenedHead::raw_parts' constants (src/head_screen.rs:148-151). */
+int focr_screen_constants(const focr_screen *screen, float *weight_abs_max, float *kappa);
+/* ScreenedHead::select / select_rows (src/head_screen.rs:169-199,274-324):
+ * the exact FP32 greedy token of each of rows (1..8) inputs x_dev
+ * [rows][dim]. tokens (host) [rows] receives the token, or -1 for
+ * Screened::Fallback (the caller then evaluates the full head, e.g.
+ * focr_linear_decode + focr_argmax); candidates (host) [rows] receives the
+ * variant's candidate count (1025 past the limit, 0 for the other
+ * fallbacks). fp32_head is the same head uploaded with focr_linear_upload
+ * (bits 32, no exception columns). Allocates nothing; synchronous. */
+int focr_screen_select(focr_ctx *ctx, const focr_screen *screen, const focr_linear *fp32_head,
+                       const float *x_dev, size_t rows, int32_t *tokens, uint32_t *candidates);
 
 #ifdef __cplusplus
 }

@@ -22,7 +22,8 @@ def test_header_declares_the_boundary():
     names = declared_functions()
     for required in ("focr_linear_upload", "focr_linear_decode", "focr_linear_decode_glu", "focr_linear_prefill",
                      "focr_linear_dequantize", "focr_row_scales", "focr_attention_prefill", "focr_argmax",
-                     "focr_linear_decode_ex", "focr_qkv_rows", "focr_attention_decode"):
+                     "focr_linear_decode_ex", "focr_qkv_rows", "focr_attention_decode", "focr_screen_build",
+                     "focr_screen_upload", "focr_screen_select", "focr_screen_free", "focr_screen_constants"):
         assert required in names
 
 
@@ -48,8 +49,13 @@ def test_null_arguments_are_errors_not_crashes():
     assert lib.focr_linear_decode_ex(None, None, None, 1, None, 0, 0, None) == -1
     assert lib.focr_qkv_rows(None, None, 1, None, 16, 8, 64, 0, None, None, None, None) == -1
     assert lib.focr_attention_decode(None, *([None] * 4), *([0] * 9), None, None) == -1
+    assert lib.focr_screen_build(None, None, 1, 64, None) == -1
+    assert lib.focr_screen_upload(None, None, None, 1, 64, 1.0, 0.5, None) == -1
+    assert lib.focr_screen_select(None, None, None, None, 1, None, None) == -1
+    assert lib.focr_screen_constants(None, None, None) == -1
     assert lib.focr_ctx_destroy(None) == 0
     assert lib.focr_linear_free(None) == 0
+    assert lib.focr_screen_free(None) == 0
 
 
 def test_missing_library_fails_loudly(tmp_path):

@@ -12,19 +12,19 @@
 // non-finite or huge input, or a non-finite candidate logit is a fallback
 // (the caller evaluates the full head).
 //
-// Three launches per call, all rows (at most 8) together:
-//  1. screen_kernel: 64 vocabulary rows per workgroup, 16 lanes per row (lane
-//     = 64-channel group, 64 codes in four 16-byte loads), every input scored
-//     against each row as it is loaded. The order is the reference's AVX2
+// Two launches per call, all rows (at most 8) together:
+//  1. screen_kernel: up to 768 workgroups stride over tiles of 16 vocabulary
+//     rows, 16 lanes per row (lane = 64-channel group, 64 codes in four
+//     16-byte loads, the next tile's issued before this one is scored), every
+//     input scored against each row as it is loaded. The order is the reference's AVX2
 //     screen_row (two 8-lane FMA chains per group, (a0 + a1) * s_g accumulated
 //     lane-wise over the groups, the AVX2 horizontal sum; S by one FMA chain),
 //     so q, S, the bounds and the candidate set are bit for bit the
 //     reference's. Writes q + B per row and the workgroup's largest q - B.
-//  2. candidates_kernel: tau from the workgroup maxima; rows with q + B >= tau
-//     are appended (atomic slot) to the row's candidate list.
-//  3. exact_kernel: one workgroup per input, its waves computing the
-//     candidates' FP32 logits in the reference dot order, picks the largest
-//     logit with the smallest index.
+//  2. select_kernel: one workgroup per input gathers the rows with
+//     q + B >= tau, computes their FP32 logits in the reference dot order
+//     and picks the largest logit with the smallest index, writing the
+//     result into mapped host memory.
 // HBM roofline: the screen reads vocab * (dim + 4 dim / 64) bytes once per
 // call (50.3 MB for 65,536 x 768), plus 4 dim bytes per candidate.
 #include <cmath>
@@ -40,23 +40,25 @@ constexpr int kGroup = 64;
 constexpr int kMaxGroups = 16;     // dim <= 1024: one lane per group, 16 lanes per row
 constexpr int kLimit = 1024;       // CANDIDATE_LIMIT
 constexpr int kMaxRows = 8;        // MAX_ROWS
-constexpr int kRowsPerBlock = 16;  // screen rows per workgroup (4 waves x 4)
+constexpr int kRowsPerBlock = 16;  // screen rows per tile (4 waves x 4)
+constexpr int kScreenBlocks = 768;  // screen workgroups (3 per compute unit at its register use)
 constexpr float kEta = 7.888609e-31f;  // 2^-100
 
 }  // namespace
 
 struct Screen {
-  size_t vocab = 0, dim = 0, groups = 0, blocks = 0;
+  size_t vocab = 0, dim = 0, groups = 0, blocks = 0, ustride = 0;
   float weight_abs_max = 0.0f, kappa = 0.0f;
   int8_t *codes = nullptr;   // [vocab][dim]
   float *scales = nullptr;   // [vocab][groups]
   // Per-call state for up to kMaxRows inputs, allocated with the screen so a
   // selection allocates nothing.
-  float *upper = nullptr;      // [rows][vocab]: q + B
+  float *upper = nullptr;      // [rows][ustride]: q + B
   float *block_max = nullptr;  // [rows][blocks]: largest q - B of each workgroup
-  uint32_t *words = nullptr;   // [rows][4]: candidate count, (unused), prepare flag, (unused)
-  uint32_t *cands = nullptr;   // [rows][kLimit]
-  int32_t *result = nullptr;   // [rows][2]: token (-1 = fallback), candidates
+  uint32_t *words = nullptr;   // [rows][4]: word 2 = prepare's verdict
+  // [rows][2] (token, -1 = fallback; candidates) in pinned, mapped host
+  // memory, written by the device through result_dev.
+  int32_t *host_result = nullptr, *result_dev = nullptr;
 };
 
 namespace {
@@ -67,9 +69,10 @@ struct ScreenArgs {
   const float *x;  // [rows][dim]
   const float *head;  // FP32 head [vocab][dim]
   float *upper, *block_max;
-  uint32_t *words, *cands;
+  uint32_t *words;
   int32_t *result;
   int vocab, dim, groups, rows, blocks;
+  int ustride;  // row stride of upper: vocab rounded up to a multiple of 4
   float weight_abs_max, kappa;
 };
 
@@ -125,31 +128,32 @@ __global__ __launch_bounds__(256) void screen_kernel(ScreenArgs a) {
       }
       if (ok && l1 * static_cast<double>(a.weight_abs_max) * 1.01 >= static_cast<double>(3.40282347e38f) / 2.0)
         ok = false;
-      a.words[4 * r + 0] = 0;
-      a.words[4 * r + 1] = 0;
       a.words[4 * r + 2] = ok ? 1u : 0u;
     }
     return;
   }
-  const int block = blockIdx.x - rows;
-
-  // This lane's 64 codes (group g of row v) and the group's scale: the loads
-  // go out first so their latency overlaps the staging below.
+  // Screen workgroup `block` takes tiles block, block + G, ... of 16 rows (4
+  // waves x 4 rows); the next tile's codes are loaded while this one is
+  // scored, and the staging of x and the norms happens once.
+  const int block = blockIdx.x - rows, nblocks = gridDim.x - rows;
+  const int tiles = (a.vocab + kRowsPerBlock - 1) / kRowsPerBlock;
   const int row_in_wave = lane >> 4, g = lane & 15;
-  const int v = block * kRowsPerBlock + wave * 4 + row_in_wave;
-  const bool live = v < a.vocab;
-  const bool active = live && g < groups;
   uint4 raw[4];
   float scale = 0.0f;
-  if (active) {
-    const uint4 *src = reinterpret_cast<const uint4 *>(a.codes + static_cast<size_t>(v) * dim + g * kGroup);
+  auto load_tile = [&](int tile) {
+    const int v = tile * kRowsPerBlock + wave * 4 + row_in_wave;
+    if (tile < tiles && v < a.vocab && g < groups) {
+      const uint4 *src = reinterpret_cast<const uint4 *>(a.codes + static_cast<size_t>(v) * dim + g * kGroup);
 #pragma unroll
-    for (int i = 0; i < 4; i++) raw[i] = src[i];
-    scale = a.scales[static_cast<size_t>(v) * groups + g];
-  } else {
+      for (int i = 0; i < 4; i++) raw[i] = src[i];
+      scale = a.scales[static_cast<size_t>(v) * groups + g];
+    } else {
 #pragma unroll
-    for (int i = 0; i < 4; i++) raw[i] = make_uint4(0, 0, 0, 0);
-  }
+      for (int i = 0; i < 4; i++) raw[i] = make_uint4(0, 0, 0, 0);
+      scale = 0.0f;
+    }
+  };
+  load_tile(block);
   for (int i = tid; i < rows * dim / 4; i += 256) {
     const int r = (4 * i) / dim, c = (4 * i) % dim;
     *reinterpret_cast<float4 *>(xs + r * xrow + (c / kGroup) * kXPitch + c % kGroup) =
@@ -157,114 +161,114 @@ __global__ __launch_bounds__(256) void screen_kernel(ScreenArgs a) {
   }
   __syncthreads();
   // prepare's per-group L1 norms: exact f64 sums in ascending order, rounded up.
+  // Groups past the last are zero (norm 0, scale 0, lane values 0): their
+  // steps fma(0, 0, acc) leave the chains unchanged (acc is never -0), so the
+  // chains below run a fixed 16 steps without branches.
   if (tid < rows * kMaxGroups) {
     const int r = tid / kMaxGroups, gg = tid % kMaxGroups;
+    float n = 0.0f;
     if (gg < groups) {
       double exact = 0.0;
 #pragma unroll 16
       for (int i = 0; i < kGroup; i++) exact += static_cast<double>(fabsf(xs[r * xrow + gg * kXPitch + i]));
       const float rounded = static_cast<float>(exact);
       // next_up of a finite rounded >= 0: the next bit pattern.
-      norms[r * kMaxGroups + gg] =
-          static_cast<double>(rounded) < exact ? __uint_as_float(__float_as_uint(rounded) + 1u) : rounded;
+      n = static_cast<double>(rounded) < exact ? __uint_as_float(__float_as_uint(rounded) + 1u) : rounded;
     }
-  }
-  sc[wave][row_in_wave][g] = scale;
-  // The codes as floats, once for every input.
-  float cf[kGroup];
-#pragma unroll
-  for (int i = 0; i < kGroup; i++) {
-    const uint32_t word = (&raw[i >> 4].x)[(i >> 2) & 3];
-    cf[i] = static_cast<float>(static_cast<int8_t>((word >> (8 * (i & 3))) & 0xffu));
+    norms[r * kMaxGroups + gg] = n;
   }
   __syncthreads();
+  float wave_lower[kMaxRows];
+#pragma unroll
+  for (int r = 0; r < kMaxRows; r++) wave_lower[r] = -__builtin_inff();
 
-  for (int r = 0; r < rows; r++) {
-    // screen_row's group step: a0 over x[base + j + p], a1 over
-    // x[base + j + 8 + p], j = 0, 16, 32, 48; then a0 + a1 per lane p.
-    if (active) {
-      const float4 *xg = reinterpret_cast<const float4 *>(xs + r * xrow + g * kXPitch);
-      float a0[8], a1[8];
+  for (int tile = block; tile < tiles; tile += nblocks) {
+    const int v = tile * kRowsPerBlock + wave * 4 + row_in_wave;
+    const bool live = v < a.vocab;
+    const bool active = live && g < groups;
+    // This tile's codes as floats (once for every input), then the next
+    // tile's loads go out.
+    float cf[kGroup];
 #pragma unroll
-      for (int p = 0; p < 8; p++) a0[p] = a1[p] = 0.0f;
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const float4 x0 = xg[4 * j], x1 = xg[4 * j + 1], x2 = xg[4 * j + 2], x3 = xg[4 * j + 3];
-        const float xa[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-        const float xb[8] = {x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
-#pragma unroll
-        for (int p = 0; p < 8; p++) {
-          a0[p] = __builtin_fmaf(xa[p], cf[16 * j + p], a0[p]);
-          a1[p] = __builtin_fmaf(xb[p], cf[16 * j + 8 + p], a1[p]);
-        }
-      }
-      float4 *dst = reinterpret_cast<float4 *>(u[wave][row_in_wave][g]);
-      dst[0] = make_float4(a0[0] + a1[0], a0[1] + a1[1], a0[2] + a1[2], a0[3] + a1[3]);
-      dst[1] = make_float4(a0[4] + a1[4], a0[5] + a1[5], a0[6] + a1[6], a0[7] + a1[7]);
+    for (int i = 0; i < kGroup; i++) {
+      const uint32_t word = (&raw[i >> 4].x)[(i >> 2) & 3];
+      cf[i] = static_cast<float>(static_cast<int8_t>((word >> (8 * (i & 3))) & 0xffu));
     }
-    __syncthreads();
-    float lower = -__builtin_inff();
-    if (live && g < 8) {
-      // Lane p accumulates row[p] = fma(a0 + a1, s_g, row[p]) over the
-      // groups; S = sum fma(s_g, n_g, S) alongside.
-      const int p = g;
-      float uu[kMaxGroups], ss[kMaxGroups];
+    sc[wave][row_in_wave][g] = scale;
+    load_tile(tile + nblocks);
+
+    for (int r = 0; r < rows; r++) {
+      // screen_row's group step: a0 over x[base + j + p], a1 over
+      // x[base + j + 8 + p], j = 0, 16, 32, 48; then a0 + a1 per lane p.
+      float4 *dst = reinterpret_cast<float4 *>(u[wave][row_in_wave][g]);
+      if (!active) {
+        dst[0] = dst[1] = make_float4(0.f, 0.f, 0.f, 0.f);
+      } else {
+        const float4 *xg = reinterpret_cast<const float4 *>(xs + r * xrow + g * kXPitch);
+        float a0[8], a1[8];
 #pragma unroll
-      for (int gg = 0; gg < kMaxGroups; gg++) {
-        uu[gg] = u[wave][row_in_wave][gg][p];
-        ss[gg] = sc[wave][row_in_wave][gg];
+        for (int p = 0; p < 8; p++) a0[p] = a1[p] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const float4 x0 = xg[4 * j], x1 = xg[4 * j + 1], x2 = xg[4 * j + 2], x3 = xg[4 * j + 3];
+          const float xa[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+          const float xb[8] = {x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
+#pragma unroll
+          for (int p = 0; p < 8; p++) {
+            a0[p] = __builtin_fmaf(xa[p], cf[16 * j + p], a0[p]);
+            a1[p] = __builtin_fmaf(xb[p], cf[16 * j + 8 + p], a1[p]);
+          }
+        }
+        dst[0] = make_float4(a0[0] + a1[0], a0[1] + a1[1], a0[2] + a1[2], a0[3] + a1[3]);
+        dst[1] = make_float4(a0[4] + a1[4], a0[5] + a1[5], a0[6] + a1[6], a0[7] + a1[7]);
       }
-      float acc = 0.0f, total = 0.0f;
+      // The row's 16 lanes exchange through this wave's own LDS slice.
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      if (live && g < 8) {
+        // Lane p accumulates row[p] = fma(a0 + a1, s_g, row[p]) over the
+        // groups; S = sum fma(s_g, n_g, S) alongside.
+        const int p = g;
+        float uu[kMaxGroups], ss[kMaxGroups];
 #pragma unroll
-      for (int gg = 0; gg < kMaxGroups; gg++)
-        if (gg < groups) {
+        for (int gg = 0; gg < kMaxGroups; gg++) {
+          uu[gg] = u[wave][row_in_wave][gg][p];
+          ss[gg] = sc[wave][row_in_wave][gg];
+        }
+        float acc = 0.0f, total = 0.0f;
+#pragma unroll
+        for (int gg = 0; gg < kMaxGroups; gg++) {
           acc = __builtin_fmaf(uu[gg], ss[gg], acc);
           total = __builtin_fmaf(ss[gg], norms[r * kMaxGroups + gg], total);
         }
-      const float q = sum8_lanes(acc, p);
-      const float bound = __builtin_fmaf(a.kappa, total, kEta);
-      if (p == 0) {
-        a.upper[static_cast<size_t>(r) * a.vocab + v] = q + bound;
-        lower = q - bound;
+        const float q = sum8_lanes(acc, p);
+        const float bound = __builtin_fmaf(a.kappa, total, kEta);
+        if (p == 0) {
+          a.upper[static_cast<size_t>(r) * a.ustride + v] = q + bound;
+          // f32::max: a NaN operand is ignored.
+          wave_lower[r] = __builtin_fmaxf(wave_lower[r], q - bound);
+        }
       }
+      // The next input's products overwrite this slice only after every lane
+      // has read it.
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
-    // The workgroup's largest q - B (f32::max: a NaN operand is ignored).
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) lower = __builtin_fmaxf(lower, __shfl_xor(lower, off));
-    if (lane == 0) wmax[r * 4 + wave] = lower;
-    __syncthreads();
   }
+  // The workgroup's largest q - B per input.
+  for (int r = 0; r < rows; r++) {
+    float m = wave_lower[r];
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, off));
+    if (lane == 0) wmax[r * 4 + wave] = m;
+  }
+  __syncthreads();
   if (tid < rows) {
     float m = -__builtin_inff();
     for (int w = 0; w < 4; w++) m = __builtin_fmaxf(m, wmax[tid * 4 + w]);
     a.block_max[static_cast<size_t>(tid) * a.blocks + block] = m;
-  }
-}
-
-__global__ __launch_bounds__(1024) void candidates_kernel(ScreenArgs a) {
-  __shared__ float red[16];
-  const int r = blockIdx.y, tid = threadIdx.x;
-  float m = -__builtin_inff();
-  for (int b = tid; b < a.blocks; b += 1024) m = __builtin_fmaxf(m, a.block_max[static_cast<size_t>(r) * a.blocks + b]);
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, off));
-  if ((tid & 63) == 0) red[tid >> 6] = m;
-  __syncthreads();
-  float tau = -__builtin_inff();
-  for (int w = 0; w < 16; w++) tau = __builtin_fmaxf(tau, red[w]);
-  if (!__builtin_isfinite(tau)) return;  // the selection falls back
-  const int v = blockIdx.x * 1024 + tid;
-  const bool hit = v < a.vocab && a.upper[static_cast<size_t>(r) * a.vocab + v] >= tau;
-  // One counter update per wave: the wave's hits take consecutive slots.
-  const uint64_t hits = __ballot(hit);
-  if (hits == 0) return;
-  const int lane = tid & 63;
-  uint32_t base = 0;
-  if (lane == __builtin_ctzll(hits)) base = atomicAdd(&a.words[4 * r], static_cast<uint32_t>(__builtin_popcountll(hits)));
-  base = __shfl(base, __builtin_ctzll(hits));
-  if (hit) {
-    const uint32_t slot = base + static_cast<uint32_t>(__builtin_popcountll(hits & ((uint64_t(1) << lane) - 1)));
-    if (slot < static_cast<uint32_t>(kLimit)) a.cands[static_cast<size_t>(r) * kLimit + slot] = static_cast<uint32_t>(v);
   }
 }
 
@@ -297,24 +301,77 @@ __device__ float reference_dot(const float *x, const float *w, int len, int lane
   return total;
 }
 
-// One workgroup per input: wave w computes candidates w, w + 16, ... and
-// keeps the largest logit with the smallest row; the workgroup combines the
-// waves. The reference visits candidates in ascending order with a strict >,
-// i.e. the first index of the maximum; a non-finite logit falls back.
-__global__ __launch_bounds__(1024) void exact_kernel(ScreenArgs a) {
+// One workgroup per input: tau = the largest q - B (from the screen's
+// workgroup maxima); the rows with q + B >= tau are gathered into an LDS list
+// (one slot counter update per wave); then wave w computes the FP32 logits of
+// list entries w, w + 16, ... and keeps the largest with the smallest row, and
+// the workgroup combines the waves. The reference visits candidates in
+// ascending order with a strict >, i.e. the first index of the maximum; more
+// than kLimit candidates, a non-finite tau or a non-finite logit fall back.
+__global__ __launch_bounds__(1024) void select_kernel(ScreenArgs a) {
+  __shared__ float red[16];
+  __shared__ uint32_t list[kLimit];
+  __shared__ uint32_t count_s;
   __shared__ float best_v[16];
   __shared__ uint32_t best_i[16];
   __shared__ int bad[16];
   const int r = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const uint32_t count = a.words[4 * r];
-  const uint32_t ok = a.words[4 * r + 2];
+  float m = -__builtin_inff();
+  for (int b = tid; b < a.blocks; b += 1024) m = __builtin_fmaxf(m, a.block_max[static_cast<size_t>(r) * a.blocks + b]);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, off));
+  if (lane == 0) red[wave] = m;
+  if (tid == 0) count_s = 0;
+  __syncthreads();
+  float tau = -__builtin_inff();
+  for (int w = 0; w < 16; w++) tau = __builtin_fmaxf(tau, red[w]);
+  const bool ok = a.words[4 * r + 2] != 0 && __builtin_isfinite(tau);
+  if (ok) {
+    const float *upper = a.upper + static_cast<size_t>(r) * a.ustride;
+    // Chunks of 64 Ki rows: every thread's 16 float4 loads go out first.
+    for (int base = 0; base < a.vocab; base += 16 * 4096) {
+      float4 val[16];
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        const int v0 = base + 4 * (1024 * i + tid);
+        if (v0 + 3 < a.vocab) {
+          val[i] = *reinterpret_cast<const float4 *>(upper + v0);
+        } else {
+          float t[4];
+#pragma unroll
+          for (int e = 0; e < 4; e++) t[e] = v0 + e < a.vocab ? upper[v0 + e] : -__builtin_inff();
+          val[i] = make_float4(t[0], t[1], t[2], t[3]);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 16; i++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const int v = base + 4 * (1024 * i + tid) + e;
+          const bool hit = v < a.vocab && (&val[i].x)[e] >= tau;
+          const uint64_t hits = __ballot(hit);
+          if (hits == 0) continue;
+          const int first = __builtin_ctzll(hits);
+          uint32_t slot0 = 0;
+          if (lane == first) slot0 = atomicAdd(&count_s, static_cast<uint32_t>(__builtin_popcountll(hits)));
+          slot0 = __shfl(slot0, first);
+          if (hit) {
+            const uint32_t slot =
+                slot0 + static_cast<uint32_t>(__builtin_popcountll(hits & ((uint64_t(1) << lane) - 1)));
+            if (slot < static_cast<uint32_t>(kLimit)) list[slot] = static_cast<uint32_t>(v);
+          }
+        }
+    }
+  }
+  __syncthreads();
+  const uint32_t count = count_s;
   const bool run = ok && count <= static_cast<uint32_t>(kLimit);
   float bv = -__builtin_inff();
   uint32_t bi = 0xffffffffu;
   int nonfinite = 0;
   if (run)
     for (uint32_t c = wave; c < count; c += 16) {
-      const uint32_t row = a.cands[static_cast<size_t>(r) * kLimit + c];
+      const uint32_t row = list[c];
       const float l =
           reference_dot(a.x + static_cast<size_t>(r) * a.dim, a.head + static_cast<size_t>(row) * a.dim, a.dim, lane);
       if (!__builtin_isfinite(l)) nonfinite = 1;
@@ -331,7 +388,7 @@ __global__ __launch_bounds__(1024) void exact_kernel(ScreenArgs a) {
   __syncthreads();
   if (tid != 0) return;
   int32_t token = -1, reported = 0;
-  if (count > static_cast<uint32_t>(kLimit)) {
+  if (ok && count > static_cast<uint32_t>(kLimit)) {
     reported = kLimit + 1;
   } else if (run && count > 0) {
     float fv = -__builtin_inff();
@@ -404,9 +461,10 @@ float screen_kappa(size_t dim) {
 }
 
 void free_screen(Screen *s) {
-  void *ptrs[] = {s->codes, s->scales, s->upper, s->block_max, s->words, s->cands, s->result};
+  void *ptrs[] = {s->codes, s->scales, s->upper, s->block_max, s->words};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
+  if (s->host_result) (void)hipHostFree(s->host_result);
 }
 
 int create_screen(Ctx *ctx, const int8_t *codes, const float *scales, size_t vocab, size_t dim, float wmax,
@@ -416,18 +474,22 @@ int create_screen(Ctx *ctx, const int8_t *codes, const float *scales, size_t voc
   s->vocab = vocab;
   s->dim = dim;
   s->groups = dim / kGroup;
-  s->blocks = (vocab + kRowsPerBlock - 1) / kRowsPerBlock;
+  const size_t tiles = (vocab + kRowsPerBlock - 1) / kRowsPerBlock;
+  s->blocks = tiles < static_cast<size_t>(kScreenBlocks) ? tiles : static_cast<size_t>(kScreenBlocks);
   s->weight_abs_max = wmax;
   s->kappa = kappa;
   auto alloc = [&](void **p, size_t bytes) { return hipMalloc(p, bytes); };
   hipError_t e = hipSuccess;
   if (e == hipSuccess) e = alloc(reinterpret_cast<void **>(&s->codes), vocab * dim);
   if (e == hipSuccess) e = alloc(reinterpret_cast<void **>(&s->scales), vocab * s->groups * sizeof(float));
-  if (e == hipSuccess) e = alloc(reinterpret_cast<void **>(&s->upper), kMaxRows * vocab * sizeof(float));
+  s->ustride = (vocab + 3) / 4 * 4;
+  if (e == hipSuccess) e = alloc(reinterpret_cast<void **>(&s->upper), kMaxRows * s->ustride * sizeof(float));
   if (e == hipSuccess) e = alloc(reinterpret_cast<void **>(&s->block_max), kMaxRows * s->blocks * sizeof(float));
   if (e == hipSuccess) e = alloc(reinterpret_cast<void **>(&s->words), kMaxRows * 4 * sizeof(uint32_t));
-  if (e == hipSuccess) e = alloc(reinterpret_cast<void **>(&s->cands), kMaxRows * kLimit * sizeof(uint32_t));
-  if (e == hipSuccess) e = alloc(reinterpret_cast<void **>(&s->result), kMaxRows * 2 * sizeof(int32_t));
+  if (e == hipSuccess)
+    e = hipHostMalloc(reinterpret_cast<void **>(&s->host_result), kMaxRows * 2 * sizeof(int32_t),
+                      hipHostMallocMapped | hipHostMallocCoherent);
+  if (e == hipSuccess) e = hipHostGetDevicePointer(reinterpret_cast<void **>(&s->result_dev), s->host_result, 0);
   if (e == hipSuccess) e = hipMemcpy(s->codes, codes, vocab * dim, hipMemcpyHostToDevice);
   if (e == hipSuccess) e = hipMemcpy(s->scales, scales, vocab * s->groups * sizeof(float), hipMemcpyHostToDevice);
   if (e != hipSuccess) {
@@ -518,23 +580,22 @@ int focr_screen_select(focr_ctx *handle, const focr_screen *sh, const focr_linea
   a.upper = s->upper;
   a.block_max = s->block_max;
   a.words = s->words;
-  a.cands = s->cands;
-  a.result = s->result;
+  a.result = s->result_dev;
   a.vocab = static_cast<int>(s->vocab);
   a.dim = static_cast<int>(s->dim);
   a.groups = static_cast<int>(s->groups);
   a.rows = static_cast<int>(rows);
   a.blocks = static_cast<int>(s->blocks);
+  a.ustride = static_cast<int>(s->ustride);
   a.weight_abs_max = s->weight_abs_max;
   a.kappa = s->kappa;
   hipLaunchKernelGGL(screen_kernel, dim3(a.blocks + a.rows), dim3(256), screen_lds_bytes(a.rows, a.dim), ctx->stream,
                      a);
-  hipLaunchKernelGGL(candidates_kernel, dim3((a.vocab + 1023) / 1024, a.rows), dim3(1024), 0, ctx->stream, a);
-  hipLaunchKernelGGL(exact_kernel, dim3(a.rows), dim3(1024), 0, ctx->stream, a);
+  hipLaunchKernelGGL(select_kernel, dim3(a.rows), dim3(1024), 0, ctx->stream, a);
   FOCR_HIP_CHECK(hipGetLastError());
-  int32_t result[2 * kMaxRows];
-  FOCR_HIP_CHECK(hipMemcpyAsync(result, s->result, rows * 2 * sizeof(int32_t), hipMemcpyDeviceToHost, ctx->stream));
+  // select_kernel wrote the results straight into the mapped host buffer.
   FOCR_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+  const volatile int32_t *result = s->host_result;
   for (size_t r = 0; r < rows; r++) {
     tokens[r] = result[2 * r];
     candidates[r] = static_cast<uint32_t>(result[2 * r + 1]);

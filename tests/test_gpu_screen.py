@@ -131,3 +131,20 @@ def test_vocabulary_head_at_checkpoint_size(fh):
         assert got[r] == oracle_select(xs[r], head, parts), r
         assert got[r][0] == full[r], r
     assert got[3][0] == 12345
+
+
+def test_odd_vocabulary_and_narrow_head(fh):
+    # A vocabulary that is no multiple of the 16-row tiles or of 4, dim 128.
+    vocab, dim = 1001, 128
+    rng = np.random.default_rng(5)
+    head = rng.normal(0, 0.05, (vocab, dim)).astype(np.float32)
+    head[1000] = head[999]
+    parts = oracle.screen_build(head, vocab, dim)
+    screen = fh.ScreenedHead.build(head)
+    lin = fh.Linear.from_f32(head)
+    xs = rng.normal(0, 1, (3, dim)).astype(np.float32)
+    xs[1] = head[999] * F32(30.0)
+    got = screen.select(to_dev(xs), 3, lin)
+    for r in range(3):
+        assert got[r] == oracle_select(xs[r], head, parts), r
+    assert got[1][0] == 999

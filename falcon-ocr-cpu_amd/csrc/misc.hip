@@ -123,44 +123,94 @@ __global__ __launch_bounds__(256) void row_scales_fixed_kernel(const float *__re
 }
 
 // argmax (src/runner/mod.rs:916-930): first index of the maximum, and a flag
-// when any value is non-finite. One workgroup per row.
-__global__ __launch_bounds__(256) void argmax_kernel(const float *__restrict__ logits, int vocab,
-                                                     uint32_t *__restrict__ result) {
+// when any value is non-finite. One workgroup of 1024 threads per row; each
+// thread keeps the first maximum of its own values (visited in ascending
+// index order), and the workgroup combines (value, index) pairs, the smaller
+// index winning ties. Every thread issues its loads of a pass (8 float4, or 8
+// floats for rows that are not 16-byte aligned) before comparing them.
+__global__ __launch_bounds__(1024) void argmax_kernel(const float *__restrict__ logits, int vocab,
+                                                      uint32_t *__restrict__ result) {
   const float *row = logits + static_cast<size_t>(blockIdx.x) * vocab;
+  const int tid = threadIdx.x;
   float best = -__builtin_inff();
   int best_i = -1;
   int nonfinite = 0;
-  for (int i = threadIdx.x; i < vocab; i += blockDim.x) {
-    const float v = row[i];
+  auto visit = [&](float v, int i) {
     nonfinite |= !__builtin_isfinite(v);
     if (best_i < 0 || v > best) {
       best = v;
       best_i = i;
     }
-  }
-  __shared__ float s_val[256];
-  __shared__ int s_idx[256];
-  __shared__ int s_bad[256];
-  s_val[threadIdx.x] = best;
-  s_idx[threadIdx.x] = best_i;
-  s_bad[threadIdx.x] = nonfinite;
-  __syncthreads();
-  for (int stride = 128; stride > 0; stride /= 2) {
-    if (threadIdx.x < stride) {
-      const int o = threadIdx.x + stride;
-      const float a = s_val[threadIdx.x], b = s_val[o];
-      const int ia = s_idx[threadIdx.x], ib = s_idx[o];
-      if (ib >= 0 && (ia < 0 || b > a || (b == a && ib < ia))) {
-        s_val[threadIdx.x] = b;
-        s_idx[threadIdx.x] = ib;
+  };
+  const bool vec = (reinterpret_cast<uintptr_t>(row) & 15) == 0;
+  if (vec) {
+    const int quads = vocab / 4;
+    for (int base = 0; base < quads; base += 8 * 1024) {
+      float4 q[8];
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const int at = base + 1024 * j + tid;
+        q[j] = at < quads ? reinterpret_cast<const float4 *>(row)[at] : make_float4(0.f, 0.f, 0.f, 0.f);
       }
-      s_bad[threadIdx.x] |= s_bad[o];
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const int at = base + 1024 * j + tid;
+        if (at < quads) {
+          visit(q[j].x, 4 * at);
+          visit(q[j].y, 4 * at + 1);
+          visit(q[j].z, 4 * at + 2);
+          visit(q[j].w, 4 * at + 3);
+        }
+      }
     }
-    __syncthreads();
+    for (int i = 4 * quads + tid; i < vocab; i += 1024) visit(row[i], i);
+  } else {
+    for (int base = 0; base < vocab; base += 8 * 1024) {
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const int at = base + 1024 * j + tid;
+        v[j] = at < vocab ? row[at] : 0.0f;
+      }
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const int at = base + 1024 * j + tid;
+        if (at < vocab) visit(v[j], at);
+      }
+    }
   }
-  if (threadIdx.x == 0) {
-    result[2 * blockIdx.x] = static_cast<uint32_t>(s_idx[0]);
-    result[2 * blockIdx.x + 1] = static_cast<uint32_t>(s_bad[0]);
+  // Wave, then workgroup combination.
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float ov = __shfl_xor(best, off);
+    const int oi = __shfl_xor(best_i, off);
+    if (oi >= 0 && (best_i < 0 || ov > best || (ov == best && oi < best_i))) {
+      best = ov;
+      best_i = oi;
+    }
+    nonfinite |= __shfl_xor(nonfinite, off);
+  }
+  __shared__ float s_val[16];
+  __shared__ int s_idx[16];
+  __shared__ int s_bad[16];
+  if ((tid & 63) == 0) {
+    s_val[tid >> 6] = best;
+    s_idx[tid >> 6] = best_i;
+    s_bad[tid >> 6] = nonfinite;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float fv = s_val[0];
+    int fi = s_idx[0], bad = s_bad[0];
+    for (int w = 1; w < 16; w++) {
+      bad |= s_bad[w];
+      if (s_idx[w] >= 0 && (fi < 0 || s_val[w] > fv || (s_val[w] == fv && s_idx[w] < fi))) {
+        fv = s_val[w];
+        fi = s_idx[w];
+      }
+    }
+    result[2 * blockIdx.x] = static_cast<uint32_t>(fi);
+    result[2 * blockIdx.x + 1] = static_cast<uint32_t>(bad);
   }
 }
 
@@ -210,7 +260,7 @@ int launch_row_scales(Ctx *ctx, const float *h, size_t rows, size_t width, float
 
 int launch_argmax(Ctx *ctx, const float *logits, size_t rows, size_t vocab, uint32_t *result_dev) {
   FOCR_REQUIRE(rows < (size_t(1) << 31), FOCR_E_SHAPE, "focr_argmax: too many rows");
-  hipLaunchKernelGGL(argmax_kernel, dim3(static_cast<unsigned>(rows)), dim3(256), 0, ctx->stream, logits,
+  hipLaunchKernelGGL(argmax_kernel, dim3(static_cast<unsigned>(rows)), dim3(1024), 0, ctx->stream, logits,
                      static_cast<int>(vocab), result_dev);
   FOCR_HIP_CHECK(hipGetLastError());
   return FOCR_OK;

@@ -47,3 +47,19 @@ def test_argmax(fh):
     logits[4, 12345] = np.inf
     with pytest.raises(fh.FocrError):
         fh.argmax(to_dev(logits), 5, vocab)
+
+
+def test_argmax_unaligned_rows_and_ties(fh):
+    # vocab 1001: rows after the first are not 16-byte aligned; ties inside one
+    # thread's values, across threads and across waves; an all-equal row.
+    vocab = 1001
+    logits = gen.normal((4, vocab), 1.0, 32)
+    logits[0, 5] = logits[0, 5 + 4096 % vocab] = logits[0, 900] = np.float32(9.0)
+    logits[1, 1000] = logits[1, 999] = np.float32(9.0)
+    logits[2, :] = np.float32(-3.5)
+    logits[3, 64] = logits[3, 63] = np.float32(7.0)
+    got = fh.argmax(to_dev(logits), 4, vocab)
+    assert got == [oracle.argmax(row) for row in logits] == [5, 999, 0, 63]
+    big = gen.normal((2, 70001), 1.0, 33)
+    big[1, 65537] = big[1, 70000] = np.float32(40.0)
+    assert fh.argmax(to_dev(big), 2, 70001) == [oracle.argmax(r) for r in big]

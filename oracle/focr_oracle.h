@@ -177,6 +177,24 @@ int orc_screen_select(const float *x, const float *fp32, const int8_t *codes, co
                       size_t vocab, size_t dim, float weight_abs_max, float kappa, float *upper,
                       uint32_t *token, uint32_t *candidates);
 
+/* ---- Sealed split KV cache, Kv::Q8 / Kv::Q16 (src/quant/kv.rs) ------------ */
+uint16_t orc_bf16_up(float scale);
+float orc_bf16_f32(uint16_t bits);
+/* SplitPrefix::seal: records [n_kv][P][160] codes (int8 for bits 8, int16
+ * for 16) and BF16 steps [n_kv][P][5]. 0 ok; -1 temporal keys differ inside
+ * a pair; -2 non-finite value; -3 decoded overflow; -4 shape. */
+int orc_kv_seal(int bits, const float *prefix_k, const float *v, size_t prefix_len, size_t n_heads,
+                size_t n_kv, void *codes, uint16_t *scales);
+/* push_unique: generated position `index` of a [n_kv][capacity] tail; keys
+ * and values [n_kv][64]; tail records [128] codes and 4 steps. */
+void orc_kv_push(int bits, const float *k, const float *v, size_t n_kv, size_t capacity, size_t index,
+                 void *codes, uint16_t *scales);
+/* The decoded cache in the compact layout: prefix keys [P][n_heads][64],
+ * values [P + tail_len][n_kv][64], generated keys [tail_len][n_kv][64]. */
+void orc_kv_dequantize(int bits, const void *codes, const uint16_t *scales, size_t prefix_len, size_t n_heads,
+                       size_t n_kv, const void *tail_codes, const uint16_t *tail_scales, size_t capacity,
+                       size_t tail_len, float *prefix_k, float *values, float *generated_k);
+
 /* Threads the oracle uses for its parallel loops (1 = scalar). */
 void orc_set_threads(int threads);
 int orc_get_threads(void);

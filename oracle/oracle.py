@@ -85,6 +85,11 @@ _sig("orc_screen_build", _I, _P, _Z, _Z, _P, _P, _P, _P)
 _sig("orc_screen_prepare", _I, _P, _Z, _F, _P)
 _sig("orc_screen_row", None, _P, _P, _P, _P, _Z, _P, _P)
 _sig("orc_screen_select", _I, _P, _P, _P, _P, _Z, _Z, _F, _F, _P, _P, _P)
+_sig("orc_bf16_up", ctypes.c_uint16, _F)
+_sig("orc_bf16_f32", _F, ctypes.c_uint16)
+_sig("orc_kv_seal", _I, _I, _P, _P, _Z, _Z, _Z, _P, _P)
+_sig("orc_kv_push", None, _I, _P, _P, _Z, _Z, _Z, _P, _P)
+_sig("orc_kv_dequantize", None, _I, _P, _P, _Z, _Z, _Z, _P, _P, _Z, _Z, _P, _P, _P)
 _sig("orc_qkv_rows", None, _P, _Z, _P, _Z, _Z, _Z, _P, _P, _P, _P)
 _sig("orc_attention_decode", None, _P, _P, _P, _P, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _P, _P)
 _sig("orc_set_threads", None, _I)
@@ -407,3 +412,48 @@ def screen_select(x, fp32, codes, scales, vocab, dim, weight_abs_max, kappa):
     ok = _lib.orc_screen_select(_ptr(x), _ptr(fp32), _ptr(codes), _ptr(scales), vocab, dim, weight_abs_max, kappa,
                                 _ptr(upper), ctypes.byref(token), ctypes.byref(cand))
     return (int(token.value) if ok else None), int(cand.value), upper
+
+
+# ---- Sealed split KV cache, Kv::Q8 / Kv::Q16 (src/quant/kv.rs) -------------
+def bf16_up(scale: float) -> int:
+    return int(_lib.orc_bf16_up(scale))
+
+
+def bf16_f32(bits: int) -> float:
+    return float(_lib.orc_bf16_f32(bits))
+
+
+def kv_seal(bits, prefix_k, v, prefix_len, n_heads, n_kv):
+    """SplitPrefix::seal: (codes [n_kv][P][160], steps [n_kv][P][5] as uint16)
+    or the error code (-1 pair, -2 non-finite, -3 overflow, -4 shape)."""
+    prefix_k, v = _f32(prefix_k), _f32(v)
+    codes = np.zeros((n_kv, prefix_len, 160), dtype=np.int8 if bits == 8 else np.int16)
+    scales = np.zeros((n_kv, prefix_len, 5), dtype=np.uint16)
+    rc = _lib.orc_kv_seal(bits, _ptr(prefix_k), _ptr(v), prefix_len, n_heads, n_kv, _ptr(codes), _ptr(scales))
+    return rc if rc != 0 else (codes, scales)
+
+
+def kv_tail(bits, n_kv, capacity):
+    """An empty tail: (codes [n_kv][capacity][128], steps [n_kv][capacity][4])."""
+    return (np.zeros((n_kv, capacity, 128), dtype=np.int8 if bits == 8 else np.int16),
+            np.zeros((n_kv, capacity, 4), dtype=np.uint16))
+
+
+def kv_push(bits, k, v, n_kv, capacity, index, tail):
+    """push_unique of one generated position (keys, values [n_kv][64]) into `tail`."""
+    k, v = _f32(k), _f32(v)
+    codes, scales = tail
+    _lib.orc_kv_push(bits, _ptr(k), _ptr(v), n_kv, capacity, index, _ptr(codes), _ptr(scales))
+
+
+def kv_dequantize(bits, sealed, prefix_len, n_heads, n_kv, tail, capacity, tail_len):
+    """(prefix_k [P][n_heads][64], values [P + tail_len][n_kv][64],
+    generated_k [tail_len][n_kv][64]) decoded from the records."""
+    codes, scales = sealed
+    tcodes, tscales = tail
+    pk = np.zeros((prefix_len, n_heads, 64), dtype=np.float32)
+    vals = np.zeros((prefix_len + tail_len, n_kv, 64), dtype=np.float32)
+    gk = np.zeros((max(tail_len, 1), n_kv, 64), dtype=np.float32)
+    _lib.orc_kv_dequantize(bits, _ptr(codes), _ptr(scales), prefix_len, n_heads, n_kv, _ptr(tcodes), _ptr(tscales),
+                           capacity, tail_len, _ptr(pk), _ptr(vals), _ptr(gk))
+    return pk, vals, gk[:tail_len]

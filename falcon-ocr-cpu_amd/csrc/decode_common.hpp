@@ -1,0 +1,126 @@
+// Pieces shared by the decode attention kernels (compact cache and sealed
+// split records): lane reductions, the online-softmax state merge and the
+// kernel that combines the split-K partial states of every (row, head).
+#pragma once
+
+#include "focr_internal.hpp"
+
+namespace focr {
+namespace decode {
+
+constexpr int kWaves = 4;  // waves per workgroup
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over the 16 lanes of a DPP row; every lane of the row gets the same
+// value (each step adds a value and its mirror image, so partners agree).
+__device__ __forceinline__ float row_sum16(float v) {
+  v = v + dpp<0xB1>(v);   // quad_perm [1,0,3,2]
+  v = v + dpp<0x4E>(v);   // quad_perm [2,3,0,1]
+  v = v + dpp<0x141>(v);  // row_half_mirror
+  return v + dpp<0x140>(v);  // row_mirror
+}
+
+__device__ __forceinline__ float xor_lane(float x, int mask) {
+  const int lane = threadIdx.x & 63;
+  return __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, __float_as_int(x)));
+}
+
+__device__ __forceinline__ float4 ld4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
+
+// Merge two online-softmax states (max m, denominator d, output o); both
+// partners compute the same bits (products identical, sums commutative).
+__device__ __forceinline__ void merge(float &m, float &d, float4 &o, float m2, float d2, float4 o2) {
+  const float mn = m > m2 ? m : m2;
+  if (mn == -__builtin_inff()) return;  // both empty
+  const float f1 = m == -__builtin_inff() ? 0.0f : expf_acc(m - mn);
+  const float f2 = m2 == -__builtin_inff() ? 0.0f : expf_acc(m2 - mn);
+  d = d * f1 + d2 * f2;
+  o = make_float4(o.x * f1 + o2.x * f2, o.y * f1 + o2.y * f2, o.z * f1 + o2.z * f2, o.w * f1 + o2.w * f2);
+  m = mn;
+}
+
+struct CombineArgs {
+  const float *part_o, *part_md, *sinks;
+  float *out;
+  int n_heads, chunks;
+};
+
+constexpr int kMaxChunks = 1024;
+
+// Sum over a wave in a fixed order (every lane gets the same value).
+__device__ __forceinline__ float wave_sum(float v) {
+  v = row_sum16(v);
+  v = v + xor_lane(v, 16);
+  return v + xor_lane(v, 32);
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int mask = 1; mask < 64; mask *= 2) {
+    const float o = xor_lane(v, mask);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+// One workgroup per (row, head). Thread t takes chunks t, t + 256, ... for
+// the maximum and the weights exp(m_c - M); then lane = dim and wave w sums
+// the outputs of chunks w, w + 4, ...; the partial sums are added in a fixed
+// order. Final step as online.rs head (lines 144-149):
+// lse = max + ln(den), out = (o / den) * 1/(1 + exp(sink - lse)).
+static __global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgs a) {
+  __shared__ float s_f[kMaxChunks];
+  __shared__ float s_red[kWaves], s_o[kWaves][64];
+  const int rh = blockIdx.x, h = rh % a.n_heads;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const float *md = a.part_md + static_cast<size_t>(rh) * a.chunks * 2;
+  const float *po = a.part_o + static_cast<size_t>(rh) * a.chunks * 64;
+  const float ninf = -__builtin_inff();
+  float mx = ninf;
+  for (int c = tid; c < a.chunks; c += 256) {
+    const float mc = md[2 * c];
+    mx = mc > mx ? mc : mx;
+  }
+  mx = wave_max(mx);
+  if (lane == 0) s_red[wave] = mx;
+  __syncthreads();
+  float big = s_red[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; w++) big = s_red[w] > big ? s_red[w] : big;
+  __syncthreads();
+  float den = 0.0f;
+  for (int c = tid; c < a.chunks; c += 256) {
+    const float mc = md[2 * c];
+    const float f = mc == ninf || big == ninf ? 0.0f : expf_acc(mc - big);
+    s_f[c] = f;
+    den = den + md[2 * c + 1] * f;
+  }
+  den = wave_sum(den);
+  if (lane == 0) s_red[wave] = den;
+  __syncthreads();
+  float o = 0.0f;
+  int c = wave;
+  for (; c + 12 < a.chunks; c += 16) {
+    const float o0 = po[static_cast<size_t>(c) * 64 + lane], o1 = po[static_cast<size_t>(c + 4) * 64 + lane];
+    const float o2 = po[static_cast<size_t>(c + 8) * 64 + lane], o3 = po[static_cast<size_t>(c + 12) * 64 + lane];
+    o = fmaf_(o0, s_f[c], o);
+    o = fmaf_(o1, s_f[c + 4], o);
+    o = fmaf_(o2, s_f[c + 8], o);
+    o = fmaf_(o3, s_f[c + 12], o);
+  }
+  for (; c < a.chunks; c += 4) o = fmaf_(po[static_cast<size_t>(c) * 64 + lane], s_f[c], o);
+  s_o[wave][lane] = o;
+  __syncthreads();
+  if (wave != 0) return;
+  const float d = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+  const float total = (s_o[0][lane] + s_o[1][lane]) + (s_o[2][lane] + s_o[3][lane]);
+  const float lse = big + logf_acc(d);
+  const float sink_scale = __fdiv_rn(1.0f, 1.0f + expf_acc(a.sinks[h] - lse));
+  a.out[static_cast<size_t>(rh) * 64 + lane] = __fdiv_rn(total, d) * sink_scale;
+}
+
+}  // namespace decode
+}  // namespace focr

@@ -1,0 +1,568 @@
+// The sealed split KV cache (Kv::Q8 / Kv::Q16, src/quant/kv.rs) and decode
+// attention over it.
+//
+// Sealing turns the compact FP32 prefix cache into group-major records, one
+// per (KV group g, position t): [T 0..32 | S(2g) 32..64 | S(2g+1) 64..96 |
+// V 96..160], the temporal key half shared by the two query heads of the
+// pair, each head's spatial half and the value (kv.rs:1-24). Every 32-element
+// block is coded against the smallest BF16 step at or above absmax / 127
+// (Q8) or absmax / 32767 (Q16), codes rounded to nearest even in f64 and
+// clamped (codec.rs:9-86). Generated positions go to 128-element tail
+// records [K | V] per group in the same format (push_unique, kv.rs:451-515).
+// Decoded values are code * step, exactly as the reference's Records::value.
+//
+// Device layout: record = the codes, then the BF16 steps (5 per prefix
+// record, 4 per tail record), padded to a multiple of 16 bytes (Q8: 176 and
+// 144 bytes; Q16: 336 and 272). Prefix records [group][position], tail
+// records [group][capacity].
+//
+// Decode: one wave task per (group, key chunk) serves both heads of the pair
+// (the record is read once for both), with the compact decode kernel's lane
+// map (lane group lg = lane / 16 takes keys 4i + lg, lane lp = lane % 16 dims
+// 4lp..4lp+3): lanes 0-7 read the temporal codes, lanes 8-15 both spatial
+// halves, all 16 the value. Online softmax per (head, row) over the chunk,
+// then the shared combine kernel. Roofline: HBM; bytes per call = the visible
+// records (Q8: 176 bytes per group and prefix position, 8 groups = 1,408
+// bytes per position against 6,144 for the FP32 compact cache).
+#include <vector>
+
+#include "decode_common.hpp"
+
+namespace focr {
+
+struct KvSplit {
+  int bits = 8;
+  int n_heads = 0, n_kv = 0;
+  size_t prefix_len = 0, capacity = 0, tail_len = 0;
+  size_t record_bytes = 0, tail_bytes = 0;
+  unsigned char *records = nullptr;  // [n_kv][prefix_len][record_bytes]
+  unsigned char *tail = nullptr;     // [n_kv][capacity - prefix_len][tail_bytes]
+  uint32_t *error = nullptr;         // seal's refusal flags
+  size_t device_bytes = 0;
+};
+
+namespace {
+
+using namespace decode;
+
+constexpr int kRecord = 160, kTail = 128;
+
+__device__ __forceinline__ float bf16_widen(uint16_t bits) { return __uint_as_float(static_cast<uint32_t>(bits) << 16); }
+
+// The smallest BF16 at or above a finite scale >= 0, or the NaN pattern.
+__device__ __forceinline__ uint16_t bf16_up(float scale) {
+  if (scale != scale) return 0x7FC0;
+  const uint32_t bits = __float_as_uint(scale);
+  const uint16_t high = static_cast<uint16_t>(bits >> 16);
+  return (bits & 0xFFFFu) ? static_cast<uint16_t>(high + 1) : high;
+}
+
+// The step of a 32-element block (q8_scale / q16_scale): absmax / limit in
+// f64 rounded to f32, at least the smallest subnormal, 0 for a zero block.
+__device__ __forceinline__ float block_step(const float *x, double limit) {
+  float max = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 32; i++) max = __builtin_fmaxf(max, fabsf(x[i]));
+  if (max == 0.0f) return 0.0f;
+  const float s = static_cast<float>(static_cast<double>(max) / limit);
+  return s > 1.40129846e-45f ? s : 1.40129846e-45f;
+}
+
+// round_clamped(value / step): clamp to +-limit in f64, round to nearest
+// even; NaN gives 0 (Rust's saturating cast); a zero step gives 0.
+__device__ __forceinline__ int code_of(float value, float step, double limit) {
+  if (step == 0.0f) return 0;
+  double x = static_cast<double>(value) / static_cast<double>(step);
+  if (x != x) return 0;
+  x = x < -limit ? -limit : (x > limit ? limit : x);
+  return static_cast<int>(rint(x));
+}
+
+template <typename C>
+__device__ __forceinline__ void code_block(const float *x, double limit, C *codes, uint16_t *step_out, bool nan_step,
+                                           bool *overflow) {
+  const uint16_t stored = bf16_up(nan_step ? __builtin_nanf("") : block_step(x, limit));
+  *step_out = stored;
+  const float step = bf16_widen(stored);
+#pragma unroll
+  for (int i = 0; i < 32; i++) {
+    const int c = code_of(x[i], step, limit);
+    codes[i] = static_cast<C>(c);
+    if (overflow && !__builtin_isfinite(static_cast<float>(c) * step)) *overflow = true;
+  }
+}
+
+enum : uint32_t { kErrPair = 1, kErrNonFinite = 2, kErrOverflow = 4 };
+
+struct SealArgs {
+  const float *k, *v;
+  unsigned char *records;
+  uint32_t *error;
+  int prefix_len, n_heads, n_kv, record_bytes;
+};
+
+// One thread per (record, block): gathers the block's 32 values, checks the
+// pair sharing (block 0) and finiteness, codes them.
+template <typename C>
+__global__ __launch_bounds__(256) void seal_kernel(SealArgs a) {
+  const long idx = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
+  const long total = static_cast<long>(a.n_kv) * a.prefix_len * 5;
+  if (idx >= total) return;
+  const int blk = static_cast<int>(idx % 5);
+  const long record = idx / 5;
+  const int g = static_cast<int>(record / a.prefix_len), t = static_cast<int>(record % a.prefix_len);
+  const float *ka = a.k + (static_cast<size_t>(t) * a.n_heads + 2 * g) * 64;
+  const float *src = blk == 0 ? ka : blk == 1 ? ka + 32 : blk == 2 ? ka + 64 + 32
+                   : a.v + (static_cast<size_t>(t) * a.n_kv + g) * 64 + 32 * (blk - 3);
+  float x[32];
+  uint32_t err = 0;
+#pragma unroll
+  for (int i = 0; i < 32; i++) {
+    x[i] = src[i];
+    if (!__builtin_isfinite(x[i])) err |= kErrNonFinite;
+  }
+  if (blk == 0)
+    for (int i = 0; i < 32; i++)
+      if (__float_as_uint(ka[i]) != __float_as_uint(ka[64 + i])) err |= kErrPair;
+  unsigned char *rec = a.records + static_cast<size_t>(record) * a.record_bytes;
+  C *codes = reinterpret_cast<C *>(rec) + 32 * blk;
+  uint16_t *steps = reinterpret_cast<uint16_t *>(rec + kRecord * sizeof(C));
+  bool overflow = false;
+  code_block<C>(x, sizeof(C) == 1 ? 127.0 : 32767.0, codes, steps + blk, false, &overflow);
+  if (overflow) err |= kErrOverflow;
+  if (err) atomicOr(a.error, err);
+}
+
+struct AppendArgs {
+  const float *k, *v;  // [rows][n_kv][64]
+  unsigned char *tail;
+  int n_kv, tail_capacity, first, rows, tail_bytes;
+};
+
+// One thread per (row, group, block) of the appended positions.
+template <typename C>
+__global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
+  const int idx = blockIdx.x * 256 + threadIdx.x;
+  if (idx >= a.rows * a.n_kv * 4) return;
+  const int blk = idx % 4, g = (idx / 4) % a.n_kv, r = idx / (4 * a.n_kv);
+  const float *src = (blk < 2 ? a.k : a.v) + (static_cast<size_t>(r) * a.n_kv + g) * 64 + 32 * (blk & 1);
+  float x[32];
+  bool finite = true;
+#pragma unroll
+  for (int i = 0; i < 32; i++) {
+    x[i] = src[i];
+    finite = finite && __builtin_isfinite(x[i]);
+  }
+  unsigned char *rec = a.tail + (static_cast<size_t>(g) * a.tail_capacity + a.first + r) * a.tail_bytes;
+  C *codes = reinterpret_cast<C *>(rec) + 32 * blk;
+  uint16_t *steps = reinterpret_cast<uint16_t *>(rec + kTail * sizeof(C));
+  code_block<C>(x, sizeof(C) == 1 ? 127.0 : 32767.0, codes, steps + blk, !finite, nullptr);
+}
+
+struct DequantArgs {
+  const unsigned char *records, *tail;
+  float *prefix_k, *values, *generated_k;
+  int prefix_len, tail_len, tail_capacity, n_heads, n_kv, record_bytes, tail_bytes;
+};
+
+// The decoded cache in the compact layout (kv.rs dequantized_compact plus
+// the tail): one thread per (position, group, element).
+template <typename C>
+__global__ __launch_bounds__(256) void dequantize_kernel(DequantArgs a) {
+  const long idx = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
+  const long prefix_items = static_cast<long>(a.prefix_len) * a.n_kv * kRecord;
+  const long tail_items = static_cast<long>(a.tail_len) * a.n_kv * kTail;
+  if (idx < prefix_items) {
+    const int e = static_cast<int>(idx % kRecord);
+    const long rg = idx / kRecord;
+    const int g = static_cast<int>(rg % a.n_kv), t = static_cast<int>(rg / a.n_kv);
+    const unsigned char *rec = a.records + (static_cast<size_t>(g) * a.prefix_len + t) * a.record_bytes;
+    const float x = static_cast<float>(reinterpret_cast<const C *>(rec)[e]) *
+                    bf16_widen(reinterpret_cast<const uint16_t *>(rec + kRecord * sizeof(C))[e / 32]);
+    float *k0 = a.prefix_k + (static_cast<size_t>(t) * a.n_heads + 2 * g) * 64;
+    if (e < 32) {
+      k0[e] = x;
+      k0[64 + e] = x;
+    } else if (e < 64) {
+      k0[e] = x;
+    } else if (e < 96) {
+      k0[64 + e - 32] = x;
+    } else {
+      a.values[(static_cast<size_t>(t) * a.n_kv + g) * 64 + e - 96] = x;
+    }
+  } else if (idx < prefix_items + tail_items) {
+    const long j = idx - prefix_items;
+    const int e = static_cast<int>(j % kTail);
+    const long rg = j / kTail;
+    const int g = static_cast<int>(rg % a.n_kv), i = static_cast<int>(rg / a.n_kv);
+    const unsigned char *rec = a.tail + (static_cast<size_t>(g) * a.tail_capacity + i) * a.tail_bytes;
+    const float x = static_cast<float>(reinterpret_cast<const C *>(rec)[e]) *
+                    bf16_widen(reinterpret_cast<const uint16_t *>(rec + kTail * sizeof(C))[e / 32]);
+    if (e < 64)
+      a.generated_k[(static_cast<size_t>(i) * a.n_kv + g) * 64 + e] = x;
+    else
+      a.values[(static_cast<size_t>(a.prefix_len + i) * a.n_kv + g) * 64 + e - 64] = x;
+  }
+}
+
+struct SplitDecArgs {
+  const unsigned char *records, *tail;
+  const float *q;
+  float *part_o, *part_md;
+  int prefix_len, tail_capacity, n_heads, n_kv, record_bytes, tail_bytes;
+  int last;  // positions in the cache; row r sees keys [0, last - rows + r + 1)
+  int chunks, tasks;
+};
+
+// Four consecutive codes of a record as floats (one 4- or 8-byte load).
+template <typename C>
+__device__ __forceinline__ float4 codes4(const unsigned char *p) {
+  if constexpr (sizeof(C) == 1) {
+    const uint32_t w = *reinterpret_cast<const uint32_t *>(p);
+    return make_float4(static_cast<float>(static_cast<int8_t>(w & 0xff)), static_cast<float>(static_cast<int8_t>((w >> 8) & 0xff)),
+                       static_cast<float>(static_cast<int8_t>((w >> 16) & 0xff)), static_cast<float>(static_cast<int8_t>(w >> 24)));
+  } else {
+    const uint2 w = *reinterpret_cast<const uint2 *>(p);
+    return make_float4(static_cast<float>(static_cast<int16_t>(w.x & 0xffff)), static_cast<float>(static_cast<int16_t>(w.x >> 16)),
+                       static_cast<float>(static_cast<int16_t>(w.y & 0xffff)), static_cast<float>(static_cast<int16_t>(w.y >> 16)));
+  }
+}
+
+__device__ __forceinline__ float4 scale4(float4 c, float s) { return make_float4(c.x * s, c.y * s, c.z * s, c.w * s); }
+
+// A key's (both heads') and value's decoded values for lane lp.
+struct KeyVal {
+  float4 k0, k1, v;
+};
+
+template <typename C>
+__device__ __forceinline__ KeyVal load_key(const SplitDecArgs &a, int g, int j, int lp) {
+  KeyVal kv;
+  if (j < a.prefix_len) {
+    const unsigned char *rec = a.records + (static_cast<size_t>(g) * a.prefix_len + j) * a.record_bytes;
+    const uint16_t *steps = reinterpret_cast<const uint16_t *>(rec + kRecord * sizeof(C));
+    if (lp < 8) {
+      kv.k0 = scale4(codes4<C>(rec + 4 * lp * sizeof(C)), bf16_widen(steps[0]));
+      kv.k1 = kv.k0;
+    } else {
+      kv.k0 = scale4(codes4<C>(rec + (32 + 4 * (lp - 8)) * sizeof(C)), bf16_widen(steps[1]));
+      kv.k1 = scale4(codes4<C>(rec + (64 + 4 * (lp - 8)) * sizeof(C)), bf16_widen(steps[2]));
+    }
+    kv.v = scale4(codes4<C>(rec + (96 + 4 * lp) * sizeof(C)), bf16_widen(steps[3 + (lp >> 3)]));
+  } else {
+    const unsigned char *rec =
+        a.tail + (static_cast<size_t>(g) * a.tail_capacity + (j - a.prefix_len)) * a.tail_bytes;
+    const uint16_t *steps = reinterpret_cast<const uint16_t *>(rec + kTail * sizeof(C));
+    kv.k0 = scale4(codes4<C>(rec + 4 * lp * sizeof(C)), bf16_widen(steps[lp >> 3]));
+    kv.k1 = kv.k0;
+    kv.v = scale4(codes4<C>(rec + (64 + 4 * lp) * sizeof(C)), bf16_widen(steps[2 + (lp >> 3)]));
+  }
+  return kv;
+}
+
+constexpr int kKpl = 4;  // keys per lane group per iteration (16 per wave)
+
+// M: query rows. Task = (group g, chunk c); heads 2g and 2g + 1.
+template <typename C, int M>
+__global__ __launch_bounds__(256) void split_partial_kernel(SplitDecArgs a, int iters, int rows) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lg = lane >> 4, lp = lane & 15;
+  const int task = blockIdx.x * kWaves + wave;
+  if (task >= a.tasks) return;
+  const int c = task % a.chunks, g = task / a.chunks;
+  const int key0 = c * iters * 4 * kKpl;
+  int vis[M], limit = 0;
+#pragma unroll
+  for (int r = 0; r < M; r++) {
+    vis[r] = a.last - rows + r + 1;
+    limit = vis[r] > limit ? vis[r] : limit;
+  }
+  float4 qv[2][M];
+#pragma unroll
+  for (int e = 0; e < 2; e++)
+#pragma unroll
+    for (int r = 0; r < M; r++)
+      qv[e][r] = ld4(a.q + (static_cast<size_t>(r) * a.n_heads + 2 * g + e) * 64 + 4 * lp);
+  const float ninf = -__builtin_inff();
+  float m[2][M], den[2][M];
+  float4 o[2][M];
+#pragma unroll
+  for (int e = 0; e < 2; e++)
+#pragma unroll
+    for (int r = 0; r < M; r++) {
+      m[e][r] = ninf;
+      den[e][r] = 0.0f;
+      o[e][r] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+  auto load = [&](KeyVal (&kb)[kKpl], int it) {
+#pragma unroll
+    for (int i = 0; i < kKpl; i++) {
+      const int j = key0 + 16 * it + 4 * i + lg;
+      kb[i] = load_key<C>(a, g, j < limit ? j : 0, lp);
+    }
+  };
+  auto consume = [&](const KeyVal (&kb)[kKpl], int it) {
+    float s[2][kKpl][M];
+#pragma unroll
+    for (int i = 0; i < kKpl; i++) {
+      const int j = key0 + 16 * it + 4 * i + lg;
+#pragma unroll
+      for (int e = 0; e < 2; e++) {
+        const float4 k = e == 0 ? kb[i].k0 : kb[i].k1;
+#pragma unroll
+        for (int r = 0; r < M; r++) {
+          float d = qv[e][r].x * k.x;
+          d = fmaf_(qv[e][r].y, k.y, d);
+          d = fmaf_(qv[e][r].z, k.z, d);
+          d = fmaf_(qv[e][r].w, k.w, d);
+          d = row_sum16(d) * 0.125f;
+          s[e][i][r] = j < vis[r] ? d : ninf;
+        }
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 2; e++)
+#pragma unroll
+      for (int r = 0; r < M; r++) {
+        float bmax = s[e][0][r];
+#pragma unroll
+        for (int i = 1; i < kKpl; i++) bmax = s[e][i][r] > bmax ? s[e][i][r] : bmax;
+        const float mn = bmax > m[e][r] ? bmax : m[e][r];
+        if (mn == ninf) continue;
+        const float rs = m[e][r] == ninf ? 0.0f : expf_acc(m[e][r] - mn);
+        den[e][r] = den[e][r] * rs;
+        o[e][r] = scale4(o[e][r], rs);
+        m[e][r] = mn;
+#pragma unroll
+        for (int i = 0; i < kKpl; i++) {
+          const float p = s[e][i][r] == ninf ? 0.0f : expf_acc(s[e][i][r] - mn);
+          const float4 v = kb[i].v;
+          den[e][r] = den[e][r] + p;
+          o[e][r] = make_float4(fmaf_(p, v.x, o[e][r].x), fmaf_(p, v.y, o[e][r].y), fmaf_(p, v.z, o[e][r].z),
+                                fmaf_(p, v.w, o[e][r].w));
+        }
+      }
+  };
+  KeyVal ka[kKpl], kb[kKpl];
+  load(ka, 0);
+  for (int it = 0; it < iters; it += 2) {
+    if (it + 1 < iters) load(kb, it + 1);
+    consume(ka, it);
+    if (it + 1 < iters) {
+      if (it + 2 < iters) load(ka, it + 2);
+      consume(kb, it + 1);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 2; e++)
+#pragma unroll
+    for (int r = 0; r < M; r++) {
+#pragma unroll
+      for (int mask = 16; mask <= 32; mask *= 2) {
+        const float m2 = xor_lane(m[e][r], mask), d2 = xor_lane(den[e][r], mask);
+        const float4 o2 = make_float4(xor_lane(o[e][r].x, mask), xor_lane(o[e][r].y, mask),
+                                      xor_lane(o[e][r].z, mask), xor_lane(o[e][r].w, mask));
+        merge(m[e][r], den[e][r], o[e][r], m2, d2, o2);
+      }
+      const size_t slot = (static_cast<size_t>(r) * a.n_heads + 2 * g + e) * a.chunks + c;
+      if (lg == 0) *reinterpret_cast<float4 *>(a.part_o + slot * 64 + 4 * lp) = o[e][r];
+      if (lane == 0) *reinterpret_cast<float2 *>(a.part_md + slot * 2) = make_float2(m[e][r], den[e][r]);
+    }
+}
+
+template <typename C, int M>
+int launch_split(Ctx *ctx, SplitDecArgs a, int rows, const float *sinks, float *out) {
+  // Keys per wave task: about 2048 tasks over the chip (each serves two
+  // heads), at most kMaxChunks chunks, whole 16-key iterations.
+  const long limit = a.last;
+  const long want = (limit * a.n_kv + 2047) / 2048;
+  long per = (want + 15) / 16 * 16;
+  const long min_per = ((limit + kMaxChunks - 1) / kMaxChunks + 15) / 16 * 16;
+  if (per < min_per) per = min_per;
+  if (per < 16) per = 16;
+  const int iters = static_cast<int>(per / 16);
+  a.chunks = static_cast<int>((limit + per - 1) / per);
+  a.tasks = a.n_kv * a.chunks;
+  const size_t slots = static_cast<size_t>(rows) * a.n_heads * a.chunks;
+  int rc = ensure_scratch(ctx, slots * 66 * sizeof(float));
+  if (rc != FOCR_OK) return rc;
+  a.part_o = static_cast<float *>(ctx->scratch);
+  a.part_md = a.part_o + slots * 64;
+  hipLaunchKernelGGL((split_partial_kernel<C, M>), dim3((a.tasks + kWaves - 1) / kWaves), dim3(64 * kWaves), 0,
+                     ctx->stream, a, iters, rows);
+  FOCR_HIP_CHECK(hipGetLastError());
+  CombineArgs cb;
+  cb.part_o = a.part_o;
+  cb.part_md = a.part_md;
+  cb.sinks = sinks;
+  cb.out = out;
+  cb.n_heads = a.n_heads;
+  cb.chunks = a.chunks;
+  hipLaunchKernelGGL(decode_combine_kernel, dim3(static_cast<unsigned>(rows * a.n_heads)), dim3(64 * kWaves), 0,
+                     ctx->stream, cb);
+  FOCR_HIP_CHECK(hipGetLastError());
+  return FOCR_OK;
+}
+
+template <typename C>
+int launch_split_rows(Ctx *ctx, const SplitDecArgs &a, int rows, const float *sinks, float *out) {
+  switch (rows) {
+    case 1: return launch_split<C, 1>(ctx, a, rows, sinks, out);
+    case 2: return launch_split<C, 2>(ctx, a, rows, sinks, out);
+    case 3: return launch_split<C, 3>(ctx, a, rows, sinks, out);
+    case 4: return launch_split<C, 4>(ctx, a, rows, sinks, out);
+    case 5: return launch_split<C, 5>(ctx, a, rows, sinks, out);
+    case 6: return launch_split<C, 6>(ctx, a, rows, sinks, out);
+    case 7: return launch_split<C, 7>(ctx, a, rows, sinks, out);
+    default: return launch_split<C, 8>(ctx, a, rows, sinks, out);
+  }
+}
+
+}  // namespace
+}  // namespace focr
+
+using namespace focr;
+
+extern "C" {
+
+int focr_kv_seal(focr_ctx *handle, int bits, const float *prefix_k, const float *v, size_t prefix_len,
+                 size_t capacity, size_t n_heads, size_t n_kv_heads, size_t head_dim, focr_kv_split **out) {
+  Ctx *ctx = reinterpret_cast<Ctx *>(handle);
+  FOCR_REQUIRE(ctx && prefix_k && v && out, FOCR_E_ARG, "focr_kv_seal: null argument");
+  *out = nullptr;
+  FOCR_REQUIRE(bits == 8 || bits == 16, FOCR_E_ARG, "focr_kv_seal: bits must be 8 (Kv::Q8) or 16 (Kv::Q16)");
+  FOCR_REQUIRE(head_dim == 64 && n_heads == 2 * n_kv_heads && n_kv_heads >= 1 && n_kv_heads <= 8, FOCR_E_SHAPE,
+               "split cache requires Falcon 64-wide paired GQA heads");
+  FOCR_REQUIRE(prefix_len > 0 && capacity >= prefix_len && capacity < (size_t(1) << 30), FOCR_E_SHAPE,
+               "invalid split-prefix capacity");
+  FOCR_HIP_CHECK(hipSetDevice(ctx->device));
+  KvSplit *s = new KvSplit();
+  s->bits = bits;
+  s->n_heads = static_cast<int>(n_heads);
+  s->n_kv = static_cast<int>(n_kv_heads);
+  s->prefix_len = prefix_len;
+  s->capacity = capacity;
+  const size_t cb = bits / 8;
+  s->record_bytes = (kRecord * cb + 10 + 15) / 16 * 16;
+  s->tail_bytes = (kTail * cb + 8 + 15) / 16 * 16;
+  const size_t rec_total = n_kv_heads * prefix_len * s->record_bytes;
+  const size_t tail_total = n_kv_heads * (capacity - prefix_len) * s->tail_bytes;
+  hipError_t e = hipMalloc(reinterpret_cast<void **>(&s->records), rec_total);
+  if (e == hipSuccess && tail_total) e = hipMalloc(reinterpret_cast<void **>(&s->tail), tail_total);
+  if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void **>(&s->error), sizeof(uint32_t));
+  if (e == hipSuccess) e = hipMemsetAsync(s->error, 0, sizeof(uint32_t), ctx->stream);
+  if (e != hipSuccess) {
+    focr_kv_free(reinterpret_cast<focr_kv_split *>(s));
+    return set_error(FOCR_E_HIP, std::string("focr_kv_seal: ") + hipGetErrorString(e));
+  }
+  s->device_bytes = rec_total + tail_total;
+  SealArgs a{prefix_k, v, s->records, s->error, static_cast<int>(prefix_len), s->n_heads, s->n_kv,
+             static_cast<int>(s->record_bytes)};
+  const long threads = static_cast<long>(n_kv_heads) * prefix_len * 5;
+  const dim3 grid(static_cast<unsigned>((threads + 255) / 256));
+  if (bits == 8)
+    hipLaunchKernelGGL(seal_kernel<int8_t>, grid, dim3(256), 0, ctx->stream, a);
+  else
+    hipLaunchKernelGGL(seal_kernel<int16_t>, grid, dim3(256), 0, ctx->stream, a);
+  uint32_t err = 0;
+  e = hipGetLastError();
+  if (e == hipSuccess) e = hipMemcpyAsync(&err, s->error, sizeof(err), hipMemcpyDeviceToHost, ctx->stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) {
+    focr_kv_free(reinterpret_cast<focr_kv_split *>(s));
+    return set_error(FOCR_E_HIP, std::string("focr_kv_seal: ") + hipGetErrorString(e));
+  }
+  if (err) {
+    focr_kv_free(reinterpret_cast<focr_kv_split *>(s));
+    if (err & kErrPair) return set_error(FOCR_E_VALUE, "temporal keys differ inside GQA pair; refusing illegal sharing");
+    if (err & kErrNonFinite) return set_error(FOCR_E_VALUE, "nonfinite or incomplete KV group");
+    return set_error(FOCR_E_VALUE, bits == 8 ? "Q8 KV conversion overflow" : "Q16 KV conversion overflow");
+  }
+  *out = reinterpret_cast<focr_kv_split *>(s);
+  return FOCR_OK;
+}
+
+int focr_kv_append(focr_ctx *handle, focr_kv_split *kv, const float *k, const float *v, size_t rows) {
+  Ctx *ctx = reinterpret_cast<Ctx *>(handle);
+  KvSplit *s = reinterpret_cast<KvSplit *>(kv);
+  FOCR_REQUIRE(ctx && s && k && v, FOCR_E_ARG, "focr_kv_append: null argument");
+  if (rows == 0) return FOCR_OK;
+  FOCR_REQUIRE(s->prefix_len + s->tail_len + rows <= s->capacity, FOCR_E_SHAPE, "split tail capacity");
+  FOCR_HIP_CHECK(hipSetDevice(ctx->device));
+  AppendArgs a{k, v, s->tail, s->n_kv, static_cast<int>(s->capacity - s->prefix_len), static_cast<int>(s->tail_len),
+               static_cast<int>(rows), static_cast<int>(s->tail_bytes)};
+  const int threads = static_cast<int>(rows) * s->n_kv * 4;
+  if (s->bits == 8)
+    hipLaunchKernelGGL(append_kernel<int8_t>, dim3((threads + 255) / 256), dim3(256), 0, ctx->stream, a);
+  else
+    hipLaunchKernelGGL(append_kernel<int16_t>, dim3((threads + 255) / 256), dim3(256), 0, ctx->stream, a);
+  FOCR_HIP_CHECK(hipGetLastError());
+  s->tail_len += rows;
+  return FOCR_OK;
+}
+
+int focr_kv_attention_decode(focr_ctx *handle, const focr_kv_split *kv, const float *q, size_t rows,
+                             const float *sinks, float *out) {
+  Ctx *ctx = reinterpret_cast<Ctx *>(handle);
+  const KvSplit *s = reinterpret_cast<const KvSplit *>(kv);
+  FOCR_REQUIRE(ctx && s && q && sinks && out, FOCR_E_ARG, "focr_kv_attention_decode: null argument");
+  FOCR_REQUIRE(rows >= 1 && rows <= 8 && rows <= (s->tail_len > 0 ? s->tail_len : 1), FOCR_E_SHAPE,
+               "split decode: 1 to 8 rows, at most the appended positions");
+  FOCR_HIP_CHECK(hipSetDevice(ctx->device));
+  SplitDecArgs a;
+  a.records = s->records;
+  a.tail = s->tail;
+  a.q = q;
+  a.prefix_len = static_cast<int>(s->prefix_len);
+  a.tail_capacity = static_cast<int>(s->capacity - s->prefix_len);
+  a.n_heads = s->n_heads;
+  a.n_kv = s->n_kv;
+  a.record_bytes = static_cast<int>(s->record_bytes);
+  a.tail_bytes = static_cast<int>(s->tail_bytes);
+  a.last = static_cast<int>(s->prefix_len + s->tail_len);
+  const int r = static_cast<int>(rows);
+  return s->bits == 8 ? launch_split_rows<int8_t>(ctx, a, r, sinks, out) : launch_split_rows<int16_t>(ctx, a, r, sinks, out);
+}
+
+int focr_kv_dequantize(focr_ctx *handle, const focr_kv_split *kv, float *prefix_k, float *values, float *generated_k) {
+  Ctx *ctx = reinterpret_cast<Ctx *>(handle);
+  const KvSplit *s = reinterpret_cast<const KvSplit *>(kv);
+  FOCR_REQUIRE(ctx && s && prefix_k && values && (generated_k || s->tail_len == 0), FOCR_E_ARG,
+               "focr_kv_dequantize: null argument");
+  FOCR_HIP_CHECK(hipSetDevice(ctx->device));
+  DequantArgs a{s->records, s->tail, prefix_k, values, generated_k, static_cast<int>(s->prefix_len),
+                static_cast<int>(s->tail_len), static_cast<int>(s->capacity - s->prefix_len), s->n_heads, s->n_kv,
+                static_cast<int>(s->record_bytes), static_cast<int>(s->tail_bytes)};
+  const long items = static_cast<long>(s->prefix_len) * s->n_kv * kRecord + static_cast<long>(s->tail_len) * s->n_kv * kTail;
+  const dim3 grid(static_cast<unsigned>((items + 255) / 256));
+  if (s->bits == 8)
+    hipLaunchKernelGGL(dequantize_kernel<int8_t>, grid, dim3(256), 0, ctx->stream, a);
+  else
+    hipLaunchKernelGGL(dequantize_kernel<int16_t>, grid, dim3(256), 0, ctx->stream, a);
+  FOCR_HIP_CHECK(hipGetLastError());
+  return FOCR_OK;
+}
+
+int focr_kv_info(const focr_kv_split *kv, int *bits, size_t *prefix_len, size_t *tail_len, size_t *capacity,
+                 size_t *device_bytes) {
+  const KvSplit *s = reinterpret_cast<const KvSplit *>(kv);
+  FOCR_REQUIRE(s, FOCR_E_ARG, "focr_kv_info: null cache");
+  if (bits) *bits = s->bits;
+  if (prefix_len) *prefix_len = s->prefix_len;
+  if (tail_len) *tail_len = s->tail_len;
+  if (capacity) *capacity = s->capacity;
+  if (device_bytes) *device_bytes = s->device_bytes;
+  return FOCR_OK;
+}
+
+int focr_kv_free(focr_kv_split *kv) {
+  KvSplit *s = reinterpret_cast<KvSplit *>(kv);
+  if (!s) return FOCR_OK;
+  if (s->records) (void)hipFree(s->records);
+  if (s->tail) (void)hipFree(s->tail);
+  if (s->error) (void)hipFree(s->error);
+  delete s;
+  return FOCR_OK;
+}
+
+}  // extern "C"

@@ -74,6 +74,12 @@ SIGNATURES = {
     "focr_attention_prefill": (_I, [_P, _P, _P, _P, _P, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _P, _I, _I, _P]),
     "focr_attention_prefill_bf16": (_I, [_P, _P, _P, _P, _Z, _Z, _Z, _Z, _Z, _Z, _P, _I, _I, _P]),
     "focr_argmax": (_I, [_P, _P, _Z, _Z, _P]),
+    "focr_kv_seal": (_I, [_P, _I, _P, _P, _Z, _Z, _Z, _Z, _Z, ctypes.POINTER(_P)]),
+    "focr_kv_append": (_I, [_P, _P, _P, _P, _Z]),
+    "focr_kv_attention_decode": (_I, [_P, _P, _P, _Z, _P, _P]),
+    "focr_kv_dequantize": (_I, [_P, _P, _P, _P, _P]),
+    "focr_kv_info": (_I, [_P, _P, _P, _P, _P, _P]),
+    "focr_kv_free": (_I, [_P]),
     "focr_screen_build": (_I, [_P, _P, _Z, _Z, ctypes.POINTER(_P)]),
     "focr_screen_upload": (_I, [_P, _P, _P, _Z, _Z, ctypes.c_float, ctypes.c_float, ctypes.POINTER(_P)]),
     "focr_screen_free": (_I, [_P]),
@@ -461,6 +467,65 @@ def argmax(logits, rows: int, vocab: int, ctx: Optional[Context] = None):
     tokens = (ctypes.c_uint32 * rows)()
     _check(lib().focr_argmax(ctx.handle, _dev(logits), rows, vocab, ctypes.cast(tokens, ctypes.c_void_p)))
     return list(tokens)
+
+
+class KvSplit:
+    """`SplitPrefix` (src/quant/kv.rs) for `Kv::Q8` (bits 8) and `Kv::Q16`
+    (bits 16): the sealed prefix records and the generated tail, on the device."""
+
+    def __init__(self, handle, bits: int, n_heads: int, n_kv_heads: int, ctx: Context):
+        self.handle, self.bits, self.n_heads, self.n_kv_heads, self.ctx = handle, bits, n_heads, n_kv_heads, ctx
+
+    @classmethod
+    def seal(cls, bits: int, prefix_k, v, prefix_len: int, capacity: int, n_heads: int = 16, n_kv_heads: int = 8,
+             ctx: Optional[Context] = None) -> "KvSplit":
+        """`SplitPrefix::from_compact` of a compact prefix (device tensors)."""
+        ctx = ctx or default_context()
+        handle = ctypes.c_void_p()
+        _check(lib().focr_kv_seal(ctx.handle, bits, _dev(prefix_k), _dev(v), prefix_len, capacity, n_heads,
+                                  n_kv_heads, 64, ctypes.byref(handle)))
+        return cls(handle, bits, n_heads, n_kv_heads, ctx)
+
+    def append(self, k, v, rows: int) -> None:
+        """`push_unique` of `rows` positions: k, v [rows][n_kv_heads][64]."""
+        _check(lib().focr_kv_append(self.ctx.handle, self.handle, _dev(k), _dev(v), rows))
+
+    def attention_decode(self, q, rows: int, sinks, out=None):
+        """`attention_decode_rows`: [rows][n_heads][64] for the last `rows` positions."""
+        torch = _torch()
+        if out is None:
+            out = torch.empty((rows, self.n_heads, 64), dtype=torch.float32, device=q.device)
+        _check(lib().focr_kv_attention_decode(self.ctx.handle, self.handle, _dev(q), rows, _dev(sinks), _dev(out)))
+        return out
+
+    def info(self):
+        """(bits, prefix_len, tail_len, capacity, device_bytes)."""
+        b, p, t, c, n = ctypes.c_int(), ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_size_t()
+        _check(lib().focr_kv_info(self.handle, ctypes.byref(b), ctypes.byref(p), ctypes.byref(t), ctypes.byref(c),
+                                  ctypes.byref(n)))
+        return b.value, p.value, t.value, c.value, n.value
+
+    def dequantize(self):
+        """(prefix_k [P][n_heads][64], values [P + tail][n_kv][64], generated_k [tail][n_kv][64])."""
+        torch = _torch()
+        _, p, t, _, _ = self.info()
+        dev = f"cuda:{self.ctx.device}"
+        pk = torch.empty((p, self.n_heads, 64), dtype=torch.float32, device=dev)
+        vals = torch.empty((p + t, self.n_kv_heads, 64), dtype=torch.float32, device=dev)
+        gk = torch.empty((max(t, 1), self.n_kv_heads, 64), dtype=torch.float32, device=dev)
+        _check(lib().focr_kv_dequantize(self.ctx.handle, self.handle, _dev(pk), _dev(vals), _dev(gk)))
+        return pk, vals, gk[:t]
+
+    def free(self) -> None:
+        if getattr(self, "handle", None):
+            _check(lib().focr_kv_free(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
 
 
 SCREEN_LIMIT = 1024  # CANDIDATE_LIMIT (src/head_screen.rs:29)

@@ -64,6 +64,7 @@ extern "C" {
 typedef struct focr_ctx focr_ctx;
 typedef struct focr_linear focr_linear;
 typedef struct focr_screen focr_screen;
+typedef struct focr_kv_split focr_kv_split;
 
 /* ---- context ------------------------------------------------------------ */
 /* No reference counterpart (the CPU runner needs no device state); the
@@ -233,6 +234,44 @@ int focr_attention_decode(focr_ctx *ctx, const float *q_dev, const float *prefix
  * logits_dev [rows][vocab]; tokens (host) [rows]. Synchronous. */
 int focr_argmax(focr_ctx *ctx, const float *logits_dev, size_t rows, size_t vocab,
                 uint32_t *tokens);
+
+/* ---- Sealed split KV cache, Kv::Q8 / Kv::Q16 (src/quant/kv.rs) ---------- */
+/* SplitPrefix::from_compact / seal (src/quant/kv.rs:225-421): seals the
+ * compact prefix cache (prefix_k_dev [prefix_len][n_heads][64], v_dev
+ * [prefix_len][n_kv_heads][64]) into group-major records [T | S(2g) |
+ * S(2g+1) | V] of 8-bit (bits 8, Kv::Q8) or 16-bit (bits 16, Kv::Q16) codes
+ * with one BF16 step (rounded up) per 32 elements, and reserves a tail for
+ * capacity - prefix_len generated positions. FOCR_E_SHAPE unless head_dim is
+ * 64 and n_heads = 2 n_kv_heads <= 16; FOCR_E_VALUE (nothing kept) if the
+ * paired heads' temporal halves differ, a value is non-finite or a decoded
+ * value overflows. Synchronous. */
+int focr_kv_seal(focr_ctx *ctx, int bits, const float *prefix_k_dev, const float *v_dev,
+                 size_t prefix_len, size_t capacity, size_t n_heads, size_t n_kv_heads,
+                 size_t head_dim, focr_kv_split **out);
+/* SplitPrefix::append / push_unique (src/quant/kv.rs:430-515): appends rows
+ * generated positions, one key and one value per KV group (k_dev, v_dev
+ * [rows][n_kv_heads][64]: the pair's identical heads once), coded as the
+ * prefix; a block holding a non-finite value decodes to NaN. FOCR_E_SHAPE
+ * past the capacity. */
+int focr_kv_append(focr_ctx *ctx, focr_kv_split *kv, const float *k_dev, const float *v_dev,
+                   size_t rows);
+/* SplitPrefix::attention_decode / attention_decode_rows (src/quant/kv.rs:
+ * 568-580,856-900): q_dev [rows][n_heads][64], rows 1..8 (at most the
+ * appended positions); row r attends to keys [0, len - rows + r + 1) of the
+ * len cached positions, with the per-head sink; out_dev [rows][n_heads][64].
+ * Within FP32 rounding of the compact kernel over the decoded values. Uses
+ * the context scratch for the partial states. */
+int focr_kv_attention_decode(focr_ctx *ctx, const focr_kv_split *kv, const float *q_dev, size_t rows,
+                             const float *sinks_dev, float *out_dev);
+/* The decoded cache in the compact layout (the reference's test view
+ * dequantized_compact, src/quant/kv.rs:533-563, plus the tail): prefix keys
+ * [prefix_len][n_heads][64], values [prefix_len + tail_len][n_kv_heads][64],
+ * generated keys [tail_len][n_kv_heads][64]. */
+int focr_kv_dequantize(focr_ctx *ctx, const focr_kv_split *kv, float *prefix_k_dev, float *values_dev,
+                       float *generated_k_dev);
+int focr_kv_info(const focr_kv_split *kv, int *bits, size_t *prefix_len, size_t *tail_len,
+                 size_t *capacity, size_t *device_bytes);
+int focr_kv_free(focr_kv_split *kv);
 
 /* ---- INT8 screened vocabulary head (src/head_screen.rs) ------------------ */
 /* ScreenedHead::build (src/head_screen.rs:84-118): quantizes the FP32 head

@@ -23,7 +23,8 @@ def test_header_declares_the_boundary():
     for required in ("focr_linear_upload", "focr_linear_decode", "focr_linear_decode_glu", "focr_linear_prefill",
                      "focr_linear_dequantize", "focr_row_scales", "focr_attention_prefill", "focr_argmax",
                      "focr_linear_decode_ex", "focr_qkv_rows", "focr_attention_decode", "focr_screen_build",
-                     "focr_screen_upload", "focr_screen_select", "focr_screen_free", "focr_screen_constants"):
+                     "focr_screen_upload", "focr_screen_select", "focr_screen_free", "focr_screen_constants",
+                     "focr_kv_seal", "focr_kv_append", "focr_kv_attention_decode", "focr_kv_dequantize"):
         assert required in names
 
 
@@ -56,6 +57,12 @@ def test_null_arguments_are_errors_not_crashes():
     assert lib.focr_ctx_destroy(None) == 0
     assert lib.focr_linear_free(None) == 0
     assert lib.focr_screen_free(None) == 0
+    assert lib.focr_kv_seal(None, 8, None, None, 1, 1, 16, 8, 64, None) == -1
+    assert lib.focr_kv_append(None, None, None, None, 1) == -1
+    assert lib.focr_kv_attention_decode(None, None, None, 1, None, None) == -1
+    assert lib.focr_kv_dequantize(None, None, None, None, None) == -1
+    assert lib.focr_kv_info(None, None, None, None, None, None) == -1
+    assert lib.focr_kv_free(None) == 0
 
 
 def test_missing_library_fails_loudly(tmp_path):

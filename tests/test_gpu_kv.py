@@ -1,0 +1,121 @@
+"""The sealed split KV cache on the GPU (focr_kv_*) against the oracle: the
+decoded prefix and tail are bit for bit the oracle's records (Kv::Q8 and
+Kv::Q16), the refusals are the reference's, and decode attention over the
+records is within FP32 rounding of the compact decode oracle over the decoded
+values (src/quant/kv.rs; kv.rs:7-17: decode over records is the compact
+kernel over their decoded values)."""
+import numpy as np
+import pytest
+
+import gen
+import oracle
+from gpu_util import F32, assert_bitwise, host, to_dev
+from test_oracle_kv import pair_cache
+
+pytestmark = pytest.mark.gpu
+
+N_HEADS, N_KV = 16, 8
+
+
+@pytest.fixture(scope="module")
+def fh():
+    import focr_hip
+
+    return focr_hip
+
+
+def max_rel(got, want):
+    return float(np.abs(got.astype(np.float64) - want).max() / max(np.abs(want).max(), 1e-30))
+
+
+def oracle_cache(bits, k, v, prefix_len, tail_k, tail_v, capacity):
+    sealed = oracle.kv_seal(bits, k, v, prefix_len, N_HEADS, N_KV)
+    assert not isinstance(sealed, int), sealed
+    tail = oracle.kv_tail(bits, N_KV, capacity - prefix_len)
+    for i in range(len(tail_k)):
+        oracle.kv_push(bits, tail_k[i], tail_v[i], N_KV, capacity - prefix_len, i, tail)
+    return oracle.kv_dequantize(bits, sealed, prefix_len, N_HEADS, N_KV, tail, capacity - prefix_len, len(tail_k))
+
+
+@pytest.mark.parametrize("bits", [8, 16])
+@pytest.mark.parametrize("prefix_len", [1, 37, 1000])
+def test_seal_and_append_are_bitwise_the_oracle(fh, bits, prefix_len):
+    k, v = pair_cache(prefix_len, N_KV, 11, 2.0)
+    cap = prefix_len + 9
+    tk = gen.normal((9, N_KV, 64), 1.5, 12)
+    tv = gen.normal((9, N_KV, 64), 1.5, 13)
+    tk[4, 3, 50] = np.nan  # that block decodes to NaN
+    kv = fh.KvSplit.seal(bits, to_dev(k), to_dev(v), prefix_len, cap, N_HEADS, N_KV)
+    kv.append(to_dev(tk[:5]), to_dev(tv[:5]), 5)
+    kv.append(to_dev(tk[5:9]), to_dev(tv[5:9]), 4)
+    assert kv.info()[:4] == (bits, prefix_len, 9, cap)
+    pk, vals, gk = (host(t) for t in kv.dequantize())
+    wpk, wvals, wgk = oracle_cache(bits, k, v, prefix_len, tk, tv, cap)
+    assert_bitwise(pk, wpk, "prefix keys")
+    assert_bitwise(vals, wvals, "values")
+    assert_bitwise(gk, wgk, "generated keys")
+    assert np.all(np.isnan(gk[4, 3, 32:])) and np.all(np.isfinite(gk[4, 3, :32]))
+    kv.free()
+
+
+def test_refusals(fh):
+    P = 6
+    k, v = pair_cache(P, N_KV, 21)
+    bad = k.copy()
+    bad[2, 5, 3] = np.nextafter(bad[2, 5, 3], F32(np.inf))
+    with pytest.raises(fh.FocrError, match="temporal keys differ"):
+        fh.KvSplit.seal(8, to_dev(bad), to_dev(v), P, P + 2, N_HEADS, N_KV)
+    nan = v.copy()
+    nan[4, 7, 63] = np.nan
+    with pytest.raises(fh.FocrError, match="nonfinite"):
+        fh.KvSplit.seal(16, to_dev(k), to_dev(nan), P, P + 2, N_HEADS, N_KV)
+    with pytest.raises(fh.FocrError) as e:
+        fh.KvSplit.seal(8, to_dev(k), to_dev(v), P, P + 2, 16, 4)
+    assert e.value.code == -2
+    kv = fh.KvSplit.seal(8, to_dev(k), to_dev(v), P, P + 2, N_HEADS, N_KV)
+    one = gen.normal((3, N_KV, 64), 1.0, 22)
+    with pytest.raises(fh.FocrError) as e:
+        kv.append(to_dev(one), to_dev(one), 3)  # capacity for 2
+    assert e.value.code == -2
+    kv.free()
+
+
+@pytest.mark.parametrize("bits", [8, 16])
+@pytest.mark.parametrize("prefix_len,tail,rows", [(64, 1, 1), (700, 3, 3), (2000, 8, 8), (129, 5, 2)])
+def test_decode_within_fp32_rounding_of_the_compact_oracle(fh, bits, prefix_len, tail, rows):
+    k, v = pair_cache(prefix_len, N_KV, 31)
+    cap = prefix_len + 16
+    tk = gen.normal((tail, N_KV, 64), 1.0, 32)
+    tv = gen.normal((tail, N_KV, 64), 1.0, 33)
+    kv = fh.KvSplit.seal(bits, to_dev(k), to_dev(v), prefix_len, cap, N_HEADS, N_KV)
+    kv.append(to_dev(tk), to_dev(tv), tail)
+    q = gen.normal((rows, N_HEADS, 64), 1.0, 34)
+    sinks = gen.uniform(N_HEADS, -2.0, 2.0, 35)
+    got = host(kv.attention_decode(to_dev(q), rows, to_dev(sinks)))
+    pk, vals, gk = oracle_cache(bits, k, v, prefix_len, tk, tv, cap)
+    total = prefix_len + tail
+    want = oracle.attention_decode(q, pk, gk, vals, rows, prefix_len, total, N_HEADS, N_KV, total - rows, 0, 0, sinks)
+    assert np.all(np.isfinite(got))
+    assert max_rel(got, want) <= 1e-5
+    assert np.all(np.abs(got - want) <= 1e-5 * (1 + np.abs(want)))
+    kv.free()
+
+
+def test_config5_decode_over_q8_records(fh):
+    # BASELINE config 5's decode: a 16,320-row prefix, 64 generated
+    # positions, one query row at 16,384 (sampled against the oracle).
+    P, T = 16320, 64
+    k, v = pair_cache(P, N_KV, 41)
+    tk = gen.normal((T, N_KV, 64), 1.0, 42)
+    tv = gen.normal((T, N_KV, 64), 1.0, 43)
+    kv = fh.KvSplit.seal(8, to_dev(k), to_dev(v), P, P + T, N_HEADS, N_KV)
+    kv.append(to_dev(tk), to_dev(tv), T)
+    q = gen.normal((1, N_HEADS, 64), 1.0, 44)
+    sinks = gen.uniform(N_HEADS, -2.0, 2.0, 45)
+    got = host(kv.attention_decode(to_dev(q), 1, to_dev(sinks)))
+    pk, vals, gk = oracle_cache(8, k, v, P, tk, tv, P + T)
+    want = oracle.attention_decode(q, pk, gk, vals, 1, P, P + T, N_HEADS, N_KV, P + T - 1, 0, 0, sinks)
+    assert max_rel(got, want) <= 1e-5
+    bits, plen, tlen, cap, nbytes = kv.info()
+    assert (bits, plen, tlen) == (8, P, T) and nbytes == N_KV * (P * 176 + T * 144)
+    kv.free()

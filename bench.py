@@ -209,7 +209,9 @@ def bench_layer(torch, fh, gen, np, steps=64):
     """one GPTQ INT8 g64 decoder layer (checkpoint shapes:
     dim 768, QKV 768->2048, WO 1024->768, W13 768->4608 + GLU, W2 2304->768;
     16 query / 8 KV heads of 64) prefilled over P = 16,320 rows (image
-    [0, 4096)), then `steps` greedy decode steps growing the cache to 16,384.
+    [0, 4096)), then `steps` greedy decode steps growing the cache to 16,384,
+    first over the compact FP32 cache (Kv::Compact), then over the sealed Q8
+    records (Kv::Q8: the prefill seals the prefix after its attention).
     Prefill stages are timed with HIP events (the layer's phase marks); the
     decode steps are captured into one HIP graph and replayed."""
     P, img, dim, heads, kv = 16384 - steps, 4096, 768, 16, 8
@@ -221,68 +223,88 @@ def bench_layer(torch, fh, gen, np, steps=64):
         scales = gen.uniform((n, k // 64), 1e-4, 4e-4, 31 + 2 * i)
         lins[name] = fh.QuantLinear(8, codes, scales, 64)
     sinks = torch.from_numpy(gen.uniform(heads, -2.0, 2.0, 40)).cuda()
-    layer = fh.DecoderLayer(lins["qkv"], lins["wo"], lins["w13"], lins["w2"], sinks, capacity=P + steps)
     ang = gen.uniform((P + steps, heads, 32), -3.14159, 3.14159, 41)
+    ang[:, 1::2, :16] = ang[:, 0::2, :16]  # 2D RoPE: a GQA pair shares the temporal pairs
     rope = torch.from_numpy(np.stack([np.cos(ang), np.sin(ang)], -1).astype(np.float32)).cuda()
     h0 = torch.from_numpy(gen.normal((P, dim), 1.0, 42)).cuda()
     xs = torch.from_numpy(gen.normal((steps, 1, dim), 1.0, 43)).cuda()
     stream = torch.cuda.current_stream()
-    # Prefill: one untimed pass (allocates the workspace), then a timed one.
-    marks = []
-    clock = lambda stage: marks.append((stage, torch.cuda.Event(enable_timing=True))) or marks[-1][1].record(stream)
-    layer.prefill(h0.clone(), rope[:P], 0, img)
-    h = h0.clone()
-    layer.len = 0
-    torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    layer.prefill(h, rope[:P], 0, img, clock=clock)
-    torch.cuda.synchronize()
-    stage_ms, prev = {}, start
-    for stage, ev in marks:
-        stage_ms[stage] = round(prev.elapsed_time(ev), 4)
-        prev = ev
-    prefill_ms = start.elapsed_time(marks[-1][1])
+    ctx = fh.default_context()
     proj_flop = 2.0 * P * sum(n * k for n, k in shapes.values())
     visible = img * img + sum(q + 1 for q in range(img, P))
     attn_flop = 4.0 * 64 * visible * heads
-    # Decode: a warm step allocates the decode workspace; the cache is then
-    # rewound and the `steps` steps are captured and replayed once.
-    layer.decode(xs[0].clone(), rope[P:P + 1])
-    layer.len = P
-    torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    ctx = fh.default_context()
-    cap = torch.cuda.Stream()
-    cap.wait_stream(stream)
-    with torch.cuda.stream(cap):
-        with torch.cuda.graph(g, stream=cap):
-            ctx.use_stream(torch.cuda.current_stream())
-            for t in range(steps):
-                layer.decode(xs[t], rope[P + t:P + t + 1])
-    stream.wait_stream(cap)
-    ctx.use_stream(stream)
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    g.replay()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    decode_ms = e0.elapsed_time(e1)
-    # Bytes per decode step: the four matrices' GEMV tiles and scales, the
-    # visible keys (prefix keys per query head, generated per KV head) and values.
+    # Bytes per decode step: the four matrices' GEMV tiles and scales plus
+    # the visible cache at the average length.
     w_bytes = sum(n * k + 4 * n * (k // 64) for n, k in shapes.values())
     avg_total = P + (steps + 1) / 2.0
-    kv_bytes = 4 * 64 * (P * heads + (avg_total - P) * kv + avg_total * kv)
-    step_bytes = w_bytes + kv_bytes
+
+    def run(kv_bits):
+        layer = fh.DecoderLayer(lins["qkv"], lins["wo"], lins["w13"], lins["w2"], sinks, capacity=P + steps,
+                                kv_bits=kv_bits)
+        # Prefill: one untimed pass (allocates the workspace), then a timed one.
+        marks = []
+        clock = lambda stage: marks.append((stage, torch.cuda.Event(enable_timing=True))) or \
+            marks[-1][1].record(stream)
+        layer.prefill(h0.clone(), rope[:P], 0, img)
+        h = h0.clone()
+        layer.len = 0
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        layer.prefill(h, rope[:P], 0, img, clock=clock)
+        torch.cuda.synchronize()
+        stage_ms, prev = {}, start
+        for stage, ev in marks:
+            stage_ms[stage] = round(prev.elapsed_time(ev), 4)
+            prev = ev
+        prefill_ms = start.elapsed_time(marks[-1][1])
+        # Decode: a warm step allocates the decode workspace; the cache is
+        # then truncated back to the prompt and the `steps` steps are
+        # captured and replayed once.
+        layer.decode(xs[0].clone(), rope[P:P + 1])
+        layer.truncate(P)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        cap = torch.cuda.Stream()
+        cap.wait_stream(stream)
+        with torch.cuda.stream(cap):
+            with torch.cuda.graph(g, stream=cap):
+                ctx.use_stream(torch.cuda.current_stream())
+                for t in range(steps):
+                    layer.decode(xs[t], rope[P + t:P + t + 1])
+        stream.wait_stream(cap)
+        ctx.use_stream(stream)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        g.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        decode_ms = e0.elapsed_time(e1)
+        if kv_bits == 32:
+            # Prefix keys per query head, generated keys per KV head, values.
+            kv_bytes = 4 * 64 * (P * heads + (avg_total - P) * kv + avg_total * kv)
+            cache_bytes = 4 * 64 * (P + steps) * (heads + 2 * kv)
+        else:
+            # Stored records: 176 bytes per prefix position and group (160
+            # codes, five BF16 steps, padded to 16 bytes), 144 per tail one.
+            _, _, _, _, cache_bytes = layer.split.info()
+            kv_bytes = kv * (P * 176 + (avg_total - P) * 144)
+        step_bytes = w_bytes + kv_bytes
+        del g
+        layer.free()
+        return {"prefill_ms": round(prefill_ms, 3), "prefill_stage_ms": stage_ms,
+                "prefill_tflops": round((proj_flop + attn_flop) / (prefill_ms * 1e-3) / 1e12, 2),
+                "decode_us_per_step": round(decode_ms * 1e3 / steps, 2), "decode_bytes_per_step": int(step_bytes),
+                "decode_gbs": round(step_bytes / (decode_ms * 1e-3 / steps) / 1e9, 1),
+                "cache_bytes": int(cache_bytes)}
+
+    res = {"prefill_rows": P, "decode_steps": steps, "prefill_gflop": round((proj_flop + attn_flop) / 1e9, 2)}
+    res.update(run(32))
+    res["q8"] = run(8)
     for lin in lins.values():
         lin.free()
-    return {"prefill_rows": P, "prefill_ms": round(prefill_ms, 3), "prefill_stage_ms": stage_ms,
-            "prefill_gflop": round((proj_flop + attn_flop) / 1e9, 2),
-            "prefill_tflops": round((proj_flop + attn_flop) / (prefill_ms * 1e-3) / 1e12, 2),
-            "decode_steps": steps, "decode_us_per_step": round(decode_ms * 1e3 / steps, 2),
-            "decode_bytes_per_step": int(step_bytes),
-            "decode_gbs": round(step_bytes / (decode_ms * 1e-3 / steps) / 1e9, 1)}
+    return res
 
 
 def bench_screen(torch, fh, gen, np, reps=40):

@@ -543,6 +543,14 @@ int focr_kv_dequantize(focr_ctx *handle, const focr_kv_split *kv, float *prefix_
   return FOCR_OK;
 }
 
+int focr_kv_truncate_tail(focr_kv_split *kv, size_t tail_len) {
+  KvSplit *s = reinterpret_cast<KvSplit *>(kv);
+  FOCR_REQUIRE(s, FOCR_E_ARG, "focr_kv_truncate_tail: null cache");
+  FOCR_REQUIRE(tail_len <= s->tail_len, FOCR_E_SHAPE, "cannot grow the tail by truncation");
+  s->tail_len = tail_len;
+  return FOCR_OK;
+}
+
 int focr_kv_info(const focr_kv_split *kv, int *bits, size_t *prefix_len, size_t *tail_len, size_t *capacity,
                  size_t *device_bytes) {
   const KvSplit *s = reinterpret_cast<const KvSplit *>(kv);

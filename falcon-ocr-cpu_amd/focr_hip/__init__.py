@@ -78,6 +78,7 @@ SIGNATURES = {
     "focr_kv_append": (_I, [_P, _P, _P, _P, _Z]),
     "focr_kv_attention_decode": (_I, [_P, _P, _P, _Z, _P, _P]),
     "focr_kv_dequantize": (_I, [_P, _P, _P, _P, _P]),
+    "focr_kv_truncate_tail": (_I, [_P, _Z]),
     "focr_kv_info": (_I, [_P, _P, _P, _P, _P, _P]),
     "focr_kv_free": (_I, [_P]),
     "focr_screen_build": (_I, [_P, _P, _Z, _Z, ctypes.POINTER(_P)]),
@@ -497,6 +498,10 @@ class KvSplit:
             out = torch.empty((rows, self.n_heads, 64), dtype=torch.float32, device=q.device)
         _check(lib().focr_kv_attention_decode(self.ctx.handle, self.handle, _dev(q), rows, _dev(sinks), _dev(out)))
         return out
+
+    def truncate_tail(self, tail_len: int) -> None:
+        """`truncate_tail`: forget the generated positions past `tail_len`."""
+        _check(lib().focr_kv_truncate_tail(self.handle, tail_len))
 
     def info(self):
         """(bits, prefix_len, tail_len, capacity, device_bytes)."""

@@ -25,7 +25,12 @@ mod.rs:421-492)::
 
 The compact cache (prefix keys per query head, generated keys and values per
 KV head) lives in device memory sized for `capacity` positions, as
-``Session::new`` sizes the reference's (model/cache.rs:364). RoPE factors
+``Session::new`` sizes the reference's (model/cache.rs:364). With
+``kv_bits`` 8 (Kv::Q8) or 16 (Kv::Q16) the prefill seals the prefix after its
+attention (``seal_layer``, model/cache.rs:218-276) into a `KvSplit`, and decode
+appends each step's keys and values to its tail and attends over the records
+(``LayerCache::Split``); ``kv_bits`` 32 keeps the compact FP32 cache
+(Kv::Compact). RoPE factors
 come from the caller ([rows][n_heads][32][2] cos/sin pairs), as
 ``rotary_factors`` provides them to the reference's row kernels.
 
@@ -36,14 +41,14 @@ from __future__ import annotations
 
 from typing import Optional
 
-from . import (CompactKv, Context, Epilogue, FocrError, Geometry, PrefillOptions, PrefillProjection, attention_with,
-               default_context, qkv_rows, row_scales)
+from . import (CompactKv, Context, Epilogue, FocrError, Geometry, KvSplit, PrefillOptions, PrefillProjection,
+               attention_with, default_context, qkv_rows, row_scales)
 
 
 class DecoderLayer:
     def __init__(self, qkv, wo, w13, w2, sinks, capacity: int, n_heads: int = 16, n_kv_heads: int = 8,
                  head_dim: int = 64, projection: PrefillProjection = PrefillProjection.I16,
-                 options: PrefillOptions = PrefillOptions(), ctx: Optional[Context] = None):
+                 options: PrefillOptions = PrefillOptions(), ctx: Optional[Context] = None, kv_bits: int = 32):
         import torch
 
         self.ctx = ctx or default_context()
@@ -56,8 +61,12 @@ class DecoderLayer:
             raise FocrError(-2, "layer shapes: qkv [qdim + 2 kdim][dim], wo [dim][qdim]")
         if w13.in_dim != self.dim or w2.in_dim != w13.out_dim // 2 or w2.out_dim != self.dim:
             raise FocrError(-2, "layer shapes: w13 [2 ffn][dim], w2 [dim][ffn]")
+        if kv_bits not in (8, 16, 32):
+            raise FocrError(-1, "kv_bits: 32 (compact FP32), 16 (Q16) or 8 (Q8)")
         self.projection, self.options = projection, options
         self.capacity = capacity
+        self.kv_bits = kv_bits
+        self.split: Optional[KvSplit] = None
         dev = f"cuda:{self.ctx.device}"
         f32 = torch.float32
         self.prefix_k = torch.empty((capacity, n_heads, head_dim), dtype=f32, device=dev)
@@ -99,6 +108,9 @@ class DecoderLayer:
             raise FocrError(-2, "attention image must be inside the prefix")
         ctx = self.ctx
         mark = clock or (lambda stage: None)
+        if self.split is not None:
+            self.split.free()
+            self.split = None
         rs = row_scales(h, self.dim, out=self._buf("rs", (rows,)), ctx=ctx)
         qkv = self.qkv.prefill(h, rows, row_scale=rs, epilogue=Epilogue.STORE, kernel=self.projection,
                                out=self._buf("qkv", (rows, self.qkv.out_dim)))
@@ -111,6 +123,10 @@ class DecoderLayer:
         attn = attention_with(q, self.kv(rows), rows, Geometry(0, image_start, image_end), self.sinks, self.options,
                               output=self._buf("attn", (rows, self.n_heads, 64)), ctx=ctx)
         mark("attention")
+        if self.kv_bits != 32:
+            self.split = KvSplit.seal(self.kv_bits, self.prefix_k[:rows], self.v[:rows], rows, self.capacity,
+                                      self.n_heads, self.n_kv_heads, ctx=ctx)
+            mark("seal")
         self.wo.prefill(attn, rows, epilogue=Epilogue.ADD, out=h, kernel=self.projection)
         mark("wo")
         rs = row_scales(h, self.dim, out=rs, ctx=ctx)
@@ -134,12 +150,22 @@ class DecoderLayer:
         mark = clock or (lambda stage: None)
         qkv = self.qkv.linear_ex(h, rows, rms_norm=True, out=self._buf("dqkv", (rows, self.qkv.out_dim)))
         mark("qkv")
-        q = qkv_rows(qkv, rows, rope, self.n_heads, self.n_kv_heads, 0, q=self._buf("dq", (rows, self.n_heads, 64)),
-                     generated_k=self.generated_k[pos - p: pos - p + rows], v=self.v[pos: pos + rows], ctx=ctx)
-        mark("qkv_rows")
         total = pos + rows
-        attn = attention_with(q, self.kv(total), rows, Geometry(pos, *self.image), self.sinks, self.options,
-                              output=self._buf("dattn", (rows, self.n_heads, 64)), ctx=ctx)
+        out = self._buf("dattn", (rows, self.n_heads, 64))
+        if self.split is None:
+            q = qkv_rows(qkv, rows, rope, self.n_heads, self.n_kv_heads, 0, q=self._buf("dq", (rows, self.n_heads, 64)),
+                         generated_k=self.generated_k[pos - p: pos - p + rows], v=self.v[pos: pos + rows], ctx=ctx)
+            mark("qkv_rows")
+            attn = attention_with(q, self.kv(total), rows, Geometry(pos, *self.image), self.sinks, self.options,
+                                  output=out, ctx=ctx)
+        else:
+            k = self._buf("dk", (rows, self.n_kv_heads, 64))
+            v = self._buf("dv", (rows, self.n_kv_heads, 64))
+            q = qkv_rows(qkv, rows, rope, self.n_heads, self.n_kv_heads, 0, q=self._buf("dq", (rows, self.n_heads, 64)),
+                         generated_k=k, v=v, ctx=ctx)
+            mark("qkv_rows")
+            self.split.append(k, v, rows)
+            attn = self.split.attention_decode(q, rows, self.sinks, out=out)
         mark("attention")
         self.wo.linear_ex(attn, rows, epilogue=Epilogue.ADD, out=h)
         mark("wo")
@@ -150,3 +176,19 @@ class DecoderLayer:
         mark("w2")
         self.len = total
         return h
+
+    def truncate(self, length: int) -> None:
+        """``Session::truncate`` (model/cache.rs:281-298): drop the newest
+        positions so that `length` remain (rejected draft tokens); the prompt
+        stays. A sealed cache forgets its tail past them; the compact cache
+        overwrites them on the next decode."""
+        if not (self.prefix_len <= length <= self.len) or self.len == 0:
+            raise FocrError(-2, "truncation must keep the prompt")
+        if self.split is not None:
+            self.split.truncate_tail(length - self.prefix_len)
+        self.len = length
+
+    def free(self) -> None:
+        if self.split is not None:
+            self.split.free()
+            self.split = None

@@ -269,6 +269,11 @@ int focr_kv_attention_decode(focr_ctx *ctx, const focr_kv_split *kv, const float
  * generated keys [tail_len][n_kv_heads][64]. */
 int focr_kv_dequantize(focr_ctx *ctx, const focr_kv_split *kv, float *prefix_k_dev, float *values_dev,
                        float *generated_k_dev);
+/* SplitPrefix::truncate_tail (src/quant/kv.rs:845-849): forgets the generated
+ * positions past tail_len (rejected draft tokens; Session::truncate, src/model/
+ * cache.rs:281-298); the next append overwrites them. Host state only, no
+ * device work. FOCR_E_SHAPE if tail_len exceeds the stored tail. */
+int focr_kv_truncate_tail(focr_kv_split *kv, size_t tail_len);
 int focr_kv_info(const focr_kv_split *kv, int *bits, size_t *prefix_len, size_t *tail_len,
                  size_t *capacity, size_t *device_bytes);
 int focr_kv_free(focr_kv_split *kv);

@@ -22,9 +22,14 @@ def fh():
     return focr_hip
 
 
-def rope_table(rows, seed):
+def rope_table(rows, seed, paired=False):
+    """[rows][H][32] (cos, sin) pairs; `paired`: the temporal pairs 0..16 of
+    both heads of a GQA pair agree, as the checkpoint's 2D RoPE makes them (the
+    sealed cache stores that half once per pair and refuses otherwise)."""
     rng = np.random.default_rng(seed)
     ang = rng.uniform(-3.2, 3.2, size=(rows, H, 32))
+    if paired:
+        ang[:, 1::2, :16] = ang[:, 0::2, :16]
     return np.ascontiguousarray(np.stack([np.cos(ang), np.sin(ang)], -1).astype(np.float32))
 
 
@@ -259,5 +264,64 @@ def test_decoder_layer_prefill_and_decode(fh):
         assert_bitwise(host(layer.v[pos: pos + m]), new_v, f"step {step} values")
         close(host(layer._buf("dattn", (m, H, 64))), want_attn)
         assert max_rel(host(x), want_x) <= 1e-4, step
+    for lin in lins.values():
+        lin.free()
+
+
+@pytest.mark.parametrize("bits", [8, 16])
+def test_decoder_layer_over_the_sealed_cache(fh, bits):
+    """Kv::Q8 / Kv::Q16: the prefill seals the prefix after its attention
+    (seal_layer, model/cache.rs:218-276); decode appends to the tail and
+    attends over the records; a truncation drops rejected drafts
+    (Session::truncate, model/cache.rs:281-298). The oracle runs the same
+    steps over the oracle's decoded records."""
+    import torch
+
+    rows, image, cap = 200, (0, 120), 220
+    w = layer_weights(50)
+    lins = {name: fh.QuantLinear(8, *w[name], 64) for name in w}
+    sinks = gen.uniform(H, -2.0, 2.0, 51)
+    layer = fh.DecoderLayer(lins["qkv"], lins["wo"], lins["w13"], lins["w2"], to_dev(sinks), capacity=cap,
+                            kv_bits=bits)
+    h0 = gen.normal((rows, DIM), 1.0, 52)
+    rope = rope_table(rows, 53, paired=True)
+    h = to_dev(h0)
+    layer.prefill(h, to_dev(rope), *image)
+    want_h, _, want_pk, want_v, _ = oracle_layer_prefill(w, h0, rope, image, sinks)
+    torch.cuda.synchronize()
+    assert max_rel(host(h), want_h) <= 1e-4
+    sealed = oracle.kv_seal(bits, want_pk, want_v, rows, H, G)
+    assert not isinstance(sealed, int), sealed
+    tail = oracle.kv_tail(bits, G, cap - rows)
+    tail_len = 0
+    assert layer.split.info()[:4] == (bits, rows, 0, cap)
+    dec = lambda name, x, m, glu=False: (oracle.linear_decode_glu if glu else oracle.linear_decode)(
+        8, *w[name], w[name][0].shape[0], w[name][0].shape[1], 64, x, m)
+    for step, (m, drop) in enumerate([(1, 0), (5, 3), (1, 0), (8, 2), (2, 0)]):
+        x0 = gen.normal((m, DIM), 1.0, 80 + step)
+        rope_m = rope_table(m, 90 + step, paired=True)
+        x = to_dev(x0)
+        layer.decode(x, to_dev(rope_m))
+        qkv = dec("qkv", x0 * oracle.row_scales(x0, DIM)[:, None], m)
+        q, _, new_k, new_v = oracle.qkv_rows(qkv, m, rope_m, H, G, 0)
+        for i in range(m):
+            oracle.kv_push(bits, new_k[i], new_v[i], G, cap - rows, tail_len + i, tail)
+        tail_len += m
+        pk, vals, gk = oracle.kv_dequantize(bits, sealed, rows, H, G, tail, cap - rows, tail_len)
+        total = rows + tail_len
+        want_attn = oracle.attention_decode(q, pk, gk, vals, m, rows, total, H, G, total - m, image[0], image[1],
+                                            sinks)
+        close(host(layer._buf("dattn", (m, H, 64))), want_attn)
+        want_x = x0 + dec("wo", want_attn.reshape(m, -1), m)
+        gated = dec("w13", want_x * oracle.row_scales(want_x, DIM)[:, None], m, glu=True)
+        want_x = want_x + dec("w2", gated, m)
+        assert max_rel(host(x), want_x) <= 1e-4, step
+        if drop:
+            layer.truncate(layer.len - drop)
+            tail_len -= drop
+        assert layer.split.info()[2] == tail_len and layer.len == rows + tail_len
+    with pytest.raises(fh.FocrError):
+        layer.truncate(rows - 1)  # the prompt stays
+    layer.free()
     for lin in lins.values():
         lin.free()

@@ -101,8 +101,17 @@ static __global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgs 
   den = wave_sum(den);
   if (lane == 0) s_red[wave] = den;
   __syncthreads();
+  // Sixteen of the wave's chunks load before their products are added (in
+  // chunk order), so the loads' latencies overlap.
   float o = 0.0f;
   int c = wave;
+  for (; c + 60 < a.chunks; c += 64) {
+    float ov[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) ov[i] = po[static_cast<size_t>(c + 4 * i) * 64 + lane];
+#pragma unroll
+    for (int i = 0; i < 16; i++) o = fmaf_(ov[i], s_f[c + 4 * i], o);
+  }
   for (; c + 12 < a.chunks; c += 16) {
     const float o0 = po[static_cast<size_t>(c) * 64 + lane], o1 = po[static_cast<size_t>(c + 4) * 64 + lane];
     const float o2 = po[static_cast<size_t>(c + 8) * 64 + lane], o3 = po[static_cast<size_t>(c + 12) * 64 + lane];

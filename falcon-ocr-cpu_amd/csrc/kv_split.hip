@@ -16,12 +16,17 @@
 // 144 bytes; Q16: 336 and 272). Prefix records [group][position], tail
 // records [group][capacity].
 //
-// Decode: one wave task per (group, key chunk) serves both heads of the pair
-// (the record is read once for both), with the compact decode kernel's lane
-// map (lane group lg = lane / 16 takes keys 4i + lg, lane lp = lane % 16 dims
-// 4lp..4lp+3): lanes 0-7 read the temporal codes, lanes 8-15 both spatial
-// halves, all 16 the value. Online softmax per (head, row) over the chunk,
-// then the shared combine kernel. Roofline: HBM; bytes per call = the visible
+// Seal and append code one element per lane (a 32-element block is one
+// half-wave; its absmax is a lane exchange), so a decode step's append is a
+// single short kernel.
+//
+// Decode: one workgroup task per (group, key chunk) serves both heads of the
+// pair (the record is read once for both); its four waves take interleaved
+// 16-key iterations with the compact decode kernel's lane map (lane group
+// lg = lane / 16 takes keys 4i + lg, lane lp = lane % 16 dims 4lp..4lp+3),
+// every lane reading its codes at offsets selected without branches. Online
+// softmax per (head, row), the four waves merged in a fixed order through
+// LDS, then the shared combine kernel. Roofline: HBM; bytes per call = the visible
 // records (Q8: 176 bytes per group and prefix position, 8 groups = 1,408
 // bytes per position against 6,144 for the FP32 compact cache).
 #include <vector>
@@ -57,17 +62,6 @@ __device__ __forceinline__ uint16_t bf16_up(float scale) {
   return (bits & 0xFFFFu) ? static_cast<uint16_t>(high + 1) : high;
 }
 
-// The step of a 32-element block (q8_scale / q16_scale): absmax / limit in
-// f64 rounded to f32, at least the smallest subnormal, 0 for a zero block.
-__device__ __forceinline__ float block_step(const float *x, double limit) {
-  float max = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 32; i++) max = __builtin_fmaxf(max, fabsf(x[i]));
-  if (max == 0.0f) return 0.0f;
-  const float s = static_cast<float>(static_cast<double>(max) / limit);
-  return s > 1.40129846e-45f ? s : 1.40129846e-45f;
-}
-
 // round_clamped(value / step): clamp to +-limit in f64, round to nearest
 // even; NaN gives 0 (Rust's saturating cast); a zero step gives 0.
 __device__ __forceinline__ int code_of(float value, float step, double limit) {
@@ -78,18 +72,30 @@ __device__ __forceinline__ int code_of(float value, float step, double limit) {
   return static_cast<int>(rint(x));
 }
 
-template <typename C>
-__device__ __forceinline__ void code_block(const float *x, double limit, C *codes, uint16_t *step_out, bool nan_step,
-                                           bool *overflow) {
-  const uint16_t stored = bf16_up(nan_step ? __builtin_nanf("") : block_step(x, limit));
-  *step_out = stored;
-  const float step = bf16_widen(stored);
+// Codes one 32-element block held by the 32 lanes of a half-wave (lane & 31
+// = element; every lane of the wave takes part in the exchanges). The step
+// (q8_scale / q16_scale) is absmax / limit in f64 rounded to f32, at least
+// the smallest subnormal, 0 for an all-zero block, stored as the smallest
+// BF16 at or above it; `nan_step` stores the NaN pattern instead. The max is
+// exact, so the exchange order does not matter. Returns the code; `step`
+// receives the stored BF16.
+__device__ __forceinline__ int code_lane(float x, bool nan_step, double limit, uint16_t &stored) {
+  float mx = __builtin_fmaxf(0.0f, fabsf(x));  // a NaN element counts as 0
 #pragma unroll
-  for (int i = 0; i < 32; i++) {
-    const int c = code_of(x[i], step, limit);
-    codes[i] = static_cast<C>(c);
-    if (overflow && !__builtin_isfinite(static_cast<float>(c) * step)) *overflow = true;
+  for (int mask = 1; mask < 32; mask *= 2) mx = __builtin_fmaxf(mx, xor_lane(mx, mask));
+  float step = 0.0f;
+  if (mx != 0.0f) {
+    step = static_cast<float>(static_cast<double>(mx) / limit);
+    step = step > 1.40129846e-45f ? step : 1.40129846e-45f;
   }
+  stored = bf16_up(nan_step ? __builtin_nanf("") : step);
+  return code_of(x, bf16_widen(stored), limit);
+}
+
+// Whether any lane of this lane's half-wave has `pred` set.
+__device__ __forceinline__ bool half_any(bool pred) {
+  const unsigned long long b = __ballot(pred);
+  return ((b >> (threadIdx.x & 32)) & 0xffffffffull) != 0;
 }
 
 enum : uint32_t { kErrPair = 1, kErrNonFinite = 2, kErrOverflow = 4 };
@@ -101,36 +107,33 @@ struct SealArgs {
   int prefix_len, n_heads, n_kv, record_bytes;
 };
 
-// One thread per (record, block): gathers the block's 32 values, checks the
-// pair sharing (block 0) and finiteness, codes them.
+// One lane per record element (group-major records of 160 = 5 blocks of 32,
+// so every block is one aligned half-wave): gathers the element, checks the
+// pair sharing (block 0) and finiteness, codes it.
 template <typename C>
 __global__ __launch_bounds__(256) void seal_kernel(SealArgs a) {
   const long idx = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
-  const long total = static_cast<long>(a.n_kv) * a.prefix_len * 5;
-  if (idx >= total) return;
-  const int blk = static_cast<int>(idx % 5);
-  const long record = idx / 5;
+  const long total = static_cast<long>(a.n_kv) * a.prefix_len * kRecord;
+  const bool valid = idx < total;
+  const long record = valid ? idx / kRecord : 0;
+  const int e = static_cast<int>(idx % kRecord);
   const int g = static_cast<int>(record / a.prefix_len), t = static_cast<int>(record % a.prefix_len);
   const float *ka = a.k + (static_cast<size_t>(t) * a.n_heads + 2 * g) * 64;
-  const float *src = blk == 0 ? ka : blk == 1 ? ka + 32 : blk == 2 ? ka + 64 + 32
-                   : a.v + (static_cast<size_t>(t) * a.n_kv + g) * 64 + 32 * (blk - 3);
-  float x[32];
+  const float *src = e < 64 ? ka + e : e < 96 ? ka + 32 + e : a.v + (static_cast<size_t>(t) * a.n_kv + g) * 64 + e - 96;
+  const float x = valid ? *src : 0.0f;
   uint32_t err = 0;
-#pragma unroll
-  for (int i = 0; i < 32; i++) {
-    x[i] = src[i];
-    if (!__builtin_isfinite(x[i])) err |= kErrNonFinite;
+  if (valid && !__builtin_isfinite(x)) err |= kErrNonFinite;
+  if (valid && e < 32 && __float_as_uint(x) != __float_as_uint(ka[64 + e])) err |= kErrPair;
+  uint16_t stored;
+  const double limit = sizeof(C) == 1 ? 127.0 : 32767.0;
+  const int code = code_lane(x, false, limit, stored);
+  if (valid) {
+    unsigned char *rec = a.records + static_cast<size_t>(record) * a.record_bytes;
+    reinterpret_cast<C *>(rec)[e] = static_cast<C>(code);
+    if ((e & 31) == 0) reinterpret_cast<uint16_t *>(rec + kRecord * sizeof(C))[e >> 5] = stored;
+    if (!__builtin_isfinite(static_cast<float>(code) * bf16_widen(stored))) err |= kErrOverflow;
+    if (err) atomicOr(a.error, err);
   }
-  if (blk == 0)
-    for (int i = 0; i < 32; i++)
-      if (__float_as_uint(ka[i]) != __float_as_uint(ka[64 + i])) err |= kErrPair;
-  unsigned char *rec = a.records + static_cast<size_t>(record) * a.record_bytes;
-  C *codes = reinterpret_cast<C *>(rec) + 32 * blk;
-  uint16_t *steps = reinterpret_cast<uint16_t *>(rec + kRecord * sizeof(C));
-  bool overflow = false;
-  code_block<C>(x, sizeof(C) == 1 ? 127.0 : 32767.0, codes, steps + blk, false, &overflow);
-  if (overflow) err |= kErrOverflow;
-  if (err) atomicOr(a.error, err);
 }
 
 struct AppendArgs {
@@ -139,24 +142,23 @@ struct AppendArgs {
   int n_kv, tail_capacity, first, rows, tail_bytes;
 };
 
-// One thread per (row, group, block) of the appended positions.
+// One lane per tail-record element (128 = 4 blocks, so the grid is whole
+// waves): a block holding a non-finite value is coded against the NaN step.
 template <typename C>
 __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
   const int idx = blockIdx.x * 256 + threadIdx.x;
-  if (idx >= a.rows * a.n_kv * 4) return;
-  const int blk = idx % 4, g = (idx / 4) % a.n_kv, r = idx / (4 * a.n_kv);
-  const float *src = (blk < 2 ? a.k : a.v) + (static_cast<size_t>(r) * a.n_kv + g) * 64 + 32 * (blk & 1);
-  float x[32];
-  bool finite = true;
-#pragma unroll
-  for (int i = 0; i < 32; i++) {
-    x[i] = src[i];
-    finite = finite && __builtin_isfinite(x[i]);
+  const bool valid = idx < a.rows * a.n_kv * kTail;
+  const int e = idx % kTail, g = (idx / kTail) % a.n_kv, r = idx / (kTail * a.n_kv);
+  const float *src = (e < 64 ? a.k + e : a.v + e - 64) + (static_cast<size_t>(r) * a.n_kv + g) * 64;
+  const float x = valid ? *src : 0.0f;
+  const bool nonfinite = half_any(!__builtin_isfinite(x));
+  uint16_t stored;
+  const int code = code_lane(x, nonfinite, sizeof(C) == 1 ? 127.0 : 32767.0, stored);
+  if (valid) {
+    unsigned char *rec = a.tail + (static_cast<size_t>(g) * a.tail_capacity + a.first + r) * a.tail_bytes;
+    reinterpret_cast<C *>(rec)[e] = static_cast<C>(code);
+    if ((e & 31) == 0) reinterpret_cast<uint16_t *>(rec + kTail * sizeof(C))[e >> 5] = stored;
   }
-  unsigned char *rec = a.tail + (static_cast<size_t>(g) * a.tail_capacity + a.first + r) * a.tail_bytes;
-  C *codes = reinterpret_cast<C *>(rec) + 32 * blk;
-  uint16_t *steps = reinterpret_cast<uint16_t *>(rec + kTail * sizeof(C));
-  code_block<C>(x, sizeof(C) == 1 ? 127.0 : 32767.0, codes, steps + blk, !finite, nullptr);
 }
 
 struct DequantArgs {
@@ -230,45 +232,52 @@ __device__ __forceinline__ float4 codes4(const unsigned char *p) {
 
 __device__ __forceinline__ float4 scale4(float4 c, float s) { return make_float4(c.x * s, c.y * s, c.z * s, c.w * s); }
 
-// A key's (both heads') and value's decoded values for lane lp.
+// A key's (both heads') and value's decoded values for lane lp (dims
+// 4lp..4lp+3 of each 64-wide head). Branch-free over the record kind: in a
+// prefix record head 2g's key is codes [0, 64) (T then S(2g)) and head
+// 2g+1's is T then S(2g+1) = codes [64, 96); a tail record holds one key
+// [0, 64) for both heads. The BF16 steps follow the codes, 16-byte aligned.
 struct KeyVal {
   float4 k0, k1, v;
 };
 
+__device__ __forceinline__ float step_of(uint4 w, int i) {
+  const uint32_t word = i < 2 ? w.x : i < 4 ? w.y : i < 6 ? w.z : w.w;
+  return bf16_widen(static_cast<uint16_t>((i & 1) ? word >> 16 : word & 0xffffu));
+}
+
 template <typename C>
 __device__ __forceinline__ KeyVal load_key(const SplitDecArgs &a, int g, int j, int lp) {
+  const bool prefix = j < a.prefix_len;
+  const unsigned char *rec =
+      prefix ? a.records + (static_cast<size_t>(g) * a.prefix_len + j) * a.record_bytes
+             : a.tail + (static_cast<size_t>(g) * a.tail_capacity + (j - a.prefix_len)) * a.tail_bytes;
+  const int hi = lp >> 3;
+  const int k1_at = prefix ? 4 * lp + 32 * hi : 4 * lp;
+  const int v_at = (prefix ? 96 : 64) + 4 * lp;
+  const uint4 steps = *reinterpret_cast<const uint4 *>(rec + (prefix ? kRecord : kTail) * sizeof(C));
+  const float4 c0 = codes4<C>(rec + 4 * lp * sizeof(C));
+  const float4 c1 = codes4<C>(rec + k1_at * sizeof(C));
+  const float4 cv = codes4<C>(rec + v_at * sizeof(C));
   KeyVal kv;
-  if (j < a.prefix_len) {
-    const unsigned char *rec = a.records + (static_cast<size_t>(g) * a.prefix_len + j) * a.record_bytes;
-    const uint16_t *steps = reinterpret_cast<const uint16_t *>(rec + kRecord * sizeof(C));
-    if (lp < 8) {
-      kv.k0 = scale4(codes4<C>(rec + 4 * lp * sizeof(C)), bf16_widen(steps[0]));
-      kv.k1 = kv.k0;
-    } else {
-      kv.k0 = scale4(codes4<C>(rec + (32 + 4 * (lp - 8)) * sizeof(C)), bf16_widen(steps[1]));
-      kv.k1 = scale4(codes4<C>(rec + (64 + 4 * (lp - 8)) * sizeof(C)), bf16_widen(steps[2]));
-    }
-    kv.v = scale4(codes4<C>(rec + (96 + 4 * lp) * sizeof(C)), bf16_widen(steps[3 + (lp >> 3)]));
-  } else {
-    const unsigned char *rec =
-        a.tail + (static_cast<size_t>(g) * a.tail_capacity + (j - a.prefix_len)) * a.tail_bytes;
-    const uint16_t *steps = reinterpret_cast<const uint16_t *>(rec + kTail * sizeof(C));
-    kv.k0 = scale4(codes4<C>(rec + 4 * lp * sizeof(C)), bf16_widen(steps[lp >> 3]));
-    kv.k1 = kv.k0;
-    kv.v = scale4(codes4<C>(rec + (64 + 4 * lp) * sizeof(C)), bf16_widen(steps[2 + (lp >> 3)]));
-  }
+  kv.k0 = scale4(c0, step_of(steps, hi));
+  kv.k1 = scale4(c1, step_of(steps, prefix ? 2 * hi : hi));
+  kv.v = scale4(cv, step_of(steps, (prefix ? 3 : 2) + hi));
   return kv;
 }
 
 constexpr int kKpl = 4;  // keys per lane group per iteration (16 per wave)
 
-// M: query rows. Task = (group g, chunk c); heads 2g and 2g + 1.
+// M: query rows. One workgroup per task (group g, key chunk c) serves heads
+// 2g and 2g + 1: wave w takes the chunk's 16-key iterations w, w + 4, ...,
+// and the four waves' states are merged in a fixed order through LDS.
 template <typename C, int M>
 __global__ __launch_bounds__(256) void split_partial_kernel(SplitDecArgs a, int iters, int rows) {
+  __shared__ float4 s_o[kWaves][2][M][16];
+  __shared__ float2 s_md[kWaves][2][M];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int lg = lane >> 4, lp = lane & 15;
-  const int task = blockIdx.x * kWaves + wave;
-  if (task >= a.tasks) return;
+  const int task = blockIdx.x;
   const int c = task % a.chunks, g = task / a.chunks;
   const int key0 = c * iters * 4 * kKpl;
   int vis[M], limit = 0;
@@ -343,15 +352,13 @@ __global__ __launch_bounds__(256) void split_partial_kernel(SplitDecArgs a, int 
         }
       }
   };
-  KeyVal ka[kKpl], kb[kKpl];
-  load(ka, 0);
-  for (int it = 0; it < iters; it += 2) {
-    if (it + 1 < iters) load(kb, it + 1);
-    consume(ka, it);
-    if (it + 1 < iters) {
-      if (it + 2 < iters) load(ka, it + 2);
-      consume(kb, it + 1);
-    }
+  // iters is a multiple of kWaves: every wave takes iters / kWaves
+  // iterations (one at the usual chunk of 64 keys). Single-buffered: the
+  // latency is hidden by the other resident waves, not by registers.
+  for (int it = wave; it < iters; it += kWaves) {
+    KeyVal kb[kKpl];
+    load(kb, it);
+    consume(kb, it);
   }
 #pragma unroll
   for (int e = 0; e < 2; e++)
@@ -364,22 +371,41 @@ __global__ __launch_bounds__(256) void split_partial_kernel(SplitDecArgs a, int 
                                       xor_lane(o[e][r].z, mask), xor_lane(o[e][r].w, mask));
         merge(m[e][r], den[e][r], o[e][r], m2, d2, o2);
       }
-      const size_t slot = (static_cast<size_t>(r) * a.n_heads + 2 * g + e) * a.chunks + c;
-      if (lg == 0) *reinterpret_cast<float4 *>(a.part_o + slot * 64 + 4 * lp) = o[e][r];
-      if (lane == 0) *reinterpret_cast<float2 *>(a.part_md + slot * 2) = make_float2(m[e][r], den[e][r]);
+      if (lg == 0) s_o[wave][e][r][lp] = o[e][r];
+      if (lane == 0) s_md[wave][e][r] = make_float2(m[e][r], den[e][r]);
     }
+  __syncthreads();
+  // Wave w's lanes 16e' + lp merge the four waves for (head e, rows r = w,
+  // w + 4): lane group lg < 2 is the head.
+  if (lg >= 2) return;
+  const int e = lg;
+#pragma unroll
+  for (int r = 0; r < M; r++) {
+    if (r % kWaves != wave) continue;
+    float2 md = s_md[0][e][r];
+    float4 acc = s_o[0][e][r][lp];
+#pragma unroll
+    for (int w = 1; w < kWaves; w++) {
+      const float2 md2 = s_md[w][e][r];
+      merge(md.x, md.y, acc, md2.x, md2.y, s_o[w][e][r][lp]);
+    }
+    const size_t slot = (static_cast<size_t>(r) * a.n_heads + 2 * g + e) * a.chunks + c;
+    *reinterpret_cast<float4 *>(a.part_o + slot * 64 + 4 * lp) = acc;
+    if (lp == 0) *reinterpret_cast<float2 *>(a.part_md + slot * 2) = md;
+  }
 }
 
 template <typename C, int M>
 int launch_split(Ctx *ctx, SplitDecArgs a, int rows, const float *sinks, float *out) {
-  // Keys per wave task: about 2048 tasks over the chip (each serves two
-  // heads), at most kMaxChunks chunks, whole 16-key iterations.
+  // Keys per workgroup task: about 2048 tasks over the chip (each serves two
+  // heads), at most kMaxChunks chunks, whole multiples of 64 keys (every
+  // wave of the task takes the same number of 16-key iterations).
   const long limit = a.last;
   const long want = (limit * a.n_kv + 2047) / 2048;
-  long per = (want + 15) / 16 * 16;
-  const long min_per = ((limit + kMaxChunks - 1) / kMaxChunks + 15) / 16 * 16;
+  long per = (want + 63) / 64 * 64;
+  const long min_per = ((limit + kMaxChunks - 1) / kMaxChunks + 63) / 64 * 64;
   if (per < min_per) per = min_per;
-  if (per < 16) per = 16;
+  if (per < 64) per = 64;
   const int iters = static_cast<int>(per / 16);
   a.chunks = static_cast<int>((limit + per - 1) / per);
   a.tasks = a.n_kv * a.chunks;
@@ -388,8 +414,7 @@ int launch_split(Ctx *ctx, SplitDecArgs a, int rows, const float *sinks, float *
   if (rc != FOCR_OK) return rc;
   a.part_o = static_cast<float *>(ctx->scratch);
   a.part_md = a.part_o + slots * 64;
-  hipLaunchKernelGGL((split_partial_kernel<C, M>), dim3((a.tasks + kWaves - 1) / kWaves), dim3(64 * kWaves), 0,
-                     ctx->stream, a, iters, rows);
+  hipLaunchKernelGGL((split_partial_kernel<C, M>), dim3(a.tasks), dim3(64 * kWaves), 0, ctx->stream, a, iters, rows);
   FOCR_HIP_CHECK(hipGetLastError());
   CombineArgs cb;
   cb.part_o = a.part_o;
@@ -435,6 +460,8 @@ int focr_kv_seal(focr_ctx *handle, int bits, const float *prefix_k, const float 
                "split cache requires Falcon 64-wide paired GQA heads");
   FOCR_REQUIRE(prefix_len > 0 && capacity >= prefix_len && capacity < (size_t(1) << 30), FOCR_E_SHAPE,
                "invalid split-prefix capacity");
+  FOCR_REQUIRE(prefix_len * n_kv_heads * kRecord / 256 < (size_t(1) << 31), FOCR_E_SHAPE,
+               "split prefix too long for one seal launch");
   FOCR_HIP_CHECK(hipSetDevice(ctx->device));
   KvSplit *s = new KvSplit();
   s->bits = bits;
@@ -458,8 +485,9 @@ int focr_kv_seal(focr_ctx *handle, int bits, const float *prefix_k, const float 
   s->device_bytes = rec_total + tail_total;
   SealArgs a{prefix_k, v, s->records, s->error, static_cast<int>(prefix_len), s->n_heads, s->n_kv,
              static_cast<int>(s->record_bytes)};
-  const long threads = static_cast<long>(n_kv_heads) * prefix_len * 5;
+  const long threads = static_cast<long>(n_kv_heads) * prefix_len * kRecord;
   const dim3 grid(static_cast<unsigned>((threads + 255) / 256));
+  static_assert(kRecord % 32 == 0 && kTail % 64 == 0, "blocks are whole half-waves");
   if (bits == 8)
     hipLaunchKernelGGL(seal_kernel<int8_t>, grid, dim3(256), 0, ctx->stream, a);
   else
@@ -491,7 +519,7 @@ int focr_kv_append(focr_ctx *handle, focr_kv_split *kv, const float *k, const fl
   FOCR_HIP_CHECK(hipSetDevice(ctx->device));
   AppendArgs a{k, v, s->tail, s->n_kv, static_cast<int>(s->capacity - s->prefix_len), static_cast<int>(s->tail_len),
                static_cast<int>(rows), static_cast<int>(s->tail_bytes)};
-  const int threads = static_cast<int>(rows) * s->n_kv * 4;
+  const int threads = static_cast<int>(rows) * s->n_kv * kTail;
   if (s->bits == 8)
     hipLaunchKernelGGL(append_kernel<int8_t>, dim3((threads + 255) / 256), dim3(256), 0, ctx->stream, a);
   else

@@ -17,7 +17,7 @@
 // reference's.
 //
 // One workgroup of 4 waves per row; each wave normalizes and rotates whole
-// heads, lane = element. The 64-wide pairwise sum is two 32-leaves folded
+// heads, lane = element, loading up to 8 heads before computing any. The 64-wide pairwise sum is two 32-leaves folded
 // 16-8-4-2-1 (xor butterflies: lane i < w adds lane i + w, the other lanes'
 // values are never read) and then leaf0 + leaf1.
 //
@@ -67,26 +67,56 @@ __global__ __launch_bounds__(256) void qkv_rows_kernel(RowArgs a) {
   const float2 *rope = reinterpret_cast<const float2 *>(a.rope) + static_cast<size_t>(row) * a.n_heads * 32;
   const bool prefix = row < a.prefix_rows;
   // Jobs: n_heads query heads, then the key heads (n_heads expanded ones for
-  // a prefix row, n_kv_heads unique ones for a generated row).
+  // a prefix row, n_kv_heads unique ones for a generated row). Job j reads
+  // element `lane` of its source head and its rope factor pair; the first
+  // kHoist jobs of a wave load before any computes, so their latencies
+  // overlap (a decode row has 24 jobs, a prefill row 32: at most 8 a wave).
   const int key_jobs = prefix ? a.n_heads : a.n_kv_heads;
   const int jobs = a.n_heads + key_jobs;
-  for (int job = wave; job < jobs; job += 4) {
+  auto source = [&](int job, int &x_at, int &f_at) {
     if (job < a.n_heads) {
-      const int h = job;
-      const float y = norm_rope(src[h * 64 + lane], rope[h * 32 + lane / 2], lane);
-      a.q[static_cast<size_t>(row) * qdim + h * 64 + lane] = y;
+      x_at = job * 64;
+      f_at = job * 32;
     } else if (prefix) {
       const int h = job - a.n_heads;  // expanded key head: KV head h / repeat
-      const float y = norm_rope(src[qdim + (h / repeat) * 64 + lane], rope[h * 32 + lane / 2], lane);
-      a.prefix_k[static_cast<size_t>(row) * qdim + h * 64 + lane] = y;
+      x_at = qdim + (h / repeat) * 64;
+      f_at = h * 32;
     } else {
       const int g = job - a.n_heads;  // unique key head g = expanded head g * repeat
-      const float y = norm_rope(src[qdim + g * 64 + lane], rope[g * repeat * 32 + lane / 2], lane);
-      a.generated_k[static_cast<size_t>(row - a.prefix_rows) * kdim + g * 64 + lane] = y;
+      x_at = qdim + g * 64;
+      f_at = g * repeat * 32;
+    }
+  };
+  auto dest = [&](int job) -> float * {
+    if (job < a.n_heads) return a.q + static_cast<size_t>(row) * qdim + job * 64;
+    if (prefix) return a.prefix_k + static_cast<size_t>(row) * qdim + (job - a.n_heads) * 64;
+    return a.generated_k + static_cast<size_t>(row - a.prefix_rows) * kdim + (job - a.n_heads) * 64;
+  };
+  constexpr int kHoist = 8;
+  float xs[kHoist];
+  float2 fs[kHoist];
+#pragma unroll
+  for (int i = 0; i < kHoist; i++) {
+    const int job = wave + 4 * i;
+    if (job < jobs) {
+      int x_at, f_at;
+      source(job, x_at, f_at);
+      xs[i] = src[x_at + lane];
+      fs[i] = rope[f_at + lane / 2];
     }
   }
   // Values: the KV heads' slice of the row, copied.
   for (int i = threadIdx.x; i < kdim; i += 256) a.v[static_cast<size_t>(row) * kdim + i] = src[qdim + kdim + i];
+#pragma unroll
+  for (int i = 0; i < kHoist; i++) {
+    const int job = wave + 4 * i;
+    if (job < jobs) dest(job)[lane] = norm_rope(xs[i], fs[i], lane);
+  }
+  for (int job = wave + 4 * kHoist; job < jobs; job += 4) {
+    int x_at, f_at;
+    source(job, x_at, f_at);
+    dest(job)[lane] = norm_rope(src[x_at + lane], rope[f_at + lane / 2], lane);
+  }
 }
 
 }  // namespace

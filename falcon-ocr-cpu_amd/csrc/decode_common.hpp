@@ -29,6 +29,28 @@ __device__ __forceinline__ float xor_lane(float x, int mask) {
   return __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, __float_as_int(x)));
 }
 
+// rms_norm_row (width 64, no weight, eps f32::EPSILON) then the pairwise
+// RoPE rotation for the head whose element `lane` is x (split_norm_rope and
+// fused_row, src/model/rope.rs:60-72, src/model/fused.rs:107-120): the
+// 64-wide pairwise sum of squares is two 32-leaves folded 16-8-4-2-1 (xor
+// butterflies) then leaf0 + leaf1; scale = 1 / sqrt(sum / 64 + eps) with IEEE
+// division and square root; separate roundings, no contraction. Returns the
+// rotated element.
+__device__ __forceinline__ float norm_rope(float x, float2 factor, int lane) {
+  float part = x * x;
+#pragma unroll
+  for (int w = 16; w >= 1; w /= 2) part = part + xor_lane(part, w);
+  const float leaf0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 0));
+  const float leaf1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 32));
+  const float sum = leaf0 + leaf1;
+  const float scale = __fdiv_rn(1.0f, __builtin_sqrtf(__fdiv_rn(sum, 64.0f) + 1.1920929e-7f));
+  const float y = x * scale;
+  const float partner = xor_lane(y, 1);
+  const bool even = (lane & 1) == 0;
+  const float a = even ? y : partner, b = even ? partner : y;
+  return even ? a * factor.x - b * factor.y : a * factor.y + b * factor.x;
+}
+
 __device__ __forceinline__ float4 ld4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
 
 // Merge two online-softmax states (max m, denominator d, output o); both

@@ -161,6 +161,80 @@ __global__ __launch_bounds__(256) void append_kernel(AppendArgs a) {
   }
 }
 
+struct RowAppendArgs {
+  const float *qkv, *rope;  // [rows][qdim + 2 kdim], [rows][n_heads][32] (cos, sin)
+  float *q;                 // [rows][n_heads][64]
+  unsigned char *tail;
+  int n_heads, n_kv, tail_capacity, first, tail_bytes;
+};
+
+// The decode row step over a sealed cache, one workgroup per row: the query
+// heads normalized and rotated as split_norm_rope does (to q), the unique key
+// heads likewise (head g * repeat's factors, append_unique_heads) and the
+// values copied, both coded straight into the row's tail records (push_unique)
+// instead of through an FP32 buffer. Every value is the unfused path's bit for
+// bit (the same norm_rope, the same code_lane). A key head is one wave (two
+// blocks); the values are coded one element per lane.
+template <typename C>
+__global__ __launch_bounds__(256) void row_append_kernel(RowAppendArgs a) {
+  const int row = blockIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int qdim = a.n_heads * 64, kdim = a.n_kv * 64, repeat = a.n_heads / a.n_kv;
+  const float *src = a.qkv + static_cast<size_t>(row) * (qdim + 2 * kdim);
+  const float2 *rope = reinterpret_cast<const float2 *>(a.rope) + static_cast<size_t>(row) * a.n_heads * 32;
+  const double limit = sizeof(C) == 1 ? 127.0 : 32767.0;
+  auto record = [&](int g) {
+    return a.tail + (static_cast<size_t>(g) * a.tail_capacity + a.first + row) * a.tail_bytes;
+  };
+  const int jobs = a.n_heads + a.n_kv;
+  constexpr int kHoist = 8;
+  float xs[kHoist];
+  float2 fs[kHoist];
+#pragma unroll
+  for (int i = 0; i < kHoist; i++) {
+    const int job = wave + 4 * i;
+    if (job < jobs) {
+      const bool query = job < a.n_heads;
+      const int g = job - a.n_heads;
+      xs[i] = src[(query ? job * 64 : qdim + g * 64) + lane];
+      fs[i] = rope[(query ? job : g * repeat) * 32 + lane / 2];
+    }
+  }
+  // Values: element i of the row's KV slice is element 64 + i % 64 of group
+  // i / 64's record.
+  for (int i = threadIdx.x; i < kdim; i += 256) {
+    const float x = src[qdim + kdim + i];
+    uint16_t stored;
+    const int code = code_lane(x, half_any(!__builtin_isfinite(x)), limit, stored);
+    unsigned char *rec = record(i / 64);
+    const int e = 64 + (i & 63);
+    reinterpret_cast<C *>(rec)[e] = static_cast<C>(code);
+    if ((e & 31) == 0) reinterpret_cast<uint16_t *>(rec + kTail * sizeof(C))[e >> 5] = stored;
+  }
+  auto finish = [&](int job, float y) {
+    if (job < a.n_heads) {
+      a.q[static_cast<size_t>(row) * qdim + job * 64 + lane] = y;
+    } else {
+      uint16_t stored;
+      const int code = code_lane(y, half_any(!__builtin_isfinite(y)), limit, stored);
+      unsigned char *rec = record(job - a.n_heads);
+      reinterpret_cast<C *>(rec)[lane] = static_cast<C>(code);
+      if ((lane & 31) == 0) reinterpret_cast<uint16_t *>(rec + kTail * sizeof(C))[lane >> 5] = stored;
+    }
+  };
+#pragma unroll
+  for (int i = 0; i < kHoist; i++) {
+    const int job = wave + 4 * i;
+    if (job < jobs) finish(job, norm_rope(xs[i], fs[i], lane));
+  }
+  for (int job = wave + 4 * kHoist; job < jobs; job += 4) {
+    const bool query = job < a.n_heads;
+    const int g = job - a.n_heads;
+    finish(job, norm_rope(src[(query ? job * 64 : qdim + g * 64) + lane],
+                          rope[(query ? job : g * repeat) * 32 + lane / 2], lane));
+  }
+}
+
 struct DequantArgs {
   const unsigned char *records, *tail;
   float *prefix_k, *values, *generated_k;
@@ -524,6 +598,26 @@ int focr_kv_append(focr_ctx *handle, focr_kv_split *kv, const float *k, const fl
     hipLaunchKernelGGL(append_kernel<int8_t>, dim3((threads + 255) / 256), dim3(256), 0, ctx->stream, a);
   else
     hipLaunchKernelGGL(append_kernel<int16_t>, dim3((threads + 255) / 256), dim3(256), 0, ctx->stream, a);
+  FOCR_HIP_CHECK(hipGetLastError());
+  s->tail_len += rows;
+  return FOCR_OK;
+}
+
+int focr_kv_qkv_rows(focr_ctx *handle, focr_kv_split *kv, const float *qkv, size_t rows, const float *rope,
+                     float *q) {
+  Ctx *ctx = reinterpret_cast<Ctx *>(handle);
+  KvSplit *s = reinterpret_cast<KvSplit *>(kv);
+  FOCR_REQUIRE(ctx && s && qkv && rope && q, FOCR_E_ARG, "focr_kv_qkv_rows: null argument");
+  if (rows == 0) return FOCR_OK;
+  FOCR_REQUIRE(rows <= 8, FOCR_E_SHAPE, "decode takes 1..=8 rows");
+  FOCR_REQUIRE(s->prefix_len + s->tail_len + rows <= s->capacity, FOCR_E_SHAPE, "split tail capacity");
+  FOCR_HIP_CHECK(hipSetDevice(ctx->device));
+  RowAppendArgs a{qkv, rope, q, s->tail, s->n_heads, s->n_kv, static_cast<int>(s->capacity - s->prefix_len),
+                  static_cast<int>(s->tail_len), static_cast<int>(s->tail_bytes)};
+  if (s->bits == 8)
+    hipLaunchKernelGGL(row_append_kernel<int8_t>, dim3(static_cast<unsigned>(rows)), dim3(256), 0, ctx->stream, a);
+  else
+    hipLaunchKernelGGL(row_append_kernel<int16_t>, dim3(static_cast<unsigned>(rows)), dim3(256), 0, ctx->stream, a);
   FOCR_HIP_CHECK(hipGetLastError());
   s->tail_len += rows;
   return FOCR_OK;

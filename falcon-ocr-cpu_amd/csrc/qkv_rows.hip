@@ -17,13 +17,14 @@
 // reference's.
 //
 // One workgroup of 4 waves per row; each wave normalizes and rotates whole
-// heads, lane = element, loading up to 8 heads before computing any. The 64-wide pairwise sum is two 32-leaves folded
-// 16-8-4-2-1 (xor butterflies: lane i < w adds lane i + w, the other lanes'
-// values are never read) and then leaf0 + leaf1.
+// heads, lane = element, loading up to 8 heads before computing any. The
+// 64-wide pairwise sum is two 32-leaves folded 16-8-4-2-1 (xor butterflies:
+// lane i < w adds lane i + w, the other lanes' values are never read) and
+// then leaf0 + leaf1 (norm_rope, decode_common.hpp).
 //
 // Roofline: HBM. Bytes per row = 4 * (qkv width + n_heads * 64 rope floats
 // + q + keys + values written).
-#include "focr_internal.hpp"
+#include "decode_common.hpp"
 
 namespace focr {
 namespace {
@@ -34,29 +35,7 @@ struct RowArgs {
   int rows, prefix_rows, n_heads, n_kv_heads;
 };
 
-// x[lane ^ mask] with ds_swizzle-free cross-lane reads (ds_bpermute).
-__device__ __forceinline__ float xor_lane(float x, int mask) {
-  const int lane = threadIdx.x & 63;
-  return __int_as_float(__builtin_amdgcn_ds_bpermute((lane ^ mask) << 2, __float_as_int(x)));
-}
-
-// rms_norm_row (width 64, no weight) then the pairwise rotation, for the
-// head whose element `lane` is x. Returns the rotated element.
-__device__ __forceinline__ float norm_rope(float x, float2 factor, int lane) {
-  float part = x * x;
-#pragma unroll
-  for (int w = 16; w >= 1; w /= 2) part = part + xor_lane(part, w);
-  // Lane 0 holds leaf(0..32), lane 32 leaf(32..64).
-  const float leaf0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 0));
-  const float leaf1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), 32));
-  const float sum = leaf0 + leaf1;
-  const float scale = __fdiv_rn(1.0f, __builtin_sqrtf(__fdiv_rn(sum, 64.0f) + 1.1920929e-7f));
-  const float y = x * scale;
-  const float partner = xor_lane(y, 1);
-  const bool even = (lane & 1) == 0;
-  const float a = even ? y : partner, b = even ? partner : y;
-  return even ? a * factor.x - b * factor.y : a * factor.y + b * factor.x;
-}
+using namespace decode;
 
 __global__ __launch_bounds__(256) void qkv_rows_kernel(RowArgs a) {
   const int row = blockIdx.x;

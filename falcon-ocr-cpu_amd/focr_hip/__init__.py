@@ -79,6 +79,7 @@ SIGNATURES = {
     "focr_kv_attention_decode": (_I, [_P, _P, _P, _Z, _P, _P]),
     "focr_kv_dequantize": (_I, [_P, _P, _P, _P, _P]),
     "focr_kv_truncate_tail": (_I, [_P, _Z]),
+    "focr_kv_qkv_rows": (_I, [_P, _P, _P, _Z, _P, _P]),
     "focr_kv_info": (_I, [_P, _P, _P, _P, _P, _P]),
     "focr_kv_free": (_I, [_P]),
     "focr_screen_build": (_I, [_P, _P, _Z, _Z, ctypes.POINTER(_P)]),
@@ -490,6 +491,15 @@ class KvSplit:
     def append(self, k, v, rows: int) -> None:
         """`push_unique` of `rows` positions: k, v [rows][n_kv_heads][64]."""
         _check(lib().focr_kv_append(self.ctx.handle, self.handle, _dev(k), _dev(v), rows))
+
+    def qkv_rows(self, qkv, rows: int, rope, q=None):
+        """The decode row step fused with the append: queries [rows][n_heads][64]
+        out, the rows' unique keys and values coded into the tail."""
+        torch = _torch()
+        if q is None:
+            q = torch.empty((rows, self.n_heads, 64), dtype=torch.float32, device=qkv.device)
+        _check(lib().focr_kv_qkv_rows(self.ctx.handle, self.handle, _dev(qkv), rows, _dev(rope), _dev(q)))
+        return q
 
     def attention_decode(self, q, rows: int, sinks, out=None):
         """`attention_decode_rows`: [rows][n_heads][64] for the last `rows` positions."""

@@ -159,12 +159,9 @@ class DecoderLayer:
             attn = attention_with(q, self.kv(total), rows, Geometry(pos, *self.image), self.sinks, self.options,
                                   output=out, ctx=ctx)
         else:
-            k = self._buf("dk", (rows, self.n_kv_heads, 64))
-            v = self._buf("dv", (rows, self.n_kv_heads, 64))
-            q = qkv_rows(qkv, rows, rope, self.n_heads, self.n_kv_heads, 0, q=self._buf("dq", (rows, self.n_heads, 64)),
-                         generated_k=k, v=v, ctx=ctx)
+            # split_norm_rope and the tail append in one kernel.
+            q = self.split.qkv_rows(qkv, rows, rope, q=self._buf("dq", (rows, self.n_heads, 64)))
             mark("qkv_rows")
-            self.split.append(k, v, rows)
             attn = self.split.attention_decode(q, rows, self.sinks, out=out)
         mark("attention")
         self.wo.linear_ex(attn, rows, epilogue=Epilogue.ADD, out=h)

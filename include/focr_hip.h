@@ -255,6 +255,17 @@ int focr_kv_seal(focr_ctx *ctx, int bits, const float *prefix_k_dev, const float
  * past the capacity. */
 int focr_kv_append(focr_ctx *ctx, focr_kv_split *kv, const float *k_dev, const float *v_dev,
                    size_t rows);
+/* The decode row step over a sealed cache: focr_qkv_rows for rows past the
+ * prefix (split_norm_rope, src/model/rope.rs:14-86) fused with
+ * LayerCache::append of the split cache (src/model/cache.rs:117-140 ->
+ * SplitPrefix::append, src/quant/kv.rs:430-515): qkv_dev [rows][qdim + 2 kdim]
+ * and rope_dev [rows][n_heads][32][2] as for focr_qkv_rows; the queries go to
+ * q_dev [rows][n_heads][64], the unique keys and the values are coded into
+ * the tail without an FP32 copy. Records and queries are bitwise those of
+ * focr_qkv_rows followed by focr_kv_append. rows 1..8; FOCR_E_SHAPE past the
+ * capacity. */
+int focr_kv_qkv_rows(focr_ctx *ctx, focr_kv_split *kv, const float *qkv_dev, size_t rows,
+                     const float *rope_dev, float *q_dev);
 /* SplitPrefix::attention_decode / attention_decode_rows (src/quant/kv.rs:
  * 568-580,856-900): q_dev [rows][n_heads][64], rows 1..8 (at most the
  * appended positions); row r attends to keys [0, len - rows + r + 1) of the

@@ -119,3 +119,34 @@ def test_config5_decode_over_q8_records(fh):
     bits, plen, tlen, cap, nbytes = kv.info()
     assert (bits, plen, tlen) == (8, P, T) and nbytes == N_KV * (P * 176 + T * 144)
     kv.free()
+
+
+def test_fused_row_step_is_bitwise_the_unfused_one(fh):
+    # focr_kv_qkv_rows = focr_qkv_rows (rows past the prefix) + focr_kv_append,
+    # bit for bit: queries, and the decoded tail keys and values.
+    import torch
+
+    P, cap = 40, 60
+    k, v = pair_cache(P, N_KV, 51)
+    unfused = fh.KvSplit.seal(8, to_dev(k), to_dev(v), P, cap, N_HEADS, N_KV)
+    fused = fh.KvSplit.seal(8, to_dev(k), to_dev(v), P, cap, N_HEADS, N_KV)
+    width = N_HEADS * 64 + 2 * N_KV * 64
+    for step, rows in enumerate([1, 3, 8]):
+        qkv = gen.normal((rows, width), 2.0, 60 + step)
+        if step == 1:
+            qkv[2, N_HEADS * 64 + N_KV * 64 + 100] = np.inf  # a value block of group 1 decodes to NaN
+        ang = gen.uniform((rows, N_HEADS, 32), -3.2, 3.2, 70 + step)
+        rope = to_dev(np.stack([np.cos(ang), np.sin(ang)], -1).astype(np.float32))
+        gk = torch.empty((rows, N_KV, 64), device="cuda")
+        vv = torch.empty((rows, N_KV, 64), device="cuda")
+        q1 = fh.qkv_rows(to_dev(qkv), rows, rope, N_HEADS, N_KV, 0, generated_k=gk, v=vv)
+        unfused.append(gk, vv, rows)
+        q2 = fused.qkv_rows(to_dev(qkv), rows, rope)
+        assert_bitwise(host(q2), host(q1), f"step {step} queries")
+    assert fused.info()[2] == unfused.info()[2] == 12
+    for a, b, what in zip(fused.dequantize(), unfused.dequantize(), ("prefix keys", "values", "generated keys")):
+        assert_bitwise(host(a), host(b), what)
+    vals = host(fused.dequantize()[1])
+    assert np.all(np.isnan(vals[P + 1 + 2, 1, 32:64])) and np.all(np.isfinite(vals[P + 1 + 2, 1, :32]))
+    fused.free()
+    unfused.free()

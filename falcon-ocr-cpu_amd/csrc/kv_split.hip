@@ -168,70 +168,74 @@ struct RowAppendArgs {
   int n_heads, n_kv, tail_capacity, first, tail_bytes;
 };
 
-// The decode row step over a sealed cache, one workgroup per row: the query
-// heads normalized and rotated as split_norm_rope does (to q), the unique key
-// heads likewise (head g * repeat's factors, append_unique_heads) and the
-// values copied, both coded straight into the row's tail records (push_unique)
-// instead of through an FP32 buffer. Every value is the unfused path's bit for
-// bit (the same norm_rope, the same code_lane). A key head is one wave (two
-// blocks); the values are coded one element per lane.
+// The decode row step over a sealed cache, one workgroup of 16 waves per
+// row: the query heads normalized and rotated as split_norm_rope does (to q),
+// the unique key heads likewise (head g * repeat's factors,
+// append_unique_heads) and the values copied, both coded straight into the
+// row's tail records (push_unique) instead of through an FP32 buffer. Every
+// value is the unfused path's bit for bit (the same norm_rope, the same
+// code_lane). Jobs of one wave each, lane = element: n_heads queries, n_kv
+// keys (two blocks each), n_kv value halves of records; a wave loads its
+// (at most two) jobs before computing.
+constexpr int kRowWaves = 16;
+
 template <typename C>
-__global__ __launch_bounds__(256) void row_append_kernel(RowAppendArgs a) {
+__global__ __launch_bounds__(1024) void row_append_kernel(RowAppendArgs a) {
   const int row = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int qdim = a.n_heads * 64, kdim = a.n_kv * 64, repeat = a.n_heads / a.n_kv;
   const float *src = a.qkv + static_cast<size_t>(row) * (qdim + 2 * kdim);
   const float2 *rope = reinterpret_cast<const float2 *>(a.rope) + static_cast<size_t>(row) * a.n_heads * 32;
   const double limit = sizeof(C) == 1 ? 127.0 : 32767.0;
-  auto record = [&](int g) {
-    return a.tail + (static_cast<size_t>(g) * a.tail_capacity + a.first + row) * a.tail_bytes;
+  const int jobs = a.n_heads + 2 * a.n_kv;
+  // Job j: query head j, key head j - n_heads, or the values of group
+  // j - n_heads - n_kv.
+  auto load = [&](int job, float &x, float2 &f) {
+    if (job < a.n_heads) {
+      x = src[job * 64 + lane];
+      f = rope[job * 32 + lane / 2];
+    } else if (job < a.n_heads + a.n_kv) {
+      const int g = job - a.n_heads;
+      x = src[qdim + g * 64 + lane];
+      f = rope[g * repeat * 32 + lane / 2];
+    } else {
+      x = src[qdim + kdim + (job - a.n_heads - a.n_kv) * 64 + lane];
+    }
   };
-  const int jobs = a.n_heads + a.n_kv;
-  constexpr int kHoist = 8;
+  auto finish = [&](int job, float x, float2 f) {
+    if (job < a.n_heads) {
+      a.q[static_cast<size_t>(row) * qdim + job * 64 + lane] = norm_rope(x, f, lane);
+      return;
+    }
+    const bool key = job < a.n_heads + a.n_kv;
+    const int g = key ? job - a.n_heads : job - a.n_heads - a.n_kv;
+    const float y = key ? norm_rope(x, f, lane) : x;
+    uint16_t stored;
+    const int code = code_lane(y, half_any(!__builtin_isfinite(y)), limit, stored);
+    unsigned char *rec = a.tail + (static_cast<size_t>(g) * a.tail_capacity + a.first + row) * a.tail_bytes;
+    const int e = (key ? 0 : 64) + lane;
+    reinterpret_cast<C *>(rec)[e] = static_cast<C>(code);
+    if ((e & 31) == 0) reinterpret_cast<uint16_t *>(rec + kTail * sizeof(C))[e >> 5] = stored;
+  };
+  constexpr int kHoist = 2;
   float xs[kHoist];
   float2 fs[kHoist];
 #pragma unroll
   for (int i = 0; i < kHoist; i++) {
-    const int job = wave + 4 * i;
-    if (job < jobs) {
-      const bool query = job < a.n_heads;
-      const int g = job - a.n_heads;
-      xs[i] = src[(query ? job * 64 : qdim + g * 64) + lane];
-      fs[i] = rope[(query ? job : g * repeat) * 32 + lane / 2];
-    }
+    const int job = wave + kRowWaves * i;
+    fs[i] = make_float2(0.0f, 0.0f);
+    if (job < jobs) load(job, xs[i], fs[i]);
   }
-  // Values: element i of the row's KV slice is element 64 + i % 64 of group
-  // i / 64's record.
-  for (int i = threadIdx.x; i < kdim; i += 256) {
-    const float x = src[qdim + kdim + i];
-    uint16_t stored;
-    const int code = code_lane(x, half_any(!__builtin_isfinite(x)), limit, stored);
-    unsigned char *rec = record(i / 64);
-    const int e = 64 + (i & 63);
-    reinterpret_cast<C *>(rec)[e] = static_cast<C>(code);
-    if ((e & 31) == 0) reinterpret_cast<uint16_t *>(rec + kTail * sizeof(C))[e >> 5] = stored;
-  }
-  auto finish = [&](int job, float y) {
-    if (job < a.n_heads) {
-      a.q[static_cast<size_t>(row) * qdim + job * 64 + lane] = y;
-    } else {
-      uint16_t stored;
-      const int code = code_lane(y, half_any(!__builtin_isfinite(y)), limit, stored);
-      unsigned char *rec = record(job - a.n_heads);
-      reinterpret_cast<C *>(rec)[lane] = static_cast<C>(code);
-      if ((lane & 31) == 0) reinterpret_cast<uint16_t *>(rec + kTail * sizeof(C))[lane >> 5] = stored;
-    }
-  };
 #pragma unroll
   for (int i = 0; i < kHoist; i++) {
-    const int job = wave + 4 * i;
-    if (job < jobs) finish(job, norm_rope(xs[i], fs[i], lane));
+    const int job = wave + kRowWaves * i;
+    if (job < jobs) finish(job, xs[i], fs[i]);
   }
-  for (int job = wave + 4 * kHoist; job < jobs; job += 4) {
-    const bool query = job < a.n_heads;
-    const int g = job - a.n_heads;
-    finish(job, norm_rope(src[(query ? job * 64 : qdim + g * 64) + lane],
-                          rope[(query ? job : g * repeat) * 32 + lane / 2], lane));
+  for (int job = wave + kRowWaves * kHoist; job < jobs; job += kRowWaves) {
+    float x;
+    float2 f = make_float2(0.0f, 0.0f);
+    load(job, x, f);
+    finish(job, x, f);
   }
 }
 
@@ -615,9 +619,11 @@ int focr_kv_qkv_rows(focr_ctx *handle, focr_kv_split *kv, const float *qkv, size
   RowAppendArgs a{qkv, rope, q, s->tail, s->n_heads, s->n_kv, static_cast<int>(s->capacity - s->prefix_len),
                   static_cast<int>(s->tail_len), static_cast<int>(s->tail_bytes)};
   if (s->bits == 8)
-    hipLaunchKernelGGL(row_append_kernel<int8_t>, dim3(static_cast<unsigned>(rows)), dim3(256), 0, ctx->stream, a);
+    hipLaunchKernelGGL(row_append_kernel<int8_t>, dim3(static_cast<unsigned>(rows)), dim3(64 * kRowWaves), 0,
+                       ctx->stream, a);
   else
-    hipLaunchKernelGGL(row_append_kernel<int16_t>, dim3(static_cast<unsigned>(rows)), dim3(256), 0, ctx->stream, a);
+    hipLaunchKernelGGL(row_append_kernel<int16_t>, dim3(static_cast<unsigned>(rows)), dim3(64 * kRowWaves), 0,
+                       ctx->stream, a);
   FOCR_HIP_CHECK(hipGetLastError());
   s->tail_len += rows;
   return FOCR_OK;

@@ -16,8 +16,9 @@
 // with separate roundings (no contraction), so outputs are bitwise the
 // reference's.
 //
-// One workgroup of 4 waves per row; each wave normalizes and rotates whole
-// heads, lane = element, loading up to 8 heads before computing any. The
+// One workgroup per row (16 waves for up to 64 rows, else 4); each wave
+// normalizes and rotates whole heads, lane = element, loading its heads
+// (up to 32 / waves of them) before computing any. The
 // 64-wide pairwise sum is two 32-leaves folded 16-8-4-2-1 (xor butterflies:
 // lane i < w adds lane i + w, the other lanes' values are never read) and
 // then leaf0 + leaf1 (norm_rope, decode_common.hpp).
@@ -37,7 +38,11 @@ struct RowArgs {
 
 using namespace decode;
 
-__global__ __launch_bounds__(256) void qkv_rows_kernel(RowArgs a) {
+// W waves per row's workgroup: 16 for a few decode rows (one or two heads a
+// wave), 4 for prefill pages (enough workgroups to fill the chip anyway).
+template <int W>
+__global__ __launch_bounds__(64 * W) void qkv_rows_kernel(RowArgs a) {
+  constexpr int kRowWaves = W;
   const int row = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int qdim = a.n_heads * 64, kdim = a.n_kv_heads * 64;
@@ -49,7 +54,7 @@ __global__ __launch_bounds__(256) void qkv_rows_kernel(RowArgs a) {
   // a prefix row, n_kv_heads unique ones for a generated row). Job j reads
   // element `lane` of its source head and its rope factor pair; the first
   // kHoist jobs of a wave load before any computes, so their latencies
-  // overlap (a decode row has 24 jobs, a prefill row 32: at most 8 a wave).
+  // overlap (a decode row has 24 jobs, a prefill row 32).
   const int key_jobs = prefix ? a.n_heads : a.n_kv_heads;
   const int jobs = a.n_heads + key_jobs;
   auto source = [&](int job, int &x_at, int &f_at) {
@@ -71,12 +76,12 @@ __global__ __launch_bounds__(256) void qkv_rows_kernel(RowArgs a) {
     if (prefix) return a.prefix_k + static_cast<size_t>(row) * qdim + (job - a.n_heads) * 64;
     return a.generated_k + static_cast<size_t>(row - a.prefix_rows) * kdim + (job - a.n_heads) * 64;
   };
-  constexpr int kHoist = 8;
+  constexpr int kHoist = 32 / W;
   float xs[kHoist];
   float2 fs[kHoist];
 #pragma unroll
   for (int i = 0; i < kHoist; i++) {
-    const int job = wave + 4 * i;
+    const int job = wave + kRowWaves * i;
     if (job < jobs) {
       int x_at, f_at;
       source(job, x_at, f_at);
@@ -85,13 +90,14 @@ __global__ __launch_bounds__(256) void qkv_rows_kernel(RowArgs a) {
     }
   }
   // Values: the KV heads' slice of the row, copied.
-  for (int i = threadIdx.x; i < kdim; i += 256) a.v[static_cast<size_t>(row) * kdim + i] = src[qdim + kdim + i];
+  for (int i = threadIdx.x; i < kdim; i += 64 * kRowWaves)
+    a.v[static_cast<size_t>(row) * kdim + i] = src[qdim + kdim + i];
 #pragma unroll
   for (int i = 0; i < kHoist; i++) {
-    const int job = wave + 4 * i;
+    const int job = wave + kRowWaves * i;
     if (job < jobs) dest(job)[lane] = norm_rope(xs[i], fs[i], lane);
   }
-  for (int job = wave + 4 * kHoist; job < jobs; job += 4) {
+  for (int job = wave + kRowWaves * kHoist; job < jobs; job += kRowWaves) {
     int x_at, f_at;
     source(job, x_at, f_at);
     dest(job)[lane] = norm_rope(src[x_at + lane], rope[f_at + lane / 2], lane);
@@ -114,7 +120,10 @@ int launch_qkv_rows(Ctx *ctx, const float *qkv, size_t rows, const float *rope, 
   a.prefix_rows = static_cast<int>(prefix_rows < rows ? prefix_rows : rows);
   a.n_heads = static_cast<int>(n_heads);
   a.n_kv_heads = static_cast<int>(n_kv_heads);
-  hipLaunchKernelGGL(qkv_rows_kernel, dim3(static_cast<unsigned>(rows)), dim3(256), 0, ctx->stream, a);
+  if (rows <= 64)
+    hipLaunchKernelGGL(qkv_rows_kernel<16>, dim3(static_cast<unsigned>(rows)), dim3(1024), 0, ctx->stream, a);
+  else
+    hipLaunchKernelGGL(qkv_rows_kernel<4>, dim3(static_cast<unsigned>(rows)), dim3(256), 0, ctx->stream, a);
   FOCR_HIP_CHECK(hipGetLastError());
   return FOCR_OK;
 }

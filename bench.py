@@ -211,7 +211,8 @@ def bench_layer(torch, fh, gen, np, steps=64):
     16 query / 8 KV heads of 64) prefilled over P = 16,320 rows (image
     [0, 4096)), then `steps` greedy decode steps growing the cache to 16,384,
     first over the compact FP32 cache (Kv::Compact), then over the sealed Q8
-    records (Kv::Q8: the prefill seals the prefix after its attention).
+    records (Kv::Q8: the prefill seals the prefix after its attention), then
+    with fast mode's BF16 prefill attention as well (`fast_plan`).
     Prefill stages are timed with HIP events (the layer's phase marks); the
     decode steps are captured into one HIP graph and replayed."""
     P, img, dim, heads, kv = 16384 - steps, 4096, 768, 16, 8
@@ -238,9 +239,9 @@ def bench_layer(torch, fh, gen, np, steps=64):
     w_bytes = sum(n * k + 4 * n * (k // 64) for n, k in shapes.values())
     avg_total = P + (steps + 1) / 2.0
 
-    def run(kv_bits):
+    def run(kv_bits, bf16=False):
         layer = fh.DecoderLayer(lins["qkv"], lins["wo"], lins["w13"], lins["w2"], sinks, capacity=P + steps,
-                                kv_bits=kv_bits)
+                                kv_bits=kv_bits, bf16_attention=bf16)
         # Prefill: one untimed pass (allocates the workspace), then a timed one.
         marks = []
         clock = lambda stage: marks.append((stage, torch.cuda.Event(enable_timing=True))) or \
@@ -302,6 +303,9 @@ def bench_layer(torch, fh, gen, np, steps=64):
     res = {"prefill_rows": P, "decode_steps": steps, "prefill_gflop": round((proj_flop + attn_flop) / 1e9, 2)}
     res.update(run(32))
     res["q8"] = run(8)
+    # Fast mode's whole plan (w8-body-kv-q8 with hip-i16 + hip-bf16-static):
+    # BF16 static-softmax prefill attention, then decode over Q8 records.
+    res["fast_plan"] = run(8, bf16=True)
     for lin in lins.values():
         lin.free()
     return res

@@ -30,7 +30,9 @@ KV head) lives in device memory sized for `capacity` positions, as
 attention (``seal_layer``, model/cache.rs:218-276) into a `KvSplit`, and decode
 appends each step's keys and values to its tail and attends over the records
 (``LayerCache::Split``); ``kv_bits`` 32 keeps the compact FP32 cache
-(Kv::Compact). RoPE factors
+(Kv::Compact). ``bf16_attention`` runs the prefill attention in BF16 as the
+fast mode's plan does (``PrefillAttention::Bf16`` / ``Bf16Static`` by
+``options.softmax``). RoPE factors
 come from the caller ([rows][n_heads][32][2] cos/sin pairs), as
 ``rotary_factors`` provides them to the reference's row kernels.
 
@@ -42,13 +44,14 @@ from __future__ import annotations
 from typing import Optional
 
 from . import (CompactKv, Context, Epilogue, FocrError, Geometry, KvSplit, PrefillOptions, PrefillProjection,
-               attention_with, default_context, qkv_rows, row_scales)
+               attention_prefill_bf16, attention_with, default_context, qkv_rows, row_scales)
 
 
 class DecoderLayer:
     def __init__(self, qkv, wo, w13, w2, sinks, capacity: int, n_heads: int = 16, n_kv_heads: int = 8,
                  head_dim: int = 64, projection: PrefillProjection = PrefillProjection.I16,
-                 options: PrefillOptions = PrefillOptions(), ctx: Optional[Context] = None, kv_bits: int = 32):
+                 options: PrefillOptions = PrefillOptions(), ctx: Optional[Context] = None, kv_bits: int = 32,
+                 bf16_attention: bool = False):
         import torch
 
         self.ctx = ctx or default_context()
@@ -66,6 +69,7 @@ class DecoderLayer:
         self.projection, self.options = projection, options
         self.capacity = capacity
         self.kv_bits = kv_bits
+        self.bf16_attention = bf16_attention
         self.split: Optional[KvSplit] = None
         dev = f"cuda:{self.ctx.device}"
         f32 = torch.float32
@@ -120,8 +124,15 @@ class DecoderLayer:
                      prefix_k=self.prefix_k[:rows], v=self.v[:rows], ctx=ctx)
         mark("qkv_rows")
         self.image = (image_start, image_end)
-        attn = attention_with(q, self.kv(rows), rows, Geometry(0, image_start, image_end), self.sinks, self.options,
-                              output=self._buf("attn", (rows, self.n_heads, 64)), ctx=ctx)
+        attn = self._buf("attn", (rows, self.n_heads, 64))
+        geometry = Geometry(0, image_start, image_end)
+        # Fast mode's BF16 attention where the plan has it; the reference's
+        # `false` (a shape it does not take) falls back to the FP32 tiles
+        # (Model::forward_layers, model/mod.rs:621-646 -> LayerCache::attention,
+        # model/cache.rs:142-197).
+        if not (self.bf16_attention and attention_prefill_bf16(q, self.kv(rows), rows, geometry, self.sinks, attn,
+                                                               self.options, ctx=ctx)):
+            attn = attention_with(q, self.kv(rows), rows, geometry, self.sinks, self.options, output=attn, ctx=ctx)
         mark("attention")
         if self.kv_bits != 32:
             self.split = KvSplit.seal(self.kv_bits, self.prefix_k[:rows], self.v[:rows], rows, self.capacity,

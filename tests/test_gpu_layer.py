@@ -325,3 +325,32 @@ def test_decoder_layer_over_the_sealed_cache(fh, bits):
     layer.free()
     for lin in lins.values():
         lin.free()
+
+
+@pytest.mark.parametrize("softmax", ["static", "online"])
+def test_decoder_layer_with_bf16_attention(fh, softmax):
+    """Fast mode's plan: INT16 projections and BF16 prefill attention
+    (PrefillAttention::Bf16Static / Bf16). The layer's attention output is
+    within the BF16 tolerance of the BF16 attention oracle on the layer's own
+    queries and cache."""
+    import torch
+
+    rows, image = 200, (0, 128)
+    w = layer_weights(70)
+    lins = {name: fh.QuantLinear(8, *w[name], 64) for name in w}
+    sinks = gen.uniform(H, -2.0, 2.0, 71)
+    opts = fh.PrefillOptions(softmax=fh.Softmax.STATIC if softmax == "static" else fh.Softmax.ONLINE)
+    layer = fh.DecoderLayer(lins["qkv"], lins["wo"], lins["w13"], lins["w2"], to_dev(sinks), capacity=rows + 4,
+                            options=opts, bf16_attention=True)
+    h0 = gen.normal((rows, DIM), 1.0, 72)
+    rope = rope_table(rows, 73)
+    layer.prefill(to_dev(h0), to_dev(rope), *image)
+    torch.cuda.synchronize()
+    _, want_q, want_pk, want_v, _ = oracle_layer_prefill(w, h0, rope, image, sinks)
+    want = oracle.attention_prefill_bf16(want_q, want_pk, want_v, rows, H, G, image[0], image[1], sinks,
+                                         static=softmax == "static")
+    got = host(layer._buf("attn", (rows, H, 64)))
+    assert np.all(np.isfinite(got))
+    assert max_rel(got, want) <= 2e-3
+    for lin in lins.values():
+        lin.free()

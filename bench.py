@@ -370,6 +370,43 @@ def bench_copy(torch, reps):
     return {"bytes_read": n, "bytes_written": n, "ms": round(avg, 4), "gbs": round(2 * n / (avg * 1e-3) / 1e9, 1)}
 
 
+def bench_launch_floor(torch, steps=2000):
+    """What a launch costs in the headline's own setup (K launches replayed
+    from one HIP graph, HIP events around the replay): a one-workgroup fill
+    (4 bytes: the dispatch floor), and a plain device copy moving the headline
+    GEMV's 8,671,232 bytes (4,335,616 read from a rotating 520 MB pool of
+    sources, so they come from HBM, and as many written)."""
+    res = {}
+    tiny = torch.zeros(1, device="cuda")
+    n = 8671232 // 2 // 4
+    pool = [torch.ones(n, device="cuda") for _ in range(120)]
+    dst = torch.empty(n, device="cuda")
+    for name, fn in (("fill_4B", lambda i: tiny.fill_(1.0)),
+                     ("copy_8.67MB_from_pool", lambda i: dst.copy_(pool[i % len(pool)]))):
+        for i in range(3):
+            fn(i)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        cap = torch.cuda.Stream()
+        cap.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(cap):
+            with torch.cuda.graph(g, stream=cap):
+                for i in range(steps):
+                    fn(i)
+        torch.cuda.current_stream().wait_stream(cap)
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        res[name + "_us"] = round(e0.elapsed_time(e1) * 1e3 / steps, 3)
+        del g
+    del pool
+    return res
+
+
 def cpu_baseline(np, gen, seconds=10.0):
     """The oracle's INT16 GEMV (reference dot_q order) on the host cores, on the
     headline matrix. Like the GPU side, calls rotate through a pool of copies
@@ -529,6 +566,8 @@ def main():
         log(f"screened head: {per_op['screened_head_65536x768']}")
     if "copy" in ops:
         per_op["copy_256MiB"] = bench_copy(torch, 10)
+        per_op["launch_floor"] = bench_launch_floor(torch)
+        log(f"launch floor: {per_op['launch_floor']}")
     if not args.no_cpu and "prefill_f32" in per_op and "attention_prefill" in per_op:
         per_op["prefill_page_vs_cpu"] = cpu_prefill_page(np, gen, per_op["prefill_f32"], per_op["attention_prefill"])
         log(f"prefill page vs CPU: {per_op['prefill_page_vs_cpu']}")

@@ -153,3 +153,30 @@ def test_shape_errors(fh):
     odd = fh.QuantLinear(8, np.ones((3, 64), np.int8), np.ones((3, 1), np.float32), 64)
     with pytest.raises(fh.FocrError, match="GLU"):
         odd.linear_glu(torch.zeros(64, device="cuda:0"), 1)
+
+
+@pytest.mark.parametrize("bits,n,k,group", [(8, 16384, 1024, 64), (8, 65536, 768, 64), (16, 16387, 520, 64),
+                                            (8, 16386, 256, 32), (16, 20000, 100, 32)])
+def test_large_matrices_several_tiles_per_wave(fh, bits, n, k, group):
+    # From 4,096 wave tiles (16,384 channels) each wave computes several tiles
+    # (1 or 2 rows); ragged last workgroups, every epilogue and exception
+    # columns stay bitwise the reference's dot.
+    codes = gen.codes_uniform((n, k), -127 if bits == 8 else -32768, 127 if bits == 8 else 32767,
+                              np.int8 if bits == 8 else np.int16, 90)
+    scales = gen.uniform((n, -(-k // group)), 1e-4, 4e-4, 91)
+    cols = [3, k - 1]
+    codes[:, cols] = 0
+    vals = gen.normal((n, 2), 0.1, 92)
+    lin = fh.QuantLinear(bits, codes, scales, group, exc_cols=cols, exc_vals=vals)
+    for rows in (1, 2, 3):
+        x = gen.normal((rows, k), 1.0, 93 + rows)
+        want = oracle.linear_decode(bits, codes, scales, n, k, group, x, rows, exc_cols=cols, exc_vals=vals)
+        assert_bitwise(host(lin.linear(to_dev(x), rows)), want, f"large {n}x{k} rows {rows}")
+        if n % 2 == 0:
+            glu = oracle.linear_decode_glu(bits, codes, scales, n, k, group, x, rows, exc_cols=cols, exc_vals=vals)
+            assert_bitwise(host(lin.linear_glu(to_dev(x), rows)), glu, f"large glu rows {rows}")
+        base = gen.normal((rows, n), 1.0, 97)
+        h = to_dev(base)
+        lin.linear_ex(to_dev(x), rows, epilogue=fh.Epilogue.ADD, out=h)
+        assert_bitwise(host(h), (base + want).astype(np.float32), f"large add rows {rows}")
+    lin.free()

@@ -431,8 +431,9 @@ __global__ __launch_bounds__(256) void split_partial_kernel(SplitDecArgs a, int 
       }
   };
   // iters is a multiple of kWaves: every wave takes iters / kWaves
-  // iterations (one at the usual chunk of 64 keys). Single-buffered: the
-  // latency is hidden by the other resident waves, not by registers.
+  // iterations (two at 16K keys). Single-buffered: the latency is hidden by
+  // the other resident waves, not by registers (double-buffering measured
+  // slower: fewer waves fit).
   for (int it = wave; it < iters; it += kWaves) {
     KeyVal kb[kKpl];
     load(kb, it);
@@ -475,11 +476,11 @@ __global__ __launch_bounds__(256) void split_partial_kernel(SplitDecArgs a, int 
 
 template <typename C, int M>
 int launch_split(Ctx *ctx, SplitDecArgs a, int rows, const float *sinks, float *out) {
-  // Keys per workgroup task: about 2048 tasks over the chip (each serves two
+  // Keys per workgroup task: about 1024 tasks over the chip (each serves two
   // heads), at most kMaxChunks chunks, whole multiples of 64 keys (every
   // wave of the task takes the same number of 16-key iterations).
   const long limit = a.last;
-  const long want = (limit * a.n_kv + 2047) / 2048;
+  const long want = (limit * a.n_kv + 1023) / 1024;
   long per = (want + 63) / 64 * 64;
   const long min_per = ((limit + kMaxChunks - 1) / kMaxChunks + 63) / 64 * 64;
   if (per < min_per) per = min_per;

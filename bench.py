@@ -510,7 +510,7 @@ def main():
     ap.add_argument("--no-graph", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (see DESIGN.md, 'Sharding').", file=sys.stderr)
+        print("bench.py measures one GPU: this build has no multi-GPU path (the kernels run on one GPU's share).", file=sys.stderr)
         sys.exit(2)
     import numpy as np
     import torch

@@ -14,7 +14,7 @@
 //
 // Two launches per call, all rows (at most 8) together:
 //  1. screen_kernel: up to 768 workgroups stride over tiles of 16 vocabulary
-//     rows, 16 lanes per row (lane = 64-channel group, 64 codes in four
+//     rows, 16 lanes per row (lane 4g + row: 64-channel group g, 64 codes in four
 //     16-byte loads, the next tile's issued before this one is scored), every
 //     input scored against each row as it is loaded. The order is the reference's AVX2
 //     screen_row (two 8-lane FMA chains per group, (a0 + a1) * s_g accumulated
@@ -76,6 +76,15 @@ struct ScreenArgs {
   float weight_abs_max, kappa;
 };
 
+// The same sum over the lanes p = lane / 4 < 8 of the screen kernel's lane
+// map (lane = 4 * group + row): p ^ 4, p ^ 1, p ^ 2 are lane ^ 16, ^ 4, ^ 8.
+__device__ __forceinline__ float sum8_stride4(float v) {
+  v = v + __shfl_xor(v, 16, 32);
+  v = v + __shfl_xor(v, 4, 32);
+  v = v + __shfl_xor(v, 8, 32);
+  return v;
+}
+
 __device__ __forceinline__ float sum8_lanes(float v, int p) {
   // ((v0+v4)+(v1+v5))+((v2+v6)+(v3+v7)) over lanes p = 0..7 of a row group;
   // the partner values come by exchange, and a + b = b + a exactly.
@@ -86,9 +95,11 @@ __device__ __forceinline__ float sum8_lanes(float v, int p) {
 }
 
 // Dynamic LDS of screen_kernel: x [rows][groups][68] (each 64-channel group
-// padded by 16 bytes, so the 16 group lanes of a row read distinct banks),
-// then the per-(wave, row, group) lane values u [4][4][16][8] and scales
-// [4][4][16], then norms [rows][16] and the per-(row, wave) maxima [rows][4].
+// padded by 16 bytes, so neighbouring groups start in different banks; the
+// four lanes of a group read the same address), then the per-(wave, group,
+// row) lane values u [4][16][4][8] and scales [4][16][4] (consecutive lanes,
+// consecutive words), then norms [rows][16] and the per-(row, wave) maxima
+// [rows][4].
 constexpr int kXPitch = kGroup + 4;
 __host__ __device__ inline size_t screen_lds_bytes(int rows, int dim) {
   return sizeof(float) * (static_cast<size_t>(rows) * (dim / kGroup) * kXPitch + 4 * 4 * kMaxGroups * 8 +
@@ -101,8 +112,8 @@ __global__ __launch_bounds__(256) void screen_kernel(ScreenArgs a) {
   const int dim = a.dim, groups = a.groups, rows = a.rows;
   const int xrow = groups * kXPitch;                    // floats per staged input row
   float *xs = lds;                                      // [rows][groups][kXPitch]
-  float(*u)[4][kMaxGroups][8] = reinterpret_cast<float(*)[4][kMaxGroups][8]>(xs + rows * xrow);
-  float(*sc)[4][kMaxGroups] = reinterpret_cast<float(*)[4][kMaxGroups]>(xs + rows * xrow + 4 * 4 * kMaxGroups * 8);
+  float(*u)[kMaxGroups][4][8] = reinterpret_cast<float(*)[kMaxGroups][4][8]>(xs + rows * xrow);
+  float(*sc)[kMaxGroups][4] = reinterpret_cast<float(*)[kMaxGroups][4]>(xs + rows * xrow + 4 * 4 * kMaxGroups * 8);
   float *norms = xs + rows * xrow + 4 * 4 * kMaxGroups * 9;  // [rows][16]
   float *wmax = norms + rows * kMaxGroups;                  // [rows][4]
 
@@ -137,7 +148,9 @@ __global__ __launch_bounds__(256) void screen_kernel(ScreenArgs a) {
   // scored, and the staging of x and the norms happens once.
   const int block = blockIdx.x - rows, nblocks = gridDim.x - rows;
   const int tiles = (a.vocab + kRowsPerBlock - 1) / kRowsPerBlock;
-  const int row_in_wave = lane >> 4, g = lane & 15;
+  // Lane = 4 * group + row: the four rows' lanes of a group are neighbours,
+  // so their reads of the same x address share one LDS access.
+  const int row_in_wave = lane & 3, g = lane >> 2;
   uint4 raw[4];
   float scale = 0.0f;
   auto load_tile = [&](int tile) {
@@ -194,13 +207,21 @@ __global__ __launch_bounds__(256) void screen_kernel(ScreenArgs a) {
       const uint32_t word = (&raw[i >> 4].x)[(i >> 2) & 3];
       cf[i] = static_cast<float>(static_cast<int8_t>((word >> (8 * (i & 3))) & 0xffu));
     }
-    sc[wave][row_in_wave][g] = scale;
+    sc[wave][g][row_in_wave] = scale;
     load_tile(tile + nblocks);
+    // The row's 16 group scales, read once for every input (lanes g < 8 use
+    // them; the write above is this wave's own and is waited for here).
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float ss[kMaxGroups];
+#pragma unroll
+    for (int gg = 0; gg < kMaxGroups; gg++) ss[gg] = sc[wave][gg][row_in_wave];
 
     for (int r = 0; r < rows; r++) {
       // screen_row's group step: a0 over x[base + j + p], a1 over
       // x[base + j + 8 + p], j = 0, 16, 32, 48; then a0 + a1 per lane p.
-      float4 *dst = reinterpret_cast<float4 *>(u[wave][row_in_wave][g]);
+      float4 *dst = reinterpret_cast<float4 *>(u[wave][g][row_in_wave]);
       if (!active) {
         dst[0] = dst[1] = make_float4(0.f, 0.f, 0.f, 0.f);
       } else {
@@ -230,19 +251,16 @@ __global__ __launch_bounds__(256) void screen_kernel(ScreenArgs a) {
         // Lane p accumulates row[p] = fma(a0 + a1, s_g, row[p]) over the
         // groups; S = sum fma(s_g, n_g, S) alongside.
         const int p = g;
-        float uu[kMaxGroups], ss[kMaxGroups];
+        float uu[kMaxGroups];
 #pragma unroll
-        for (int gg = 0; gg < kMaxGroups; gg++) {
-          uu[gg] = u[wave][row_in_wave][gg][p];
-          ss[gg] = sc[wave][row_in_wave][gg];
-        }
+        for (int gg = 0; gg < kMaxGroups; gg++) uu[gg] = u[wave][gg][row_in_wave][p];
         float acc = 0.0f, total = 0.0f;
 #pragma unroll
         for (int gg = 0; gg < kMaxGroups; gg++) {
           acc = __builtin_fmaf(uu[gg], ss[gg], acc);
           total = __builtin_fmaf(ss[gg], norms[r * kMaxGroups + gg], total);
         }
-        const float q = sum8_lanes(acc, p);
+        const float q = sum8_stride4(acc);
         const float bound = __builtin_fmaf(a.kappa, total, kEta);
         if (p == 0) {
           a.upper[static_cast<size_t>(r) * a.ustride + v] = q + bound;

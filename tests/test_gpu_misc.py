@@ -63,3 +63,21 @@ def test_argmax_unaligned_rows_and_ties(fh):
     big = gen.normal((2, 70001), 1.0, 33)
     big[1, 65537] = big[1, 70000] = np.float32(40.0)
     assert fh.argmax(to_dev(big), 2, 70001) == [oracle.argmax(r) for r in big]
+
+
+def test_argmax_ties_across_partial_workgroups(fh):
+    # Rows are split into 2,048-logit partials combined per row: a tie across
+    # a partial boundary, across distant partials and inside one, a maximum in
+    # the ragged last partial, and many rows (one launch batch each 65,535).
+    vocab = 3 * 2048 + 5
+    logits = gen.normal((6, vocab), 1.0, 34)
+    logits[0, 2047] = logits[0, 2048] = np.float32(9.0)
+    logits[1, 6000] = logits[1, 100] = np.float32(9.0)
+    logits[2, 4100] = logits[2, 4101] = np.float32(9.0)
+    logits[3, vocab - 1] = np.float32(9.0)
+    logits[4, :] = np.float32(0.25)
+    logits[5, vocab - 5:] = np.float32(9.0)
+    got = fh.argmax(to_dev(logits), 6, vocab)
+    assert got == [oracle.argmax(row) for row in logits] == [2047, 100, 4100, vocab - 1, 0, vocab - 5]
+    many = gen.normal((3000, 64), 1.0, 35)
+    assert fh.argmax(to_dev(many), 3000, 64) == [int(np.argmax(r)) for r in many]

@@ -316,7 +316,8 @@ class SafeTensorsFile:
         self.header = safetensors_header(self.path)
         self.metadata = header_metadata(self.header)
         size = self.path.stat().st_size
-        base = 8 + struct.unpack("<Q", open(self.path, "rb").read(8))[0]
+        with open(self.path, "rb") as f:
+            base = 8 + struct.unpack("<Q", f.read(8))[0]
         infos: Dict[str, TensorInfo] = {}
         spans = []
         for name, entry in self.header.items():

@@ -408,7 +408,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void a
       // Online step (softmax_pairs, bf16.rs:409-473).
       float tile_max = st[0];
 #pragma unroll
-      for (int r = 1; r < 16; r++) tile_max = st[r] > tile_max ? st[r] : tile_max;
+      for (int r = 1; r < 16; r++) tile_max = __builtin_fmaxf(tile_max, st[r]);  // v_max3 pairs
       tile_max = halves_max(tile_max);
       const float new_max = tile_max > run_max ? tile_max : run_max;
       const bool skip = new_max == -__builtin_inff();
@@ -417,11 +417,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void a
       rescale = first ? 0.0f : rescale;
       rescale = skip ? 1.0f : rescale;
       const float shift = skip ? 0.0f : new_max;  // skip: every s is -inf, p = +0
+      // p = 2^(s log2(e) - shift log2(e)): one FMA per score (the argument
+      // rounds once instead of twice; p is rounded to BF16 next).
+      const float shift_l = shift * kLog2e;
       float psum = 0.0f;
 #pragma unroll
       for (int i = 0; i < 8; i++) {
-        const float p0 = __builtin_amdgcn_exp2f(kLog2e * (st[2 * i] - shift));
-        const float p1 = __builtin_amdgcn_exp2f(kLog2e * (st[2 * i + 1] - shift));
+        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[2 * i], kLog2e, -shift_l));
+        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[2 * i + 1], kLog2e, -shift_l));
         psum = psum + p0;
         psum = psum + p1;
         reinterpret_cast<uint32_t *>(&pb[i / 4].u)[i % 4] = pack_bf16(p0, p1);

@@ -311,6 +311,63 @@ def bench_layer(torch, fh, gen, np, steps=64):
     return res
 
 
+def bench_kv(torch, fh, gen, np, reps=30):
+    """Decode attention of one query row over one layer's cache, cold (a
+    512 MiB write before every call evicts the Infinity Cache, as a 22-layer
+    cache is evicted between a layer's steps): sealed Q8 records
+    (focr_kv_attention_decode) against the FP32 compact cache
+    (focr_attention_decode), at 4,096 / 16,320 / 65,472 prefix positions plus
+    64 generated ones. Bytes = the records (176 B per group and prefix
+    position, 144 per generated one) or the compact keys and values."""
+    heads, kvh, T = 16, 8, 64
+    flush = torch.empty(128 << 20, dtype=torch.float32, device="cuda")
+    res = {}
+
+    def cold_us(fn):
+        for _ in range(3):
+            fn()
+        ts = []
+        for _ in range(reps):
+            flush.fill_(1.0)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1) * 1e3)
+        ts.sort()
+        return ts[len(ts) // 2]
+
+    for P in (4096, 16320, 65472):
+        k = gen.normal((P, 2 * kvh, 64), 1.0, 60)
+        k[:, 1::2, :32] = k[:, 0::2, :32]  # the pair's shared temporal half
+        v = gen.normal((P, kvh, 64), 1.0, 61)
+        gk = torch.from_numpy(gen.normal((T, kvh, 64), 1.0, 62)).cuda()
+        gv = torch.from_numpy(gen.normal((T, kvh, 64), 1.0, 63)).cuda()
+        q = torch.from_numpy(gen.normal((1, heads, 64), 1.0, 64)).cuda()
+        sinks = torch.from_numpy(gen.uniform(heads, -2.0, 2.0, 65)).cuda()
+        out = torch.empty((1, heads, 64), device="cuda")
+        kd, vd = torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda()
+        split = fh.KvSplit.seal(8, kd, vd, P, P + T, heads, kvh)
+        split.append(gk, gv, T)
+        q8_us = cold_us(lambda: split.attention_decode(q, 1, sinks, out=out))
+        split.free()
+        vals = torch.cat([vd, gv])
+        kv = fh.CompactKv(kd, gk, vals, P, P + T, heads, kvh, 64)
+        geo = fh.Geometry(P + T - 1, 0, 4096)
+        f32_us = cold_us(lambda: fh.attention_decode(q, kv, 1, geo, sinks, output=out))
+        q8_bytes = kvh * (P * 176 + T * 144)
+        f32_bytes = 4 * 64 * (P * heads + T * kvh + (P + T) * kvh)
+        res[f"prefix_{P}"] = {"q8_us": round(q8_us, 2), "q8_bytes": q8_bytes,
+                              "q8_gbs": round(q8_bytes / (q8_us * 1e-6) / 1e9, 1),
+                              "compact_us": round(f32_us, 2), "compact_bytes": f32_bytes,
+                              "compact_gbs": round(f32_bytes / (f32_us * 1e-6) / 1e9, 1),
+                              "speedup": round(f32_us / q8_us, 2)}
+        del kd, vd, vals
+    del flush
+    return res
+
+
 def bench_screen(torch, fh, gen, np, reps=40):
     """The INT8 screened vocabulary head (65,536 x 768, FP32 head N(0, 0.02)):
     one exact greedy selection per call (rows 1 and 5, synchronous, host wall
@@ -504,7 +561,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--ops", default="gemv,gemm,i16,attention,layer,screen,copy")
+    ap.add_argument("--ops", default="gemv,gemm,i16,attention,layer,kv,screen,copy")
     ap.add_argument("--reps", type=int, default=20, help="timed launches per secondary op")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
@@ -561,6 +618,9 @@ def main():
     if "layer" in ops:
         per_op["layer_int8_16k"] = bench_layer(torch, fh, gen, np)
         log(f"layer: {per_op['layer_int8_16k']}")
+    if "kv" in ops:
+        per_op["kv_decode_cold"] = bench_kv(torch, fh, gen, np)
+        log(f"kv decode (cold): {per_op['kv_decode_cold']}")
     if "screen" in ops:
         per_op["screened_head_65536x768"] = bench_screen(torch, fh, gen, np)
         log(f"screened head: {per_op['screened_head_65536x768']}")

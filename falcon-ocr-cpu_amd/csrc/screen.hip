@@ -96,13 +96,14 @@ __device__ __forceinline__ float sum8_lanes(float v, int p) {
 
 // Dynamic LDS of screen_kernel: x [rows][groups][68] (each 64-channel group
 // padded by 16 bytes, so neighbouring groups start in different banks; the
-// four lanes of a group read the same address), then the per-(wave, group,
-// row) lane values u [4][16][4][8] and scales [4][16][4] (consecutive lanes,
+// four lanes of a group read the same address), then the per-(input of a
+// pair, wave, group, row) lane values u [2][4][16][4][8] and scales
+// [4][16][4] (consecutive lanes,
 // consecutive words), then norms [rows][16] and the per-(row, wave) maxima
 // [rows][4].
 constexpr int kXPitch = kGroup + 4;
 __host__ __device__ inline size_t screen_lds_bytes(int rows, int dim) {
-  return sizeof(float) * (static_cast<size_t>(rows) * (dim / kGroup) * kXPitch + 4 * 4 * kMaxGroups * 8 +
+  return sizeof(float) * (static_cast<size_t>(rows) * (dim / kGroup) * kXPitch + 2 * 4 * 4 * kMaxGroups * 8 +
                           4 * 4 * kMaxGroups + rows * kMaxGroups + rows * 4);
 }
 
@@ -112,9 +113,9 @@ __global__ __launch_bounds__(256) void screen_kernel(ScreenArgs a) {
   const int dim = a.dim, groups = a.groups, rows = a.rows;
   const int xrow = groups * kXPitch;                    // floats per staged input row
   float *xs = lds;                                      // [rows][groups][kXPitch]
-  float(*u)[kMaxGroups][4][8] = reinterpret_cast<float(*)[kMaxGroups][4][8]>(xs + rows * xrow);
-  float(*sc)[kMaxGroups][4] = reinterpret_cast<float(*)[kMaxGroups][4]>(xs + rows * xrow + 4 * 4 * kMaxGroups * 8);
-  float *norms = xs + rows * xrow + 4 * 4 * kMaxGroups * 9;  // [rows][16]
+  float(*u)[4][kMaxGroups][4][8] = reinterpret_cast<float(*)[4][kMaxGroups][4][8]>(xs + rows * xrow);
+  float(*sc)[kMaxGroups][4] = reinterpret_cast<float(*)[kMaxGroups][4]>(xs + rows * xrow + 2 * 4 * 4 * kMaxGroups * 8);
+  float *norms = xs + rows * xrow + 2 * 4 * 4 * kMaxGroups * 8 + 4 * 4 * kMaxGroups;  // [rows][16]
   float *wmax = norms + rows * kMaxGroups;                  // [rows][4]
 
   // The first `rows` workgroups run prepare's input checks instead (all
@@ -218,58 +219,71 @@ __global__ __launch_bounds__(256) void screen_kernel(ScreenArgs a) {
 #pragma unroll
     for (int gg = 0; gg < kMaxGroups; gg++) ss[gg] = sc[wave][gg][row_in_wave];
 
-    for (int r = 0; r < rows; r++) {
-      // screen_row's group step: a0 over x[base + j + p], a1 over
-      // x[base + j + 8 + p], j = 0, 16, 32, 48; then a0 + a1 per lane p.
-      float4 *dst = reinterpret_cast<float4 *>(u[wave][g][row_in_wave]);
+    // screen_row's group step for input r into LDS slice `half`: a0 over
+    // x[base + j + p], a1 over x[base + j + 8 + p], j = 0, 16, 32, 48; then
+    // a0 + a1 per lane p.
+    auto products = [&](int r, int half) {
+      float4 *dst = reinterpret_cast<float4 *>(u[half][wave][g][row_in_wave]);
       if (!active) {
         dst[0] = dst[1] = make_float4(0.f, 0.f, 0.f, 0.f);
-      } else {
-        const float4 *xg = reinterpret_cast<const float4 *>(xs + r * xrow + g * kXPitch);
-        float a0[8], a1[8];
-#pragma unroll
-        for (int p = 0; p < 8; p++) a0[p] = a1[p] = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-          const float4 x0 = xg[4 * j], x1 = xg[4 * j + 1], x2 = xg[4 * j + 2], x3 = xg[4 * j + 3];
-          const float xa[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-          const float xb[8] = {x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
-#pragma unroll
-          for (int p = 0; p < 8; p++) {
-            a0[p] = __builtin_fmaf(xa[p], cf[16 * j + p], a0[p]);
-            a1[p] = __builtin_fmaf(xb[p], cf[16 * j + 8 + p], a1[p]);
-          }
-        }
-        dst[0] = make_float4(a0[0] + a1[0], a0[1] + a1[1], a0[2] + a1[2], a0[3] + a1[3]);
-        dst[1] = make_float4(a0[4] + a1[4], a0[5] + a1[5], a0[6] + a1[6], a0[7] + a1[7]);
+        return;
       }
-      // The row's 16 lanes exchange through this wave's own LDS slice.
+      const float4 *xg = reinterpret_cast<const float4 *>(xs + r * xrow + g * kXPitch);
+      float a0[8], a1[8];
+#pragma unroll
+      for (int p = 0; p < 8; p++) a0[p] = a1[p] = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const float4 x0 = xg[4 * j], x1 = xg[4 * j + 1], x2 = xg[4 * j + 2], x3 = xg[4 * j + 3];
+        const float xa[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        const float xb[8] = {x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
+#pragma unroll
+        for (int p = 0; p < 8; p++) {
+          a0[p] = __builtin_fmaf(xa[p], cf[16 * j + p], a0[p]);
+          a1[p] = __builtin_fmaf(xb[p], cf[16 * j + 8 + p], a1[p]);
+        }
+      }
+      dst[0] = make_float4(a0[0] + a1[0], a0[1] + a1[1], a0[2] + a1[2], a0[3] + a1[3]);
+      dst[1] = make_float4(a0[4] + a1[4], a0[5] + a1[5], a0[6] + a1[6], a0[7] + a1[7]);
+    };
+    // Inputs go in pairs: both inputs' products, then lanes g < 8 finish
+    // input r0 and lanes g >= 8 input r0 + 1 (each a 32-lane half of the
+    // wave), so the exchange and its waits happen once per pair.
+    for (int r0 = 0; r0 < rows; r0 += 2) {
+      products(r0, 0);
+      if (r0 + 1 < rows) products(r0 + 1, 1);
+      // The row's 16 lanes exchange through this wave's own LDS slices.
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      if (live && g < 8) {
+      const int half = g >> 3, p = g & 7;
+      const int r = r0 + half;
+      if (live && r < rows) {
         // Lane p accumulates row[p] = fma(a0 + a1, s_g, row[p]) over the
         // groups; S = sum fma(s_g, n_g, S) alongside.
-        const int p = g;
         float uu[kMaxGroups];
 #pragma unroll
-        for (int gg = 0; gg < kMaxGroups; gg++) uu[gg] = u[wave][gg][row_in_wave][p];
+        for (int gg = 0; gg < kMaxGroups; gg++) uu[gg] = u[half][wave][gg][row_in_wave][p];
         float acc = 0.0f, total = 0.0f;
 #pragma unroll
         for (int gg = 0; gg < kMaxGroups; gg++) {
           acc = __builtin_fmaf(uu[gg], ss[gg], acc);
           total = __builtin_fmaf(ss[gg], norms[r * kMaxGroups + gg], total);
         }
-        const float q = sum8_stride4(acc);
+        const float q = sum8_stride4(acc);  // within this lane's 32-lane half
         const float bound = __builtin_fmaf(a.kappa, total, kEta);
         if (p == 0) {
           a.upper[static_cast<size_t>(r) * a.ustride + v] = q + bound;
-          // f32::max: a NaN operand is ignored.
-          wave_lower[r] = __builtin_fmaxf(wave_lower[r], q - bound);
+          // f32::max: a NaN operand is ignored. (Indexed by the pair's
+          // uniform r0, so the array stays in registers.)
+          if (half == 0)
+            wave_lower[r0] = __builtin_fmaxf(wave_lower[r0], q - bound);
+          else
+            wave_lower[r0 + 1] = __builtin_fmaxf(wave_lower[r0 + 1], q - bound);
         }
       }
-      // The next input's products overwrite this slice only after every lane
-      // has read it.
+      // The next pair's products overwrite these slices only after every
+      // lane has read them.
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");

@@ -1,6 +1,6 @@
 """Writes tests/golden/vectors.npz: the oracle's outputs (oracle/focr_oracle.c,
-the C restatement of the reference's operators) for small seeded inputs of
-every hot-path operator. The inputs are not stored: `vectors()` regenerates
+focr_kv.c and focr_screen.c, the C restatements of the reference's operators)
+for small seeded inputs of every hot-path operator. The inputs are not stored: `vectors()` regenerates
 them from the seeded generators of tests/gen.py, and the file keeps only the
 keys listed in OUTPUTS. Committed so that the oracle's results are frozen
 (tests/test_golden.py recomputes them bit for bit) and so that the GPU tests
@@ -90,6 +90,41 @@ def vectors():
     rope = np.stack([np.cos(ang), np.sin(ang)], -1).astype(np.float32)
     v["qkv_in"], v["qkv_rope"] = qkv, rope
     v["qkv_q"], v["qkv_pk"], v["qkv_gk"], v["qkv_v"] = oracle.qkv_rows(qkv, 4, rope, H, G, 2)
+    # Sealed Q8 and Q16 KV records (Kv::Q8 / Kv::Q16): a 9-position prefix
+    # whose GQA pairs share the temporal half, 3 generated positions (one
+    # value block holding an infinity), decoded as the compact cache; decode
+    # attention of 2 rows over the first two generated positions.
+    P, T, cap = 9, 3, 16
+    kp = gen.values(P * H * 64, 29, 2.0).reshape(P, H, 64)
+    kp[:, 1::2, :32] = kp[:, 0::2, :32]
+    vp = gen.values(P * G * 64, 30, 2.0).reshape(P, G, 64)
+    tk = gen.values(T * G * 64, 31, 1.5).reshape(T, G, 64)
+    tv = gen.values(T * G * 64, 32, 1.5).reshape(T, G, 64)
+    tv[2, 4, 40] = np.inf
+    v["kv_pk"], v["kv_v"], v["kv_tk"], v["kv_tv"] = kp, vp, tk, tv
+    kq = gen.values(2 * H * 64, 33, 1.0).reshape(2, H, 64)
+    v["kv_q"] = kq
+    for bits in (8, 16):
+        sealed = oracle.kv_seal(bits, kp, vp, P, H, G)
+        tail = oracle.kv_tail(bits, G, cap - P)
+        for i in range(T):
+            oracle.kv_push(bits, tk[i], tv[i], G, cap - P, i, tail)
+        dpk, dv, dgk = oracle.kv_dequantize(bits, sealed, P, H, G, tail, cap - P, T)
+        v[f"kv{bits}_pk"], v[f"kv{bits}_v"], v[f"kv{bits}_gk"] = dpk, dv, dgk
+        # Decode over the finite part of the cache: 2 rows at the first two
+        # generated positions (the NaN block is in the third).
+        v[f"kv{bits}_dec"] = oracle.attention_decode(kq, dpk, dgk[:2], dv[:P + 2], 2, P, P + 2, H, G, P, 0, 0,
+                                                     v["att_sinks"])
+    # The INT8 screen of a 512 x 128 FP32 head: codes, scales and constants,
+    # and the exact greedy token of 2 inputs.
+    head = gen.values(512 * 128, 34, 0.05).reshape(512, 128)
+    sc_codes, sc_scales, sc_wmax, sc_kappa = oracle.screen_build(head, 512, 128)
+    v["screen_head"], v["screen_codes"], v["screen_scales"] = head, sc_codes, sc_scales
+    v["screen_consts"] = np.array([sc_wmax, sc_kappa], np.float32)
+    sx = gen.values(2 * 128, 35, 1.0).reshape(2, 128)
+    v["screen_x"] = sx
+    v["screen_token"] = np.array([oracle.argmax(oracle.linear_decode(32, head, None, 512, 128, 32, sx[r:r + 1], 1)[0])
+                                  for r in range(2)], np.int64)
     # A9: argmax over one row.
     logits = gen.values(1000, 28)
     v["argmax_logits"], v["argmax_token"] = logits, np.array([oracle.argmax(logits)], np.int64)
@@ -98,7 +133,9 @@ def vectors():
 
 OUTPUTS = ("gemv8_out", "gemv8_glu", "dequant8", "gemv16_out", "gemv16_glu", "dequant16", "gemv32_out", "rms_out",
            "panel_store", "panel_glu", "panel_add", "i16_store", "i16_glu", "att_online", "att_static", "att_bf16",
-           "dec_out", "qkv_q", "qkv_pk", "qkv_gk", "qkv_v", "argmax_token")
+           "dec_out", "qkv_q", "qkv_pk", "qkv_gk", "qkv_v", "argmax_token", "kv8_pk", "kv8_v", "kv8_gk", "kv8_dec",
+           "kv16_pk", "kv16_v", "kv16_gk", "kv16_dec", "screen_codes", "screen_scales", "screen_consts",
+           "screen_token")
 FILE = Path(__file__).resolve().parent / "vectors.npz"
 
 if __name__ == "__main__":

@@ -113,3 +113,35 @@ def test_argmax(case):
     fh, v, want = case
     logits = v["argmax_logits"]
     assert fh.argmax(to_dev(logits), 1, logits.size) == [int(want["argmax_token"][0])]
+
+
+@pytest.mark.parametrize("bits", [8, 16])
+def test_sealed_kv_records(case, bits):
+    # Seal, append (one block holding an infinity decodes to NaN), the decoded
+    # records bit for bit, and decode attention over them within FP32 rounding.
+    fh, v, want = case
+    P, T, cap = 9, 3, 16
+    kv = fh.KvSplit.seal(bits, to_dev(v["kv_pk"]), to_dev(v["kv_v"]), P, cap, H, G)
+    kv.append(to_dev(v["kv_tk"][:2]), to_dev(v["kv_tv"][:2]), 2)
+    got = host(kv.attention_decode(to_dev(v["kv_q"]), 2, to_dev(v["att_sinks"])))
+    close(got, want[f"kv{bits}_dec"], 1e-5)
+    kv.append(to_dev(v["kv_tk"][2:]), to_dev(v["kv_tv"][2:]), T - 2)
+    pk, vals, gk = (host(t) for t in kv.dequantize())
+    assert_bitwise(pk, want[f"kv{bits}_pk"], "prefix keys")
+    assert_bitwise(vals, want[f"kv{bits}_v"], "values")
+    assert_bitwise(gk, want[f"kv{bits}_gk"], "generated keys")
+    kv.free()
+
+
+def test_screened_head(case):
+    fh, v, want = case
+    wmax, kappa = (float(c) for c in want["screen_consts"])
+    built = fh.ScreenedHead.build(v["screen_head"])
+    assert built.constants() == (wmax, kappa)
+    stored = fh.ScreenedHead.from_parts(want["screen_codes"], want["screen_scales"], wmax, kappa)
+    head = fh.Linear.from_f32(v["screen_head"])
+    for screen in (built, stored):
+        picks = screen.select(to_dev(v["screen_x"]), 2, head)
+        assert [tok for tok, _ in picks] == [int(t) for t in want["screen_token"]]
+        screen.free()
+    head.free()

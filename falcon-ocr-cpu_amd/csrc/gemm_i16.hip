@@ -162,7 +162,9 @@ struct GroupTile {
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(1))) const void global_void;
 
-template <int EPI>
+// NB: 16-column blocks per wave (4: 128-column workgroup tiles; 2: 64-column
+// tiles, twice the workgroups for the narrower projections).
+template <int EPI, int NB>
 __global__ __launch_bounds__(256) void gemm_kernel(const int8_t *__restrict__ a_tiles, const float *__restrict__ steps,
                                                    const float *__restrict__ exc_inputs, const int8_t *__restrict__ b_tiles,
                                                    const int32_t *__restrict__ wsum, const float *__restrict__ sw,
@@ -174,7 +176,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const int8_t *__restrict__ a_
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
   const int mb0 = blockIdx.x * (kBM / 16);
-  const int nb0 = blockIdx.y * (kBN / 16);
+  const int nb0 = blockIdx.y * (2 * NB);
   const int col_blocks = n / 16;
 
   // Group g -> t by DMA (16 B per lane; sources clamped into their arrays,
@@ -187,7 +189,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const int8_t *__restrict__ a_
       __builtin_amdgcn_global_load_lds((global_void *)(ga + 16 * (tid + 256 * i)), (lds_void *)(&t.a[64 * wave + 256 * i]),
                                        16, 0, 0);
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
+    for (int i = 0; i < NB / 2; i++) {
       const int idx = tid + 256 * i;
       int blk = nb0 + idx / 64;
       blk = blk < col_blocks ? blk : col_blocks - 1;
@@ -209,11 +211,11 @@ __global__ __launch_bounds__(256) void gemm_kernel(const int8_t *__restrict__ a_
     }
   };
 
-  float acc[4][4][4];
+  float acc[4][NB][4];
 #pragma unroll
   for (int i = 0; i < 4; i++)
 #pragma unroll
-    for (int j = 0; j < 4; j++)
+    for (int j = 0; j < NB; j++)
 #pragma unroll
       for (int r = 0; r < 4; r++) acc[i][j][r] = 0.0f;
 
@@ -223,7 +225,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const int8_t *__restrict__ a_
     __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's copies of cur
     __syncthreads();                     // everyone's; nobody still reads next
     if (g + 1 < groups) copy_group(next, g + 1);
-    v4i ahi[4], alo[4], b[4];
+    v4i ahi[4], alo[4], b[NB];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const int rb = wm * 4 + i;
@@ -232,15 +234,15 @@ __global__ __launch_bounds__(256) void gemm_kernel(const int8_t *__restrict__ a_
       alo[i] = v4i{static_cast<int>(lv.x), static_cast<int>(lv.y), static_cast<int>(lv.z), static_cast<int>(lv.w)};
     }
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const uint4 w = cur.b[(wn * 4 + j) * 64 + lane];
+    for (int j = 0; j < NB; j++) {
+      const uint4 w = cur.b[(wn * NB + j) * 64 + lane];
       b[j] = v4i{static_cast<int>(w.x), static_cast<int>(w.y), static_cast<int>(w.z), static_cast<int>(w.w)};
     }
-    int32_t ws[4];
-    float swv[4];
+    int32_t ws[NB];
+    float swv[NB];
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const int c = (wn * 4 + j) * 16 + col_in;
+    for (int j = 0; j < NB; j++) {
+      const int c = (wn * NB + j) * 16 + col_in;
       ws[j] = cur.wsum[c];
       swv[j] = cur.sw[c];
     }
@@ -256,7 +258,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const int8_t *__restrict__ a_
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
+      for (int j = 0; j < NB; j++) {
         const v4i zero = {0, 0, 0, 0};
         v4i hsum = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi[i], b[j], zero, 0, 0, 0);
         v4i c;
@@ -281,8 +283,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(const int8_t *__restrict__ a_
   for (int i = 0; i < 4; i++) {
     const int row_base = (mb0 + wm * 4 + i) * 16 + 4 * quad;
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const int col = (nb0 + wn * 4 + j) * 16 + col_in;
+    for (int j = 0; j < NB; j++) {
+      const int col = (nb0 + wn * NB + j) * 16 + col_in;
       const bool col_ok = col < n;
 #pragma unroll
       for (int r = 0; r < 4; r++) {
@@ -331,18 +333,22 @@ int launch_prefill_i16(Ctx *ctx, const Linear *lin, const float *x, size_t rows,
                      row_scale, lin->exc_index, static_cast<int>(lin->n_exc), a_tiles, steps, exc_inputs,
                      static_cast<int>(m_pad));
   FOCR_HIP_CHECK(hipGetLastError());
-  const dim3 grid(static_cast<unsigned>(m_pad / kBM), static_cast<unsigned>((n + kBN - 1) / kBN));
-#define FOCR_LAUNCH_I16(E)                                                                                      \
-  hipLaunchKernelGGL(gemm_kernel<E>, grid, dim3(256), 0, ctx->stream, a_tiles, steps, exc_inputs, lin->i16_b,   \
+  // Outputs up to 2,048 columns take 64-column tiles: the 768-output
+  // projections would otherwise fill only 6 column tiles, QKV 16.
+  const bool narrow = n <= 2048;
+  const dim3 grid(static_cast<unsigned>(m_pad / kBM), static_cast<unsigned>((n + (narrow ? 63 : 127)) / (narrow ? 64 : 128)));
+#define FOCR_LAUNCH_I16(E, NB)                                                                                  \
+  hipLaunchKernelGGL((gemm_kernel<E, NB>), grid, dim3(256), 0, ctx->stream, a_tiles, steps, exc_inputs, lin->i16_b, \
                      lin->i16_wsum, lin->i16_sw, lin->exc_vals, static_cast<int>(lin->n_exc), static_cast<int>(m), \
                      static_cast<int>(n), static_cast<int>(groups), static_cast<int>(row_blocks),                \
                      static_cast<int>(m_pad), out)
-  if (epilogue == FOCR_EPI_GLU)
-    FOCR_LAUNCH_I16(FOCR_EPI_GLU);
-  else if (epilogue == FOCR_EPI_ADD)
-    FOCR_LAUNCH_I16(FOCR_EPI_ADD);
-  else
-    FOCR_LAUNCH_I16(FOCR_EPI_STORE);
+  if (epilogue == FOCR_EPI_GLU) {
+    if (narrow) FOCR_LAUNCH_I16(FOCR_EPI_GLU, 2); else FOCR_LAUNCH_I16(FOCR_EPI_GLU, 4);
+  } else if (epilogue == FOCR_EPI_ADD) {
+    if (narrow) FOCR_LAUNCH_I16(FOCR_EPI_ADD, 2); else FOCR_LAUNCH_I16(FOCR_EPI_ADD, 4);
+  } else {
+    if (narrow) FOCR_LAUNCH_I16(FOCR_EPI_STORE, 2); else FOCR_LAUNCH_I16(FOCR_EPI_STORE, 4);
+  }
 #undef FOCR_LAUNCH_I16
   FOCR_HIP_CHECK(hipGetLastError());
   return FOCR_OK;

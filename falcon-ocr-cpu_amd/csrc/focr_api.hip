@@ -21,6 +21,15 @@ int set_error(int code, const std::string &message) {
 
 int ensure_scratch(Ctx *ctx, size_t bytes) {
   if (bytes <= ctx->scratch_bytes) return FOCR_OK;
+  // Growing frees the old buffer: a graph captured earlier would replay into
+  // freed memory, and neither a free nor a synchronization may run while the
+  // stream is being captured. Callers that capture pre-grow the scratch with
+  // focr_ctx_reserve_scratch (or one uncaptured call of the same shape).
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  FOCR_HIP_CHECK(hipStreamIsCapturing(ctx->stream, &capture));
+  FOCR_REQUIRE(capture == hipStreamCaptureStatusNone, FOCR_E_UNSUPPORTED,
+               "the context scratch must grow to " + std::to_string(bytes) +
+                   " bytes, which cannot happen during stream capture; call focr_ctx_reserve_scratch first");
   if (ctx->scratch) {
     FOCR_HIP_CHECK(hipStreamSynchronize(ctx->stream));
     FOCR_HIP_CHECK(hipFree(ctx->scratch));
@@ -165,6 +174,20 @@ void *focr_ctx_stream(const focr_ctx *handle) {
   return ctx ? static_cast<void *>(ctx->stream) : nullptr;
 }
 
+int focr_ctx_reserve_scratch(focr_ctx *handle, size_t bytes) {
+  Ctx *ctx = reinterpret_cast<Ctx *>(handle);
+  FOCR_REQUIRE(ctx, FOCR_E_ARG, "focr_ctx_reserve_scratch: null context");
+  FOCR_HIP_CHECK(hipSetDevice(ctx->device));
+  return ensure_scratch(ctx, bytes);
+}
+
+int focr_ctx_scratch_bytes(const focr_ctx *handle, size_t *bytes) {
+  const Ctx *ctx = reinterpret_cast<const Ctx *>(handle);
+  FOCR_REQUIRE(ctx && bytes, FOCR_E_ARG, "focr_ctx_scratch_bytes: null argument");
+  *bytes = ctx->scratch_bytes;
+  return FOCR_OK;
+}
+
 int focr_ctx_sync(focr_ctx *handle) {
   Ctx *ctx = reinterpret_cast<Ctx *>(handle);
   FOCR_REQUIRE(ctx, FOCR_E_ARG, "focr_ctx_sync: null context");
@@ -238,6 +261,8 @@ int focr_linear_upload(focr_ctx *handle, int bits, size_t n, size_t k, size_t gr
   // with_exceptions' rules (src/quant/linear.rs:366-390,437-452).
   if (n_exc) {
     FOCR_REQUIRE(bits != 32, FOCR_E_ARG, "exception columns need 8- or 16-bit codes");
+    // The kernels find a column's exception through a 16-bit index per input.
+    FOCR_REQUIRE(n_exc <= size_t(INT16_MAX), FOCR_E_UNSUPPORTED, "at most 32767 exception columns");
     FOCR_REQUIRE(exc_cols && exc_vals, FOCR_E_ARG, "focr_linear_upload: null exception arrays");
     for (size_t e = 0; e < n_exc; e++) {
       FOCR_REQUIRE(exc_cols[e] >= 0 && size_t(exc_cols[e]) < k, FOCR_E_VALUE, "exception column outside the inputs");

@@ -56,6 +56,8 @@ SIGNATURES = {
     "focr_ctx_use_own_stream": (_I, [_P]),
     "focr_ctx_stream": (_P, [_P]),
     "focr_ctx_sync": (_I, [_P]),
+    "focr_ctx_reserve_scratch": (_I, [_P, _Z]),
+    "focr_ctx_scratch_bytes": (_I, [_P, ctypes.POINTER(_Z)]),
     "focr_last_error": (ctypes.c_char_p, []),
     "focr_malloc": (_I, [_P, _Z, ctypes.POINTER(_P)]),
     "focr_free": (_I, [_P, _P]),
@@ -164,6 +166,15 @@ class Context:
 
     def sync(self) -> None:
         _check(lib().focr_ctx_sync(self.handle))
+
+    def reserve_scratch(self, nbytes: int) -> None:
+        """Grow the context scratch now (before a HIP graph capture)."""
+        _check(lib().focr_ctx_reserve_scratch(self.handle, int(nbytes)))
+
+    def scratch_bytes(self) -> int:
+        out = ctypes.c_size_t()
+        _check(lib().focr_ctx_scratch_bytes(self.handle, ctypes.byref(out)))
+        return out.value
 
     def close(self) -> None:
         if self.handle:

@@ -3,7 +3,7 @@
 `DecoderLayer` strings the C ABI's operators together the way
 ``Model::forward_layers`` does for one layer (src/model/mod.rs:513-691):
 
-prefill (rows > 8, a quantized body on the panel path, mod.rs:568,956-1007)::
+prefill of more than 8 rows (the panel path, mod.rs:568,956-1007)::
 
     row_scales(h)                          panel_qkv (rms norm folded into packing)
     qkv.prefill(h, row_scale) -> qkv        Epilogue::Store
@@ -13,8 +13,10 @@ prefill (rows > 8, a quantized body on the panel path, mod.rs:568,956-1007)::
     row_scales(h); w13.prefill(h) -> gated  Epilogue::Glu
     w2.prefill(gated) += h                  Epilogue::Add(h)
 
-decode / draft verification (1..=8 rows, project_qkv + attention_out_ffn,
-mod.rs:421-492)::
+decode / draft verification, and a prefill of at most 8 rows (1..=8 rows,
+project_qkv + attention_out_ffn, mod.rs:421-492; a short prefill keeps the
+online FP32 softmax and no BF16 attention, ``PrefillPlan::softmaxes(false)``,
+src/kernels/mod.rs:148-153)::
 
     rms_norm(h) . qkv -> qkv                focr_linear_decode_ex, rms_norm in the GEMV
     qkv_rows -> q, generated keys, values   split_norm_rope + LayerCache::append
@@ -43,7 +45,7 @@ from __future__ import annotations
 
 from typing import Optional
 
-from . import (CompactKv, Context, Epilogue, FocrError, Geometry, KvSplit, PrefillOptions, PrefillProjection,
+from . import (CompactKv, Context, Epilogue, FocrError, Geometry, KvSplit, PrefillOptions, PrefillProjection, Softmax,
                attention_prefill_bf16, attention_with, default_context, qkv_rows, row_scales)
 
 
@@ -115,9 +117,15 @@ class DecoderLayer:
         if self.split is not None:
             self.split.free()
             self.split = None
-        rs = row_scales(h, self.dim, out=self._buf("rs", (rows,)), ctx=ctx)
-        qkv = self.qkv.prefill(h, rows, row_scale=rs, epilogue=Epilogue.STORE, kernel=self.projection,
-                               out=self._buf("qkv", (rows, self.qkv.out_dim)))
+        # The panel path takes more than 8 rows (`panel = rows > 8 && ...`,
+        # model/mod.rs:568); shorter prompts run the decode step's GEMVs.
+        panel = rows > 8
+        if panel:
+            rs = row_scales(h, self.dim, out=self._buf("rs", (rows,)), ctx=ctx)
+            qkv = self.qkv.prefill(h, rows, row_scale=rs, epilogue=Epilogue.STORE, kernel=self.projection,
+                                   out=self._buf("qkv", (rows, self.qkv.out_dim)))
+        else:
+            qkv = self.qkv.linear_ex(h, rows, rms_norm=True, out=self._buf("qkv", (rows, self.qkv.out_dim)))
         mark("qkv")
         self.prefix_len = rows
         q = qkv_rows(qkv, rows, rope, self.n_heads, self.n_kv_heads, rows, q=self._buf("q", (rows, self.n_heads, 64)),
@@ -130,21 +138,31 @@ class DecoderLayer:
         # `false` (a shape it does not take) falls back to the FP32 tiles
         # (Model::forward_layers, model/mod.rs:621-646 -> LayerCache::attention,
         # model/cache.rs:142-197).
-        if not (self.bf16_attention and attention_prefill_bf16(q, self.kv(rows), rows, geometry, self.sinks, attn,
-                                                               self.options, ctx=ctx)):
-            attn = attention_with(q, self.kv(rows), rows, geometry, self.sinks, self.options, output=attn, ctx=ctx)
+        options = self.options if panel else PrefillOptions(exp=self.options.exp, fp32_softmax=Softmax.ONLINE,
+                                                            softmax=self.options.softmax)
+        if not (panel and self.bf16_attention and attention_prefill_bf16(q, self.kv(rows), rows, geometry,
+                                                                         self.sinks, attn, options, ctx=ctx)):
+            attn = attention_with(q, self.kv(rows), rows, geometry, self.sinks, options, output=attn, ctx=ctx)
         mark("attention")
         if self.kv_bits != 32:
             self.split = KvSplit.seal(self.kv_bits, self.prefix_k[:rows], self.v[:rows], rows, self.capacity,
                                       self.n_heads, self.n_kv_heads, ctx=ctx)
             mark("seal")
-        self.wo.prefill(attn, rows, epilogue=Epilogue.ADD, out=h, kernel=self.projection)
-        mark("wo")
-        rs = row_scales(h, self.dim, out=rs, ctx=ctx)
-        gated = self.w13.prefill(h, rows, row_scale=rs, epilogue=Epilogue.GLU, kernel=self.projection,
-                                 out=self._buf("gated", (rows, self.w13.out_dim // 2)))
-        mark("w13")
-        self.w2.prefill(gated, rows, epilogue=Epilogue.ADD, out=h, kernel=self.projection)
+        if panel:
+            self.wo.prefill(attn, rows, epilogue=Epilogue.ADD, out=h, kernel=self.projection)
+            mark("wo")
+            rs = row_scales(h, self.dim, out=rs, ctx=ctx)
+            gated = self.w13.prefill(h, rows, row_scale=rs, epilogue=Epilogue.GLU, kernel=self.projection,
+                                     out=self._buf("gated", (rows, self.w13.out_dim // 2)))
+            mark("w13")
+            self.w2.prefill(gated, rows, epilogue=Epilogue.ADD, out=h, kernel=self.projection)
+        else:
+            self.wo.linear_ex(attn, rows, epilogue=Epilogue.ADD, out=h)
+            mark("wo")
+            gated = self.w13.linear_ex(h, rows, rms_norm=True, epilogue=Epilogue.GLU,
+                                       out=self._buf("gated", (rows, self.w13.out_dim // 2)))
+            mark("w13")
+            self.w2.linear_ex(gated, rows, epilogue=Epilogue.ADD, out=h)
         mark("w2")
         self.len = rows
         return h

@@ -78,6 +78,16 @@ int focr_ctx_set_stream(focr_ctx *ctx, void *hip_stream);
 int focr_ctx_use_own_stream(focr_ctx *ctx);
 void *focr_ctx_stream(const focr_ctx *ctx);
 int focr_ctx_sync(focr_ctx *ctx);
+/* The context scratch (INT16 activation codes, attention partial states,
+ * BF16 K/V copies) grows on demand by free + malloc. No reference
+ * counterpart: the reference's Scratch (src/quant/linear.rs:311-315) is a
+ * host Vec. Growing invalidates graphs captured earlier (they would replay
+ * into freed memory) and is refused with FOCR_E_UNSUPPORTED while the
+ * stream is capturing: a caller that captures reserves the largest size
+ * first, or makes one uncaptured call of each shape. Synchronizes the
+ * context's stream when it grows. */
+int focr_ctx_reserve_scratch(focr_ctx *ctx, size_t bytes);
+int focr_ctx_scratch_bytes(const focr_ctx *ctx, size_t *bytes);
 /* Message of the calling thread's last failure ("" if none). */
 const char *focr_last_error(void);
 /* Device memory helpers for callers without HIP headers. */

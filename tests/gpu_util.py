@@ -38,3 +38,15 @@ def max_rel(got, want):
     """max |got - want| / max |want| over the tensor (the FP32 tolerance metric)."""
     want = np.asarray(want, dtype=np.float64)
     return float(np.max(np.abs(np.asarray(got, np.float64) - want)) / max(np.max(np.abs(want)), 1e-30))
+
+
+def oracle_threads():
+    """Threads for the CPU oracle: the CPUs this process may run on, at most 16
+    (the host share of a one-GPU job)."""
+    import os
+
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))

@@ -268,6 +268,54 @@ def test_decoder_layer_prefill_and_decode(fh):
         lin.free()
 
 
+@pytest.mark.parametrize("rows", [1, 3, 5, 8])
+def test_decoder_layer_short_prefill_takes_the_decode_path(fh, rows):
+    """A prompt of at most 8 rows is not a panel prefill (`panel = rows > 8`,
+    model/mod.rs:568): project_qkv / attention_out_ffn run the FP32 decode
+    GEMVs with the separate rms_norm passes, and the attention is the online
+    FP32 one whatever the plan's BF16 or static choice
+    (PrefillPlan::softmaxes(false), kernels/mod.rs:148-153). Everything before
+    the attention is bitwise the oracle; the attention within the FP32
+    tolerance; the layer output within 1e-4 (it carries the attention's)."""
+    import torch
+
+    image = (0, max(rows - 1, 0))
+    w = layer_weights(90 + rows)
+    lins = {name: fh.QuantLinear(8, *w[name], 64) for name in w}
+    sinks = gen.uniform(H, -2.0, 2.0, 91)
+    opts = fh.PrefillOptions(fp32_softmax=fh.Softmax.STATIC, softmax=fh.Softmax.STATIC)
+    layer = fh.DecoderLayer(lins["qkv"], lins["wo"], lins["w13"], lins["w2"], to_dev(sinks), capacity=rows + 2,
+                            options=opts, bf16_attention=True)
+    h0 = gen.normal((rows, DIM), 1.0, 92)
+    rope = rope_table(rows, 93)
+    h = to_dev(h0)
+    layer.prefill(h, to_dev(rope), *image)
+    torch.cuda.synchronize()
+    dec = lambda name, x, glu=False: (oracle.linear_decode_glu if glu else oracle.linear_decode)(
+        8, *w[name], w[name][0].shape[0], w[name][0].shape[1], 64, x, rows)
+    qkv = dec("qkv", h0 * oracle.row_scales(h0, DIM)[:, None])
+    q, pk, _, v = oracle.qkv_rows(qkv, rows, rope, H, G, rows)
+    assert_bitwise(host(layer._buf("qkv", (rows, qkv.shape[1]))), qkv, "qkv GEMV")
+    assert_bitwise(host(layer.prefix_k[:rows]), pk, "prefix keys")
+    assert_bitwise(host(layer.v[:rows]), v, "values")
+    if rows >= 4:  # the prefill tiles (attention/mod.rs:271-299), online softmax
+        want_attn = oracle.attention_prefill(q, pk, v, rows, rows, rows, H, G, 0, *image, sinks)
+    else:  # decode64 / online::attention
+        want_attn = oracle.attention_decode(q, pk, None, v, rows, rows, rows, H, G, 0, *image, sinks)
+    close(host(layer._buf("attn", (rows, H, 64))), want_attn)
+    want_h = h0 + dec("wo", want_attn.reshape(rows, -1))
+    gated = dec("w13", want_h * oracle.row_scales(want_h, DIM)[:, None], glu=True)
+    want_h = want_h + dec("w2", gated)
+    assert max_rel(host(h), want_h) <= 1e-4
+    # The layer output is bitwise the decode path's on the layer's own attention.
+    attn = host(layer._buf("attn", (rows, H, 64))).reshape(rows, -1)
+    exact = h0 + dec("wo", attn)
+    exact = exact + dec("w2", dec("w13", exact * oracle.row_scales(exact, DIM)[:, None], glu=True))
+    assert_bitwise(host(h), exact, "layer output over the layer's attention")
+    for lin in lins.values():
+        lin.free()
+
+
 @pytest.mark.parametrize("bits", [8, 16])
 def test_decoder_layer_over_the_sealed_cache(fh, bits):
     """Kv::Q8 / Kv::Q16: the prefill seals the prefix after its attention

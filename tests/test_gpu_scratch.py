@@ -1,0 +1,64 @@
+"""The context scratch and HIP graph capture: a call that would grow the
+scratch during capture is refused (FOCR_E_UNSUPPORTED, nothing launched);
+after focr_ctx_reserve_scratch the same call captures, and every replay of
+the graph, with eager work and synchronizations between the replays, equals
+the eager result bit for bit."""
+import numpy as np
+import pytest
+
+import gen
+from gpu_util import assert_bitwise, host, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def test_scratch_growth_refused_during_capture_then_reserved():
+    import torch
+
+    import focr_hip as fh
+
+    ctx = fh.Context(0)
+    m, k, n = 300, 768, 256
+    codes = gen.codes_uniform((n, k), -127, 127, np.int8, 1)
+    scales = gen.uniform((n, k // 64), 1e-4, 4e-4, 2)
+    lin = fh.QuantLinear(8, codes, scales, 64, ctx=ctx)
+    x = to_dev(gen.normal((m, k), 1.0, 3))
+    out = torch.empty((m, n), device="cuda:0")
+    assert ctx.scratch_bytes() == 0
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            ctx.use_stream(torch.cuda.current_stream())
+            out.zero_()
+            with pytest.raises(fh.FocrError, match="stream capture"):
+                lin.prefill(x, m, out=out, kernel=fh.PrefillProjection.I16)
+    ctx.use_stream(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    assert ctx.scratch_bytes() == 0
+    del g
+
+    # Reserve, capture, replay.
+    ctx.reserve_scratch(8 << 20)
+    reserved = ctx.scratch_bytes()
+    assert reserved >= 8 << 20
+    eager = host(lin.prefill(x, m, kernel=fh.PrefillProjection.I16))
+    g = torch.cuda.CUDAGraph()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            ctx.use_stream(torch.cuda.current_stream())
+            lin.prefill(x, m, out=out, kernel=fh.PrefillProjection.I16)
+    ctx.use_stream(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    assert ctx.scratch_bytes() == reserved
+    for rep in range(3):
+        out.fill_(float("nan"))
+        lin.prefill(x, m, kernel=fh.PrefillProjection.I16)  # eager work between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert_bitwise(host(out), eager, f"replay {rep}")
+    lin.free()
+    ctx.close()

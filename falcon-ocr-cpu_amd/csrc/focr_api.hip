@@ -123,6 +123,8 @@ int focr_ctx_create(int device, focr_ctx **out) {
   FOCR_HIP_CHECK(hipGetDeviceProperties(&prop, device));
   FOCR_REQUIRE(std::strncmp(prop.gcnArchName, "gfx950", 6) == 0, FOCR_E_UNSUPPORTED,
                std::string("focr_hip is built for gfx950, device is ") + prop.gcnArchName);
+  int rc = noalloc_scratch_init(device);
+  if (rc != FOCR_OK) return rc;
   Ctx *ctx = new (std::nothrow) Ctx();
   FOCR_REQUIRE(ctx, FOCR_E_ARG, "focr_ctx_create: out of host memory");
   ctx->device = device;

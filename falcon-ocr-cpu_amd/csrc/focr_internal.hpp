@@ -46,6 +46,9 @@ struct Ctx {
 
 // Grows the context scratch to at least `bytes` (hipMalloc on growth only).
 int ensure_scratch(Ctx *ctx, size_t bytes);
+// Resolves the device address of the no-alloc decode scratch for `device`
+// (which must be current); once per device.
+int noalloc_scratch_init(int device);
 
 // ---- device-resident matrix ---------------------------------------------
 // Decode GEMV layout (built at upload): wave tiles of kGemvChannels output

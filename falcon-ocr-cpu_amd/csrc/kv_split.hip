@@ -29,11 +29,51 @@
 // LDS, then the shared combine kernel. Roofline: HBM; bytes per call = the visible
 // records (Q8: 176 bytes per group and prefix position, 8 groups = 1,408
 // bytes per position against 6,144 for the FP32 compact cache).
+#include <mutex>
 #include <vector>
 
 #include "decode_common.hpp"
 
+// Partial softmax states of focr_kv_attention_decode_noalloc: a fixed
+// device-resident array instead of the context scratch, so that the call
+// allocates nothing. Every GPU the library runs on holds its own copy for
+// the life of the process. In host code `scratch` names a host-side stand-in,
+// never device memory: kernels get the per-device address that
+// hipGetSymbolAddress returns (noalloc_scratch below).
+constexpr size_t kNoAllocScratchBytes = size_t(4608) << 10;  // 4.5 MiB
+static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
+
 namespace focr {
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+float *g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+// Resolves this device's address of `scratch`, once per device, with the
+// device current (called by focr_ctx_create).
+int noalloc_scratch_init(int device) {
+  FOCR_REQUIRE(device >= 0 && device < kMaxDevices, FOCR_E_UNSUPPORTED, "device index beyond the no-alloc table");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[device]) return FOCR_OK;
+  int current = -1;
+  FOCR_HIP_CHECK(hipGetDevice(&current));
+  FOCR_REQUIRE(current == device, FOCR_E_ARG, "noalloc_scratch_init: the device must be current");
+  void *ptr = nullptr;
+  FOCR_HIP_CHECK(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+  FOCR_REQUIRE(ptr, FOCR_E_HIP, "hipGetSymbolAddress returned no address for the no-alloc scratch");
+  g_scratch_ptr[device] = static_cast<float *>(ptr);
+  return FOCR_OK;
+}
+
+namespace {
+float *noalloc_scratch(int device) {
+  if (device < 0 || device >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  return g_scratch_ptr[device];
+}
+}  // namespace
 
 struct KvSplit {
   int bits = 8;
@@ -474,8 +514,11 @@ __global__ __launch_bounds__(256) void split_partial_kernel(SplitDecArgs a, int 
   }
 }
 
+// `fixed` (optional): a caller-provided partial-state buffer of
+// `fixed_bytes` used instead of the context scratch (nothing is allocated).
 template <typename C, int M>
-int launch_split(Ctx *ctx, SplitDecArgs a, int rows, const float *sinks, float *out) {
+int launch_split(Ctx *ctx, SplitDecArgs a, int rows, const float *sinks, float *out, float *fixed,
+                 size_t fixed_bytes) {
   // Keys per workgroup task: about 1024 tasks over the chip (each serves two
   // heads), at most kMaxChunks chunks, whole multiples of 64 keys (every
   // wave of the task takes the same number of 16-key iterations).
@@ -489,9 +532,17 @@ int launch_split(Ctx *ctx, SplitDecArgs a, int rows, const float *sinks, float *
   a.chunks = static_cast<int>((limit + per - 1) / per);
   a.tasks = a.n_kv * a.chunks;
   const size_t slots = static_cast<size_t>(rows) * a.n_heads * a.chunks;
-  int rc = ensure_scratch(ctx, slots * 66 * sizeof(float));
-  if (rc != FOCR_OK) return rc;
-  a.part_o = static_cast<float *>(ctx->scratch);
+  const size_t need = slots * 66 * sizeof(float);
+  if (fixed) {
+    FOCR_REQUIRE(need <= fixed_bytes, FOCR_E_UNSUPPORTED,
+                 "split decode needs " + std::to_string(need) + " bytes of partial states; the no-alloc path holds " +
+                     std::to_string(fixed_bytes));
+    a.part_o = fixed;
+  } else {
+    int rc = ensure_scratch(ctx, need);
+    if (rc != FOCR_OK) return rc;
+    a.part_o = static_cast<float *>(ctx->scratch);
+  }
   a.part_md = a.part_o + slots * 64;
   hipLaunchKernelGGL((split_partial_kernel<C, M>), dim3(a.tasks), dim3(64 * kWaves), 0, ctx->stream, a, iters, rows);
   FOCR_HIP_CHECK(hipGetLastError());
@@ -509,17 +560,34 @@ int launch_split(Ctx *ctx, SplitDecArgs a, int rows, const float *sinks, float *
 }
 
 template <typename C>
-int launch_split_rows(Ctx *ctx, const SplitDecArgs &a, int rows, const float *sinks, float *out) {
+int launch_split_rows(Ctx *ctx, const SplitDecArgs &a, int rows, const float *sinks, float *out, float *fixed,
+                      size_t fixed_bytes) {
   switch (rows) {
-    case 1: return launch_split<C, 1>(ctx, a, rows, sinks, out);
-    case 2: return launch_split<C, 2>(ctx, a, rows, sinks, out);
-    case 3: return launch_split<C, 3>(ctx, a, rows, sinks, out);
-    case 4: return launch_split<C, 4>(ctx, a, rows, sinks, out);
-    case 5: return launch_split<C, 5>(ctx, a, rows, sinks, out);
-    case 6: return launch_split<C, 6>(ctx, a, rows, sinks, out);
-    case 7: return launch_split<C, 7>(ctx, a, rows, sinks, out);
-    default: return launch_split<C, 8>(ctx, a, rows, sinks, out);
+    case 1: return launch_split<C, 1>(ctx, a, rows, sinks, out, fixed, fixed_bytes);
+    case 2: return launch_split<C, 2>(ctx, a, rows, sinks, out, fixed, fixed_bytes);
+    case 3: return launch_split<C, 3>(ctx, a, rows, sinks, out, fixed, fixed_bytes);
+    case 4: return launch_split<C, 4>(ctx, a, rows, sinks, out, fixed, fixed_bytes);
+    case 5: return launch_split<C, 5>(ctx, a, rows, sinks, out, fixed, fixed_bytes);
+    case 6: return launch_split<C, 6>(ctx, a, rows, sinks, out, fixed, fixed_bytes);
+    case 7: return launch_split<C, 7>(ctx, a, rows, sinks, out, fixed, fixed_bytes);
+    default: return launch_split<C, 8>(ctx, a, rows, sinks, out, fixed, fixed_bytes);
   }
+}
+
+// The arguments of a decode over `s`, shared by both entry points.
+SplitDecArgs split_args(const KvSplit *s, const float *q) {
+  SplitDecArgs a;
+  a.records = s->records;
+  a.tail = s->tail;
+  a.q = q;
+  a.prefix_len = static_cast<int>(s->prefix_len);
+  a.tail_capacity = static_cast<int>(s->capacity - s->prefix_len);
+  a.n_heads = s->n_heads;
+  a.n_kv = s->n_kv;
+  a.record_bytes = static_cast<int>(s->record_bytes);
+  a.tail_bytes = static_cast<int>(s->tail_bytes);
+  a.last = static_cast<int>(s->prefix_len + s->tail_len);
+  return a;
 }
 
 }  // namespace
@@ -638,19 +706,26 @@ int focr_kv_attention_decode(focr_ctx *handle, const focr_kv_split *kv, const fl
   FOCR_REQUIRE(rows >= 1 && rows <= 8 && rows <= (s->tail_len > 0 ? s->tail_len : 1), FOCR_E_SHAPE,
                "split decode: 1 to 8 rows, at most the appended positions");
   FOCR_HIP_CHECK(hipSetDevice(ctx->device));
-  SplitDecArgs a;
-  a.records = s->records;
-  a.tail = s->tail;
-  a.q = q;
-  a.prefix_len = static_cast<int>(s->prefix_len);
-  a.tail_capacity = static_cast<int>(s->capacity - s->prefix_len);
-  a.n_heads = s->n_heads;
-  a.n_kv = s->n_kv;
-  a.record_bytes = static_cast<int>(s->record_bytes);
-  a.tail_bytes = static_cast<int>(s->tail_bytes);
-  a.last = static_cast<int>(s->prefix_len + s->tail_len);
+  const SplitDecArgs a = split_args(s, q);
   const int r = static_cast<int>(rows);
-  return s->bits == 8 ? launch_split_rows<int8_t>(ctx, a, r, sinks, out) : launch_split_rows<int16_t>(ctx, a, r, sinks, out);
+  return s->bits == 8 ? launch_split_rows<int8_t>(ctx, a, r, sinks, out, nullptr, 0)
+                      : launch_split_rows<int16_t>(ctx, a, r, sinks, out, nullptr, 0);
+}
+
+int focr_kv_attention_decode_noalloc(focr_ctx *handle, const focr_kv_split *kv, const float *q, size_t rows,
+                                     const float *sinks, float *out) {
+  Ctx *ctx = reinterpret_cast<Ctx *>(handle);
+  const KvSplit *s = reinterpret_cast<const KvSplit *>(kv);
+  FOCR_REQUIRE(ctx && s && q && sinks && out, FOCR_E_ARG, "focr_kv_attention_decode_noalloc: null argument");
+  FOCR_REQUIRE(rows >= 1 && rows <= 8 && rows <= (s->tail_len > 0 ? s->tail_len : 1), FOCR_E_SHAPE,
+               "split decode: 1 to 8 rows, at most the appended positions");
+  FOCR_HIP_CHECK(hipSetDevice(ctx->device));
+  float *fixed = noalloc_scratch(ctx->device);
+  FOCR_REQUIRE(fixed, FOCR_E_HIP, "the no-alloc scratch of this device was not resolved (focr_ctx_create does it)");
+  const SplitDecArgs a = split_args(s, q);
+  const int r = static_cast<int>(rows);
+  return s->bits == 8 ? launch_split_rows<int8_t>(ctx, a, r, sinks, out, fixed, kNoAllocScratchBytes)
+                      : launch_split_rows<int16_t>(ctx, a, r, sinks, out, fixed, kNoAllocScratchBytes);
 }
 
 int focr_kv_dequantize(focr_ctx *handle, const focr_kv_split *kv, float *prefix_k, float *values, float *generated_k) {

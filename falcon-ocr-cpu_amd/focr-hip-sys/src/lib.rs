@@ -265,6 +265,14 @@ extern "C" {
         sinks_dev: *const f32,
         out_dev: *mut f32,
     ) -> c_int;
+    pub fn focr_kv_attention_decode_noalloc(
+        ctx: *mut focr_ctx,
+        kv: *const focr_kv_split,
+        q_dev: *const f32,
+        rows: usize,
+        sinks_dev: *const f32,
+        out_dev: *mut f32,
+    ) -> c_int;
     pub fn focr_kv_dequantize(
         ctx: *mut focr_ctx,
         kv: *const focr_kv_split,

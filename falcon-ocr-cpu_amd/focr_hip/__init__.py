@@ -79,6 +79,7 @@ SIGNATURES = {
     "focr_kv_seal": (_I, [_P, _I, _P, _P, _Z, _Z, _Z, _Z, _Z, ctypes.POINTER(_P)]),
     "focr_kv_append": (_I, [_P, _P, _P, _P, _Z]),
     "focr_kv_attention_decode": (_I, [_P, _P, _P, _Z, _P, _P]),
+    "focr_kv_attention_decode_noalloc": (_I, [_P, _P, _P, _Z, _P, _P]),
     "focr_kv_dequantize": (_I, [_P, _P, _P, _P, _P]),
     "focr_kv_truncate_tail": (_I, [_P, _Z]),
     "focr_kv_qkv_rows": (_I, [_P, _P, _P, _Z, _P, _P]),
@@ -518,6 +519,14 @@ class KvSplit:
         if out is None:
             out = torch.empty((rows, self.n_heads, 64), dtype=torch.float32, device=q.device)
         _check(lib().focr_kv_attention_decode(self.ctx.handle, self.handle, _dev(q), rows, _dev(sinks), _dev(out)))
+        return out
+
+    def attention_decode_noalloc(self, q, rows: int, sinks, out):
+        """`attention_decode_rows` through the entry point that allocates
+        nothing (a fixed per-GPU array holds the partial states; calls that
+        overlap on one GPU race). `out` [rows][n_heads][64] is required."""
+        _check(lib().focr_kv_attention_decode_noalloc(self.ctx.handle, self.handle, _dev(q), rows, _dev(sinks),
+                                                      _dev(out)))
         return out
 
     def truncate_tail(self, tail_len: int) -> None:

@@ -284,6 +284,19 @@ int focr_kv_qkv_rows(focr_ctx *ctx, focr_kv_split *kv, const float *qkv_dev, siz
  * the context scratch for the partial states. */
 int focr_kv_attention_decode(focr_ctx *ctx, const focr_kv_split *kv, const float *q_dev, size_t rows,
                              const float *sinks_dev, float *out_dev);
+/* focr_kv_attention_decode with its partial softmax states in a fixed
+ * device array instead of the context scratch: the call allocates nothing
+ * (no hipMalloc / hipFree), for callers that cannot allocate — code under
+ * HIP graph capture and tight serving loops. No counterpart in the
+ * reference (a CPU runner allocates no device memory). The array holds
+ * 4.5 MiB per GPU for the life of the process; every valid shape of this
+ * format (n_heads = 2 n_kv_heads <= 16, rows <= 8) needs at most about
+ * 4.4 MB, and a call that would need more returns FOCR_E_UNSUPPORTED. The
+ * array is shared by every call on a GPU: calls that overlap on one GPU (two
+ * streams, two contexts) race and must be serialized by the caller. Same
+ * arguments and results (bit for bit) as focr_kv_attention_decode. */
+int focr_kv_attention_decode_noalloc(focr_ctx *ctx, const focr_kv_split *kv, const float *q_dev, size_t rows,
+                                     const float *sinks_dev, float *out_dev);
 /* The decoded cache in the compact layout (the reference's test view
  * dequantized_compact, src/quant/kv.rs:533-563, plus the tail): prefix keys
  * [prefix_len][n_heads][64], values [prefix_len + tail_len][n_kv_heads][64],

@@ -1,0 +1,81 @@
+"""focr_kv_attention_decode_noalloc, the decode attention over sealed Q8 /
+Q16 records that allocates nothing (its partial states live in a fixed
+per-GPU device array): called through the C ABI, its output equals the
+allocating entry point's bit for bit (the same kernels and order), and the
+oracle's within the FP32 tolerance, on two calls in a row, the second with
+a smaller input (fewer rows over a shorter cache), so stale partial states
+of the first call cannot leak into the second."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import gen
+import oracle
+from gpu_util import assert_bitwise, host, max_rel, to_dev
+
+pytestmark = pytest.mark.gpu
+H, G = 16, 8
+
+
+def sealed_cache(fh, bits, prefix, tail_rows, seed):
+    import torch
+
+    pk = gen.att_values(prefix * H * 64, seed, 0.75).reshape(prefix, H, 64)
+    pk[:, 1::2, :32] = pk[:, 0::2, :32]  # paired temporal halves, as the seal requires
+    v = gen.att_values(prefix * G * 64, seed + 1, 1.0).reshape(prefix, G, 64)
+    kv = fh.KvSplit.seal(bits, to_dev(pk), to_dev(v), prefix, prefix + tail_rows)
+    k_new = gen.att_values(tail_rows * G * 64, seed + 2, 0.75).reshape(tail_rows, G, 64)
+    v_new = gen.att_values(tail_rows * G * 64, seed + 3, 1.0).reshape(tail_rows, G, 64)
+    kv.append(to_dev(k_new), to_dev(v_new), tail_rows)
+    torch.cuda.synchronize()
+    return kv
+
+
+def call_noalloc(fh, kv, q, rows, sinks, out):
+    rc = fh.lib().focr_kv_attention_decode_noalloc(kv.ctx.handle, kv.handle, ctypes.c_void_p(q.data_ptr()), rows,
+                                                   ctypes.c_void_p(sinks.data_ptr()), ctypes.c_void_p(out.data_ptr()))
+    assert rc == 0, fh.lib().focr_last_error().decode()
+
+
+@pytest.mark.parametrize("bits", [8, 16])
+def test_noalloc_decode_equals_the_allocating_entry_point(bits):
+    import torch
+
+    import focr_hip as fh
+
+    sinks = to_dev(gen.uniform(H, -2.0, 2.0, 7))
+    # First call: 8 rows over 16,320 + 64 positions; second: 3 rows over 1,000 + 5.
+    for prefix, tail_rows, rows, seed in ((16320, 64, 8, 11), (1000, 5, 3, 21)):
+        kv = sealed_cache(fh, bits, prefix, tail_rows, seed)
+        q = to_dev(gen.att_values(rows * H * 64, seed + 5, 0.75).reshape(rows, H, 64))
+        out = torch.full((rows, H, 64), float("nan"), device="cuda:0")
+        call_noalloc(fh, kv, q, rows, sinks, out)
+        want = kv.attention_decode(q, rows, sinks)
+        torch.cuda.synchronize()
+        assert_bitwise(host(out), host(want), f"no-alloc vs allocating, {rows} rows over {prefix}+{tail_rows}")
+        pk, vals, gk = kv.dequantize()
+        total = prefix + tail_rows
+        ref = oracle.attention_decode(host(q), host(pk), host(gk), host(vals), rows, prefix, total, H, G,
+                                      total - rows, 0, 0, host(sinks))
+        got = host(out)
+        assert np.all(np.isfinite(got))
+        assert np.all(np.abs(got - ref) <= 1e-5 * (1.0 + np.abs(ref)))
+        assert max_rel(got, ref) <= 1e-5
+        kv.free()
+
+
+def test_noalloc_decode_rejects_bad_arguments():
+    import torch
+
+    import focr_hip as fh
+
+    kv = sealed_cache(fh, 8, 64, 2, 31)
+    q = torch.zeros((3, H, 64), device="cuda:0")
+    sinks = torch.zeros(H, device="cuda:0")
+    out = torch.zeros((3, H, 64), device="cuda:0")
+    rc = fh.lib().focr_kv_attention_decode_noalloc(kv.ctx.handle, kv.handle, ctypes.c_void_p(q.data_ptr()), 3,
+                                                   ctypes.c_void_p(sinks.data_ptr()), ctypes.c_void_p(out.data_ptr()))
+    assert rc == -2  # FOCR_E_SHAPE: more rows than appended positions
+    assert fh.lib().focr_kv_attention_decode_noalloc(kv.ctx.handle, kv.handle, None, 1, None, None) == -1
+    kv.free()

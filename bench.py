@@ -111,6 +111,12 @@ def bench_gemv(torch, fh, gen, np, bits, rows, steps, warmup, graph=True, n=4096
         def run():
             for i in range(steps):
                 step(i)
+    # The warm-up replay just touched the first K copies of the pool; write a
+    # 512 MiB buffer (twice the 256 MB Infinity Cache) so that the timed steps
+    # read their weights from HBM whatever K is.
+    flush = torch.empty(128 << 20, dtype=torch.float32, device="cuda")
+    flush.fill_(1.0)
+    del flush
     # Timed region: barrier, events on the launch stream around the K steps.
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -121,7 +127,7 @@ def bench_gemv(torch, fh, gen, np, bits, rows, steps, warmup, graph=True, n=4096
     wall = time.perf_counter() - t0
     avg_ms = ev0.elapsed_time(ev1) / steps
     return {"bytes": nbytes, "wall_s": wall, "steps": steps, "avg_launch_ms": avg_ms,
-            "pool_copies": len(pool), "codes": codes, "scales": scales, "x": x}
+            "pool_copies": len(pool), "codes": codes, "scales": scales, "x": x, "cache_flushed": True}
 
 
 def bench_gemm(torch, fh, gen, np, reps):
@@ -464,13 +470,73 @@ def bench_launch_floor(torch, steps=2000):
     return res
 
 
-def cpu_baseline(np, gen, seconds=10.0):
+def host_facts():
+    """The host CPU the baselines run on: logical CPUs, the CPUs this job may
+    use (affinity, capped by OMP_NUM_THREADS, the one-GPU job's host share),
+    the physical cores among them, model, clock and the ISA flags the
+    reference's kernels select on (avx2/fma: the AVX2 panels and tiles;
+    avx512f/vl: the 16-lane attention tiles; avx512_vnni / avx512_bf16: the
+    VNNI INT16 panels and the BF16 attention)."""
+    import oracle
+
+    facts = {"nproc": os.cpu_count()}
+    try:
+        allowed = sorted(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        allowed = list(range(os.cpu_count() or 1))
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    share = len(allowed)
+    if omp.isdigit() and int(omp) > 0:
+        share = min(share, int(omp))
+    facts["affinity"] = len(allowed)
+    facts["omp_num_threads"] = omp or None
+    facts["share"] = share
+    cores = set()
+    for cpu in allowed[:share]:
+        base = Path(f"/sys/devices/system/cpu/cpu{cpu}/topology")
+        try:
+            cores.add(((base / "physical_package_id").read_text().strip(), (base / "core_id").read_text().strip()))
+        except OSError:
+            cores.add(("?", str(cpu)))
+    facts["physical_cores_in_share"] = len(cores)
+    try:
+        count = 0
+        for part in Path("/sys/devices/system/cpu/cpu0/topology/thread_siblings_list").read_text().strip().split(","):
+            lo, _, hi = part.partition("-")
+            count += int(hi) - int(lo) + 1 if hi else 1
+        facts["threads_per_core"] = count
+    except (OSError, ValueError):
+        facts["threads_per_core"] = None
+    model, mhz = None, []
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name") and model is None:
+                model = line.split(":", 1)[1].strip()
+            elif line.startswith("cpu MHz"):
+                mhz.append(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    facts["model"] = model
+    try:
+        facts["max_mhz"] = int(Path("/sys/devices/system/cpu/cpu0/cpufreq/cpuinfo_max_freq").read_text()) // 1000
+    except (OSError, ValueError):
+        facts["max_mhz"] = None
+    facts["mean_mhz"] = round(sum(mhz) / len(mhz)) if mhz else None
+    flags = oracle.cpu_flags()
+    facts["isa"] = [f for f in ("avx2", "fma", "avx512f", "avx512vl", "avx512bw", "avx512_vnni", "avx512_bf16",
+                                "amx_tile") if f in flags]
+    facts["oracle_build"] = oracle.variant()
+    return facts
+
+
+def cpu_baseline(np, gen, facts, seconds=10.0):
     """The oracle's INT16 GEMV (reference dot_q order) on the host cores, on the
     headline matrix. Like the GPU side, calls rotate through a pool of copies
     (1 GiB, above any host last-level cache) so weights stream from DRAM."""
     import oracle
 
-    threads = min(os.cpu_count() or 1, 16)
+    # The reference's decode team: one thread per physical core (docs/PERFORMANCE.md:48).
+    threads = max(1, facts["physical_cores_in_share"])
     oracle.set_threads(threads)
     n, k = 4096, 1024
     codes = gen.codes_uniform((n, k), -32768, 32767, np.int16, 1)
@@ -492,10 +558,12 @@ def cpu_baseline(np, gen, seconds=10.0):
     oracle.set_threads(1)
     return {"value": round(gemv_bytes(n, k, 1, 2) / med / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"INT16 g64 GEMV W[4096x1024] M=1 over a {len(pool)}-copy pool (1 GiB), median of {len(times)} "
-                      f"calls in ~{seconds:.0f} s (oracle/focr_oracle.c, OpenMP {threads} threads)"}
+                      f"calls in ~{seconds:.0f} s (oracle/focr_oracle.c, OpenMP, one thread per physical core of the "
+                      f"job's {facts['share']}-CPU host share; host {facts['nproc']} logical CPUs, {facts['model']})",
+            "host": facts}
 
 
-def cpu_prefill_page(np, gen, gpu_gemm, gpu_attention, reps=2):
+def cpu_prefill_page(np, gen, gpu_gemm, gpu_attention, facts, reps=2):
     """The FP32 prefill of one 6,544-token page on the host cores against the
     GPU's: the literal projection X[6544x1024] x W[1024x4096] and the four
     checkpoint projections, each plus the config-4 attention (16 heads, image
@@ -504,7 +572,9 @@ def cpu_prefill_page(np, gen, gpu_gemm, gpu_attention, reps=2):
     oracle's results), over the whole page; best of `reps` calls each."""
     import oracle
 
-    threads = min(os.cpu_count() or 1, 16)
+    # The reference's prefill pool: every logical CPU it may use (threads = 0,
+    # src/config.rs:391-395) -- here the job's host share.
+    threads = max(1, facts["share"])
     oracle.set_threads(threads)
     m = 6544
 
@@ -529,20 +599,40 @@ def cpu_prefill_page(np, gen, gpu_gemm, gpu_attention, reps=2):
     v, sinks = gen.normal(L * 8 * 64, 1.0, 22), gen.uniform(16, -2.0, 2.0, 23)
     cpu["attention"] = best(lambda: oracle.attention_prefill_fast(q, k, v, L, L, L, 16, 8, 0, 0, img, sinks))
     log(f"cpu attention: {cpu['attention']:.1f} ms")
+    # Thread scaling of the literal GEMM and the attention (half the share).
+    half = max(1, threads // 2)
+    oracle.set_threads(half)
+    a = gen.normal((m, 1024), 1.0, 10)
+    w = gen.normal((4096, 1024), 0.02, 11)
+    half_ms = {"literal": round(best(lambda: oracle.panel_gemm_fast(a, m, 1024, w, 4096)), 2),
+               "attention": round(best(lambda: oracle.attention_prefill_fast(q, k, v, L, L, L, 16, 8, 0, 0, img,
+                                                                            sinks)), 2)}
     oracle.set_threads(1)
+    # MACs per cycle per core of the FP32 panels (the reference's 7700X: about
+    # 14.3 of a 16-MAC ceiling, docs/PERFORMANCE.md:544-558), at the clock the
+    # host reports (its maximum if known, else the mean current clock).
+    ghz = (facts.get("max_mhz") or facts.get("mean_mhz") or 0) / 1000.0
+    cores = max(1, facts["physical_cores_in_share"])
+    macs_cycle_core = None
+    if ghz:
+        macs_cycle_core = round(m * 1024 * 4096 / (cpu["literal"] * 1e-3) / (cores * ghz * 1e9), 2)
     layer = ("qkv", "wo", "w13", "w2")
     gpu_literal = gpu_gemm["literal_mfma"]["ms"] + gpu_attention["online_fast"]["ms"]
     gpu_layer = sum(gpu_gemm[f"{s}_mfma"]["ms"] for s in layer) + gpu_attention["online_fast"]["ms"]
     cpu_literal = cpu["literal"] + cpu["attention"]
     cpu_layer = sum(cpu[s] for s in layer) + cpu["attention"]
-    return {"cores": threads, "kind": "port",
+    return {"cores": threads, "kind": "port", "physical_cores": cores, "ghz_assumed": ghz or None,
+            "gemm_macs_per_cycle_per_core": macs_cycle_core, "reference_macs_per_cycle_per_core": 14.3,
             "cpu_ms": {s: round(t, 2) for s, t in cpu.items()},
+            "cpu_ms_half_threads": {"threads": half, **half_ms},
             "literal_page": {"gpu_ms": round(gpu_literal, 4), "cpu_ms": round(cpu_literal, 1),
                              "speedup": round(cpu_literal / gpu_literal, 1)},
             "layer_page": {"gpu_ms": round(gpu_layer, 4), "cpu_ms": round(cpu_layer, 1),
                            "speedup": round(cpu_layer / gpu_layer, 1)},
-            "sample": f"whole page, best of {reps} calls, OpenMP {threads} threads "
-                      "(oracle/focr_cpu_panels.c, oracle/focr_cpu_attention.c; online softmax, Fast exp)"}
+            "sample": f"whole page, best of {reps} calls, OpenMP {threads} threads = the job's host share of "
+                      f"{facts['nproc']} logical CPUs ({facts['model']}); oracle/focr_cpu_panels.c (AVX2 6x16 panels), "
+                      f"oracle/focr_cpu_attention.c ({'16' if facts['oracle_build'] == 'v4' else '8'}-lane tiles, "
+                      "online softmax, Fast exp)"}
 
 
 def measured_traffic():
@@ -628,10 +718,13 @@ def main():
         per_op["copy_256MiB"] = bench_copy(torch, 10)
         per_op["launch_floor"] = bench_launch_floor(torch)
         log(f"launch floor: {per_op['launch_floor']}")
+    facts = host_facts()
+    log(f"host: {facts}")
     if not args.no_cpu and "prefill_f32" in per_op and "attention_prefill" in per_op:
-        per_op["prefill_page_vs_cpu"] = cpu_prefill_page(np, gen, per_op["prefill_f32"], per_op["attention_prefill"])
+        per_op["prefill_page_vs_cpu"] = cpu_prefill_page(np, gen, per_op["prefill_f32"], per_op["attention_prefill"],
+                                                         facts)
         log(f"prefill page vs CPU: {per_op['prefill_page_vs_cpu']}")
-    cpu = None if args.no_cpu else cpu_baseline(np, gen)
+    cpu = None if args.no_cpu else cpu_baseline(np, gen, facts)
     line = {
         "metric": "decode GEMV HBM GB/s (INT16 group-64, W 4096x1024, M=1)",
         "value": round(value, 1),
@@ -646,7 +739,8 @@ def main():
         "dtype": "i16xf32",
         "data": "synthetic (seeded PCG64: codes uniform [-32768,32767], scales U(1e-6,4e-6), x ~ N(0,1))",
         "config": {"workload": "BASELINE configs[1]: near-exact INT16 g64 decode GEMV, W[4096x1024], M=1",
-                   "pool_copies": head["pool_copies"], "graph_replay": not args.no_graph},
+                   "pool_copies": head["pool_copies"], "graph_replay": not args.no_graph,
+                   "infinity_cache_flushed_before_timing": head["cache_flushed"]},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic()},
         "cpu_baseline": cpu,

@@ -8,7 +8,10 @@
  * the compiler vectorizes across the 32 query lanes as the reference's SIMD
  * lanes do: QK two keys at a time, the softmax and exp_poly branch-free over
  * the lanes. Bit for bit orc_attention_prefill in the Fast exp mode and the
- * static softmax (tests/test_cpu_baseline.py checks it); tiles off the
+ * static softmax (tests/test_cpu_baseline.py checks it). Built for AVX-512
+ * (the x86-64-v4 variant) the lanes are 16 wide, as the reference's "wide"
+ * tiles on AVX-512 hosts (src/kernels/mod.rs:44-46, prefill64.rs:721-882);
+ * the per-lane operations do not change. Tiles off the
  * reference's main path (q*k <= 256, k < 3 or q < 2) run the oracle's
  * scalar code.
  */
@@ -16,7 +19,7 @@
 
 #include <math.h>
 #include <string.h>
-#if defined(__AVX2__) && defined(__FMA__)
+#if defined(__AVX2__) && defined(__FMA__) || defined(__AVX512F__)
 #include <immintrin.h>
 #endif
 
@@ -103,6 +106,38 @@ static inline __m256 exp_fast8(__m256 x) {
 }
 #endif
 
+#if defined(__AVX512F__)
+/* exp_un and exp_fast on sixteen lanes (the reference's 16-lane "wide"
+ * tiles on AVX-512 hosts, prefill64.rs:721-882, bitwise the 8-lane ones):
+ * the same operations in the same order. */
+static inline __m512 exp_un16(__m512 x) {
+    const __m512 n = _mm512_roundscale_ps(_mm512_mul_ps(x, _mm512_set1_ps(1.44269504088896340735992468100189214f)),
+                                          _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC);
+    __m512 r = _mm512_fmadd_ps(n, _mm512_set1_ps(-0.6933594f), x);
+    r = _mm512_fmadd_ps(n, _mm512_set1_ps(2.1219444e-4f), r);
+    __m512 p = _mm512_set1_ps(1.9875691e-4f);
+    p = _mm512_fmadd_ps(p, r, _mm512_set1_ps(1.3981999e-3f));
+    p = _mm512_fmadd_ps(p, r, _mm512_set1_ps(8.333452e-3f));
+    p = _mm512_fmadd_ps(p, r, _mm512_set1_ps(4.1665796e-2f));
+    p = _mm512_fmadd_ps(p, r, _mm512_set1_ps(0.16666665f));
+    p = _mm512_fmadd_ps(p, r, _mm512_set1_ps(0.5f));
+    const __m512 y = _mm512_add_ps(_mm512_fmadd_ps(p, _mm512_mul_ps(r, r), r), _mm512_set1_ps(1.0f));
+    const __m512i e = _mm512_slli_epi32(_mm512_add_epi32(_mm512_cvtps_epi32(n), _mm512_set1_epi32(127)), 23);
+    return _mm512_mul_ps(y, _mm512_castsi512_ps(e));
+}
+
+static inline __m512 exp_fast16(__m512 x) {
+    const __m512 lo = _mm512_set1_ps(-87.0f), hi = _mm512_set1_ps(88.376f);
+    const __mmask16 below = _mm512_cmp_ps_mask(x, lo, _CMP_LT_OQ), above = _mm512_cmp_ps_mask(x, hi, _CMP_GT_OQ);
+    __m512 xc = _mm512_mask_blend_ps(below, x, lo);
+    xc = _mm512_mask_blend_ps(above, xc, hi);
+    __m512 y = exp_un16(xc);
+    y = _mm512_mask_blend_ps(below, y, _mm512_setzero_ps());
+    y = _mm512_mask_blend_ps(above, y, _mm512_set1_ps(INFINITY));
+    return _mm512_mask_blend_ps(_mm512_cmp_ps_mask(x, x, _CMP_UNORD_Q), y, x);
+}
+#endif
+
 static void tile_fast(const float *q, const FCache *cache, size_t query_offset, size_t image_start, size_t image_end,
                       size_t tile, size_t queries, size_t head, const float *sinks, int is_static, float *output) {
     const size_t qw = cache->n_heads * HD;
@@ -140,7 +175,27 @@ static void tile_fast(const float *q, const FCache *cache, size_t query_offset, 
             /* QK: each (key, query) is one FMA chain over d from +0; two keys
              * per pass so the chains of 64 lanes interleave. */
             size_t j = 0;
-#if defined(__AVX2__) && defined(__FMA__)
+#if defined(__AVX512F__)
+            /* The 32 lanes of two keys in four registers. */
+            const __m512 wscale = _mm512_set1_ps(scale);
+            for (; j + 2 <= keys; j += 2) {
+                __m512 a0[2], a1[2];
+                for (int v = 0; v < 2; v++) a0[v] = a1[v] = _mm512_setzero_ps();
+                const float *k0 = krow[j], *k1 = krow[j + 1];
+                for (int d = 0; d < HD; d++) {
+                    const __m512 x0 = _mm512_set1_ps(k0[d]), x1 = _mm512_set1_ps(k1[d]);
+                    for (int v = 0; v < 2; v++) {
+                        const __m512 qd = _mm512_loadu_ps(&qt[d][16 * v]);
+                        a0[v] = _mm512_fmadd_ps(qd, x0, a0[v]);
+                        a1[v] = _mm512_fmadd_ps(qd, x1, a1[v]);
+                    }
+                }
+                for (int v = 0; v < 2; v++) {
+                    _mm512_storeu_ps(&st[j][16 * v], _mm512_mul_ps(wscale, a0[v]));
+                    _mm512_storeu_ps(&st[j + 1][16 * v], _mm512_mul_ps(wscale, a1[v]));
+                }
+            }
+#elif defined(__AVX2__) && defined(__FMA__)
             /* The 32 lanes of two keys in eight registers. */
             const __m256 vscale = _mm256_set1_ps(scale);
             for (; j + 2 <= keys; j += 2) {
@@ -175,7 +230,17 @@ static void tile_fast(const float *q, const FCache *cache, size_t query_offset, 
                         if (fmasked(first_absolute + r, key_start + jj, image_start, image_end)) st[jj][r] = -INFINITY;
             if (is_static) {
                 size_t jj = 0;
-#if defined(__AVX2__) && defined(__FMA__)
+#if defined(__AVX512F__)
+                const __m512 ninf = _mm512_set1_ps(-INFINITY);
+                for (; jj < keys; jj++)
+                    for (int v = 0; v < 2; v++) {
+                        const __m512 score = _mm512_loadu_ps(&st[jj][16 * v]);
+                        __m512 p = exp_un16(score);
+                        if (!all_image) p = _mm512_mask_blend_ps(_mm512_cmp_ps_mask(score, ninf, _CMP_EQ_OQ), p, _mm512_setzero_ps());
+                        _mm512_storeu_ps(&den[16 * v], _mm512_add_ps(_mm512_loadu_ps(&den[16 * v]), p));
+                        _mm512_storeu_ps(&st[jj][16 * v], p);
+                    }
+#elif defined(__AVX2__) && defined(__FMA__)
                 const __m256 ninf = _mm256_set1_ps(-INFINITY);
                 for (; jj < keys; jj++)
                     for (int v = 0; v < 4; v++) {
@@ -215,7 +280,16 @@ static void tile_fast(const float *q, const FCache *cache, size_t query_offset, 
                     if (skip[r] == 0.0f && resc[r] != 1.0f)
                         for (int d = 0; d < HD; d++) out[r][d] *= resc[r];
                 size_t jj = 0;
-#if defined(__AVX2__) && defined(__FMA__)
+#if defined(__AVX512F__)
+                for (; jj < keys; jj++)
+                    for (int v = 0; v < 2; v++) {
+                        __m512 p = exp_fast16(_mm512_sub_ps(_mm512_loadu_ps(&st[jj][16 * v]), _mm512_loadu_ps(&newm[16 * v])));
+                        p = _mm512_mask_blend_ps(_mm512_cmp_ps_mask(_mm512_loadu_ps(&skip[16 * v]), _mm512_setzero_ps(), _CMP_NEQ_OQ),
+                                                 p, _mm512_setzero_ps());
+                        _mm512_storeu_ps(&den[16 * v], _mm512_add_ps(_mm512_loadu_ps(&den[16 * v]), p));
+                        _mm512_storeu_ps(&st[jj][16 * v], p);
+                    }
+#elif defined(__AVX2__) && defined(__FMA__)
                 for (; jj < keys; jj++)
                     for (int v = 0; v < 4; v++) {
                         __m256 p = exp_fast8(_mm256_sub_ps(_mm256_loadu_ps(&st[jj][8 * v]), _mm256_loadu_ps(&newm[8 * v])));
@@ -235,7 +309,27 @@ static void tile_fast(const float *q, const FCache *cache, size_t query_offset, 
             }
             /* PV: chains over keys from +0 per (query, dim), then + out. */
             size_t r = 0;
-#if defined(__AVX2__) && defined(__FMA__)
+#if defined(__AVX512F__)
+            /* Two query rows x 64 dims per pass: eight accumulators. */
+            for (; r + 2 <= queries; r += 2) {
+                __m512 a0[4], a1[4];
+                for (int v = 0; v < 4; v++) a0[v] = a1[v] = _mm512_setzero_ps();
+                for (size_t jj = 0; jj < keys; jj++) {
+                    const __m512 p0 = _mm512_set1_ps(st[jj][r]), p1 = _mm512_set1_ps(st[jj][r + 1]);
+                    const float *vr = vrow[jj];
+                    for (int v = 0; v < 4; v++) {
+                        const __m512 x = _mm512_loadu_ps(vr + 16 * v);
+                        a0[v] = _mm512_fmadd_ps(x, p0, a0[v]);
+                        a1[v] = _mm512_fmadd_ps(x, p1, a1[v]);
+                    }
+                }
+                for (int v = 0; v < 4; v++) {
+                    float *o0 = &out[r][16 * v], *o1 = &out[r + 1][16 * v];
+                    _mm512_storeu_ps(o0, _mm512_add_ps(a0[v], _mm512_loadu_ps(o0)));
+                    _mm512_storeu_ps(o1, _mm512_add_ps(a1[v], _mm512_loadu_ps(o1)));
+                }
+            }
+#elif defined(__AVX2__) && defined(__FMA__)
             /* Two query rows x 32 dims per pass: eight accumulators. */
             for (; r + 2 <= queries; r += 2)
                 for (int h = 0; h < 2; h++) {

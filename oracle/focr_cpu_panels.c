@@ -2,7 +2,8 @@
  * The CPU baseline of the FP32 prefill projections — TEST INFRASTRUCTURE ONLY
  * (bench.py's cpu_baseline leg and tests/). A performance restatement of the
  * reference's AVX2 FP32 panel GEMM: panel::gemm / kernel_generic with MR = 6
- * rows x NR = 16 columns in twelve 8-lane FMA accumulators
+ * rows x NR = 16 columns in twelve 8-lane FMA accumulators, rows packed
+ * [group of 6][k][6] and weights [panel][k][16]
  * (src/kernels/panels/panel.rs:57-172), row blocks of 96 rows split across
  * threads with panel groups (src/kernels/panels/driver.rs:57-140). Every
  * output is one FMA chain over ascending k from +0.0, so the result is bit
@@ -44,33 +45,24 @@ static inline void emit_panel(int epilogue, float *out, size_t n, size_t row, si
 }
 
 #if defined(__AVX2__) && defined(__FMA__)
-/* rows (<= 6) rows of A' times one packed panel [k][16]. */
-static void micro(const float *ar, size_t lda, int rows, const float *bp, size_t k, float c[MR][NRP]) {
+/* One 6-row group of A' packed [k][6] (rows past the block zero) times one
+ * packed panel [k][16]: kernel_avx2's twelve accumulators. */
+static void micro(const float *ap, const float *bp, size_t k, float c[MR][NRP]) {
     __m256 acc[MR][2];
     for (int r = 0; r < MR; r++) acc[r][0] = acc[r][1] = _mm256_setzero_ps();
-    if (rows == MR) {
-        for (size_t kk = 0; kk < k; kk++) {
-            const __m256 b0 = _mm256_loadu_ps(bp + kk * NRP), b1 = _mm256_loadu_ps(bp + kk * NRP + 8);
-#define ROW(r)                                                      \
-    {                                                               \
-        const __m256 a = _mm256_broadcast_ss(ar + (r) * lda + kk);  \
-        acc[r][0] = _mm256_fmadd_ps(a, b0, acc[r][0]);              \
-        acc[r][1] = _mm256_fmadd_ps(a, b1, acc[r][1]);              \
+    for (size_t kk = 0; kk < k; kk++) {
+        const __m256 b0 = _mm256_loadu_ps(bp + kk * NRP), b1 = _mm256_loadu_ps(bp + kk * NRP + 8);
+        const float *a = ap + kk * MR;
+#define ROW(r)                                             \
+    {                                                      \
+        const __m256 x = _mm256_broadcast_ss(a + (r));     \
+        acc[r][0] = _mm256_fmadd_ps(x, b0, acc[r][0]);     \
+        acc[r][1] = _mm256_fmadd_ps(x, b1, acc[r][1]);     \
     }
-            ROW(0) ROW(1) ROW(2) ROW(3) ROW(4) ROW(5)
+        ROW(0) ROW(1) ROW(2) ROW(3) ROW(4) ROW(5)
 #undef ROW
-        }
-    } else {
-        for (size_t kk = 0; kk < k; kk++) {
-            const __m256 b0 = _mm256_loadu_ps(bp + kk * NRP), b1 = _mm256_loadu_ps(bp + kk * NRP + 8);
-            for (int r = 0; r < rows; r++) {
-                const __m256 a = _mm256_broadcast_ss(ar + r * lda + kk);
-                acc[r][0] = _mm256_fmadd_ps(a, b0, acc[r][0]);
-                acc[r][1] = _mm256_fmadd_ps(a, b1, acc[r][1]);
-            }
-        }
     }
-    for (int r = 0; r < rows; r++) {
+    for (int r = 0; r < MR; r++) {
         _mm256_storeu_ps(c[r], acc[r][0]);
         _mm256_storeu_ps(c[r] + 8, acc[r][1]);
     }
@@ -100,6 +92,7 @@ void orc_panel_gemm_fast(const float *a, size_t m, size_t k, const float *w, siz
     const size_t per_split = (panels + splits - 1) / splits;
 #pragma omp parallel
     {
+        /* The row block as F32Panels::pack_rows leaves it: [group][k][6]. */
         float *ar = (float *)malloc(ROW_BLOCK * (k ? k : 1) * sizeof(float));
         float c[MR][NRP];
 #pragma omp for schedule(dynamic, 1)
@@ -108,16 +101,26 @@ void orc_panel_gemm_fast(const float *a, size_t m, size_t k, const float *w, siz
             const size_t p0 = sp * per_split, p1 = p0 + per_split < panels ? p0 + per_split : panels;
             const size_t r_begin = blk * ROW_BLOCK;
             const size_t r_end = r_begin + ROW_BLOCK < m ? r_begin + ROW_BLOCK : m;
-            /* pack_rows for the block: A'[r][k] = a * row_scale[r] (panel.rs:79-106). */
-            for (size_t r = r_begin; r < r_end; r++)
-                for (size_t kk = 0; kk < k; kk++)
-                    ar[(r - r_begin) * k + kk] = row_scale ? a[r * k + kk] * row_scale[r] : a[r * k + kk];
+            /* pack_rows for the block: A'[r][k] = a * row_scale[r], k-major in
+             * groups of 6 rows, the last group zero-padded (panel.rs:77-104). */
+            const size_t groups = (r_end - r_begin + MR - 1) / MR;
+            for (size_t g = 0; g < groups; g++)
+                for (int r = 0; r < MR; r++) {
+                    const size_t row = r_begin + g * MR + (size_t)r;
+                    float *dst = ar + g * k * MR + (size_t)r;
+                    if (row < r_end)
+                        for (size_t kk = 0; kk < k; kk++)
+                            dst[kk * MR] = row_scale ? a[row * k + kk] * row_scale[row] : a[row * k + kk];
+                    else
+                        for (size_t kk = 0; kk < k; kk++) dst[kk * MR] = 0.0f;
+                }
             /* Each panel stays in cache while every 6-row group of the block uses it. */
             for (size_t p = p0; p < p1; p++) {
                 const size_t cols = n - p * NRP < NRP ? n - p * NRP : NRP;
-                for (size_t r0 = r_begin; r0 < r_end; r0 += MR) {
+                for (size_t g = 0; g < groups; g++) {
+                    const size_t r0 = r_begin + g * MR;
                     const int rows = r_end - r0 < MR ? (int)(r_end - r0) : MR;
-                    micro(ar + (r0 - r_begin) * k, k, rows, wp + p * k * NRP, k, c);
+                    micro(ar + g * k * MR, wp + p * k * NRP, k, c);
                     for (int r = 0; r < rows; r++) emit_panel(epilogue, out, n, r0 + r, p * NRP, c[r], cols);
                 }
             }

@@ -19,12 +19,25 @@ _BUILD = _HERE / "_build"
 STORE, GLU, ADD = 0, 1, 2
 
 
-def _cpu_has_v3() -> bool:
+def cpu_flags() -> set:
     try:
-        flags = Path("/proc/cpuinfo").read_text().split("flags", 2)[1].split("\n", 1)[0].split()
+        return set(Path("/proc/cpuinfo").read_text().split("flags", 2)[1].split("\n", 1)[0].split(":", 1)[1].split())
     except (OSError, IndexError):
-        return False
-    return all(f in flags for f in ("avx2", "fma", "bmi2", "movbe"))
+        return set()
+
+
+V3_FLAGS = ("avx2", "fma", "bmi2", "movbe")
+V4_FLAGS = V3_FLAGS + ("avx512f", "avx512bw", "avx512cd", "avx512dq", "avx512vl")
+
+
+def variant() -> str:
+    """The widest oracle build the host CPU runs: v4 (AVX-512), v3 (AVX2) or generic."""
+    flags = cpu_flags()
+    if all(f in flags for f in V4_FLAGS):
+        return "v4"
+    if all(f in flags for f in V3_FLAGS):
+        return "v3"
+    return "generic"
 
 
 def build() -> None:
@@ -35,7 +48,7 @@ def build() -> None:
 
 
 def _load() -> ctypes.CDLL:
-    name = "liboracle_v3.so" if _cpu_has_v3() else "liboracle_generic.so"
+    name = f"liboracle_{variant()}.so"
     path = _BUILD / name
     if not path.exists():
         build()

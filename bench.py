@@ -80,6 +80,10 @@ def make_pool(fh, gen, np, bits, n, k, count_bytes, seed):
 
 def bench_gemv(torch, fh, gen, np, bits, rows, steps, warmup, graph=True, n=4096, k=1024):
     """Decode GEMV over a rotating pool; returns whole-job and per-launch numbers."""
+    # A 512 MiB buffer (twice the 256 MB Infinity Cache), written before the
+    # pool's uploads push its lines out of the cache, read before the timed
+    # replay (below).
+    flush = torch.ones(128 << 20, dtype=torch.float32, device="cuda")
     codes, scales, pool = make_pool(fh, gen, np, bits, n, k, POOL_BYTES, 1 if bits == 16 else 4)
     x = torch.from_numpy(gen.normal((rows, k), 1.0, 3)).cuda()
     out = torch.empty((rows, n), device="cuda")
@@ -111,11 +115,13 @@ def bench_gemv(torch, fh, gen, np, bits, rows, steps, warmup, graph=True, n=4096
         def run():
             for i in range(steps):
                 step(i)
-    # The warm-up replay just touched the first K copies of the pool; write a
-    # 512 MiB buffer (twice the 256 MB Infinity Cache) so that the timed steps
-    # read their weights from HBM whatever K is.
-    flush = torch.empty(128 << 20, dtype=torch.float32, device="cuda")
-    flush.fill_(1.0)
+    # The warm-up replay just touched the first K copies of the pool; reading
+    # the flush buffer evicts them, so that the timed steps read their weights
+    # from HBM whatever K is. A read, not a write: a decode step's other
+    # matrices and caches pass through the cache as reads, and a freshly
+    # written buffer would leave dirty lines whose write-back the timed reads
+    # would pay for.
+    float(flush.sum())
     del flush
     # Timed region: barrier, events on the launch stream around the K steps.
     torch.cuda.synchronize()

@@ -19,8 +19,9 @@
 // for bit.
 //
 // Each group's A and B tiles, activation steps, column sums and scales are
-// copied HBM -> LDS by the LDS-DMA path into one of two buffers while the
-// previous group is computed from the other.
+// copied HBM -> LDS by the LDS-DMA path into one of two stages while the
+// previous group is computed from the other; tiles are ordered per XCD so
+// that the workgroups sharing an L2 share operands.
 //
 // Roofline: the i8 matrix cores do 2 x 64 MACs per output and group; the
 // FP32 group epilogue (4 VALU ops per output and group) bounds it in practice.
@@ -31,8 +32,8 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-constexpr int kBM = 128;  // rows per workgroup tile
-constexpr int kBN = 128;  // columns per workgroup tile
+constexpr int kBM = 128;  // rows padded to a multiple of this (the largest tile)
+constexpr int kBN = 64;   // columns per workgroup tile
 
 // One wave per (16-row block, group): lane l owns row l%16, inputs
 // 16*(l/16) .. +16 of the group; the group's absmax is a 4-lane reduction.
@@ -149,118 +150,162 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float *__restrict__
   if (lane < 16) steps[static_cast<size_t>(g) * m_pad + row] = step * scale;
 }
 
-// One group's operands in LDS, filled by the LDS-DMA path (25.5 KB; two
-// buffers).
+// One group's operands of a BM x 64 tile in LDS, filled by the LDS-DMA path;
+// two stages (the group being computed and the next one).
+template <int BM>
 struct GroupTile {
-  uint4 a[kBM / 16 * 2 * 64];  // [8 row blocks][hi, lo][64 lanes] x 16 B
-  uint4 b[kBN / 16 * 64];      // [8 column blocks][64 lanes] x 16 B
-  float steps[kBM];            // activation steps of the tile's rows
-  int32_t wsum[kBN];           // 128 * sum of the group's codes per column
-  float sw[kBN];               // weight scales per column
+  uint4 a[BM / 16 * 2 * 64];  // [row blocks][hi, lo][64 lanes] x 16 B
+  uint4 b[kBN / 16 * 64];     // [4 column blocks][64 lanes] x 16 B
+  float steps[BM];            // activation steps of the tile's rows
+  int32_t wsum[kBN];          // 128 * sum of the group's codes per column
+  float sw[kBN];              // weight scales per column
 };
 
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(1))) const void global_void;
 
-// NB: 16-column blocks per wave (4: 128-column workgroup tiles; 2: 64-column
-// tiles, the ones launched).
-template <int EPI, int NB>
+// Compiler-only ordering around the plain workgroup barrier: the waits are
+// explicit (a __syncthreads fence would wait for every copy in flight).
+__device__ __forceinline__ void plain_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Tile order. Workgroups are dealt to the 8 XCDs round robin (block b runs on
+// XCD b % 8); block b takes tile t = (b % 8) * per + b / 8 so that each XCD
+// walks one contiguous run of tiles, and tiles run in panels of kPanel row
+// tiles, column tiles in order, rows fastest: the workgroups an XCD holds at
+// once share a few A row tiles and B column tiles in its own L2.
+constexpr int kPanel = 4;
+__device__ __forceinline__ void tile_of(int b, int row_tiles, int col_tiles, int &rt, int &ct) {
+  const int total = row_tiles * col_tiles;
+  const int per = total / 8;
+  const int t = b < 8 * per ? (b % 8) * per + b / 8 : b;
+  const int panel = t / (kPanel * col_tiles);
+  const int rem = t - panel * kPanel * col_tiles;
+  const int rows = row_tiles - panel * kPanel < kPanel ? row_tiles - panel * kPanel : kPanel;
+  ct = rem / rows;
+  rt = panel * kPanel + rem % rows;
+}
+
+// BM x 64 outputs per workgroup; wave (wm, wn) holds BM / 2 rows x 32
+// columns, RW = BM / 32 row blocks x 2 column blocks of 16 x 16.
+//
+// Step g: wait for this wave's copies of group g, meet the other waves
+// (nobody still reads the other stage), start group g + 1's copies into it,
+// then compute group g: per block two i8 matrix-core products and the FP32
+// epilogue acc = fma(f32(S), fl(s_w * s_a), acc).
+template <int EPI, int BM>
 __global__ __launch_bounds__(256) void gemm_kernel(const int8_t *__restrict__ a_tiles, const float *__restrict__ steps,
                                                    const float *__restrict__ exc_inputs, const int8_t *__restrict__ b_tiles,
                                                    const int32_t *__restrict__ wsum, const float *__restrict__ sw,
                                                    const float *__restrict__ exc_vals, int n_exc, int m, int n,
-                                                   int groups, int row_blocks, int m_pad, float *__restrict__ out) {
-  __shared__ GroupTile buf0;
-  __shared__ GroupTile buf1;
+                                                   int groups, int row_blocks, int m_pad, int row_tiles, int col_tiles,
+                                                   float *__restrict__ out) {
+  constexpr int RB = BM / 16, RW = RB / 2;
+  typedef GroupTile<BM> Tile;
+  // Two distinct LDS objects (not one array): the compiler then sees that
+  // reads of one stage do not alias copies into the other.
+  __shared__ Tile ring0, ring1;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
-  const int mb0 = blockIdx.x * (kBM / 16);
-  const int nb0 = blockIdx.y * (2 * NB);
+  int rt, ct;
+  tile_of(blockIdx.x, row_tiles, col_tiles, rt, ct);
+  const int mb0 = rt * RB;
+  const int nb0 = ct * (kBN / 16);
   const int col_blocks = n / 16;
 
-  // Group g -> t by DMA (16 B per lane; sources clamped into their arrays,
-  // columns past n are computed and discarded): A 4 and B 2 instructions per
-  // thread; the steps, column sums and scales by lanes 0-31 of waves 0-2.
-  auto copy_group = [&](GroupTile &t, int g) {
-    const char *ga = reinterpret_cast<const char *>(a_tiles) + (static_cast<size_t>(g) * row_blocks + mb0) * 2048;
+  // Sources of this thread's copies per group (advanced by a group's
+  // stride): A RB / 2 x 16 B, B 16 B (column blocks past n repeat the last
+  // one: computed and discarded), and 4 B of the steps (waves 0 and 2, 64
+  // rows each), of the column sums (wave 1) or of the scales (wave 3).
+  const char *asrc = reinterpret_cast<const char *>(a_tiles) + static_cast<size_t>(mb0) * 2048 + 16 * tid;
+  const size_t a_stride = static_cast<size_t>(row_blocks) * 2048;
+  int blk = nb0 + (tid >> 6);
+  blk = blk < col_blocks ? blk : col_blocks - 1;
+  const char *bsrc = reinterpret_cast<const char *>(b_tiles) + (static_cast<size_t>(blk) * 64 + lane) * 16;
+  const size_t b_stride = static_cast<size_t>(col_blocks) * 1024;
+  const bool x_copy = (wave & 1) != 0 || 64 * (wave >> 1) < BM;
+  const char *xsrc;
+  size_t x_stride;
+  int x_dst;  // byte offset of the wave's 256 B in the stage
+  if ((wave & 1) == 0) {
+    xsrc = reinterpret_cast<const char *>(steps + mb0 * 16 + 64 * (wave >> 1) + lane);
+    x_stride = static_cast<size_t>(m_pad) * sizeof(float);
+    x_dst = static_cast<int>(offsetof(Tile, steps)) + 256 * (wave >> 1);
+  } else {
+    int col = nb0 * 16 + lane;
+    col = col < n ? col : n - 1;
+    const bool scales = (wave >> 1) != 0;
+    xsrc = scales ? reinterpret_cast<const char *>(sw + col) : reinterpret_cast<const char *>(wsum + col);
+    x_stride = static_cast<size_t>(n) * 4;
+    x_dst = scales ? static_cast<int>(offsetof(Tile, sw)) : static_cast<int>(offsetof(Tile, wsum));
+  }
+  auto issue = [&](Tile &t, int g) {
+    const char *ga = asrc + static_cast<size_t>(g) * a_stride;
 #pragma unroll
-    for (int i = 0; i < 4; i++)
-      __builtin_amdgcn_global_load_lds((global_void *)(ga + 16 * (tid + 256 * i)), (lds_void *)(&t.a[64 * wave + 256 * i]),
-                                       16, 0, 0);
-#pragma unroll
-    for (int i = 0; i < NB / 2; i++) {
-      const int idx = tid + 256 * i;
-      int blk = nb0 + idx / 64;
-      blk = blk < col_blocks ? blk : col_blocks - 1;
-      const char *gb = reinterpret_cast<const char *>(b_tiles) + ((static_cast<size_t>(g) * col_blocks + blk) * 64 + (idx & 63)) * 16;
-      __builtin_amdgcn_global_load_lds((global_void *)gb, (lds_void *)(&t.b[64 * wave + 256 * i]), 16, 0, 0);
-    }
-    if (lane < 32) {
-      if (wave == 0) {
-        __builtin_amdgcn_global_load_lds((global_void *)(steps + static_cast<size_t>(g) * m_pad + mb0 * 16 + 4 * lane),
-                                         (lds_void *)(&t.steps[0]), 16, 0, 0);
-      } else if (wave < 3) {
-        int col = nb0 * 16 + 4 * lane;
-        col = col < n ? col : n - 4;
-        const void *src = wave == 1 ? static_cast<const void *>(wsum + static_cast<size_t>(g) * n + col)
-                                    : static_cast<const void *>(sw + static_cast<size_t>(g) * n + col);
-        __builtin_amdgcn_global_load_lds((global_void *)src, wave == 1 ? (lds_void *)(&t.wsum[0]) : (lds_void *)(&t.sw[0]),
-                                         16, 0, 0);
-      }
-    }
+    for (int i = 0; i < RB / 2; i++)
+      __builtin_amdgcn_global_load_lds((global_void *)(ga + 4096 * i), (lds_void *)(&t.a[64 * wave + 256 * i]), 16, 0,
+                                       0);
+    __builtin_amdgcn_global_load_lds((global_void *)(bsrc + static_cast<size_t>(g) * b_stride),
+                                     (lds_void *)(&t.b[64 * wave]), 16, 0, 0);
+    if (x_copy)
+      __builtin_amdgcn_global_load_lds((global_void *)(xsrc + static_cast<size_t>(g) * x_stride),
+                                       (lds_void *)(reinterpret_cast<char *>(&t) + x_dst), 4, 0, 0);
   };
 
-  float acc[4][NB][4];
+  float acc[RW][2][4];
 #pragma unroll
-  for (int i = 0; i < 4; i++)
+  for (int i = 0; i < RW; i++)
 #pragma unroll
-    for (int j = 0; j < NB; j++)
+    for (int j = 0; j < 2; j++)
 #pragma unroll
       for (int r = 0; r < 4; r++) acc[i][j][r] = 0.0f;
 
   const int quad = lane >> 4, col_in = lane & 15;
-  // Group g is read from one buffer while g + 1 is copied into the other.
-  auto step = [&](GroupTile &cur, GroupTile &next, int g) __attribute__((always_inline)) {
-    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's copies of cur
-    __syncthreads();                     // everyone's; nobody still reads next
-    if (g + 1 < groups) copy_group(next, g + 1);
-    v4i ahi[4], alo[4], b[NB];
+  auto step = [&](Tile &cur, Tile &next, int g) __attribute__((always_inline)) {
+    __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0): group g landed
+    plain_barrier();
+    // Past the last group the copy repeats it into the free stage.
+    issue(next, g + 1 < groups ? g + 1 : groups - 1);
+    v4i ahi[RW], alo[RW], b[2];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int rb = wm * 4 + i;
+    for (int i = 0; i < RW; i++) {
+      const int rb = wm * RW + i;
       const uint4 hv = cur.a[(rb * 2) * 64 + lane], lv = cur.a[(rb * 2 + 1) * 64 + lane];
       ahi[i] = v4i{static_cast<int>(hv.x), static_cast<int>(hv.y), static_cast<int>(hv.z), static_cast<int>(hv.w)};
       alo[i] = v4i{static_cast<int>(lv.x), static_cast<int>(lv.y), static_cast<int>(lv.z), static_cast<int>(lv.w)};
     }
 #pragma unroll
-    for (int j = 0; j < NB; j++) {
-      const uint4 w = cur.b[(wn * NB + j) * 64 + lane];
+    for (int j = 0; j < 2; j++) {
+      const uint4 w = cur.b[(wn * 2 + j) * 64 + lane];
       b[j] = v4i{static_cast<int>(w.x), static_cast<int>(w.y), static_cast<int>(w.z), static_cast<int>(w.w)};
     }
-    int32_t ws[NB];
-    float swv[NB];
+    int32_t ws[2];
+    float swv[2];
 #pragma unroll
-    for (int j = 0; j < NB; j++) {
-      const int c = (wn * NB + j) * 16 + col_in;
+    for (int j = 0; j < 2; j++) {
+      const int c = (wn * 2 + j) * 16 + col_in;
       ws[j] = cur.wsum[c];
       swv[j] = cur.sw[c];
     }
-    float sa[4][4];
+    float sa[RW][4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const float4 sv = *reinterpret_cast<const float4 *>(&cur.steps[(wm * 4 + i) * 16 + 4 * quad]);
+    for (int i = 0; i < RW; i++) {
+      const float4 sv = *reinterpret_cast<const float4 *>(&cur.steps[(wm * RW + i) * 16 + 4 * quad]);
       sa[i][0] = sv.x;
       sa[i][1] = sv.y;
       sa[i][2] = sv.z;
       sa[i][3] = sv.w;
     }
+    const v4i zero = {0, 0, 0, 0};
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < RW; i++)
 #pragma unroll
-      for (int j = 0; j < NB; j++) {
-        const v4i zero = {0, 0, 0, 0};
-        v4i hsum = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi[i], b[j], zero, 0, 0, 0);
+      for (int j = 0; j < 2; j++) {
+        const v4i hsum = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi[i], b[j], zero, 0, 0, 0);
         v4i c;
 #pragma unroll
         for (int r = 0; r < 4; r++) c[r] = (hsum[r] << 8) + ws[j];
@@ -272,19 +317,23 @@ __global__ __launch_bounds__(256) void gemm_kernel(const int8_t *__restrict__ a_
         }
       }
   };
-  copy_group(buf0, 0);
-  for (int g = 0; g < groups; g += 2) {
-    step(buf0, buf1, g);
-    if (g + 1 < groups) step(buf1, buf0, g + 1);
+  issue(ring0, 0);
+  int g = 0;
+  for (; g + 2 <= groups; g += 2) {
+    step(ring0, ring1, g);
+    step(ring1, ring0, g + 1);
   }
+  if (g < groups) step(ring0, ring1, g);
+  // The repeated copies must land before the workgroup's LDS is released.
+  __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
 
   // Exception FMAs (ascending columns), then the epilogue.
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int row_base = (mb0 + wm * 4 + i) * 16 + 4 * quad;
+  for (int i = 0; i < RW; i++) {
+    const int row_base = (mb0 + wm * RW + i) * 16 + 4 * quad;
 #pragma unroll
-    for (int j = 0; j < NB; j++) {
-      const int col = (nb0 + wn * NB + j) * 16 + col_in;
+    for (int j = 0; j < 2; j++) {
+      const int col = (nb0 + wn * 2 + j) * 16 + col_in;
       const bool col_ok = col < n;
 #pragma unroll
       for (int r = 0; r < 4; r++) {
@@ -333,17 +382,17 @@ int launch_prefill_i16(Ctx *ctx, const Linear *lin, const float *x, size_t rows,
                      row_scale, lin->exc_index, static_cast<int>(lin->n_exc), a_tiles, steps, exc_inputs,
                      static_cast<int>(m_pad));
   FOCR_HIP_CHECK(hipGetLastError());
-  // 64-column workgroup tiles (two 16-column blocks per wave): twice the
-  // workgroups of 128-column tiles, measured faster on every shape (m = 6,544:
-  // literal 0.130 -> 0.115 ms, W13 0.118 -> 0.106, QKV 0.062 -> 0.057,
-  // WO 0.058 -> 0.046, W2 0.096 -> 0.075).
-  constexpr int kNB = 2;
-  const dim3 grid(static_cast<unsigned>(m_pad / kBM), static_cast<unsigned>((n + 32 * kNB - 1) / (32 * kNB)));
+#ifndef FOCR_I16_BM
+#define FOCR_I16_BM 64
+#endif
+  constexpr int BM = FOCR_I16_BM;
+  const int row_tiles = static_cast<int>(m_pad / BM), col_tiles = static_cast<int>((n + kBN - 1) / kBN);
+  const dim3 grid(static_cast<unsigned>(row_tiles * col_tiles));
 #define FOCR_LAUNCH_I16(E)                                                                                      \
-  hipLaunchKernelGGL((gemm_kernel<E, kNB>), grid, dim3(256), 0, ctx->stream, a_tiles, steps, exc_inputs, lin->i16_b, \
+  hipLaunchKernelGGL((gemm_kernel<E, BM>), grid, dim3(256), 0, ctx->stream, a_tiles, steps, exc_inputs, lin->i16_b, \
                      lin->i16_wsum, lin->i16_sw, lin->exc_vals, static_cast<int>(lin->n_exc), static_cast<int>(m), \
                      static_cast<int>(n), static_cast<int>(groups), static_cast<int>(row_blocks),                \
-                     static_cast<int>(m_pad), out)
+                     static_cast<int>(m_pad), row_tiles, col_tiles, out)
   if (epilogue == FOCR_EPI_GLU)
     FOCR_LAUNCH_I16(FOCR_EPI_GLU);
   else if (epilogue == FOCR_EPI_ADD)

@@ -35,6 +35,7 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
 # file records the commands and the scaling).
 TRAFFIC_FILE = ROOT / "profiles" / "gemv_i16_m1_traffic.md"
 FP32_MFMA_PEAK = 157.3  # TFLOP/s dense
+FP32_VALU_PEAK = 78.6  # TFLOP/s, FMA without packed math (the exact-order chain kernels)
 INT8_MFMA_PEAK = 5000.0  # TOP/s dense
 POOL_BYTES = 600 << 20  # > 2 x 256 MB Infinity Cache
 
@@ -136,8 +137,12 @@ def bench_gemv(torch, fh, gen, np, bits, rows, steps, warmup, graph=True, n=4096
             "pool_copies": len(pool), "codes": codes, "scales": scales, "x": x, "cache_flushed": True}
 
 
-def bench_gemm(torch, fh, gen, np, reps):
-    """BASELINE config 1 (FP32, m = 6544) on the checkpoint shapes and the literal shape."""
+def bench_gemm(torch, fh, gen, np, reps, bits=32):
+    """BASELINE config 1 (FP32, m = 6544) on the checkpoint shapes and the
+    literal shape; with bits=16 the same projections on a near-exact body
+    (INT16 g64 codes, scales U(1e-6, 4e-6), dequantized fl(code * scale) as
+    the kernels stage them: the FP32 panels' exact chain is near-exact
+    mode's prefill projection)."""
     m = 6544
     shapes = [("qkv", 768, 2048, fh.Epilogue.STORE), ("wo", 1024, 768, fh.Epilogue.ADD),
               ("w13", 768, 4608, fh.Epilogue.GLU), ("w2", 2304, 768, fh.Epilogue.ADD),
@@ -146,8 +151,11 @@ def bench_gemm(torch, fh, gen, np, reps):
     res = {}
     for name, k, n, epi in shapes:
         a = torch.from_numpy(gen.normal((m, k), 1.0, 10)).cuda()
-        w = gen.normal((n, k), 0.02, 11)
-        lin = fh.Linear.from_f32(w)
+        if bits == 32:
+            lin = fh.Linear.from_f32(gen.normal((n, k), 0.02, 11))
+        else:
+            lin = fh.QuantLinear(16, gen.codes_uniform((n, k), -32767, 32767, np.int16, 11),
+                                 gen.uniform((n, k // 64), 1e-6, 4e-6, 12), 64)
         width = n // 2 if epi == fh.Epilogue.GLU else n
         out = torch.zeros((m, width), device="cuda")
         for kern in (fh.PrefillProjection.F32_MFMA, fh.PrefillProjection.F32_CHAIN):
@@ -157,7 +165,9 @@ def bench_gemm(torch, fh, gen, np, reps):
             avg, med = timer.per_launch_ms(fn, reps)
             flops = 2.0 * m * k * n
             tag = "mfma" if kern == fh.PrefillProjection.F32_MFMA else "chain"
-            res[f"{name}_{tag}"] = {"ms": round(avg, 4), "tflops": round(flops / (avg * 1e-3) / 1e12, 2)}
+            tflops = flops / (avg * 1e-3) / 1e12
+            peak = FP32_MFMA_PEAK if tag == "mfma" else FP32_VALU_PEAK
+            res[f"{name}_{tag}"] = {"ms": round(avg, 4), "tflops": round(tflops, 2), "frac": round(tflops / peak, 3)}
         lin.free()
     return res
 
@@ -657,7 +667,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--ops", default="gemv,gemm,i16,attention,layer,kv,screen,copy")
+    ap.add_argument("--ops", default="gemv,gemm,nearexact,i16,attention,layer,kv,screen,copy")
     ap.add_argument("--reps", type=int, default=20, help="timed launches per secondary op")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
@@ -705,6 +715,9 @@ def main():
     if "gemm" in ops:
         per_op["prefill_f32"] = bench_gemm(torch, fh, gen, np, args.reps)
         log(f"prefill_f32: {per_op['prefill_f32']}")
+    if "nearexact" in ops:
+        per_op["prefill_i16codes"] = bench_gemm(torch, fh, gen, np, args.reps, bits=16)
+        log(f"prefill_i16codes: {per_op['prefill_i16codes']}")
     if "i16" in ops:
         per_op["prefill_i16xi8"] = bench_i16(torch, fh, gen, np, args.reps)
         log(f"prefill_i16xi8: {per_op['prefill_i16xi8']}")

@@ -40,6 +40,45 @@ __device__ __forceinline__ float to_f32(int8_t v) { return static_cast<float>(st
 __device__ __forceinline__ float to_f32(int16_t v) { return static_cast<float>(static_cast<int32_t>(v)); }
 __device__ __forceinline__ float to_f32(float v) { return v; }
 
+// Code `I` of a 16-byte weight chunk as a float, exactly: one
+// v_cvt_f32_i32 whose source operand selects and sign-extends the byte
+// (int8) or half-word (int16) in place (SDWA), instead of a shift, a
+// bit-field extract and a conversion.
+template <int SEL>
+__device__ __forceinline__ float sdwa_cvt(uint32_t w) {
+  float r;
+  if constexpr (SEL == 0)
+    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0" : "=v"(r) : "v"(w));
+  else if constexpr (SEL == 1)
+    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1" : "=v"(r) : "v"(w));
+  else if constexpr (SEL == 2)
+    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2" : "=v"(r) : "v"(w));
+  else if constexpr (SEL == 3)
+    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3" : "=v"(r) : "v"(w));
+  else if constexpr (SEL == 4)
+    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:WORD_0" : "=v"(r) : "v"(w));
+  else
+    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:WORD_1" : "=v"(r) : "v"(w));
+  return r;
+}
+template <typename T, int I>
+__device__ __forceinline__ float chunk_code(const uint4 &raw) {
+  const uint32_t words[4] = {raw.x, raw.y, raw.z, raw.w};
+  if constexpr (sizeof(T) == 1)
+    return sdwa_cvt<I % 4>(words[I / 4]);
+  else if constexpr (sizeof(T) == 2)
+    return sdwa_cvt<4 + I % 2>(words[I / 2]);
+  else
+    return __uint_as_float(words[I]);
+}
+template <typename T, int N>
+__device__ __forceinline__ void chunk_codes(const uint4 &raw, float *out) {
+  if constexpr (N > 0) {
+    chunk_codes<T, N - 1>(raw, out);
+    out[N - 1] = chunk_code<T, N - 1>(raw);
+  }
+}
+
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
@@ -244,8 +283,8 @@ __global__ __launch_bounds__(256) void kernel(Args a) {
 
   // Step t: S blocks of this lane's phase for both channels.
   auto step = [&](int t, const uint4 &raw) {
-    T vals[S][2];
-    __builtin_memcpy(vals, &raw, 16);
+    float vals[S * 2];  // [block][channel], as laid out in the chunk
+    chunk_codes<T, S * 2>(raw, vals);
     Scales<NS> sc;
     if constexpr (NS > 0) sc = load_scales<NS>(my_scales + t * 2 * NS);
 #pragma unroll
@@ -258,7 +297,7 @@ __global__ __launch_bounds__(256) void kernel(Args a) {
       }
 #pragma unroll
       for (int c = 0; c < 2; c++) {
-        float w = to_f32(vals[s][c]);
+        float w = vals[2 * s + c];
         if constexpr (SPS > 0) w = w * sc.v[c * SPS + s / (S / SPS)];
 #pragma unroll
         for (int r = 0; r < M; r++) acc[c][r] = fmaf_(xr[r], w, acc[c][r]);

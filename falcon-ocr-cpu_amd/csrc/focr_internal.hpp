@@ -110,6 +110,27 @@ int launch_attention_decode(Ctx *ctx, const float *q, const float *prefix_k, con
 // ---- device helpers ---------------------------------------------------------
 __device__ __forceinline__ float fmaf_(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
 
+// A signed byte (SEL 0..3) or half-word (SEL 4, 5: low, high) of `w` as a
+// float, exactly: one v_cvt_f32_i32 whose source operand selects and
+// sign-extends the sub-word in place (SDWA), instead of a shift, a bit-field
+// extract and a conversion.
+template <int SEL>
+__device__ __forceinline__ float sdwa_cvt(uint32_t w) {
+  float r;
+  if constexpr (SEL == 0)
+    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0" : "=v"(r) : "v"(w));
+  else if constexpr (SEL == 1)
+    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1" : "=v"(r) : "v"(w));
+  else if constexpr (SEL == 2)
+    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2" : "=v"(r) : "v"(w));
+  else if constexpr (SEL == 3)
+    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3" : "=v"(r) : "v"(w));
+  else if constexpr (SEL == 4)
+    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:WORD_0" : "=v"(r) : "v"(w));
+  else
+    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:WORD_1" : "=v"(r) : "v"(w));
+  return r;
+}
 // squared_relu_glu, src/kernels/mod.rs:567-572.
 __device__ __forceinline__ float squared_relu_glu(float gate, float up) {
   float relu = gate > 0.0f ? gate : 0.0f;

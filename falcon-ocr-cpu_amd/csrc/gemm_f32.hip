@@ -529,9 +529,10 @@ __device__ __forceinline__ void chain2_weights(const GemmArgs &a, int row, int c
 #pragma unroll
     for (int e = 0; e < COUNT; e++) {
       if constexpr (sizeof(T) == 2)
-        w[e] = static_cast<float>(static_cast<int16_t>((u[e / 2] >> (16 * (e % 2))) & 0xffffu));
+        w[e] = e % 2 == 0 ? sdwa_cvt<4>(u[e / 2]) : sdwa_cvt<5>(u[e / 2]);
       else
-        w[e] = static_cast<float>(static_cast<int8_t>((u[e / 4] >> (8 * (e % 4))) & 0xffu));
+        w[e] = e % 4 == 0 ? sdwa_cvt<0>(u[e / 4])
+                          : e % 4 == 1 ? sdwa_cvt<1>(u[e / 4]) : e % 4 == 2 ? sdwa_cvt<2>(u[e / 4]) : sdwa_cvt<3>(u[e / 4]);
     }
     const float sc = a.scales[static_cast<size_t>(row) * a.groups + col / a.group];
 #pragma unroll

@@ -40,27 +40,7 @@ __device__ __forceinline__ float to_f32(int8_t v) { return static_cast<float>(st
 __device__ __forceinline__ float to_f32(int16_t v) { return static_cast<float>(static_cast<int32_t>(v)); }
 __device__ __forceinline__ float to_f32(float v) { return v; }
 
-// Code `I` of a 16-byte weight chunk as a float, exactly: one
-// v_cvt_f32_i32 whose source operand selects and sign-extends the byte
-// (int8) or half-word (int16) in place (SDWA), instead of a shift, a
-// bit-field extract and a conversion.
-template <int SEL>
-__device__ __forceinline__ float sdwa_cvt(uint32_t w) {
-  float r;
-  if constexpr (SEL == 0)
-    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0" : "=v"(r) : "v"(w));
-  else if constexpr (SEL == 1)
-    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1" : "=v"(r) : "v"(w));
-  else if constexpr (SEL == 2)
-    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2" : "=v"(r) : "v"(w));
-  else if constexpr (SEL == 3)
-    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3" : "=v"(r) : "v"(w));
-  else if constexpr (SEL == 4)
-    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:WORD_0" : "=v"(r) : "v"(w));
-  else
-    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:WORD_1" : "=v"(r) : "v"(w));
-  return r;
-}
+// Code `I` of a 16-byte weight chunk as a float, exactly (sdwa_cvt).
 template <typename T, int I>
 __device__ __forceinline__ float chunk_code(const uint4 &raw) {
   const uint32_t words[4] = {raw.x, raw.y, raw.z, raw.w};

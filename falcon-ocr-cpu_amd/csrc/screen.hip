@@ -204,9 +204,12 @@ __global__ __launch_bounds__(256) void screen_kernel(ScreenArgs a) {
     // tile's loads go out.
     float cf[kGroup];
 #pragma unroll
-    for (int i = 0; i < kGroup; i++) {
+    for (int i = 0; i < kGroup; i += 4) {
       const uint32_t word = (&raw[i >> 4].x)[(i >> 2) & 3];
-      cf[i] = static_cast<float>(static_cast<int8_t>((word >> (8 * (i & 3))) & 0xffu));
+      cf[i] = sdwa_cvt<0>(word);
+      cf[i + 1] = sdwa_cvt<1>(word);
+      cf[i + 2] = sdwa_cvt<2>(word);
+      cf[i + 3] = sdwa_cvt<3>(word);
     }
     sc[wave][g][row_in_wave] = scale;
     load_tile(tile + nblocks);

@@ -33,7 +33,7 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, GB/s
 # HBM bytes per launch of the headline kernel, from rocprofv3 FETCH_SIZE and
 # WRITE_SIZE runs scaled by the same counters on a copy of known size (the
 # file records the commands and the scaling).
-TRAFFIC_FILE = ROOT / "profiles" / "gemv_i16_m1_traffic.md"
+TRAFFIC_FILE = ROOT / "profiles" / "gemv_decode_traffic.md"
 FP32_MFMA_PEAK = 157.3  # TFLOP/s dense
 FP32_VALU_PEAK = 78.6  # TFLOP/s, FMA without packed math (the exact-order chain kernels)
 INT8_MFMA_PEAK = 5000.0  # TOP/s dense

@@ -117,14 +117,16 @@ __device__ __forceinline__ float4 load_weights4(const GemmArgs &a, int row, int 
     return f;
   } else if constexpr (std::is_same<T, int16_t>::value) {
     const uint2 raw = *reinterpret_cast<const uint2 *>(codes + at);
-    w[0] = static_cast<float>(static_cast<int16_t>(raw.x & 0xffffu));
-    w[1] = static_cast<float>(static_cast<int16_t>(raw.x >> 16));
-    w[2] = static_cast<float>(static_cast<int16_t>(raw.y & 0xffffu));
-    w[3] = static_cast<float>(static_cast<int16_t>(raw.y >> 16));
+    w[0] = sdwa_cvt<4>(raw.x);
+    w[1] = sdwa_cvt<5>(raw.x);
+    w[2] = sdwa_cvt<4>(raw.y);
+    w[3] = sdwa_cvt<5>(raw.y);
   } else {
     const uint32_t raw = *reinterpret_cast<const uint32_t *>(codes + at);
-#pragma unroll
-    for (int i = 0; i < 4; i++) w[i] = static_cast<float>(static_cast<int8_t>((raw >> (8 * i)) & 0xffu));
+    w[0] = sdwa_cvt<0>(raw);
+    w[1] = sdwa_cvt<1>(raw);
+    w[2] = sdwa_cvt<2>(raw);
+    w[3] = sdwa_cvt<3>(raw);
   }
   const float s = a.scales[static_cast<size_t>(row) * a.groups + col / a.group];
 #pragma unroll

@@ -401,7 +401,7 @@ int launch_tiles(Ctx *ctx, AttnArgs a, int softmax, int exp_mode) {
     m.tiles = tiles;
     m.slots = slots;
     m.merge_end = a.query_len;
-    hipLaunchKernelGGL(split::merge_kernel, dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(a.n_heads)),
+    hipLaunchKernelGGL(split::merge_kernel, dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(a.n_heads), split::kMergeSplit),
                        dim3(256), 0, ctx->stream, m, plan);
     FOCR_HIP_CHECK(hipGetLastError());
   }

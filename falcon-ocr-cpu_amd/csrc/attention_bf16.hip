@@ -581,7 +581,7 @@ int launch_attention_bf16(Ctx *ctx, const float *q, const float *k, const float 
       // merge_kernel's rows are relative to the launch: offset the output.
       m.out = out + q0 * n_heads * 64;
       m.merge_end = merge_end - static_cast<int>(q0);
-      hipLaunchKernelGGL(split::merge_kernel, dim3(static_cast<unsigned>(qtiles), static_cast<unsigned>(n_heads)),
+      hipLaunchKernelGGL(split::merge_kernel, dim3(static_cast<unsigned>(qtiles), static_cast<unsigned>(n_heads), split::kMergeSplit),
                          dim3(256), 0, ctx->stream, m, plan);
       FOCR_HIP_CHECK(hipGetLastError());
     }

@@ -113,42 +113,66 @@ __device__ inline float2 *part_md(const Args &a, const Plan &plan, const Item &i
          slot * kQueries + row_in_tile;
 }
 
-// One workgroup per tile and head (unsplit tiles exit); two threads per row.
+// Grid (tiles, heads, kMergeSplit): a workgroup merges kQueries /
+// kMergeSplit rows of one tile and head (unsplit tiles exit), eight threads
+// per row, each 8 of the 64 dims. The parts' maxima are read first, then
+// their outputs kMergeBatch parts at a time (all loads of a batch in flight
+// together), added in part order.
+constexpr int kMergeSplit = 4;
+constexpr int kMergeBatch = 4;
 static __global__ __launch_bounds__(256) void merge_kernel(Args a, Plan plan) {
   const int order = blockIdx.x, head = blockIdx.y;
   const int parts = plan.first[order + 1] - plan.first[order];
   if (parts <= 1) return;
-  const int row_in_tile = threadIdx.x >> 1, half = threadIdx.x & 1;
+  const int row_in_tile = blockIdx.z * (kQueries / kMergeSplit) + (threadIdx.x >> 3), slice = threadIdx.x & 7;
   const int row = (a.tiles - 1 - order) * kQueries + row_in_tile;
   if (row >= a.merge_end) return;
   const float2 *md = reinterpret_cast<const float2 *>(a.part + static_cast<size_t>(a.slots) * a.n_heads * kQueries * 64);
+  const size_t slot0 = static_cast<size_t>(plan.slot[order]) * a.n_heads + head;
+  const size_t pstride = static_cast<size_t>(a.n_heads);  // slots between consecutive parts of a tile and head
   const float ninf = -__builtin_inff();
   float big = ninf;
-  for (int p = 0; p < parts; p++) {
-    const size_t slot = static_cast<size_t>(plan.slot[order] + p) * a.n_heads + head;
-    big = __builtin_fmaxf(big, md[slot * kQueries + row_in_tile].x);
+  for (int p0 = 0; p0 < parts; p0 += kMergeBatch) {
+    float2 m[kMergeBatch];
+#pragma unroll
+    for (int j = 0; j < kMergeBatch; j++) {
+      const int p = p0 + j < parts ? p0 + j : parts - 1;
+      m[j] = md[(slot0 + p * pstride) * kQueries + row_in_tile];
+    }
+#pragma unroll
+    for (int j = 0; j < kMergeBatch; j++)
+      if (p0 + j < parts) big = __builtin_fmaxf(big, m[j].x);
   }
   float den = 0.0f;
-  float4 o[8];
+  float4 o[2] = {make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f)};
+  for (int p0 = 0; p0 < parts; p0 += kMergeBatch) {
+    float2 m[kMergeBatch];
+    float4 v[kMergeBatch][2];
 #pragma unroll
-  for (int i = 0; i < 8; i++) o[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int p = 0; p < parts; p++) {
-    const size_t slot = static_cast<size_t>(plan.slot[order] + p) * a.n_heads + head;
-    const float2 m = md[slot * kQueries + row_in_tile];
-    const float f = m.x == ninf ? 0.0f : expf_acc(m.x - big);
-    den = den + m.y * f;
-    const float4 *src = reinterpret_cast<const float4 *>(a.part + (slot * kQueries + row_in_tile) * 64 + 32 * half);
+    for (int j = 0; j < kMergeBatch; j++) {
+      const int p = p0 + j < parts ? p0 + j : parts - 1;
+      const size_t slot = slot0 + p * pstride;
+      m[j] = md[slot * kQueries + row_in_tile];
+      const float4 *src = reinterpret_cast<const float4 *>(a.part + (slot * kQueries + row_in_tile) * 64 + 8 * slice);
+      v[j][0] = src[0];
+      v[j][1] = src[1];
+    }
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const float4 v = src[i];
-      o[i] = make_float4(fmaf_(v.x, f, o[i].x), fmaf_(v.y, f, o[i].y), fmaf_(v.z, f, o[i].z), fmaf_(v.w, f, o[i].w));
+    for (int j = 0; j < kMergeBatch; j++) {
+      if (p0 + j >= parts) break;
+      const float f = m[j].x == ninf ? 0.0f : expf_acc(m[j].x - big);
+      den = den + m[j].y * f;
+#pragma unroll
+      for (int i = 0; i < 2; i++)
+        o[i] = make_float4(fmaf_(v[j][i].x, f, o[i].x), fmaf_(v[j][i].y, f, o[i].y), fmaf_(v[j][i].z, f, o[i].z),
+                           fmaf_(v[j][i].w, f, o[i].w));
     }
   }
   const float lse = big + logf_acc(den);
   const float sink_scale = __fdiv_rn(1.0f, 1.0f + expf_acc(a.sinks[head] - lse));
-  float4 *dst = reinterpret_cast<float4 *>(a.out + (static_cast<size_t>(row) * a.n_heads + head) * 64 + 32 * half);
+  float4 *dst = reinterpret_cast<float4 *>(a.out + (static_cast<size_t>(row) * a.n_heads + head) * 64 + 8 * slice);
 #pragma unroll
-  for (int i = 0; i < 8; i++)
+  for (int i = 0; i < 2; i++)
     dst[i] = make_float4(__fmul_rn(__fdiv_rn(o[i].x, den), sink_scale), __fmul_rn(__fdiv_rn(o[i].y, den), sink_scale),
                          __fmul_rn(__fdiv_rn(o[i].z, den), sink_scale), __fmul_rn(__fdiv_rn(o[i].w, den), sink_scale));
 }

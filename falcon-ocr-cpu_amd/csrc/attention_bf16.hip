@@ -288,9 +288,11 @@ __global__ __launch_bounds__(128) void short_rows_kernel(Bf16Args a, int first_r
 
 static_assert(split::kQueries == kQueries, "one query tile per split plan entry");
 
+// A stage is two 32-key tiles (64 keys): one online-softmax update per 64
+// keys, two independent score blocks in flight.
 struct KvLds {
-  uint4 k[256];  // 32 keys x 8 chunks
-  uint4 v[256];  // 64 dims x 4 chunks
+  uint4 k[2][256];  // [tile][32 keys x 8 chunks]
+  uint4 v[2][256];  // [tile][64 dims x 4 chunks]
 };
 
 template <bool STATIC>
@@ -356,59 +358,74 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void a
   const uint4 *kt = a.kb + static_cast<size_t>(head) * a.tiles * 256;
   const uint4 *vt = a.vb + static_cast<size_t>(kv_head) * a.tiles * 256;
   // Each thread moves one 16-byte chunk of K and one of V per tile; wave w
-  // fills bytes [1 KB w, 1 KB (w + 1)) of each.
-  auto copy_tile = [&](KvLds &dst, int tile) {
+  // fills bytes [1 KB w, 1 KB (w + 1)) of each. A second tile past the last
+  // one repeats it (its keys are hidden by the mask: they follow every query).
+  auto copy_stage = [&](KvLds &dst, int tile) {
+    const int t1 = tile + 1 < a.tiles ? tile + 1 : a.tiles - 1;
     __builtin_amdgcn_global_load_lds((global_void *)(kt + static_cast<size_t>(tile) * 256 + tid),
-                                     (lds_void *)(&dst.k[64 * wave]), 16, 0, 0);
+                                     (lds_void *)(&dst.k[0][64 * wave]), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((global_void *)(kt + static_cast<size_t>(t1) * 256 + tid),
+                                     (lds_void *)(&dst.k[1][64 * wave]), 16, 0, 0);
     __builtin_amdgcn_global_load_lds((global_void *)(vt + static_cast<size_t>(tile) * 256 + tid),
-                                     (lds_void *)(&dst.v[64 * wave]), 16, 0, 0);
+                                     (lds_void *)(&dst.v[0][64 * wave]), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((global_void *)(vt + static_cast<size_t>(t1) * 256 + tid),
+                                     (lds_void *)(&dst.v[1][64 * wave]), 16, 0, 0);
   };
 
   auto step = [&](KvLds &cur, KvLds &next, int kstart) __attribute__((always_inline)) {
     __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's copies of cur
     __syncthreads();                     // everyone's copies; nobody still reads next
-    if (kstart + kKeys < visible_end) copy_tile(next, (kstart + kKeys) / kKeys);
+    if (kstart + 2 * kKeys < visible_end) copy_stage(next, (kstart + 2 * kKeys) / kKeys);
     if (!(w_queries > 0 && kstart < w_bf16_end)) return;
-    // S^T = K Q^T (register r: key kstart + 8(r/4) + 4h + r%4, query l32).
-    v16f st;
+    // S^T = K Q^T per tile t (register r: key kstart + 32 t + 8(r/4) + 4h + r%4, query l32).
+    v16f st[2];
 #pragma unroll
-    for (int r = 0; r < 16; r++) st[r] = 0.0f;
+    for (int t = 0; t < 2; t++) {
+      // The tile's four K fragments are read before its products.
+      Bf16x8 kf[4];
 #pragma unroll
-    for (int s = 0; s < 4; s++) {
-      Bf16x8 kf;
-      kf.u = cur.k[l32 * 8 + ((2 * s + h) ^ (l32 & 7))];
-      st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf.v, qb[s].v, st, 0, 0, 0);
+      for (int s = 0; s < 4; s++) kf[s].u = cur.k[t][l32 * 8 + ((2 * s + h) ^ (l32 & 7))];
+#pragma unroll
+      for (int r = 0; r < 16; r++) st[t][r] = 0.0f;
+#pragma unroll
+      for (int s = 0; s < 4; s++) st[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[s].v, qb[s].v, st[t], 0, 0, 0);
     }
-    const bool full = kstart + kKeys <= w_first + 1 ||
-                      (w_all_image && kstart >= a.image_start && kstart + kKeys <= a.image_end);
+    const bool full = kstart + 2 * kKeys <= w_first + 1 ||
+                      (w_all_image && kstart >= a.image_start && kstart + 2 * kKeys <= a.image_end);
     if (!full) {
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int key = kstart + 8 * (r / 4) + 4 * h + (r % 4);
-        const bool hidden = key > my_query && !(my_image && key >= a.image_start && key < a.image_end);
-        st[r] = hidden ? -__builtin_inff() : st[r];
-      }
+      for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const int key = kstart + 32 * t + 8 * (r / 4) + 4 * h + (r % 4);
+          const bool hidden = key > my_query && !(my_image && key >= a.image_start && key < a.image_end);
+          st[t][r] = hidden ? -__builtin_inff() : st[t][r];
+        }
     }
-    Bf16x8 pb[2];
+    Bf16x8 pb[2][2];
     if constexpr (STATIC) {
       // p = 2^(log2(e) * s), masked +0; denominators add the rounded p.
-      float psum = 0.0f;
+      float psum[2] = {0.0f, 0.0f};
 #pragma unroll
-      for (int i = 0; i < 8; i++) {
-        const float s0 = st[2 * i], s1 = st[2 * i + 1];
-        const float p0 = s0 == -__builtin_inff() ? 0.0f : exp2_minimax(kLog2e * s0);
-        const float p1 = s1 == -__builtin_inff() ? 0.0f : exp2_minimax(kLog2e * s1);
-        const uint32_t pk = pack_bf16(p0, p1);
-        psum = psum + bf16_lo(pk);
-        psum = psum + bf16_hi(pk);
-        reinterpret_cast<uint32_t *>(&pb[i / 4].u)[i % 4] = pk;
-      }
-      den = den + halves_sum(psum);
+      for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+          const float s0 = st[t][2 * i], s1 = st[t][2 * i + 1];
+          const float p0 = s0 == -__builtin_inff() ? 0.0f : exp2_minimax(kLog2e * s0);
+          const float p1 = s1 == -__builtin_inff() ? 0.0f : exp2_minimax(kLog2e * s1);
+          const uint32_t pk = pack_bf16(p0, p1);
+          psum[t] = psum[t] + bf16_lo(pk);
+          psum[t] = psum[t] + bf16_hi(pk);
+          reinterpret_cast<uint32_t *>(&pb[t][i / 4].u)[i % 4] = pk;
+        }
+      den = den + halves_sum(psum[0] + psum[1]);
     } else {
-      // Online step (softmax_pairs, bf16.rs:409-473).
-      float tile_max = st[0];
+      // Online step over the stage's 64 keys (softmax_pairs, bf16.rs:409-473).
+      float tile_max = st[0][0];
 #pragma unroll
-      for (int r = 1; r < 16; r++) tile_max = __builtin_fmaxf(tile_max, st[r]);  // v_max3 pairs
+      for (int r = 1; r < 16; r++) tile_max = __builtin_fmaxf(tile_max, st[0][r]);  // v_max3 pairs
+#pragma unroll
+      for (int r = 0; r < 16; r++) tile_max = __builtin_fmaxf(tile_max, st[1][r]);
       tile_max = halves_max(tile_max);
       const float new_max = tile_max > run_max ? tile_max : run_max;
       const bool skip = new_max == -__builtin_inff();
@@ -420,16 +437,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void a
       // p = 2^(s log2(e) - shift log2(e)): one FMA per score (the argument
       // rounds once instead of twice; p is rounded to BF16 next).
       const float shift_l = shift * kLog2e;
-      float psum = 0.0f;
+      float psum[2] = {0.0f, 0.0f};
 #pragma unroll
-      for (int i = 0; i < 8; i++) {
-        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[2 * i], kLog2e, -shift_l));
-        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[2 * i + 1], kLog2e, -shift_l));
-        psum = psum + p0;
-        psum = psum + p1;
-        reinterpret_cast<uint32_t *>(&pb[i / 4].u)[i % 4] = pack_bf16(p0, p1);
-      }
-      den = den * rescale + halves_sum(psum);
+      for (int t = 0; t < 2; t++)
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+          const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[t][2 * i], kLog2e, -shift_l));
+          const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(st[t][2 * i + 1], kLog2e, -shift_l));
+          psum[t] = psum[t] + p0;
+          psum[t] = psum[t] + p1;
+          reinterpret_cast<uint32_t *>(&pb[t][i / 4].u)[i % 4] = pack_bf16(p0, p1);
+        }
+      den = den * rescale + halves_sum(psum[0] + psum[1]);
       run_max = skip ? run_max : new_max;
       if (__builtin_amdgcn_ballot_w64(rescale != 1.0f)) {
 #pragma unroll
@@ -438,23 +457,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void a
           for (int r = 0; r < 16; r++) o[d][r] = o[d][r] * rescale;
       }
     }
-    // O^T += V^T P^T: step s takes score registers 8s .. 8s + 7 (keys
-    // 16s + 4h + 8(e/4) + e%4), V^T slots 16s + 8h .. +7 of dim l32 + 32d.
+    // O^T += V^T P^T: tile t, step s takes score registers 8s .. 8s + 7
+    // (keys 32 t + 16s + 4h + 8(e/4) + e%4), V^T slots 16s + 8h .. +7 of
+    // dim l32 + 32d.
 #pragma unroll
-    for (int s = 0; s < 2; s++)
+    for (int t = 0; t < 2; t++)
 #pragma unroll
-      for (int d = 0; d < 2; d++) {
-        const int dim = l32 + 32 * d;
-        Bf16x8 vf;
-        vf.u = cur.v[dim * 4 + ((2 * s + h) ^ ((dim >> 1) & 3))];
-        o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf.v, pb[s].v, o[d], 0, 0, 0);
-      }
+      for (int s = 0; s < 2; s++)
+#pragma unroll
+        for (int d = 0; d < 2; d++) {
+          const int dim = l32 + 32 * d;
+          Bf16x8 vf;
+          vf.u = cur.v[t][dim * 4 + ((2 * s + h) ^ ((dim >> 1) & 3))];
+          o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf.v, pb[t][s].v, o[d], 0, 0, 0);
+        }
   };
 
-  copy_tile(buf0, key_begin / kKeys);
-  for (int kstart = key_begin; kstart < visible_end; kstart += 2 * kKeys) {
+  copy_stage(buf0, key_begin / kKeys);
+  for (int kstart = key_begin; kstart < visible_end; kstart += 4 * kKeys) {
     step(buf0, buf1, kstart);
-    if (kstart + kKeys < visible_end) step(buf1, buf0, kstart + kKeys);
+    if (kstart + 2 * kKeys < visible_end) step(buf1, buf0, kstart + 2 * kKeys);
   }
 
   // The short last key tile lies in one part (parts are whole 128-key tiles).

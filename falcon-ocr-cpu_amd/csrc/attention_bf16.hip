@@ -26,12 +26,15 @@
 // Layout: a pre-pass writes this call's K and V as BF16 tiles of 32 keys
 // (zero past the last key) into the context scratch:
 //   K: [head][tile][32 keys][8 chunks of 8 dims], chunk c of key r stored at
-//      c ^ (r % 8): the 32 lanes that read one chunk of 32 keys hit
-//      distinct banks;
+//      c ^ k_swizzle(r);
 //   V: [kv head][tile][64 dims][4 chunks of 8 key slots], transposed, with
 //      slot p = 16s + 8h + e holding key 16s + 4h + 8(e/4) + e%4 (the key
 //      order in which the score registers feed the PV product), chunk c of
-//      dim d stored at c ^ ((d / 2) % 4).
+//      dim d stored at c ^ v_swizzle(d).
+// gfx950 serves a ds_read_b128 sixteen lanes (256 bytes) at a time: the
+// swizzles put the sixteen 16-byte chunks that sixteen consecutive lanes read
+// (one chunk of 16 consecutive keys, or of 16 consecutive dims) in distinct
+// 16-byte bank groups (also every 8 consecutive lanes within 128 bytes).
 // The main kernel copies each 4 KB + 4 KB tile to LDS with the LDS-DMA path,
 // double buffered, and runs v_mfma_f32_32x32x16_bf16: S^T = K Q^T (4 per
 // 32-key tile), O^T += V^T P^T (4 per tile). A lane holds the 16 scores of
@@ -77,6 +80,9 @@ __device__ __forceinline__ float exp2_minimax(float t) {
   return __builtin_ldexpf(p, static_cast<int>(n));
 }
 
+__device__ __forceinline__ int k_swizzle(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+__device__ __forceinline__ int v_swizzle(int d) { return ((d >> 1) & 3) ^ ((d >> 3) & 1); }
+
 union Bf16x8 {
   bf16x8 v;
   uint4 u;
@@ -99,7 +105,7 @@ __global__ __launch_bounds__(256) void convert_kv_kernel(const float *__restrict
       const float4 a = src[0], b = src[1];
       out = make_uint4(pack_bf16(a.x, a.y), pack_bf16(a.z, a.w), pack_bf16(b.x, b.y), pack_bf16(b.z, b.w));
     }
-    kb[(static_cast<size_t>(head) * tiles + tile) * 256 + r * 8 + (c ^ (r & 7))] = out;
+    kb[(static_cast<size_t>(head) * tiles + tile) * 256 + r * 8 + (c ^ k_swizzle(r))] = out;
   }
   if (head < n_kv_heads) {
     const int d = t >> 2, c = t & 3;
@@ -111,7 +117,7 @@ __global__ __launch_bounds__(256) void convert_kv_kernel(const float *__restrict
       const int key = tile * kKeys + 16 * s + 4 * hh + 8 * (ee >> 2) + (ee & 3);
       val[e] = key < total ? v[(static_cast<size_t>(key) * n_kv_heads + head) * 64 + d] : 0.0f;
     }
-    vb[(static_cast<size_t>(head) * tiles + tile) * 256 + d * 4 + (c ^ ((d >> 1) & 3))] =
+    vb[(static_cast<size_t>(head) * tiles + tile) * 256 + d * 4 + (c ^ v_swizzle(d))] =
         make_uint4(pack_bf16(val[0], val[1]), pack_bf16(val[2], val[3]), pack_bf16(val[4], val[5]),
                    pack_bf16(val[6], val[7]));
   }
@@ -384,7 +390,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void a
       // The tile's four K fragments are read before its products.
       Bf16x8 kf[4];
 #pragma unroll
-      for (int s = 0; s < 4; s++) kf[s].u = cur.k[t][l32 * 8 + ((2 * s + h) ^ (l32 & 7))];
+      for (int s = 0; s < 4; s++) kf[s].u = cur.k[t][l32 * 8 + ((2 * s + h) ^ k_swizzle(l32))];
 #pragma unroll
       for (int r = 0; r < 16; r++) st[t][r] = 0.0f;
 #pragma unroll
@@ -468,7 +474,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void a
         for (int d = 0; d < 2; d++) {
           const int dim = l32 + 32 * d;
           Bf16x8 vf;
-          vf.u = cur.v[t][dim * 4 + ((2 * s + h) ^ ((dim >> 1) & 3))];
+          vf.u = cur.v[t][dim * 4 + ((2 * s + h) ^ v_swizzle(dim))];
           o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf.v, pb[t][s].v, o[d], 0, 0, 0);
         }
   };

@@ -373,7 +373,7 @@ int launch_tiles(Ctx *ctx, AttnArgs a, int softmax, int exp_mode) {
   split::Plan plan;
   int slots = 0;
   const int items = split::make_plan(plan, tiles, a.query_len, a.query_offset, a.image_start, a.image_end, a.n_heads,
-                                     kKeys, &slots);
+                                     kKeys, split::kSplitItemsF32, &slots);
   a.tiles = tiles;
   a.slots = slots;
   a.part = nullptr;

@@ -567,7 +567,7 @@ int launch_attention_bf16(Ctx *ctx, const float *q, const float *k, const float 
     split::Plan plan;
     int slots = 0;
     const int items = split::make_plan(plan, qtiles, n, static_cast<int>(q0), a.image_start, a.image_end,
-                                       a.n_heads, 128, &slots);
+                                       a.n_heads, 128, split::kSplitItemsBf16, &slots);
     a.q_base = static_cast<int>(q0);
     a.qtiles = qtiles;
     a.slots = slots;

@@ -3,8 +3,8 @@
 // A 128-query tile of a causal or image-prefixed prefill sees between 128 and
 // the whole context's keys, so one workgroup per tile leaves the chip idle
 // while the last (longest) tiles finish. Each tile's visible keys are split
-// into equal work items of at most `chunk_keys` keys (about kSplitItems items
-// per call); an item runs the tile's online softmax over its keys only and,
+// into equal work items (about `target_items` items per call, at least
+// kMinChunkKeys keys each); an item runs the tile's online softmax over its keys only and,
 // when its tile is split, stores the unnormalized state (max, denominator,
 // output) per query row. merge_kernel combines the parts of a row in part
 // order — M = max of the maxima, den = sum den_p exp(m_p - M),
@@ -20,7 +20,12 @@ namespace split {
 
 constexpr int kQueries = 128;   // query rows per tile
 constexpr int kMaxTiles = 256;  // plan table size: 32,768 query rows per launch
-constexpr long long kSplitItems = 3072;  // target work items per call (about 4 per slot)
+// Target work items per call. The FP32 kernel's items are long (about 3 per
+// workgroup slot balance the tail); the BF16 kernel's are about five times
+// shorter, so fewer, larger parts (less partial-state traffic and merge
+// work) measure faster there.
+constexpr long long kSplitItemsF32 = 3072;
+constexpr long long kSplitItemsBf16 = 1536;
 constexpr long long kMinChunkKeys = 1024;
 
 // Work plan (computed on the host, passed by value): query tiles in dispatch
@@ -53,7 +58,7 @@ __host__ __device__ inline int tile_visible_end(int tile, int query_len, int que
 // Builds the plan for `tiles` (<= kMaxTiles) tiles; part sizes are multiples
 // of `align` keys. Returns the number of work items; *slots = partial slots.
 inline int make_plan(Plan &plan, int tiles, int query_len, int query_offset, int image_start, int image_end,
-                     int n_heads, int align, int *slots_out) {
+                     int n_heads, int align, long long target_items, int *slots_out) {
   long long total = 0;
   int vis[kMaxTiles], most = 0;
   for (int t = 0; t < tiles; t++) {
@@ -61,7 +66,7 @@ inline int make_plan(Plan &plan, int tiles, int query_len, int query_offset, int
     total += vis[t];
     most = vis[t] > most ? vis[t] : most;
   }
-  const long long want = total * static_cast<long long>(n_heads) / kSplitItems;
+  const long long want = total * static_cast<long long>(n_heads) / target_items;
   long long chunk = ((want > kMinChunkKeys ? want : kMinChunkKeys) + align - 1) / align * align;
   // Tiles of nearly equal cost (an all-image or short prefill) balance by
   // themselves: splitting them would only add the merge traffic.

@@ -13,8 +13,10 @@
 // Weights are dequantized while staging into LDS; full FP32 weights are
 // never stored in HBM.
 //
-// Roofline: FP32 matrix cores (157.3 TFLOP/s) for mfma_kernel; FP32 VALU
-// without packed math (78.6 TFLOP/s) for chain_kernel. FLOPs = 2*m*k*n.
+// Roofline: FP32 matrix cores (157.3 TFLOP/s) for mfma_kernel; the FP32
+// vector peak (157.3 TFLOP/s: gfx950 issues even non-packed FMAs faster than
+// 16 lanes per clock, measured 114 TFLOP/s for a register-only FMA loop) for
+// the chain kernels. FLOPs = 2*m*k*n.
 #include <type_traits>
 
 #include "focr_internal.hpp"

@@ -221,38 +221,45 @@ __global__ __launch_bounds__(256) void gemm_kernel(const int8_t *__restrict__ a_
   // stride): A RB / 2 x 16 B, B 16 B (column blocks past n repeat the last
   // one: computed and discarded), and 4 B of the steps (waves 0 and 2, 64
   // rows each), of the column sums (wave 1) or of the scales (wave 3).
-  const char *asrc = reinterpret_cast<const char *>(a_tiles) + static_cast<size_t>(mb0) * 2048 + 16 * tid;
+  // Uniform bases (scalar registers, advanced by a group's stride) plus
+  // 32-bit lane offsets, so every copy takes the scalar-base address form.
+  const char *abase = reinterpret_cast<const char *>(a_tiles) + static_cast<size_t>(mb0) * 2048;
+  const uint32_t aoff = 16u * tid;
   const size_t a_stride = static_cast<size_t>(row_blocks) * 2048;
+  const char *bbase = reinterpret_cast<const char *>(b_tiles) + static_cast<size_t>(nb0) * 1024;
   int blk = nb0 + (tid >> 6);
   blk = blk < col_blocks ? blk : col_blocks - 1;
-  const char *bsrc = reinterpret_cast<const char *>(b_tiles) + (static_cast<size_t>(blk) * 64 + lane) * 16;
+  const uint32_t boff = static_cast<uint32_t>((blk - nb0) * 64 + lane) * 16u;
   const size_t b_stride = static_cast<size_t>(col_blocks) * 1024;
   const bool x_copy = (wave & 1) != 0 || 64 * (wave >> 1) < BM;
-  const char *xsrc;
+  const char *xbase;
+  uint32_t xoff;
   size_t x_stride;
   int x_dst;  // byte offset of the wave's 256 B in the stage
   if ((wave & 1) == 0) {
-    xsrc = reinterpret_cast<const char *>(steps + mb0 * 16 + 64 * (wave >> 1) + lane);
+    xbase = reinterpret_cast<const char *>(steps + mb0 * 16 + 64 * (wave >> 1));
+    xoff = 4u * lane;
     x_stride = static_cast<size_t>(m_pad) * sizeof(float);
     x_dst = static_cast<int>(offsetof(Tile, steps)) + 256 * (wave >> 1);
   } else {
     int col = nb0 * 16 + lane;
     col = col < n ? col : n - 1;
     const bool scales = (wave >> 1) != 0;
-    xsrc = scales ? reinterpret_cast<const char *>(sw + col) : reinterpret_cast<const char *>(wsum + col);
+    xbase = scales ? reinterpret_cast<const char *>(sw + nb0 * 16) : reinterpret_cast<const char *>(wsum + nb0 * 16);
+    xoff = 4u * static_cast<uint32_t>(col - nb0 * 16);
     x_stride = static_cast<size_t>(n) * 4;
     x_dst = scales ? static_cast<int>(offsetof(Tile, sw)) : static_cast<int>(offsetof(Tile, wsum));
   }
   auto issue = [&](Tile &t, int g) {
-    const char *ga = asrc + static_cast<size_t>(g) * a_stride;
+    const char *ga = abase + static_cast<size_t>(g) * a_stride;
 #pragma unroll
     for (int i = 0; i < RB / 2; i++)
-      __builtin_amdgcn_global_load_lds((global_void *)(ga + 4096 * i), (lds_void *)(&t.a[64 * wave + 256 * i]), 16, 0,
-                                       0);
-    __builtin_amdgcn_global_load_lds((global_void *)(bsrc + static_cast<size_t>(g) * b_stride),
+      __builtin_amdgcn_global_load_lds((global_void *)((ga + 4096 * i) + aoff), (lds_void *)(&t.a[64 * wave + 256 * i]),
+                                       16, 0, 0);
+    __builtin_amdgcn_global_load_lds((global_void *)(bbase + static_cast<size_t>(g) * b_stride + boff),
                                      (lds_void *)(&t.b[64 * wave]), 16, 0, 0);
     if (x_copy)
-      __builtin_amdgcn_global_load_lds((global_void *)(xsrc + static_cast<size_t>(g) * x_stride),
+      __builtin_amdgcn_global_load_lds((global_void *)(xbase + static_cast<size_t>(g) * x_stride + xoff),
                                        (lds_void *)(reinterpret_cast<char *>(&t) + x_dst), 4, 0, 0);
   };
 

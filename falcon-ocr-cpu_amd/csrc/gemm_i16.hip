@@ -23,8 +23,12 @@
 // previous group is computed from the other; tiles are ordered per XCD so
 // that the workgroups sharing an L2 share operands.
 //
-// Roofline: the i8 matrix cores do 2 x 64 MACs per output and group; the
-// FP32 group epilogue (4 VALU ops per output and group) bounds it in practice.
+// Roofline: the i8 matrix cores do 2 x 64 MACs per output and group, the
+// FP32 group epilogue 4 VALU ops per output and group (shift-add and convert
+// issue at half the FMA rate). Measured, neither bounds it alone: without the
+// epilogue it runs about 25 % faster, without the products about 15 %; the
+// operand copies (L2 -> LDS, about 1 GB per 6544 x 1024 x 4096 call) and the
+// per-group barrier take the rest.
 #include "focr_internal.hpp"
 
 namespace focr {
@@ -32,8 +36,8 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-constexpr int kBM = 128;  // rows padded to a multiple of this (the largest tile)
-constexpr int kBN = 64;   // columns per workgroup tile
+constexpr int kMPad = 128;  // rows padded to a multiple of this
+constexpr int kBM = 64;     // rows per workgroup tile
 
 // One wave per (16-row block, group): lane l owns row l%16, inputs
 // 16*(l/16) .. +16 of the group; the group's absmax is a 4-lane reduction.
@@ -150,15 +154,15 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float *__restrict__
   if (lane < 16) steps[static_cast<size_t>(g) * m_pad + row] = step * scale;
 }
 
-// One group's operands of a BM x 64 tile in LDS, filled by the LDS-DMA path;
+// One group's operands of a 64 x BN tile in LDS, filled by the LDS-DMA path;
 // two stages (the group being computed and the next one).
-template <int BM>
+template <int BN>
 struct GroupTile {
-  uint4 a[BM / 16 * 2 * 64];  // [row blocks][hi, lo][64 lanes] x 16 B
-  uint4 b[kBN / 16 * 64];     // [4 column blocks][64 lanes] x 16 B
-  float steps[BM];            // activation steps of the tile's rows
-  int32_t wsum[kBN];          // 128 * sum of the group's codes per column
-  float sw[kBN];              // weight scales per column
+  uint4 a[kBM / 16 * 2 * 64];  // [4 row blocks][hi, lo][64 lanes] x 16 B
+  uint4 b[BN / 16 * 64];       // [column blocks][64 lanes] x 16 B
+  float steps[kBM];            // activation steps of the tile's rows
+  int32_t wsum[BN];            // 128 * sum of the group's codes per column
+  float sw[BN];                // weight scales per column
 };
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -189,73 +193,76 @@ __device__ __forceinline__ void tile_of(int b, int row_tiles, int col_tiles, int
   rt = panel * kPanel + rem % rows;
 }
 
-// BM x 64 outputs per workgroup; wave (wm, wn) holds BM / 2 rows x 32
-// columns, RW = BM / 32 row blocks x 2 column blocks of 16 x 16.
+// 64 x BN outputs per workgroup of BN / 16 waves; wave (wm, wn) holds 32
+// rows x 32 columns, 2 row blocks x 2 column blocks of 16 x 16. A wider tile
+// moves fewer operand bytes per output (the activation planes are copied once
+// per BN columns, the weights once per 64 rows).
 //
 // Step g: wait for this wave's copies of group g, meet the other waves
 // (nobody still reads the other stage), start group g + 1's copies into it,
 // then compute group g: per block two i8 matrix-core products and the FP32
-// epilogue acc = fma(f32(S), fl(s_w * s_a), acc).
-template <int EPI, int BM>
-__global__ __launch_bounds__(256) void gemm_kernel(const int8_t *__restrict__ a_tiles, const float *__restrict__ steps,
+// epilogue acc = fma(f32(S), fl(s_w * s_a), acc). 128-column tiles hold 8
+// waves; at most 80 VGPRs keep three such workgroups (6 waves per SIMD) on a
+// compute unit.
+template <int EPI, int BN>
+__global__ __launch_bounds__(BN * 4) __attribute__((amdgpu_waves_per_eu(BN == 128 ? 6 : 1)))
+void gemm_kernel(const int8_t *__restrict__ a_tiles, const float *__restrict__ steps,
                                                    const float *__restrict__ exc_inputs, const int8_t *__restrict__ b_tiles,
                                                    const int32_t *__restrict__ wsum, const float *__restrict__ sw,
                                                    const float *__restrict__ exc_vals, int n_exc, int m, int n,
                                                    int groups, int row_blocks, int m_pad, int row_tiles, int col_tiles,
                                                    float *__restrict__ out) {
-  constexpr int RB = BM / 16, RW = RB / 2;
-  typedef GroupTile<BM> Tile;
+  constexpr int RB = kBM / 16, RW = 2, WAVES = BN / 16, THREADS = 64 * WAVES;
+  constexpr int ACP = RB * 2 * 64 / THREADS;  // A copies per thread and group
+  typedef GroupTile<BN> Tile;
   // Two distinct LDS objects (not one array): the compiler then sees that
   // reads of one stage do not alias copies into the other.
   __shared__ Tile ring0, ring1;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / (BN / 32), wn = wave % (BN / 32);
   int rt, ct;
   tile_of(blockIdx.x, row_tiles, col_tiles, rt, ct);
   const int mb0 = rt * RB;
-  const int nb0 = ct * (kBN / 16);
+  const int nb0 = ct * (BN / 16);
   const int col_blocks = n / 16;
 
-  // Sources of this thread's copies per group (advanced by a group's
-  // stride): A RB / 2 x 16 B, B 16 B (column blocks past n repeat the last
-  // one: computed and discarded), and 4 B of the steps (waves 0 and 2, 64
-  // rows each), of the column sums (wave 1) or of the scales (wave 3).
-  // Uniform bases (scalar registers, advanced by a group's stride) plus
-  // 32-bit lane offsets, so every copy takes the scalar-base address form.
+  // Sources of this thread's copies per group, each a uniform base (scalar
+  // registers, advanced by a group's stride) plus a 32-bit lane offset so that
+  // every copy takes the scalar-base address form: ACP x 16 B of the A planes;
+  // 16 B of column block nb0 + wave of B (blocks past n repeat the last one:
+  // computed and discarded); and, for waves 0 .. 2 BN / 64, 4 B of the steps
+  // (wave 0), of the column sums or of the scales (64 columns per wave).
   const char *abase = reinterpret_cast<const char *>(a_tiles) + static_cast<size_t>(mb0) * 2048;
   const uint32_t aoff = 16u * tid;
   const size_t a_stride = static_cast<size_t>(row_blocks) * 2048;
   const char *bbase = reinterpret_cast<const char *>(b_tiles) + static_cast<size_t>(nb0) * 1024;
-  int blk = nb0 + (tid >> 6);
+  int blk = nb0 + wave;
   blk = blk < col_blocks ? blk : col_blocks - 1;
   const uint32_t boff = static_cast<uint32_t>((blk - nb0) * 64 + lane) * 16u;
   const size_t b_stride = static_cast<size_t>(col_blocks) * 1024;
-  const bool x_copy = (wave & 1) != 0 || 64 * (wave >> 1) < BM;
-  const char *xbase;
-  uint32_t xoff;
-  size_t x_stride;
-  int x_dst;  // byte offset of the wave's 256 B in the stage
-  if ((wave & 1) == 0) {
-    xbase = reinterpret_cast<const char *>(steps + mb0 * 16 + 64 * (wave >> 1));
-    xoff = 4u * lane;
-    x_stride = static_cast<size_t>(m_pad) * sizeof(float);
-    x_dst = static_cast<int>(offsetof(Tile, steps)) + 256 * (wave >> 1);
-  } else {
-    int col = nb0 * 16 + lane;
+  constexpr int XP = BN / 64;  // 64-column pieces of the sums and of the scales
+  const bool x_copy = wave <= 2 * XP;
+  const char *xbase = reinterpret_cast<const char *>(steps + mb0 * 16);
+  uint32_t xoff = 4u * lane;
+  size_t x_stride = static_cast<size_t>(m_pad) * sizeof(float);
+  int x_dst = static_cast<int>(offsetof(Tile, steps));  // byte offset of the wave's 256 B in the stage
+  if (wave != 0 && x_copy) {
+    const bool scales = wave > XP;
+    const int piece = scales ? wave - 1 - XP : wave - 1;
+    int col = nb0 * 16 + 64 * piece + lane;
     col = col < n ? col : n - 1;
-    const bool scales = (wave >> 1) != 0;
     xbase = scales ? reinterpret_cast<const char *>(sw + nb0 * 16) : reinterpret_cast<const char *>(wsum + nb0 * 16);
     xoff = 4u * static_cast<uint32_t>(col - nb0 * 16);
     x_stride = static_cast<size_t>(n) * 4;
-    x_dst = scales ? static_cast<int>(offsetof(Tile, sw)) : static_cast<int>(offsetof(Tile, wsum));
+    x_dst = (scales ? static_cast<int>(offsetof(Tile, sw)) : static_cast<int>(offsetof(Tile, wsum))) + 256 * piece;
   }
   auto issue = [&](Tile &t, int g) {
     const char *ga = abase + static_cast<size_t>(g) * a_stride;
 #pragma unroll
-    for (int i = 0; i < RB / 2; i++)
-      __builtin_amdgcn_global_load_lds((global_void *)((ga + 4096 * i) + aoff), (lds_void *)(&t.a[64 * wave + 256 * i]),
-                                       16, 0, 0);
+    for (int i = 0; i < ACP; i++)
+      __builtin_amdgcn_global_load_lds((global_void *)((ga + 16 * THREADS * i) + aoff),
+                                       (lds_void *)(&t.a[64 * wave + THREADS * i]), 16, 0, 0);
     __builtin_amdgcn_global_load_lds((global_void *)(bbase + static_cast<size_t>(g) * b_stride + boff),
                                      (lds_void *)(&t.b[64 * wave]), 16, 0, 0);
     if (x_copy)
@@ -372,7 +379,7 @@ int launch_prefill_i16(Ctx *ctx, const Linear *lin, const float *x, size_t rows,
                        int epilogue, float *out) {
   const size_t m = rows, k = lin->k, n = lin->n, groups = lin->groups;
   FOCR_REQUIRE(m < (size_t(1) << 30) && n % 32 == 0 && k % 64 == 0, FOCR_E_SHAPE, "INT16 panel shape");
-  const size_t m_pad = (m + kBM - 1) / kBM * kBM;
+  const size_t m_pad = (m + kMPad - 1) / kMPad * kMPad;
   const size_t row_blocks = m_pad / 16;
   const size_t a_bytes = m_pad * k * 2;
   const size_t s_bytes = groups * m_pad * sizeof(float);
@@ -389,23 +396,24 @@ int launch_prefill_i16(Ctx *ctx, const Linear *lin, const float *x, size_t rows,
                      row_scale, lin->exc_index, static_cast<int>(lin->n_exc), a_tiles, steps, exc_inputs,
                      static_cast<int>(m_pad));
   FOCR_HIP_CHECK(hipGetLastError());
-#ifndef FOCR_I16_BM
-#define FOCR_I16_BM 64
-#endif
-  constexpr int BM = FOCR_I16_BM;
-  const int row_tiles = static_cast<int>(m_pad / BM), col_tiles = static_cast<int>((n + kBN - 1) / kBN);
-  const dim3 grid(static_cast<unsigned>(row_tiles * col_tiles));
-#define FOCR_LAUNCH_I16(E)                                                                                      \
-  hipLaunchKernelGGL((gemm_kernel<E, BM>), grid, dim3(256), 0, ctx->stream, a_tiles, steps, exc_inputs, lin->i16_b, \
-                     lin->i16_wsum, lin->i16_sw, lin->exc_vals, static_cast<int>(lin->n_exc), static_cast<int>(m), \
-                     static_cast<int>(n), static_cast<int>(groups), static_cast<int>(row_blocks),                \
-                     static_cast<int>(m_pad), row_tiles, col_tiles, out)
-  if (epilogue == FOCR_EPI_GLU)
-    FOCR_LAUNCH_I16(FOCR_EPI_GLU);
-  else if (epilogue == FOCR_EPI_ADD)
-    FOCR_LAUNCH_I16(FOCR_EPI_ADD);
-  else
-    FOCR_LAUNCH_I16(FOCR_EPI_STORE);
+  // 128-column tiles where n gives at least 16 of them (fewer operand bytes
+  // per output: +5 % on 1024 -> 4096), 64-column ones for narrow outputs
+  // (n = 768: the wider tiles leave too few workgroups).
+  const int row_tiles = static_cast<int>(m_pad / kBM);
+#define FOCR_LAUNCH_I16(E, BN)                                                                                    \
+  hipLaunchKernelGGL((gemm_kernel<E, BN>), dim3(static_cast<unsigned>(row_tiles * ((n + BN - 1) / BN))), dim3(BN * 4), \
+                     0, ctx->stream, a_tiles, steps, exc_inputs, lin->i16_b, lin->i16_wsum, lin->i16_sw,             \
+                     lin->exc_vals, static_cast<int>(lin->n_exc), static_cast<int>(m), static_cast<int>(n),          \
+                     static_cast<int>(groups), static_cast<int>(row_blocks), static_cast<int>(m_pad), row_tiles,     \
+                     static_cast<int>((n + BN - 1) / BN), out)
+  const bool wide = n >= 2048;
+  if (epilogue == FOCR_EPI_GLU) {
+    if (wide) FOCR_LAUNCH_I16(FOCR_EPI_GLU, 128); else FOCR_LAUNCH_I16(FOCR_EPI_GLU, 64);
+  } else if (epilogue == FOCR_EPI_ADD) {
+    if (wide) FOCR_LAUNCH_I16(FOCR_EPI_ADD, 128); else FOCR_LAUNCH_I16(FOCR_EPI_ADD, 64);
+  } else {
+    if (wide) FOCR_LAUNCH_I16(FOCR_EPI_STORE, 128); else FOCR_LAUNCH_I16(FOCR_EPI_STORE, 64);
+  }
 #undef FOCR_LAUNCH_I16
   FOCR_HIP_CHECK(hipGetLastError());
   return FOCR_OK;

@@ -339,14 +339,16 @@ def bench_layer(torch, fh, gen, np, steps=64):
 
 def bench_kv(torch, fh, gen, np, reps=30):
     """Decode attention of one query row over one layer's cache, cold (a
-    512 MiB write before every call evicts the Infinity Cache, as a 22-layer
-    cache is evicted between a layer's steps): sealed Q8 records
+    512 MiB read before every call evicts the Infinity Cache, as the other
+    layers' weights and caches do between a layer's steps; a read, so no
+    dirty lines are left for the timed call to write back): sealed Q8 records
     (focr_kv_attention_decode) against the FP32 compact cache
     (focr_attention_decode), at 4,096 / 16,320 / 65,472 prefix positions plus
     64 generated ones. Bytes = the records (176 B per group and prefix
     position, 144 per generated one) or the compact keys and values."""
     heads, kvh, T = 16, 8, 64
-    flush = torch.empty(128 << 20, dtype=torch.float32, device="cuda")
+    flush = torch.ones(128 << 20, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
     res = {}
 
     def cold_us(fn):
@@ -354,7 +356,7 @@ def bench_kv(torch, fh, gen, np, reps=30):
             fn()
         ts = []
         for _ in range(reps):
-            flush.fill_(1.0)
+            flush.sum()
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record()
             fn()
@@ -399,13 +401,13 @@ def bench_screen(torch, fh, gen, np, reps=40):
     one exact greedy selection per call (rows 1 and 5, synchronous, host wall
     time) against the full FP32 head GEMV + argmax. "warm": back-to-back
     calls (the 201 MB FP32 head stays in the 256 MB Infinity Cache); "cold":
-    a 512 MiB write between calls evicts it first, as the other layers'
+    a 512 MiB read between calls evicts it first, as the other layers'
     weights and caches do in a decode step."""
     vocab, dim = 65536, 768
     head = gen.normal((vocab, dim), 0.02, 40)
     screen = fh.ScreenedHead.build(head)
     lin = fh.Linear.from_f32(head)
-    flush = torch.empty(128 << 20, dtype=torch.float32, device="cuda")
+    flush = torch.ones(128 << 20, dtype=torch.float32, device="cuda")
     screen_bytes = vocab * (dim + 4 * (dim // 64))
     res = {"vocab": vocab, "dim": dim, "screen_bytes": screen_bytes, "fp32_head_bytes": vocab * dim * 4}
 
@@ -413,7 +415,7 @@ def bench_screen(torch, fh, gen, np, reps=40):
         t = []
         for _ in range(reps):
             if cold:
-                flush.fill_(1.0)
+                flush.sum()
             torch.cuda.synchronize()
             t0 = time.perf_counter()
             fn()

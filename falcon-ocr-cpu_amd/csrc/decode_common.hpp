@@ -90,22 +90,43 @@ __device__ __forceinline__ float wave_max(float v) {
 
 // One workgroup per (row, head). Thread t takes chunks t, t + 256, ... for
 // the maximum and the weights exp(m_c - M); then lane = dim and wave w sums
-// the outputs of chunks w, w + 4, ...; the partial sums are added in a fixed
-// order. Final step as online.rs head (lines 144-149):
-// lse = max + ln(den), out = (o / den) * 1/(1 + exp(sink - lse)).
-static __global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgs a) {
-  __shared__ float s_f[kMaxChunks];
-  __shared__ float s_red[kWaves], s_o[kWaves][64];
-  const int rh = blockIdx.x, h = rh % a.n_heads;
+// the outputs of chunks w, w + 4, ... in ascending order; the partial sums
+// are added in a fixed order. The (max, den) pairs are read once, and each
+// wave's first 16 output loads are issued with them, before the maximum is
+// known, so the reads overlap instead of following one another. Final step
+// as online.rs head (lines 144-149): lse = max + ln(den),
+// out = (o / den) * 1/(1 + exp(sink - lse)).
+// The work of one (row, head): a workgroup of 256 threads, `sh` its LDS.
+struct CombineShared {
+  float f[kMaxChunks];
+  float red[kWaves], o[kWaves][64];
+};
+__device__ __forceinline__ void combine_row(const CombineArgs &a, int rh, CombineShared &sh) {
+  constexpr int kPer = kMaxChunks / 256;  // (max, den) pairs per thread
+  constexpr int kPre = 16;                // outputs per wave loaded up front
+  float *s_f = sh.f;
+  float *s_red = sh.red;
+  float (*s_o)[64] = sh.o;
+  const int h = rh % a.n_heads;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const float *md = a.part_md + static_cast<size_t>(rh) * a.chunks * 2;
+  const float2 *md = reinterpret_cast<const float2 *>(a.part_md) + static_cast<size_t>(rh) * a.chunks;
   const float *po = a.part_o + static_cast<size_t>(rh) * a.chunks * 64;
   const float ninf = -__builtin_inff();
-  float mx = ninf;
-  for (int c = tid; c < a.chunks; c += 256) {
-    const float mc = md[2 * c];
-    mx = mc > mx ? mc : mx;
+  float2 mdv[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; i++) {
+    const int c = tid + 256 * i;
+    mdv[i] = c < a.chunks ? md[c] : make_float2(ninf, 0.0f);
   }
+  float ov[kPre];
+#pragma unroll
+  for (int i = 0; i < kPre; i++) {
+    const int c = wave + 4 * i;
+    ov[i] = c < a.chunks ? po[static_cast<size_t>(c) * 64 + lane] : 0.0f;
+  }
+  float mx = ninf;
+#pragma unroll
+  for (int i = 0; i < kPer; i++) mx = mdv[i].x > mx ? mdv[i].x : mx;
   mx = wave_max(mx);
   if (lane == 0) s_red[wave] = mx;
   __syncthreads();
@@ -114,43 +135,49 @@ static __global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgs 
   for (int w = 1; w < kWaves; w++) big = s_red[w] > big ? s_red[w] : big;
   __syncthreads();
   float den = 0.0f;
-  for (int c = tid; c < a.chunks; c += 256) {
-    const float mc = md[2 * c];
-    const float f = mc == ninf || big == ninf ? 0.0f : expf_acc(mc - big);
-    s_f[c] = f;
-    den = den + md[2 * c + 1] * f;
+#pragma unroll
+  for (int i = 0; i < kPer; i++) {
+    const int c = tid + 256 * i;
+    if (c < a.chunks) {
+      const float mc = mdv[i].x;
+      const float f = mc == ninf || big == ninf ? 0.0f : expf_acc(mc - big);
+      s_f[c] = f;
+      den = den + mdv[i].y * f;
+    }
   }
   den = wave_sum(den);
   if (lane == 0) s_red[wave] = den;
   __syncthreads();
-  // Sixteen of the wave's chunks load before their products are added (in
-  // chunk order), so the loads' latencies overlap.
   float o = 0.0f;
   int c = wave;
+#pragma unroll
+  for (int i = 0; i < kPre; i++, c += 4)
+    if (c < a.chunks) o = fmaf_(ov[i], s_f[c], o);
+  // The rest, sixteen loads in flight before their products are added (in
+  // chunk order).
   for (; c + 60 < a.chunks; c += 64) {
-    float ov[16];
+    float v[16];
 #pragma unroll
-    for (int i = 0; i < 16; i++) ov[i] = po[static_cast<size_t>(c + 4 * i) * 64 + lane];
+    for (int i = 0; i < 16; i++) v[i] = po[static_cast<size_t>(c + 4 * i) * 64 + lane];
 #pragma unroll
-    for (int i = 0; i < 16; i++) o = fmaf_(ov[i], s_f[c + 4 * i], o);
-  }
-  for (; c + 12 < a.chunks; c += 16) {
-    const float o0 = po[static_cast<size_t>(c) * 64 + lane], o1 = po[static_cast<size_t>(c + 4) * 64 + lane];
-    const float o2 = po[static_cast<size_t>(c + 8) * 64 + lane], o3 = po[static_cast<size_t>(c + 12) * 64 + lane];
-    o = fmaf_(o0, s_f[c], o);
-    o = fmaf_(o1, s_f[c + 4], o);
-    o = fmaf_(o2, s_f[c + 8], o);
-    o = fmaf_(o3, s_f[c + 12], o);
+    for (int i = 0; i < 16; i++) o = fmaf_(v[i], s_f[c + 4 * i], o);
   }
   for (; c < a.chunks; c += 4) o = fmaf_(po[static_cast<size_t>(c) * 64 + lane], s_f[c], o);
   s_o[wave][lane] = o;
   __syncthreads();
-  if (wave != 0) return;
-  const float d = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
-  const float total = (s_o[0][lane] + s_o[1][lane]) + (s_o[2][lane] + s_o[3][lane]);
-  const float lse = big + logf_acc(d);
-  const float sink_scale = __fdiv_rn(1.0f, 1.0f + expf_acc(a.sinks[h] - lse));
-  a.out[static_cast<size_t>(rh) * 64 + lane] = __fdiv_rn(total, d) * sink_scale;
+  if (wave == 0) {
+    const float d = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+    const float total = (s_o[0][lane] + s_o[1][lane]) + (s_o[2][lane] + s_o[3][lane]);
+    const float lse = big + logf_acc(d);
+    const float sink_scale = __fdiv_rn(1.0f, 1.0f + expf_acc(a.sinks[h] - lse));
+    a.out[static_cast<size_t>(rh) * 64 + lane] = __fdiv_rn(total, d) * sink_scale;
+  }
+  __syncthreads();  // the LDS may be reused for the next (row, head)
+}
+
+static __global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgs a) {
+  __shared__ CombineShared sh;
+  combine_row(a, blockIdx.x, sh);
 }
 
 }  // namespace decode

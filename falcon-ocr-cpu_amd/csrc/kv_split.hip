@@ -384,15 +384,47 @@ __device__ __forceinline__ KeyVal load_key(const SplitDecArgs &a, int g, int j, 
   return kv;
 }
 
+// load_key of a prefix record that sits in LDS at `rec`.
+template <typename C>
+__device__ __forceinline__ KeyVal lds_key(const unsigned char *rec, int lp) {
+  const int hi = lp >> 3;
+  const uint4 steps = *reinterpret_cast<const uint4 *>(rec + kRecord * sizeof(C));
+  const float4 c0 = codes4<C>(rec + 4 * lp * sizeof(C));
+  const float4 c1 = codes4<C>(rec + (4 * lp + 32 * hi) * sizeof(C));
+  const float4 cv = codes4<C>(rec + (96 + 4 * lp) * sizeof(C));
+  KeyVal kv;
+  kv.k0 = scale4(c0, step_of(steps, hi));
+  kv.k1 = scale4(c1, step_of(steps, 2 * hi));
+  kv.v = scale4(cv, step_of(steps, 3 + hi));
+  return kv;
+}
+
 constexpr int kKpl = 4;  // keys per lane group per iteration (16 per wave)
+constexpr int kRoundKeys = 16 * kWaves;  // positions per workgroup round
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) const void global_void;
 
 // M: query rows. One workgroup per task (group g, key chunk c) serves heads
-// 2g and 2g + 1: wave w takes the chunk's 16-key iterations w, w + 4, ...,
-// and the four waves' states are merged in a fixed order through LDS.
+// 2g and 2g + 1 in rounds of 64 positions: wave w takes positions 16w ..
+// 16w + 15 of each round, and the four waves' states are merged in a fixed
+// order through LDS. The round's prefix records (contiguous in HBM) are
+// copied to LDS by the LDS-DMA path, 16 bytes per lane, the next round's
+// while the current one is scored; generated keys (the tail) and the padding
+// keys past the last visible one are read from HBM as before.
+template <typename C>
+struct RoundBuf {
+  static constexpr int kCopies = (kRoundKeys * (kRecord * static_cast<int>(sizeof(C)) + 16) + 4095) / 4096;
+  uint4 chunk[256 * kCopies];  // [kCopies][256 threads] x 16 B
+};
+
 template <typename C, int M>
 __global__ __launch_bounds__(256) void split_partial_kernel(SplitDecArgs a, int iters, int rows) {
   __shared__ float4 s_o[kWaves][2][M][16];
   __shared__ float2 s_md[kWaves][2][M];
+  // Two distinct LDS objects, so the compiler sees that reading one does not
+  // wait for the copies into the other.
+  __shared__ RoundBuf<C> rb0, rb1;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int lg = lane >> 4, lp = lane & 15;
   const int task = blockIdx.x;
@@ -421,6 +453,25 @@ __global__ __launch_bounds__(256) void split_partial_kernel(SplitDecArgs a, int 
       den[e][r] = 0.0f;
       o[e][r] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
+  // Round t's copies: chunk q = tid + 256 i of the rows [b, b + 64) of group
+  // g's prefix records (b = key0 + 64 t); chunks past the prefix (or a round
+  // entirely in the tail) copy the group's first chunk instead, into slots
+  // that are never read.
+  constexpr int kCopies = RoundBuf<C>::kCopies;
+  const int rbytes = a.record_bytes;
+  const unsigned char *group_base = a.records + static_cast<size_t>(g) * a.prefix_len * rbytes;
+  auto issue = [&](RoundBuf<C> &dst, int t) {
+    const int b = key0 + kRoundKeys * t;
+    const int in_prefix = a.prefix_len - b;
+    const int valid = in_prefix <= 0 ? 0 : (in_prefix < kRoundKeys ? in_prefix : kRoundKeys) * rbytes;
+    const unsigned char *src = group_base + static_cast<size_t>(in_prefix > 0 ? b : 0) * rbytes;
+#pragma unroll
+    for (int i = 0; i < kCopies; i++) {
+      const int off = (threadIdx.x + 256 * i) * 16;
+      __builtin_amdgcn_global_load_lds((global_void *)(src + (off < valid ? off : 0)),
+                                       (lds_void *)(&dst.chunk[64 * wave + 256 * i]), 16, 0, 0);
+    }
+  };
   auto load = [&](KeyVal (&kb)[kKpl], int it) {
 #pragma unroll
     for (int i = 0; i < kKpl; i++) {
@@ -471,14 +522,38 @@ __global__ __launch_bounds__(256) void split_partial_kernel(SplitDecArgs a, int 
       }
   };
   // iters is a multiple of kWaves: every wave takes iters / kWaves
-  // iterations (two at 16K keys). Single-buffered: the latency is hidden by
-  // the other resident waves, not by registers (double-buffering measured
-  // slower: fewer waves fit).
-  for (int it = wave; it < iters; it += kWaves) {
+  // iterations, one per round. Past the last round the copy repeats it into
+  // the free buffer (no branch around the copies: a branch join would make
+  // the compiler wait for every copy in flight).
+  const int rounds = iters / kWaves;
+  auto round = [&](const RoundBuf<C> &cur, RoundBuf<C> &next, int t) __attribute__((always_inline)) {
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's copies of round t
+    __syncthreads();                     // everyone's copies; nobody still reads `next`
+    issue(next, t + 1 < rounds ? t + 1 : rounds - 1);
+    const int it = kWaves * t + wave, b = key0 + kRoundKeys * t;
     KeyVal kb[kKpl];
-    load(kb, it);
-    consume(kb, it);
+    // A round wholly inside the visible prefix is scored from LDS; the
+    // round that reaches the tail or the last visible key reads HBM. Each
+    // branch consumes its own keys: a key loaded from HBM must not reach
+    // past the join, where waiting for it would also wait for the copies.
+    if (b + kRoundKeys <= a.prefix_len && b + kRoundKeys <= limit) {
+#pragma unroll
+      for (int i = 0; i < kKpl; i++)
+        kb[i] = lds_key<C>(reinterpret_cast<const unsigned char *>(cur.chunk) + (16 * wave + 4 * i + lg) * rbytes, lp);
+      consume(kb, it);
+    } else {
+      load(kb, it);
+      consume(kb, it);
+    }
+  };
+  issue(rb0, 0);
+  int t = 0;
+  for (; t + 2 <= rounds; t += 2) {
+    round(rb0, rb1, t);
+    round(rb1, rb0, t + 1);
   }
+  if (t < rounds) round(rb0, rb1, t);
+  __builtin_amdgcn_s_waitcnt(0x0f70);  // the repeated copies land before LDS is reused
 #pragma unroll
   for (int e = 0; e < 2; e++)
 #pragma unroll
@@ -496,21 +571,22 @@ __global__ __launch_bounds__(256) void split_partial_kernel(SplitDecArgs a, int 
   __syncthreads();
   // Wave w's lanes 16e' + lp merge the four waves for (head e, rows r = w,
   // w + 4): lane group lg < 2 is the head.
-  if (lg >= 2) return;
-  const int e = lg;
+  if (lg < 2) {
+    const int e = lg;
 #pragma unroll
-  for (int r = 0; r < M; r++) {
-    if (r % kWaves != wave) continue;
-    float2 md = s_md[0][e][r];
-    float4 acc = s_o[0][e][r][lp];
+    for (int r = 0; r < M; r++) {
+      if (r % kWaves != wave) continue;
+      float2 md = s_md[0][e][r];
+      float4 acc = s_o[0][e][r][lp];
 #pragma unroll
-    for (int w = 1; w < kWaves; w++) {
-      const float2 md2 = s_md[w][e][r];
-      merge(md.x, md.y, acc, md2.x, md2.y, s_o[w][e][r][lp]);
+      for (int w = 1; w < kWaves; w++) {
+        const float2 md2 = s_md[w][e][r];
+        merge(md.x, md.y, acc, md2.x, md2.y, s_o[w][e][r][lp]);
+      }
+      const size_t slot = (static_cast<size_t>(r) * a.n_heads + 2 * g + e) * a.chunks + c;
+      *reinterpret_cast<float4 *>(a.part_o + slot * 64 + 4 * lp) = acc;
+      if (lp == 0) *reinterpret_cast<float2 *>(a.part_md + slot * 2) = md;
     }
-    const size_t slot = (static_cast<size_t>(r) * a.n_heads + 2 * g + e) * a.chunks + c;
-    *reinterpret_cast<float4 *>(a.part_o + slot * 64 + 4 * lp) = acc;
-    if (lp == 0) *reinterpret_cast<float2 *>(a.part_md + slot * 2) = md;
   }
 }
 

@@ -237,7 +237,8 @@ def bench_layer(torch, fh, gen, np, steps=64):
     16 query / 8 KV heads of 64) prefilled over P = 16,320 rows (image
     [0, 4096)), then `steps` greedy decode steps growing the cache to 16,384,
     first over the compact FP32 cache (Kv::Compact), then over the sealed Q8
-    records (Kv::Q8: the prefill seals the prefix after its attention), then
+    records (Kv::Q8: the prefill seals the prefix after its attention; fast
+    mode's decode exp for Q8, default_fast_exp), then
     with fast mode's BF16 prefill attention as well (`fast_plan`).
     Prefill stages are timed with HIP events (the layer's phase marks); the
     decode steps are captured into one HIP graph and replayed."""
@@ -318,13 +319,14 @@ def bench_layer(torch, fh, gen, np, steps=64):
             _, _, _, _, cache_bytes = layer.split.info()
             kv_bytes = kv * (P * 176 + (avg_total - P) * 144)
         step_bytes = w_bytes + kv_bytes
+        fast_exp = layer.decode_fast_exp
         del g
         layer.free()
         return {"prefill_ms": round(prefill_ms, 3), "prefill_stage_ms": stage_ms,
                 "prefill_tflops": round((proj_flop + attn_flop) / (prefill_ms * 1e-3) / 1e12, 2),
                 "decode_us_per_step": round(decode_ms * 1e3 / steps, 2), "decode_bytes_per_step": int(step_bytes),
                 "decode_gbs": round(step_bytes / (decode_ms * 1e-3 / steps) / 1e9, 1),
-                "cache_bytes": int(cache_bytes)}
+                "cache_bytes": int(cache_bytes), "decode_fast_exp": fast_exp}
 
     res = {"prefill_rows": P, "decode_steps": steps, "prefill_gflop": round((proj_flop + attn_flop) / 1e9, 2)}
     res.update(run(32))
@@ -344,7 +346,9 @@ def bench_kv(torch, fh, gen, np, reps=30):
     dirty lines are left for the timed call to write back): sealed Q8 records
     (focr_kv_attention_decode) against the FP32 compact cache
     (focr_attention_decode), at 4,096 / 16,320 / 65,472 prefix positions plus
-    64 generated ones. Bytes = the records (176 B per group and prefix
+    64 generated ones; the Q8 records with the exact exp and with the fast
+    exp (q8_fast_us: the reference runner's default for Q8 caches in fast
+    mode, default_fast_exp). Bytes = the records (176 B per group and prefix
     position, 144 per generated one) or the compact keys and values."""
     heads, kvh, T = 16, 8, 64
     flush = torch.ones(128 << 20, dtype=torch.float32, device="cuda")
@@ -379,6 +383,8 @@ def bench_kv(torch, fh, gen, np, reps=30):
         split = fh.KvSplit.seal(8, kd, vd, P, P + T, heads, kvh)
         split.append(gk, gv, T)
         q8_us = cold_us(lambda: split.attention_decode(q, 1, sinks, out=out))
+        split.set_fast_exp(True)
+        q8_fast_us = cold_us(lambda: split.attention_decode(q, 1, sinks, out=out))
         split.free()
         vals = torch.cat([vd, gv])
         kv = fh.CompactKv(kd, gk, vals, P, P + T, heads, kvh, 64)
@@ -388,6 +394,8 @@ def bench_kv(torch, fh, gen, np, reps=30):
         f32_bytes = 4 * 64 * (P * heads + T * kvh + (P + T) * kvh)
         res[f"prefix_{P}"] = {"q8_us": round(q8_us, 2), "q8_bytes": q8_bytes,
                               "q8_gbs": round(q8_bytes / (q8_us * 1e-6) / 1e9, 1),
+                              "q8_fast_us": round(q8_fast_us, 2),
+                              "q8_fast_gbs": round(q8_bytes / (q8_fast_us * 1e-6) / 1e9, 1),
                               "compact_us": round(f32_us, 2), "compact_bytes": f32_bytes,
                               "compact_gbs": round(f32_bytes / (f32_us * 1e-6) / 1e9, 1),
                               "speedup": round(f32_us / q8_us, 2)}

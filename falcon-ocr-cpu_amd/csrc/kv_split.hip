@@ -26,7 +26,13 @@
 // lg = lane / 16 takes keys 4i + lg, lane lp = lane % 16 dims 4lp..4lp+3),
 // every lane reading its codes at offsets selected without branches. Online
 // softmax per (head, row), the four waves merged in a fixed order through
-// LDS, then the shared combine kernel. Roofline: HBM; bytes per call = the visible
+// LDS, then the shared combine kernel. With the cache's fast exp
+// (SplitPrefix::with_fast_exp, kv.rs:423; the polynomial exp of the
+// reference's exp_shifted, decode.rs:346-347) the per-key probabilities
+// p = exp(s - max) use the hardware exp2 of log2(e) * x instead of the device
+// libm expf, within a few ulp of the reference's exp_poly; the block rescale
+// and the chunk merge keep expf, as the reference keeps the platform exp
+// there. Roofline: HBM; bytes per call = the visible
 // records (Q8: 176 bytes per group and prefix position, 8 groups = 1,408
 // bytes per position against 6,144 for the FP32 compact cache).
 #include <mutex>
@@ -84,6 +90,7 @@ struct KvSplit {
   unsigned char *tail = nullptr;     // [n_kv][capacity - prefix_len][tail_bytes]
   uint32_t *error = nullptr;         // seal's refusal flags
   size_t device_bytes = 0;
+  bool fast_exp = false;  // SplitPrefix::fast_exp (kv.rs:168-170)
 };
 
 namespace {
@@ -418,7 +425,19 @@ struct RoundBuf {
   uint4 chunk[256 * kCopies];  // [kCopies][256 threads] x 16 B
 };
 
-template <typename C, int M>
+constexpr float kLog2e = 1.44269504088896340736f;
+
+// p = exp(x) for x <= 0: the exact device expf, or with FAST the hardware
+// exp2 (v_exp_f32, 1 ulp) of log2(e) * x.
+template <bool FAST>
+__device__ __forceinline__ float prob_exp(float x) {
+  if constexpr (FAST)
+    return __builtin_amdgcn_exp2f(kLog2e * x);
+  else
+    return expf_acc(x);
+}
+
+template <typename C, int M, bool FAST>
 __global__ __launch_bounds__(256) void split_partial_kernel(SplitDecArgs a, int iters, int rows) {
   __shared__ float4 s_o[kWaves][2][M][16];
   __shared__ float2 s_md[kWaves][2][M];
@@ -513,7 +532,7 @@ __global__ __launch_bounds__(256) void split_partial_kernel(SplitDecArgs a, int 
         m[e][r] = mn;
 #pragma unroll
         for (int i = 0; i < kKpl; i++) {
-          const float p = s[e][i][r] == ninf ? 0.0f : expf_acc(s[e][i][r] - mn);
+          const float p = s[e][i][r] == ninf ? 0.0f : prob_exp<FAST>(s[e][i][r] - mn);
           const float4 v = kb[i].v;
           den[e][r] = den[e][r] + p;
           o[e][r] = make_float4(fmaf_(p, v.x, o[e][r].x), fmaf_(p, v.y, o[e][r].y), fmaf_(p, v.z, o[e][r].z),
@@ -593,7 +612,7 @@ __global__ __launch_bounds__(256) void split_partial_kernel(SplitDecArgs a, int 
 // `fixed` (optional): a caller-provided partial-state buffer of
 // `fixed_bytes` used instead of the context scratch (nothing is allocated).
 template <typename C, int M>
-int launch_split(Ctx *ctx, SplitDecArgs a, int rows, const float *sinks, float *out, float *fixed,
+int launch_split(Ctx *ctx, SplitDecArgs a, int rows, bool fast, const float *sinks, float *out, float *fixed,
                  size_t fixed_bytes) {
   // Keys per workgroup task: about 1024 tasks over the chip (each serves two
   // heads), at most kMaxChunks chunks, whole multiples of 64 keys (every
@@ -620,7 +639,12 @@ int launch_split(Ctx *ctx, SplitDecArgs a, int rows, const float *sinks, float *
     a.part_o = static_cast<float *>(ctx->scratch);
   }
   a.part_md = a.part_o + slots * 64;
-  hipLaunchKernelGGL((split_partial_kernel<C, M>), dim3(a.tasks), dim3(64 * kWaves), 0, ctx->stream, a, iters, rows);
+  if (fast)
+    hipLaunchKernelGGL((split_partial_kernel<C, M, true>), dim3(a.tasks), dim3(64 * kWaves), 0, ctx->stream, a,
+                       iters, rows);
+  else
+    hipLaunchKernelGGL((split_partial_kernel<C, M, false>), dim3(a.tasks), dim3(64 * kWaves), 0, ctx->stream, a,
+                       iters, rows);
   FOCR_HIP_CHECK(hipGetLastError());
   CombineArgs cb;
   cb.part_o = a.part_o;
@@ -636,17 +660,17 @@ int launch_split(Ctx *ctx, SplitDecArgs a, int rows, const float *sinks, float *
 }
 
 template <typename C>
-int launch_split_rows(Ctx *ctx, const SplitDecArgs &a, int rows, const float *sinks, float *out, float *fixed,
-                      size_t fixed_bytes) {
+int launch_split_rows(Ctx *ctx, const SplitDecArgs &a, int rows, bool fast, const float *sinks, float *out,
+                      float *fixed, size_t fixed_bytes) {
   switch (rows) {
-    case 1: return launch_split<C, 1>(ctx, a, rows, sinks, out, fixed, fixed_bytes);
-    case 2: return launch_split<C, 2>(ctx, a, rows, sinks, out, fixed, fixed_bytes);
-    case 3: return launch_split<C, 3>(ctx, a, rows, sinks, out, fixed, fixed_bytes);
-    case 4: return launch_split<C, 4>(ctx, a, rows, sinks, out, fixed, fixed_bytes);
-    case 5: return launch_split<C, 5>(ctx, a, rows, sinks, out, fixed, fixed_bytes);
-    case 6: return launch_split<C, 6>(ctx, a, rows, sinks, out, fixed, fixed_bytes);
-    case 7: return launch_split<C, 7>(ctx, a, rows, sinks, out, fixed, fixed_bytes);
-    default: return launch_split<C, 8>(ctx, a, rows, sinks, out, fixed, fixed_bytes);
+    case 1: return launch_split<C, 1>(ctx, a, rows, fast, sinks, out, fixed, fixed_bytes);
+    case 2: return launch_split<C, 2>(ctx, a, rows, fast, sinks, out, fixed, fixed_bytes);
+    case 3: return launch_split<C, 3>(ctx, a, rows, fast, sinks, out, fixed, fixed_bytes);
+    case 4: return launch_split<C, 4>(ctx, a, rows, fast, sinks, out, fixed, fixed_bytes);
+    case 5: return launch_split<C, 5>(ctx, a, rows, fast, sinks, out, fixed, fixed_bytes);
+    case 6: return launch_split<C, 6>(ctx, a, rows, fast, sinks, out, fixed, fixed_bytes);
+    case 7: return launch_split<C, 7>(ctx, a, rows, fast, sinks, out, fixed, fixed_bytes);
+    default: return launch_split<C, 8>(ctx, a, rows, fast, sinks, out, fixed, fixed_bytes);
   }
 }
 
@@ -784,8 +808,8 @@ int focr_kv_attention_decode(focr_ctx *handle, const focr_kv_split *kv, const fl
   FOCR_HIP_CHECK(hipSetDevice(ctx->device));
   const SplitDecArgs a = split_args(s, q);
   const int r = static_cast<int>(rows);
-  return s->bits == 8 ? launch_split_rows<int8_t>(ctx, a, r, sinks, out, nullptr, 0)
-                      : launch_split_rows<int16_t>(ctx, a, r, sinks, out, nullptr, 0);
+  return s->bits == 8 ? launch_split_rows<int8_t>(ctx, a, r, s->fast_exp, sinks, out, nullptr, 0)
+                      : launch_split_rows<int16_t>(ctx, a, r, s->fast_exp, sinks, out, nullptr, 0);
 }
 
 int focr_kv_attention_decode_noalloc(focr_ctx *handle, const focr_kv_split *kv, const float *q, size_t rows,
@@ -800,8 +824,8 @@ int focr_kv_attention_decode_noalloc(focr_ctx *handle, const focr_kv_split *kv, 
   FOCR_REQUIRE(fixed, FOCR_E_HIP, "the no-alloc scratch of this device was not resolved (focr_ctx_create does it)");
   const SplitDecArgs a = split_args(s, q);
   const int r = static_cast<int>(rows);
-  return s->bits == 8 ? launch_split_rows<int8_t>(ctx, a, r, sinks, out, fixed, kNoAllocScratchBytes)
-                      : launch_split_rows<int16_t>(ctx, a, r, sinks, out, fixed, kNoAllocScratchBytes);
+  return s->bits == 8 ? launch_split_rows<int8_t>(ctx, a, r, s->fast_exp, sinks, out, fixed, kNoAllocScratchBytes)
+                      : launch_split_rows<int16_t>(ctx, a, r, s->fast_exp, sinks, out, fixed, kNoAllocScratchBytes);
 }
 
 int focr_kv_dequantize(focr_ctx *handle, const focr_kv_split *kv, float *prefix_k, float *values, float *generated_k) {
@@ -840,6 +864,20 @@ int focr_kv_info(const focr_kv_split *kv, int *bits, size_t *prefix_len, size_t 
   if (tail_len) *tail_len = s->tail_len;
   if (capacity) *capacity = s->capacity;
   if (device_bytes) *device_bytes = s->device_bytes;
+  return FOCR_OK;
+}
+
+int focr_kv_set_fast_exp(focr_kv_split *kv, int fast) {
+  KvSplit *s = reinterpret_cast<KvSplit *>(kv);
+  FOCR_REQUIRE(s, FOCR_E_ARG, "focr_kv_set_fast_exp: null cache");
+  s->fast_exp = fast != 0;
+  return FOCR_OK;
+}
+
+int focr_kv_fast_exp(const focr_kv_split *kv, int *fast) {
+  const KvSplit *s = reinterpret_cast<const KvSplit *>(kv);
+  FOCR_REQUIRE(s && fast, FOCR_E_ARG, "focr_kv_fast_exp: null argument");
+  *fast = s->fast_exp ? 1 : 0;
   return FOCR_OK;
 }
 

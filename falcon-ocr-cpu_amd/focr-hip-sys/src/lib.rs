@@ -281,6 +281,8 @@ extern "C" {
         generated_k_dev: *mut f32,
     ) -> c_int;
     pub fn focr_kv_truncate_tail(kv: *mut focr_kv_split, tail_len: usize) -> c_int;
+    pub fn focr_kv_set_fast_exp(kv: *mut focr_kv_split, fast: c_int) -> c_int;
+    pub fn focr_kv_fast_exp(kv: *const focr_kv_split, fast: *mut c_int) -> c_int;
     pub fn focr_kv_info(
         kv: *const focr_kv_split,
         bits: *mut c_int,

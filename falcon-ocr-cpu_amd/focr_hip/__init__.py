@@ -82,6 +82,8 @@ SIGNATURES = {
     "focr_kv_attention_decode_noalloc": (_I, [_P, _P, _P, _Z, _P, _P]),
     "focr_kv_dequantize": (_I, [_P, _P, _P, _P, _P]),
     "focr_kv_truncate_tail": (_I, [_P, _Z]),
+    "focr_kv_set_fast_exp": (_I, [_P, _I]),
+    "focr_kv_fast_exp": (_I, [_P, _P]),
     "focr_kv_qkv_rows": (_I, [_P, _P, _P, _Z, _P, _P]),
     "focr_kv_info": (_I, [_P, _P, _P, _P, _P, _P]),
     "focr_kv_free": (_I, [_P]),
@@ -483,6 +485,15 @@ def argmax(logits, rows: int, vocab: int, ctx: Optional[Context] = None):
     return list(tokens)
 
 
+def default_fast_exp(kv_bits: int, fast_exps: bool, requested: Optional[bool] = None) -> bool:
+    """`default_fast_exp` (src/quant/kv.rs:176-184): the fast decode exp for
+    8-bit records when the run allows fast exps (ExpMode::FAST), the exact one
+    otherwise; `requested` (`Tuning::decode_fast_exp`) overrides it."""
+    if requested is not None:
+        return bool(requested)
+    return bool(fast_exps) and kv_bits == 8
+
+
 class KvSplit:
     """`SplitPrefix` (src/quant/kv.rs) for `Kv::Q8` (bits 8) and `Kv::Q16`
     (bits 16): the sealed prefix records and the generated tail, on the device."""
@@ -528,6 +539,19 @@ class KvSplit:
         _check(lib().focr_kv_attention_decode_noalloc(self.ctx.handle, self.handle, _dev(q), rows, _dev(sinks),
                                                       _dev(out)))
         return out
+
+    def set_fast_exp(self, fast: bool) -> "KvSplit":
+        """`with_fast_exp` (kv.rs:423): the decode softmax's per-key
+        probabilities use the hardware exp2 (the reference's polynomial exp)."""
+        _check(lib().focr_kv_set_fast_exp(self.handle, int(bool(fast))))
+        return self
+
+    @property
+    def fast_exp(self) -> bool:
+        """`SplitPrefix::fast_exp` (kv/record_bits.rs:6-8)."""
+        f = ctypes.c_int()
+        _check(lib().focr_kv_fast_exp(self.handle, ctypes.byref(f)))
+        return bool(f.value)
 
     def truncate_tail(self, tail_len: int) -> None:
         """`truncate_tail`: forget the generated positions past `tail_len`."""

@@ -32,7 +32,11 @@ KV head) lives in device memory sized for `capacity` positions, as
 attention (``seal_layer``, model/cache.rs:218-276) into a `KvSplit`, and decode
 appends each step's keys and values to its tail and attends over the records
 (``LayerCache::Split``); ``kv_bits`` 32 keeps the compact FP32 cache
-(Kv::Compact). ``bf16_attention`` runs the prefill attention in BF16 as the
+(Kv::Compact). The sealed cache's decode exp follows ``default_fast_exp``
+(kv.rs:182-184, applied in seal_layer, model/cache.rs:260-264): the fast exp
+for Q8 records when ``options.exp`` is ExpMode.FAST, the exact one otherwise;
+``decode_fast_exp`` overrides it as ``Tuning::decode_fast_exp`` does.
+``bf16_attention`` runs the prefill attention in BF16 as the
 fast mode's plan does (``PrefillAttention::Bf16`` / ``Bf16Static`` by
 ``options.softmax``). RoPE factors
 come from the caller ([rows][n_heads][32][2] cos/sin pairs), as
@@ -45,15 +49,16 @@ from __future__ import annotations
 
 from typing import Optional
 
-from . import (CompactKv, Context, Epilogue, FocrError, Geometry, KvSplit, PrefillOptions, PrefillProjection, Softmax,
-               attention_prefill_bf16, attention_with, default_context, qkv_rows, row_scales)
+from . import (CompactKv, Context, Epilogue, ExpMode, FocrError, Geometry, KvSplit, PrefillOptions, PrefillProjection,
+               Softmax, attention_prefill_bf16, attention_with, default_context, default_fast_exp, qkv_rows,
+               row_scales)
 
 
 class DecoderLayer:
     def __init__(self, qkv, wo, w13, w2, sinks, capacity: int, n_heads: int = 16, n_kv_heads: int = 8,
                  head_dim: int = 64, projection: PrefillProjection = PrefillProjection.I16,
                  options: PrefillOptions = PrefillOptions(), ctx: Optional[Context] = None, kv_bits: int = 32,
-                 bf16_attention: bool = False):
+                 bf16_attention: bool = False, decode_fast_exp: Optional[bool] = None):
         import torch
 
         self.ctx = ctx or default_context()
@@ -72,6 +77,7 @@ class DecoderLayer:
         self.capacity = capacity
         self.kv_bits = kv_bits
         self.bf16_attention = bf16_attention
+        self.decode_fast_exp = default_fast_exp(kv_bits, options.exp == ExpMode.FAST, decode_fast_exp)
         self.split: Optional[KvSplit] = None
         dev = f"cuda:{self.ctx.device}"
         f32 = torch.float32
@@ -146,7 +152,7 @@ class DecoderLayer:
         mark("attention")
         if self.kv_bits != 32:
             self.split = KvSplit.seal(self.kv_bits, self.prefix_k[:rows], self.v[:rows], rows, self.capacity,
-                                      self.n_heads, self.n_kv_heads, ctx=ctx)
+                                      self.n_heads, self.n_kv_heads, ctx=ctx).set_fast_exp(self.decode_fast_exp)
             mark("seal")
         if panel:
             self.wo.prefill(attn, rows, epilogue=Epilogue.ADD, out=h, kernel=self.projection)

@@ -308,6 +308,16 @@ int focr_kv_dequantize(focr_ctx *ctx, const focr_kv_split *kv, float *prefix_k_d
  * cache.rs:281-298); the next append overwrites them. Host state only, no
  * device work. FOCR_E_SHAPE if tail_len exceeds the stored tail. */
 int focr_kv_truncate_tail(focr_kv_split *kv, size_t tail_len);
+/* SplitPrefix::with_fast_exp (src/quant/kv.rs:423-426): fast != 0 makes the
+ * decode softmax's per-key probabilities exp(s - max) use the hardware exp2
+ * of log2(e) * x (the reference's polynomial exp_poly there, decode.rs:
+ * 346-347), within a few ulp of the exact expf; the rescale and the chunk
+ * merge stay exact. Off after focr_kv_seal, as SplitPrefix::from_compact
+ * leaves it (kv.rs:415); the reference's runner turns it on for Kv::Q8 in
+ * fast mode (default_fast_exp, kv.rs:182-184). Host state only. */
+int focr_kv_set_fast_exp(focr_kv_split *kv, int fast);
+/* SplitPrefix::fast_exp (src/quant/kv/record_bits.rs:6-8): *fast = 0 or 1. */
+int focr_kv_fast_exp(const focr_kv_split *kv, int *fast);
 int focr_kv_info(const focr_kv_split *kv, int *bits, size_t *prefix_len, size_t *tail_len,
                  size_t *capacity, size_t *device_bytes);
 int focr_kv_free(focr_kv_split *kv);

@@ -902,8 +902,13 @@ void orc_qkv_rows(const float *qkv, size_t rows, const float *rope, size_t n_hea
 /* online::head (src/kernels/attention/online.rs:96-150) with the 64-wide
  * simd::dot / simd::axpy (src/simd.rs:749-777,925-940) and the platform expf
  * and logf, for query qh = query * n_heads + head. */
+/* exp_fast: the per-key probabilities exp(s - max) by exp_poly, as the
+ * sealed cache's decode with SplitPrefix::fast_exp (its exp_shifted through
+ * simd::Avx2Fast, src/quant/kv/decode.rs:346-347, src/simd.rs:440-445); the
+ * rescale and the sink keep the platform exp. */
 static void decode_head(const float *q, const Cache *cache, size_t query_offset, size_t image_start,
-                        size_t image_end, size_t query, size_t head, const float *sinks, float *out) {
+                        size_t image_end, size_t query, size_t head, const float *sinks, int exp_fast,
+                        float *out) {
     const float scale = 1.0f / sqrtf((float)HD);
     size_t repeat = cache->n_heads / cache->n_kv_heads, kv_head = head / repeat;
     size_t absolute = query_offset + query;
@@ -923,7 +928,8 @@ static void decode_head(const float *q, const Cache *cache, size_t query_offset,
         float rescale = running_max == -INFINITY ? 0.0f : expf(running_max - new_max);
         for (int d = 0; d < HD; d++) out[d] *= rescale;
         denominator *= rescale;
-        for (size_t j = 0; j < len; j++) logits[j] = expf(logits[j] - new_max);
+        for (size_t j = 0; j < len; j++)
+            logits[j] = exp_fast ? orc_exp_poly(logits[j] - new_max) : expf(logits[j] - new_max);
         for (size_t j = 0; j < len; j++) {
             float p = logits[j];
             const float *value = cache_value(cache, start + j, kv_head);
@@ -937,13 +943,21 @@ static void decode_head(const float *q, const Cache *cache, size_t query_offset,
     for (int d = 0; d < HD; d++) out[d] = (out[d] / denominator) * sink_scale;
 }
 
-void orc_attention_decode(const float *q, const float *prefix_k, const float *generated_k, const float *v,
-                          size_t query_len, size_t prefix_len, size_t total_len, size_t n_heads,
-                          size_t n_kv_heads, size_t query_offset, size_t image_start, size_t image_end,
-                          const float *sinks, float *out) {
+void orc_attention_decode_ex(const float *q, const float *prefix_k, const float *generated_k, const float *v,
+                             size_t query_len, size_t prefix_len, size_t total_len, size_t n_heads,
+                             size_t n_kv_heads, size_t query_offset, size_t image_start, size_t image_end,
+                             const float *sinks, int exp_fast, float *out) {
     Cache cache = {prefix_k, generated_k, v, prefix_len, total_len, n_heads, n_kv_heads};
 #pragma omp parallel for schedule(static)
     for (long qh = 0; qh < (long)(query_len * n_heads); qh++)
         decode_head(q, &cache, query_offset, image_start, image_end, (size_t)qh / n_heads, (size_t)qh % n_heads,
-                    sinks, out + (size_t)qh * HD);
+                    sinks, exp_fast, out + (size_t)qh * HD);
+}
+
+void orc_attention_decode(const float *q, const float *prefix_k, const float *generated_k, const float *v,
+                          size_t query_len, size_t prefix_len, size_t total_len, size_t n_heads,
+                          size_t n_kv_heads, size_t query_offset, size_t image_start, size_t image_end,
+                          const float *sinks, float *out) {
+    orc_attention_decode_ex(q, prefix_k, generated_k, v, query_len, prefix_len, total_len, n_heads, n_kv_heads,
+                            query_offset, image_start, image_end, sinks, 0, out);
 }

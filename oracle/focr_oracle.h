@@ -152,6 +152,14 @@ void orc_attention_decode(const float *q, const float *prefix_k, const float *ge
                           size_t query_len, size_t prefix_len, size_t total_len, size_t n_heads,
                           size_t n_kv_heads, size_t query_offset, size_t image_start, size_t image_end,
                           const float *sinks, float *out);
+/* orc_attention_decode; exp_fast = 1 takes the per-key probabilities
+ * exp(s - max) from orc_exp_poly, as the sealed cache's decode does with
+ * SplitPrefix::fast_exp (src/quant/kv/decode.rs:346-347 through
+ * simd::Avx2Fast, src/simd.rs:440-445); the rescale and the sink stay expf. */
+void orc_attention_decode_ex(const float *q, const float *prefix_k, const float *generated_k, const float *v,
+                             size_t query_len, size_t prefix_len, size_t total_len, size_t n_heads,
+                             size_t n_kv_heads, size_t query_offset, size_t image_start, size_t image_end,
+                             const float *sinks, int exp_fast, float *out);
 
 /* ---- A9: greedy selection --------------------------------------------- */
 /* argmax, src/runner/mod.rs:916-930. 0 ok, -1 on non-finite/empty. */

@@ -105,6 +105,7 @@ _sig("orc_kv_push", None, _I, _P, _P, _Z, _Z, _Z, _P, _P)
 _sig("orc_kv_dequantize", None, _I, _P, _P, _Z, _Z, _Z, _P, _P, _Z, _Z, _P, _P, _P)
 _sig("orc_qkv_rows", None, _P, _Z, _P, _Z, _Z, _Z, _P, _P, _P, _P)
 _sig("orc_attention_decode", None, _P, _P, _P, _P, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _P, _P)
+_sig("orc_attention_decode_ex", None, _P, _P, _P, _P, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _P, _I, _P)
 _sig("orc_set_threads", None, _I)
 _sig("orc_get_threads", _I)
 
@@ -358,14 +359,17 @@ def qkv_rows(qkv, rows, rope, n_heads, n_kv_heads, prefix_rows):
 
 
 def attention_decode(q, prefix_k, generated_k, v, query_len, prefix_len, total_len, n_heads, n_kv_heads,
-                     query_offset, image_start, image_end, sinks):
-    """online::head (src/kernels/attention/online.rs:96-150) for every (query, head)."""
+                     query_offset, image_start, image_end, sinks, exp_fast=False):
+    """online::head (src/kernels/attention/online.rs:96-150) for every (query, head).
+    exp_fast: the per-key probabilities by exp_poly, as the sealed cache's
+    decode with SplitPrefix::fast_exp (src/quant/kv/decode.rs:346-347)."""
     q, v, sinks = _f32(q), _f32(v), _f32(sinks)
     pk = _f32(prefix_k) if prefix_len else None
     gk = _f32(generated_k) if total_len > prefix_len else None
     out = np.zeros(query_len * n_heads * 64, dtype=np.float32)
-    _lib.orc_attention_decode(_ptr(q), _ptr(pk), _ptr(gk), _ptr(v), query_len, prefix_len, total_len, n_heads,
-                              n_kv_heads, query_offset, image_start, image_end, _ptr(sinks), _ptr(out))
+    _lib.orc_attention_decode_ex(_ptr(q), _ptr(pk), _ptr(gk), _ptr(v), query_len, prefix_len, total_len, n_heads,
+                                 n_kv_heads, query_offset, image_start, image_end, _ptr(sinks), int(exp_fast),
+                                 _ptr(out))
     return out.reshape(query_len, n_heads, 64)
 
 

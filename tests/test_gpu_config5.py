@@ -146,7 +146,9 @@ def test_config5_layer_prefill_then_64_decode_steps(kv_bits):
             assert_bitwise(host(layer.v[pos:pos + 1]), new_v, f"step {step} value")
             gk = np.concatenate([gk, new_k])
             v = np.concatenate([v, new_v])
-        want_attn = oracle.attention_decode(q, pk, gk, v, 1, PREFIX, pos + 1, H, G, pos, *IMAGE, sinks)
+        # Fast mode's Q8 records decode with the fast exp (default_fast_exp).
+        want_attn = oracle.attention_decode(q, pk, gk, v, 1, PREFIX, pos + 1, H, G, pos, *IMAGE, sinks,
+                                            exp_fast=kv_bits == 8)
         got_attn = host(layer._buf("dattn", (1, H, 64)))
         close(got_attn, want_attn)
         got_x = host(x)

@@ -3,7 +3,9 @@ decoded prefix and tail are bit for bit the oracle's records (Kv::Q8 and
 Kv::Q16), the refusals are the reference's, and decode attention over the
 records is within FP32 rounding of the compact decode oracle over the decoded
 values (src/quant/kv.rs; kv.rs:7-17: decode over records is the compact
-kernel over their decoded values)."""
+kernel over their decoded values). With the cache's fast exp
+(SplitPrefix::with_fast_exp) the oracle takes the per-key probabilities from
+its exp_poly, as the reference's decode does, and the bound is the same."""
 import numpy as np
 import pytest
 
@@ -80,21 +82,26 @@ def test_refusals(fh):
     kv.free()
 
 
+@pytest.mark.parametrize("fast", [False, True])
 @pytest.mark.parametrize("bits", [8, 16])
 @pytest.mark.parametrize("prefix_len,tail,rows", [(64, 1, 1), (700, 3, 3), (2000, 8, 8), (129, 5, 2)])
-def test_decode_within_fp32_rounding_of_the_compact_oracle(fh, bits, prefix_len, tail, rows):
+def test_decode_within_fp32_rounding_of_the_compact_oracle(fh, bits, prefix_len, tail, rows, fast):
     k, v = pair_cache(prefix_len, N_KV, 31)
     cap = prefix_len + 16
     tk = gen.normal((tail, N_KV, 64), 1.0, 32)
     tv = gen.normal((tail, N_KV, 64), 1.0, 33)
     kv = fh.KvSplit.seal(bits, to_dev(k), to_dev(v), prefix_len, cap, N_HEADS, N_KV)
     kv.append(to_dev(tk), to_dev(tv), tail)
+    assert kv.fast_exp is False  # SplitPrefix::from_compact leaves it off
+    kv.set_fast_exp(fast)
+    assert kv.fast_exp is fast
     q = gen.normal((rows, N_HEADS, 64), 1.0, 34)
     sinks = gen.uniform(N_HEADS, -2.0, 2.0, 35)
     got = host(kv.attention_decode(to_dev(q), rows, to_dev(sinks)))
     pk, vals, gk = oracle_cache(bits, k, v, prefix_len, tk, tv, cap)
     total = prefix_len + tail
-    want = oracle.attention_decode(q, pk, gk, vals, rows, prefix_len, total, N_HEADS, N_KV, total - rows, 0, 0, sinks)
+    want = oracle.attention_decode(q, pk, gk, vals, rows, prefix_len, total, N_HEADS, N_KV, total - rows, 0, 0, sinks,
+                                   exp_fast=fast)
     assert np.all(np.isfinite(got))
     assert max_rel(got, want) <= 1e-5
     assert np.all(np.abs(got - want) <= 1e-5 * (1 + np.abs(want)))
@@ -103,18 +110,20 @@ def test_decode_within_fp32_rounding_of_the_compact_oracle(fh, bits, prefix_len,
 
 def test_config5_decode_over_q8_records(fh):
     # BASELINE config 5's decode: a 16,320-row prefix, 64 generated
-    # positions, one query row at 16,384 (sampled against the oracle).
+    # positions, one query row at 16,384 (sampled against the oracle), with
+    # the fast exp the reference's runner gives Q8 caches in fast mode.
     P, T = 16320, 64
     k, v = pair_cache(P, N_KV, 41)
     tk = gen.normal((T, N_KV, 64), 1.0, 42)
     tv = gen.normal((T, N_KV, 64), 1.0, 43)
     kv = fh.KvSplit.seal(8, to_dev(k), to_dev(v), P, P + T, N_HEADS, N_KV)
     kv.append(to_dev(tk), to_dev(tv), T)
+    kv.set_fast_exp(fh.default_fast_exp(8, True))
     q = gen.normal((1, N_HEADS, 64), 1.0, 44)
     sinks = gen.uniform(N_HEADS, -2.0, 2.0, 45)
     got = host(kv.attention_decode(to_dev(q), 1, to_dev(sinks)))
     pk, vals, gk = oracle_cache(8, k, v, P, tk, tv, P + T)
-    want = oracle.attention_decode(q, pk, gk, vals, 1, P, P + T, N_HEADS, N_KV, P + T - 1, 0, 0, sinks)
+    want = oracle.attention_decode(q, pk, gk, vals, 1, P, P + T, N_HEADS, N_KV, P + T - 1, 0, 0, sinks, exp_fast=True)
     assert max_rel(got, want) <= 1e-5
     bits, plen, tlen, cap, nbytes = kv.info()
     assert (bits, plen, tlen) == (8, P, T) and nbytes == N_KV * (P * 176 + T * 144)

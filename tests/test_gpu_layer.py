@@ -357,8 +357,10 @@ def test_decoder_layer_over_the_sealed_cache(fh, bits):
         tail_len += m
         pk, vals, gk = oracle.kv_dequantize(bits, sealed, rows, H, G, tail, cap - rows, tail_len)
         total = rows + tail_len
+        # default_fast_exp: fast mode gives Q8 records the fast decode exp.
+        assert layer.split.fast_exp is (bits == 8)
         want_attn = oracle.attention_decode(q, pk, gk, vals, m, rows, total, H, G, total - m, image[0], image[1],
-                                            sinks)
+                                            sinks, exp_fast=bits == 8)
         close(host(layer._buf("dattn", (m, H, 64))), want_attn)
         want_x = x0 + dec("wo", want_attn.reshape(m, -1), m)
         gated = dec("w13", want_x * oracle.row_scales(want_x, DIM)[:, None], m, glu=True)

@@ -154,6 +154,51 @@ def test_decode_compact_equals_expanded(n_kv):
     np.testing.assert_array_equal(got.view(np.uint32), expanded.view(np.uint32))
 
 
+@pytest.mark.parametrize("total,prefix,rows,offset,image", [
+    (17, 9, 1, 16, (1, 8)), (161, 129, 3, 60, (1, 128)), (300, 200, 4, 296, (0, 150))])
+def test_fast_exp_decode_against_f64(total, prefix, rows, offset, image):
+    # SplitPrefix::fast_exp changes the per-key exps only: same bound as exact.
+    q, pk, gk, v, sinks, exact = decode_case(total, prefix, rows, offset, image, total)
+    fast = oracle.attention_decode(q, pk, gk, v, rows, prefix, total, H, G, offset, image[0], image[1], sinks,
+                                   exp_fast=True)
+    want = f64_decode(q, pk, gk, v, rows, prefix, total, offset, image, sinks)
+    assert np.all(np.abs(fast - want) <= 1e-5 * (1.0 + np.abs(want)))
+    assert not np.array_equal(fast.view(np.uint32), exact.view(np.uint32))  # the switch does something
+
+
+def fma32(a, b, c):
+    """fl32(a * b + c) for float32 operands whose exact sum f64 holds."""
+    return np.float32(float(a) * float(b) + float(c))
+
+
+def test_fast_exp_decode_two_key_closed_form():
+    # Two keys with scores 0 and x < 0 (one-hot q and k), sinks -1000 (scale
+    # exactly 1), integer values: p0 = exp(0), p1 = exp_poly(x), out =
+    # fma(p1, v1, p0 * v0) / (p0 + p1). The exact path takes expf(x) instead.
+    xs = np.array([-0.3711, -1.0, -2.5, -0.0625, -7.75, -13.0, -0.9, -4.1, -0.01, -20.5, -3.3, -1.7, -0.55, -6.2,
+                   -11.9, -2.05], np.float32)
+    q = np.zeros((1, H, 64), np.float32)
+    q[0, :, 0] = 8.0
+    pk = np.zeros((2, H, 64), np.float32)
+    pk[1, :, 0] = xs
+    v = gen.uniform((2, G, 64), -8.0, 8.0, 7).round().astype(np.float32)
+    sinks = np.full(H, -1000.0, np.float32)
+    for exp_fast in (True, False):
+        got = oracle.attention_decode(q, pk, None, v, 1, 2, 2, H, G, 1, 0, 0, sinks, exp_fast=exp_fast)
+        for h in range(H):
+            x = np.float32(np.float32(xs[h] * np.float32(8.0)) * np.float32(0.125))
+            assert x == xs[h]
+            p0 = np.float32(oracle.exp_poly(0.0)) if exp_fast else np.float32(1.0)
+            p1 = np.float32(oracle.exp_poly(float(x))) if exp_fast else np.float32(math.exp(float(x)))
+            den = np.float32(p0 + p1)
+            for d in range(64):
+                o = fma32(p1, v[1, h // 2, d], np.float32(p0 * v[0, h // 2, d]))
+                assert got[0, h, d] == np.float32(o / den), (exp_fast, h, d)
+    assert oracle.exp_poly(0.0) == 1.0
+    # Some of these inputs separate exp_poly from expf, so the two paths differ.
+    assert any(np.float32(oracle.exp_poly(float(x))) != np.float32(math.exp(float(x))) for x in xs)
+
+
 def test_decode_single_key_closed_form():
     # One visible key: p = 1, den = 1, lse = s, out = v / (1 + exp(sink - s)).
     q = gen.att_values(H * 64, 3, 0.5).reshape(1, H, 64)

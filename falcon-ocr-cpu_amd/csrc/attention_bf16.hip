@@ -51,6 +51,8 @@ namespace {
 
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float float2v __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(1))) const void global_void;
 
@@ -59,14 +61,14 @@ constexpr int kKeys = 32;       // per tile
 constexpr int kTileBytes = 4096;  // one BF16 K or V tile
 constexpr float kLog2e = 1.44269504088896340736f;
 
-// Two FP32 values to one BF16 pair (round to nearest even; v_cvt_pk_bf16_f32).
+// Two FP32 values to one BF16 pair (round to nearest even): the compiler
+// emits v_cvt_pk_bf16_f32 and, unlike for the same instruction written as
+// inline assembly, keeps the wait state that a VALU read of a just-written
+// v_exp_f32 result needs on gfx950 (without it the pair is read stale).
 __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
-  uint32_t u;
-  asm volatile("v_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(u) : "v"(lo), "v"(hi));
-  return u;
+  const float2v f = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
 }
-__device__ __forceinline__ float bf16_lo(uint32_t u) { return __uint_as_float(u << 16); }
-__device__ __forceinline__ float bf16_hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
 
 // exp2_lanes (bf16/static_shift.rs:277-289): n = round-to-even(t), f = t - n
 // (exact), the minimax in f by FMA from the top (the reference's
@@ -410,20 +412,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void a
     }
     Bf16x8 pb[2][2];
     if constexpr (STATIC) {
-      // p = 2^(log2(e) * s), masked +0; denominators add the rounded p.
+      // p = 2^(log2(e) * s), masked +0 (only tiles with hidden keys hold
+      // -inf scores); the denominators add the rounded p a pair at a time
+      // (v_dot2 of the packed pair with (1, 1)).
       float psum[2] = {0.0f, 0.0f};
+      const bf16x2 ones = __builtin_bit_cast(bf16x2, 0x3F803F80u);
+      auto probs = [&](bool masked) __attribute__((always_inline)) {
 #pragma unroll
-      for (int t = 0; t < 2; t++)
+        for (int t = 0; t < 2; t++)
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-          const float s0 = st[t][2 * i], s1 = st[t][2 * i + 1];
-          const float p0 = s0 == -__builtin_inff() ? 0.0f : exp2_minimax(kLog2e * s0);
-          const float p1 = s1 == -__builtin_inff() ? 0.0f : exp2_minimax(kLog2e * s1);
-          const uint32_t pk = pack_bf16(p0, p1);
-          psum[t] = psum[t] + bf16_lo(pk);
-          psum[t] = psum[t] + bf16_hi(pk);
-          reinterpret_cast<uint32_t *>(&pb[t][i / 4].u)[i % 4] = pk;
-        }
+          for (int i = 0; i < 8; i++) {
+            const float s0 = st[t][2 * i], s1 = st[t][2 * i + 1];
+            float p0 = exp2_minimax(kLog2e * s0), p1 = exp2_minimax(kLog2e * s1);
+            if (masked) {
+              p0 = s0 == -__builtin_inff() ? 0.0f : p0;
+              p1 = s1 == -__builtin_inff() ? 0.0f : p1;
+            }
+            const uint32_t pk = pack_bf16(p0, p1);
+            psum[t] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pk), ones, psum[t], false);
+            reinterpret_cast<uint32_t *>(&pb[t][i / 4].u)[i % 4] = pk;
+          }
+      };
+      if (full)
+        probs(false);
+      else
+        probs(true);
       den = den + halves_sum(psum[0] + psum[1]);
     } else {
       // Online step over the stage's 64 keys (softmax_pairs, bf16.rs:409-473).

@@ -4,7 +4,8 @@ per-GPU device array): called through the C ABI, its output equals the
 allocating entry point's bit for bit (the same kernels and order), and the
 oracle's within the FP32 tolerance, on two calls in a row, the second with
 a smaller input (fewer rows over a shorter cache), so stale partial states
-of the first call cannot leak into the second."""
+of the first call cannot leak into the second; with the cache's exact and
+fast exp (focr_kv_set_fast_exp)."""
 import ctypes
 
 import numpy as np
@@ -38,8 +39,9 @@ def call_noalloc(fh, kv, q, rows, sinks, out):
     assert rc == 0, fh.lib().focr_last_error().decode()
 
 
+@pytest.mark.parametrize("fast", [False, True])
 @pytest.mark.parametrize("bits", [8, 16])
-def test_noalloc_decode_equals_the_allocating_entry_point(bits):
+def test_noalloc_decode_equals_the_allocating_entry_point(bits, fast):
     import torch
 
     import focr_hip as fh
@@ -47,7 +49,7 @@ def test_noalloc_decode_equals_the_allocating_entry_point(bits):
     sinks = to_dev(gen.uniform(H, -2.0, 2.0, 7))
     # First call: 8 rows over 16,320 + 64 positions; second: 3 rows over 1,000 + 5.
     for prefix, tail_rows, rows, seed in ((16320, 64, 8, 11), (1000, 5, 3, 21)):
-        kv = sealed_cache(fh, bits, prefix, tail_rows, seed)
+        kv = sealed_cache(fh, bits, prefix, tail_rows, seed).set_fast_exp(fast)
         q = to_dev(gen.att_values(rows * H * 64, seed + 5, 0.75).reshape(rows, H, 64))
         out = torch.full((rows, H, 64), float("nan"), device="cuda:0")
         call_noalloc(fh, kv, q, rows, sinks, out)
@@ -57,7 +59,7 @@ def test_noalloc_decode_equals_the_allocating_entry_point(bits):
         pk, vals, gk = kv.dequantize()
         total = prefix + tail_rows
         ref = oracle.attention_decode(host(q), host(pk), host(gk), host(vals), rows, prefix, total, H, G,
-                                      total - rows, 0, 0, host(sinks))
+                                      total - rows, 0, 0, host(sinks), exp_fast=fast)
         got = host(out)
         assert np.all(np.isfinite(got))
         assert np.all(np.abs(got - ref) <= 1e-5 * (1.0 + np.abs(ref)))

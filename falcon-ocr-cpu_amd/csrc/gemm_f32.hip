@@ -708,12 +708,22 @@ void launch_one(bool chain, const GemmArgs &a, hipStream_t stream) {
       hipLaunchKernelGGL((mfma_kernel<T, EPI, 128, 128, true>), grid, dim3(256), 0, stream, a);
     else
       hipLaunchKernelGGL((mfma_kernel<T, EPI, 128, 128, false>), grid, dim3(256), 0, stream, a);
-  } else {
+  } else if (static_cast<long>((a.m + 127) / 128) * ((a.n + 63) / 64) >= 1024) {
     const dim3 grid((a.m + 127) / 128, (a.n + 63) / 64);
     if (vec)
       hipLaunchKernelGGL((mfma_kernel<T, EPI, 128, 64, true>), grid, dim3(256), 0, stream, a);
     else
       hipLaunchKernelGGL((mfma_kernel<T, EPI, 128, 64, false>), grid, dim3(256), 0, stream, a);
+  } else {
+    // n = 768: 624 tiles of 128 x 64 took two rounds of 512 workgroup slots
+    // (two per compute unit by LDS), the second a fifth full; 64 x 64 tiles
+    // fit four per unit and make both rounds half as long (WO 39 -> 58,
+    // W2 42 -> 63 TFLOP/s on INT16 codes; outputs unchanged).
+    const dim3 grid((a.m + 63) / 64, (a.n + 63) / 64);
+    if (vec)
+      hipLaunchKernelGGL((mfma_kernel<T, EPI, 64, 64, true>), grid, dim3(256), 0, stream, a);
+    else
+      hipLaunchKernelGGL((mfma_kernel<T, EPI, 64, 64, false>), grid, dim3(256), 0, stream, a);
   }
 }
 

@@ -11,7 +11,11 @@ and `value` is algorithmic bytes / wall time over those K steps.
 
 `roofline` describes the GEMV kernel: algorithmic bytes per launch divided by
 the average launch duration, i.e. the HIP-event time of the K replayed launches
-(events recorded on the stream the kernels run on) divided by K. `per_op` reports the other BASELINE configurations on the
+(events recorded on the stream the kernels run on) divided by K, from a second
+flushed replay whose events bracket the kernels rather than the host's
+submission of the replay (the stream sleeps while the host submits it); the
+first replay's event window, which includes that submission, is reported as
+`per_op.gemv_i16_m1.timed_window_us_per_step`. `per_op` reports the other BASELINE configurations on the
 same box (FP32 prefill GEMM, INT16-activation x INT8 prefill GEMM, INT8 GEMV,
 attention prefill). `cpu_baseline` times the C oracle (a restatement of the
 reference's CPU operator) on the host cores for a bounded sample.
@@ -42,6 +46,10 @@ FP32_MFMA_PEAK = 157.3  # TFLOP/s dense
 FP32_VECTOR_PEAK = 157.3
 INT8_MFMA_PEAK = 5000.0  # TOP/s dense
 POOL_BYTES = 600 << 20  # > 2 x 256 MB Infinity Cache
+# Device clock cycles the stream sleeps (torch.cuda._sleep: a spin on the
+# clock, no memory traffic) while the host submits the timed replay whose
+# launches the events then bracket: well over a replay's submission time.
+SUBMIT_COVER_CYCLES = 2_000_000
 
 
 def gemv_bytes(n, k, rows, code_bytes, group=64):
@@ -127,7 +135,6 @@ def bench_gemv(torch, fh, gen, np, bits, rows, steps, warmup, graph=True, n=4096
     # written buffer would leave dirty lines whose write-back the timed reads
     # would pay for.
     float(flush.sum())
-    del flush
     # Timed region: barrier, events on the launch stream around the K steps.
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -136,8 +143,23 @@ def bench_gemv(torch, fh, gen, np, bits, rows, steps, warmup, graph=True, n=4096
     ev1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    avg_ms = ev0.elapsed_time(ev1) / steps
-    return {"bytes": nbytes, "wall_s": wall, "steps": steps, "avg_launch_ms": avg_ms,
+    window_ms = ev0.elapsed_time(ev1) / steps
+    # The launches' own duration: the same K steps once more after another
+    # flush, with the stream held by a bounded sleep (no memory traffic)
+    # while the host submits them, so the events bracket the K kernels and
+    # not the host's submission of the replay (which the window above, and
+    # the whole-job wall clock, include).
+    float(flush.sum())
+    del flush
+    torch.cuda.synchronize()
+    k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(SUBMIT_COVER_CYCLES)
+    k0.record(stream)
+    run()
+    k1.record(stream)
+    torch.cuda.synchronize()
+    avg_ms = k0.elapsed_time(k1) / steps
+    return {"bytes": nbytes, "wall_s": wall, "steps": steps, "avg_launch_ms": avg_ms, "window_ms": window_ms,
             "pool_copies": len(pool), "codes": codes, "scales": scales, "x": x, "cache_flushed": True}
 
 
@@ -700,12 +722,14 @@ def main():
     fh.default_context()
     log(f"device: {torch.cuda.get_device_name(0)}")
     head = bench_gemv(torch, fh, gen, np, 16, 1, args.steps, args.warmup, graph=not args.no_graph)
-    log(f"gemv16 M=1: wall {head['wall_s'] * 1e3:.2f} ms / {args.steps} steps, launch {head['avg_launch_ms'] * 1e3:.2f} us")
+    log(f"gemv16 M=1: wall {head['wall_s'] * 1e3:.2f} ms / {args.steps} steps, launch {head['avg_launch_ms'] * 1e3:.2f} us"
+        f" (event window of the timed replay {head['window_ms'] * 1e3:.2f} us per step)")
     ms_per_step = head["wall_s"] * 1e3 / args.steps
     value = head["bytes"] / (head["wall_s"] / args.steps) / 1e9
     achieved = head["bytes"] / (head["avg_launch_ms"] * 1e-3) / 1e9
     per_op = {"gemv_i16_m1": {"bytes": head["bytes"], "launch_us": round(head["avg_launch_ms"] * 1e3, 3),
                               "gbs_per_launch": round(achieved, 1), "gbs_whole_job": round(value, 1),
+                              "timed_window_us_per_step": round(head["window_ms"] * 1e3, 3),
                               "pool_copies": head["pool_copies"]}}
     if "gemv" in ops:
         for bits, rows in ((16, 5), (8, 1), (8, 5)):

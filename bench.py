@@ -163,6 +163,26 @@ def bench_gemv(torch, fh, gen, np, bits, rows, steps, warmup, graph=True, n=4096
             "pool_copies": len(pool), "codes": codes, "scales": scales, "x": x, "cache_flushed": True}
 
 
+def bench_gemv_sustained(torch, fh, gen, np, graph=True, k=1024, ns=(4096, 16384, 65536, 131072, 262144)):
+    """The INT8 g64 GEMV (M = 1) at growing output widths, each launch on a
+    cold copy: per-launch time t(B) over algorithmic bytes B, and the
+    least-squares line t = t0 + B / R over the points from 16,384 channels
+    up. R is the rate the kernel streams at once its launch is long enough to
+    hide t0, the fixed cost of a launch (dispatch, first-byte latency, drain)."""
+    points = []
+    for n in ns:
+        r = bench_gemv(torch, fh, gen, np, 8, 1, 200 if n <= 65536 else 60, 5, graph=graph, n=n, k=k)
+        us = r["avg_launch_ms"] * 1e3
+        points.append({"n": n, "bytes": r["bytes"], "launch_us": round(us, 3), "gbs": round(r["bytes"] / us / 1e3, 1),
+                       "frac_hbm": round(r["bytes"] / us / 1e3 / HBM_PEAK_GBS, 3), "pool_copies": r["pool_copies"]})
+    fit = [p for p in points if p["n"] >= 16384]
+    slope, t0 = np.polyfit(np.array([p["bytes"] for p in fit], float), np.array([p["launch_us"] for p in fit], float), 1)
+    rate = 1e-3 / slope  # GB/s
+    return {"k": k, "points": points,
+            "fit": {"over_n": [p["n"] for p in fit], "t0_us": round(float(t0), 3), "streaming_gbs": round(float(rate), 1),
+                    "streaming_frac_hbm": round(float(rate) / HBM_PEAK_GBS, 3)}}
+
+
 def bench_gemm(torch, fh, gen, np, reps, bits=32):
     """BASELINE config 1 (FP32, m = 6544) on the checkpoint shapes and the
     literal shape; with bits=16 the same projections on a near-exact body
@@ -750,6 +770,8 @@ def main():
                            "gbs_per_launch": round(r["bytes"] / (r["avg_launch_ms"] * 1e-3) / 1e9, 1),
                            "frac_hbm_per_launch": round(r["bytes"] / (r["avg_launch_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 3)}
             log(f"{key}: {per_op[key]}")
+        per_op["gemv_i8_m1_sustained"] = bench_gemv_sustained(torch, fh, gen, np, graph=not args.no_graph)
+        log(f"gemv_i8_m1_sustained: {per_op['gemv_i8_m1_sustained']}")
     if "gemm" in ops:
         per_op["prefill_f32"] = bench_gemm(torch, fh, gen, np, args.reps)
         log(f"prefill_f32: {per_op['prefill_f32']}")

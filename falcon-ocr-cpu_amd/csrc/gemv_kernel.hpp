@@ -15,9 +15,9 @@
 // phase for its two channels. Dequantization fl(code * scale) happens in
 // registers; FP32 weights are never materialized.
 //
-// Latency structure. Every thread first loads its share of x, then issues
-// the scale loads and the weight loads of up to W steps, all unconditional
-// with in-bounds clamped indices. It waits only for the x loads (the oldest:
+// Latency structure. Every thread first loads its outputs' residual (ADD
+// epilogue only) and its share of x, then issues the scale loads and the
+// weight loads of up to W steps, all with in-bounds clamped indices. It waits only for the x loads (the oldest:
 // vmcnt counts down in issue order) to store x in LDS, meets the other waves
 // at one barrier, and then consumes step t as soon as its own weights have
 // arrived, while the later steps are still in flight. x sits in LDS as [row][32 * S * steps]
@@ -188,6 +188,26 @@ __global__ __launch_bounds__(256) void kernel(Args a) {
     return reinterpret_cast<const float4 *>(a.tile_scales)[g < sc_total4 ? g : sc_total4 - 1];
   };
 
+  // 0. The ADD epilogue's residual (h), loaded first: the x loads below are
+  // waited for anyway, and vmcnt counts down in issue order, so the residual
+  // arrives within that wait instead of after the reduction; and the later
+  // waits count only loads issued after x, so they are the same whether or
+  // not this branch ran.
+  const int ch0 = my_tile * kGemvChannels + h * 2;
+  float res[2][M];
+  if (a.add) {
+#pragma unroll
+    for (int c = 0; c < 2; c++)
+#pragma unroll
+      for (int r = 0; r < M; r++) res[c][r] = a.out[static_cast<size_t>(r) * a.n + (ch0 + c < a.n ? ch0 + c : a.n - 1)];
+  } else {
+#pragma unroll
+    for (int c = 0; c < 2; c++)
+#pragma unroll
+      for (int r = 0; r < M; r++) res[c][r] = 0.0f;
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
   // 1. Without ROLL: x and scales go to registers first (clamped, in bounds)
   // and to LDS only after the weight loads are issued, so their stores wait
   // for the x and scale loads only (the oldest: vmcnt counts down in issue
@@ -300,7 +320,6 @@ __global__ __launch_bounds__(256) void kernel(Args a) {
     }
   }
 
-  const int ch0 = tile * kGemvChannels + h * 2;
   auto x_col = [&](int r, int i) {
     const float v = a.x[static_cast<size_t>(r) * k + i];
     if constexpr (RMS > 0) return v * rsc[r];
@@ -368,8 +387,7 @@ __global__ __launch_bounds__(256) void kernel(Args a) {
       if (ch0 + c < a.n)
 #pragma unroll
         for (int r = 0; r < M; r++) {
-          float *o = a.out + static_cast<size_t>(r) * a.n + ch0 + c;
-          *o = *o + total[c][r];
+          a.out[static_cast<size_t>(r) * a.n + ch0 + c] = res[c][r] + total[c][r];
         }
   } else {
 #pragma unroll

@@ -8,9 +8,9 @@
 // multiple of 32 from a segment start that is itself one, so the leaves are
 // the consecutive 32-chunks of the row (the last one possibly shorter); only
 // the order in which leaves are added depends on the width. PairTree<LEN>
-// unrolls that order at compile time, so a wave computes the leaves in
-// parallel (lane i: leaves i, i + 64, ...) and adds them in the reference's
-// order in straight-line code.
+// unrolls that order at compile time; a wave computes every leaf with its
+// lanes (two leaves per register, the folds across lanes) and adds the leaves
+// in the reference's order in straight-line code.
 #pragma once
 
 #include "focr_internal.hpp"
@@ -42,46 +42,57 @@ struct PairTree<LEN, false> {
   }
 };
 
-// One leaf (at most 32 values, zero-padded): squares, then the 16-8-4-2-1 folds.
-template <typename Load>
-__device__ __forceinline__ float leaf_squares(const Load &load, int len) {
-  float part[32];
-#pragma unroll
-  for (int i = 0; i < 32; i++) {
-    const float v = i < len ? load(i) : 0.0f;
-    part[i] = v * v;
-  }
-#pragma unroll
-  for (int w = 16; w >= 1; w /= 2)
-#pragma unroll
-    for (int i = 0; i < w; i++) part[i] = part[i] + part[i + w];
-  return part[0];
+template <int CTRL>
+__device__ __forceinline__ float rms_dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
 }
 
-// Leaf values held by lanes: leaf L lives in lane L % 64 of register L / 64.
-template <int NL>
-struct LaneLeaves {
-  float v[(NL + 63) / 64];
+// Two leaves in one register: lane i of each 32-lane half holds the square of
+// element i of its leaf (zero past the row). The 16-8-4-2-1 folds
+// partial[i] += partial[i + w] run across lanes: v_permlane16_swap pairs the
+// two 16-lane rows of each half (w = 16); row_ror:8 pairs lanes i and i ^ 8
+// (w = 8); row_ror:12, 14, 15 bring lane i + 4, i + 2, i + 1 to lane i
+// (w = 4, 2, 1; only the lanes below w are used at each level). IEEE addition
+// is commutative, so each sum is bitwise the reference's; lane 0 of each half
+// ends with its leaf.
+__device__ __forceinline__ float fold_leaf_pair(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  float s = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  s = s + rms_dpp<0x128>(s);
+  s = s + rms_dpp<0x12C>(s);
+  s = s + rms_dpp<0x12E>(s);
+  return s + rms_dpp<0x12F>(s);
+}
+
+// Leaf L lives in lane 32 (L % 2) of register L / 2.
+template <int NJ>
+struct PairLeaves {
+  float v[NJ];
   template <int L>
   __device__ __forceinline__ float get() const {
-    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[L / 64]), L % 64));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[L / 2]), 32 * (L % 2)));
   }
 };
 
 // rms_scale of one LEN-wide row, computed by a whole wave (every lane returns
-// it). `at(i)` reads element i of the row (global or LDS).
+// it). `at(i)` reads element i of the row (global or LDS); lane l reads
+// elements l, l + 64, ... (consecutive addresses across the wave), so register
+// j holds leaves 2j and 2j + 1.
 template <int LEN, typename At>
 __device__ __forceinline__ float rms_scale_wave(const At &at, float eps) {
   constexpr int NL = (LEN + 31) / 32;
+  constexpr int NJ = (NL + 1) / 2;
   const int lane = threadIdx.x & 63;
-  LaneLeaves<NL> leaves;
+  float sq[NJ];
 #pragma unroll
-  for (int j = 0; j < (NL + 63) / 64; j++) {
-    const int leaf = lane + 64 * j;
-    const int len = leaf < NL ? (LEN - 32 * leaf < 32 ? LEN - 32 * leaf : 32) : 0;
-    const int base = 32 * (leaf < NL ? leaf : 0);
-    leaves.v[j] = leaf_squares([&](int i) { return at(base + i); }, len);
+  for (int j = 0; j < NJ; j++) {
+    const int i = 64 * j + lane;
+    const float v = i < LEN ? at(i) : 0.0f;
+    sq[j] = v * v;
   }
+  PairLeaves<NJ> leaves;
+#pragma unroll
+  for (int j = 0; j < NJ; j++) leaves.v[j] = fold_leaf_pair(sq[j]);
   const float sum = PairTree<LEN>::template eval<0>(leaves);
   return __fdiv_rn(1.0f, __builtin_sqrtf(__fdiv_rn(sum, static_cast<float>(LEN)) + eps));
 }

@@ -609,6 +609,252 @@ __global__ __launch_bounds__(256) void split_partial_kernel(SplitDecArgs a, int 
   }
 }
 
+// Code I (0..3) of a 32-bit word of four Q8 codes, or (0..1) of two Q16
+// codes, as a float (exact). Plain C: the compiler forms the SDWA conversion
+// itself and, unlike for inline assembly, knows it needs no wait state
+// before the FMA that reads it.
+template <typename C, int I>
+__device__ __forceinline__ float word_code(uint32_t w) {
+  if constexpr (sizeof(C) == 1)
+    return static_cast<float>(static_cast<int8_t>(w >> (8 * I)));
+  else
+    return static_cast<float>(static_cast<int16_t>(w >> (16 * I)));
+}
+
+// The scan for one or two query rows, with the work of a 16-key slice laid
+// out so that no lane repeats another's: for the scores, lane (key kk, head
+// e, half) forms the dot of its 32 dims of head 2g + e with the key's codes
+// (T for half 0, S(2g + e) for half 1 of a prefix record; the key's dims
+// 0-31 / 32-63 of a tail record), scaled once by the block's step, and the
+// two halves are added across lanes; for the values, lane (dim quad dq, key
+// quarter ks) accumulates dims 4dq .. 4dq + 3 of both heads over keys
+// 4i + ks with the block's step folded into p. The running max is taken per
+// 16-key slice (uniform over the slice's lanes), each score lane keeps its
+// own denominator part, and the parts are summed at the end. Tolerance-only
+// against the reference's operation order, as the split-K scan already is.
+template <typename C, int M, bool FAST>
+__global__ __launch_bounds__(256) void split_scan_kernel(SplitDecArgs a, int iters, int rows) {
+  __shared__ float4 s_o[kWaves][2][M][16];
+  __shared__ float2 s_md[kWaves][2][M];
+  __shared__ float2 s_p[kWaves][16][M];  // the slice's probabilities (head 2g, head 2g + 1)
+  __shared__ RoundBuf<C> rb0, rb1;
+  constexpr int B = sizeof(C);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int kk = lane & 15, e = (lane >> 4) & 1, half = lane >> 5;
+  const int dq = lane & 15, ks = lane >> 4;
+  const int task = blockIdx.x;
+  const int c = task % a.chunks, g = task / a.chunks;
+  const int key0 = c * iters * 4 * kKpl;
+  int vis[M], limit = 0;
+#pragma unroll
+  for (int r = 0; r < M; r++) {
+    vis[r] = a.last - rows + r + 1;
+    limit = vis[r] > limit ? vis[r] : limit;
+  }
+  float qv[M][32];
+#pragma unroll
+  for (int r = 0; r < M; r++)
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const float4 t = ld4(a.q + (static_cast<size_t>(r) * a.n_heads + 2 * g + e) * 64 + 32 * half + 4 * i);
+      qv[r][4 * i] = t.x;
+      qv[r][4 * i + 1] = t.y;
+      qv[r][4 * i + 2] = t.z;
+      qv[r][4 * i + 3] = t.w;
+    }
+  const float ninf = -__builtin_inff();
+  float m[M], dl[M];
+  float4 o[M][2];
+#pragma unroll
+  for (int r = 0; r < M; r++) {
+    m[r] = ninf;
+    dl[r] = 0.0f;
+    o[r][0] = o[r][1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
+  constexpr int kCopies = RoundBuf<C>::kCopies;
+  const int rbytes = a.record_bytes;
+  const unsigned char *group_base = a.records + static_cast<size_t>(g) * a.prefix_len * rbytes;
+  auto issue = [&](RoundBuf<C> &dst, int t) {
+    const int b = key0 + kRoundKeys * t;
+    const int in_prefix = a.prefix_len - b;
+    const int valid = in_prefix <= 0 ? 0 : (in_prefix < kRoundKeys ? in_prefix : kRoundKeys) * rbytes;
+    const unsigned char *src = group_base + static_cast<size_t>(in_prefix > 0 ? b : 0) * rbytes;
+#pragma unroll
+    for (int i = 0; i < kCopies; i++) {
+      const int off = (threadIdx.x + 256 * i) * 16;
+      __builtin_amdgcn_global_load_lds((global_void *)(src + (off < valid ? off : 0)),
+                                       (lds_void *)(&dst.chunk[64 * wave + 256 * i]), 16, 0, 0);
+    }
+  };
+  // One 16-key slice starting at position b; rec(q) gives key b + q's record
+  // and whether it is a prefix record.
+  auto slice = [&](int b, auto rec) __attribute__((always_inline)) {
+    // Scores.
+    const int j = b + kk;
+    const auto kr = rec(kk);
+    const unsigned char *kp = kr.ptr;
+    const bool pre = kr.prefix;
+    const int koff = half == 0 ? 0 : (pre ? 32 + 32 * e : 32);
+    const int sidx = half == 0 ? 0 : (pre ? 1 + e : 1);
+    const uint16_t *ksteps = reinterpret_cast<const uint16_t *>(kp + (pre ? kRecord : kTail) * B);
+    const float kstep = bf16_widen(ksteps[sidx]);
+    float acc[M];
+#pragma unroll
+    for (int r = 0; r < M; r++) acc[r] = 0.0f;
+#pragma unroll
+    for (int w4 = 0; w4 < 2 * B; w4++) {
+      const uint4 w = *reinterpret_cast<const uint4 *>(kp + koff * B + 16 * w4);
+      const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int wi = 0; wi < 4; wi++) {
+        constexpr int kPer = 4 / B;  // codes per word
+#pragma unroll
+        for (int ci = 0; ci < kPer; ci++) {
+          float code;
+          if constexpr (B == 1)
+            code = ci == 0 ? word_code<C, 0>(words[wi]) : ci == 1 ? word_code<C, 1>(words[wi])
+                 : ci == 2 ? word_code<C, 2>(words[wi]) : word_code<C, 3>(words[wi]);
+          else
+            code = ci == 0 ? word_code<C, 0>(words[wi]) : word_code<C, 1>(words[wi]);
+          const int d = (16 * w4 + 4 * wi) / B + ci;
+#pragma unroll
+          for (int r = 0; r < M; r++) acc[r] = fmaf_(qv[r][d], code, acc[r]);
+        }
+      }
+    }
+    float p[M], rsv[M];
+#pragma unroll
+    for (int r = 0; r < M; r++) {
+      const float part = acc[r] * kstep;
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(part), __float_as_uint(part), false, false);
+      float sc = (__uint_as_float(sw[0]) + __uint_as_float(sw[1])) * 0.125f;
+      sc = j < vis[r] ? sc : ninf;
+      // Slice maximum over the 16 keys (every lane of the row gets it).
+      float bm = sc;
+      bm = __builtin_fmaxf(bm, dpp<0x128>(bm));
+      bm = __builtin_fmaxf(bm, dpp<0x124>(bm));
+      bm = __builtin_fmaxf(bm, dpp<0x122>(bm));
+      bm = __builtin_fmaxf(bm, dpp<0x121>(bm));
+      const float mn = bm > m[r] ? bm : m[r];
+      const float rs = m[r] == ninf ? 0.0f : expf_acc(m[r] - mn);
+      p[r] = sc == ninf ? 0.0f : prob_exp<FAST>(sc - mn);
+      dl[r] = dl[r] * rs + p[r];
+      m[r] = mn;
+      rsv[r] = rs;
+    }
+    if (half == 0) {
+#pragma unroll
+      for (int r = 0; r < M; r++) reinterpret_cast<float *>(&s_p[wave][kk][r])[e] = p[r];
+    }
+    // Values: rescale, then keys 4i + ks.
+#pragma unroll
+    for (int r = 0; r < M; r++) {
+      const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rsv[r]), 0));
+      const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rsv[r]), 16));
+      if (r0 != 1.0f) o[r][0] = scale4(o[r][0], r0);
+      if (r1 != 1.0f) o[r][1] = scale4(o[r][1], r1);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int q = 4 * i + ks;
+      const auto vr = rec(q);
+      const unsigned char *vp = vr.ptr;
+      const bool vpre = vr.prefix;
+      const int voff = vpre ? 96 : 64;
+      const int vsidx = (vpre ? 3 : 2) + (dq >> 3);
+      const float vstep = bf16_widen(reinterpret_cast<const uint16_t *>(vp + (vpre ? kRecord : kTail) * B)[vsidx]);
+      const float4 cv = codes4<C>(vp + (voff + 4 * dq) * B);
+#pragma unroll
+      for (int r = 0; r < M; r++) {
+        const float2 pp = s_p[wave][q][r];
+        // A masked or vanished key adds nothing, whatever its step holds.
+        const float pv0 = pp.x == 0.0f ? 0.0f : pp.x * vstep;
+        const float pv1 = pp.y == 0.0f ? 0.0f : pp.y * vstep;
+        o[r][0] = make_float4(fmaf_(pv0, cv.x, o[r][0].x), fmaf_(pv0, cv.y, o[r][0].y), fmaf_(pv0, cv.z, o[r][0].z),
+                              fmaf_(pv0, cv.w, o[r][0].w));
+        o[r][1] = make_float4(fmaf_(pv1, cv.x, o[r][1].x), fmaf_(pv1, cv.y, o[r][1].y), fmaf_(pv1, cv.z, o[r][1].z),
+                              fmaf_(pv1, cv.w, o[r][1].w));
+      }
+    }
+  };
+  struct RecRef {
+    const unsigned char *ptr;
+    bool prefix;
+  };
+  const int rounds = iters / kWaves;
+  auto round = [&](const RoundBuf<C> &cur, RoundBuf<C> &next, int t) __attribute__((always_inline)) {
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): this wave's copies of round t
+    __syncthreads();                     // everyone's copies; nobody still reads `next`
+    issue(next, t + 1 < rounds ? t + 1 : rounds - 1);
+    const int b = key0 + kRoundKeys * t;
+    const int bw = b + 16 * wave;
+    // As in split_partial_kernel: a round wholly inside the visible prefix is
+    // scored from LDS, the others read HBM, each branch consuming its own keys.
+    if (b + kRoundKeys <= a.prefix_len && b + kRoundKeys <= limit) {
+      const unsigned char *base = reinterpret_cast<const unsigned char *>(cur.chunk) + 16 * wave * rbytes;
+      slice(bw, [&](int q) { return RecRef{base + q * rbytes, true}; });
+    } else {
+      slice(bw, [&](int q) {
+        const int jj = bw + q < limit ? bw + q : 0;
+        const bool pre = jj < a.prefix_len;
+        const unsigned char *ptr =
+            pre ? a.records + (static_cast<size_t>(g) * a.prefix_len + jj) * rbytes
+                : a.tail + (static_cast<size_t>(g) * a.tail_capacity + (jj - a.prefix_len)) * a.tail_bytes;
+        return RecRef{ptr, pre};
+      });
+    }
+  };
+  issue(rb0, 0);
+  int t = 0;
+  for (; t + 2 <= rounds; t += 2) {
+    round(rb0, rb1, t);
+    round(rb1, rb0, t + 1);
+  }
+  if (t < rounds) round(rb0, rb1, t);
+  __builtin_amdgcn_s_waitcnt(0x0f70);  // the repeated copies land before LDS is reused
+  // The wave's state: denominators summed over the slice lanes, outputs over
+  // the key quarters.
+#pragma unroll
+  for (int r = 0; r < M; r++) {
+    const float den = row_sum16(dl[r]);
+#pragma unroll
+    for (int h2 = 0; h2 < 2; h2++) {
+      float4 v = o[r][h2];
+      auto add_pairs16 = [](float x) {
+        const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+        return __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+      };
+      auto add_pairs32 = [](float x) {
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+        return __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+      };
+      v = make_float4(add_pairs32(add_pairs16(v.x)), add_pairs32(add_pairs16(v.y)), add_pairs32(add_pairs16(v.z)),
+                      add_pairs32(add_pairs16(v.w)));
+      if (ks == 0) s_o[wave][h2][r][dq] = v;
+    }
+    if (lane == 0 || lane == 16) s_md[wave][e][r] = make_float2(m[r], den);
+  }
+  __syncthreads();
+  if (lane < 32) {
+    const int lg = lane >> 4, lp = lane & 15;
+    const int he = lg;
+#pragma unroll
+    for (int r = 0; r < M; r++) {
+      if (r % kWaves != wave) continue;
+      float2 md = s_md[0][he][r];
+      float4 accv = s_o[0][he][r][lp];
+#pragma unroll
+      for (int w = 1; w < kWaves; w++) {
+        const float2 md2 = s_md[w][he][r];
+        merge(md.x, md.y, accv, md2.x, md2.y, s_o[w][he][r][lp]);
+      }
+      const size_t slot = (static_cast<size_t>(r) * a.n_heads + 2 * g + he) * a.chunks + c;
+      *reinterpret_cast<float4 *>(a.part_o + slot * 64 + 4 * lp) = accv;
+      if (lp == 0) *reinterpret_cast<float2 *>(a.part_md + slot * 2) = md;
+    }
+  }
+}
+
 // `fixed` (optional): a caller-provided partial-state buffer of
 // `fixed_bytes` used instead of the context scratch (nothing is allocated).
 template <typename C, int M>
@@ -639,12 +885,21 @@ int launch_split(Ctx *ctx, SplitDecArgs a, int rows, bool fast, const float *sin
     a.part_o = static_cast<float *>(ctx->scratch);
   }
   a.part_md = a.part_o + slots * 64;
-  if (fast)
-    hipLaunchKernelGGL((split_partial_kernel<C, M, true>), dim3(a.tasks), dim3(64 * kWaves), 0, ctx->stream, a,
-                       iters, rows);
-  else
-    hipLaunchKernelGGL((split_partial_kernel<C, M, false>), dim3(a.tasks), dim3(64 * kWaves), 0, ctx->stream, a,
-                       iters, rows);
+  if constexpr (M <= 2) {
+    if (fast)
+      hipLaunchKernelGGL((split_scan_kernel<C, M, true>), dim3(a.tasks), dim3(64 * kWaves), 0, ctx->stream, a, iters,
+                         rows);
+    else
+      hipLaunchKernelGGL((split_scan_kernel<C, M, false>), dim3(a.tasks), dim3(64 * kWaves), 0, ctx->stream, a, iters,
+                         rows);
+  } else {
+    if (fast)
+      hipLaunchKernelGGL((split_partial_kernel<C, M, true>), dim3(a.tasks), dim3(64 * kWaves), 0, ctx->stream, a,
+                         iters, rows);
+    else
+      hipLaunchKernelGGL((split_partial_kernel<C, M, false>), dim3(a.tasks), dim3(64 * kWaves), 0, ctx->stream, a,
+                         iters, rows);
+  }
   FOCR_HIP_CHECK(hipGetLastError());
   CombineArgs cb;
   cb.part_o = a.part_o;

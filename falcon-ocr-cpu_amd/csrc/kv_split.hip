@@ -339,6 +339,11 @@ struct SplitDecArgs {
   int prefix_len, tail_capacity, n_heads, n_kv, record_bytes, tail_bytes;
   int last;  // positions in the cache; row r sees keys [0, last - rows + r + 1)
   int chunks, tasks;
+  // The fused row step (split_scan_kernel with ROW): the row's raw q|k|v, its
+  // RoPE factors, where its queries go (optional), and the record to write.
+  const float *qkv, *rope;
+  float *q_out;
+  unsigned char *tail_w;
 };
 
 // Four consecutive codes of a record as floats (one 4- or 8-byte load).
@@ -632,11 +637,21 @@ __device__ __forceinline__ float word_code(uint32_t w) {
 // 16-key slice (uniform over the slice's lanes), each score lane keeps its
 // own denominator part, and the parts are summed at the end. Tolerance-only
 // against the reference's operation order, as the split-K scan already is.
-template <typename C, int M, bool FAST>
+//
+// ROW (one row): the decode row step runs in the same launch. Waves 0 and 1
+// of every task normalize and rotate the query heads 2g and 2g + 1 from the
+// raw q|k|v row (norm_rope, as row_append_kernel), and the task holding the
+// new position (the last chunk) codes the group's key and values into the
+// new tail record (waves 2, 3) before any round reads it; the other tasks
+// never read that record. Queries and records are bitwise the
+// row_append_kernel's, so the output is bitwise the unfused pair of calls.
+template <typename C, int M, bool FAST, bool ROW = false>
 __global__ __launch_bounds__(256) void split_scan_kernel(SplitDecArgs a, int iters, int rows) {
+  static_assert(!ROW || M == 1, "the fused row step takes one row");
   __shared__ float4 s_o[kWaves][2][M][16];
   __shared__ float2 s_md[kWaves][2][M];
   __shared__ float2 s_p[kWaves][16][M];  // the slice's probabilities (head 2g, head 2g + 1)
+  __shared__ float s_q[2][64];
   __shared__ RoundBuf<C> rb0, rb1;
   constexpr int B = sizeof(C);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -650,26 +665,6 @@ __global__ __launch_bounds__(256) void split_scan_kernel(SplitDecArgs a, int ite
   for (int r = 0; r < M; r++) {
     vis[r] = a.last - rows + r + 1;
     limit = vis[r] > limit ? vis[r] : limit;
-  }
-  float qv[M][32];
-#pragma unroll
-  for (int r = 0; r < M; r++)
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const float4 t = ld4(a.q + (static_cast<size_t>(r) * a.n_heads + 2 * g + e) * 64 + 32 * half + 4 * i);
-      qv[r][4 * i] = t.x;
-      qv[r][4 * i + 1] = t.y;
-      qv[r][4 * i + 2] = t.z;
-      qv[r][4 * i + 3] = t.w;
-    }
-  const float ninf = -__builtin_inff();
-  float m[M], dl[M];
-  float4 o[M][2];
-#pragma unroll
-  for (int r = 0; r < M; r++) {
-    m[r] = ninf;
-    dl[r] = 0.0f;
-    o[r][0] = o[r][1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   }
   constexpr int kCopies = RoundBuf<C>::kCopies;
   const int rbytes = a.record_bytes;
@@ -686,6 +681,52 @@ __global__ __launch_bounds__(256) void split_scan_kernel(SplitDecArgs a, int ite
                                        (lds_void *)(&dst.chunk[64 * wave + 256 * i]), 16, 0, 0);
     }
   };
+  issue(rb0, 0);
+  float qv[M][32];
+  if constexpr (ROW) {
+    // The row step while round 0's copies are in flight.
+    const int qdim = a.n_heads * 64, kdim = a.n_kv * 64, repeat = a.n_heads / a.n_kv;
+    const float2 *rope = reinterpret_cast<const float2 *>(a.rope);
+    if (wave < 2) {
+      const int head = 2 * g + wave;
+      const float y = norm_rope(a.qkv[head * 64 + lane], rope[head * 32 + lane / 2], lane);
+      s_q[wave][lane] = y;
+      if (a.q_out && c == 0) a.q_out[head * 64 + lane] = y;
+    } else if (c == a.chunks - 1) {
+      const bool key = wave == 2;
+      const float x = key ? a.qkv[qdim + g * 64 + lane] : a.qkv[qdim + kdim + g * 64 + lane];
+      const float y = key ? norm_rope(x, rope[g * repeat * 32 + lane / 2], lane) : x;
+      uint16_t stored;
+      const int code = code_lane(y, half_any(!__builtin_isfinite(y)), sizeof(C) == 1 ? 127.0 : 32767.0, stored);
+      unsigned char *rec = a.tail_w + static_cast<size_t>(g) * a.tail_capacity * a.tail_bytes;
+      const int el = (key ? 0 : 64) + lane;
+      reinterpret_cast<C *>(rec)[el] = static_cast<C>(code);
+      if ((el & 31) == 0) reinterpret_cast<uint16_t *>(rec + kTail * sizeof(C))[el >> 5] = stored;
+    }
+    __syncthreads();  // the queries in LDS, the new record written (read by this task only)
+#pragma unroll
+    for (int i = 0; i < 32; i++) qv[0][i] = s_q[e][32 * half + i];
+  } else {
+#pragma unroll
+    for (int r = 0; r < M; r++)
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const float4 t = ld4(a.q + (static_cast<size_t>(r) * a.n_heads + 2 * g + e) * 64 + 32 * half + 4 * i);
+        qv[r][4 * i] = t.x;
+        qv[r][4 * i + 1] = t.y;
+        qv[r][4 * i + 2] = t.z;
+        qv[r][4 * i + 3] = t.w;
+      }
+  }
+  const float ninf = -__builtin_inff();
+  float m[M], dl[M];
+  float4 o[M][2];
+#pragma unroll
+  for (int r = 0; r < M; r++) {
+    m[r] = ninf;
+    dl[r] = 0.0f;
+    o[r][0] = o[r][1] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
   // One 16-key slice starting at position b; rec(q) gives key b + q's record
   // and whether it is a prefix record.
   auto slice = [&](int b, auto rec) __attribute__((always_inline)) {
@@ -804,7 +845,6 @@ __global__ __launch_bounds__(256) void split_scan_kernel(SplitDecArgs a, int ite
       });
     }
   };
-  issue(rb0, 0);
   int t = 0;
   for (; t + 2 <= rounds; t += 2) {
     round(rb0, rb1, t);
@@ -857,7 +897,7 @@ __global__ __launch_bounds__(256) void split_scan_kernel(SplitDecArgs a, int ite
 
 // `fixed` (optional): a caller-provided partial-state buffer of
 // `fixed_bytes` used instead of the context scratch (nothing is allocated).
-template <typename C, int M>
+template <typename C, int M, bool ROW = false>
 int launch_split(Ctx *ctx, SplitDecArgs a, int rows, bool fast, const float *sinks, float *out, float *fixed,
                  size_t fixed_bytes) {
   // Keys per workgroup task: about 1024 tasks over the chip (each serves two
@@ -887,12 +927,13 @@ int launch_split(Ctx *ctx, SplitDecArgs a, int rows, bool fast, const float *sin
   a.part_md = a.part_o + slots * 64;
   if constexpr (M <= 2) {
     if (fast)
-      hipLaunchKernelGGL((split_scan_kernel<C, M, true>), dim3(a.tasks), dim3(64 * kWaves), 0, ctx->stream, a, iters,
-                         rows);
+      hipLaunchKernelGGL((split_scan_kernel<C, M, true, ROW>), dim3(a.tasks), dim3(64 * kWaves), 0, ctx->stream, a,
+                         iters, rows);
     else
-      hipLaunchKernelGGL((split_scan_kernel<C, M, false>), dim3(a.tasks), dim3(64 * kWaves), 0, ctx->stream, a, iters,
-                         rows);
+      hipLaunchKernelGGL((split_scan_kernel<C, M, false, ROW>), dim3(a.tasks), dim3(64 * kWaves), 0, ctx->stream, a,
+                         iters, rows);
   } else {
+    static_assert(!ROW, "the fused row step takes one row");
     if (fast)
       hipLaunchKernelGGL((split_partial_kernel<C, M, true>), dim3(a.tasks), dim3(64 * kWaves), 0, ctx->stream, a,
                          iters, rows);
@@ -942,6 +983,9 @@ SplitDecArgs split_args(const KvSplit *s, const float *q) {
   a.record_bytes = static_cast<int>(s->record_bytes);
   a.tail_bytes = static_cast<int>(s->tail_bytes);
   a.last = static_cast<int>(s->prefix_len + s->tail_len);
+  a.qkv = a.rope = nullptr;
+  a.q_out = nullptr;
+  a.tail_w = nullptr;
   return a;
 }
 
@@ -1051,6 +1095,26 @@ int focr_kv_qkv_rows(focr_ctx *handle, focr_kv_split *kv, const float *qkv, size
   FOCR_HIP_CHECK(hipGetLastError());
   s->tail_len += rows;
   return FOCR_OK;
+}
+
+int focr_kv_decode_row(focr_ctx *handle, focr_kv_split *kv, const float *qkv, const float *rope, const float *sinks,
+                       float *q, float *out) {
+  Ctx *ctx = reinterpret_cast<Ctx *>(handle);
+  KvSplit *s = reinterpret_cast<KvSplit *>(kv);
+  FOCR_REQUIRE(ctx && s && qkv && rope && sinks && out, FOCR_E_ARG, "focr_kv_decode_row: null argument");
+  FOCR_REQUIRE(s->prefix_len + s->tail_len + 1 <= s->capacity, FOCR_E_SHAPE, "split tail capacity");
+  FOCR_REQUIRE(s->n_heads == 2 * s->n_kv, FOCR_E_SHAPE, "split decode: two query heads per KV head");
+  FOCR_HIP_CHECK(hipSetDevice(ctx->device));
+  SplitDecArgs a = split_args(s, nullptr);
+  a.last += 1;  // the new row is position prefix_len + tail_len
+  a.qkv = qkv;
+  a.rope = rope;
+  a.q_out = q;
+  a.tail_w = s->tail + s->tail_len * s->tail_bytes;
+  const int rc = s->bits == 8 ? launch_split<int8_t, 1, true>(ctx, a, 1, s->fast_exp, sinks, out, nullptr, 0)
+                              : launch_split<int16_t, 1, true>(ctx, a, 1, s->fast_exp, sinks, out, nullptr, 0);
+  if (rc == FOCR_OK) s->tail_len += 1;
+  return rc;
 }
 
 int focr_kv_attention_decode(focr_ctx *handle, const focr_kv_split *kv, const float *q, size_t rows,

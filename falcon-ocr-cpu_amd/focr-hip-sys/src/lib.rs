@@ -257,6 +257,15 @@ extern "C" {
         rope_dev: *const f32,
         q_dev: *mut f32,
     ) -> c_int;
+    pub fn focr_kv_decode_row(
+        ctx: *mut focr_ctx,
+        kv: *mut focr_kv_split,
+        qkv_dev: *const f32,
+        rope_dev: *const f32,
+        sinks_dev: *const f32,
+        q_dev: *mut f32,
+        out_dev: *mut f32,
+    ) -> c_int;
     pub fn focr_kv_attention_decode(
         ctx: *mut focr_ctx,
         kv: *const focr_kv_split,

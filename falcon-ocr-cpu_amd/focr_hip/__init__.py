@@ -85,6 +85,7 @@ SIGNATURES = {
     "focr_kv_set_fast_exp": (_I, [_P, _I]),
     "focr_kv_fast_exp": (_I, [_P, _P]),
     "focr_kv_qkv_rows": (_I, [_P, _P, _P, _Z, _P, _P]),
+    "focr_kv_decode_row": (_I, [_P, _P, _P, _P, _P, _P, _P]),
     "focr_kv_info": (_I, [_P, _P, _P, _P, _P, _P]),
     "focr_kv_free": (_I, [_P]),
     "focr_screen_build": (_I, [_P, _P, _Z, _Z, ctypes.POINTER(_P)]),
@@ -523,6 +524,18 @@ class KvSplit:
             q = torch.empty((rows, self.n_heads, 64), dtype=torch.float32, device=qkv.device)
         _check(lib().focr_kv_qkv_rows(self.ctx.handle, self.handle, _dev(qkv), rows, _dev(rope), _dev(q)))
         return q
+
+    def decode_row(self, qkv, rope, sinks, q=None, out=None):
+        """One greedy step in one launch: the row step and append of
+        `qkv_rows` for one row, then `attention_decode` of that row over the
+        cache including it (bitwise the two calls). Returns out [1][n_heads][64];
+        `q` [1][n_heads][64], if given, receives the rotated query."""
+        torch = _torch()
+        if out is None:
+            out = torch.empty((1, self.n_heads, 64), dtype=torch.float32, device=qkv.device)
+        _check(lib().focr_kv_decode_row(self.ctx.handle, self.handle, _dev(qkv), _dev(rope), _dev(sinks), _dev(q),
+                                        _dev(out)))
+        return out
 
     def attention_decode(self, q, rows: int, sinks, out=None):
         """`attention_decode_rows`: [rows][n_heads][64] for the last `rows` positions."""

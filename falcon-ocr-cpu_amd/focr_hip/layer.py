@@ -193,6 +193,9 @@ class DecoderLayer:
             mark("qkv_rows")
             attn = attention_with(q, self.kv(total), rows, Geometry(pos, *self.image), self.sinks, self.options,
                                   output=out, ctx=ctx)
+        elif rows == 1:
+            # The row step, the tail append and the attention in one launch.
+            attn = self.split.decode_row(qkv, rope, self.sinks, q=self._buf("dq", (1, self.n_heads, 64)), out=out)
         else:
             # split_norm_rope and the tail append in one kernel.
             q = self.split.qkv_rows(qkv, rows, rope, q=self._buf("dq", (rows, self.n_heads, 64)))

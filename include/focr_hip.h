@@ -276,6 +276,20 @@ int focr_kv_append(focr_ctx *ctx, focr_kv_split *kv, const float *k_dev, const f
  * capacity. */
 int focr_kv_qkv_rows(focr_ctx *ctx, focr_kv_split *kv, const float *qkv_dev, size_t rows,
                      const float *rope_dev, float *q_dev);
+/* One greedy decode step's attention over a sealed cache in one launch:
+ * focr_kv_qkv_rows for one row (split_norm_rope, src/model/rope.rs:14-86,
+ * and the split cache's append, src/model/cache.rs:117-140 ->
+ * SplitPrefix::append, src/quant/kv.rs:430-515) fused with
+ * focr_kv_attention_decode for that row (SplitPrefix::attention_decode,
+ * src/quant/kv.rs:568-580): qkv_dev [qdim + 2 kdim] and rope_dev
+ * [n_heads][32][2] as for focr_kv_qkv_rows; the row is appended to the tail
+ * and its query attends to every cached position including itself, with the
+ * per-head sink; out_dev [n_heads][64]; q_dev (may be NULL) receives the
+ * normalized, rotated query. Queries, records and output are bitwise those
+ * of focr_kv_qkv_rows followed by focr_kv_attention_decode (rows = 1).
+ * FOCR_E_SHAPE past the capacity. Uses the context scratch. */
+int focr_kv_decode_row(focr_ctx *ctx, focr_kv_split *kv, const float *qkv_dev, const float *rope_dev,
+                       const float *sinks_dev, float *q_dev, float *out_dev);
 /* SplitPrefix::attention_decode / attention_decode_rows (src/quant/kv.rs:
  * 568-580,856-900): q_dev [rows][n_heads][64], rows 1..8 (at most the
  * appended positions); row r attends to keys [0, len - rows + r + 1) of the

@@ -159,3 +159,47 @@ def test_fused_row_step_is_bitwise_the_unfused_one(fh):
     assert np.all(np.isnan(vals[P + 1 + 2, 1, 32:64])) and np.all(np.isfinite(vals[P + 1 + 2, 1, :32]))
     fused.free()
     unfused.free()
+
+
+@pytest.mark.parametrize("fast", [False, True])
+@pytest.mark.parametrize("bits", [8, 16])
+@pytest.mark.parametrize("prefix_len,tail", [(700, 2), (16320, 5)])
+def test_decode_row_is_bitwise_the_two_calls(fh, bits, fast, prefix_len, tail):
+    # focr_kv_decode_row = focr_kv_qkv_rows (one row) + focr_kv_attention_decode
+    # (rows = 1), bit for bit: query, output, and the records it appends.
+    import torch
+
+    k, v = pair_cache(prefix_len, N_KV, 81)
+    cap = prefix_len + tail + 4
+    tk = to_dev(gen.normal((tail, N_KV, 64), 1.0, 82))
+    tv = to_dev(gen.normal((tail, N_KV, 64), 1.0, 83))
+    two = fh.KvSplit.seal(bits, to_dev(k), to_dev(v), prefix_len, cap, N_HEADS, N_KV)
+    one = fh.KvSplit.seal(bits, to_dev(k), to_dev(v), prefix_len, cap, N_HEADS, N_KV)
+    for kv in (two, one):
+        kv.append(tk, tv, tail)
+        kv.set_fast_exp(fast)
+    sinks = to_dev(gen.uniform(N_HEADS, -2.0, 2.0, 84))
+    width = N_HEADS * 64 + 2 * N_KV * 64
+    for step in range(3):
+        qkv = gen.normal((1, width), 2.0, 90 + step)
+        if step == 2:
+            qkv[0, N_HEADS * 64 + N_KV * 64 + 3 * 64 + 7] = np.inf  # group 3's first value block decodes to NaN
+        ang = gen.uniform((1, N_HEADS, 32), -3.2, 3.2, 95 + step)
+        rope = to_dev(np.stack([np.cos(ang), np.sin(ang)], -1).astype(np.float32))
+        q2 = two.qkv_rows(to_dev(qkv), 1, rope)
+        out2 = two.attention_decode(q2, 1, sinks)
+        q1 = torch.empty_like(q2)
+        out1 = one.decode_row(to_dev(qkv), rope, sinks, q=q1)
+        assert one.info()[2] == two.info()[2] == tail + step + 1
+        assert_bitwise(host(q1), host(q2), f"step {step} query")
+        assert_bitwise(host(out1), host(out2), f"step {step} output")
+        if step < 2:
+            assert np.all(np.isfinite(host(out1)))
+        else:
+            o = host(out1)[0]  # heads 6 and 7 read group 3's values: dims 0-31 NaN, the rest finite
+            assert np.all(np.isnan(o[6:8, :32])) and np.all(np.isfinite(o[6:8, 32:]))
+            assert np.all(np.isfinite(o[:6])) and np.all(np.isfinite(o[8:]))
+    for a, b, what in zip(one.dequantize(), two.dequantize(), ("prefix keys", "values", "generated keys")):
+        assert_bitwise(host(a), host(b), what)
+    one.free()
+    two.free()

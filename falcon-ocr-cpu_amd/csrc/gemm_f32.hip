@@ -65,6 +65,7 @@ struct GemmArgs {
   int n_exc;
   int m, n, k, group, groups;
   float *out;
+  int row0;  // dma_kernel: first output row of the launch's tiles (0 for the other kernels)
 };
 
 // Stages A'[m0.., k0..k0+32) and W[n0.., k0..k0+32) into LDS as [row][k].
@@ -325,7 +326,7 @@ __global__ __launch_bounds__(256) void dma_kernel(GemmArgs a) {
   __shared__ float4 lb0[BN * 4], lb1[BN * 4], lb2[BN * 4], lb3[BN * 4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
+  const int m0 = a.row0 + blockIdx.x * BM, n0 = blockIdx.y * BN;
   const int h = lane >> 5, l32 = lane & 31;
   const float *w = static_cast<const float *>(a.codes);
 
@@ -653,6 +654,7 @@ GemmArgs make_args(const Linear *lin, const float *x, size_t rows, const float *
   a.group = static_cast<int>(lin->group);
   a.groups = static_cast<int>(lin->groups);
   a.out = out;
+  a.row0 = 0;
   return a;
 }
 
@@ -691,9 +693,31 @@ void launch_one(bool chain, const GemmArgs &a, hipStream_t stream) {
       // 64 x 64 on 1,280 slots do not): WO 72.5 -> 85.9 and W2 77.7 -> 87.6
       // TFLOP/s, outputs unchanged (each one's k order is the tile's).
       const long tiles128x64 = static_cast<long>((a.m + 127) / 128) * ((a.n + 63) / 64);
-      if (tiles128 >= 1024)
-        hipLaunchKernelGGL((dma_kernel<EPI, 128>), dim3((a.m + 127) / 128, (a.n + 127) / 128), dim3(256), 0, stream, a);
-      else if (tiles128x64 >= 1024)
+      if (tiles128 >= 1024) {
+        // 128 x 128 tiles take two workgroup slots per compute unit (512 on
+        // the chip). When they leave a last round mostly empty (6,544 x 4096:
+        // 1,664 tiles = 3.25 rounds), the row blocks of whole rounds run as
+        // 128 x 128 tiles and the rows left over as 64 x 64 tiles in a second
+        // launch, if those fit one round of its 1,280 slots (five per compute
+        // unit): the literal shape 0.560 -> 0.538 ms in A/B runs; W13 (3.66
+        // rounds, 1,368 leftover tiles) gained nothing and keeps one launch.
+        // Every output is the same 32 x 32 block computation either way
+        // (bitwise unchanged).
+        const int slots = 512, small_slots = 1280;
+        const int mtiles = (a.m + 127) / 128, ntiles = (a.n + 127) / 128;
+        const int rb = static_cast<int>((tiles128 / slots) * slots / ntiles);  // row blocks of whole rounds
+        const long small = static_cast<long>((a.m - 128 * rb + 63) / 64) * ((a.n + 63) / 64);
+        const bool mostly_empty = tiles128 % slots != 0 && tiles128 % slots <= slots / 2;
+        if (mostly_empty && rb > 0 && rb < mtiles && small <= small_slots) {
+          hipLaunchKernelGGL((dma_kernel<EPI, 128>), dim3(rb, ntiles), dim3(256), 0, stream, a);
+          GemmArgs rest = a;
+          rest.row0 = 128 * rb;
+          hipLaunchKernelGGL((dma_kernel<EPI, 64, 64>), dim3((a.m - rest.row0 + 63) / 64, (a.n + 63) / 64), dim3(256),
+                             0, stream, rest);
+        } else {
+          hipLaunchKernelGGL((dma_kernel<EPI, 128>), dim3(mtiles, ntiles), dim3(256), 0, stream, a);
+        }
+      } else if (tiles128x64 >= 1024)
         hipLaunchKernelGGL((dma_kernel<EPI, 64>), dim3((a.m + 127) / 128, (a.n + 63) / 64), dim3(256), 0, stream, a);
       else
         hipLaunchKernelGGL((dma_kernel<EPI, 64, 64>), dim3((a.m + 63) / 64, (a.n + 63) / 64), dim3(256), 0, stream, a);

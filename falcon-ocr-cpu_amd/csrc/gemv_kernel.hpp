@@ -17,12 +17,14 @@
 //
 // Latency structure. Every thread first loads its outputs' residual (ADD
 // epilogue only) and its share of x, then issues the scale loads and the
-// weight loads of up to W steps, all with in-bounds clamped indices. It waits only for the x loads (the oldest:
-// vmcnt counts down in issue order) to store x in LDS, meets the other waves
-// at one barrier, and then consumes step t as soon as its own weights have
-// arrived, while the later steps are still in flight. x sits in LDS as [row][32 * S * steps]
-// with the blocks past the last full one zeroed; the tile layout holds zero
-// codes there, so the padded products are fma(0, 0, acc) = acc exactly.
+// weight loads of up to W steps, all with in-bounds clamped indices. It
+// waits only for the x loads (the oldest: vmcnt counts down in issue order)
+// to store x in LDS, meets the other waves at one barrier, and then consumes
+// step t as soon as its own weights have arrived, while the later steps are
+// still in flight. x sits in LDS transposed, [row][phase][block] (x_at), so
+// a lane's S blocks of a step are one or two vector reads per row, with the
+// blocks past the last full one zeroed; the tile layout holds zero codes
+// there, so the padded products are fma(0, 0, acc) = acc exactly.
 //
 // Roofline: HBM. Bytes per call = codes + scales (+ x, out), e.g. 4,476,928 B
 // for an INT8 4096x1024 matrix at one row.
@@ -127,8 +129,18 @@ struct Args {
   float *out;
 };
 
-// Floats per LDS row of x: every block a step can touch.
-__host__ __device__ inline int x_pitch(int steps, int S) { return 32 * S * steps; }
+// x in LDS, transposed: row r, phase p (0..31), block b at
+// r * 32 * P + p * P + b, so that the S blocks a lane reads in one step are
+// consecutive (one or two 16-byte reads instead of S 4-byte ones). P holds
+// every block a step can touch, rounded to a multiple of 4 with P / 4 odd:
+// the 16 lanes a ds_read_b128 serves at once then start on distinct 16-byte
+// bank groups.
+__host__ __device__ inline int x_phase_pitch(int steps, int S) {
+  const int p = (S * steps + 3) / 4 * 4;
+  return (p / 4) % 2 == 1 ? p : p + 4;
+}
+__host__ __device__ inline int x_pitch(int steps, int S) { return 32 * x_phase_pitch(steps, S); }
+__device__ __forceinline__ int x_at(int pp, int i) { return (i & 31) * pp + (i >> 5); }
 
 // T: code type; M: rows; SPS: scales per lane-channel per step (0 for FP32
 // weights); W: steps held in registers; ROLL: steps > W, so the window is
@@ -142,7 +154,7 @@ __global__ __launch_bounds__(256) void kernel(Args a) {
   constexpr int B = sizeof(T);
   constexpr int S = 16 / (2 * B);  // 32-blocks per step
   constexpr int NS = 2 * SPS;      // scales per lane per step
-  extern __shared__ float xs[];    // [M][x_pitch], then scales [kWaves][steps][2][NS]
+  extern __shared__ float xs[];    // [M][32][pp] (x_pitch per row), then scales [kWaves][steps][2][NS]
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -151,7 +163,7 @@ __global__ __launch_bounds__(256) void kernel(Args a) {
   const bool active = tile < a.tiles_total;
   const int my_tile = active ? tile : a.tiles_total - 1;
   const int k = a.k, nb = a.nb, steps = a.steps;
-  const int pitch = x_pitch(steps, S);
+  const int pitch = x_pitch(steps, S), pp = x_phase_pitch(steps, S);
   const T *codes = static_cast<const T *>(a.codes);
   float *ss = xs + M * pitch;
 
@@ -230,7 +242,14 @@ __global__ __launch_bounds__(256) void kernel(Args a) {
   } else {
     // Rows longer than the window: stage directly (the weights wait).
     for (int r = 0; r < M; r++)
-      for (int i = tid; i < cols4; i += 256) *reinterpret_cast<float4 *>(xs + r * pitch + 4 * i) = x_load(r, i);
+      for (int i = tid; i < cols4; i += 256) {
+        const float4 v = x_load(r, i);
+        float *row = xs + r * pitch;
+        row[x_at(pp, 4 * i)] = v.x;
+        row[x_at(pp, 4 * i + 1)] = v.y;
+        row[x_at(pp, 4 * i + 2)] = v.z;
+        row[x_at(pp, 4 * i + 3)] = v.w;
+      }
     if constexpr (NS > 0)
       for (int i = tid; i < sc_count4; i += 256) reinterpret_cast<float4 *>(ss)[i] = sc_load(i);
   }
@@ -252,16 +271,24 @@ __global__ __launch_bounds__(256) void kernel(Args a) {
 #pragma unroll
       for (int j = 0; j < XJ; j++) {
         const int i = tid + 256 * j;
-        if (i < cols4) *reinterpret_cast<float4 *>(xs + r * pitch + 4 * i) = xv[r][j];
+        if (i < cols4) {
+          float *row = xs + r * pitch;
+          row[x_at(pp, 4 * i)] = xv[r][j].x;
+          row[x_at(pp, 4 * i + 1)] = xv[r][j].y;
+          row[x_at(pp, 4 * i + 2)] = xv[r][j].z;
+          row[x_at(pp, 4 * i + 3)] = xv[r][j].w;
+        }
       }
     if constexpr (NS > 0)
 #pragma unroll
       for (int j = 0; j < SJ; j++)
         if (tid + 256 * j < sc_count4) reinterpret_cast<float4 *>(ss)[tid + 256 * j] = sv[j];
   }
-  for (int i = tid; i < M * (pitch - cols); i += 64 * kWaves) {
-    const int r = i / (pitch - cols), c = cols + i % (pitch - cols);
-    xs[r * pitch + c] = 0.0f;
+  // Blocks nb .. pp - 1 of every phase row: zero (the padded blocks a step
+  // reads past the last full one, and the pitch padding).
+  for (int i = tid; i < M * 32 * (pp - nb); i += 64 * kWaves) {
+    const int r = i / (32 * (pp - nb)), rest = i % (32 * (pp - nb));
+    xs[r * pitch + (rest / (pp - nb)) * pp + nb + rest % (pp - nb)] = 0.0f;
   }
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   if (!active) return;
@@ -269,7 +296,7 @@ __global__ __launch_bounds__(256) void kernel(Args a) {
 #pragma unroll
   for (int r = 0; r < M; r++) {
     if constexpr (RMS > 0)
-      rsc[r] = rms_scale_wave<RMS>([&](int i) { return xs[r * pitch + i]; }, 1.1920929e-7f);
+      rsc[r] = rms_scale_wave<RMS>([&](int i) { return xs[r * pitch + x_at(pp, i)]; }, 1.1920929e-7f);
     else
       rsc[r] = 1.0f;
   }
@@ -287,12 +314,32 @@ __global__ __launch_bounds__(256) void kernel(Args a) {
     chunk_codes<T, S * 2>(raw, vals);
     Scales<NS> sc;
     if constexpr (NS > 0) sc = load_scales<NS>(my_scales + t * 2 * NS);
+    // This lane's S blocks of the step, for every row: consecutive in LDS.
+    float xb[M][S];
+#pragma unroll
+    for (int r = 0; r < M; r++) {
+      const float *src = xs + r * pitch + p * pp + t * S;
+      if constexpr (S % 4 == 0) {
+#pragma unroll
+        for (int q = 0; q < S / 4; q++) {
+          const float4 v = reinterpret_cast<const float4 *>(src)[q];
+          xb[r][4 * q] = v.x;
+          xb[r][4 * q + 1] = v.y;
+          xb[r][4 * q + 2] = v.z;
+          xb[r][4 * q + 3] = v.w;
+        }
+      } else {
+        const float2 v = *reinterpret_cast<const float2 *>(src);
+        xb[r][0] = v.x;
+        xb[r][1] = v.y;
+      }
+    }
 #pragma unroll
     for (int s = 0; s < S; s++) {
       float xr[M];
 #pragma unroll
       for (int r = 0; r < M; r++) {
-        xr[r] = xs[r * pitch + 32 * (t * S + s) + p];
+        xr[r] = xb[r][s];
         if constexpr (RMS > 0) xr[r] = xr[r] * rsc[r];
       }
 #pragma unroll

@@ -180,3 +180,28 @@ def test_large_matrices_several_tiles_per_wave(fh, bits, n, k, group):
         lin.linear_ex(to_dev(x), rows, epilogue=fh.Epilogue.ADD, out=h)
         assert_bitwise(host(h), (base + want).astype(np.float32), f"large add rows {rows}")
     lin.free()
+
+
+@pytest.mark.parametrize("bits,k", [(8, 6144), (16, 3072), (32, 2560), (8, 5160), (16, 2600)])
+def test_long_rows_refill_the_weight_window(fh, bits, k):
+    # Rows longer than the register window (more than 20 steps of 16-byte
+    # chunks, 36 for FP32 weights) stage x directly and refill the weight
+    # window as it is consumed: still bitwise the reference's dot, with the
+    # 8-wide and scalar tails (k % 32 != 0) and an exception column.
+    n, group = 70, 64
+    if bits == 32:
+        w = gen.normal((n, k), 0.02, 120)
+        lin = fh.Linear.from_f32(w)
+        x = gen.normal((2, k), 1.0, 121)
+        for rows in (1, 2):
+            want = oracle.linear_decode(32, w, None, n, k, 32, x[:rows], rows)
+            assert_bitwise(host(lin.linear(to_dev(x[:rows]), rows)), want, f"fp32 k {k} rows {rows}")
+        lin.free()
+        return
+    codes, scales, vals = quantized(bits, n, k, group, 122, exc=[k - 3])
+    x = gen.normal((2, k), 1.0, 123)
+    lin = fh.QuantLinear(bits, codes, scales, group, exc_cols=[k - 3], exc_vals=vals)
+    for rows in (1, 2):
+        want = oracle.linear_decode(bits, codes, scales, n, k, group, x[:rows], rows, exc_cols=[k - 3], exc_vals=vals)
+        assert_bitwise(host(lin.linear(to_dev(x[:rows]), rows)), want, f"bits {bits} k {k} rows {rows}")
+    lin.free()

@@ -42,6 +42,28 @@ int ensure_scratch(Ctx *ctx, size_t bytes) {
   return FOCR_OK;
 }
 
+int ensure_weights(Ctx *ctx, size_t bytes, bool *ready) {
+  *ready = false;
+  if (bytes <= ctx->weights_bytes) {
+    *ready = true;
+    return FOCR_OK;
+  }
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  FOCR_HIP_CHECK(hipStreamIsCapturing(ctx->stream, &capture));
+  if (capture != hipStreamCaptureStatusNone) return FOCR_OK;
+  if (ctx->weights) {
+    // Kernels queued earlier may still read the old buffer.
+    FOCR_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+    FOCR_HIP_CHECK(hipFree(ctx->weights));
+    ctx->weights = nullptr;
+    ctx->weights_bytes = 0;
+  }
+  FOCR_HIP_CHECK(hipMalloc(&ctx->weights, bytes));
+  ctx->weights_bytes = bytes;
+  *ready = true;
+  return FOCR_OK;
+}
+
 namespace {
 
 int code_bytes(int bits) { return bits == 8 ? 1 : bits == 16 ? 2 : 4; }
@@ -152,6 +174,7 @@ int focr_ctx_destroy(focr_ctx *handle) {
   if (ctx->scratch) FOCR_HIP_CHECK(hipFree(ctx->scratch));
   if (ctx->argmax_dev) FOCR_HIP_CHECK(hipFree(ctx->argmax_dev));
   if (ctx->rms_dev) FOCR_HIP_CHECK(hipFree(ctx->rms_dev));
+  if (ctx->weights) FOCR_HIP_CHECK(hipFree(ctx->weights));
   FOCR_HIP_CHECK(hipStreamDestroy(ctx->own));
   delete ctx;
   return FOCR_OK;

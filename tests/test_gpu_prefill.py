@@ -154,6 +154,29 @@ def test_f32_mfma_within_fp32_tolerance(fh, bits, m, k, n):
     assert_bitwise(glu, (np.where(g > 0, g, F32(0)) ** 2 * u).astype(np.float32), "glu of store")
 
 
+@pytest.mark.parametrize("bits", [16, 8])
+def test_f32_mfma_on_codes_keeps_exception_columns(fh, bits):
+    # Codes on the matrix cores: k a multiple of 64 dequantizes into the
+    # context's weight buffer first (it grows, then serves a smaller matrix);
+    # k = 100 stages codes in registers. Exception columns in place either way.
+    for m, k, n in ((13, 768, 64), (40, 1024, 96), (9, 192, 32), (9, 100, 48)):
+        columns = [0, k // 2, k - 1]
+        w = gen.matrix(n * k, 6).reshape(n, k)
+        vals = (w[:, columns] * F32(300.0)).astype(np.float32)
+        w[:, columns] = 0.0
+        codes, scales = oracle.quantize_bits(w, n, k, 64 if k % 64 == 0 else 32, bits)
+        group = 64 if k % 64 == 0 else 32
+        lin = fh.QuantLinear(bits, codes, scales, group, exc_cols=columns, exc_vals=vals)
+        dense = oracle.dequantize(bits, codes, scales, n, k, group, exc_cols=columns, exc_vals=vals)
+        a = gen.matrix(m * k, 7).reshape(m, k)
+        base = gen.matrix(m * n, 8).reshape(m, n)
+        for epi, o_epi in ((fh.Epilogue.STORE, oracle.STORE), (fh.Epilogue.ADD, oracle.ADD)):
+            got = run_prefill(fh, lin, a, m, None, epi, fh.PrefillProjection.F32_MFMA,
+                              base=base if epi == fh.Epilogue.ADD else None)
+            want = oracle.panel_gemm(a, m, k, dense, n, epilogue=o_epi, out=base.copy() if o_epi == oracle.ADD else None)
+            assert max_rel(got, want) <= 1e-5, (bits, m, k, n, epi.name)
+
+
 @pytest.mark.parametrize("name,k,n,epi", [("qkv", 768, 2048, 0), ("wo", 1024, 768, 2), ("w13", 768, 4608, 1),
                                           ("w2", 2304, 768, 2), ("literal", 1024, 4096, 0)])
 def test_config1_fp32_gemm_checkpoint_shapes(fh, name, k, n, epi):

@@ -10,9 +10,9 @@
 //  - chain2_kernel (k a multiple of 16) / chain_kernel (any shape): SIMT
 //    register tiles in which every output is one FMA chain over ascending k
 //    from +0.0: bitwise the reference's FP32 panels.
-// Weights are dequantized while staging into LDS, except on the matrix-core
-// path where the DMA kernel takes the shape: there the codes are dequantized
-// into a per-context FP32 buffer first (launch_f32_common).
+// Weights are dequantized while staging into LDS, except where the FP32
+// DMA kernel or the k-major chain kernel takes the shape: there the codes are
+// dequantized into a per-context FP32 buffer first (launch_f32_common).
 //
 // Roofline: FP32 matrix cores (157.3 TFLOP/s) for mfma_kernel; the FP32
 // vector peak (157.3 TFLOP/s: gfx950 issues even non-packed FMAs faster than
@@ -766,15 +766,17 @@ int launch_f32_common(bool chain, Ctx *ctx, const Linear *lin, const float *x, s
                       int epilogue, float *out) {
   FOCR_REQUIRE(rows < (size_t(1) << 30), FOCR_E_SHAPE, "prefill rows too large");
   GemmArgs a = make_args(lin, x, rows, row_scale, out);
-  // Codes on the matrix cores, where the FP32 DMA kernel takes the shape:
-  // the weights fl(code * scale) (exception columns in place, the values
-  // mfma_kernel forms while staging) are dequantized into the context's
-  // weight buffer, then dma_kernel runs on them. The extra HBM traffic, 6 or
-  // 8 bytes per weight for INT16 / INT8 codes plus the 4 bytes the GEMM
-  // then reads, is small beside the register staging it replaces (literal
-  // 1024 -> 4096 at 6,544 rows: 16 MiB written, about 4 us, on a GEMM of
-  // about 0.55 ms).
-  if (!chain && lin->bits != 32 && a.k % (4 * kDmaBK) == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0) {
+  // Codes, where the FP32 kernels take the shape (the DMA kernel on the
+  // matrix cores, the k-major exact-order chain): the weights fl(code *
+  // scale) (exception columns in place, the values the code kernels form
+  // while staging) are dequantized into the context's weight buffer, then
+  // the FP32 kernel runs on them; the chain's outputs are the same FMA
+  // chains, bitwise. The extra HBM traffic, 6 or 8 bytes per weight for
+  // INT16 / INT8 codes plus the 4 bytes the GEMM then reads, is small beside
+  // the per-tile conversion it replaces (literal 1024 -> 4096 at 6,544 rows:
+  // 16 MiB written, about 4 us, on a GEMM of 0.55-0.75 ms).
+  const bool x16 = reinterpret_cast<uintptr_t>(x) % 16 == 0;
+  if (lin->bits != 32 && x16 && a.k % (chain ? kC2K : 4 * kDmaBK) == 0) {
     bool ready = false;
     int rc = ensure_weights(ctx, lin->n * lin->k * sizeof(float), &ready);
     if (rc != FOCR_OK) return rc;
@@ -786,7 +788,7 @@ int launch_f32_common(bool chain, Ctx *ctx, const Linear *lin, const float *x, s
       a.exc_index = nullptr;
       a.exc_vals = nullptr;
       a.n_exc = 0;
-      launch_epi<float>(false, epilogue, a, ctx->stream);
+      launch_epi<float>(chain, epilogue, a, ctx->stream);
       FOCR_HIP_CHECK(hipGetLastError());
       return FOCR_OK;
     }

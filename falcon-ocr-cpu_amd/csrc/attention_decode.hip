@@ -22,6 +22,15 @@
 // same sum). Consecutive tasks are the query heads of one KV head on the same
 // chunk, so their value rows are read together.
 //
+// Fused row step (launch_attention_decode_row, one generated row): the
+// query is this wave's head of the new QKV row, normalized and rotated in
+// the kernel (norm_rope, lane = element, then gathered to the float4 lane
+// layout); the waves whose chunk holds the new position form its key and
+// value the same way, use them in place of the cache's row in that one
+// iteration, and the first query head of the pair writes them to the cache.
+// No wave waits for another, and every value is the bits the separate row
+// step would have stored, so the output is bitwise the two calls'.
+//
 // Roofline: HBM. Bytes per call = keys (prefix keys per query head, generated
 // keys per KV head) + values per KV head over the visible keys, + q, out and
 // the partial states.
@@ -37,16 +46,31 @@ struct DecArgs {
   float *part_o, *part_md;  // [rows * n_heads][chunks][64], [rows * n_heads][chunks][2]
   int prefix_len, total_len, n_heads, n_kv_heads, query_offset, image_start, image_end;
   int chunks, tasks;
+  // Fused row step: the row's QKV and RoPE factors, where its query (may be
+  // null), key and value go; the row is at query_offset.
+  const float *qkv, *rope;
+  float *q_out, *k_new, *v_new;
 };
+
+// v of lanes 4 lp .. 4 lp + 3 (lane = element to the float4 lane layout).
+__device__ __forceinline__ float4 gather4(float v, int lp) {
+  const int x = __float_as_int(v);
+  return make_float4(__int_as_float(__builtin_amdgcn_ds_bpermute((4 * lp) << 2, x)),
+                     __int_as_float(__builtin_amdgcn_ds_bpermute((4 * lp + 1) << 2, x)),
+                     __int_as_float(__builtin_amdgcn_ds_bpermute((4 * lp + 2) << 2, x)),
+                     __int_as_float(__builtin_amdgcn_ds_bpermute((4 * lp + 3) << 2, x)));
+}
 
 // Keys per lane group per iteration (a wave takes 4 * kKpl = 32 keys per
 // iteration, double-buffered: the next iteration's keys and values are in
 // flight while the current ones are scored).
 constexpr int kKpl = 8;
 
-// M: query rows. A wave task covers `iters` iterations of 32 keys.
-template <int M>
+// M: query rows. A wave task covers `iters` iterations of 32 keys. ROW: the
+// fused row step (M = 1).
+template <int M, bool ROW>
 __global__ __launch_bounds__(256) void decode_partial_kernel(DecArgs a, int iters) {
+  static_assert(!ROW || M == 1, "the fused row step takes one row");
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int lg = lane >> 4, lp = lane & 15;
   const int task = blockIdx.x * kWaves + wave;
@@ -80,11 +104,57 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(DecArgs a, int iter
       vb[i] = ld4(a.v + (static_cast<size_t>(jj) * a.n_kv_heads + g) * 64 + 4 * lp);
     }
   };
+  // Fused row step: the row's loads go first, so that waiting for them does
+  // not wait for the cache reads.
+  const int pos = a.query_offset;
+  const bool holds = ROW && pos >= key0 && pos < key0 + iters * 4 * kKpl;  // wave-uniform
+  float xq = 0.0f, xk = 0.0f;
+  float2 fq = make_float2(0.0f, 0.0f), fk = fq;
+  float4 vnew = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if constexpr (ROW) {
+    const int qdim = a.n_heads * 64, kdim = a.n_kv_heads * 64;
+    const float2 *rope2 = reinterpret_cast<const float2 *>(a.rope);
+    xq = a.qkv[h * 64 + lane];
+    fq = rope2[h * 32 + lane / 2];
+    if (holds) {
+      // The unique key head g is the expanded head g * repeat (its factors).
+      xk = a.qkv[qdim + g * 64 + lane];
+      fk = rope2[g * repeat * 32 + lane / 2];
+      vnew = ld4(a.qkv + qdim + kdim + g * 64 + 4 * lp);
+    }
+  }
   float4 ka[kKpl], va[kKpl], kb[kKpl], vb[kKpl];
   load(ka, va, 0);
   float4 qv[M];
+  if constexpr (ROW) {
+    const float qe = norm_rope(xq, fq, lane);
+    if (a.q_out && c == 0) a.q_out[h * 64 + lane] = qe;
+    qv[0] = gather4(qe, lp);
+  } else {
 #pragma unroll
-  for (int r = 0; r < M; r++) qv[r] = ld4(a.q + (static_cast<size_t>(r) * a.n_heads + h) * 64 + 4 * lp);
+    for (int r = 0; r < M; r++) qv[r] = ld4(a.q + (static_cast<size_t>(r) * a.n_heads + h) * 64 + 4 * lp);
+  }
+  // The new key of this wave's chunk: iteration it_pos, key 4 i + lg = slot.
+  float4 knew = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  int it_pos = -1, slot = 0;
+  if (holds) {
+    const float ke = norm_rope(xk, fk, lane);
+    knew = gather4(ke, lp);
+    if (t == 0) {
+      a.k_new[g * 64 + lane] = ke;
+      if (lg == 0) *reinterpret_cast<float4 *>(a.v_new + g * 64 + 4 * lp) = vnew;
+    }
+    it_pos = (pos - key0) / (4 * kKpl);
+    slot = (pos - key0) % (4 * kKpl);
+  }
+  auto patch = [&](float4 (&kk4)[kKpl], float4 (&vv4)[kKpl]) {
+#pragma unroll
+    for (int i = 0; i < kKpl; i++)
+      if (4 * i + lg == slot) {
+        kk4[i] = knew;
+        vv4[i] = vnew;
+      }
+  };
 
   const float ninf = -__builtin_inff();
   float m[M], den[M];
@@ -139,9 +209,11 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(DecArgs a, int iter
   };
   for (int it = 0; it < iters; it += 2) {
     if (it + 1 < iters) load(kb, vb, it + 1);
+    if (ROW && it == it_pos) patch(ka, va);
     consume(ka, va, it);
     if (it + 1 < iters) {
       if (it + 2 < iters) load(ka, va, it + 2);
+      if (ROW && it + 1 == it_pos) patch(kb, vb);
       consume(kb, vb, it + 1);
     }
   }
@@ -161,7 +233,7 @@ __global__ __launch_bounds__(256) void decode_partial_kernel(DecArgs a, int iter
   }
 }
 
-template <int M>
+template <int M, bool ROW = false>
 int launch_rows(Ctx *ctx, DecArgs a, int limit, const float *sinks, float *out, size_t rows) {
   // Keys per wave: enough waves to fill the chip (about 2048), at most
   // kMaxChunks chunks per head, whole 32-key iterations.
@@ -180,7 +252,7 @@ int launch_rows(Ctx *ctx, DecArgs a, int limit, const float *sinks, float *out, 
   a.part_o = static_cast<float *>(ctx->scratch);
   a.part_md = a.part_o + slots * 64;
   const unsigned blocks = static_cast<unsigned>((a.tasks + kWaves - 1) / kWaves);
-  hipLaunchKernelGGL((decode_partial_kernel<M>), dim3(blocks), dim3(64 * kWaves), 0, ctx->stream, a, iters);
+  hipLaunchKernelGGL((decode_partial_kernel<M, ROW>), dim3(blocks), dim3(64 * kWaves), 0, ctx->stream, a, iters);
   FOCR_HIP_CHECK(hipGetLastError());
   CombineArgs c;
   c.part_o = a.part_o;
@@ -202,7 +274,7 @@ int launch_attention_decode(Ctx *ctx, const float *q, const float *prefix_k, con
                             size_t query_offset, size_t image_start, size_t image_end, const float *sinks,
                             float *out) {
   FOCR_REQUIRE(total_len < (size_t(1) << 30) && n_heads <= 4096, FOCR_E_SHAPE, "decode attention: shape too large");
-  DecArgs a;
+  DecArgs a = {};
   a.q = q;
   a.prefix_k = prefix_k;
   a.generated_k = generated_k;
@@ -233,6 +305,31 @@ int launch_attention_decode(Ctx *ctx, const float *q, const float *prefix_k, con
     case 8: return launch_rows<8>(ctx, a, static_cast<int>(limit), sinks, out, query_len);
     default: return set_error(FOCR_E_SHAPE, "decode attention takes 1..=8 query rows");
   }
+}
+
+int launch_attention_decode_row(Ctx *ctx, const float *qkv, const float *rope, const float *prefix_k, float *generated_k,
+                                float *v, size_t prefix_len, size_t total_len, size_t n_heads, size_t n_kv_heads,
+                                size_t image_start, size_t image_end, const float *sinks, float *q_out, float *out) {
+  FOCR_REQUIRE(total_len < (size_t(1) << 30) && n_heads <= 4096, FOCR_E_SHAPE, "decode attention: shape too large");
+  const size_t pos = total_len - 1, kdim = n_kv_heads * 64;
+  DecArgs a = {};
+  a.prefix_k = prefix_k;
+  a.generated_k = generated_k;
+  a.v = v;
+  a.prefix_len = static_cast<int>(prefix_len);
+  a.total_len = static_cast<int>(total_len);
+  a.n_heads = static_cast<int>(n_heads);
+  a.n_kv_heads = static_cast<int>(n_kv_heads);
+  a.query_offset = static_cast<int>(pos);
+  a.image_start = static_cast<int>(image_start);
+  a.image_end = static_cast<int>(image_end);
+  a.qkv = qkv;
+  a.rope = rope;
+  a.q_out = q_out;
+  a.k_new = generated_k + (pos - prefix_len) * kdim;
+  a.v_new = v + pos * kdim;
+  // The row is past the prefix and so past the image: it sees keys 0 ..= pos.
+  return launch_rows<1, true>(ctx, a, static_cast<int>(total_len), sinks, out, 1);
 }
 
 }  // namespace focr

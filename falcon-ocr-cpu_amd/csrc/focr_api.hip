@@ -577,6 +577,24 @@ int focr_attention_decode(focr_ctx *handle, const float *q, const float *prefix_
                                  n_kv_heads, query_offset, image_start, image_end, sinks, out);
 }
 
+int focr_attention_decode_row(focr_ctx *handle, const float *qkv, const float *rope, const float *prefix_k,
+                              float *generated_k, float *v, size_t prefix_len, size_t total_len, size_t n_heads,
+                              size_t n_kv_heads, size_t head_dim, size_t image_start, size_t image_end,
+                              const float *sinks, float *q, float *out) {
+  Ctx *ctx = reinterpret_cast<Ctx *>(handle);
+  FOCR_REQUIRE(ctx, FOCR_E_ARG, "focr_attention_decode_row: null context");
+  FOCR_REQUIRE(head_dim > 0 && n_heads > 0 && n_kv_heads > 0, FOCR_E_SHAPE, "attention head dimensions must be positive");
+  FOCR_REQUIRE(head_dim == 64, FOCR_E_UNSUPPORTED, "the hip decode attention takes head_dim 64");
+  FOCR_REQUIRE(n_heads % n_kv_heads == 0, FOCR_E_SHAPE, "attention GQA grouping");
+  FOCR_REQUIRE(prefix_len < total_len, FOCR_E_SHAPE, "the decode row is a generated row: prefix_len < total_len");
+  FOCR_REQUIRE(image_start <= image_end && image_end <= prefix_len, FOCR_E_SHAPE, "attention image must be inside the prefix");
+  FOCR_REQUIRE(qkv && rope && generated_k && v && sinks && out, FOCR_E_ARG, "focr_attention_decode_row: null buffer");
+  FOCR_REQUIRE(prefix_len == 0 || prefix_k, FOCR_E_ARG, "prefix keys missing");
+  FOCR_HIP_CHECK(hipSetDevice(ctx->device));
+  return launch_attention_decode_row(ctx, qkv, rope, prefix_k, generated_k, v, prefix_len, total_len, n_heads,
+                                     n_kv_heads, image_start, image_end, sinks, q, out);
+}
+
 int focr_argmax(focr_ctx *handle, const float *logits, size_t rows, size_t vocab, uint32_t *tokens) {
   Ctx *ctx = reinterpret_cast<Ctx *>(handle);
   FOCR_REQUIRE(ctx, FOCR_E_ARG, "focr_argmax: null context");

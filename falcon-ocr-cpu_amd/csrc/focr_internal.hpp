@@ -114,6 +114,10 @@ int launch_attention_decode(Ctx *ctx, const float *q, const float *prefix_k, con
                             size_t query_len, size_t prefix_len, size_t total_len, size_t n_heads, size_t n_kv_heads,
                             size_t query_offset, size_t image_start, size_t image_end, const float *sinks,
                             float *out);
+int launch_attention_decode_row(Ctx *ctx, const float *qkv, const float *rope, const float *prefix_k,
+                                float *generated_k, float *v, size_t prefix_len, size_t total_len, size_t n_heads,
+                                size_t n_kv_heads, size_t image_start, size_t image_end, const float *sinks,
+                                float *q_out, float *out);
 
 // ---- device helpers ---------------------------------------------------------
 __device__ __forceinline__ float fmaf_(float a, float b, float c) { return __builtin_fmaf(a, b, c); }

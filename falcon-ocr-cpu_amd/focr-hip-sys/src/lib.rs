@@ -219,6 +219,24 @@ extern "C" {
         sinks_dev: *const f32,
         out_dev: *mut f32,
     ) -> c_int;
+    pub fn focr_attention_decode_row(
+        ctx: *mut focr_ctx,
+        qkv_dev: *const f32,
+        rope_dev: *const f32,
+        prefix_k_dev: *const f32,
+        generated_k_dev: *mut f32,
+        v_dev: *mut f32,
+        prefix_len: usize,
+        total_len: usize,
+        n_heads: usize,
+        n_kv_heads: usize,
+        head_dim: usize,
+        image_start: usize,
+        image_end: usize,
+        sinks_dev: *const f32,
+        q_dev: *mut f32,
+        out_dev: *mut f32,
+    ) -> c_int;
 
     // ---- A9: greedy selection
     pub fn focr_argmax(

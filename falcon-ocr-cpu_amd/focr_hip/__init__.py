@@ -95,6 +95,7 @@ SIGNATURES = {
     "focr_screen_select": (_I, [_P, _P, _P, _P, _Z, _P, _P]),
     "focr_qkv_rows": (_I, [_P, _P, _Z, _P, _Z, _Z, _Z, _Z, _P, _P, _P, _P]),
     "focr_attention_decode": (_I, [_P, _P, _P, _P, _P, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _P, _P]),
+    "focr_attention_decode_row": (_I, [_P] * 6 + [_Z] * 7 + [_P] * 3),
 }
 
 
@@ -429,6 +430,24 @@ def attention_decode(q, kv: CompactKv, query_len: int, geometry: Geometry, sinks
                                        query_len, kv.prefix_len, kv.total_len, kv.n_heads, kv.n_kv_heads,
                                        kv.head_dim, geometry.query_offset, geometry.image_start, geometry.image_end,
                                        _dev(sinks), _dev(output)))
+    return output
+
+
+def attention_decode_row(qkv, rope, kv: CompactKv, image_start: int, image_end: int, sinks, q=None, output=None,
+                         ctx: Optional[Context] = None):
+    """One greedy step in one launch: `qkv_rows` for the generated row at
+    position kv.total_len - 1 (its key and value written to the cache kv
+    views, which must include that row), then `attention_decode` of that row
+    over kv (bitwise the two calls). Returns output [1][n_heads][64]; `q`
+    [1][n_heads][64], if given, receives the rotated query."""
+    torch = _torch()
+    ctx = ctx or default_context()
+    if output is None:
+        output = torch.empty((1, kv.n_heads, kv.head_dim), dtype=torch.float32, device=qkv.device)
+    _check(lib().focr_attention_decode_row(ctx.handle, _dev(qkv), _dev(rope), _dev(kv.prefix_k), _dev(kv.generated_k),
+                                           _dev(kv.v), kv.prefix_len, kv.total_len, kv.n_heads, kv.n_kv_heads,
+                                           kv.head_dim, image_start, image_end, _dev(sinks), _dev(q),
+                                           _dev(output)))
     return output
 
 

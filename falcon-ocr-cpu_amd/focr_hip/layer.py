@@ -50,7 +50,8 @@ from __future__ import annotations
 from typing import Optional
 
 from . import (CompactKv, Context, Epilogue, ExpMode, FocrError, Geometry, KvSplit, PrefillOptions, PrefillProjection,
-               Softmax, attention_prefill_bf16, attention_with, default_context, default_fast_exp, qkv_rows,
+               Softmax, attention_decode_row, attention_prefill_bf16, attention_with, default_context,
+               default_fast_exp, qkv_rows,
                row_scales)
 
 
@@ -187,7 +188,11 @@ class DecoderLayer:
         mark("qkv")
         total = pos + rows
         out = self._buf("dattn", (rows, self.n_heads, 64))
-        if self.split is None:
+        if self.split is None and rows == 1:
+            # The row step, the cache append and the attention in one launch.
+            attn = attention_decode_row(qkv, rope, self.kv(total), *self.image, self.sinks,
+                                        q=self._buf("dq", (1, self.n_heads, 64)), output=out, ctx=ctx)
+        elif self.split is None:
             q = qkv_rows(qkv, rows, rope, self.n_heads, self.n_kv_heads, 0, q=self._buf("dq", (rows, self.n_heads, 64)),
                          generated_k=self.generated_k[pos - p: pos - p + rows], v=self.v[pos: pos + rows], ctx=ctx)
             mark("qkv_rows")

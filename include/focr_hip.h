@@ -237,6 +237,26 @@ int focr_attention_decode(focr_ctx *ctx, const float *q_dev, const float *prefix
                           size_t prefix_len, size_t total_len, size_t n_heads, size_t n_kv_heads,
                           size_t head_dim, size_t query_offset, size_t image_start,
                           size_t image_end, const float *sinks_dev, float *out_dev);
+/* One greedy decode step's attention over a compact cache in one launch:
+ * focr_qkv_rows for one generated row (split_norm_rope, src/model/rope.rs:
+ * 14-86, and LayerCache::append, src/model/cache.rs:117-140) fused with
+ * focr_attention_decode for that row (attention_with -> online::head,
+ * src/kernels/attention/mod.rs:256-311, online.rs:96-150). The row is at
+ * position total_len - 1 (> prefix_len - 1: past the prefix); qkv_dev
+ * [qdim + 2 kdim] and rope_dev [n_heads][32][2] as for focr_qkv_rows; its key
+ * is written to generated_k_dev row total_len - 1 - prefix_len and its value
+ * to v_dev row total_len - 1 (the other arguments as for
+ * focr_attention_decode); its query attends to keys 0 ..= total_len - 1 with
+ * the per-head sink; out_dev [n_heads][64]; q_dev (may be NULL) receives
+ * the normalized, rotated query. Query, cache rows and output are bitwise
+ * those of focr_qkv_rows (rows = 1, prefix_rows = 0) followed by
+ * focr_attention_decode (query_len = 1, query_offset = total_len - 1).
+ * Uses the context scratch. */
+int focr_attention_decode_row(focr_ctx *ctx, const float *qkv_dev, const float *rope_dev,
+                              const float *prefix_k_dev, float *generated_k_dev, float *v_dev,
+                              size_t prefix_len, size_t total_len, size_t n_heads, size_t n_kv_heads,
+                              size_t head_dim, size_t image_start, size_t image_end,
+                              const float *sinks_dev, float *q_dev, float *out_dev);
 
 /* ---- A9: greedy selection ------------------------------------------------ */
 /* argmax of each row (src/runner/mod.rs:916-939): first index of the

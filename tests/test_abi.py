@@ -67,6 +67,7 @@ def test_null_arguments_are_errors_not_crashes():
     assert lib.focr_kv_fast_exp(None, None) == -1
     assert lib.focr_kv_qkv_rows(None, None, None, 1, None, None) == -1
     assert lib.focr_kv_decode_row(None, None, None, None, None, None, None) == -1
+    assert lib.focr_attention_decode_row(None, *([None] * 5), *([0] * 7), None, None, None) == -1
     assert lib.focr_kv_free(None) == 0
     assert lib.focr_ctx_reserve_scratch(None, 1) == -1
     assert lib.focr_ctx_scratch_bytes(None, None) == -1

@@ -132,6 +132,57 @@ def run_decode(fh, q, pk, gk, v, sinks, rows, prefix, total, offset, image, n_kv
     return host(out)
 
 
+@pytest.mark.parametrize("prefix_len,tail", [(1, 0), (64, 0), (700, 2), (16320, 5)])
+def test_decode_row_compact_is_bitwise_the_two_calls(fh, prefix_len, tail):
+    # focr_attention_decode_row = focr_qkv_rows (one generated row) +
+    # focr_attention_decode (query_len 1 at that row), bit for bit: query,
+    # output and the key and value rows it appends, over three steps (the
+    # third with an infinite value input, NaN in group 3's output dims).
+    import torch
+
+    dev = torch.device("cuda:0")
+    cap = prefix_len + tail + 3
+    image = (0, min(prefix_len, 256))
+    pk = gen.normal((prefix_len, H, 64), 1.0, 71)
+    gk = np.full((cap - prefix_len, G, 64), np.nan, np.float32)
+    gk[:tail] = gen.normal((tail, G, 64), 1.0, 72) if tail else gk[:0]
+    v = np.full((cap, G, 64), np.nan, np.float32)
+    v[:prefix_len + tail] = gen.normal((prefix_len + tail, G, 64), 1.0, 73)
+    caches = [(to_dev(pk), to_dev(gk), to_dev(v)) for _ in range(2)]
+    sinks = to_dev(gen.uniform(H, -2.0, 2.0, 74))
+    width = H * 64 + 2 * G * 64
+    for step in range(3):
+        pos = prefix_len + tail + step
+        total = pos + 1
+        qkv = gen.normal((1, width), 2.0, 75 + step)
+        if step == 2:
+            qkv[0, H * 64 + G * 64 + 3 * 64 + 7] = np.inf
+        rope = to_dev(rope_table(1, 80 + step))
+        (pk2, gk2, v2), (pk1, gk1, v1) = caches
+        q2 = fh.qkv_rows(to_dev(qkv), 1, rope, H, G, 0, generated_k=gk2[pos - prefix_len: pos - prefix_len + 1],
+                         v=v2[pos: pos + 1])
+        kv2 = fh.CompactKv(pk2, gk2[: total - prefix_len], v2[:total], prefix_len, total, H, G, 64)
+        out2 = fh.attention_decode(q2, kv2, 1, fh.Geometry(pos, *image), sinks)
+        q1 = torch.empty_like(q2)
+        kv1 = fh.CompactKv(pk1, gk1[: total - prefix_len], v1[:total], prefix_len, total, H, G, 64)
+        out1 = fh.attention_decode_row(to_dev(qkv), rope, kv1, *image, sinks, q=q1)
+        assert_bitwise(host(q1), host(q2), f"step {step} query")
+        assert_bitwise(host(out1), host(out2), f"step {step} output")
+        assert_bitwise(host(gk1), host(gk2), f"step {step} generated keys")
+        assert_bitwise(host(v1), host(v2), f"step {step} values")
+        o = host(out1)[0]
+        if step < 2:
+            assert np.all(np.isfinite(o))
+        else:  # heads 6 and 7 read group 3's values: dim 7 not finite, every other output finite
+            assert not np.any(np.isfinite(o[6:8, 7]))
+            assert np.all(np.isfinite(o[:6])) and np.all(np.isfinite(o[8:])) and np.all(np.isfinite(o[6:8, :7]))
+    # A row inside the prefix is not a generated row: a shape error, nothing launched.
+    with pytest.raises(fh.FocrError):
+        fh.attention_decode_row(to_dev(gen.normal((1, width), 1.0, 79)), rope,
+                                fh.CompactKv(pk1, None, v1[:prefix_len], prefix_len, prefix_len, H, G, 64), 0, 0,
+                                sinks)
+
+
 # The reference's decode cases (decode64.rs tests): causal tile tails, image and
 # generated boundaries, compact crossovers, GQA repeats, full-page and full-context.
 CAUSAL = [1, 2, 17, 63, 64, 127, 128, 129, 143, 144, 161, 255, 256, 257, 1025]

@@ -125,11 +125,22 @@ __device__ __forceinline__ int code_of(float value, float step, double limit) {
 // the smallest subnormal, 0 for an all-zero block, stored as the smallest
 // BF16 at or above it; `nan_step` stores the NaN pattern instead. The max is
 // exact, so the exchange order does not matter. Returns the code; `step`
-// receives the stored BF16.
+// receives the stored BF16. DPP: the exchanges by v_permlane16_swap (the
+// half's two rows) and DPP within the rows instead of five LDS permutes.
+template <bool DPP = false>
 __device__ __forceinline__ int code_lane(float x, bool nan_step, double limit, uint16_t &stored) {
   float mx = __builtin_fmaxf(0.0f, fabsf(x));  // a NaN element counts as 0
+  if constexpr (DPP) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+    mx = __builtin_fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));  // lanes i and i ^ 16
+    mx = __builtin_fmaxf(mx, dpp<0xB1>(mx));   // quad_perm [1,0,3,2]
+    mx = __builtin_fmaxf(mx, dpp<0x4E>(mx));   // quad_perm [2,3,0,1]
+    mx = __builtin_fmaxf(mx, dpp<0x141>(mx));  // row_half_mirror
+    mx = __builtin_fmaxf(mx, dpp<0x140>(mx));  // row_mirror
+  } else {
 #pragma unroll
-  for (int mask = 1; mask < 32; mask *= 2) mx = __builtin_fmaxf(mx, xor_lane(mx, mask));
+    for (int mask = 1; mask < 32; mask *= 2) mx = __builtin_fmaxf(mx, xor_lane(mx, mask));
+  }
   float step = 0.0f;
   if (mx != 0.0f) {
     step = static_cast<float>(static_cast<double>(mx) / limit);
@@ -154,33 +165,50 @@ struct SealArgs {
   int prefix_len, n_heads, n_kv, record_bytes;
 };
 
-// One lane per record element (group-major records of 160 = 5 blocks of 32,
-// so every block is one aligned half-wave): gathers the element, checks the
-// pair sharing (block 0) and finiteness, codes it.
+// Records per seal_kernel lane.
+constexpr int kSealPer = 8;
+
+// Lane = element e of kSealPer records, `pass` records apart (group-major
+// records of 160 = 5 blocks of 32, so every block is one aligned half-wave):
+// gathers the elements (every load issued before any element is coded, so
+// a wave has kSealPer loads in flight instead of one), checks the pair
+// sharing (block 0) and finiteness, codes them.
 template <typename C>
-__global__ __launch_bounds__(256) void seal_kernel(SealArgs a) {
+__global__ __launch_bounds__(256) void seal_kernel(SealArgs a, long pass) {
   const long idx = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
-  const long total = static_cast<long>(a.n_kv) * a.prefix_len * kRecord;
-  const bool valid = idx < total;
-  const long record = valid ? idx / kRecord : 0;
+  const long nrec = static_cast<long>(a.n_kv) * a.prefix_len;
+  const long rec0 = idx / kRecord;
   const int e = static_cast<int>(idx % kRecord);
-  const int g = static_cast<int>(record / a.prefix_len), t = static_cast<int>(record % a.prefix_len);
-  const float *ka = a.k + (static_cast<size_t>(t) * a.n_heads + 2 * g) * 64;
-  const float *src = e < 64 ? ka + e : e < 96 ? ka + 32 + e : a.v + (static_cast<size_t>(t) * a.n_kv + g) * 64 + e - 96;
-  const float x = valid ? *src : 0.0f;
-  uint32_t err = 0;
-  if (valid && !__builtin_isfinite(x)) err |= kErrNonFinite;
-  if (valid && e < 32 && __float_as_uint(x) != __float_as_uint(ka[64 + e])) err |= kErrPair;
-  uint16_t stored;
-  const double limit = sizeof(C) == 1 ? 127.0 : 32767.0;
-  const int code = code_lane(x, false, limit, stored);
-  if (valid) {
-    unsigned char *rec = a.records + static_cast<size_t>(record) * a.record_bytes;
-    reinterpret_cast<C *>(rec)[e] = static_cast<C>(code);
-    if ((e & 31) == 0) reinterpret_cast<uint16_t *>(rec + kRecord * sizeof(C))[e >> 5] = stored;
-    if (!__builtin_isfinite(static_cast<float>(code) * bf16_widen(stored))) err |= kErrOverflow;
-    if (err) atomicOr(a.error, err);
+  float x[kSealPer], pair[kSealPer];
+  bool valid[kSealPer];
+#pragma unroll
+  for (int j = 0; j < kSealPer; j++) {
+    const long record = rec0 + j * pass;
+    valid[j] = rec0 < pass && record < nrec;
+    const long r = valid[j] ? record : 0;
+    const int g = static_cast<int>(r / a.prefix_len), t = static_cast<int>(r % a.prefix_len);
+    const float *ka = a.k + (static_cast<size_t>(t) * a.n_heads + 2 * g) * 64;
+    const float *src =
+        e < 64 ? ka + e : e < 96 ? ka + 32 + e : a.v + (static_cast<size_t>(t) * a.n_kv + g) * 64 + e - 96;
+    x[j] = valid[j] ? *src : 0.0f;
+    pair[j] = valid[j] && e < 32 ? ka[64 + e] : 0.0f;
   }
+  uint32_t err = 0;
+  const double limit = sizeof(C) == 1 ? 127.0 : 32767.0;
+#pragma unroll
+  for (int j = 0; j < kSealPer; j++) {
+    if (valid[j] && !__builtin_isfinite(x[j])) err |= kErrNonFinite;
+    if (valid[j] && e < 32 && __float_as_uint(x[j]) != __float_as_uint(pair[j])) err |= kErrPair;
+    uint16_t stored;
+    const int code = code_lane<true>(x[j], false, limit, stored);
+    if (valid[j]) {
+      unsigned char *rec = a.records + static_cast<size_t>(rec0 + j * pass) * a.record_bytes;
+      reinterpret_cast<C *>(rec)[e] = static_cast<C>(code);
+      if ((e & 31) == 0) reinterpret_cast<uint16_t *>(rec + kRecord * sizeof(C))[e >> 5] = stored;
+      if (!__builtin_isfinite(static_cast<float>(code) * bf16_widen(stored))) err |= kErrOverflow;
+    }
+  }
+  if (err) atomicOr(a.error, err);
 }
 
 struct AppendArgs {
@@ -1031,13 +1059,14 @@ int focr_kv_seal(focr_ctx *handle, int bits, const float *prefix_k, const float 
   s->device_bytes = rec_total + tail_total;
   SealArgs a{prefix_k, v, s->records, s->error, static_cast<int>(prefix_len), s->n_heads, s->n_kv,
              static_cast<int>(s->record_bytes)};
-  const long threads = static_cast<long>(n_kv_heads) * prefix_len * kRecord;
-  const dim3 grid(static_cast<unsigned>((threads + 255) / 256));
+  const long nrec = static_cast<long>(n_kv_heads) * prefix_len;
+  const long pass = (nrec + kSealPer - 1) / kSealPer;
+  const dim3 grid(static_cast<unsigned>((pass * kRecord + 255) / 256));
   static_assert(kRecord % 32 == 0 && kTail % 64 == 0, "blocks are whole half-waves");
   if (bits == 8)
-    hipLaunchKernelGGL(seal_kernel<int8_t>, grid, dim3(256), 0, ctx->stream, a);
+    hipLaunchKernelGGL(seal_kernel<int8_t>, grid, dim3(256), 0, ctx->stream, a, pass);
   else
-    hipLaunchKernelGGL(seal_kernel<int16_t>, grid, dim3(256), 0, ctx->stream, a);
+    hipLaunchKernelGGL(seal_kernel<int16_t>, grid, dim3(256), 0, ctx->stream, a, pass);
   uint32_t err = 0;
   e = hipGetLastError();
   if (e == hipSuccess) e = hipMemcpyAsync(&err, s->error, sizeof(err), hipMemcpyDeviceToHost, ctx->stream);

@@ -774,7 +774,7 @@ int launch_f32_common(bool chain, Ctx *ctx, const Linear *lin, const float *x, s
   // chains, bitwise. The extra HBM traffic, 6 or 8 bytes per weight for
   // INT16 / INT8 codes plus the 4 bytes the GEMM then reads, is small beside
   // the per-tile conversion it replaces (literal 1024 -> 4096 at 6,544 rows:
-  // 16 MiB written, about 4 us, on a GEMM of 0.55-0.75 ms).
+  // 16 MiB written, about 7 us, on a GEMM of 0.54-0.70 ms).
   const bool x16 = reinterpret_cast<uintptr_t>(x) % 16 == 0;
   if (lin->bits != 32 && x16 && a.k % (chain ? kC2K : 4 * kDmaBK) == 0) {
     bool ready = false;

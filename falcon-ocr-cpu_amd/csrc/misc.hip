@@ -26,6 +26,43 @@ __global__ __launch_bounds__(256) void dequantize_kernel(const T *__restrict__ c
   }
 }
 
+// The same, four consecutive weights of a row per thread (k and the group a
+// multiple of 4, fewer than 2^31 weights): 32-bit indexing, one code load,
+// one scale, one 16-byte store.
+template <typename T>
+__global__ __launch_bounds__(256) void dequantize4_kernel(const T *__restrict__ codes, const float *__restrict__ scales,
+                                                          const int16_t *__restrict__ exc_index,
+                                                          const float *__restrict__ exc_vals, int n_exc, int n, int k,
+                                                          int group, int groups, float *__restrict__ out) {
+  const int per_row = k / 4, quads = n * per_row;
+  for (int q = blockIdx.x * 256 + threadIdx.x; q < quads; q += gridDim.x * 256) {
+    const int row = q / per_row, col = (q - row * per_row) * 4;
+    const float sc = scales[static_cast<size_t>(row) * groups + col / group];
+    float w[4];
+    if constexpr (sizeof(T) == 2) {
+      const uint2 u = *reinterpret_cast<const uint2 *>(codes + static_cast<size_t>(q) * 4);
+      w[0] = static_cast<float>(static_cast<int16_t>(u.x & 0xffffu));
+      w[1] = static_cast<float>(static_cast<int16_t>(u.x >> 16));
+      w[2] = static_cast<float>(static_cast<int16_t>(u.y & 0xffffu));
+      w[3] = static_cast<float>(static_cast<int16_t>(u.y >> 16));
+    } else {
+      const uint32_t u = *reinterpret_cast<const uint32_t *>(codes + static_cast<size_t>(q) * 4);
+#pragma unroll
+      for (int i = 0; i < 4; i++) w[i] = static_cast<float>(static_cast<int8_t>((u >> (8 * i)) & 0xffu));
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) w[i] = w[i] * sc;
+    if (exc_index) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int e = exc_index[col + i];
+        if (e >= 0) w[i] = exc_vals[static_cast<size_t>(row) * n_exc + e];
+      }
+    }
+    *reinterpret_cast<float4 *>(out + static_cast<size_t>(q) * 4) = make_float4(w[0], w[1], w[2], w[3]);
+  }
+}
+
 // One 32-element leaf of sum_squares_pairwise (src/kernels/mod.rs:546-552):
 // squares into 32 zero-padded slots, then partial[i] += partial[i + w] for
 // w = 16, 8, 4, 2, 1.
@@ -221,6 +258,23 @@ int launch_dequantize(Ctx *ctx, const Linear *lin, float *out) {
   const size_t total = lin->n * lin->k;
   if (lin->bits == 32) {
     FOCR_HIP_CHECK(hipMemcpyAsync(out, lin->codes, total * sizeof(float), hipMemcpyDeviceToDevice, ctx->stream));
+    return FOCR_OK;
+  }
+  if (lin->k % 4 == 0 && lin->group % 4 == 0 && total < (size_t(1) << 31) &&
+      reinterpret_cast<uintptr_t>(out) % 16 == 0) {
+    const size_t want = (total / 4 + 255) / 256;
+    const int blocks = static_cast<int>(want < 65536 ? want : 65536);
+    const int n = static_cast<int>(lin->n), k = static_cast<int>(lin->k), group = static_cast<int>(lin->group),
+              groups = static_cast<int>(lin->groups), n_exc = static_cast<int>(lin->n_exc);
+    if (lin->bits == 8)
+      hipLaunchKernelGGL(dequantize4_kernel<int8_t>, dim3(blocks), dim3(256), 0, ctx->stream,
+                         static_cast<const int8_t *>(lin->codes), lin->scales, lin->exc_index, lin->exc_vals, n_exc, n,
+                         k, group, groups, out);
+    else
+      hipLaunchKernelGGL(dequantize4_kernel<int16_t>, dim3(blocks), dim3(256), 0, ctx->stream,
+                         static_cast<const int16_t *>(lin->codes), lin->scales, lin->exc_index, lin->exc_vals, n_exc,
+                         n, k, group, groups, out);
+    FOCR_HIP_CHECK(hipGetLastError());
     return FOCR_OK;
   }
   const size_t want = (total + 255) / 256;

@@ -117,14 +117,16 @@ def test_config3_int8_gemv_full_size(fh):
 
 
 @pytest.mark.parametrize("bits,group", [(8, 64), (16, 64), (8, 32), (16, 128)])
-def test_dequantize_is_bit_exact(fh, bits, group):
-    n, k = 48, 300
-    codes, scales, vals = quantized(bits, n, k, group, 11, exc=[0, 299])
+@pytest.mark.parametrize("k", [300, 301])  # four weights per thread; element by element (k % 4 != 0)
+def test_dequantize_is_bit_exact(fh, bits, group, k):
+    n = 48
+    exc = [0, 299]
+    codes, scales, vals = quantized(bits, n, k, group, 11, exc=exc)
     scales = scales.copy()
     scales[0, 0] = np.float32(3e-39)  # subnormal scale
-    lin = fh.QuantLinear(bits, codes, scales, group, exc_cols=[0, 299], exc_vals=vals)
+    lin = fh.QuantLinear(bits, codes, scales, group, exc_cols=exc, exc_vals=vals)
     got = host(lin.dequantize())
-    assert_bitwise(got, oracle.dequantize(bits, codes, scales, n, k, group, [0, 299], vals), "dequant")
+    assert_bitwise(got, oracle.dequantize(bits, codes, scales, n, k, group, exc, vals), "dequant")
 
 
 def test_w8_validation(fh):

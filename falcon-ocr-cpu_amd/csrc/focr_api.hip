@@ -42,25 +42,25 @@ int ensure_scratch(Ctx *ctx, size_t bytes) {
   return FOCR_OK;
 }
 
-int ensure_weights(Ctx *ctx, size_t bytes, bool *ready) {
-  *ready = false;
-  if (bytes <= ctx->weights_bytes) {
-    *ready = true;
+// The context's work moves to a new stream only behind everything already
+// queued on the old one (an event the new stream waits for), so a call on the
+// new stream cannot overwrite the context scratch while an earlier call on
+// the old stream still reads it. A stream under capture cannot wait for an
+// event recorded outside the capture: when either stream is being captured
+// the switch happens without the wait, and the caller orders the two streams
+// (as torch.cuda.graph's side stream is ordered by wait_stream first).
+int order_streams(Ctx *ctx, hipStream_t from, hipStream_t to) {
+  if (from == to) return FOCR_OK;
+  hipStreamCaptureStatus cap_to = hipStreamCaptureStatusNone, cap_from = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(to, &cap_to) != hipSuccess || cap_to != hipStreamCaptureStatusNone ||
+      hipStreamIsCapturing(from, &cap_from) != hipSuccess || cap_from != hipStreamCaptureStatusNone) {
+    // A refused query (the null stream while another stream captures)
+    // leaves no error behind for the next launch check.
+    (void)hipGetLastError();
     return FOCR_OK;
   }
-  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
-  FOCR_HIP_CHECK(hipStreamIsCapturing(ctx->stream, &capture));
-  if (capture != hipStreamCaptureStatusNone) return FOCR_OK;
-  if (ctx->weights) {
-    // Kernels queued earlier may still read the old buffer.
-    FOCR_HIP_CHECK(hipStreamSynchronize(ctx->stream));
-    FOCR_HIP_CHECK(hipFree(ctx->weights));
-    ctx->weights = nullptr;
-    ctx->weights_bytes = 0;
-  }
-  FOCR_HIP_CHECK(hipMalloc(&ctx->weights, bytes));
-  ctx->weights_bytes = bytes;
-  *ready = true;
+  FOCR_HIP_CHECK(hipEventRecord(ctx->order, from));
+  FOCR_HIP_CHECK(hipStreamWaitEvent(to, ctx->order, 0));
   return FOCR_OK;
 }
 
@@ -156,8 +156,15 @@ int focr_ctx_create(int device, focr_ctx **out) {
     return set_error(FOCR_E_HIP, std::string("hipStreamCreate: ") + hipGetErrorString(err));
   }
   ctx->stream = ctx->own;
+  err = hipEventCreateWithFlags(&ctx->order, hipEventDisableTiming);
+  if (err != hipSuccess) {
+    (void)hipStreamDestroy(ctx->own);
+    delete ctx;
+    return set_error(FOCR_E_HIP, std::string("hipEventCreate: ") + hipGetErrorString(err));
+  }
   err = hipMalloc(&ctx->rms_dev, 8 * sizeof(float));
   if (err != hipSuccess) {
+    (void)hipEventDestroy(ctx->order);
     (void)hipStreamDestroy(ctx->own);
     delete ctx;
     return set_error(FOCR_E_HIP, std::string("hipMalloc: ") + hipGetErrorString(err));
@@ -174,7 +181,7 @@ int focr_ctx_destroy(focr_ctx *handle) {
   if (ctx->scratch) FOCR_HIP_CHECK(hipFree(ctx->scratch));
   if (ctx->argmax_dev) FOCR_HIP_CHECK(hipFree(ctx->argmax_dev));
   if (ctx->rms_dev) FOCR_HIP_CHECK(hipFree(ctx->rms_dev));
-  if (ctx->weights) FOCR_HIP_CHECK(hipFree(ctx->weights));
+  FOCR_HIP_CHECK(hipEventDestroy(ctx->order));
   FOCR_HIP_CHECK(hipStreamDestroy(ctx->own));
   delete ctx;
   return FOCR_OK;
@@ -183,6 +190,8 @@ int focr_ctx_destroy(focr_ctx *handle) {
 int focr_ctx_set_stream(focr_ctx *handle, void *stream) {
   Ctx *ctx = reinterpret_cast<Ctx *>(handle);
   FOCR_REQUIRE(ctx, FOCR_E_ARG, "focr_ctx_set_stream: null context");
+  const int rc = order_streams(ctx, ctx->stream, static_cast<hipStream_t>(stream));
+  if (rc != FOCR_OK) return rc;
   ctx->stream = static_cast<hipStream_t>(stream);
   return FOCR_OK;
 }
@@ -190,6 +199,8 @@ int focr_ctx_set_stream(focr_ctx *handle, void *stream) {
 int focr_ctx_use_own_stream(focr_ctx *handle) {
   Ctx *ctx = reinterpret_cast<Ctx *>(handle);
   FOCR_REQUIRE(ctx, FOCR_E_ARG, "focr_ctx_use_own_stream: null context");
+  const int rc = order_streams(ctx, ctx->stream, ctx->own);
+  if (rc != FOCR_OK) return rc;
   ctx->stream = ctx->own;
   return FOCR_OK;
 }

@@ -42,18 +42,11 @@ struct Ctx {
   uint32_t *argmax_dev = nullptr;  // [2 * rows] result words for focr_argmax
   size_t argmax_rows = 0;
   float *rms_dev = nullptr;  // [8] row scales of a decode GEMV whose width has no in-kernel rms_norm
-  // FP32 weights of a code matrix dequantized for one prefill call on the
-  // matrix cores (grown on demand; never during stream capture).
-  float *weights = nullptr;
-  size_t weights_bytes = 0;
+  hipEvent_t order = nullptr;  // orders a new stream after the old one (focr_ctx_set_stream)
 };
 
 // Grows the context scratch to at least `bytes` (hipMalloc on growth only).
 int ensure_scratch(Ctx *ctx, size_t bytes);
-// Grows the context's dequantized-weight buffer to at least `bytes`; sets
-// *ready false, changing nothing, where that would need an allocation while
-// the stream is being captured.
-int ensure_weights(Ctx *ctx, size_t bytes, bool *ready);
 // Resolves the device address of the no-alloc decode scratch for `device`
 // (which must be current); once per device.
 int noalloc_scratch_init(int device);

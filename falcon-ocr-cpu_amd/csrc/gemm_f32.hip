@@ -3,16 +3,18 @@
 // through the Store / Glu / Add epilogues (src/kernels/panels/panel.rs:26-172,
 // driver.rs:57-140; kernels::linear_with_simd's large-M path, mod.rs:434-476).
 //
-// Two kernels:
-//  - mfma_kernel: v_mfma_f32_32x32x2f32 tiles (FP32 inputs, FP32 accumulate).
-//    The matrix core sums k-slices in its own order, so results match the
-//    reference's ascending-k FMA chain within FP32 rounding (tolerance).
+// Kernels:
+//  - dma_kernel (k a multiple of 64) / mfma_kernel (other shapes):
+//    v_mfma_f32_32x32x2f32 tiles (FP32 inputs, FP32 accumulate). The matrix
+//    core sums k-slices in its own order, so results match the reference's
+//    ascending-k FMA chain within FP32 rounding (tolerance).
 //  - chain2_kernel (k a multiple of 16) / chain_kernel (any shape): SIMT
 //    register tiles in which every output is one FMA chain over ascending k
 //    from +0.0: bitwise the reference's FP32 panels.
-// Weights are dequantized while staging into LDS, except where the FP32
-// DMA kernel or the k-major chain kernel takes the shape: there the codes are
-// dequantized into a per-context FP32 buffer first (launch_f32_common).
+// INT16 / INT8 codes are read as codes by every kernel and turned into
+// fl(code * scale) in registers (in dma_kernel as the B fragments are read,
+// in the others on the way into LDS); no FP32 copy of a code matrix is ever
+// written to memory.
 //
 // Roofline: FP32 matrix cores (157.3 TFLOP/s) for mfma_kernel; the FP32
 // vector peak (157.3 TFLOP/s: gfx950 issues even non-packed FMAs faster than
@@ -62,6 +64,7 @@ struct GemmArgs {
   const void *codes;
   const float *scales;
   const int16_t *exc_index;
+  const int32_t *exc_cols;
   const float *exc_vals;
   int n_exc;
   int m, n, k, group, groups;
@@ -294,21 +297,37 @@ __global__ __launch_bounds__(256) void mfma_kernel(GemmArgs a) {
       }
 }
 
-// FP32 weights, k a multiple of 64: A and W stages of 16 k are copied
-// HBM -> LDS by the LDS-DMA path (global_load_lds, 16 bytes per lane) into a
-// ring of four stages, three stages ahead of the matrix cores, so the copies'
-// latency never stalls them and no registers stage the data. Rows of a stage
-// hold 16 floats as four 16-byte chunks, chunk c of row r stored at position
-// c ^ dma_swizzle(r) (conflict-free for the 32-row fragment reads). The row
-// scale is applied to the fragments as they are read (the same single
+// The matrix-core kernel for k a multiple of 64. A' stages of 16 k are
+// copied HBM -> LDS by the LDS-DMA path (global_load_lds, 16 bytes per lane)
+// into a ring of four stages, three stages ahead of the matrix cores, so the
+// copies' latency never stalls them and no registers stage the data. Rows of
+// a stage hold 16 floats as four 16-byte chunks, chunk c of row r stored at
+// position c ^ dma_swizzle(r) (conflict-free for the 32-row fragment reads).
+// The row scale is applied to the fragments as they are read (the same single
 // rounding fl(a * row_scale)). Rows past m or n repeat the last row (in
 // bounds); their outputs are not written.
+//
+// W, by weight type T:
+//  - float: stages copied into a second LDS ring beside A's.
+//  - int16 / int8 codes (group 64): never in LDS and never expanded to FP32
+//    in memory. Each wave loads its own B fragments' codes straight into
+//    registers one 64-k group ahead: lane (half h, column l32) of block j
+//    holds, for stage t of the group, the 8 codes k = 16 t + 8 h + 0..7 of its
+//    column (one 16-byte load for INT16, 8 bytes for INT8; the four loads of
+//    a group cover the column's 128 or 64 code bytes whole) and the group's
+//    scale. A fragment becomes fl(code * scale) in registers as it is read.
+//    The codes of exception columns are zero (upload refuses others), so each
+//    exception adds a'[r][col_e] * value[c][e] to the sums before the
+//    epilogue; the matrix cores sum in their own order anyway.
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(1))) const void global_void;
 
 constexpr int kDmaBK = 16;
 
 __device__ __forceinline__ int dma_swizzle(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+
+// s_waitcnt immediate for vmcnt(n) (n < 64) and lgkmcnt(0), expcnt not waited.
+constexpr int wait_vm_lgkm0(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0070; }
 
 // Compiler-only ordering around the plain workgroup barrier: the waits are
 // explicit (a __syncthreads fence would wait for every copy in flight).
@@ -318,43 +337,75 @@ __device__ __forceinline__ void plain_barrier() {
   asm volatile("" ::: "memory");
 }
 
-template <int EPI, int BN, int BM = 128>
+template <typename T, int EPI, int BN, int BM = 128>
 __global__ __launch_bounds__(256) void dma_kernel(GemmArgs a) {
+  constexpr bool kCodes = !std::is_same<T, float>::value;
   constexpr int WM = BM / 64, WN = BN / 64;
-  constexpr int AT = BM / 64, BT = BN / 64;  // copies of 1 KB per wave per stage
+  constexpr int AT = BM / 64, BT = kCodes ? 0 : BN / 64;  // LDS-DMA copies of 1 KB per wave per stage
   constexpr int PER = AT + BT;
+  constexpr int NB = kCodes ? 5 * WN : 0;  // code-register loads per wave per group: 4 pieces + the scale, per block
+  constexpr int LB = kCodes ? 1 : BN * 4;
+  using Piece = typename std::conditional<sizeof(T) == 1, uint2, uint4>::type;  // 8 codes
   __shared__ float4 la0[BM * 4], la1[BM * 4], la2[BM * 4], la3[BM * 4];
-  __shared__ float4 lb0[BN * 4], lb1[BN * 4], lb2[BN * 4], lb3[BN * 4];
+  __shared__ float4 lb0[LB], lb1[LB], lb2[LB], lb3[LB];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int m0 = a.row0 + blockIdx.x * BM, n0 = blockIdx.y * BN;
   const int h = lane >> 5, l32 = lane & 31;
-  const float *w = static_cast<const float *>(a.codes);
 
   // Copy t of this wave fills LDS chunks [64 (wave + 4 t), +64): row
   // 16 (wave + 4 t) + lane / 4, position lane % 4.
   const float *asrc[AT];
-  const float *bsrc[BT];
+  const float *bsrc[BT > 0 ? BT : 1];
 #pragma unroll
   for (int t = 0; t < AT; t++) {
     const int row = 16 * (wave + 4 * t) + (lane >> 2);
     const int g = m0 + row < a.m ? m0 + row : a.m - 1;
     asrc[t] = a.x + static_cast<size_t>(g) * a.k + 4 * ((lane & 3) ^ dma_swizzle(row));
   }
+  if constexpr (!kCodes) {
+    const float *w = static_cast<const float *>(a.codes);
 #pragma unroll
-  for (int t = 0; t < BT; t++) {
-    const int row = 16 * (wave + 4 * t) + (lane >> 2);
-    const int g = n0 + row < a.n ? n0 + row : a.n - 1;
-    bsrc[t] = w + static_cast<size_t>(g) * a.k + 4 * ((lane & 3) ^ dma_swizzle(row));
+    for (int t = 0; t < BT; t++) {
+      const int row = 16 * (wave + 4 * t) + (lane >> 2);
+      const int g = n0 + row < a.n ? n0 + row : a.n - 1;
+      bsrc[t] = w + static_cast<size_t>(g) * a.k + 4 * ((lane & 3) ^ dma_swizzle(row));
+    }
   }
   auto issue = [&](float4 *la, float4 *lb, int stage) {
     const int off = stage * kDmaBK;
 #pragma unroll
     for (int t = 0; t < AT; t++)
       __builtin_amdgcn_global_load_lds((global_void *)(asrc[t] + off), (lds_void *)(la + 64 * (wave + 4 * t)), 16, 0, 0);
+    if constexpr (!kCodes) {
 #pragma unroll
-    for (int t = 0; t < BT; t++)
-      __builtin_amdgcn_global_load_lds((global_void *)(bsrc[t] + off), (lds_void *)(lb + 64 * (wave + 4 * t)), 16, 0, 0);
+      for (int t = 0; t < BT; t++)
+        __builtin_amdgcn_global_load_lds((global_void *)(bsrc[t] + off), (lds_void *)(lb + 64 * (wave + 4 * t)), 16, 0,
+                                         0);
+    }
+  };
+
+  // Codes: this lane's column of block j, from k = 8 h.
+  const T *csrc[WN];
+  const float *ssrc[WN];
+  Piece nxt[WN][4], cur[WN][4];
+  float nsc[WN], csc[WN];
+  if constexpr (kCodes) {
+#pragma unroll
+    for (int j = 0; j < WN; j++) {
+      const int c = n0 + wn * (BN / 2) + 32 * j + l32;
+      const int cc = c < a.n ? c : a.n - 1;
+      csrc[j] = static_cast<const T *>(a.codes) + static_cast<size_t>(cc) * a.k + 8 * h;
+      ssrc[j] = a.scales + static_cast<size_t>(cc) * a.groups;
+    }
+  }
+  auto load_group = [&](int g) {
+#pragma unroll
+    for (int j = 0; j < WN; j++)
+#pragma unroll
+      for (int t = 0; t < 4; t++) nxt[j][t] = *reinterpret_cast<const Piece *>(csrc[j] + 64 * g + 16 * t);
+#pragma unroll
+    for (int j = 0; j < WN; j++) nsc[j] = ssrc[j][g];
   };
 
   float rs[WM];
@@ -366,7 +417,7 @@ __global__ __launch_bounds__(256) void dma_kernel(GemmArgs a) {
   const bool scaled = a.row_scale != nullptr;
 
   // Lane half h holds k = 8 h .. 8 h + 7 of the stage (chunks 2h, 2h + 1).
-  auto read = [&](const float4 *la, const float4 *lb, float (*va)[8], float (*vb)[8]) {
+  auto read_a = [&](const float4 *la, float (*va)[8]) {
 #pragma unroll
     for (int i = 0; i < WM; i++) {
       const int r = wm * (BM / 2) + 32 * i + l32;
@@ -375,6 +426,8 @@ __global__ __launch_bounds__(256) void dma_kernel(GemmArgs a) {
       va[i][0] = x0.x; va[i][1] = x0.y; va[i][2] = x0.z; va[i][3] = x0.w;
       va[i][4] = x1.x; va[i][5] = x1.y; va[i][6] = x1.z; va[i][7] = x1.w;
     }
+  };
+  auto read_b = [&](const float4 *lb, float (*vb)[8]) {
 #pragma unroll
     for (int j = 0; j < WN; j++) {
       const int r = wn * (BN / 2) + 32 * j + l32;
@@ -382,6 +435,27 @@ __global__ __launch_bounds__(256) void dma_kernel(GemmArgs a) {
       const float4 y1 = lb[4 * r + ((2 * h + 1) ^ dma_swizzle(r))];
       vb[j][0] = y0.x; vb[j][1] = y0.y; vb[j][2] = y0.z; vb[j][3] = y0.w;
       vb[j][4] = y1.x; vb[j][5] = y1.y; vb[j][6] = y1.z; vb[j][7] = y1.w;
+    }
+  };
+  // Stage t of the current group's codes: fl(code * scale), k = 8 h + e.
+  auto codes_b = [&](auto tc, float (*vb)[8]) {
+    constexpr int t = decltype(tc)::value;
+#pragma unroll
+    for (int j = 0; j < WN; j++) {
+      const Piece p = cur[j][t];
+      if constexpr (sizeof(T) == 2) {
+        vb[j][0] = sdwa_cvt<4>(p.x); vb[j][1] = sdwa_cvt<5>(p.x);
+        vb[j][2] = sdwa_cvt<4>(p.y); vb[j][3] = sdwa_cvt<5>(p.y);
+        vb[j][4] = sdwa_cvt<4>(p.z); vb[j][5] = sdwa_cvt<5>(p.z);
+        vb[j][6] = sdwa_cvt<4>(p.w); vb[j][7] = sdwa_cvt<5>(p.w);
+      } else {
+        vb[j][0] = sdwa_cvt<0>(p.x); vb[j][1] = sdwa_cvt<1>(p.x);
+        vb[j][2] = sdwa_cvt<2>(p.x); vb[j][3] = sdwa_cvt<3>(p.x);
+        vb[j][4] = sdwa_cvt<0>(p.y); vb[j][5] = sdwa_cvt<1>(p.y);
+        vb[j][6] = sdwa_cvt<2>(p.y); vb[j][7] = sdwa_cvt<3>(p.y);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; e++) vb[j][e] = vb[j][e] * csc[j];
     }
   };
 
@@ -412,32 +486,92 @@ __global__ __launch_bounds__(256) void dma_kernel(GemmArgs a) {
   // of stage st (and its reads of the previous slot), meet the other waves,
   // start stage st + 3 into the previous stage's slot, read stage st's
   // fragments, then run the products of stage st - 1 while they arrive.
+  // Codes: the first step of group g (st = 4 g) takes the group's codes,
+  // loaded during group g - 1, and loads group g + 1's after stage st + 3's
+  // copies. The waits count the copies issued after stage st's: two stages'
+  // copies, plus group g + 1's code loads in steps 4 g + 1 .. 4 g + 3.
   const int stages = a.k / kDmaBK;  // a multiple of 4
+  const int groups = stages / 4;
   float fa[2][WM][8], fb[2][WN][8];
+  if constexpr (kCodes) load_group(0);
   issue(la0, lb0, 0);
   issue(la1, lb1, 1);
   issue(la2, lb2, 2);
-  auto step = [&](int st, const float4 *ca, const float4 *cb, float4 *na, float4 *nb, float (*ra)[8],
+  auto step = [&](int st, auto uc, const float4 *ca, const float4 *cb, float4 *na, float4 *nb, float (*ra)[8],
                   float (*rb)[8], float (*pa)[8], float (*pb)[8]) __attribute__((always_inline)) {
-    __builtin_amdgcn_s_waitcnt((2 * PER) | 0x0070);  // vmcnt(2 PER) lgkmcnt(0)
+    constexpr int u = decltype(uc)::value;
+    __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(2 * PER + (u == 0 ? 0 : NB)));
     plain_barrier();
     // Past the last stage the copy repeats it into the free slot, so the
-    // count of copies in flight (and the wait above) stays the same.
+    // count of copies in flight (and the waits) stay the same; past the last
+    // group the code loads repeat it.
     issue(na, nb, st + 3 < stages ? st + 3 : stages - 1);
-    read(ca, cb, ra, rb);
+    if constexpr (kCodes) {
+      if constexpr (u == 0) {
+#pragma unroll
+        for (int j = 0; j < WN; j++) {
+#pragma unroll
+          for (int t = 0; t < 4; t++) cur[j][t] = nxt[j][t];
+          csc[j] = nsc[j];
+        }
+        const int g = st / 4 + 1;
+        load_group(g < groups ? g : groups - 1);
+      }
+      read_a(ca, ra);
+      codes_b(uc, rb);
+    } else {
+      read_a(ca, ra);
+      read_b(cb, rb);
+    }
     if (st > 0) products(pa, pb);
   };
+  using U0 = std::integral_constant<int, 0>;
+  using U1 = std::integral_constant<int, 1>;
+  using U2 = std::integral_constant<int, 2>;
+  using U3 = std::integral_constant<int, 3>;
   for (int st = 0; st < stages; st += 4) {
-    step(st, la0, lb0, la3, lb3, fa[0], fb[0], fa[1], fb[1]);
-    step(st + 1, la1, lb1, la0, lb0, fa[1], fb[1], fa[0], fb[0]);
-    step(st + 2, la2, lb2, la1, lb1, fa[0], fb[0], fa[1], fb[1]);
-    step(st + 3, la3, lb3, la2, lb2, fa[1], fb[1], fa[0], fb[0]);
+    step(st, U0(), la0, lb0, la3, lb3, fa[0], fb[0], fa[1], fb[1]);
+    step(st + 1, U1(), la1, lb1, la0, lb0, fa[1], fb[1], fa[0], fb[0]);
+    step(st + 2, U2(), la2, lb2, la1, lb1, fa[0], fb[0], fa[1], fb[1]);
+    step(st + 3, U3(), la3, lb3, la2, lb2, fa[1], fb[1], fa[0], fb[0]);
   }
   products(fa[1], fb[1]);
   // The repeated copies must land before the workgroup's LDS is released.
   __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
 
   // D layout of 32x32: column = lane % 32, row = 8 (r / 4) + 4 (lane / 32) + r % 4.
+  if constexpr (kCodes) {
+    // Exception columns: fl(a * row_scale) times the exception value, one
+    // output row at a time (only its WN sums leave the accumulators).
+    if (a.n_exc) {
+      const float *wv[WN];
+#pragma unroll
+      for (int j = 0; j < WN; j++) {
+        const int c = n0 + wn * (BN / 2) + 32 * j + l32;
+        wv[j] = a.exc_vals + static_cast<size_t>(c < a.n ? c : a.n - 1) * a.n_exc;
+      }
+#pragma unroll
+      for (int i = 0; i < WM; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const int row = m0 + wm * (BM / 2) + i * 32 + 8 * (r / 4) + 4 * h + (r % 4);
+          const int rr = row < a.m ? row : a.m - 1;
+          const float *xr = a.x + static_cast<size_t>(rr) * a.k;
+          const float s = scaled ? a.row_scale[rr] : 1.0f;
+          float sum[WN];
+#pragma unroll
+          for (int j = 0; j < WN; j++) sum[j] = acc[i][j][r];
+          for (int e = 0; e < a.n_exc; e++) {
+            float av = xr[a.exc_cols[e]];
+            if (scaled) av = av * s;
+#pragma unroll
+            for (int j = 0; j < WN; j++) sum[j] = fmaf_(av, wv[j][e], sum[j]);
+          }
+#pragma unroll
+          for (int j = 0; j < WN; j++) acc[i][j][r] = sum[j];
+        }
+    }
+  }
 #pragma unroll
   for (int i = 0; i < WM; i++)
 #pragma unroll
@@ -500,55 +634,52 @@ __global__ __launch_bounds__(256) void chain_kernel(GemmArgs a) {
 // columns 4 tx + 64 j + {0..3}), every output one FMA chain over ascending k
 // from +0.0 (bitwise the FP32 panels). Stages of 16 k are held k-major in
 // LDS, [k][BM] for A' and [k][BN] for W, so a thread reads the values of one
-// k with 16-byte loads; the next stage's A (times the row scale) and codes
-// (dequantized to fl(code * scale), exception columns in place) are loaded
-// into registers before the current stage's FMAs and stored to the other
-// buffer after them.
+// k with 16-byte loads. The next stage's A and weights (FP32, or INT16 / INT8
+// codes and their group's scale) are loaded raw into registers before the
+// current stage's FMAs; only after them are they turned into A' = fl(a *
+// row_scale) and W = fl(code * scale) (exception columns in place) and
+// stored to the other buffer, so no wait for those loads precedes the FMAs.
+// Rows past m and columns past n stage the last row / column in bounds; their
+// outputs are not written.
 constexpr int kC2K = 16;   // k per stage
 constexpr int kC2Pad = 4;  // floats of padding per LDS k-row
 
-// `count` (4 or 8) consecutive dequantized weights of row `row` from column
-// `col` (a multiple of `count`, inside one scale group).
+// COUNT consecutive elements of T (a 4-, 8-, 16- or 32-byte aligned run) as
+// raw 32-bit words.
 template <typename T, int COUNT>
-__device__ __forceinline__ void chain2_weights(const GemmArgs &a, int row, int col, float *w) {
-  const T *codes = static_cast<const T *>(a.codes);
-  const size_t at = static_cast<size_t>(row) * a.k + col;
-  if constexpr (std::is_same<T, float>::value) {
-#pragma unroll
-    for (int q = 0; q < COUNT / 4; q++) {
-      const float4 y = *reinterpret_cast<const float4 *>(codes + at + 4 * q);
-      w[4 * q] = y.x; w[4 * q + 1] = y.y; w[4 * q + 2] = y.z; w[4 * q + 3] = y.w;
-    }
-    return;
+__device__ __forceinline__ void load_raw(const T *p, uint32_t *u) {
+  constexpr int B = COUNT * static_cast<int>(sizeof(T));
+  if constexpr (B == 32) {
+    const uint4 x = reinterpret_cast<const uint4 *>(p)[0], y = reinterpret_cast<const uint4 *>(p)[1];
+    u[0] = x.x; u[1] = x.y; u[2] = x.z; u[3] = x.w; u[4] = y.x; u[5] = y.y; u[6] = y.z; u[7] = y.w;
+  } else if constexpr (B == 16) {
+    const uint4 x = *reinterpret_cast<const uint4 *>(p);
+    u[0] = x.x; u[1] = x.y; u[2] = x.z; u[3] = x.w;
+  } else if constexpr (B == 8) {
+    const uint2 x = *reinterpret_cast<const uint2 *>(p);
+    u[0] = x.x; u[1] = x.y;
   } else {
-    uint32_t u[COUNT * sizeof(T) / 4];
-    if constexpr (COUNT * sizeof(T) == 16) {
-      const uint4 raw = *reinterpret_cast<const uint4 *>(codes + at);
-      u[0] = raw.x; u[1] = raw.y; u[2] = raw.z; u[3] = raw.w;
-    } else if constexpr (COUNT * sizeof(T) == 8) {
-      const uint2 raw = *reinterpret_cast<const uint2 *>(codes + at);
-      u[0] = raw.x; u[1] = raw.y;
-    } else {
-      u[0] = *reinterpret_cast<const uint32_t *>(codes + at);
-    }
+    static_assert(B == 4, "run of 4, 8, 16 or 32 bytes");
+    u[0] = *reinterpret_cast<const uint32_t *>(p);
+  }
+}
+
+// The COUNT weights held raw in `u`: FP32 as they are, codes as
+// fl(code * scale).
+template <typename T, int COUNT>
+__device__ __forceinline__ void weights_of(const uint32_t *u, float scale, float *w) {
 #pragma unroll
-    for (int e = 0; e < COUNT; e++) {
-      if constexpr (sizeof(T) == 2)
-        w[e] = e % 2 == 0 ? sdwa_cvt<4>(u[e / 2]) : sdwa_cvt<5>(u[e / 2]);
-      else
-        w[e] = e % 4 == 0 ? sdwa_cvt<0>(u[e / 4])
-                          : e % 4 == 1 ? sdwa_cvt<1>(u[e / 4]) : e % 4 == 2 ? sdwa_cvt<2>(u[e / 4]) : sdwa_cvt<3>(u[e / 4]);
-    }
-    const float sc = a.scales[static_cast<size_t>(row) * a.groups + col / a.group];
-#pragma unroll
-    for (int e = 0; e < COUNT; e++) w[e] = w[e] * sc;
-    if (a.exc_index) {
-#pragma unroll
-      for (int e = 0; e < COUNT; e++) {
-        const int x = a.exc_index[col + e];
-        if (x >= 0) w[e] = a.exc_vals[static_cast<size_t>(row) * a.n_exc + x];
-      }
-    }
+  for (int e = 0; e < COUNT; e++) {
+    if constexpr (std::is_same<T, float>::value)
+      w[e] = __uint_as_float(u[e]);
+    else if constexpr (sizeof(T) == 2)
+      w[e] = (e % 2 == 0 ? sdwa_cvt<4>(u[e / 2]) : sdwa_cvt<5>(u[e / 2])) * scale;
+    else
+      w[e] = (e % 4 == 0   ? sdwa_cvt<0>(u[e / 4])
+              : e % 4 == 1 ? sdwa_cvt<1>(u[e / 4])
+              : e % 4 == 2 ? sdwa_cvt<2>(u[e / 4])
+                           : sdwa_cvt<3>(u[e / 4])) *
+             scale;
   }
 }
 
@@ -556,6 +687,7 @@ template <typename T, int EPI, int BM, int BN>
 __global__ __launch_bounds__(256) void chain2_kernel(GemmArgs a) {
   constexpr int TM = BM / 16, TN = BN / 16;     // outputs per thread
   constexpr int AK = BM / 16, BK = BN / 16;     // k staged per thread (A, W)
+  constexpr int BW = BK * static_cast<int>(sizeof(T)) / 4;  // raw words of W per thread
   __shared__ float as[2][kC2K][BM + kC2Pad];
   __shared__ float bs[2][kC2K][BN + kC2Pad];
   const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
@@ -566,30 +698,37 @@ __global__ __launch_bounds__(256) void chain2_kernel(GemmArgs a) {
   const int srow = tid / (256 / BM), sk = (tid % (256 / BM)) * AK;
   const int wrow_t = tid / (256 / BN), wk = (tid % (256 / BN)) * BK;
   const int arow = m0 + srow < a.m ? m0 + srow : a.m - 1;
-  const float ascale = m0 + srow < a.m ? (a.row_scale ? a.row_scale[arow] : 1.0f) : 0.0f;
+  const float ascale = a.row_scale ? a.row_scale[arow] : 1.0f;
   const float *aptr = a.x + static_cast<size_t>(arow) * a.k + sk;
-  const bool wlive = n0 + wrow_t < a.n;
-  const int wrow = wlive ? n0 + wrow_t : a.n - 1;
-  float ra[AK], rb[BK];
+  const int wrow = n0 + wrow_t < a.n ? n0 + wrow_t : a.n - 1;
+  const T *wptr = static_cast<const T *>(a.codes) + static_cast<size_t>(wrow) * a.k + wk;
+  const float *sptr = a.scales ? a.scales + static_cast<size_t>(wrow) * a.groups : nullptr;
+  uint32_t ua[AK], ub[BW];
+  float sc = 1.0f;
   auto load = [&](int k0) {
-#pragma unroll
-    for (int q = 0; q < AK / 4; q++) {
-      const float4 x = *reinterpret_cast<const float4 *>(aptr + k0 + 4 * q);
-      const float v[4] = {x.x, x.y, x.z, x.w};
-#pragma unroll
-      for (int e = 0; e < 4; e++)
-        ra[4 * q + e] = a.row_scale ? v[e] * ascale : (ascale != 0.0f ? v[e] : 0.0f);
+    load_raw<float, AK>(aptr + k0, ua);
+    load_raw<T, BK>(wptr + k0, ub);
+    if constexpr (!std::is_same<T, float>::value) {
+      const int col = k0 + wk;
+      sc = sptr[a.group == 64 ? col >> 6 : col / a.group];
     }
-    float w[BK];
-    chain2_weights<T, BK>(a, wrow, k0 + wk, w);
-#pragma unroll
-    for (int e = 0; e < BK; e++) rb[e] = wlive ? w[e] : 0.0f;
   };
-  auto store = [&](int buf) {
+  auto store = [&](int buf, int k0) {
 #pragma unroll
-    for (int e = 0; e < AK; e++) as[buf][sk + e][srow] = ra[e];
+    for (int e = 0; e < AK; e++) as[buf][sk + e][srow] = __uint_as_float(ua[e]) * ascale;
+    float w[BK];
+    weights_of<T, BK>(ub, sc, w);
+    if constexpr (!std::is_same<T, float>::value) {
+      if (a.exc_index) {
 #pragma unroll
-    for (int e = 0; e < BK; e++) bs[buf][wk + e][wrow_t] = rb[e];
+        for (int e = 0; e < BK; e++) {
+          const int x = a.exc_index[k0 + wk + e];
+          if (x >= 0) w[e] = a.exc_vals[static_cast<size_t>(wrow) * a.n_exc + x];
+        }
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < BK; e++) bs[buf][wk + e][wrow_t] = w[e];
   };
 
   float acc[TM][TN];
@@ -620,13 +759,13 @@ __global__ __launch_bounds__(256) void chain2_kernel(GemmArgs a) {
 
   const int stages = a.k / kC2K;
   load(0);
-  store(0);
+  store(0, 0);
   __syncthreads();
   for (int st = 0; st < stages; st++) {
     const int buf = st & 1;
     if (st + 1 < stages) load((st + 1) * kC2K);
     compute(buf);
-    if (st + 1 < stages) store(buf ^ 1);
+    if (st + 1 < stages) store(buf ^ 1, (st + 1) * kC2K);
     __syncthreads();
   }
 #pragma unroll
@@ -647,6 +786,7 @@ GemmArgs make_args(const Linear *lin, const float *x, size_t rows, const float *
   a.codes = lin->codes;
   a.scales = lin->scales;
   a.exc_index = lin->exc_index;
+  a.exc_cols = lin->exc_cols;
   a.exc_vals = lin->exc_vals;
   a.n_exc = static_cast<int>(lin->n_exc);
   a.m = static_cast<int>(rows);
@@ -685,45 +825,46 @@ void launch_one(bool chain, const GemmArgs &a, hipStream_t stream) {
   // workgroups over the 256 compute units (QKV 768 -> 2048 at 6,544 rows
   // measured 0.240 -> 0.231 ms with it).
   const long tiles128 = static_cast<long>((a.m + 127) / 128) * ((a.n + 127) / 128);
-  if constexpr (std::is_same<T, float>::value) {
-    const bool aligned = (reinterpret_cast<uintptr_t>(a.x) | reinterpret_cast<uintptr_t>(a.codes)) % 16 == 0;
-    if (a.k % (4 * kDmaBK) == 0 && aligned) {
-      // 64 x 64 tiles when even 128 x 64 gives fewer than 1,024 (n = 768 at
-      // 6,544 rows: 624 tiles of 128 x 64 on 768 workgroup slots leave a
-      // third of the compute units a tile short at the end; 1,236 tiles of
-      // 64 x 64 on 1,280 slots do not): WO 72.5 -> 85.9 and W2 77.7 -> 87.6
-      // TFLOP/s, outputs unchanged (each one's k order is the tile's).
-      const long tiles128x64 = static_cast<long>((a.m + 127) / 128) * ((a.n + 63) / 64);
-      if (tiles128 >= 1024) {
-        // 128 x 128 tiles take two workgroup slots per compute unit (512 on
-        // the chip). When they leave a last round mostly empty (6,544 x 4096:
-        // 1,664 tiles = 3.25 rounds), the row blocks of whole rounds run as
-        // 128 x 128 tiles and the rows left over as 64 x 64 tiles in a second
-        // launch, if those fit one round of its 1,280 slots (five per compute
-        // unit): the literal shape 0.560 -> 0.538 ms in A/B runs; W13 (3.66
-        // rounds, 1,368 leftover tiles) gained nothing and keeps one launch.
-        // Every output is the same 32 x 32 block computation either way
-        // (bitwise unchanged).
-        const int slots = 512, small_slots = 1280;
-        const int mtiles = (a.m + 127) / 128, ntiles = (a.n + 127) / 128;
-        const int rb = static_cast<int>((tiles128 / slots) * slots / ntiles);  // row blocks of whole rounds
-        const long small = static_cast<long>((a.m - 128 * rb + 63) / 64) * ((a.n + 63) / 64);
-        const bool mostly_empty = tiles128 % slots != 0 && tiles128 % slots <= slots / 2;
-        if (mostly_empty && rb > 0 && rb < mtiles && small <= small_slots) {
-          hipLaunchKernelGGL((dma_kernel<EPI, 128>), dim3(rb, ntiles), dim3(256), 0, stream, a);
-          GemmArgs rest = a;
-          rest.row0 = 128 * rb;
-          hipLaunchKernelGGL((dma_kernel<EPI, 64, 64>), dim3((a.m - rest.row0 + 63) / 64, (a.n + 63) / 64), dim3(256),
-                             0, stream, rest);
-        } else {
-          hipLaunchKernelGGL((dma_kernel<EPI, 128>), dim3(mtiles, ntiles), dim3(256), 0, stream, a);
-        }
-      } else if (tiles128x64 >= 1024)
-        hipLaunchKernelGGL((dma_kernel<EPI, 64>), dim3((a.m + 127) / 128, (a.n + 63) / 64), dim3(256), 0, stream, a);
-      else
-        hipLaunchKernelGGL((dma_kernel<EPI, 64, 64>), dim3((a.m + 63) / 64, (a.n + 63) / 64), dim3(256), 0, stream, a);
-      return;
-    }
+  // The DMA kernel: k a multiple of 64, 16-byte aligned operands, and for
+  // codes one scale per 64-k group.
+  const bool aligned = (reinterpret_cast<uintptr_t>(a.x) | reinterpret_cast<uintptr_t>(a.codes)) % 16 == 0;
+  if (a.k % (4 * kDmaBK) == 0 && aligned && (std::is_same<T, float>::value || a.group == 4 * kDmaBK)) {
+    // 64 x 64 tiles when even 128 x 64 gives fewer than 1,024 (n = 768 at
+    // 6,544 rows: 624 tiles of 128 x 64 on 768 workgroup slots leave a
+    // third of the compute units a tile short at the end; 1,236 tiles of
+    // 64 x 64 on 1,280 slots do not): WO 72.5 -> 85.9 and W2 77.7 -> 87.6
+    // TFLOP/s, outputs unchanged (each one's k order is the tile's).
+    const long tiles128x64 = static_cast<long>((a.m + 127) / 128) * ((a.n + 63) / 64);
+    if (tiles128 >= 1024) {
+      // 128 x 128 tiles take two workgroup slots per compute unit (512 on
+      // the chip). When they leave a last round mostly empty (6,544 x 4096:
+      // 1,664 tiles = 3.25 rounds), the row blocks of whole rounds run as
+      // 128 x 128 tiles and the rows left over as 64 x 64 tiles in a second
+      // launch, if those fit one round of its 1,280 slots (five per compute
+      // unit): the literal shape 0.560 -> 0.538 ms in A/B runs; W13 (3.66
+      // rounds, 1,368 leftover tiles) gained nothing and keeps one launch.
+      // Every output is the same 32 x 32 block computation either way
+      // (bitwise unchanged).
+      const int slots = 512, small_slots = 1280;
+      const int mtiles = (a.m + 127) / 128, ntiles = (a.n + 127) / 128;
+      const int rb = static_cast<int>((tiles128 / slots) * slots / ntiles);  // row blocks of whole rounds
+      const long small = static_cast<long>((a.m - 128 * rb + 63) / 64) * ((a.n + 63) / 64);
+      const bool mostly_empty = tiles128 % slots != 0 && tiles128 % slots <= slots / 2;
+      if (mostly_empty && rb > 0 && rb < mtiles && small <= small_slots) {
+        hipLaunchKernelGGL((dma_kernel<T, EPI, 128>), dim3(rb, ntiles), dim3(256), 0, stream, a);
+        GemmArgs rest = a;
+        rest.row0 = 128 * rb;
+        hipLaunchKernelGGL((dma_kernel<T, EPI, 64, 64>), dim3((a.m - rest.row0 + 63) / 64, (a.n + 63) / 64),
+                           dim3(256), 0, stream, rest);
+      } else {
+        hipLaunchKernelGGL((dma_kernel<T, EPI, 128>), dim3(mtiles, ntiles), dim3(256), 0, stream, a);
+      }
+    } else if (tiles128x64 >= 1024)
+      hipLaunchKernelGGL((dma_kernel<T, EPI, 64>), dim3((a.m + 127) / 128, (a.n + 63) / 64), dim3(256), 0, stream, a);
+    else
+      hipLaunchKernelGGL((dma_kernel<T, EPI, 64, 64>), dim3((a.m + 63) / 64, (a.n + 63) / 64), dim3(256), 0, stream,
+                         a);
+    return;
   }
   // Vector staging needs rows of whole float4 (and whole 32-stages of k).
   const bool vec = a.k % kBK == 0;
@@ -765,34 +906,10 @@ void launch_epi(bool chain, int epilogue, const GemmArgs &a, hipStream_t stream)
 int launch_f32_common(bool chain, Ctx *ctx, const Linear *lin, const float *x, size_t rows, const float *row_scale,
                       int epilogue, float *out) {
   FOCR_REQUIRE(rows < (size_t(1) << 30), FOCR_E_SHAPE, "prefill rows too large");
-  GemmArgs a = make_args(lin, x, rows, row_scale, out);
-  // Codes, where the FP32 kernels take the shape (the DMA kernel on the
-  // matrix cores, the k-major exact-order chain): the weights fl(code *
-  // scale) (exception columns in place, the values the code kernels form
-  // while staging) are dequantized into the context's weight buffer, then
-  // the FP32 kernel runs on them; the chain's outputs are the same FMA
-  // chains, bitwise. The extra HBM traffic, 6 or 8 bytes per weight for
-  // INT16 / INT8 codes plus the 4 bytes the GEMM then reads, is small beside
-  // the per-tile conversion it replaces (literal 1024 -> 4096 at 6,544 rows:
-  // 16 MiB written, about 7 us, on a GEMM of 0.54-0.70 ms).
-  const bool x16 = reinterpret_cast<uintptr_t>(x) % 16 == 0;
-  if (lin->bits != 32 && x16 && a.k % (chain ? kC2K : 4 * kDmaBK) == 0) {
-    bool ready = false;
-    int rc = ensure_weights(ctx, lin->n * lin->k * sizeof(float), &ready);
-    if (rc != FOCR_OK) return rc;
-    if (ready) {
-      rc = launch_dequantize(ctx, lin, ctx->weights);
-      if (rc != FOCR_OK) return rc;
-      a.codes = ctx->weights;
-      a.scales = nullptr;
-      a.exc_index = nullptr;
-      a.exc_vals = nullptr;
-      a.n_exc = 0;
-      launch_epi<float>(chain, epilogue, a, ctx->stream);
-      FOCR_HIP_CHECK(hipGetLastError());
-      return FOCR_OK;
-    }
-  }
+  // Codes stay codes: every kernel forms fl(code * scale) (exception columns
+  // in place) in registers from the uploaded matrix; no FP32 copy of the
+  // weights is written.
+  const GemmArgs a = make_args(lin, x, rows, row_scale, out);
   if (lin->bits == 8)
     launch_epi<int8_t>(chain, epilogue, a, ctx->stream);
   else if (lin->bits == 16)

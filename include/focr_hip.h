@@ -72,9 +72,14 @@ typedef struct focr_kv_split focr_kv_split;
 int focr_ctx_create(int device, focr_ctx **out);
 int focr_ctx_destroy(focr_ctx *ctx);
 /* Run on an existing hipStream_t (e.g. a framework's stream) instead of the
- * context's own; NULL selects the device's default (null) stream. */
+ * context's own; NULL selects the device's default (null) stream. The new
+ * stream first waits (an event) for the work already queued on the old one,
+ * which may still read the context scratch. When either stream is being
+ * captured that wait cannot be recorded and the switch happens without it:
+ * the caller orders the streams itself (e.g. side.wait_stream(current)
+ * before a capture on a side stream). */
 int focr_ctx_set_stream(focr_ctx *ctx, void *hip_stream);
-/* Return to the context's own stream. */
+/* Return to the context's own stream (with the same wait). */
 int focr_ctx_use_own_stream(focr_ctx *ctx);
 void *focr_ctx_stream(const focr_ctx *ctx);
 int focr_ctx_sync(focr_ctx *ctx);
@@ -85,7 +90,13 @@ int focr_ctx_sync(focr_ctx *ctx);
  * into freed memory) and is refused with FOCR_E_UNSUPPORTED while the
  * stream is capturing: a caller that captures reserves the largest size
  * first, or makes one uncaptured call of each shape. Synchronizes the
- * context's stream when it grows. */
+ * context's stream when it grows.
+ * Device buffers a context owns, and so the only addresses of its own that a
+ * captured graph can hold: the scratch (above) and an 8-float row-scale
+ * array allocated at creation (focr_argmax's result words are read back to
+ * the host within the call, which therefore cannot be captured). No
+ * context buffer holds weights: prefill on INT8/INT16 codes reads the codes
+ * and forms fl(code * scale) in registers. */
 int focr_ctx_reserve_scratch(focr_ctx *ctx, size_t bytes);
 int focr_ctx_scratch_bytes(const focr_ctx *ctx, size_t *bytes);
 /* Message of the calling thread's last failure ("" if none). */

@@ -156,9 +156,9 @@ def test_f32_mfma_within_fp32_tolerance(fh, bits, m, k, n):
 
 @pytest.mark.parametrize("bits", [16, 8])
 def test_f32_mfma_on_codes_keeps_exception_columns(fh, bits):
-    # Codes on the matrix cores: k a multiple of 64 dequantizes into the
-    # context's weight buffer first (it grows, then serves a smaller matrix);
-    # k = 100 stages codes in registers. Exception columns in place either way.
+    # Codes on the matrix cores: k a multiple of 64 takes the DMA kernel (codes
+    # loaded into registers, exceptions added before the epilogue); k = 100
+    # the register-staged kernel (exceptions in place).
     for m, k, n in ((13, 768, 64), (40, 1024, 96), (9, 192, 32), (9, 100, 48)):
         columns = [0, k // 2, k - 1]
         w = gen.matrix(n * k, 6).reshape(n, k)
@@ -198,3 +198,82 @@ def test_config1_fp32_gemm_checkpoint_shapes(fh, name, k, n, epi):
         assert np.all(np.abs(got.astype(np.float64) - want) <= 2 * k * EPS * mag + 1e-30), name
     chain = run_prefill(fh, lin, a, m, None, fh.Epilogue(epi), fh.PrefillProjection.F32_CHAIN, base=base)
     assert_bitwise(chain, want, f"{name} chain")
+
+
+@pytest.mark.parametrize("bits", [16, 8])
+@pytest.mark.parametrize("name,k,n,epi", [("qkv", 768, 2048, 0), ("wo", 1024, 768, 2), ("w13", 768, 4608, 1),
+                                          ("w2", 2304, 768, 2), ("literal", 1024, 4096, 0)])
+def test_codes_at_checkpoint_shapes(fh, bits, name, k, n, epi):
+    # Near-exact mode's prefill (INT16 codes on the FP32 panels) and INT8
+    # codes on the FP32 paths, at every checkpoint shape: the codes are read
+    # as codes (no FP32 weight buffer). Chain bitwise the FP32 panels on the
+    # dequantized matrix, matrix cores within the FP32 tolerance; a row scale
+    # and three exception columns.
+    m = 1000
+    a = gen.normal((m, k), 1.0, 20)
+    w = gen.normal((n, k), 0.02, 21)
+    columns = [3, k // 3, k - 2]
+    vals = (w[:, columns] * F32(40.0)).astype(np.float32)
+    w[:, columns] = 0.0
+    codes, scales = oracle.quantize_bits(w, n, k, 64, bits)
+    lin = fh.QuantLinear(bits, codes, scales, 64, exc_cols=columns, exc_vals=vals)
+    dense = oracle.dequantize(bits, codes, scales, n, k, 64, exc_cols=columns, exc_vals=vals)
+    rs = gen.uniform(m, 0.5, 1.5, 22)
+    base = gen.normal((m, n), 1.0, 23) if epi == 2 else None
+    oracle.set_threads(oracle_threads())
+    want = oracle.panel_gemm_fast(a, m, k, dense, n, row_scale=rs, epilogue=epi, out=base)
+    chain = run_prefill(fh, lin, a, m, rs, fh.Epilogue(epi), fh.PrefillProjection.F32_CHAIN, base=base)
+    assert_bitwise(chain, want, f"{name} chain on {bits}-bit codes")
+    got = run_prefill(fh, lin, a, m, rs, fh.Epilogue(epi), fh.PrefillProjection.F32_MFMA, base=base)
+    assert np.all(np.isfinite(got))
+    assert max_rel(got, want) <= 1e-5, name
+    if epi == 0:
+        ad = (a * rs[:, None]).astype(np.float32).astype(np.float64)
+        mag = np.abs(ad) @ np.abs(dense.astype(np.float64)).T
+        assert np.all(np.abs(got.astype(np.float64) - want) <= 2 * k * EPS * mag + 1e-30), name
+
+
+def test_codes_prefill_capture_is_independent_of_later_calls(fh):
+    # A graph captured over prefills on codes holds no context buffer that a
+    # later, larger eager prefill could free: its replays equal the eager
+    # result bit for bit, with larger code prefills run between them.
+    import torch
+
+    ctx = fh.Context(0)
+    m, k, n = 300, 768, 256
+    w = gen.normal((n, k), 0.02, 30)
+    codes, scales = oracle.quantize_bits(w, n, k, 64, 16)
+    lin = fh.QuantLinear(16, codes, scales, 64, ctx=ctx)
+    wb = gen.normal((4 * n, 2 * k), 0.02, 31)
+    codes_b, scales_b = oracle.quantize_bits(wb, 4 * n, 2 * k, 64, 8)
+    big = fh.QuantLinear(8, codes_b, scales_b, 64, ctx=ctx)
+    x = to_dev(gen.normal((m, k), 1.0, 32))
+    xb = to_dev(gen.normal((2 * m, 2 * k), 1.0, 33))
+    out_m = torch.empty((m, n), device="cuda:0")
+    out_c = torch.empty((m, n), device="cuda:0")
+    eager_m = host(lin.prefill(x, m, kernel=fh.PrefillProjection.F32_MFMA))
+    eager_c = host(lin.prefill(x, m, kernel=fh.PrefillProjection.F32_CHAIN))
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            ctx.use_stream(torch.cuda.current_stream())
+            lin.prefill(x, m, out=out_m, kernel=fh.PrefillProjection.F32_MFMA)
+            lin.prefill(x, m, out=out_c, kernel=fh.PrefillProjection.F32_CHAIN)
+    ctx.use_stream(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    for rep in range(3):
+        out_m.fill_(float("nan"))
+        out_c.fill_(float("nan"))
+        big.prefill(xb, 2 * m, kernel=fh.PrefillProjection.F32_MFMA)  # larger eager calls between replays
+        big.prefill(xb, 2 * m, kernel=fh.PrefillProjection.F32_CHAIN)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert_bitwise(host(out_m), eager_m, f"matrix-core replay {rep}")
+        assert_bitwise(host(out_c), eager_c, f"chain replay {rep}")
+    del g
+    lin.free()
+    big.free()
+    ctx.close()

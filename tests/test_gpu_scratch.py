@@ -62,3 +62,39 @@ def test_scratch_growth_refused_during_capture_then_reserved():
         assert_bitwise(host(out), eager, f"replay {rep}")
     lin.free()
     ctx.close()
+
+
+def test_stream_switch_waits_for_the_old_stream():
+    # focr_ctx_set_stream orders the new stream after the work already queued
+    # on the old one. A STORE prefill queued on stream A behind a clock sleep,
+    # then (after the switch) an ADD prefill into the same output on stream B:
+    # B's ADD must see A's STORE, as the same two calls on one stream do.
+    import torch
+
+    import focr_hip as fh
+
+    ctx = fh.Context(0)
+    m, k, n = 96, 256, 128
+    lin = fh.Linear.from_f32(gen.normal((n, k), 0.05, 50), ctx=ctx)
+    x1 = to_dev(gen.normal((m, k), 1.0, 51))
+    x2 = to_dev(gen.normal((m, k), 1.0, 52))
+    chain = fh.PrefillProjection.F32_CHAIN
+    want = lin.prefill(x1, m, kernel=chain)
+    lin.prefill(x2, m, out=want, epilogue=fh.Epilogue.ADD, kernel=chain)
+    torch.cuda.synchronize()
+    want = host(want)
+
+    a_s, b_s = torch.cuda.Stream(), torch.cuda.Stream()
+    out = torch.zeros((m, n), device="cuda:0")
+    torch.cuda.synchronize()
+    with torch.cuda.stream(a_s):
+        torch.cuda._sleep(20_000_000)  # holds stream A for several milliseconds
+    ctx.use_stream(a_s)
+    lin.prefill(x1, m, out=out, kernel=chain)
+    ctx.use_stream(b_s)
+    lin.prefill(x2, m, out=out, epilogue=fh.Epilogue.ADD, kernel=chain)
+    ctx.use_stream(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    assert_bitwise(host(out), want, "ADD on the new stream after STORE on the old")
+    lin.free()
+    ctx.close()

@@ -602,8 +602,8 @@ def host_facts():
 
 
 def cpu_baseline(np, gen, facts, seconds=10.0):
-    """The oracle's INT16 GEMV (reference dot_q order) on the host cores, on the
-    headline matrix. Like the GPU side, calls rotate through a pool of copies
+    """The reference's AVX2 INT16 GEMV (dot_q restated in oracle/focr_cpu_gemv.c,
+    bitwise the oracle) on the host cores, on the headline matrix. Like the GPU side, calls rotate through a pool of copies
     (1 GiB, above any host last-level cache) so weights stream from DRAM."""
     import oracle
 
@@ -615,14 +615,14 @@ def cpu_baseline(np, gen, facts, seconds=10.0):
     scales = gen.uniform((n, k // 64), 1e-6, 4e-6, 2)
     x = gen.normal((1, k), 1.0, 3)
     pool = [(codes.copy(), scales.copy()) for _ in range(max(2, (1 << 30) // codes.nbytes))]
-    oracle.linear_decode(16, codes, scales, n, k, 64, x, 1)
+    oracle.linear_decode(16, codes, scales, n, k, 64, x, 1, fast=True)
     times = []
     t_end = time.perf_counter() + seconds
     i = 0
     while time.perf_counter() < t_end or len(times) < 5:
         c, sc = pool[i % len(pool)]
         t0 = time.perf_counter()
-        oracle.linear_decode(16, c, sc, n, k, 64, x, 1)
+        oracle.linear_decode(16, c, sc, n, k, 64, x, 1, fast=True)
         times.append(time.perf_counter() - t0)
         i += 1
     times.sort()
@@ -630,7 +630,7 @@ def cpu_baseline(np, gen, facts, seconds=10.0):
     oracle.set_threads(1)
     return {"value": round(gemv_bytes(n, k, 1, 2) / med / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"INT16 g64 GEMV W[4096x1024] M=1 over a {len(pool)}-copy pool (1 GiB), median of {len(times)} "
-                      f"calls in ~{seconds:.0f} s (oracle/focr_oracle.c, OpenMP, one thread per physical core of the "
+                      f"calls in ~{seconds:.0f} s (oracle/focr_cpu_gemv.c: the reference's AVX2 dot_q, OpenMP, one thread per physical core of the "
                       f"job's {facts['share']}-CPU host share; host {facts['nproc']} logical CPUs, {facts['model']})",
             "host": facts}
 
@@ -705,6 +705,167 @@ def cpu_prefill_page(np, gen, gpu_gemm, gpu_attention, facts, reps=2):
                       f"{facts['nproc']} logical CPUs ({facts['model']}); oracle/focr_cpu_panels.c (AVX2 6x16 panels), "
                       f"oracle/focr_cpu_attention.c ({'16' if facts['oracle_build'] == 'v4' else '8'}-lane tiles, "
                       "online softmax, Fast exp)"}
+
+
+def cpu_config3(np, gen, gpu_i16, facts, reps=2, gemv_seconds=5.0):
+    """BASELINE config 3 on the host cores, as the reference runs it there:
+    the INT16-activation x INT8-code prefill GEMM of the five shapes on its
+    AVX-512 VNNI panels (oracle/focr_cpu_panels_i16.c: weights packed once as
+    at load, activation quantization inside each call; bitwise the oracle),
+    every logical CPU of the job's share, best of `reps` calls; and the INT8
+    g64 decode GEMV W[4096x1024], M = 1, one thread per physical core over a
+    1 GiB pool of copies, median of ~`gemv_seconds` s of calls."""
+    import oracle
+
+    threads = max(1, facts["share"])
+    oracle.set_threads(threads)
+    m = 6544
+    gemm = {}
+    for name, k, n, epi in (("literal", 1024, 4096, oracle.STORE), ("qkv", 768, 2048, oracle.STORE),
+                            ("wo", 1024, 768, oracle.ADD), ("w13", 768, 4608, oracle.GLU),
+                            ("w2", 2304, 768, oracle.ADD)):
+        a = gen.normal((m, k), 1.0, 7)
+        codes = gen.codes_uniform((n, k), -127, 127, np.int8, 8)
+        scales = gen.uniform((n, k // 64), 1e-4, 4e-4, 9)
+        panels = oracle.I16Panels(codes, scales, n, k)
+        base = np.zeros((m, n), np.float32) if epi == oracle.ADD else None
+        if panels.gemm(a, m, epilogue=epi, out=base) is None:
+            panels.free()
+            return {"skipped": "host CPU without AVX-512 VNNI"}
+        t = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            panels.gemm(a, m, epilogue=epi, out=base)
+            t.append(time.perf_counter() - t0)
+        panels.free()
+        ms = min(t) * 1e3
+        gemm[name] = {"cpu_ms": round(ms, 2), "cpu_tops": round(2.0 * m * k * n / (ms * 1e-3) / 1e12, 3)}
+        if name in gpu_i16:
+            gemm[name]["gpu_ms"] = gpu_i16[name]["ms"]
+            gemm[name]["speedup"] = round(ms / gpu_i16[name]["ms"], 1)
+        log(f"cpu i16 GEMM {name}: {ms:.1f} ms")
+    ghz = (facts.get("max_mhz") or facts.get("mean_mhz") or 0) / 1000.0
+    cores = max(1, facts["physical_cores_in_share"])
+    macs = None
+    if ghz:
+        total_ms = sum(v["cpu_ms"] for v in gemm.values())
+        total_macs = m * sum(k * n for _, k, n in ((0, 1024, 4096), (0, 768, 2048), (0, 1024, 768), (0, 768, 4608),
+                                                    (0, 2304, 768)))
+        macs = {"literal": round(m * 1024 * 4096 / (gemm["literal"]["cpu_ms"] * 1e-3) / (cores * ghz * 1e9), 2),
+                "all_five": round(total_macs / (total_ms * 1e-3) / (cores * ghz * 1e9), 2)}
+    # The INT8 GEMV on the decode team (one thread per physical core).
+    oracle.set_threads(cores)
+    n, k = 4096, 1024
+    codes = gen.codes_uniform((n, k), -127, 127, np.int8, 1)
+    scales = gen.uniform((n, k // 64), 1e-4, 4e-4, 2)
+    x = gen.normal((1, k), 1.0, 3)
+    pool = [(codes.copy(), scales.copy()) for _ in range(max(2, (1 << 30) // codes.nbytes))]
+    oracle.linear_decode(8, codes, scales, n, k, 64, x, 1, fast=True)
+    times, i = [], 0
+    t_end = time.perf_counter() + gemv_seconds
+    while time.perf_counter() < t_end or len(times) < 5:
+        c, sc = pool[i % len(pool)]
+        t0 = time.perf_counter()
+        oracle.linear_decode(8, c, sc, n, k, 64, x, 1, fast=True)
+        times.append(time.perf_counter() - t0)
+        i += 1
+    times.sort()
+    med = times[len(times) // 2]
+    oracle.set_threads(1)
+    return {"gemm": gemm, "gemm_threads": threads, "physical_cores": cores, "ghz_assumed": ghz or None,
+            "gemm_macs_per_cycle_per_core": macs, "reference_macs_per_cycle_per_core": [24.5, 27.4],
+            "gemv_i8_m1": {"cpu_us": round(med * 1e6, 2), "cpu_gbs": round(gemv_bytes(n, k, 1, 1) / med / 1e9, 2),
+                           "threads": cores, "calls": len(times), "pool_copies": len(pool)},
+            "kind": "port",
+            "sample": f"GEMM: the five config-3 shapes at m = 6,544, best of {reps} calls, OpenMP {threads} threads "
+                      f"(the job's host share of {facts['nproc']} logical CPUs, {facts['model']}), "
+                      "oracle/focr_cpu_panels_i16.c (the reference's 6 x 32 vpdpwssd panels); GEMV: "
+                      f"oracle/focr_cpu_gemv.c (the reference's AVX2 dot_q), {cores} threads, median over a 1 GiB pool"}
+
+
+def cpu_layer(np, gen, gpu_layer, facts, steps=64):
+    """BASELINE config 5 on the host cores with the same plan as the GPU's
+    compact-cache run (INT16-activation x INT8-code projections, FP32 online
+    attention, FP32 compact cache): the 16,320-row prefill (row scales, QKV on
+    the VNNI panels, the QKV row step, attention on the 16-lane tiles, WO, W13
+    + GLU, W2) and `steps` decode steps (the reference-order GEMVs, the row
+    step, decode attention over the growing cache), with the same seeded
+    weights and inputs as bench_layer, once; every logical CPU of the share."""
+    import oracle
+
+    threads = max(1, facts["share"])
+    oracle.set_threads(threads)
+    P, img, dim, heads, kv = 16384 - steps, 4096, 768, 16, 8
+    qd, kd, ffn = heads * 64, kv * 64, 2304
+    shapes = {"qkv": (qd + 2 * kd, dim), "wo": (dim, qd), "w13": (2 * ffn, dim), "w2": (dim, ffn)}
+    mats, panels = {}, {}
+    for i, (name, (n, k)) in enumerate(shapes.items()):
+        codes = gen.codes_uniform((n, k), -127, 127, np.int8, 30 + 2 * i)
+        scales = gen.uniform((n, k // 64), 1e-4, 4e-4, 31 + 2 * i)
+        mats[name] = (codes, scales, n, k)
+        panels[name] = oracle.I16Panels(codes, scales, n, k)
+    sinks = gen.uniform(heads, -2.0, 2.0, 40)
+    ang = gen.uniform((P + steps, heads, 32), -3.14159, 3.14159, 41)
+    ang[:, 1::2, :16] = ang[:, 0::2, :16]
+    rope = np.stack([np.cos(ang), np.sin(ang)], -1).astype(np.float32)
+    h = gen.normal((P, dim), 1.0, 42)
+    xs = gen.normal((steps, 1, dim), 1.0, 43)
+    stage = {}
+
+    def timed(name, fn):
+        t0 = time.perf_counter()
+        r = fn()
+        stage[name] = stage.get(name, 0.0) + (time.perf_counter() - t0) * 1e3
+        return r
+
+    if panels["qkv"].gemm(np.zeros((1, dim), np.float32), 1) is None:
+        return {"skipped": "host CPU without AVX-512 VNNI"}
+    t_prefill = time.perf_counter()
+    rs = timed("row_scales", lambda: oracle.row_scales(h, dim))
+    qkv = timed("qkv", lambda: panels["qkv"].gemm(h, P, row_scale=rs))
+    q, pk, _, v = timed("qkv_rows", lambda: oracle.qkv_rows(qkv, P, rope[:P], heads, kv, P))
+    attn = timed("attention", lambda: oracle.attention_prefill_fast(q, pk, v, P, P, P, heads, kv, 0, 0, img, sinks))
+    h = timed("wo", lambda: panels["wo"].gemm(attn.reshape(P, -1), P, epilogue=oracle.ADD, out=h))
+    rs = timed("row_scales", lambda: oracle.row_scales(h, dim))
+    gated = timed("w13", lambda: panels["w13"].gemm(h, P, row_scale=rs, epilogue=oracle.GLU))
+    h = timed("w2", lambda: panels["w2"].gemm(gated, P, epilogue=oracle.ADD, out=h))
+    prefill_ms = (time.perf_counter() - t_prefill) * 1e3
+    log(f"cpu layer prefill: {prefill_ms:.0f} ms {({k: round(t, 1) for k, t in stage.items()})}")
+    # Decode over the compact cache: prefix keys per query head, generated
+    # keys per KV head, values per KV head.
+    gk = np.zeros((steps, kv, 64), np.float32)
+    vals = np.zeros((P + steps, kv, 64), np.float32)
+    vals[:P] = v.reshape(P, kv, 64)
+    dec = lambda name, x, glu=False: (oracle.linear_decode_glu if glu else oracle.linear_decode)(
+        8, mats[name][0], mats[name][1], mats[name][2], mats[name][3], 64, x, 1, fast=True)
+    t_dec = time.perf_counter()
+    for t in range(steps):
+        x = xs[t]
+        qkv1 = dec("qkv", x * oracle.row_scales(x, dim)[:, None])
+        q1, _, nk, nv = oracle.qkv_rows(qkv1, 1, rope[P + t:P + t + 1], heads, kv, 0)
+        gk[t] = nk[0]
+        vals[P + t] = nv[0]
+        a1 = oracle.attention_decode(q1, pk, gk[:t + 1], vals[:P + t + 1], 1, P, P + t + 1, heads, kv, P + t, 0, img,
+                                     sinks, fast=True)
+        x = x + dec("wo", a1.reshape(1, -1))
+        g1 = dec("w13", x * oracle.row_scales(x, dim)[:, None], glu=True)
+        x = x + dec("w2", g1)
+    decode_us = (time.perf_counter() - t_dec) * 1e6 / steps
+    for p in panels.values():
+        p.free()
+    oracle.set_threads(1)
+    res = {"cpu_prefill_ms": round(prefill_ms, 1), "cpu_prefill_stage_ms": {k: round(t, 1) for k, t in stage.items()},
+           "cpu_decode_us_per_step": round(decode_us, 1), "threads": threads, "kind": "port",
+           "sample": f"one layer, prefill of {P} rows then {steps} decode steps, once; OpenMP {threads} threads "
+                     f"(the job's host share of {facts['nproc']} logical CPUs, {facts['model']}); "
+                     "oracle/focr_cpu_panels_i16.c, oracle/focr_cpu_attention.c, oracle/focr_cpu_gemv.c (GEMVs, "
+                     "decode attention), oracle/focr_oracle.c (row scales, row step)"}
+    if gpu_layer:
+        res["gpu_prefill_ms"] = gpu_layer["prefill_ms"]
+        res["gpu_decode_us_per_step"] = gpu_layer["decode_us_per_step"]
+        res["prefill_speedup"] = round(prefill_ms / gpu_layer["prefill_ms"], 1)
+        res["decode_speedup"] = round(decode_us / gpu_layer["decode_us_per_step"], 1)
+    return res
 
 
 def measured_traffic():
@@ -803,6 +964,17 @@ def main():
         per_op["prefill_page_vs_cpu"] = cpu_prefill_page(np, gen, per_op["prefill_f32"], per_op["attention_prefill"],
                                                          facts)
         log(f"prefill page vs CPU: {per_op['prefill_page_vs_cpu']}")
+    if not args.no_cpu and "prefill_i16xi8" in per_op:
+        per_op["config3_vs_cpu"] = cpu_config3(np, gen, per_op["prefill_i16xi8"], facts)
+        log(f"config 3 vs CPU: {per_op['config3_vs_cpu']}")
+        for name, r in per_op["config3_vs_cpu"].get("gemm", {}).items():
+            per_op["prefill_i16xi8"][name]["cpu_ms"] = r["cpu_ms"]
+        if "gemv_i8_m1" in per_op and "gemv_i8_m1" in per_op["config3_vs_cpu"]:
+            per_op["gemv_i8_m1"]["cpu_us"] = per_op["config3_vs_cpu"]["gemv_i8_m1"]["cpu_us"]
+            per_op["gemv_i8_m1"]["cpu_gbs"] = per_op["config3_vs_cpu"]["gemv_i8_m1"]["cpu_gbs"]
+    if not args.no_cpu and "layer_int8_16k" in per_op:
+        per_op["layer_int8_16k"]["cpu"] = cpu_layer(np, gen, per_op["layer_int8_16k"], facts)
+        log(f"config 5 vs CPU: {per_op['layer_int8_16k']['cpu']}")
     cpu = None if args.no_cpu else cpu_baseline(np, gen, facts)
     line = {
         "metric": "decode GEMV HBM GB/s (INT16 group-64, W 4096x1024, M=1)",

@@ -59,6 +59,20 @@ void orc_linear_decode(int bits, const void *codes, const float *scales, size_t 
 void orc_linear_decode_glu(int bits, const void *codes, const float *scales, size_t n, size_t k,
                            size_t group, const int32_t *exc_cols, const float *exc_vals,
                            size_t n_exc, const float *x, size_t rows, float *gated);
+/* The same two calls with the reference's AVX2 dot_q (focr_cpu_gemv.c):
+ * bitwise orc_linear_decode(_glu), at CPU-baseline speed. */
+void orc_linear_decode_fast(int bits, const void *codes, const float *scales, size_t n, size_t k, size_t group,
+                            const int32_t *exc_cols, const float *exc_vals, size_t n_exc, const float *x, size_t rows,
+                            float *out);
+void orc_linear_decode_glu_fast(int bits, const void *codes, const float *scales, size_t n, size_t k, size_t group,
+                                const int32_t *exc_cols, const float *exc_vals, size_t n_exc, const float *x,
+                                size_t rows, float *gated);
+/* orc_attention_decode (head dimension 64) with the reference's AVX2 dot and
+ * axpy (focr_cpu_gemv.c): bitwise the same, CPU-baseline speed. */
+void orc_attention_decode_fast(const float *q, const float *prefix_k, const float *generated_k, const float *v,
+                               size_t query_len, size_t prefix_len, size_t total_len, size_t n_heads,
+                               size_t n_kv_heads, size_t query_offset, size_t image_start, size_t image_end,
+                               const float *sinks, float *out);
 
 /* ---- A6: RMS row scale ------------------------------------------------ */
 /* rms_scale + sum_squares_pairwise, src/kernels/mod.rs:531-553. */
@@ -90,6 +104,17 @@ void orc_i16_gemm(const float *a, size_t m, size_t k, const int8_t *codes, const
 void orc_i16_quantize_rows(const float *a, size_t m, size_t k, const int32_t *exc_cols,
                            size_t n_exc, const float *row_scale, int16_t *codes, float *steps,
                            float *exc_inputs);
+/* The same GEMM with the reference's AVX-512 VNNI panels
+ * (focr_cpu_panels_i16.c): weights packed once per matrix, as at load;
+ * bitwise orc_i16_gemm at CPU-baseline speed. n a multiple of 32, k of 64
+ * (pack returns NULL otherwise). The GEMM returns -1 on a CPU without
+ * AVX-512 VNNI, 0 when done. */
+typedef struct orc_i16_panels orc_i16_panels;
+orc_i16_panels *orc_i16_panels_pack(size_t n, size_t k, const int8_t *codes, const float *scales,
+                                    const int32_t *exc_cols, const float *exc_vals, size_t n_exc);
+void orc_i16_panels_free(orc_i16_panels *p);
+int orc_i16_gemm_fast(const orc_i16_panels *p, const float *a, size_t m, const float *row_scale, int epilogue,
+                      float *out);
 
 /* ---- A8: BF16 prefill attention ---------------------------------------- */
 /* compact_prefill (src/kernels/attention/prefill64/bf16.rs:70-175) for a pure

@@ -78,6 +78,8 @@ _sig("orc_validate_w8", _I, _Z, _Z, _Z, _P, _P)
 _sig("orc_dot", _F, _P, _P, _Z)
 _sig("orc_dot_q", _F, _I, _P, _P, _P, _Z, _Z)
 _sig("orc_linear_decode", None, _I, _P, _P, _Z, _Z, _Z, _P, _P, _Z, _P, _Z, _P)
+_sig("orc_linear_decode_fast", None, _I, _P, _P, _Z, _Z, _Z, _P, _P, _Z, _P, _Z, _P)
+_sig("orc_linear_decode_glu_fast", None, _I, _P, _P, _Z, _Z, _Z, _P, _P, _Z, _P, _Z, _P)
 _sig("orc_linear_decode_glu", None, _I, _P, _P, _Z, _Z, _Z, _P, _P, _Z, _P, _Z, _P)
 _sig("orc_rms_scale", _F, _P, _Z, _F)
 _sig("orc_row_scales", None, _P, _Z, _Z, _F, _P)
@@ -87,6 +89,9 @@ _sig("orc_attention_prefill_fast", None, _P, _P, _P, _P, _Z, _Z, _Z, _Z, _Z, _Z,
 _sig("orc_i16_quantize_group", _F, _P, _P)
 _sig("orc_i16_quantize_rows", None, _P, _Z, _Z, _P, _Z, _P, _P, _P, _P)
 _sig("orc_i16_gemm", None, _P, _Z, _Z, _P, _P, _Z, _P, _P, _Z, _P, _I, _P)
+_sig("orc_i16_panels_pack", _P, _Z, _Z, _P, _P, _P, _P, _Z)
+_sig("orc_i16_panels_free", None, _P)
+_sig("orc_i16_gemm_fast", _I, _P, _P, _Z, _P, _I, _P)
 _sig("orc_attention_prefill", None, _P, _P, _P, _P, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _P, _I, _I, _P)
 _sig("orc_attention_prefill_tiles", None, _P, _P, _P, _P, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _P, _I, _I, _Z, _Z, _P)
 _sig("orc_attention_prefill_bf16_tiles", None, _P, _P, _P, _Z, _Z, _Z, _Z, _Z, _P, _I, _I, _Z, _Z, _P)
@@ -106,6 +111,7 @@ _sig("orc_kv_dequantize", None, _I, _P, _P, _Z, _Z, _Z, _P, _P, _Z, _Z, _P, _P, 
 _sig("orc_qkv_rows", None, _P, _Z, _P, _Z, _Z, _Z, _P, _P, _P, _P)
 _sig("orc_attention_decode", None, _P, _P, _P, _P, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _P, _P)
 _sig("orc_attention_decode_ex", None, _P, _P, _P, _P, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _P, _I, _P)
+_sig("orc_attention_decode_fast", None, _P, _P, _P, _P, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _P, _P)
 _sig("orc_set_threads", None, _I)
 _sig("orc_get_threads", _I)
 
@@ -188,24 +194,26 @@ def dot_q(bits, x, codes, scales, group) -> float:
     return _lib.orc_dot_q(bits, _ptr(x), _ptr(codes), _ptr(scales), x.size, group)
 
 
-def linear_decode(bits, codes, scales, n, k, group, x, rows, exc_cols=None, exc_vals=None):
-    """QuantLinear::linear small-M (bits 8/16) or linear_with_simd rows<=8 (bits 32)."""
+def linear_decode(bits, codes, scales, n, k, group, x, rows, exc_cols=None, exc_vals=None, fast=False):
+    """QuantLinear::linear small-M (bits 8/16) or linear_with_simd rows<=8 (bits 32).
+    fast: the reference's AVX2 dot_q restated (oracle/focr_cpu_gemv.c), the
+    same bits at CPU-baseline speed."""
     codes = np.ascontiguousarray(codes)
     scales = _f32(scales) if scales is not None else np.zeros(1, np.float32)
     x = _f32(x)
     cols, vals, ne = _exc(exc_cols, exc_vals)
     out = np.zeros((rows, n), dtype=np.float32)
-    _lib.orc_linear_decode(bits, _ptr(codes), _ptr(scales), n, k, group, _ptr(cols), _ptr(vals), ne, _ptr(x), rows, _ptr(out))
+    (_lib.orc_linear_decode_fast if fast else _lib.orc_linear_decode)(bits, _ptr(codes), _ptr(scales), n, k, group, _ptr(cols), _ptr(vals), ne, _ptr(x), rows, _ptr(out))
     return out
 
 
-def linear_decode_glu(bits, codes, scales, n, k, group, x, rows, exc_cols=None, exc_vals=None):
+def linear_decode_glu(bits, codes, scales, n, k, group, x, rows, exc_cols=None, exc_vals=None, fast=False):
     codes = np.ascontiguousarray(codes)
     scales = _f32(scales) if scales is not None else np.zeros(1, np.float32)
     x = _f32(x)
     cols, vals, ne = _exc(exc_cols, exc_vals)
     out = np.zeros((rows, n // 2), dtype=np.float32)
-    _lib.orc_linear_decode_glu(bits, _ptr(codes), _ptr(scales), n, k, group, _ptr(cols), _ptr(vals), ne, _ptr(x), rows, _ptr(out))
+    (_lib.orc_linear_decode_glu_fast if fast else _lib.orc_linear_decode_glu)(bits, _ptr(codes), _ptr(scales), n, k, group, _ptr(cols), _ptr(vals), ne, _ptr(x), rows, _ptr(out))
     return out
 
 
@@ -285,6 +293,44 @@ def i16_gemm(a, m, k, codes, scales, n, row_scale=None, epilogue=STORE, exc_cols
     return out
 
 
+class I16Panels:
+    """INT8 codes packed once into the reference's VNNI panels
+    (oracle/focr_cpu_panels_i16.c; panel_i16::pack at load). gemm() is
+    bitwise i16_gemm at CPU-baseline speed; it returns None on a CPU
+    without AVX-512 VNNI."""
+
+    def __init__(self, codes, scales, n, k, exc_cols=None, exc_vals=None):
+        self.n, self.k = n, k
+        self._codes = np.ascontiguousarray(codes, dtype=np.int8)
+        self._scales = _f32(scales)
+        cols, vals, ne = _exc(exc_cols, exc_vals)
+        self.handle = _lib.orc_i16_panels_pack(n, k, _ptr(self._codes), _ptr(self._scales), _ptr(cols), _ptr(vals), ne)
+        if not self.handle:
+            raise ValueError("VNNI panels need n a multiple of 32 and k of 64")
+
+    def gemm(self, a, m, row_scale=None, epilogue=STORE, out=None):
+        a = _f32(a)
+        rs = _f32(row_scale) if row_scale is not None else None
+        width = self.n // 2 if epilogue == GLU else self.n
+        if out is None:
+            out = np.zeros((m, width), dtype=np.float32)
+        else:
+            out = _f32(out).copy()
+        rc = _lib.orc_i16_gemm_fast(self.handle, _ptr(a), m, _ptr(rs), epilogue, _ptr(out))
+        return None if rc == -1 else out
+
+    def free(self):
+        if self.handle:
+            _lib.orc_i16_panels_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
 def attention_prefill(q, prefix_k, v, query_len, prefix_len, total_len, n_heads, n_kv_heads,
                       query_offset, image_start, image_end, sinks, static=False, exp_fast=True,
                       generated_k=None, tiles=None):
@@ -359,14 +405,21 @@ def qkv_rows(qkv, rows, rope, n_heads, n_kv_heads, prefix_rows):
 
 
 def attention_decode(q, prefix_k, generated_k, v, query_len, prefix_len, total_len, n_heads, n_kv_heads,
-                     query_offset, image_start, image_end, sinks, exp_fast=False):
+                     query_offset, image_start, image_end, sinks, exp_fast=False, fast=False):
     """online::head (src/kernels/attention/online.rs:96-150) for every (query, head).
     exp_fast: the per-key probabilities by exp_poly, as the sealed cache's
-    decode with SplitPrefix::fast_exp (src/quant/kv/decode.rs:346-347)."""
+    decode with SplitPrefix::fast_exp (src/quant/kv/decode.rs:346-347).
+    fast: the same bits with the reference's AVX2 dot and axpy
+    (oracle/focr_cpu_gemv.c), CPU-baseline speed (platform exp only)."""
     q, v, sinks = _f32(q), _f32(v), _f32(sinks)
     pk = _f32(prefix_k) if prefix_len else None
     gk = _f32(generated_k) if total_len > prefix_len else None
     out = np.zeros(query_len * n_heads * 64, dtype=np.float32)
+    if fast and not exp_fast:
+        _lib.orc_attention_decode_fast(_ptr(q), _ptr(pk), _ptr(gk), _ptr(v), query_len, prefix_len, total_len,
+                                       n_heads, n_kv_heads, query_offset, image_start, image_end, _ptr(sinks),
+                                       _ptr(out))
+        return out.reshape(query_len, n_heads, 64)
     _lib.orc_attention_decode_ex(_ptr(q), _ptr(pk), _ptr(gk), _ptr(v), query_len, prefix_len, total_len, n_heads,
                                  n_kv_heads, query_offset, image_start, image_end, _ptr(sinks), int(exp_fast),
                                  _ptr(out))

@@ -859,9 +859,26 @@ void launch_one(bool chain, const GemmArgs &a, hipStream_t stream) {
       } else {
         hipLaunchKernelGGL((dma_kernel<T, EPI, 128>), dim3(mtiles, ntiles), dim3(256), 0, stream, a);
       }
-    } else if (tiles128x64 >= 1024)
-      hipLaunchKernelGGL((dma_kernel<T, EPI, 64>), dim3((a.m + 127) / 128, (a.n + 63) / 64), dim3(256), 0, stream, a);
-    else
+    } else if (tiles128x64 >= 1024) {
+      // 128 x 64 tiles take three workgroup slots per compute unit (768 on
+      // the chip); the same split when their last round is at most half full
+      // (QKV 768 -> 2048 at 6,544 rows: 1,664 tiles = 2.17 rounds; 48 row
+      // blocks of whole rounds, then 400 rows as 224 tiles of 64 x 64).
+      const int slots = 768, small_slots = 1280;
+      const int mtiles = (a.m + 127) / 128, ntiles = (a.n + 63) / 64;
+      const int rb = static_cast<int>((tiles128x64 / slots) * slots / ntiles);
+      const long small = static_cast<long>((a.m - 128 * rb + 63) / 64) * ((a.n + 63) / 64);
+      const bool mostly_empty = tiles128x64 % slots != 0 && tiles128x64 % slots <= slots / 2;
+      if (mostly_empty && rb > 0 && rb < mtiles && small <= small_slots) {
+        hipLaunchKernelGGL((dma_kernel<T, EPI, 64>), dim3(rb, ntiles), dim3(256), 0, stream, a);
+        GemmArgs rest = a;
+        rest.row0 = 128 * rb;
+        hipLaunchKernelGGL((dma_kernel<T, EPI, 64, 64>), dim3((a.m - rest.row0 + 63) / 64, (a.n + 63) / 64),
+                           dim3(256), 0, stream, rest);
+      } else {
+        hipLaunchKernelGGL((dma_kernel<T, EPI, 64>), dim3(mtiles, ntiles), dim3(256), 0, stream, a);
+      }
+    } else
       hipLaunchKernelGGL((dma_kernel<T, EPI, 64, 64>), dim3((a.m + 63) / 64, (a.n + 63) / 64), dim3(256), 0, stream,
                          a);
     return;

@@ -13,18 +13,25 @@
 // (the caller evaluates the full head).
 //
 // Two launches per call, all rows (at most 8) together:
-//  1. screen_kernel: up to 768 workgroups stride over tiles of 16 vocabulary
-//     rows, 16 lanes per row (lane 4g + row: 64-channel group g, 64 codes in four
-//     16-byte loads, the next tile's issued before this one is scored), every
-//     input scored against each row as it is loaded. The order is the reference's AVX2
-//     screen_row (two 8-lane FMA chains per group, (a0 + a1) * s_g accumulated
-//     lane-wise over the groups, the AVX2 horizontal sum; S by one FMA chain),
-//     so q, S, the bounds and the candidate set are bit for bit the
-//     reference's. Writes q + B per row and the workgroup's largest q - B.
-//  2. select_kernel: one workgroup per input gathers the rows with
-//     q + B >= tau, computes their FP32 logits in the reference dot order
-//     and picks the largest logit with the smallest index, writing the
-//     result into mapped host memory.
+//  1. screen_kernel: one workgroup per 64 vocabulary rows, lane l row 64 b + l.
+//     The reference's AVX2 screen_row keeps eight phase lanes p per row: two
+//     FMA chains per group (a0 over x[64 g + j + p], a1 over x[64 g + j + 8 + p],
+//     j = 0, 16, 32, 48), (a0 + a1) * s_g accumulated per phase over the
+//     groups, then the AVX2 horizontal sum; S by one FMA chain. Here wave w
+//     runs the phases p = 2w and 2w + 1 of all 64 rows, so the x values a wave
+//     needs at any step are the same for every lane: the inputs are staged in
+//     LDS in the order a wave reads them, and each step's 16 values are four
+//     LDS broadcast reads. The codes are stored at upload in the order one
+//     wave consumes them (16 bytes per row, group and wave: one coalesced 1 KB
+//     load), group-major. The four waves' phase sums meet in LDS for the
+//     horizontal sum, so q, S, the bounds and the candidate set are bit for
+//     bit the reference's. Writes q + B per row and the block's largest q - B
+//     and q + B.
+//  2. select_kernel: one workgroup per input takes tau from the blocks'
+//     maxima, tests only the rows of blocks whose largest q + B reaches tau,
+//     computes the candidates' FP32 logits in the reference dot order and
+//     picks the largest logit with the smallest index, writing the result
+//     into mapped host memory.
 // HBM roofline: the screen reads vocab * (dim + 4 dim / 64) bytes once per
 // call (50.3 MB for 65,536 x 768), plus 4 dim bytes per candidate.
 #include <cmath>
@@ -40,8 +47,7 @@ constexpr int kGroup = 64;
 constexpr int kMaxGroups = 16;     // dim <= 1024: one lane per group, 16 lanes per row
 constexpr int kLimit = 1024;       // CANDIDATE_LIMIT
 constexpr int kMaxRows = 8;        // MAX_ROWS
-constexpr int kRowsPerBlock = 16;  // screen rows per tile (4 waves x 4)
-constexpr int kScreenBlocks = 768;  // screen workgroups (3 per compute unit at its register use)
+constexpr int kBlockRows = 64;     // vocabulary rows per screen workgroup (one per lane)
 constexpr float kEta = 7.888609e-31f;  // 2^-100
 
 }  // namespace
@@ -54,7 +60,8 @@ struct Screen {
   // Per-call state for up to kMaxRows inputs, allocated with the screen so a
   // selection allocates nothing.
   float *upper = nullptr;      // [rows][ustride]: q + B
-  float *block_max = nullptr;  // [rows][blocks]: largest q - B of each workgroup
+  float *block_max = nullptr;    // [rows][blocks]: largest q - B of each 64-row block
+  float *block_upper = nullptr;  // [rows][blocks]: largest q + B of each 64-row block
   uint32_t *words = nullptr;   // [rows][4]: word 2 = prepare's verdict
   // [rows][2] (token, -1 = fallback; candidates) in pinned, mapped host
   // memory, written by the device through result_dev.
@@ -68,7 +75,7 @@ struct ScreenArgs {
   const float *scales;
   const float *x;  // [rows][dim]
   const float *head;  // FP32 head [vocab][dim]
-  float *upper, *block_max;
+  float *upper, *block_max, *block_upper;
   uint32_t *words;
   int32_t *result;
   int vocab, dim, groups, rows, blocks;
@@ -76,53 +83,48 @@ struct ScreenArgs {
   float weight_abs_max, kappa;
 };
 
-// The same sum over the lanes p = lane / 4 < 8 of the screen kernel's lane
-// map (lane = 4 * group + row): p ^ 4, p ^ 1, p ^ 2 are lane ^ 16, ^ 4, ^ 8.
-__device__ __forceinline__ float sum8_stride4(float v) {
-  v = v + __shfl_xor(v, 16, 32);
-  v = v + __shfl_xor(v, 4, 32);
-  v = v + __shfl_xor(v, 8, 32);
-  return v;
+// Device layout of the screen (written at upload, rows padded to a multiple
+// of 64 with zero codes and scales), group-major so that the loads every
+// workgroup issues together cover one contiguous span:
+//  codes  [group][block][wave][lane][16]: wave w's bytes of row 64 block +
+//         lane and group g are, for j = 0, 16, 32, 48, the codes j + 2w,
+//         j + 2w + 1 (chain a0 of phases 2w, 2w + 1) and j + 8 + 2w, j + 9 + 2w
+//         (chain a1);
+//  scales [group][block][lane].
+__host__ __device__ inline size_t screen_code_offset(size_t blocks, size_t block, size_t g, int wave, int lane) {
+  return (((g * blocks + block) * 4 + static_cast<size_t>(wave)) * kBlockRows + static_cast<size_t>(lane)) * 16;
 }
 
-__device__ __forceinline__ float sum8_lanes(float v, int p) {
-  // ((v0+v4)+(v1+v5))+((v2+v6)+(v3+v7)) over lanes p = 0..7 of a row group;
-  // the partner values come by exchange, and a + b = b + a exactly.
-  v = v + __shfl_xor(v, 4, 8);
-  v = v + __shfl_xor(v, 1, 8);
-  v = v + __shfl_xor(v, 2, 8);
-  return v;
-}
+// Staged input blocks: input r, group g at xp[(r * groups + g) * kXBlock],
+// 4 padding floats after each so that lanes reading different blocks at the
+// same offset use distinct LDS banks.
+constexpr int kXBlock = kGroup + 4;
+union ScreenLds {
+  float x[kMaxGroups * kGroup];  // prepare workgroups: the staged input row
+  struct {
+    // The inputs in the order a wave reads them, within a block [wave][16]
+    // with element 4 j + c = x[64 g + 16 j + 2 wave + (0, 1, 8, 9)[c]] (four
+    // 16-byte reads per step, the same address in every lane: an LDS
+    // broadcast), and prepare's norms [input][group].
+    float xp[kMaxRows * kMaxGroups * kXBlock];
+    float norms[kMaxRows * kMaxGroups];
+  } in;
+  float part[kMaxRows][8][kBlockRows];  // per input, phase, row: the phase sums
+};
 
-// Dynamic LDS of screen_kernel: x [rows][groups][68] (each 64-channel group
-// padded by 16 bytes, so neighbouring groups start in different banks; the
-// four lanes of a group read the same address), then the per-(input of a
-// pair, wave, group, row) lane values u [2][4][16][4][8] and scales
-// [4][16][4] (consecutive lanes,
-// consecutive words), then norms [rows][16] and the per-(row, wave) maxima
-// [rows][4].
-constexpr int kXPitch = kGroup + 4;
-__host__ __device__ inline size_t screen_lds_bytes(int rows, int dim) {
-  return sizeof(float) * (static_cast<size_t>(rows) * (dim / kGroup) * kXPitch + 2 * 4 * 4 * kMaxGroups * 8 +
-                          4 * 4 * kMaxGroups + rows * kMaxGroups + rows * 4);
-}
-
+// ROWS inputs (1..8).
+template <int ROWS>
 __global__ __launch_bounds__(256) void screen_kernel(ScreenArgs a) {
-  extern __shared__ float lds[];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int dim = a.dim, groups = a.groups, rows = a.rows;
-  const int xrow = groups * kXPitch;                    // floats per staged input row
-  float *xs = lds;                                      // [rows][groups][kXPitch]
-  float(*u)[4][kMaxGroups][4][8] = reinterpret_cast<float(*)[4][kMaxGroups][4][8]>(xs + rows * xrow);
-  float(*sc)[kMaxGroups][4] = reinterpret_cast<float(*)[kMaxGroups][4]>(xs + rows * xrow + 2 * 4 * 4 * kMaxGroups * 8);
-  float *norms = xs + rows * xrow + 2 * 4 * 4 * kMaxGroups * 8 + 4 * 4 * kMaxGroups;  // [rows][16]
-  float *wmax = norms + rows * kMaxGroups;                  // [rows][4]
-
-  // The first `rows` workgroups run prepare's input checks instead (all
+  __shared__ ScreenLds lds;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int dim = a.dim, groups = a.groups;
+  // The first ROWS workgroups run prepare's input checks instead (all
   // finite; the overflow guard on the f64 L1 norm summed in ascending order)
-  // and clear the later kernels' counters, while the others screen.
-  if (static_cast<int>(blockIdx.x) < rows) {
+  // while the others screen.
+  if (static_cast<int>(blockIdx.x) < ROWS) {
     const int r = blockIdx.x;
+    float *xs = lds.x;
     for (int i = tid; i < dim / 4; i += 256)
       reinterpret_cast<float4 *>(xs)[i] = reinterpret_cast<const float4 *>(a.x + static_cast<size_t>(r) * dim)[i];
     __syncthreads();
@@ -144,167 +146,170 @@ __global__ __launch_bounds__(256) void screen_kernel(ScreenArgs a) {
     }
     return;
   }
-  // Screen workgroup `block` takes tiles block, block + G, ... of 16 rows (4
-  // waves x 4 rows); the next tile's codes are loaded while this one is
-  // scored, and the staging of x and the norms happens once.
-  const int block = blockIdx.x - rows, nblocks = gridDim.x - rows;
-  const int tiles = (a.vocab + kRowsPerBlock - 1) / kRowsPerBlock;
-  // Lane = 4 * group + row: the four rows' lanes of a group are neighbours,
-  // so their reads of the same x address share one LDS access.
-  const int row_in_wave = lane & 3, g = lane >> 2;
-  uint4 raw[4];
-  float scale = 0.0f;
-  auto load_tile = [&](int tile) {
-    const int v = tile * kRowsPerBlock + wave * 4 + row_in_wave;
-    if (tile < tiles && v < a.vocab && g < groups) {
-      const uint4 *src = reinterpret_cast<const uint4 *>(a.codes + static_cast<size_t>(v) * dim + g * kGroup);
+  const int block = blockIdx.x - ROWS;
+  const int v = block * kBlockRows + lane;
+  // The inputs for the staging, then the codes and scales of the lane's row
+  // for kWindow groups (group g + kWindow's loads go out when group g is
+  // converted). Thread t stages inputs' elements 4t .. 4t + 3 (dim <= 1024).
+  const int k4 = 4 * tid;
+  float4 xin[ROWS];
 #pragma unroll
-      for (int i = 0; i < 4; i++) raw[i] = src[i];
-      scale = a.scales[static_cast<size_t>(v) * groups + g];
-    } else {
+  for (int r = 0; r < ROWS; r++)
+    xin[r] = k4 < dim ? *reinterpret_cast<const float4 *>(a.x + static_cast<size_t>(r) * dim + k4)
+                      : make_float4(0.f, 0.f, 0.f, 0.f);
+  constexpr int kWindow = 8;
+  const uint4 *csrc = reinterpret_cast<const uint4 *>(a.codes + screen_code_offset(a.blocks, block, 0, wave, lane));
+  const float *ssrc = a.scales + static_cast<size_t>(block) * kBlockRows + lane;
+  const size_t cstride = static_cast<size_t>(a.blocks) * 4 * kBlockRows, sstride = static_cast<size_t>(a.blocks) * kBlockRows;
+  uint4 raw[kWindow];
+  float sg[kWindow];
 #pragma unroll
-      for (int i = 0; i < 4; i++) raw[i] = make_uint4(0, 0, 0, 0);
-      scale = 0.0f;
-    }
-  };
-  load_tile(block);
-  for (int i = tid; i < rows * dim / 4; i += 256) {
-    const int r = (4 * i) / dim, c = (4 * i) % dim;
-    *reinterpret_cast<float4 *>(xs + r * xrow + (c / kGroup) * kXPitch + c % kGroup) =
-        reinterpret_cast<const float4 *>(a.x)[i];
+  for (int u = 0; u < kWindow; u++) {
+    raw[u] = u < groups ? csrc[u * cstride] : make_uint4(0, 0, 0, 0);
+    sg[u] = u < groups ? ssrc[u * sstride] : 0.0f;
   }
-  __syncthreads();
-  // prepare's per-group L1 norms: exact f64 sums in ascending order, rounded up.
-  // Groups past the last are zero (norm 0, scale 0, lane values 0): their
-  // steps fma(0, 0, acc) leave the chains unchanged (acc is never -0), so the
-  // chains below run a fixed 16 steps without branches.
-  if (tid < rows * kMaxGroups) {
-    const int r = tid / kMaxGroups, gg = tid % kMaxGroups;
+  // Stage: elements m0 .. m0 + 3 of a 16-block (m0 = 0, 4, 8, 12) go to
+  // waves w0, w0 + 1 (w0 = 0 or 2), slots c0, c0 + 1 (c0 = 0 or 2).
+  if (k4 < dim) {
+    const int g = k4 / kGroup, j = (k4 % kGroup) / 16, m0 = k4 % 16;
+    const int w0 = (m0 & 4) >> 1, c0 = (m0 >> 3) << 1;
+#pragma unroll
+    for (int r = 0; r < ROWS; r++) {
+      float *dst = lds.in.xp + (r * groups + g) * kXBlock + w0 * 16 + 4 * j + c0;
+      *reinterpret_cast<float2 *>(dst) = make_float2(xin[r].x, xin[r].y);
+      *reinterpret_cast<float2 *>(dst + 16) = make_float2(xin[r].z, xin[r].w);
+    }
+  }
+  // Plain barriers: LDS writes complete (lgkmcnt(0)); the code loads stay in
+  // flight.
+  auto lds_barrier = []() __attribute__((always_inline)) {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+  lds_barrier();
+  // prepare's per-group L1 norms (exact f64 sums in ascending order, rounded
+  // up): thread 16 r + g, from the staged block. x[64 g + 16 j + m] sits in
+  // the wave (m & 7) / 2 slice at 4 j + (m & 1) + 2 (m >> 3).
+  if (tid < ROWS * kMaxGroups) {
+    const int r = tid / kMaxGroups, g = tid % kMaxGroups;
     float n = 0.0f;
-    if (gg < groups) {
+    if (g < groups) {
+      const float *blk = lds.in.xp + (r * groups + g) * kXBlock;
       double exact = 0.0;
-#pragma unroll 16
-      for (int i = 0; i < kGroup; i++) exact += static_cast<double>(fabsf(xs[r * xrow + gg * kXPitch + i]));
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        float4 q[4];
+#pragma unroll
+        for (int w = 0; w < 4; w++) q[w] = *reinterpret_cast<const float4 *>(blk + 16 * w + 4 * j);
+#pragma unroll
+        for (int w = 0; w < 4; w++) {  // m = 2w, 2w + 1
+          exact += static_cast<double>(fabsf(q[w].x));
+          exact += static_cast<double>(fabsf(q[w].y));
+        }
+#pragma unroll
+        for (int w = 0; w < 4; w++) {  // m = 8 + 2w, 9 + 2w
+          exact += static_cast<double>(fabsf(q[w].z));
+          exact += static_cast<double>(fabsf(q[w].w));
+        }
+      }
       const float rounded = static_cast<float>(exact);
       // next_up of a finite rounded >= 0: the next bit pattern.
       n = static_cast<double>(rounded) < exact ? __uint_as_float(__float_as_uint(rounded) + 1u) : rounded;
     }
-    norms[r * kMaxGroups + gg] = n;
+    lds.in.norms[tid] = n;
   }
-  __syncthreads();
-  float wave_lower[kMaxRows];
-#pragma unroll
-  for (int r = 0; r < kMaxRows; r++) wave_lower[r] = -__builtin_inff();
+  lds_barrier();
 
-  for (int tile = block; tile < tiles; tile += nblocks) {
-    const int v = tile * kRowsPerBlock + wave * 4 + row_in_wave;
-    const bool live = v < a.vocab;
-    const bool active = live && g < groups;
-    // This tile's codes as floats (once for every input), then the next
-    // tile's loads go out.
-    float cf[kGroup];
+  // Phase sums row[p] of p = 2 wave + e for every input, and S.
+  float acc[ROWS][2], total[ROWS];
 #pragma unroll
-    for (int i = 0; i < kGroup; i += 4) {
-      const uint32_t word = (&raw[i >> 4].x)[(i >> 2) & 3];
-      cf[i] = sdwa_cvt<0>(word);
-      cf[i + 1] = sdwa_cvt<1>(word);
-      cf[i + 2] = sdwa_cvt<2>(word);
-      cf[i + 3] = sdwa_cvt<3>(word);
-    }
-    sc[wave][g][row_in_wave] = scale;
-    load_tile(tile + nblocks);
-    // The row's 16 group scales, read once for every input (lanes g < 8 use
-    // them; the write above is this wave's own and is waited for here).
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    float ss[kMaxGroups];
+  for (int r = 0; r < ROWS; r++) acc[r][0] = acc[r][1] = total[r] = 0.0f;
+  for (int g0 = 0; g0 < groups; g0 += kWindow) {
 #pragma unroll
-    for (int gg = 0; gg < kMaxGroups; gg++) ss[gg] = sc[wave][gg][row_in_wave];
-
-    // screen_row's group step for input r into LDS slice `half`: a0 over
-    // x[base + j + p], a1 over x[base + j + 8 + p], j = 0, 16, 32, 48; then
-    // a0 + a1 per lane p.
-    auto products = [&](int r, int half) {
-      float4 *dst = reinterpret_cast<float4 *>(u[half][wave][g][row_in_wave]);
-      if (!active) {
-        dst[0] = dst[1] = make_float4(0.f, 0.f, 0.f, 0.f);
-        return;
+    for (int u = 0; u < kWindow; u++) {
+      const int g = g0 + u;
+      if (g >= groups) break;
+      float cf[16];
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const uint32_t word = (&raw[u].x)[i];
+        cf[4 * i] = sdwa_cvt<0>(word);
+        cf[4 * i + 1] = sdwa_cvt<1>(word);
+        cf[4 * i + 2] = sdwa_cvt<2>(word);
+        cf[4 * i + 3] = sdwa_cvt<3>(word);
       }
-      const float4 *xg = reinterpret_cast<const float4 *>(xs + r * xrow + g * kXPitch);
-      float a0[8], a1[8];
-#pragma unroll
-      for (int p = 0; p < 8; p++) a0[p] = a1[p] = 0.0f;
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const float4 x0 = xg[4 * j], x1 = xg[4 * j + 1], x2 = xg[4 * j + 2], x3 = xg[4 * j + 3];
-        const float xa[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-        const float xb[8] = {x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
-#pragma unroll
-        for (int p = 0; p < 8; p++) {
-          a0[p] = __builtin_fmaf(xa[p], cf[16 * j + p], a0[p]);
-          a1[p] = __builtin_fmaf(xb[p], cf[16 * j + 8 + p], a1[p]);
-        }
+      const float s = sg[u];
+      if (g + kWindow < groups) {
+        raw[u] = csrc[(g + kWindow) * cstride];
+        sg[u] = ssrc[(g + kWindow) * sstride];
       }
-      dst[0] = make_float4(a0[0] + a1[0], a0[1] + a1[1], a0[2] + a1[2], a0[3] + a1[3]);
-      dst[1] = make_float4(a0[4] + a1[4], a0[5] + a1[5], a0[6] + a1[6], a0[7] + a1[7]);
-    };
-    // Inputs go in pairs: both inputs' products, then lanes g < 8 finish
-    // input r0 and lanes g >= 8 input r0 + 1 (each a 32-lane half of the
-    // wave), so the exchange and its waits happen once per pair.
-    for (int r0 = 0; r0 < rows; r0 += 2) {
-      products(r0, 0);
-      if (r0 + 1 < rows) products(r0 + 1, 1);
-      // The row's 16 lanes exchange through this wave's own LDS slices.
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      const int half = g >> 3, p = g & 7;
-      const int r = r0 + half;
-      if (live && r < rows) {
-        // Lane p accumulates row[p] = fma(a0 + a1, s_g, row[p]) over the
-        // groups; S = sum fma(s_g, n_g, S) alongside.
-        float uu[kMaxGroups];
 #pragma unroll
-        for (int gg = 0; gg < kMaxGroups; gg++) uu[gg] = u[half][wave][gg][row_in_wave][p];
-        float acc = 0.0f, total = 0.0f;
+      for (int r = 0; r < ROWS; r++) {
+        const float4 *xq = reinterpret_cast<const float4 *>(lds.in.xp + (r * groups + g) * kXBlock + wave * 16);
+        const float n = lds.in.norms[r * kMaxGroups + g];
+        float a00 = 0.0f, a01 = 0.0f, a10 = 0.0f, a11 = 0.0f;
 #pragma unroll
-        for (int gg = 0; gg < kMaxGroups; gg++) {
-          acc = __builtin_fmaf(uu[gg], ss[gg], acc);
-          total = __builtin_fmaf(ss[gg], norms[r * kMaxGroups + gg], total);
+        for (int j = 0; j < 4; j++) {
+          const float4 xv = xq[j];
+          a00 = __builtin_fmaf(xv.x, cf[4 * j], a00);
+          a01 = __builtin_fmaf(xv.y, cf[4 * j + 1], a01);
+          a10 = __builtin_fmaf(xv.z, cf[4 * j + 2], a10);
+          a11 = __builtin_fmaf(xv.w, cf[4 * j + 3], a11);
         }
-        const float q = sum8_stride4(acc);  // within this lane's 32-lane half
-        const float bound = __builtin_fmaf(a.kappa, total, kEta);
-        if (p == 0) {
-          a.upper[static_cast<size_t>(r) * a.ustride + v] = q + bound;
-          // f32::max: a NaN operand is ignored. (Indexed by the pair's
-          // uniform r0, so the array stays in registers.)
-          if (half == 0)
-            wave_lower[r0] = __builtin_fmaxf(wave_lower[r0], q - bound);
-          else
-            wave_lower[r0 + 1] = __builtin_fmaxf(wave_lower[r0 + 1], q - bound);
-        }
+        acc[r][0] = __builtin_fmaf(a00 + a10, s, acc[r][0]);
+        acc[r][1] = __builtin_fmaf(a01 + a11, s, acc[r][1]);
+        total[r] = __builtin_fmaf(s, n, total[r]);
       }
-      // The next pair's products overwrite these slices only after every
-      // lane has read them.
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
   }
-  // The workgroup's largest q - B per input.
-  for (int r = 0; r < rows; r++) {
-    float m = wave_lower[r];
+  __syncthreads();  // every wave is done with xp before part overwrites it
+  // The horizontal sum ((v0 + v4) + (v1 + v5)) + ((v2 + v6) + (v3 + v7)) of
+  // each input's eight phases; wave w finishes the inputs r = w, w + 4.
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, off));
-    if (lane == 0) wmax[r * 4 + wave] = m;
+  for (int r = 0; r < ROWS; r++) {
+    lds.part[r][2 * wave][lane] = acc[r][0];
+    lds.part[r][2 * wave + 1][lane] = acc[r][1];
   }
   __syncthreads();
-  if (tid < rows) {
-    float m = -__builtin_inff();
-    for (int w = 0; w < 4; w++) m = __builtin_fmaxf(m, wmax[tid * 4 + w]);
-    a.block_max[static_cast<size_t>(tid) * a.blocks + block] = m;
+#pragma unroll
+  for (int r = 0; r < ROWS; r++) {
+    if ((r & 3) != wave) continue;
+    float p8[8];
+#pragma unroll
+    for (int p = 0; p < 8; p++) p8[p] = lds.part[r][p][lane];
+    const float q = ((p8[0] + p8[4]) + (p8[1] + p8[5])) + ((p8[2] + p8[6]) + (p8[3] + p8[7]));
+    const float bound = __builtin_fmaf(a.kappa, total[r], kEta);
+    // f32::max: a NaN operand is ignored. The block's largest q + B lets
+    // the selection skip blocks that hold no candidate.
+    float lower = -__builtin_inff(), high = -__builtin_inff();
+    if (v < a.vocab) {
+      const float hi = q + bound;
+      a.upper[static_cast<size_t>(r) * a.ustride + v] = hi;
+      lower = __builtin_fmaxf(lower, q - bound);
+      high = __builtin_fmaxf(high, hi);
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      lower = __builtin_fmaxf(lower, __shfl_xor(lower, off));
+      high = __builtin_fmaxf(high, __shfl_xor(high, off));
+    }
+    if (lane == 0) {
+      a.block_max[static_cast<size_t>(r) * a.blocks + block] = lower;
+      a.block_upper[static_cast<size_t>(r) * a.blocks + block] = high;
+    }
   }
+}
+
+// The same sum over eight lanes p of a row group as the reference's AVX2
+// horizontal sum: ((v0+v4)+(v1+v5))+((v2+v6)+(v3+v7)), partner values by
+// exchange (a + b = b + a exactly).
+__device__ __forceinline__ float sum8_lanes(float v, int p) {
+  v = v + __shfl_xor(v, 4, 8);
+  v = v + __shfl_xor(v, 1, 8);
+  v = v + __shfl_xor(v, 2, 8);
+  return v;
 }
 
 // The reference dot of x and one FP32 head row: 32 phase lanes (a0..a3 of
@@ -336,9 +341,10 @@ __device__ float reference_dot(const float *x, const float *w, int len, int lane
   return total;
 }
 
-// One workgroup per input: tau = the largest q - B (from the screen's
-// workgroup maxima); the rows with q + B >= tau are gathered into an LDS list
-// (one slot counter update per wave); then wave w computes the FP32 logits of
+// One workgroup per input: tau = the largest q - B (from the blocks'
+// maxima); the 64-row blocks whose largest q + B reaches tau are listed, and
+// only their rows are tested: the rows with q + B >= tau go into an LDS list
+// (one slot counter update per wave). Then wave w computes the FP32 logits of
 // list entries w, w + 16, ... and keeps the largest with the smallest row, and
 // the workgroup combines the waves. The reference visits candidates in
 // ascending order with a strict >, i.e. the first index of the maximum; more
@@ -346,60 +352,56 @@ __device__ float reference_dot(const float *x, const float *w, int len, int lane
 __global__ __launch_bounds__(1024) void select_kernel(ScreenArgs a) {
   __shared__ float red[16];
   __shared__ uint32_t list[kLimit];
-  __shared__ uint32_t count_s;
+  __shared__ uint32_t hot[kLimit];
+  __shared__ uint32_t count_s, hot_s;
   __shared__ float best_v[16];
   __shared__ uint32_t best_i[16];
   __shared__ int bad[16];
   const int r = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  float m = -__builtin_inff();
-  for (int b = tid; b < a.blocks; b += 1024) m = __builtin_fmaxf(m, a.block_max[static_cast<size_t>(r) * a.blocks + b]);
+  const float *bmax = a.block_max + static_cast<size_t>(r) * a.blocks;
+  const float *bup = a.block_upper + static_cast<size_t>(r) * a.blocks;
+  // Both block arrays' first 1024 entries are loaded together.
+  const float up0 = tid < a.blocks ? bup[tid] : -__builtin_inff();
+  float m = tid < a.blocks ? bmax[tid] : -__builtin_inff();
+  for (int b = tid + 1024; b < a.blocks; b += 1024) m = __builtin_fmaxf(m, bmax[b]);
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, off));
   if (lane == 0) red[wave] = m;
-  if (tid == 0) count_s = 0;
+  if (tid == 0) count_s = hot_s = 0;
   __syncthreads();
   float tau = -__builtin_inff();
   for (int w = 0; w < 16; w++) tau = __builtin_fmaxf(tau, red[w]);
   const bool ok = a.words[4 * r + 2] != 0 && __builtin_isfinite(tau);
+  // Append the lanes' hits to an LDS list: one counter update per wave.
+  auto append = [&](bool hit, uint32_t value, uint32_t *dst, uint32_t *counter) {
+    const uint64_t hits = __ballot(hit);
+    if (hits == 0) return;
+    const int first = __builtin_ctzll(hits);
+    uint32_t slot0 = 0;
+    if (lane == first) slot0 = atomicAdd(counter, static_cast<uint32_t>(__builtin_popcountll(hits)));
+    slot0 = __shfl(slot0, first);
+    if (hit) {
+      const uint32_t slot = slot0 + static_cast<uint32_t>(__builtin_popcountll(hits & ((uint64_t(1) << lane) - 1)));
+      if (slot < static_cast<uint32_t>(kLimit)) dst[slot] = value;
+    }
+  };
   if (ok) {
+    // Every block that holds a candidate has its largest q + B >= tau, so
+    // more than kLimit such blocks means more than kLimit candidates.
+    append(tid < a.blocks && up0 >= tau, static_cast<uint32_t>(tid), hot, &hot_s);
+    for (int b = tid + 1024; b - tid < a.blocks; b += 1024) append(b < a.blocks && bup[b] >= tau, b, hot, &hot_s);
+  }
+  __syncthreads();
+  const uint32_t n_hot = hot_s;
+  if (ok && n_hot <= static_cast<uint32_t>(kLimit)) {
     const float *upper = a.upper + static_cast<size_t>(r) * a.ustride;
-    // Chunks of 64 Ki rows: every thread's 16 float4 loads go out first.
-    for (int base = 0; base < a.vocab; base += 16 * 4096) {
-      float4 val[16];
-#pragma unroll
-      for (int i = 0; i < 16; i++) {
-        const int v0 = base + 4 * (1024 * i + tid);
-        if (v0 + 3 < a.vocab) {
-          val[i] = *reinterpret_cast<const float4 *>(upper + v0);
-        } else {
-          float t[4];
-#pragma unroll
-          for (int e = 0; e < 4; e++) t[e] = v0 + e < a.vocab ? upper[v0 + e] : -__builtin_inff();
-          val[i] = make_float4(t[0], t[1], t[2], t[3]);
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < 16; i++)
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const int v = base + 4 * (1024 * i + tid) + e;
-          const bool hit = v < a.vocab && (&val[i].x)[e] >= tau;
-          const uint64_t hits = __ballot(hit);
-          if (hits == 0) continue;
-          const int first = __builtin_ctzll(hits);
-          uint32_t slot0 = 0;
-          if (lane == first) slot0 = atomicAdd(&count_s, static_cast<uint32_t>(__builtin_popcountll(hits)));
-          slot0 = __shfl(slot0, first);
-          if (hit) {
-            const uint32_t slot =
-                slot0 + static_cast<uint32_t>(__builtin_popcountll(hits & ((uint64_t(1) << lane) - 1)));
-            if (slot < static_cast<uint32_t>(kLimit)) list[slot] = static_cast<uint32_t>(v);
-          }
-        }
+    for (uint32_t i = wave; i < n_hot; i += 16) {
+      const int v = static_cast<int>(hot[i]) * kBlockRows + lane;
+      append(v < a.vocab && upper[v] >= tau, static_cast<uint32_t>(v), list, &count_s);
     }
   }
   __syncthreads();
-  const uint32_t count = count_s;
+  const uint32_t count = n_hot > static_cast<uint32_t>(kLimit) ? static_cast<uint32_t>(kLimit) + 1 : count_s;
   const bool run = ok && count <= static_cast<uint32_t>(kLimit);
   float bv = -__builtin_inff();
   uint32_t bi = 0xffffffffu;
@@ -496,7 +498,7 @@ float screen_kappa(size_t dim) {
 }
 
 void free_screen(Screen *s) {
-  void *ptrs[] = {s->codes, s->scales, s->upper, s->block_max, s->words};
+  void *ptrs[] = {s->codes, s->scales, s->upper, s->block_max, s->block_upper, s->words};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
   if (s->host_result) (void)hipHostFree(s->host_result);
@@ -505,28 +507,52 @@ void free_screen(Screen *s) {
 int create_screen(Ctx *ctx, const int8_t *codes, const float *scales, size_t vocab, size_t dim, float wmax,
                   float kappa, focr_screen **out) {
   FOCR_HIP_CHECK(hipSetDevice(ctx->device));
+  const size_t groups = dim / kGroup;
+  const size_t blocks = (vocab + kBlockRows - 1) / kBlockRows;
+  // The device layout (screen_code_offset): each wave's 16 code bytes of a
+  // row and group in the order its two phases consume them.
+  std::vector<int8_t> dev_codes(blocks * kBlockRows * dim, 0);
+  std::vector<float> dev_scales(blocks * groups * kBlockRows, 0.0f);
+  for (size_t v = 0; v < vocab; v++) {
+    const size_t b = v / kBlockRows;
+    const int l = static_cast<int>(v % kBlockRows);
+    for (size_t g = 0; g < groups; g++) {
+      dev_scales[(g * blocks + b) * kBlockRows + static_cast<size_t>(l)] = scales[v * groups + g];
+      const int8_t *src = codes + v * dim + g * kGroup;
+      for (int w = 0; w < 4; w++) {
+        int8_t *dst = dev_codes.data() + screen_code_offset(blocks, b, g, w, l);
+        for (int j = 0; j < 4; j++) {
+          dst[4 * j] = src[16 * j + 2 * w];
+          dst[4 * j + 1] = src[16 * j + 2 * w + 1];
+          dst[4 * j + 2] = src[16 * j + 8 + 2 * w];
+          dst[4 * j + 3] = src[16 * j + 9 + 2 * w];
+        }
+      }
+    }
+  }
   Screen *s = new Screen();
   s->vocab = vocab;
   s->dim = dim;
-  s->groups = dim / kGroup;
-  const size_t tiles = (vocab + kRowsPerBlock - 1) / kRowsPerBlock;
-  s->blocks = tiles < static_cast<size_t>(kScreenBlocks) ? tiles : static_cast<size_t>(kScreenBlocks);
+  s->groups = groups;
+  s->blocks = blocks;
   s->weight_abs_max = wmax;
   s->kappa = kappa;
   auto alloc = [&](void **p, size_t bytes) { return hipMalloc(p, bytes); };
   hipError_t e = hipSuccess;
-  if (e == hipSuccess) e = alloc(reinterpret_cast<void **>(&s->codes), vocab * dim);
-  if (e == hipSuccess) e = alloc(reinterpret_cast<void **>(&s->scales), vocab * s->groups * sizeof(float));
+  if (e == hipSuccess) e = alloc(reinterpret_cast<void **>(&s->codes), dev_codes.size());
+  if (e == hipSuccess) e = alloc(reinterpret_cast<void **>(&s->scales), dev_scales.size() * sizeof(float));
   s->ustride = (vocab + 3) / 4 * 4;
   if (e == hipSuccess) e = alloc(reinterpret_cast<void **>(&s->upper), kMaxRows * s->ustride * sizeof(float));
   if (e == hipSuccess) e = alloc(reinterpret_cast<void **>(&s->block_max), kMaxRows * s->blocks * sizeof(float));
+  if (e == hipSuccess) e = alloc(reinterpret_cast<void **>(&s->block_upper), kMaxRows * s->blocks * sizeof(float));
   if (e == hipSuccess) e = alloc(reinterpret_cast<void **>(&s->words), kMaxRows * 4 * sizeof(uint32_t));
   if (e == hipSuccess)
     e = hipHostMalloc(reinterpret_cast<void **>(&s->host_result), kMaxRows * 2 * sizeof(int32_t),
                       hipHostMallocMapped | hipHostMallocCoherent);
   if (e == hipSuccess) e = hipHostGetDevicePointer(reinterpret_cast<void **>(&s->result_dev), s->host_result, 0);
-  if (e == hipSuccess) e = hipMemcpy(s->codes, codes, vocab * dim, hipMemcpyHostToDevice);
-  if (e == hipSuccess) e = hipMemcpy(s->scales, scales, vocab * s->groups * sizeof(float), hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(s->codes, dev_codes.data(), dev_codes.size(), hipMemcpyHostToDevice);
+  if (e == hipSuccess)
+    e = hipMemcpy(s->scales, dev_scales.data(), dev_scales.size() * sizeof(float), hipMemcpyHostToDevice);
   if (e != hipSuccess) {
     free_screen(s);
     delete s;
@@ -597,6 +623,16 @@ int focr_screen_constants(const focr_screen *handle, float *weight_abs_max, floa
   return FOCR_OK;
 }
 
+int focr_screen_bounds(const focr_screen *handle, size_t rows, float *upper_host) {
+  const Screen *s = reinterpret_cast<const Screen *>(handle);
+  FOCR_REQUIRE(s && upper_host, FOCR_E_ARG, "focr_screen_bounds: null argument");
+  FOCR_REQUIRE(rows >= 1 && rows <= static_cast<size_t>(kMaxRows), FOCR_E_SHAPE, "screened head: 1 to 8 input rows");
+  for (size_t r = 0; r < rows; r++)
+    FOCR_HIP_CHECK(hipMemcpy(upper_host + r * s->vocab, s->upper + r * s->ustride, s->vocab * sizeof(float),
+                             hipMemcpyDeviceToHost));
+  return FOCR_OK;
+}
+
 int focr_screen_select(focr_ctx *handle, const focr_screen *sh, const focr_linear *head_handle, const float *x,
                        size_t rows, int32_t *tokens, uint32_t *candidates) {
   Ctx *ctx = reinterpret_cast<Ctx *>(handle);
@@ -614,6 +650,7 @@ int focr_screen_select(focr_ctx *handle, const focr_screen *sh, const focr_linea
   a.head = static_cast<const float *>(head->codes);
   a.upper = s->upper;
   a.block_max = s->block_max;
+  a.block_upper = s->block_upper;
   a.words = s->words;
   a.result = s->result_dev;
   a.vocab = static_cast<int>(s->vocab);
@@ -624,8 +661,17 @@ int focr_screen_select(focr_ctx *handle, const focr_screen *sh, const focr_linea
   a.ustride = static_cast<int>(s->ustride);
   a.weight_abs_max = s->weight_abs_max;
   a.kappa = s->kappa;
-  hipLaunchKernelGGL(screen_kernel, dim3(a.blocks + a.rows), dim3(256), screen_lds_bytes(a.rows, a.dim), ctx->stream,
-                     a);
+  const dim3 grid(static_cast<unsigned>(a.blocks + a.rows));
+  switch (rows) {
+    case 1: hipLaunchKernelGGL(screen_kernel<1>, grid, dim3(256), 0, ctx->stream, a); break;
+    case 2: hipLaunchKernelGGL(screen_kernel<2>, grid, dim3(256), 0, ctx->stream, a); break;
+    case 3: hipLaunchKernelGGL(screen_kernel<3>, grid, dim3(256), 0, ctx->stream, a); break;
+    case 4: hipLaunchKernelGGL(screen_kernel<4>, grid, dim3(256), 0, ctx->stream, a); break;
+    case 5: hipLaunchKernelGGL(screen_kernel<5>, grid, dim3(256), 0, ctx->stream, a); break;
+    case 6: hipLaunchKernelGGL(screen_kernel<6>, grid, dim3(256), 0, ctx->stream, a); break;
+    case 7: hipLaunchKernelGGL(screen_kernel<7>, grid, dim3(256), 0, ctx->stream, a); break;
+    default: hipLaunchKernelGGL(screen_kernel<8>, grid, dim3(256), 0, ctx->stream, a); break;
+  }
   hipLaunchKernelGGL(select_kernel, dim3(a.rows), dim3(1024), 0, ctx->stream, a);
   FOCR_HIP_CHECK(hipGetLastError());
   // select_kernel wrote the results straight into the mapped host buffer.

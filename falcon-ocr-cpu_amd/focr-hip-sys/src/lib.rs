@@ -340,6 +340,7 @@ extern "C" {
     ) -> c_int;
     pub fn focr_screen_free(screen: *mut focr_screen) -> c_int;
     pub fn focr_screen_constants(screen: *const focr_screen, weight_abs_max: *mut f32, kappa: *mut f32) -> c_int;
+    pub fn focr_screen_bounds(screen: *const focr_screen, rows: usize, upper_host: *mut f32) -> c_int;
     pub fn focr_screen_select(
         ctx: *mut focr_ctx,
         screen: *const focr_screen,

@@ -92,6 +92,7 @@ SIGNATURES = {
     "focr_screen_upload": (_I, [_P, _P, _P, _Z, _Z, ctypes.c_float, ctypes.c_float, ctypes.POINTER(_P)]),
     "focr_screen_free": (_I, [_P]),
     "focr_screen_constants": (_I, [_P, _P, _P]),
+    "focr_screen_bounds": (_I, [_P, _Z, _P]),
     "focr_screen_select": (_I, [_P, _P, _P, _P, _Z, _P, _P]),
     "focr_qkv_rows": (_I, [_P, _P, _Z, _P, _Z, _Z, _Z, _Z, _P, _P, _P, _P]),
     "focr_attention_decode": (_I, [_P, _P, _P, _P, _P, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _P, _P]),
@@ -657,6 +658,12 @@ class ScreenedHead:
         wmax, kappa = ctypes.c_float(), ctypes.c_float()
         _check(lib().focr_screen_constants(self.handle, ctypes.byref(wmax), ctypes.byref(kappa)))
         return float(wmax.value), float(kappa.value)
+
+    def bounds(self, rows: int) -> np.ndarray:
+        """q + B [rows][vocab] of the last `select` (HeadScratch::upper)."""
+        out = np.empty((rows, self.vocab), dtype=np.float32)
+        _check(lib().focr_screen_bounds(self.handle, rows, out.ctypes.data_as(ctypes.c_void_p)))
+        return out
 
     def select(self, x, rows: int, head: "Linear"):
         """`select_rows`: per input row, (token, candidates) for Screened::Token

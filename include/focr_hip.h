@@ -385,6 +385,11 @@ int focr_screen_upload(focr_ctx *ctx, const int8_t *codes_host, const float *sca
 int focr_screen_free(focr_screen *screen);
 /* ScreenedHead::raw_parts' constants (src/head_screen.rs:148-151). */
 int focr_screen_constants(const focr_screen *screen, float *weight_abs_max, float *kappa);
+/* The bounds of the last focr_screen_select on this screen: q + B of every
+ * vocabulary row for each of its first rows (1..8) inputs, into upper_host
+ * [rows][vocab] (HeadScratch::upper, src/head_screen.rs:52, filled by
+ * screen_block / screen_block_rows, 398-450). For parity tests; synchronous. */
+int focr_screen_bounds(const focr_screen *screen, size_t rows, float *upper_host);
 /* ScreenedHead::select / select_rows (src/head_screen.rs:169-199,274-324):
  * the exact FP32 greedy token of each of rows (1..8) inputs x_dev
  * [rows][dim]. tokens (host) [rows] receives the token, or -1 for

@@ -1,7 +1,8 @@
 """The screened vocabulary head on the GPU (focr_screen_*) against the oracle
 and the full FP32 head: the token, the candidate count and the fallback of
-every input are the oracle's, and every token is the full head's first-index
-argmax (src/head_screen.rs:522-699 scenarios)."""
+every input are the oracle's, the bounds q + B of every vocabulary row are the
+oracle's bit for bit, and every token is the full head's first-index argmax
+(src/head_screen.rs:522-699 scenarios)."""
 import numpy as np
 import pytest
 
@@ -25,6 +26,18 @@ def oracle_select(x, head, parts):
     vocab, dim = head.shape
     token, cand, _ = oracle.screen_select(x, head, codes, scales, vocab, dim, wmax, kappa)
     return token, cand
+
+
+def assert_bounds_bitwise(screen, xs, head, parts, inputs=None):
+    """q + B of every row for the inputs (all by default) of the last select,
+    bit for bit."""
+    codes, scales, wmax, kappa = parts
+    vocab, dim = head.shape
+    got = screen.bounds(len(xs))
+    for r in range(len(xs)) if inputs is None else inputs:
+        x = xs[r]
+        want = oracle.screen_select(x, head, codes, scales, vocab, dim, wmax, kappa)[2]
+        np.testing.assert_array_equal(got[r].view(np.uint32), want.view(np.uint32), err_msg=f"input {r}")
 
 
 @pytest.fixture(scope="module")
@@ -75,6 +88,8 @@ def test_select_rows_equals_select_per_row(fh):
         if rows > 2:
             xs[2, 5] = np.nan
         joint = screen.select(to_dev(xs), rows, lin)
+        finite = [r for r in range(rows) if np.isfinite(xs[r]).all()]
+        assert_bounds_bitwise(screen, xs, head, parts, finite)
         for r in range(rows):
             single = screen.select(to_dev(xs[r]), 1, lin)[0]
             assert joint[r] == single == oracle_select(xs[r], head, parts), (rows, r)
@@ -125,6 +140,7 @@ def test_vocabulary_head_at_checkpoint_size(fh):
     xs = gen.normal((4, dim), 1.0, 41)
     xs[3] = head[12345] * F32(60.0)
     got = screen.select(to_dev(xs), 4, lin)
+    assert_bounds_bitwise(screen, xs, head, parts)
     logits = lin.linear(to_dev(xs), 4)
     full = fh.argmax(logits, 4, vocab)
     for r in range(4):
@@ -145,6 +161,7 @@ def test_odd_vocabulary_and_narrow_head(fh):
     xs = rng.normal(0, 1, (3, dim)).astype(np.float32)
     xs[1] = head[999] * F32(30.0)
     got = screen.select(to_dev(xs), 3, lin)
+    assert_bounds_bitwise(screen, xs, head, parts)
     for r in range(3):
         assert got[r] == oracle_select(xs[r], head, parts), r
     assert got[1][0] == 999

@@ -45,6 +45,7 @@ FP32_MFMA_PEAK = 157.3  # TFLOP/s dense
 # 78.6 that 16 lanes x 2.4 GHz would allow, so the vector peak bounds them.
 FP32_VECTOR_PEAK = 157.3
 INT8_MFMA_PEAK = 5000.0  # TOP/s dense
+BF16_MFMA_PEAK = 2500.0  # TFLOP/s dense
 POOL_BYTES = 600 << 20  # > 2 x 256 MB Infinity Cache
 # Device clock cycles the stream sleeps (torch.cuda._sleep: a spin on the
 # clock, no memory traffic) while the host submits the timed replay whose
@@ -204,16 +205,24 @@ def bench_gemm(torch, fh, gen, np, reps, bits=32):
                                  gen.uniform((n, k // 64), 1e-6, 4e-6, 12), 64)
         width = n // 2 if epi == fh.Epilogue.GLU else n
         out = torch.zeros((m, width), device="cuda")
-        for kern in (fh.PrefillProjection.F32_MFMA, fh.PrefillProjection.F32_CHAIN):
+        kernels = [fh.PrefillProjection.F32_MFMA, fh.PrefillProjection.F32_CHAIN]
+        if bits == 32:
+            kernels.append(fh.PrefillProjection.F32_SPLIT)
+        for kern in kernels:
             fn = lambda i: lin.prefill(a, m, epilogue=epi, out=out, kernel=kern)
             for i in range(2):
                 fn(i)
             avg, med = timer.per_launch_ms(fn, reps)
             flops = 2.0 * m * k * n
-            tag = "mfma" if kern == fh.PrefillProjection.F32_MFMA else "chain"
+            tag = {fh.PrefillProjection.F32_MFMA: "mfma", fh.PrefillProjection.F32_CHAIN: "chain",
+                   fh.PrefillProjection.F32_SPLIT: "split"}[kern]
             tflops = flops / (avg * 1e-3) / 1e12
-            peak = FP32_MFMA_PEAK if tag == "mfma" else FP32_VECTOR_PEAK
+            peak = FP32_VECTOR_PEAK if tag == "chain" else FP32_MFMA_PEAK
             res[f"{name}_{tag}"] = {"ms": round(avg, 4), "tflops": round(tflops, 2), "frac": round(tflops / peak, 3)}
+            if tag == "split":
+                # Six BF16 part products per FP32 product: the BF16 matrix-core
+                # work done, against the 2.5 PFLOP/s dense BF16 peak.
+                res[f"{name}_{tag}"]["bf16_frac"] = round(6 * tflops / BF16_MFMA_PEAK, 3)
         lin.free()
     return res
 

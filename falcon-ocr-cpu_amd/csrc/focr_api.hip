@@ -482,6 +482,8 @@ int focr_linear_prefill(focr_ctx *handle, const focr_linear *lh, const float *x,
       return launch_prefill_f32(ctx, lin, x, rows, row_scale, epilogue, out);
     case FOCR_PROJ_F32_CHAIN:
       return launch_prefill_chain(ctx, lin, x, rows, row_scale, epilogue, out);
+    case FOCR_PROJ_F32_SPLIT:
+      return launch_prefill_split(ctx, lin, x, rows, row_scale, epilogue, out);
     case FOCR_PROJ_I16:
       FOCR_REQUIRE(lin->i16_b, FOCR_E_UNSUPPORTED,
                    "the INT16 panels take 8-bit codes in groups of 64 with out % 32 == 0 and in % 64 == 0 "

@@ -91,6 +91,8 @@ int launch_prefill_f32(Ctx *ctx, const Linear *lin, const float *x, size_t rows,
                        const float *row_scale, int epilogue, float *out);
 int launch_prefill_chain(Ctx *ctx, const Linear *lin, const float *x, size_t rows,
                          const float *row_scale, int epilogue, float *out);
+int launch_prefill_split(Ctx *ctx, const Linear *lin, const float *x, size_t rows,
+                         const float *row_scale, int epilogue, float *out);
 int launch_prefill_i16(Ctx *ctx, const Linear *lin, const float *x, size_t rows,
                        const float *row_scale, int epilogue, float *out);
 int launch_attention(Ctx *ctx, const float *q, const float *prefix_k, const float *generated_k,

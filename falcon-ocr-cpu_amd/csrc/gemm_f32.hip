@@ -910,6 +910,281 @@ void launch_one(bool chain, const GemmArgs &a, hipStream_t stream) {
   }
 }
 
+// ---- FP32 products on the BF16 matrix cores (FOCR_PROJ_F32_SPLIT) ---------
+// Every FP32 operand x is split into three BF16 parts, x = hi + mid + lo:
+// hi = x with the low 16 bits of its pattern cleared (x truncated to BF16),
+// mid = (x - hi) truncated, lo = (x - hi - mid). Both differences are exact
+// (they clear leading bits of a value of the same sign and binade), and the
+// last one has at most 8 significant bits, so lo is exact too: the split is
+// exact for every finite x (an infinity or NaN travels in hi alone). A
+// product is then the six largest of the nine part products,
+// hi.hi + hi.mid + mid.hi + hi.lo + lo.hi + mid.mid, each exact in FP32 and
+// summed by v_mfma_f32_32x32x16_bf16 in FP32; the three left out are below
+// 2^-21 |x y| together (|mid| < 2^-7 |x|, |lo| < 2^-14 |x|). Six BF16
+// products per 16 k cost 192 matrix-core cycles against 512 for eight
+// v_mfma_f32_32x32x2f32.
+constexpr int kSplitBM = 128, kSplitBN = 128, kSplitBK = 16, kSplitKAlign = 32;
+
+__device__ __forceinline__ void split3(float x, uint32_t &hi, uint32_t &mid, uint32_t &lo) {
+  const uint32_t b = __float_as_uint(x);
+  if ((b & 0x7f800000u) == 0x7f800000u) {  // infinity or NaN
+    hi = (b & 0x007fffffu) ? 0x7fc0u : (b >> 16);
+    mid = lo = 0;
+    return;
+  }
+  const uint32_t h = b & 0xffff0000u;
+  const float r1 = x - __uint_as_float(h);
+  const uint32_t m = __float_as_uint(r1) & 0xffff0000u;
+  const float r2 = r1 - __uint_as_float(m);
+  hi = h >> 16;
+  mid = m >> 16;
+  lo = __float_as_uint(r2) >> 16;  // r2 fits 8 significant bits: no rounding
+}
+
+// Three BF16 planes of fl(src * row_scale[row]) (or of src), zero past rows
+// and cols, stage-major: plane p, 16-k stage s, row r at
+// ((p * stages + s) * rows_pad + r) * 16, so that one stage of consecutive
+// rows is one contiguous run (the GEMM's copies read whole 1 KB pieces).
+// Thread (s, r, q) splits values 16 s + 4 q .. + 3 of row r: consecutive
+// threads write consecutive 8-byte pieces.
+__global__ __launch_bounds__(256) void split_planes_kernel(const float *__restrict__ src, int rows, int cols,
+                                                           const float *__restrict__ row_scale, bool vec,
+                                                           uint16_t *__restrict__ dst, int rows_pad, int cols_pad) {
+  const int stages = cols_pad / 16;
+  const long i = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= static_cast<long>(stages) * rows_pad * 4) return;
+  const int q = static_cast<int>(i & 3);
+  const long sr = i >> 2;
+  const int row = static_cast<int>(sr % rows_pad), st = static_cast<int>(sr / rows_pad);
+  const int c0 = 16 * st + 4 * q;
+  float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (row < rows) {
+    const float *r = src + static_cast<size_t>(row) * cols;
+    if (vec && c0 + 3 < cols) {
+      const float4 f = *reinterpret_cast<const float4 *>(r + c0);
+      v[0] = f.x;
+      v[1] = f.y;
+      v[2] = f.z;
+      v[3] = f.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; e++) v[e] = c0 + e < cols ? r[c0 + e] : 0.0f;
+    }
+    if (row_scale) {
+      const float sc = row_scale[row];
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+        if (c0 + e < cols) v[e] = v[e] * sc;
+    }
+  }
+  uint32_t hh[4], mm[4], ll[4];
+#pragma unroll
+  for (int e = 0; e < 4; e++) split3(v[e], hh[e], mm[e], ll[e]);
+  const size_t plane = static_cast<size_t>(stages) * rows_pad * 16;
+  const size_t off = (static_cast<size_t>(st) * rows_pad + row) * 16 + 4 * q;
+  *reinterpret_cast<uint2 *>(dst + off) = make_uint2(hh[0] | hh[1] << 16, hh[2] | hh[3] << 16);
+  *reinterpret_cast<uint2 *>(dst + plane + off) = make_uint2(mm[0] | mm[1] << 16, mm[2] | mm[3] << 16);
+  *reinterpret_cast<uint2 *>(dst + 2 * plane + off) = make_uint2(ll[0] | ll[1] << 16, ll[2] | ll[3] << 16);
+}
+
+typedef __bf16 split_bf16x8 __attribute__((ext_vector_type(8)));
+union SplitFrag {
+  uint4 u;
+  split_bf16x8 v;
+};
+
+// 128 x 128 outputs per workgroup, 4 waves in 2 x 2, each 64 x 64 in 32 x 32
+// blocks. Stages of 16 k: per operand three planes x 128 rows x 32 bytes
+// (each plane's rows of a stage contiguous in memory), copied HBM -> LDS by
+// the LDS-DMA path (16 bytes per lane, three copies of 1 KB per wave and
+// operand) into a ring of three stages, two stages ahead. A row's
+// two 16-byte chunks (k 0..7, 8..15) are stored swapped when (row / 8) is
+// odd: the 16 lanes a ds_read_b128 serves (rows r..r+15, one chunk) then hit
+// 16 distinct bank groups. Step st reads stage st's fragments while the
+// products of stage st - 1 run. Rows and columns are padded to 128 with zeros
+// in the planes; outputs past m or n are not written.
+// Tile order: workgroups are dealt to the 8 XCDs round robin (block b runs on
+// XCD b % 8); block b takes tile t = (b % 8) * per + b / 8, so each XCD walks
+// a contiguous run of tiles, in panels of kSplitPanel row tiles (column tiles
+// in order, rows fastest): the workgroups an XCD holds at once share a few A
+// row tiles and B column tiles in its own L2.
+constexpr int kSplitPanel = 4;
+__device__ __forceinline__ void split_tile(int b, int row_tiles, int col_tiles, int &rt, int &ct) {
+  const int total = row_tiles * col_tiles;
+  const int per = total / 8;
+  const int t = b < 8 * per ? (b % 8) * per + b / 8 : b;
+  const int panel = t / (kSplitPanel * col_tiles);
+  const int rem = t - panel * kSplitPanel * col_tiles;
+  const int rows = row_tiles - panel * kSplitPanel < kSplitPanel ? row_tiles - panel * kSplitPanel : kSplitPanel;
+  ct = rem / rows;
+  rt = panel * kSplitPanel + rem % rows;
+}
+
+template <int EPI>
+__global__ __launch_bounds__(256) void split_kernel(GemmArgs a, const uint16_t *__restrict__ ap,
+                                                    const uint16_t *__restrict__ bp, size_t a_plane, size_t b_plane,
+                                                    int kp, int row_tiles, int col_tiles) {
+  // The ring's three slots, each [A, B][plane * 256 + slot u], are separate
+  // arrays and every step names its slots statically: the compiler then sees
+  // that a step's fragment reads never touch the slot being copied into.
+  __shared__ uint4 ring0[2][3 * 256], ring1[2][3 * 256], ring2[2][3 * 256];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  int rt, ct;
+  split_tile(blockIdx.x, row_tiles, col_tiles, rt, ct);
+  const int m0 = a.row0 + rt * kSplitBM, n0 = ct * kSplitBN;
+  const int h = lane >> 5, l32 = lane & 31;
+  // Copy t of operand o fills slots q = 64 (wave + 4 t) + lane: plane q / 256,
+  // slot u = q % 256 = row u / 2, chunk (u % 2) ^ ((row / 8) % 2).
+  const char *src[2][3];
+#pragma unroll
+  for (int t = 0; t < 3; t++) {
+    const int q = 64 * (wave + 4 * t) + lane, p = q >> 8, u = q & 255, r = u >> 1;
+    const int c = (u & 1) ^ ((r >> 3) & 1);
+    src[0][t] = reinterpret_cast<const char *>(ap + p * a_plane + static_cast<size_t>(m0 + r) * kSplitBK + 8 * c);
+    src[1][t] = reinterpret_cast<const char *>(bp + p * b_plane + static_cast<size_t>(n0 + r) * kSplitBK + 8 * c);
+  }
+  const int stages = kp / kSplitBK;  // even
+  // Stage-major planes: stage s of a plane starts rows_pad * 32 bytes after s - 1.
+  const size_t a_step = a_plane / stages * 2, b_step = b_plane / stages * 2;  // bytes
+  auto issue = [&](uint4 (*slot)[3 * 256], int stage) __attribute__((always_inline)) {
+#pragma unroll
+    for (int o = 0; o < 2; o++) {
+      const size_t off = stage * (o == 0 ? a_step : b_step);
+#pragma unroll
+      for (int t = 0; t < 3; t++)
+        __builtin_amdgcn_global_load_lds((global_void *)(src[o][t] + off), (lds_void *)(&slot[o][64 * (wave + 4 * t)]),
+                                         16, 0, 0);
+    }
+  };
+  // Fragments of a stage: A blocks i and B blocks j, planes 0..2.
+  auto read = [&](const uint4 (*slot)[3 * 256], SplitFrag (*fa)[3], SplitFrag (*fb)[3]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const int r = wm * 64 + 32 * i + l32;
+      const int u = 2 * r + (h ^ ((r >> 3) & 1));
+#pragma unroll
+      for (int p = 0; p < 3; p++) fa[i][p].u = slot[0][p * 256 + u];
+    }
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const int r = wn * 64 + 32 * j + l32;
+      const int u = 2 * r + (h ^ ((r >> 3) & 1));
+#pragma unroll
+      for (int p = 0; p < 3; p++) fb[j][p].u = slot[1][p * 256 + u];
+    }
+  };
+  v16f acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+  // The six part products, smallest first: (mid, mid), (lo, hi), (hi, lo),
+  // (mid, hi), (hi, mid), (hi, hi).
+  auto products = [&](SplitFrag (*fa)[3], SplitFrag (*fb)[3]) __attribute__((always_inline)) {
+    constexpr int pa[6] = {1, 2, 0, 1, 0, 0}, pb[6] = {1, 0, 2, 0, 1, 0};
+#pragma unroll
+    for (int q = 0; q < 6; q++)
+#pragma unroll
+      for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i][pa[q]].v, fb[j][pb[q]].v, acc[i][j], 0, 0, 0);
+  };
+  SplitFrag fa0[2][3], fb0[2][3], fa1[2][3], fb1[2][3];
+  issue(ring0, 0);
+  issue(ring1, 1);
+  // Step st (stage st in slot st % 3): wait for this wave's copies of stage
+  // st (stage st + 1's six may still fly) and its earlier LDS reads, meet the
+  // other waves (nobody still reads stage st - 1's slot), start stage st + 2
+  // there (past the last stage the copy repeats it, so the counts stay the
+  // same), read stage st's fragments, then run stage st - 1's products.
+  auto step = [&](int st, const uint4 (*cur)[3 * 256], uint4 (*next)[3 * 256], SplitFrag (*ra)[3],
+                  SplitFrag (*rb)[3], SplitFrag (*pa)[3], SplitFrag (*pb)[3]) __attribute__((always_inline)) {
+    __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(6));
+    plain_barrier();
+    issue(next, st + 2 < stages ? st + 2 : stages - 1);
+    read(cur, ra, rb);
+    if (st > 0) products(pa, pb);
+  };
+  // Six steps cycle through the three slots and the two fragment sets.
+  int st = 0;
+  for (; st + 6 <= stages; st += 6) {
+    step(st, ring0, ring2, fa0, fb0, fa1, fb1);
+    step(st + 1, ring1, ring0, fa1, fb1, fa0, fb0);
+    step(st + 2, ring2, ring1, fa0, fb0, fa1, fb1);
+    step(st + 3, ring0, ring2, fa1, fb1, fa0, fb0);
+    step(st + 4, ring1, ring0, fa0, fb0, fa1, fb1);
+    step(st + 5, ring2, ring1, fa1, fb1, fa0, fb0);
+  }
+  if (st < stages) {  // 2 or 4 stages left
+    step(st, ring0, ring2, fa0, fb0, fa1, fb1);
+    step(st + 1, ring1, ring0, fa1, fb1, fa0, fb0);
+    if (st + 2 < stages) {
+      step(st + 2, ring2, ring1, fa0, fb0, fa1, fb1);
+      step(st + 3, ring0, ring2, fa1, fb1, fa0, fb0);
+    }
+  }
+  products(fa1, fb1);
+  // The repeated copies must land before the workgroup's LDS is released.
+  __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
+  // D layout of 32x32: column = lane % 32, row = 8 (r / 4) + 4 (lane / 32) + r % 4.
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int row = m0 + wm * 64 + i * 32 + 8 * (r / 4) + 4 * h + (r % 4);
+        const int col = n0 + wn * 64 + j * 32 + l32;
+        const float v = acc[i][j][r];
+        const float partner = EPI == FOCR_EPI_GLU ? __shfl_xor(v, 1) : 0.0f;
+        emit<EPI>(a, row, col, v, partner);
+      }
+}
+
+int launch_split(Ctx *ctx, const Linear *lin, const float *x, size_t rows, const float *row_scale, int epilogue,
+                 float *out) {
+  FOCR_REQUIRE(lin->bits == 32, FOCR_E_UNSUPPORTED,
+               "FOCR_PROJ_F32_SPLIT takes FP32 weights (codes would be materialized); plan FOCR_PROJ_F32_MFMA");
+  FOCR_REQUIRE(rows < (size_t(1) << 30), FOCR_E_SHAPE, "prefill rows too large");
+  const size_t m_pad = (rows + kSplitBM - 1) / kSplitBM * kSplitBM;
+  const size_t n_pad = (lin->n + kSplitBN - 1) / kSplitBN * kSplitBN;
+  const size_t kp = (lin->k + kSplitKAlign - 1) / kSplitKAlign * kSplitKAlign;
+  FOCR_REQUIRE(kp < (size_t(1) << 30) && n_pad < (size_t(1) << 30), FOCR_E_SHAPE, "prefill shape too large");
+  const size_t a_plane = m_pad * kp, b_plane = n_pad * kp;
+  int rc = ensure_scratch(ctx, 3 * (a_plane + b_plane) * sizeof(uint16_t));
+  if (rc != FOCR_OK) return rc;
+  uint16_t *ap = static_cast<uint16_t *>(ctx->scratch), *bp = ap + 3 * a_plane;
+  const float *w = static_cast<const float *>(lin->codes);
+  auto split = [&](const float *src, size_t r, size_t c, const float *rs, uint16_t *dst, size_t r_pad) {
+    const bool vec = c % 4 == 0 && reinterpret_cast<uintptr_t>(src) % 16 == 0;
+    const size_t threads = r_pad * (kp / 4);  // (kp / 16) stages x r_pad rows x 4
+    hipLaunchKernelGGL(split_planes_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0,
+                       ctx->stream, src, static_cast<int>(r), static_cast<int>(c), rs, vec, dst,
+                       static_cast<int>(r_pad), static_cast<int>(kp));
+  };
+  split(x, rows, lin->k, row_scale, ap, m_pad);
+  split(w, lin->n, lin->k, nullptr, bp, n_pad);
+  GemmArgs a = make_args(lin, x, rows, row_scale, out);
+  const int rtiles = static_cast<int>(m_pad / kSplitBM), ctiles = static_cast<int>(n_pad / kSplitBN);
+  const dim3 grid(static_cast<unsigned>(rtiles * ctiles));
+  const int k32 = static_cast<int>(kp);
+  if (epilogue == FOCR_EPI_GLU)
+    hipLaunchKernelGGL((split_kernel<FOCR_EPI_GLU>), grid, dim3(256), 0, ctx->stream, a, ap, bp, a_plane, b_plane, k32,
+                       rtiles, ctiles);
+  else if (epilogue == FOCR_EPI_ADD)
+    hipLaunchKernelGGL((split_kernel<FOCR_EPI_ADD>), grid, dim3(256), 0, ctx->stream, a, ap, bp, a_plane, b_plane, k32,
+                       rtiles, ctiles);
+  else
+    hipLaunchKernelGGL((split_kernel<FOCR_EPI_STORE>), grid, dim3(256), 0, ctx->stream, a, ap, bp, a_plane, b_plane,
+                       k32, rtiles, ctiles);
+  FOCR_HIP_CHECK(hipGetLastError());
+  return FOCR_OK;
+}
+
 template <typename T>
 void launch_epi(bool chain, int epilogue, const GemmArgs &a, hipStream_t stream) {
   if (epilogue == FOCR_EPI_GLU)
@@ -947,6 +1222,11 @@ int launch_prefill_f32(Ctx *ctx, const Linear *lin, const float *x, size_t rows,
 int launch_prefill_chain(Ctx *ctx, const Linear *lin, const float *x, size_t rows, const float *row_scale,
                          int epilogue, float *out) {
   return launch_f32_common(true, ctx, lin, x, rows, row_scale, epilogue, out);
+}
+
+int launch_prefill_split(Ctx *ctx, const Linear *lin, const float *x, size_t rows, const float *row_scale,
+                         int epilogue, float *out) {
+  return launch_split(ctx, lin, x, rows, row_scale, epilogue, out);
 }
 
 }  // namespace focr

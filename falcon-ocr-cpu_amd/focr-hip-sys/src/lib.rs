@@ -51,6 +51,7 @@ pub const FOCR_EPI_ADD: c_int = 2;
 pub const FOCR_PROJ_F32_MFMA: c_int = 0;
 pub const FOCR_PROJ_F32_CHAIN: c_int = 1;
 pub const FOCR_PROJ_I16: c_int = 2;
+pub const FOCR_PROJ_F32_SPLIT: c_int = 3;
 
 // Prefill softmax and exp mode.
 pub const FOCR_SOFTMAX_ONLINE: c_int = 0;

@@ -1,7 +1,7 @@
 """Prefill projections on the GPU against the oracle:
 INT16 panels bitwise (src/kernels/panels/panel_i16/tests.rs), FP32 exact-order
-panels bitwise and FP32 matrix cores within the FP32 tolerance
-(src/kernels/panels/panel.rs:243-299)."""
+panels bitwise, and FP32 matrix cores and FP32 products from exact BF16 splits
+within the FP32 tolerance (src/kernels/panels/panel.rs:243-299)."""
 import numpy as np
 import pytest
 
@@ -154,6 +154,70 @@ def test_f32_mfma_within_fp32_tolerance(fh, bits, m, k, n):
     assert_bitwise(glu, (np.where(g > 0, g, F32(0)) ** 2 * u).astype(np.float32), "glu of store")
 
 
+@pytest.mark.parametrize("m,k,n", F32_SHAPES)
+def test_f32_split_within_fp32_tolerance(fh, m, k, n):
+    # FP32 weights split exactly into three BF16 parts, six part products per
+    # FP32 product on the BF16 matrix cores: the same tolerance as the FP32
+    # matrix cores; Glu and Add are the Store output passed through them.
+    a = gen.matrix(m * k, 3).reshape(m, k)
+    w = gen.matrix(n * k, 4).reshape(n, k)
+    lin = fh.Linear.from_f32(w)
+    rs = (F32(0.5) + np.arange(m, dtype=np.float32) / F32(7.0)).astype(np.float32)
+    S = fh.PrefillProjection.F32_SPLIT
+    got = run_prefill(fh, lin, a, m, rs, fh.Epilogue.STORE, S)
+    want = oracle.panel_gemm(a, m, k, w, n, row_scale=rs)
+    ad = (a * rs[:, None]).astype(np.float32).astype(np.float64)
+    mag = np.abs(ad) @ np.abs(w.astype(np.float64)).T
+    assert np.all(np.abs(got.astype(np.float64) - want) <= 2 * k * EPS * mag + 1e-30)
+    assert max_rel(got, want) <= 1e-5
+    glu = run_prefill(fh, lin, a, m, rs, fh.Epilogue.GLU, S)
+    g, u = got[:, 0::2], got[:, 1::2]
+    assert_bitwise(glu, (np.where(g > 0, g, F32(0)) ** 2 * u).astype(np.float32), "glu of store")
+    base = gen.matrix(m * n, 5).reshape(m, n)
+    add = run_prefill(fh, lin, a, m, rs, fh.Epilogue.ADD, S, base=base)
+    assert_bitwise(add, (base + got).astype(np.float32), "add of store")
+
+
+def test_f32_split_error_is_fp32_level(fh):
+    # Against the exact (f64) product: the split kernel's error is of the
+    # FP32 matrix-core kernel's order (the three part products left out are
+    # below 2^-21 |a w| together, the FP32 sums' own rounding dominates).
+    m, k, n = 384, 2304, 256
+    a = gen.normal((m, k), 1.0, 21)
+    w = gen.normal((n, k), 0.02, 22)
+    lin = fh.Linear.from_f32(w)
+    exact = a.astype(np.float64) @ w.astype(np.float64).T
+    mag = np.abs(a.astype(np.float64)) @ np.abs(w.astype(np.float64)).T
+    err = {}
+    for kern in (fh.PrefillProjection.F32_SPLIT, fh.PrefillProjection.F32_MFMA, fh.PrefillProjection.F32_CHAIN):
+        got = run_prefill(fh, lin, a, m, None, fh.Epilogue.STORE, kern).astype(np.float64)
+        err[kern.name] = (float(np.max(np.abs(got - exact) / mag)), float(np.sqrt(np.mean(((got - exact) / mag) ** 2))))
+    assert err["F32_SPLIT"][0] <= 2 * max(err["F32_MFMA"][0], err["F32_CHAIN"][0]), err
+    assert err["F32_SPLIT"][1] <= 2 * max(err["F32_MFMA"][1], err["F32_CHAIN"][1]), err
+
+
+def test_f32_split_nonfinite_rows_stay_nonfinite_and_codes_are_refused(fh):
+    # An infinite or NaN input reaches every output of its row as a
+    # non-finite value (an infinity times a zero part is NaN where the FP32
+    # panels give the infinity); the other rows are unaffected.
+    m, k, n = 20, 256, 64
+    a = gen.matrix(m * k, 23).reshape(m, k)
+    a[3, 17] = np.inf
+    a[7, 5] = np.nan
+    w = gen.matrix(n * k, 24).reshape(n, k)
+    lin = fh.Linear.from_f32(w)
+    got = run_prefill(fh, lin, a, m, None, fh.Epilogue.STORE, fh.PrefillProjection.F32_SPLIT)
+    assert not np.any(np.isfinite(got[3])) and np.all(np.isnan(got[7]))
+    keep = [r for r in range(m) if r not in (3, 7)]
+    want = oracle.panel_gemm(a[keep], len(keep), k, w, n)
+    assert max_rel(got[keep], want) <= 1e-5
+    codes, scales = oracle.quantize_bits(w, n, k, 64, 8)
+    q = fh.QuantLinear(8, codes, scales, 64)
+    with pytest.raises(fh.FocrError) as e:
+        run_prefill(fh, q, a, m, None, fh.Epilogue.STORE, fh.PrefillProjection.F32_SPLIT)
+    assert e.value.code == fh.FOCR_E_UNSUPPORTED
+
+
 @pytest.mark.parametrize("bits", [16, 8])
 def test_f32_mfma_on_codes_keeps_exception_columns(fh, bits):
     # Codes on the matrix cores: k a multiple of 64 takes the DMA kernel (codes
@@ -182,7 +246,8 @@ def test_f32_mfma_on_codes_keeps_exception_columns(fh, bits):
 def test_config1_fp32_gemm_checkpoint_shapes(fh, name, k, n, epi):
     # X ~ N(0,1), W ~ N(0, 0.02), m = 6544. Every output
     # against the FP32 panels (their AVX2 micro-kernel, bitwise panel_gemm):
-    # the MFMA kernel within the FP32 tolerance, the chain kernel bitwise.
+    # the MFMA and split kernels within the FP32 tolerance, the chain kernel
+    # bitwise.
     m = 6544
     a = gen.normal((m, k), 1.0, 10)
     w = gen.normal((n, k), 0.02, 11)
@@ -198,6 +263,11 @@ def test_config1_fp32_gemm_checkpoint_shapes(fh, name, k, n, epi):
         assert np.all(np.abs(got.astype(np.float64) - want) <= 2 * k * EPS * mag + 1e-30), name
     chain = run_prefill(fh, lin, a, m, None, fh.Epilogue(epi), fh.PrefillProjection.F32_CHAIN, base=base)
     assert_bitwise(chain, want, f"{name} chain")
+    split = run_prefill(fh, lin, a, m, None, fh.Epilogue(epi), fh.PrefillProjection.F32_SPLIT, base=base)
+    assert np.all(np.isfinite(split))
+    assert max_rel(split, want) <= 1e-5, f"{name} split"
+    if epi == 0:
+        assert np.all(np.abs(split.astype(np.float64) - want) <= 2 * k * EPS * mag + 1e-30), f"{name} split"
 
 
 @pytest.mark.parametrize("bits", [16, 8])

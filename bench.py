@@ -698,8 +698,10 @@ def cpu_prefill_page(np, gen, gpu_gemm, gpu_attention, facts, reps=2):
     if ghz:
         macs_cycle_core = round(m * 1024 * 4096 / (cpu["literal"] * 1e-3) / (cores * ghz * 1e9), 2)
     layer = ("qkv", "wo", "w13", "w2")
-    gpu_literal = gpu_gemm["literal_mfma"]["ms"] + gpu_attention["online_fast"]["ms"]
-    gpu_layer = sum(gpu_gemm[f"{s}_mfma"]["ms"] for s in layer) + gpu_attention["online_fast"]["ms"]
+    # The GPU side runs exact mode's plan: the FP32 projections from exact
+    # BF16 splits (hip-f32-split) and the online FP32 attention.
+    gpu_literal = gpu_gemm["literal_split"]["ms"] + gpu_attention["online_fast"]["ms"]
+    gpu_layer = sum(gpu_gemm[f"{s}_split"]["ms"] for s in layer) + gpu_attention["online_fast"]["ms"]
     cpu_literal = cpu["literal"] + cpu["attention"]
     cpu_layer = sum(cpu[s] for s in layer) + cpu["attention"]
     return {"cores": threads, "kind": "port", "physical_cores": cores, "ghz_assumed": ghz or None,

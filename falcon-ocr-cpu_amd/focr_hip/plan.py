@@ -8,15 +8,17 @@ compares them (``Kernels::from_plan``, src/book/resume.rs:102-137). The `hip`
 backend adds its own kernels under their own labels, so a resumed run never
 mixes CPU and GPU records silently:
 
-    projection  hip-f32-mfma | hip-f32-chain | hip-i16
+    projection  hip-f32-split | hip-f32-mfma | hip-f32-chain | hip-i16
     attention   hip | hip-static | hip-bf16 | hip-bf16-static
 
 ``hip_prefill_plan`` applies the reference's predicate set with the GPU's
 kernels: an 8-bit body whose matrices the INT16 panels hold takes the INT16
 projections (bitwise the reference's INT16 panels) unless the tuning asks for
 FP32 ones; other quantized bodies take the bitwise FP32 chain
-(PanelAvx2's order); an FP32 body takes the FP32 matrix cores (the
-reference's ``gemm`` crate order is not reproduced bitwise by any kernel).
+(PanelAvx2's order); an FP32 body takes FP32 products from exact BF16 splits
+on the BF16 matrix cores (the reference's ``gemm`` crate order is not
+reproduced bitwise by any kernel; this one is the fastest within the FP32
+tolerance; ``hip-f32-mfma``, the FP32 matrix cores, stays a valid label).
 Attention: an 8-bit body takes BF16 attention unless ``prefill_bf16`` is off
 (static softmax when ``prefill_softmax`` asks for it); FP32 tiles take the
 static softmax for 16-bit bodies (or when ``prefill_softmax_fp32`` asks for
@@ -30,7 +32,7 @@ from typing import Optional
 from . import ExpMode, FocrError, PrefillProjection, Softmax
 
 PROJECTION_LABELS = {PrefillProjection.F32_MFMA: "hip-f32-mfma", PrefillProjection.F32_CHAIN: "hip-f32-chain",
-                     PrefillProjection.I16: "hip-i16"}
+                     PrefillProjection.I16: "hip-i16", PrefillProjection.F32_SPLIT: "hip-f32-split"}
 ATTENTION_KINDS = ("hip", "hip-static", "hip-bf16", "hip-bf16-static")
 
 
@@ -78,7 +80,7 @@ def hip_prefill_plan(body_bits: Optional[int], i16_misfit: bool, prefill_bf16: b
     fp32_softmax = prefill_softmax_fp32 or ("static" if body_bits == 16 else "online")
     static_fp32 = panel and fp32_softmax == "static"
     if not panel:
-        projection = PrefillProjection.F32_MFMA
+        projection = PrefillProjection.F32_SPLIT
     elif body_bits == 8 and not i16_misfit and prefill_projections == "i16":
         projection = PrefillProjection.I16
     else:

@@ -362,8 +362,10 @@ def test_hip_prefill_plan_follows_the_reference_predicates():
     assert near.labels() == {"projection": "hip-f32-chain", "attention": "hip-static"}
     assert hip_prefill_plan(16, False, prefill_softmax_fp32="online").attention == "hip"
     exact = hip_prefill_plan(None, False, prefill_softmax_fp32="static")  # FP32 bodies keep online
-    assert exact.labels() == {"projection": "hip-f32-mfma", "attention": "hip"}
-    for plan in (fast, near, exact):
+    assert exact.labels() == {"projection": "hip-f32-split", "attention": "hip"}
+    mfma = HipPrefillPlan(PrefillProjection.F32_MFMA, "hip")
+    assert mfma.labels() == {"projection": "hip-f32-mfma", "attention": "hip"}
+    for plan in (fast, near, exact, mfma):
         assert HipPrefillPlan.from_labels(plan.labels()) == plan
     with pytest.raises(FocrError):
         HipPrefillPlan.from_labels({"projection": "panel-avx2", "attention": "avx2"})

@@ -362,6 +362,343 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void a
   }
 }
 
+// ---- FP32 products from exact BF16 splits (focr_attention_prefill_split) ---
+// The same tiles, softmax, masks, sinks and work split as attention_kernel,
+// with every product of S^T = K Q^T and O^T = V^T P^T formed from exact
+// three-way BF16 splits (split3: x = hi + mid + lo with no rounding) on
+// v_mfma_f32_32x32x16_bf16: six part products per FP32 product (hi.hi,
+// hi.mid, mid.hi, hi.lo, lo.hi, mid.mid; the three left out are below
+// 2^-21 |x y| together), FP32 accumulation. Per 32-key tile a wave issues
+// 24 + 24 BF16 products (32 matrix-core cycles each) in place of 32 + 32
+// FP32 ones (64 cycles each).
+// A pre-pass writes the call's K and V as three BF16 planes of 32-key tiles
+// (zero past the last key), in the BF16 attention's tile layouts:
+//   K: [plane][head][tile][32 keys][8 chunks of 8 dims], chunk c of key r
+//      stored at c ^ ks(r);
+//   V: [plane][kv head][tile][64 dims][4 chunks of 8 key slots], transposed,
+//      slot 16s + 8h + e holding key 16s + 4h + 8(e/4) + e%4 (the order in
+//      which the score registers feed the PV product), chunk c of dim d at
+//      c ^ vs(d).
+// The swizzles put the sixteen 16-byte chunks that sixteen consecutive lanes
+// read in distinct bank groups. Q is split once per wave, each tile's
+// probabilities as they feed PV.
+__device__ __forceinline__ int ks(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+__device__ __forceinline__ int vs(int d) { return ((d >> 1) & 3) ^ ((d >> 3) & 1); }
+
+typedef __bf16 split_bf16x8 __attribute__((ext_vector_type(8)));
+union SplitFrag {
+  uint4 u;
+  split_bf16x8 v;
+};
+
+// Eight FP32 values as three BF16x8 fragments (hi, mid, lo).
+__device__ __forceinline__ void split8(const float (&x)[8], uint4 &hi, uint4 &mid, uint4 &lo) {
+  uint32_t h[8], m[8], l[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) split3(x[e], h[e], m[e], l[e]);
+  hi = make_uint4(h[0] | h[1] << 16, h[2] | h[3] << 16, h[4] | h[5] << 16, h[6] | h[7] << 16);
+  mid = make_uint4(m[0] | m[1] << 16, m[2] | m[3] << 16, m[4] | m[5] << 16, m[6] | m[7] << 16);
+  lo = make_uint4(l[0] | l[1] << 16, l[2] | l[3] << 16, l[4] | l[5] << 16, l[6] | l[7] << 16);
+}
+
+// Block (tile, head): K of query head `head` (thread = key row r, chunk c)
+// and, for head < n_kv_heads, V of that KV head (thread = dim d, chunk c).
+__global__ __launch_bounds__(256) void split_kv_kernel(const float *__restrict__ k, const float *__restrict__ v,
+                                                       int total, int n_heads, int n_kv_heads, int tiles,
+                                                       uint4 *__restrict__ kp, uint4 *__restrict__ vp) {
+  const int tile = blockIdx.x, head = blockIdx.y, t = threadIdx.x;
+  const size_t kplane = static_cast<size_t>(n_heads) * tiles * 256, vplane = static_cast<size_t>(n_kv_heads) * tiles * 256;
+  if (head < n_heads) {
+    const int r = t >> 3, c = t & 7;
+    const int key = tile * kKeys + r;
+    float val[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) val[e] = 0.0f;
+    if (key < total) {
+      const float4 *src = reinterpret_cast<const float4 *>(k + (static_cast<size_t>(key) * n_heads + head) * 64 + 8 * c);
+      const float4 x = src[0], y = src[1];
+      val[0] = x.x; val[1] = x.y; val[2] = x.z; val[3] = x.w;
+      val[4] = y.x; val[5] = y.y; val[6] = y.z; val[7] = y.w;
+    }
+    uint4 hi, mid, lo;
+    split8(val, hi, mid, lo);
+    const size_t i = (static_cast<size_t>(head) * tiles + tile) * 256 + r * 8 + (c ^ ks(r));
+    kp[i] = hi;
+    kp[kplane + i] = mid;
+    kp[2 * kplane + i] = lo;
+  }
+  if (head < n_kv_heads) {
+    const int d = t >> 2, c = t & 3;
+    float val[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      const int p = 8 * c + e;  // slot 16s + 8h + e'
+      const int s = p >> 4, hh = (p >> 3) & 1, ee = p & 7;
+      const int key = tile * kKeys + 16 * s + 4 * hh + 8 * (ee >> 2) + (ee & 3);
+      val[e] = key < total ? v[(static_cast<size_t>(key) * n_kv_heads + head) * 64 + d] : 0.0f;
+    }
+    uint4 hi, mid, lo;
+    split8(val, hi, mid, lo);
+    const size_t i = (static_cast<size_t>(head) * tiles + tile) * 256 + d * 4 + (c ^ vs(d));
+    vp[i] = hi;
+    vp[vplane + i] = mid;
+    vp[2 * vplane + i] = lo;
+  }
+}
+
+// One buffered key tile of the split kernel: [plane][256 chunks] of K and V.
+struct SplitKvTile {
+  uint4 k[3][256];
+  uint4 v[3][256];
+};
+
+// Copies split tile `kt` (this head's K planes, its KV head's V planes) into
+// t: thread tid moves chunk tid of each of the six 4 KB planes.
+__device__ __forceinline__ void copy_split_tile(SplitKvTile &t, const uint4 *kp, const uint4 *vp, size_t kplane,
+                                                size_t vplane, int tiles, int kt, int head, int kv_head, int wave,
+                                                int tid) {
+#pragma unroll
+  for (int p = 0; p < 3; p++) {
+    __builtin_amdgcn_global_load_lds((global_void *)(kp + p * kplane + (static_cast<size_t>(head) * tiles + kt) * 256 + tid),
+                                     (lds_void *)(&t.k[p][64 * wave]), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((global_void *)(vp + p * vplane + (static_cast<size_t>(kv_head) * tiles + kt) * 256 + tid),
+                                     (lds_void *)(&t.v[p][64 * wave]), 16, 0, 0);
+  }
+}
+
+// One 32-key tile of one wave: tile_step's softmax with split products.
+template <bool STATIC, bool FAST>
+__device__ __forceinline__ void split_tile_step(const AttnArgs &a, const SplitKvTile &t, const SplitFrag (&qb)[3][4],
+                                                v16f (&o)[2], float &run_max, float &den, int kstart, int keys,
+                                                bool need_mask, int h, int l32, int my_abs, bool my_image) {
+  // S^T = K Q^T: step s covers dims 16 s .. 16 s + 15 (lane half h: 8 h ..).
+  SplitFrag kf[3][4];
+#pragma unroll
+  for (int p = 0; p < 3; p++)
+#pragma unroll
+    for (int s = 0; s < 4; s++) kf[p][s].u = t.k[p][l32 * 8 + ((2 * s + h) ^ ks(l32))];
+  v16f st;
+#pragma unroll
+  for (int r = 0; r < 16; r++) st[r] = 0.0f;
+  // The six part products, smallest first: (mid, mid), (lo, hi), (hi, lo),
+  // (mid, hi), (hi, mid), (hi, hi).
+  constexpr int pk[6] = {1, 2, 0, 1, 0, 0}, pq[6] = {1, 0, 2, 0, 1, 0};
+#pragma unroll
+  for (int q = 0; q < 6; q++)
+#pragma unroll
+    for (int s = 0; s < 4; s++) st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[pk[q]][s].v, qb[pq[q]][s].v, st, 0, 0, 0);
+  // Register r holds key kstart + 8(r/4) + 4h + r%4.
+  if (need_mask) {
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int key = kstart + 8 * (r / 4) + 4 * h + (r % 4);
+      const bool hidden = key >= kstart + keys ||
+                          (key > my_abs && !(my_image && key >= a.image_start && key < a.image_end));
+      st[r] = hidden ? -__builtin_inff() : st[r];
+    }
+  }
+  if constexpr (STATIC) {
+    float psum = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const float p = exp_hw(st[r]);  // masked keys: exp(-inf) = +0
+      st[r] = p;
+      psum = psum + p;
+    }
+    den = den + halves_sum(psum);
+  } else {
+    float tile_max = st[0];
+#pragma unroll
+    for (int r = 1; r < 16; r++) tile_max = __builtin_fmaxf(tile_max, st[r]);
+    tile_max = halves_max(tile_max);
+    const float new_max = __builtin_fmaxf(tile_max, run_max);
+    const bool skip = new_max == -__builtin_inff();
+    const bool first = run_max == -__builtin_inff();
+    float rescale = FAST ? exp_hw(run_max - new_max) : expf_acc(run_max - new_max);
+    rescale = first ? 0.0f : rescale;
+    rescale = skip ? 1.0f : rescale;
+    const float shift = skip ? 0.0f : new_max;
+    float psum = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const float x = st[r] - shift;
+      const float p = FAST ? exp_hw(x) : expf_acc(x);
+      st[r] = p;
+      psum = psum + p;
+    }
+    den = den * rescale + halves_sum(psum);
+    run_max = skip ? run_max : new_max;
+    if (__builtin_amdgcn_ballot_w64(rescale != 1.0f)) {
+#pragma unroll
+      for (int d = 0; d < 2; d++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) o[d][r] = o[d][r] * rescale;
+    }
+  }
+  // O^T += V^T P^T: step s2 takes score registers 8 s2 .. 8 s2 + 7 (keys
+  // 16 s2 + 4h + 8(e/4) + e%4) as the B operand, V^T slots 16 s2 + 8h .. of
+  // dim l32 + 32 d as the A operand.
+  SplitFrag pf[3][2];
+#pragma unroll
+  for (int s2 = 0; s2 < 2; s2++) {
+    float pv[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) pv[e] = st[8 * s2 + e];
+    split8(pv, pf[0][s2].u, pf[1][s2].u, pf[2][s2].u);
+  }
+  SplitFrag vf[3][2][2];
+#pragma unroll
+  for (int p = 0; p < 3; p++)
+#pragma unroll
+    for (int d = 0; d < 2; d++)
+#pragma unroll
+      for (int s2 = 0; s2 < 2; s2++) {
+        const int dim = l32 + 32 * d;
+        vf[p][d][s2].u = t.v[p][dim * 4 + ((2 * s2 + h) ^ vs(dim))];
+      }
+#pragma unroll
+  for (int q = 0; q < 6; q++)
+#pragma unroll
+    for (int s2 = 0; s2 < 2; s2++)
+#pragma unroll
+      for (int d = 0; d < 2; d++)
+        o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[pk[q]][d][s2].v, pf[pq[q]][s2].v, o[d], 0, 0, 0);
+}
+
+// Pure prefill only (every key a prefix key, queries = keys from position 0).
+template <bool STATIC, bool FAST>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void attention_split_kernel(
+    AttnArgs a, const uint4 *__restrict__ kp, const uint4 *__restrict__ vp, size_t kplane, size_t vplane,
+    int ktiles, split::Plan plan) {
+  __shared__ SplitKvTile tile0;
+  __shared__ SplitKvTile tile1;
+  __shared__ SplitKvTile tile2;
+  const int head = blockIdx.y;
+  const int kv_head = head / (a.n_heads / a.n_kv_heads);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int h = lane >> 5, l32 = lane & 31;
+  const split::Item it = split::find_item(plan, a.tiles, blockIdx.x);
+  const int order = it.order, part = it.part, parts = it.parts;
+  const int first_query = (a.tiles - 1 - order) * kQueries;
+  const int wq0 = first_query + wave * 32;
+  const int my_query = wq0 + l32;
+  const int my_abs = a.query_offset + my_query;
+  const bool my_valid = my_query < a.query_len;
+  const bool my_image = my_abs >= a.image_start && my_abs < a.image_end;
+  const int wg_queries = a.query_len - first_query < kQueries ? a.query_len - first_query : kQueries;
+  const int first_abs = a.query_offset + first_query;
+  const int last_abs = first_abs + wg_queries - 1;
+  const bool intersects = first_abs < a.image_end && last_abs >= a.image_start;
+  const int tile_end = intersects ? (last_abs + 1 > a.image_end ? last_abs + 1 : a.image_end) : last_abs + 1;
+  const int key_begin = it.key_begin;
+  const int visible_end = key_begin + it.keys < tile_end ? key_begin + it.keys : tile_end;
+  const int w_queries = a.query_len - wq0 < 32 ? a.query_len - wq0 : 32;
+  const int w_first = a.query_offset + wq0, w_last = w_first + (w_queries > 0 ? w_queries : 1) - 1;
+  const bool w_intersects = w_queries > 0 && w_first < a.image_end && w_last >= a.image_start;
+  const int w_visible = w_queries <= 0 ? 0 : (w_intersects ? (w_last + 1 > a.image_end ? w_last + 1 : a.image_end) : w_last + 1);
+  const bool w_all_image = w_first >= a.image_start && w_last < a.image_end;
+
+  // Q^T operand, step s: dims 16 s + 8 h .. + 7 of query l32, times 1/8
+  // (exact), split into three planes.
+  SplitFrag qb[3][4];
+  {
+    const float *src = a.q + (static_cast<size_t>(my_valid ? my_query : 0) * a.n_heads + head) * 64 + 8 * h;
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+      const float4 x = reinterpret_cast<const float4 *>(src + 16 * s)[0];
+      const float4 y = reinterpret_cast<const float4 *>(src + 16 * s)[1];
+      const float m = my_valid ? 0.125f : 0.0f;
+      const float qv[8] = {m * x.x, m * x.y, m * x.z, m * x.w, m * y.x, m * y.y, m * y.z, m * y.w};
+      split8(qv, qb[0][s].u, qb[1][s].u, qb[2][s].u);
+    }
+  }
+  v16f o[2];
+#pragma unroll
+  for (int d = 0; d < 2; d++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) o[d][r] = 0.0f;
+  float run_max = -__builtin_inff(), den = 0.0f;
+
+  // Tile t sits in array t % 3; tiles t + 1 and t + 2 are in flight while it
+  // is computed (past the last tile the copy repeats the last one).
+  auto step = [&](SplitKvTile &cur, SplitKvTile &ahead, int kstart) __attribute__((always_inline)) {
+    const int keys = visible_end - kstart < kKeys ? visible_end - kstart : kKeys;
+    __builtin_amdgcn_s_waitcnt(6 | 0x0070);  // vmcnt(6) lgkmcnt(0): this tile's six copies
+    plain_barrier();
+    if (keys > 0 && keys < kKeys) {
+      // Last tile: clear the V slots of keys past the visible ones in every
+      // plane (p = 0 there, and 0 * V must stay finite).
+      for (int idx = tid; idx < 3 * 64 * 32; idx += 256) {
+        const int p = idx >> 11, rem = idx & 2047, dim = rem >> 5, slot = rem & 31;
+        const int s2 = slot >> 4, hh = (slot >> 3) & 1, e = slot & 7;
+        const int key = 16 * s2 + 4 * hh + 8 * (e >> 2) + (e & 3);
+        if (key >= keys)
+          reinterpret_cast<uint16_t *>(&cur.v[p][dim * 4 + ((slot >> 3) ^ vs(dim))])[e] = 0;
+      }
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+      plain_barrier();
+    }
+    const int far = kstart + 2 * kKeys;
+    copy_split_tile(ahead, kp, vp, kplane, vplane, ktiles, (far < visible_end ? far : visible_end - 1) / kKeys, head,
+                    kv_head, wave, tid);
+    if (keys > 0 && w_queries > 0 && kstart < w_visible) {
+      const bool full = keys == kKeys && (kstart + kKeys <= w_first + 1 ||
+                                          (w_all_image && kstart >= a.image_start && kstart + kKeys <= a.image_end));
+      split_tile_step<STATIC, FAST>(a, cur, qb, o, run_max, den, kstart, keys, !full, h, l32, my_abs, my_image);
+    }
+  };
+  copy_split_tile(tile0, kp, vp, kplane, vplane, ktiles, key_begin / kKeys, head, kv_head, wave, tid);
+  copy_split_tile(tile1, kp, vp, kplane, vplane, ktiles,
+                  (key_begin + kKeys < visible_end ? key_begin + kKeys : visible_end - 1) / kKeys, head, kv_head, wave,
+                  tid);
+  for (int kstart = key_begin; kstart < visible_end; kstart += 3 * kKeys) {
+    step(tile0, tile2, kstart);
+    step(tile1, tile0, kstart + kKeys);
+    step(tile2, tile1, kstart + 2 * kKeys);
+  }
+
+  const float lse = STATIC ? logf_acc(den) : run_max + logf_acc(den);
+  const float sink_scale = __fdiv_rn(1.0f, 1.0f + expf_acc(a.sinks[head] - lse));
+  const bool split = parts > 1;
+  // The copies still in flight must land before the arrays are reused.
+  __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
+  __syncthreads();
+  // Transpose through LDS (8 KB per wave): o[d][r] is output dim
+  // 32 d + 8(r/4) + 4h + r%4 of query l32.
+  float4(*stage)[16] = reinterpret_cast<float4(*)[16]>(
+      wave == 0 ? &tile0.k[0][0] : wave == 1 ? &tile0.k[2][0] : wave == 2 ? &tile1.k[0][0] : &tile1.k[2][0]);
+#pragma unroll
+  for (int d = 0; d < 2; d++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const int dim = d * 32 + 8 * (r / 4) + 4 * h + (r % 4);
+      reinterpret_cast<float *>(&stage[l32][chunk(dim >> 2, l32)])[dim & 3] =
+          split ? o[d][r] : __fmul_rn(__fdiv_rn(o[d][r], den), sink_scale);
+    }
+  __syncthreads();
+  if (!split) {
+    for (int idx = lane; idx < 32 * 16; idx += 64) {
+      const int r = idx >> 4, c4 = idx & 15;
+      const int row = wq0 + r;
+      if (row < a.query_len)
+        reinterpret_cast<float4 *>(a.out + (static_cast<size_t>(row) * a.n_heads + head) * 64)[c4] =
+            stage[r][chunk(c4, r)];
+    }
+    return;
+  }
+  const size_t slot = static_cast<size_t>(plan.slot[order] + part) * a.n_heads + head;
+  float *po = a.part + slot * kQueries * 64 + wave * 32 * 64;
+  for (int idx = lane; idx < 32 * 16; idx += 64) {
+    const int r = idx >> 4, c4 = idx & 15;
+    reinterpret_cast<float4 *>(po + r * 64)[c4] = stage[r][chunk(c4, r)];
+  }
+  if (h == 0) {
+    float *pmd = a.part + static_cast<size_t>(a.slots) * a.n_heads * kQueries * 64 + slot * kQueries * 2;
+    reinterpret_cast<float2 *>(pmd)[wave * 32 + l32] = make_float2(STATIC ? 0.0f : run_max, den);
+  }
+}
+
 }  // namespace
 
 namespace {
@@ -437,6 +774,98 @@ int launch_attention(Ctx *ctx, const float *q, const float *prefix_k, const floa
     a.query_offset = static_cast<int>(query_offset + q0);
     const int rc = launch_tiles(ctx, a, softmax, exp_mode);
     if (rc != FOCR_OK) return rc;
+  }
+  return FOCR_OK;
+}
+
+int launch_attention_split(Ctx *ctx, const float *q, const float *k, const float *v, size_t query_len,
+                           size_t n_heads, size_t n_kv_heads, size_t image_start, size_t image_end, const float *sinks,
+                           int softmax, int exp_mode, float *out) {
+  FOCR_REQUIRE(query_len < (size_t(1) << 30) && n_heads < 65536, FOCR_E_SHAPE, "attention shape too large");
+  const size_t ktiles = (query_len + kKeys - 1) / kKeys;
+  const size_t kplane = n_heads * ktiles * 256, vplane = n_kv_heads * ktiles * 256;  // uint4 per plane
+  const size_t kv_bytes = 3 * (kplane + vplane) * sizeof(uint4);
+  AttnArgs a;
+  a.prefix_k = k;
+  a.generated_k = nullptr;
+  a.v = v;
+  a.sinks = sinks;
+  a.prefix_len = static_cast<int>(query_len);
+  a.total_len = static_cast<int>(query_len);
+  a.n_heads = static_cast<int>(n_heads);
+  a.n_kv_heads = static_cast<int>(n_kv_heads);
+  a.image_start = static_cast<int>(image_start);
+  a.image_end = static_cast<int>(image_end);
+  uint4 *kp = nullptr, *vp = nullptr;
+  auto split_kv = [&]() -> int {
+    kp = static_cast<uint4 *>(ctx->scratch);
+    vp = kp + 3 * kplane;
+    hipLaunchKernelGGL(split_kv_kernel, dim3(static_cast<unsigned>(ktiles), static_cast<unsigned>(n_heads)), dim3(256),
+                       0, ctx->stream, k, v, static_cast<int>(query_len), static_cast<int>(n_heads),
+                       static_cast<int>(n_kv_heads), static_cast<int>(ktiles), kp, vp);
+    FOCR_HIP_CHECK(hipGetLastError());
+    return FOCR_OK;
+  };
+  int rc = ensure_scratch(ctx, kv_bytes);
+  if (rc != FOCR_OK) return rc;
+  rc = split_kv();
+  if (rc != FOCR_OK) return rc;
+  // Query rows in launches of at most kMaxTiles query tiles, each with its
+  // split plan (parts of whole 32-key tiles) and merge.
+  const size_t per_launch = static_cast<size_t>(kMaxTiles) * kQueries;
+  for (size_t q0 = 0; q0 < query_len; q0 += per_launch) {
+    const int n = static_cast<int>(query_len - q0 < per_launch ? query_len - q0 : per_launch);
+    const int tiles = (n + kQueries - 1) / kQueries;
+    split::Plan plan;
+    int slots = 0;
+    const int items = split::make_plan(plan, tiles, n, static_cast<int>(q0), a.image_start, a.image_end, a.n_heads,
+                                       kKeys, split::kSplitItemsF32, &slots);
+    a.q = q + q0 * n_heads * 64;
+    a.out = out + q0 * n_heads * 64;
+    a.query_len = n;
+    a.query_offset = static_cast<int>(q0);
+    a.tiles = tiles;
+    a.slots = slots;
+    a.part = nullptr;
+    if (slots > 0) {
+      const size_t part_bytes = static_cast<size_t>(slots) * n_heads * kQueries * 66 * sizeof(float);
+      // The split K/V stay at the front of the scratch; growing it would
+      // discard them, so grow first and split again.
+      if (ctx->scratch_bytes < kv_bytes + part_bytes) {
+        rc = ensure_scratch(ctx, kv_bytes + part_bytes);
+        if (rc != FOCR_OK) return rc;
+        rc = split_kv();
+        if (rc != FOCR_OK) return rc;
+      }
+      a.part = reinterpret_cast<float *>(static_cast<char *>(ctx->scratch) + kv_bytes);
+    }
+    const dim3 grid(static_cast<unsigned>(items), static_cast<unsigned>(n_heads));
+    const int kt = static_cast<int>(ktiles);
+    if (softmax == FOCR_SOFTMAX_STATIC)
+      hipLaunchKernelGGL((attention_split_kernel<true, true>), grid, dim3(256), 0, ctx->stream, a, kp, vp, kplane,
+                         vplane, kt, plan);
+    else if (exp_mode == FOCR_EXP_FAST)
+      hipLaunchKernelGGL((attention_split_kernel<false, true>), grid, dim3(256), 0, ctx->stream, a, kp, vp, kplane,
+                         vplane, kt, plan);
+    else
+      hipLaunchKernelGGL((attention_split_kernel<false, false>), grid, dim3(256), 0, ctx->stream, a, kp, vp, kplane,
+                         vplane, kt, plan);
+    FOCR_HIP_CHECK(hipGetLastError());
+    if (slots > 0) {
+      split::Args m;
+      m.sinks = a.sinks;
+      m.out = a.out;
+      m.part = a.part;
+      m.query_len = a.query_len;
+      m.n_heads = a.n_heads;
+      m.tiles = tiles;
+      m.slots = slots;
+      m.merge_end = a.query_len;
+      hipLaunchKernelGGL(split::merge_kernel,
+                         dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(a.n_heads), split::kMergeSplit),
+                         dim3(256), 0, ctx->stream, m, plan);
+      FOCR_HIP_CHECK(hipGetLastError());
+    }
   }
   return FOCR_OK;
 }

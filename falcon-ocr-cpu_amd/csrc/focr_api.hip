@@ -530,6 +530,30 @@ int focr_attention_prefill(focr_ctx *handle, const float *q, const float *prefix
                           n_kv_heads, query_offset, image_start, image_end, sinks, softmax, exp_mode, out);
 }
 
+int focr_attention_prefill_split(focr_ctx *handle, const float *q, const float *prefix_k, const float *generated_k,
+                                 const float *v, size_t query_len, size_t prefix_len, size_t total_len,
+                                 size_t n_heads, size_t n_kv_heads, size_t head_dim, size_t query_offset,
+                                 size_t image_start, size_t image_end, const float *sinks, int softmax,
+                                 int exp_mode, float *out) {
+  Ctx *ctx = reinterpret_cast<Ctx *>(handle);
+  FOCR_REQUIRE(ctx, FOCR_E_ARG, "focr_attention_prefill_split: null context");
+  FOCR_REQUIRE(head_dim > 0 && n_heads > 0 && n_kv_heads > 0, FOCR_E_SHAPE, "attention head dimensions must be positive");
+  FOCR_REQUIRE(head_dim == 64, FOCR_E_UNSUPPORTED, "the hip attention tiles take head_dim 64");
+  FOCR_REQUIRE(n_heads % n_kv_heads == 0, FOCR_E_SHAPE, "attention GQA grouping");
+  FOCR_REQUIRE(prefix_len <= total_len, FOCR_E_SHAPE, "attention prefix length");
+  FOCR_REQUIRE(image_start <= image_end && image_end <= prefix_len, FOCR_E_SHAPE, "attention image must be inside the prefix");
+  FOCR_REQUIRE(query_offset + query_len <= total_len, FOCR_E_SHAPE, "attention query interval");
+  FOCR_REQUIRE(softmax == FOCR_SOFTMAX_ONLINE || softmax == FOCR_SOFTMAX_STATIC, FOCR_E_ARG, "unknown softmax");
+  FOCR_REQUIRE(exp_mode == FOCR_EXP_FAST || exp_mode == FOCR_EXP_EXACT, FOCR_E_ARG, "unknown exp mode");
+  FOCR_REQUIRE(query_offset == 0 && query_len == prefix_len && prefix_len == total_len, FOCR_E_UNSUPPORTED,
+               "the split-product attention takes pure prefills; focr_attention_prefill takes the rest");
+  if (query_len == 0) return FOCR_OK;
+  FOCR_REQUIRE(q && prefix_k && v && sinks && out, FOCR_E_ARG, "focr_attention_prefill_split: null buffer");
+  FOCR_HIP_CHECK(hipSetDevice(ctx->device));
+  return launch_attention_split(ctx, q, prefix_k, v, query_len, n_heads, n_kv_heads, image_start, image_end, sinks,
+                                softmax, exp_mode, out);
+}
+
 int focr_attention_prefill_bf16(focr_ctx *handle, const float *q, const float *k, const float *v, size_t query_len,
                                 size_t n_heads, size_t n_kv_heads, size_t head_dim, size_t image_start,
                                 size_t image_end, const float *sinks, int softmax, int exp_mode, float *out) {

@@ -99,6 +99,9 @@ int launch_attention(Ctx *ctx, const float *q, const float *prefix_k, const floa
                      const float *v, size_t query_len, size_t prefix_len, size_t total_len,
                      size_t n_heads, size_t n_kv_heads, size_t query_offset, size_t image_start,
                      size_t image_end, const float *sinks, int softmax, int exp_mode, float *out);
+int launch_attention_split(Ctx *ctx, const float *q, const float *k, const float *v, size_t query_len,
+                           size_t n_heads, size_t n_kv_heads, size_t image_start, size_t image_end, const float *sinks,
+                           int softmax, int exp_mode, float *out);
 int launch_attention_bf16(Ctx *ctx, const float *q, const float *k, const float *v, size_t query_len,
                           size_t n_heads, size_t n_kv_heads, size_t image_start, size_t image_end,
                           const float *sinks, int softmax, float *out);
@@ -138,6 +141,29 @@ __device__ __forceinline__ float sdwa_cvt(uint32_t w) {
     asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:WORD_1" : "=v"(r) : "v"(w));
   return r;
 }
+// An FP32 value as three BF16 parts, x = hi + mid + lo exactly for every
+// finite x (bit patterns in the low 16 bits of each result): hi = x with the
+// low 16 bits of its pattern cleared (truncated to BF16), mid = (x - hi)
+// truncated, lo = x - hi - mid. Both differences are exact (they clear
+// leading bits of a value of the same sign and binade) and the last has at
+// most 8 significant bits, so no part rounds; |mid| < 2^-7 |x|, |lo| <
+// 2^-14 |x|. An infinity or NaN travels in hi alone (mid = lo = 0).
+__device__ __forceinline__ void split3(float x, uint32_t &hi, uint32_t &mid, uint32_t &lo) {
+  const uint32_t b = __float_as_uint(x);
+  if ((b & 0x7f800000u) == 0x7f800000u) {  // infinity or NaN
+    hi = (b & 0x007fffffu) ? 0x7fc0u : (b >> 16);
+    mid = lo = 0;
+    return;
+  }
+  const uint32_t h = b & 0xffff0000u;
+  const float r1 = x - __uint_as_float(h);
+  const uint32_t m = __float_as_uint(r1) & 0xffff0000u;
+  const float r2 = r1 - __uint_as_float(m);
+  hi = h >> 16;
+  mid = m >> 16;
+  lo = __float_as_uint(r2) >> 16;  // r2 fits 8 significant bits: no rounding
+}
+
 // squared_relu_glu, src/kernels/mod.rs:567-572.
 __device__ __forceinline__ float squared_relu_glu(float gate, float up) {
   float relu = gate > 0.0f ? gate : 0.0f;

@@ -925,22 +925,6 @@ void launch_one(bool chain, const GemmArgs &a, hipStream_t stream) {
 // v_mfma_f32_32x32x2f32.
 constexpr int kSplitBM = 128, kSplitBN = 128, kSplitBK = 16, kSplitKAlign = 32;
 
-__device__ __forceinline__ void split3(float x, uint32_t &hi, uint32_t &mid, uint32_t &lo) {
-  const uint32_t b = __float_as_uint(x);
-  if ((b & 0x7f800000u) == 0x7f800000u) {  // infinity or NaN
-    hi = (b & 0x007fffffu) ? 0x7fc0u : (b >> 16);
-    mid = lo = 0;
-    return;
-  }
-  const uint32_t h = b & 0xffff0000u;
-  const float r1 = x - __uint_as_float(h);
-  const uint32_t m = __float_as_uint(r1) & 0xffff0000u;
-  const float r2 = r1 - __uint_as_float(m);
-  hi = h >> 16;
-  mid = m >> 16;
-  lo = __float_as_uint(r2) >> 16;  // r2 fits 8 significant bits: no rounding
-}
-
 // Three BF16 planes of fl(src * row_scale[row]) (or of src), zero past rows
 // and cols, stage-major: plane p, 16-k stage s, row r at
 // ((p * stages + s) * rows_pad + r) * 16, so that one stage of consecutive

@@ -170,6 +170,26 @@ extern "C" {
         exp_mode: c_int,
         out_dev: *mut f32,
     ) -> c_int;
+    pub fn focr_attention_prefill_split(
+        ctx: *mut focr_ctx,
+        q_dev: *const f32,
+        prefix_k_dev: *const f32,
+        generated_k_dev: *const f32,
+        v_dev: *const f32,
+        query_len: usize,
+        prefix_len: usize,
+        total_len: usize,
+        n_heads: usize,
+        n_kv_heads: usize,
+        head_dim: usize,
+        query_offset: usize,
+        image_start: usize,
+        image_end: usize,
+        sinks_dev: *const f32,
+        softmax: c_int,
+        exp_mode: c_int,
+        out_dev: *mut f32,
+    ) -> c_int;
     pub fn focr_attention_prefill_bf16(
         ctx: *mut focr_ctx,
         q_dev: *const f32,

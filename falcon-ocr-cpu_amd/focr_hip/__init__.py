@@ -74,6 +74,7 @@ SIGNATURES = {
     "focr_linear_prefill": (_I, [_P, _P, _P, _Z, _P, _I, _I, _P]),
     "focr_row_scales": (_I, [_P, _P, _Z, _Z, _F, _P]),
     "focr_attention_prefill": (_I, [_P, _P, _P, _P, _P, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _P, _I, _I, _P]),
+    "focr_attention_prefill_split": (_I, [_P, _P, _P, _P, _P, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _Z, _P, _I, _I, _P]),
     "focr_attention_prefill_bf16": (_I, [_P, _P, _P, _P, _Z, _Z, _Z, _Z, _Z, _Z, _P, _I, _I, _P]),
     "focr_argmax": (_I, [_P, _P, _Z, _Z, _P]),
     "focr_kv_seal": (_I, [_P, _I, _P, _P, _Z, _Z, _Z, _Z, _Z, ctypes.POINTER(_P)]),
@@ -392,11 +393,15 @@ class ExpMode(enum.IntEnum):
 class PrefillOptions:
     """attention/mod.rs:205-221: `softmax` is the BF16 kernels' softmax
     (static shift by default, as the reference's PrefillSoftmax), and
-    `fp32_softmax` the FP32 tiles' one."""
+    `fp32_softmax` the FP32 tiles' one. `split_products` (a `hip` choice,
+    no reference counterpart) forms the FP32 tiles' products from exact
+    three-way BF16 splits on a pure prefill (focr_attention_prefill_split);
+    False keeps the FP32 matrix cores everywhere."""
 
     exp: ExpMode = ExpMode.FAST
     fp32_softmax: Softmax = Softmax.ONLINE
     softmax: Softmax = Softmax.STATIC
+    split_products: bool = True
 
 
 def attention_with(q, kv: CompactKv, query_len: int, geometry: Geometry, sinks, options: PrefillOptions = PrefillOptions(),
@@ -405,18 +410,20 @@ def attention_with(q, kv: CompactKv, query_len: int, geometry: Geometry, sinks, 
 
     As the reference dispatches (attention/mod.rs:271-311): fewer than 4
     queries, or up to 8 over a cache with generated keys (decode and draft
-    verification), take the decode kernel; the rest the prefill tiles."""
+    verification), take the decode kernel; the rest the prefill tiles (their
+    products from exact BF16 splits on a pure prefill unless
+    `options.split_products` is False)."""
     torch = _torch()
     ctx = ctx or default_context()
     if output is None:
         output = torch.empty_like(q)
     if query_len < 4 or (query_len <= 8 and kv.total_len > kv.prefix_len):
         return attention_decode(q, kv, query_len, geometry, sinks, output=output, ctx=ctx)
-    _check(lib().focr_attention_prefill(ctx.handle, _dev(q), _dev(kv.prefix_k), _dev(kv.generated_k), _dev(kv.v),
-                                        query_len, kv.prefix_len, kv.total_len, kv.n_heads, kv.n_kv_heads,
-                                        kv.head_dim, geometry.query_offset, geometry.image_start,
-                                        geometry.image_end, _dev(sinks), int(options.fp32_softmax),
-                                        int(options.exp), _dev(output)))
+    pure = geometry.query_offset == 0 and query_len == kv.prefix_len == kv.total_len
+    fn = lib().focr_attention_prefill_split if options.split_products and pure else lib().focr_attention_prefill
+    _check(fn(ctx.handle, _dev(q), _dev(kv.prefix_k), _dev(kv.generated_k), _dev(kv.v), query_len, kv.prefix_len,
+              kv.total_len, kv.n_heads, kv.n_kv_heads, kv.head_dim, geometry.query_offset, geometry.image_start,
+              geometry.image_end, _dev(sinks), int(options.fp32_softmax), int(options.exp), _dev(output)))
     return output
 
 

@@ -202,6 +202,21 @@ int focr_attention_prefill(focr_ctx *ctx, const float *q_dev, const float *prefi
                            size_t image_start, size_t image_end, const float *sinks_dev,
                            int softmax, int exp_mode, float *out_dev);
 
+/* The same attention for a pure prefill (query_offset 0, every key a prefix
+ * key, query_len == prefix_len == total_len), with every QK and PV product
+ * formed from exact three-way BF16 splits of its FP32 operands (x = hi + mid
+ * + lo with no rounding; the six largest part products, FP32 accumulation)
+ * on the BF16 matrix cores: within the FP32 tolerance of the reference tiles,
+ * like focr_attention_prefill, at about twice its speed. Other geometries
+ * return FOCR_E_UNSUPPORTED and write nothing (focr_attention_prefill takes
+ * them). Splits K and V into the context scratch first. */
+int focr_attention_prefill_split(focr_ctx *ctx, const float *q_dev, const float *prefix_k_dev,
+                                 const float *generated_k_dev, const float *v_dev, size_t query_len,
+                                 size_t prefix_len, size_t total_len, size_t n_heads,
+                                 size_t n_kv_heads, size_t head_dim, size_t query_offset,
+                                 size_t image_start, size_t image_end, const float *sinks_dev,
+                                 int softmax, int exp_mode, float *out_dev);
+
 /* ---- A8: BF16 prefill attention ----------------------------------------- */
 /* kernels::attention_prefill_bf16 (src/kernels/attention/mod.rs:320-352) ->
  * prefill64::bf16::compact_prefill (prefill64/bf16.rs:70-175, plans Bf16 /

@@ -1,5 +1,10 @@
 """Prefill attention on the GPU against the oracle within the FP32 tolerance
-(src/kernels/attention/prefill64/tests.rs:36-84, static_shift/tests.rs)."""
+(src/kernels/attention/prefill64/tests.rs:36-84, static_shift/tests.rs).
+
+A pure prefill takes the products from exact BF16 splits by default
+(focr_attention_prefill_split); `split_products=False` and every prefill over
+generated keys take the FP32 matrix-core products (focr_attention_prefill).
+Both are held to the same bound."""
 import numpy as np
 import pytest
 
@@ -37,24 +42,28 @@ def run(fh, q, k, v, sinks, L, geometry, options, prefix=None, total=None, gener
 
 @pytest.mark.parametrize("L,image_start,image_end", CASES)
 @pytest.mark.parametrize("exp", ["fast", "exact"])
-def test_online_prefill(fh, L, image_start, image_end, exp):
+@pytest.mark.parametrize("products", ["split", "fp32"])
+def test_online_prefill(fh, L, image_start, image_end, exp, products):
     q = gen.att_values(L * 16 * 64, 17 + L, 3.0)
     k = gen.att_values(L * 16 * 64, 19 + L, 3.0)
     v = gen.att_values(L * 8 * 64, 23 + L, 3.0)
     sinks = gen.att_values(16, 29, 2.0)
-    opts = fh.PrefillOptions(exp=fh.ExpMode.FAST if exp == "fast" else fh.ExpMode.EXACT)
+    opts = fh.PrefillOptions(exp=fh.ExpMode.FAST if exp == "fast" else fh.ExpMode.EXACT,
+                             split_products=products == "split")
     got = run(fh, q, k, v, sinks, L, (0, image_start, image_end), opts)
     want = oracle.attention_prefill(q, k, v, L, L, L, 16, 8, 0, image_start, image_end, sinks, exp_fast=exp == "fast")
     close(got, want)
 
 
 @pytest.mark.parametrize("L,image_start,image_end", CASES[:4])
-def test_static_prefill(fh, L, image_start, image_end):
+@pytest.mark.parametrize("products", ["split", "fp32"])
+def test_static_prefill(fh, L, image_start, image_end, products):
     q = gen.normalized(L * 16 * 64, 17 + L)
     k = gen.normalized(L * 16 * 64, 19 + L)
     v = gen.values(L * 8 * 64, 23 + L, 3.0)
     sinks = gen.values(16, 29, 2.0)
-    got = run(fh, q, k, v, sinks, L, (0, image_start, image_end), fh.PrefillOptions(fp32_softmax=fh.Softmax.STATIC))
+    opts = fh.PrefillOptions(fp32_softmax=fh.Softmax.STATIC, split_products=products == "split")
+    got = run(fh, q, k, v, sinks, L, (0, image_start, image_end), opts)
     want = oracle.attention_prefill(q, k, v, L, L, L, 16, 8, 0, image_start, image_end, sinks, static=True)
     close(got, want)
 
@@ -75,7 +84,8 @@ def test_generated_keys(fh, L, prefix, total, offset, image):
 
 
 @pytest.mark.parametrize("static", [False, True])
-def test_config4_full_page(fh, static):
+@pytest.mark.parametrize("products", ["split", "fp32"])
+def test_config4_full_page(fh, static, products):
     # 6,544 tokens, 16 heads x 64, image prefix 4,096,
     # Q/K/V ~ N(0,1); every output against the oracle's tiles (their
     # lane-vectorized restatement, bitwise the oracle), online softmax with
@@ -88,7 +98,8 @@ def test_config4_full_page(fh, static):
     if static:  # the static shift needs bounded scores (prefill64/static_shift.rs)
         q = gen.normalized(L * 16 * 64, 24)
         k = gen.normalized(L * 16 * 64, 25)
-    opts = fh.PrefillOptions(fp32_softmax=fh.Softmax.STATIC if static else fh.Softmax.ONLINE)
+    opts = fh.PrefillOptions(fp32_softmax=fh.Softmax.STATIC if static else fh.Softmax.ONLINE,
+                             split_products=products == "split")
     got = run(fh, q, k, v, sinks, L, (0, 0, image_end), opts)
     assert np.all(np.isfinite(got))
     oracle.set_threads(oracle_threads())
@@ -149,3 +160,64 @@ def test_more_queries_than_one_launch(fh):
     got = run(fh, q, k, v, sinks, L, (0, 0, 2048), fh.PrefillOptions())
     assert np.all(np.isfinite(got))
     close(got, oracle.attention_prefill_fast(q, k, v, L, L, L, 16, 8, 0, 0, 2048, sinks))
+
+
+def attention_f64(q, k, v, L, n_heads, n_kv, image, sinks):
+    """The exact attention of a pure prefill in float64: scores q.k / 8 over
+    the keys a query sees (causal, plus the whole image for image queries),
+    softmax, times V, scaled by 1 / (1 + exp(sink - logsumexp))."""
+    q = q.reshape(L, n_heads, 64).astype(np.float64)
+    k = k.reshape(L, n_heads, 64).astype(np.float64)
+    v = v.reshape(L, n_kv, 64).astype(np.float64)
+    i, j = np.arange(L)[:, None], np.arange(L)[None, :]
+    in_image = lambda x: (x >= image[0]) & (x < image[1])
+    visible = (j <= i) | (in_image(i) & in_image(j))
+    out = np.empty((L, n_heads, 64))
+    for h in range(n_heads):
+        s = np.where(visible, q[:, h] @ k[:, h].T / 8.0, -np.inf)
+        m = s.max(axis=1, keepdims=True)
+        p = np.exp(s - m)
+        den = p.sum(axis=1, keepdims=True)
+        lse = m + np.log(den)
+        out[:, h] = (p @ v[:, h // (n_heads // n_kv)]) / den / (1.0 + np.exp(sinks[h] - lse))
+    return out
+
+
+def test_split_products_error_is_fp32_level(fh):
+    # Against the exact attention (float64, exact exp): the split products'
+    # error is of the order of the FP32 matrix-core products' (both within the
+    # FP32 bound above), max and mean.
+    L, image = 1000, (0, 300)
+    q = gen.normal(L * 16 * 64, 1.0, 60)
+    k = gen.normal(L * 16 * 64, 1.0, 61)
+    v = gen.normal(L * 8 * 64, 1.0, 62)
+    sinks = gen.uniform(16, -2.0, 2.0, 63)
+    exact = attention_f64(q, k, v, L, 16, 8, image, sinks.astype(np.float64))
+    err = {}
+    for products in ("split", "fp32"):
+        opts = fh.PrefillOptions(exp=fh.ExpMode.EXACT, split_products=products == "split")
+        d = np.abs(run(fh, q, k, v, sinks, L, (0, *image), opts).astype(np.float64) - exact)
+        err[products] = (float(d.max()), float(d.mean()))
+    assert err["split"][0] <= 2 * err["fp32"][0] and err["split"][1] <= 2 * err["fp32"][1], err
+
+
+def test_split_products_take_pure_prefills_only(fh):
+    # A prefill over generated keys, or one that starts past key 0, is refused
+    # by the split entry point (nothing written) and taken by the FP32 one.
+    import torch
+
+    L, prefix, total = 40, 40, 48
+    q = to_dev(gen.att_values(L * 16 * 64, 71, 3.0))
+    pk = to_dev(gen.att_values(prefix * 16 * 64, 83, 3.0))
+    gk = to_dev(gen.att_values((total - prefix) * 8 * 64, 37, 3.0))
+    v = to_dev(gen.att_values(total * 8 * 64, 117, 3.0))
+    sinks = to_dev(gen.att_values(16, 29, 2.0))
+    out = torch.full((L * 16 * 64,), 7.0, device=q.device)
+    ctx = fh.default_context()
+    for qlen, prefix_len, total_len, offset in ((L, prefix, total, 8), (L - 8, prefix, prefix, 8)):
+        rc = fh.lib().focr_attention_prefill_split(ctx.handle, q.data_ptr(), pk.data_ptr(), gk.data_ptr(),
+                                                   v.data_ptr(), qlen, prefix_len, total_len, 16, 8, 64, offset, 1,
+                                                   20, sinks.data_ptr(), 0, 0, out.data_ptr())
+        assert rc == fh.FOCR_E_UNSUPPORTED
+    torch.cuda.synchronize()
+    assert bool(torch.all(out == 7.0))

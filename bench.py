@@ -265,7 +265,7 @@ def bench_attention(torch, fh, gen, np, reps):
     flops = 4.0 * 64 * visible * 16
     res = {"visible_pairs_per_head": visible, "gflop": round(flops / 1e9, 2)}
     timer = Timer(torch)
-    # FP32 products from exact BF16 splits (the default on a pure prefill),
+    # FP32 products from scaled FP16 pairs (the default on a pure prefill),
     # then on the FP32 matrix cores (split_products=False).
     for name, opts in (("online_fast", fh.PrefillOptions()), ("static", fh.PrefillOptions(fp32_softmax=fh.Softmax.STATIC)),
                        ("online_fast_fp32_mfma", fh.PrefillOptions(split_products=False)),

@@ -362,16 +362,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void a
   }
 }
 
-// ---- FP32 products from exact BF16 splits (focr_attention_prefill_split) ---
+// ---- FP32 products from FP16 pairs (focr_attention_prefill_split) --------
 // The same tiles, softmax, masks, sinks and work split as attention_kernel,
-// with every product of S^T = K Q^T and O^T = V^T P^T formed from exact
-// three-way BF16 splits (split3: x = hi + mid + lo with no rounding) on
-// v_mfma_f32_32x32x16_bf16: six part products per FP32 product (hi.hi,
-// hi.mid, mid.hi, hi.lo, lo.hi, mid.mid; the three left out are below
-// 2^-21 |x y| together), FP32 accumulation. Per 32-key tile a wave issues
-// 24 + 24 BF16 products (32 matrix-core cycles each) in place of 32 + 32
-// FP32 ones (64 cycles each).
-// A pre-pass writes the call's K and V as three BF16 planes of 32-key tiles
+// with every product of S^T = K Q^T and O^T = V^T P^T formed on
+// v_mfma_f32_32x32x16_f16 from two-term FP16 expansions of power-of-two
+// scaled FP32 operands: with x' = x 2^e, hi = fp16(x'), lo = fp16(x' - hi),
+// so x' = hi + lo to about 2^-22 |x'|. Three products per FP32 product
+// (hi.hi, hi.lo, lo.hi; lo.lo is below 2^-21 |x' y'|), FP32 accumulation and
+// exact power-of-two descaling keep the result at the FP32 products' error.
+// The exponents put the largest magnitude of each scale block in
+// [2^14, 2^15): Q per query row (in the kernel), K per 32-key tile of a head,
+// V per (KV head, dim) over every key, P per tile by 2^14 (online softmax:
+// P <= 1) or per query by a running power-of-two maximum (static softmax:
+// P = e^s). Per 32-key tile a wave issues 12 + 12 FP16 products (32 matrix-
+// core cycles each) in place of 32 + 32 FP32 ones (64 cycles each).
+// A pre-pass writes the call's K and V as two FP16 planes of 32-key tiles
 // (zero past the last key), in the BF16 attention's tile layouts:
 //   K: [plane][head][tile][32 keys][8 chunks of 8 dims], chunk c of key r
 //      stored at c ^ ks(r);
@@ -380,35 +385,89 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void a
 //      which the score registers feed the PV product), chunk c of dim d at
 //      c ^ vs(d).
 // The swizzles put the sixteen 16-byte chunks that sixteen consecutive lanes
-// read in distinct bank groups. Q is split once per wave, each tile's
-// probabilities as they feed PV.
+// read in distinct bank groups.
 __device__ __forceinline__ int ks(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 __device__ __forceinline__ int vs(int d) { return ((d >> 1) & 3) ^ ((d >> 3) & 1); }
 
-typedef __bf16 split_bf16x8 __attribute__((ext_vector_type(8)));
-union SplitFrag {
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+union HalfFrag {
   uint4 u;
-  split_bf16x8 v;
+  half8 v;
 };
 
-// Eight FP32 values as three BF16x8 fragments (hi, mid, lo).
-__device__ __forceinline__ void split8(const float (&x)[8], uint4 &hi, uint4 &mid, uint4 &lo) {
-  uint32_t h[8], m[8], l[8];
-#pragma unroll
-  for (int e = 0; e < 8; e++) split3(x[e], h[e], m[e], l[e]);
-  hi = make_uint4(h[0] | h[1] << 16, h[2] | h[3] << 16, h[4] | h[5] << 16, h[6] | h[7] << 16);
-  mid = make_uint4(m[0] | m[1] << 16, m[2] | m[3] << 16, m[4] | m[5] << 16, m[6] | m[7] << 16);
-  lo = make_uint4(l[0] | l[1] << 16, l[2] | l[3] << 16, l[4] | l[5] << 16, l[6] | l[7] << 16);
+// Exponents are kept in [-100, 127] so that 2^(15 - e) and 2^(e - 15) are
+// normal floats; a block whose largest magnitude is below 2^-101 keeps that
+// scale (its values then sit below 2^14).
+constexpr int kMinExp = -100;
+
+// The exponent e of a block's largest finite magnitude m (2^(e-1) <= m <
+// 2^e), clamped below at kMinExp (also for m = 0).
+__device__ __forceinline__ int block_exp(float m) {
+  const int e = m > 0.0f ? __builtin_amdgcn_frexp_expf(m) : kMinExp;
+  return e < kMinExp ? kMinExp : e;
 }
 
-// Block (tile, head): K of query head `head` (thread = key row r, chunk c)
-// and, for head < n_kv_heads, V of that KV head (thread = dim d, chunk c).
-__global__ __launch_bounds__(256) void split_kv_kernel(const float *__restrict__ k, const float *__restrict__ v,
-                                                       int total, int n_heads, int n_kv_heads, int tiles,
-                                                       uint4 *__restrict__ kp, uint4 *__restrict__ vp) {
+// |x| for finite x, 0 otherwise (an infinity or NaN does not set the scale).
+__device__ __forceinline__ float finite_abs(float x) {
+  const float a = __builtin_fabsf(x);
+  return a <= 3.4028234663852886e38f ? a : 0.0f;
+}
+
+// Eight FP32 values times 2^shift as FP16 (hi, lo) fragments, hi and lo
+// rounded to nearest; an infinity or NaN travels in hi alone (lo = 0).
+__device__ __forceinline__ void pair8(const float (&x)[8], int shift, uint4 &hi, uint4 &lo) {
+  HalfFrag h, l;
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    const float xs = __builtin_ldexpf(x[e], shift);
+    const _Float16 a = static_cast<_Float16>(xs);
+    const bool finite = __builtin_fabsf(x[e]) <= 3.4028234663852886e38f;
+    h.v[e] = a;
+    l.v[e] = finite ? static_cast<_Float16>(xs - static_cast<float>(a)) : static_cast<_Float16>(0.0f);
+  }
+  hi = h.u;
+  lo = l.u;
+}
+
+// Per (KV head, dim): the largest finite |v| over every key, as float bits
+// (atomic unsigned max of non-negative floats). Block (tile, kv head):
+// thread = dim d, key quarter kq.
+__global__ __launch_bounds__(256) void pair_vmax_kernel(const float *__restrict__ v, int total, int n_kv_heads,
+                                                        unsigned *__restrict__ vmax) {
+  __shared__ float part[4][64];
+  const int tile = blockIdx.x, head = blockIdx.y, t = threadIdx.x;
+  const int d = t & 63, kq = t >> 6;
+  float m = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    const int key = tile * kKeys + 8 * kq + e;
+    if (key < total) m = __builtin_fmaxf(m, finite_abs(v[(static_cast<size_t>(key) * n_kv_heads + head) * 64 + d]));
+  }
+  part[kq][d] = m;
+  __syncthreads();
+  if (t < 64) {
+    const float r = __builtin_fmaxf(__builtin_fmaxf(part[0][t], part[1][t]), __builtin_fmaxf(part[2][t], part[3][t]));
+    atomicMax(vmax + head * 64 + t, __float_as_uint(r));
+  }
+}
+
+__global__ __launch_bounds__(64) void pair_zero_kernel(unsigned *__restrict__ p, int n) {
+  const int i = blockIdx.x * 64 + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+// Block (tile, head): K of query head `head` (thread = key row r, chunk c;
+// the tile's exponent from the block's largest magnitude, kexp[head][tile])
+// and, for head < n_kv_heads, V of that KV head (thread = dim d, chunk c;
+// the dim's exponent from vmax).
+__global__ __launch_bounds__(256) void pair_kv_kernel(const float *__restrict__ k, const float *__restrict__ v,
+                                                      int total, int n_heads, int n_kv_heads, int tiles,
+                                                      const unsigned *__restrict__ vmax, uint4 *__restrict__ kp,
+                                                      uint4 *__restrict__ vp, int *__restrict__ kexp) {
+  __shared__ float wmax[4];
   const int tile = blockIdx.x, head = blockIdx.y, t = threadIdx.x;
   const size_t kplane = static_cast<size_t>(n_heads) * tiles * 256, vplane = static_cast<size_t>(n_kv_heads) * tiles * 256;
-  if (head < n_heads) {
+  {
     const int r = t >> 3, c = t & 7;
     const int key = tile * kKeys + r;
     float val[8];
@@ -420,12 +479,20 @@ __global__ __launch_bounds__(256) void split_kv_kernel(const float *__restrict__
       val[0] = x.x; val[1] = x.y; val[2] = x.z; val[3] = x.w;
       val[4] = y.x; val[5] = y.y; val[6] = y.z; val[7] = y.w;
     }
-    uint4 hi, mid, lo;
-    split8(val, hi, mid, lo);
+    float m = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) m = __builtin_fmaxf(m, finite_abs(val[e]));
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, off));
+    if ((t & 63) == 0) wmax[t >> 6] = m;
+    __syncthreads();
+    const int ex = block_exp(__builtin_fmaxf(__builtin_fmaxf(wmax[0], wmax[1]), __builtin_fmaxf(wmax[2], wmax[3])));
+    if (t == 0) kexp[head * tiles + tile] = ex;
+    uint4 hi, lo;
+    pair8(val, 15 - ex, hi, lo);
     const size_t i = (static_cast<size_t>(head) * tiles + tile) * 256 + r * 8 + (c ^ ks(r));
     kp[i] = hi;
-    kp[kplane + i] = mid;
-    kp[2 * kplane + i] = lo;
+    kp[kplane + i] = lo;
   }
   if (head < n_kv_heads) {
     const int d = t >> 2, c = t & 3;
@@ -437,28 +504,27 @@ __global__ __launch_bounds__(256) void split_kv_kernel(const float *__restrict__
       const int key = tile * kKeys + 16 * s + 4 * hh + 8 * (ee >> 2) + (ee & 3);
       val[e] = key < total ? v[(static_cast<size_t>(key) * n_kv_heads + head) * 64 + d] : 0.0f;
     }
-    uint4 hi, mid, lo;
-    split8(val, hi, mid, lo);
+    uint4 hi, lo;
+    pair8(val, 15 - block_exp(__uint_as_float(vmax[head * 64 + d])), hi, lo);
     const size_t i = (static_cast<size_t>(head) * tiles + tile) * 256 + d * 4 + (c ^ vs(d));
     vp[i] = hi;
-    vp[vplane + i] = mid;
-    vp[2 * vplane + i] = lo;
+    vp[vplane + i] = lo;
   }
 }
 
-// One buffered key tile of the split kernel: [plane][256 chunks] of K and V.
-struct SplitKvTile {
-  uint4 k[3][256];
-  uint4 v[3][256];
+// One buffered key tile of the pair kernel: [plane][256 chunks] of K and V.
+struct PairKvTile {
+  uint4 k[2][256];
+  uint4 v[2][256];
 };
 
-// Copies split tile `kt` (this head's K planes, its KV head's V planes) into
-// t: thread tid moves chunk tid of each of the six 4 KB planes.
-__device__ __forceinline__ void copy_split_tile(SplitKvTile &t, const uint4 *kp, const uint4 *vp, size_t kplane,
-                                                size_t vplane, int tiles, int kt, int head, int kv_head, int wave,
-                                                int tid) {
+// Copies pair tile `kt` (this head's K planes, its KV head's V planes) into
+// t: thread tid moves chunk tid of each of the four 4 KB planes.
+__device__ __forceinline__ void copy_pair_tile(PairKvTile &t, const uint4 *kp, const uint4 *vp, size_t kplane,
+                                               size_t vplane, int tiles, int kt, int head, int kv_head, int wave,
+                                               int tid) {
 #pragma unroll
-  for (int p = 0; p < 3; p++) {
+  for (int p = 0; p < 2; p++) {
     __builtin_amdgcn_global_load_lds((global_void *)(kp + p * kplane + (static_cast<size_t>(head) * tiles + kt) * 256 + tid),
                                      (lds_void *)(&t.k[p][64 * wave]), 16, 0, 0);
     __builtin_amdgcn_global_load_lds((global_void *)(vp + p * vplane + (static_cast<size_t>(kv_head) * tiles + kt) * 256 + tid),
@@ -466,46 +532,86 @@ __device__ __forceinline__ void copy_split_tile(SplitKvTile &t, const uint4 *kp,
   }
 }
 
-// One 32-key tile of one wave: tile_step's softmax with split products.
+// Two FP32 values as an FP16 pair each, rounded toward zero: hi of both in
+// one word, lo of both in the other (x >= 0 here, so lo >= 0 and
+// x = hi + lo to 2^-21 |x|).
+__device__ __forceinline__ void pair2_rtz(float x0, float x1, uint32_t &hi, uint32_t &lo) {
+  const auto h = __builtin_amdgcn_cvt_pkrtz(x0, x1);
+  const auto l = __builtin_amdgcn_cvt_pkrtz(x0 - static_cast<float>(h[0]), x1 - static_cast<float>(h[1]));
+  hi = __builtin_bit_cast(uint32_t, h);
+  lo = __builtin_bit_cast(uint32_t, l);
+}
+
+// One 32-key tile of one wave: tile_step's softmax with FP16-pair products.
+// c = the score factor (the Q, K and 1/8 descale, times log2(e) for the
+// static form's base-2 exp); pexp = the static form's running P exponent.
 template <bool STATIC, bool FAST>
-__device__ __forceinline__ void split_tile_step(const AttnArgs &a, const SplitKvTile &t, const SplitFrag (&qb)[3][4],
-                                                v16f (&o)[2], float &run_max, float &den, int kstart, int keys,
-                                                bool need_mask, int h, int l32, int my_abs, bool my_image) {
-  // S^T = K Q^T: step s covers dims 16 s .. 16 s + 15 (lane half h: 8 h ..).
-  SplitFrag kf[3][4];
+__device__ __forceinline__ void pair_tile_step(const PairKvTile &t, const HalfFrag (&qf)[2][4], v16f (&o)[2],
+                                               float &run_max, float &den, int &pexp, float c, int kstart, int keys,
+                                               bool need_mask, int h, int l32, int my_abs, bool my_image,
+                                               int image_start, int image_end) {
+  // S^T = K Q^T: step s covers dims 16 s .. 16 s + 15 (lane half h: 8 h ..);
+  // products (lo, hi), (hi, lo), (hi, hi).
+  HalfFrag kf[2][4];
 #pragma unroll
-  for (int p = 0; p < 3; p++)
+  for (int p = 0; p < 2; p++)
 #pragma unroll
     for (int s = 0; s < 4; s++) kf[p][s].u = t.k[p][l32 * 8 + ((2 * s + h) ^ ks(l32))];
+  // V^T fragments for the PV products below, read with K.
+  HalfFrag vf[2][2][2];
+#pragma unroll
+  for (int p = 0; p < 2; p++)
+#pragma unroll
+    for (int d = 0; d < 2; d++)
+#pragma unroll
+      for (int s2 = 0; s2 < 2; s2++) {
+        const int dim = l32 + 32 * d;
+        vf[p][d][s2].u = t.v[p][dim * 4 + ((2 * s2 + h) ^ vs(dim))];
+      }
+  constexpr int pa[3] = {1, 0, 0}, pb[3] = {0, 1, 0};
   v16f st;
 #pragma unroll
   for (int r = 0; r < 16; r++) st[r] = 0.0f;
-  // The six part products, smallest first: (mid, mid), (lo, hi), (hi, lo),
-  // (mid, hi), (hi, mid), (hi, hi).
-  constexpr int pk[6] = {1, 2, 0, 1, 0, 0}, pq[6] = {1, 0, 2, 0, 1, 0};
 #pragma unroll
-  for (int q = 0; q < 6; q++)
+  for (int q = 0; q < 3; q++)
 #pragma unroll
-    for (int s = 0; s < 4; s++) st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[pk[q]][s].v, qb[pq[q]][s].v, st, 0, 0, 0);
-  // Register r holds key kstart + 8(r/4) + 4h + r%4.
+    for (int s = 0; s < 4; s++) st = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[pa[q]][s].v, qf[pb[q]][s].v, st, 0, 0, 0);
+  // Register r holds key kstart + 8(r/4) + 4h + r%4; the descale is exact
+  // (a power of two; with log2(e), one rounding as in exp_hw's log2(e) * s).
+#pragma unroll
+  for (int r = 0; r < 16; r++) st[r] = st[r] * c;
   if (need_mask) {
 #pragma unroll
     for (int r = 0; r < 16; r++) {
       const int key = kstart + 8 * (r / 4) + 4 * h + (r % 4);
-      const bool hidden = key >= kstart + keys ||
-                          (key > my_abs && !(my_image && key >= a.image_start && key < a.image_end));
+      const bool hidden = key >= kstart + keys || (key > my_abs && !(my_image && key >= image_start && key < image_end));
       st[r] = hidden ? -__builtin_inff() : st[r];
     }
   }
+  int shift;  // P is scaled by 2^shift for its FP16 pair
   if constexpr (STATIC) {
-    float psum = 0.0f;
+    float psum = 0.0f, pmax = 0.0f;
 #pragma unroll
     for (int r = 0; r < 16; r++) {
-      const float p = exp_hw(st[r]);  // masked keys: exp(-inf) = +0
+      const float p = __builtin_amdgcn_exp2f(st[r]);  // exp_hw of the score; masked keys: +0
       st[r] = p;
       psum = psum + p;
+      pmax = __builtin_fmaxf(pmax, p);
     }
     den = den + halves_sum(psum);
+    // The running exponent of the largest P so far; the output follows it
+    // by exact powers of two.
+    const int e = block_exp(halves_max(pmax));
+    if (__builtin_amdgcn_ballot_w64(e > pexp)) {
+      const float f = __builtin_ldexpf(1.0f, pexp - e);
+      const bool up = e > pexp;
+#pragma unroll
+      for (int d = 0; d < 2; d++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) o[d][r] = up ? o[d][r] * f : o[d][r];
+      pexp = up ? e : pexp;
+    }
+    shift = 15 - pexp;
   } else {
     float tile_max = st[0];
 #pragma unroll
@@ -517,11 +623,11 @@ __device__ __forceinline__ void split_tile_step(const AttnArgs &a, const SplitKv
     float rescale = FAST ? exp_hw(run_max - new_max) : expf_acc(run_max - new_max);
     rescale = first ? 0.0f : rescale;
     rescale = skip ? 1.0f : rescale;
-    const float shift = skip ? 0.0f : new_max;
+    const float shift_max = skip ? 0.0f : new_max;
     float psum = 0.0f;
 #pragma unroll
     for (int r = 0; r < 16; r++) {
-      const float x = st[r] - shift;
+      const float x = st[r] - shift_max;
       const float p = FAST ? exp_hw(x) : expf_acc(x);
       st[r] = p;
       psum = psum + p;
@@ -534,45 +640,40 @@ __device__ __forceinline__ void split_tile_step(const AttnArgs &a, const SplitKv
 #pragma unroll
         for (int r = 0; r < 16; r++) o[d][r] = o[d][r] * rescale;
     }
+    shift = 14;  // P <= 1
   }
   // O^T += V^T P^T: step s2 takes score registers 8 s2 .. 8 s2 + 7 (keys
   // 16 s2 + 4h + 8(e/4) + e%4) as the B operand, V^T slots 16 s2 + 8h .. of
-  // dim l32 + 32 d as the A operand.
-  SplitFrag pf[3][2];
+  // dim l32 + 32 d as the A operand; products (lo, hi), (hi, lo), (hi, hi).
+  HalfFrag pf[2][2];
 #pragma unroll
   for (int s2 = 0; s2 < 2; s2++) {
-    float pv[8];
+    uint32_t hw[4], lw[4];
 #pragma unroll
-    for (int e = 0; e < 8; e++) pv[e] = st[8 * s2 + e];
-    split8(pv, pf[0][s2].u, pf[1][s2].u, pf[2][s2].u);
+    for (int e = 0; e < 4; e++)
+      pair2_rtz(__builtin_ldexpf(st[8 * s2 + 2 * e], shift), __builtin_ldexpf(st[8 * s2 + 2 * e + 1], shift), hw[e],
+                lw[e]);
+    pf[0][s2].u = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    pf[1][s2].u = make_uint4(lw[0], lw[1], lw[2], lw[3]);
   }
-  SplitFrag vf[3][2][2];
 #pragma unroll
-  for (int p = 0; p < 3; p++)
-#pragma unroll
-    for (int d = 0; d < 2; d++)
-#pragma unroll
-      for (int s2 = 0; s2 < 2; s2++) {
-        const int dim = l32 + 32 * d;
-        vf[p][d][s2].u = t.v[p][dim * 4 + ((2 * s2 + h) ^ vs(dim))];
-      }
-#pragma unroll
-  for (int q = 0; q < 6; q++)
+  for (int q = 0; q < 3; q++)
 #pragma unroll
     for (int s2 = 0; s2 < 2; s2++)
 #pragma unroll
       for (int d = 0; d < 2; d++)
-        o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[pk[q]][d][s2].v, pf[pq[q]][s2].v, o[d], 0, 0, 0);
+        o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[pa[q]][d][s2].v, pf[pb[q]][s2].v, o[d], 0, 0, 0);
 }
 
 // Pure prefill only (every key a prefix key, queries = keys from position 0).
 template <bool STATIC, bool FAST>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void attention_split_kernel(
-    AttnArgs a, const uint4 *__restrict__ kp, const uint4 *__restrict__ vp, size_t kplane, size_t vplane,
-    int ktiles, split::Plan plan) {
-  __shared__ SplitKvTile tile0;
-  __shared__ SplitKvTile tile1;
-  __shared__ SplitKvTile tile2;
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void attention_pair_kernel(
+    AttnArgs a, const uint4 *__restrict__ kp, const uint4 *__restrict__ vp, const int *__restrict__ kexp,
+    const unsigned *__restrict__ vmax, size_t kplane, size_t vplane, int ktiles, split::Plan plan) {
+  __shared__ PairKvTile tile0;
+  __shared__ PairKvTile tile1;
+  __shared__ PairKvTile tile2;
+  __shared__ int vexp[64];
   const int head = blockIdx.y;
   const int kv_head = head / (a.n_heads / a.n_kv_heads);
   const int tid = threadIdx.x, lane = tid & 63;
@@ -599,37 +700,49 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
   const int w_visible = w_queries <= 0 ? 0 : (w_intersects ? (w_last + 1 > a.image_end ? w_last + 1 : a.image_end) : w_last + 1);
   const bool w_all_image = w_first >= a.image_start && w_last < a.image_end;
 
-  // Q^T operand, step s: dims 16 s + 8 h .. + 7 of query l32, times 1/8
-  // (exact), split into three planes.
-  SplitFrag qb[3][4];
+  // Q^T operand, step s: dims 16 s + 8 h .. + 7 of query l32, scaled by the
+  // row's exponent (both lane halves of a query agree on it).
+  HalfFrag qf[2][4];
+  int qexp;
   {
     const float *src = a.q + (static_cast<size_t>(my_valid ? my_query : 0) * a.n_heads + head) * 64 + 8 * h;
+    float qv[4][8];
+    float m = 0.0f;
 #pragma unroll
     for (int s = 0; s < 4; s++) {
       const float4 x = reinterpret_cast<const float4 *>(src + 16 * s)[0];
       const float4 y = reinterpret_cast<const float4 *>(src + 16 * s)[1];
-      const float m = my_valid ? 0.125f : 0.0f;
-      const float qv[8] = {m * x.x, m * x.y, m * x.z, m * x.w, m * y.x, m * y.y, m * y.z, m * y.w};
-      split8(qv, qb[0][s].u, qb[1][s].u, qb[2][s].u);
+      const float z = my_valid ? 1.0f : 0.0f;
+      qv[s][0] = z * x.x; qv[s][1] = z * x.y; qv[s][2] = z * x.z; qv[s][3] = z * x.w;
+      qv[s][4] = z * y.x; qv[s][5] = z * y.y; qv[s][6] = z * y.z; qv[s][7] = z * y.w;
+#pragma unroll
+      for (int e = 0; e < 8; e++) m = __builtin_fmaxf(m, finite_abs(qv[s][e]));
     }
+    qexp = block_exp(halves_max(m));
+#pragma unroll
+    for (int s = 0; s < 4; s++) pair8(qv[s], 15 - qexp, qf[0][s].u, qf[1][s].u);
   }
+  // The score factor of a key tile with exponent ke: 2^(qexp + ke - 30) / 8,
+  // times log2(e) for the static form.
+  const float cbase = STATIC ? kLog2e : 1.0f;
   v16f o[2];
 #pragma unroll
   for (int d = 0; d < 2; d++)
 #pragma unroll
     for (int r = 0; r < 16; r++) o[d][r] = 0.0f;
   float run_max = -__builtin_inff(), den = 0.0f;
+  int pexp = kMinExp;
 
   // Tile t sits in array t % 3; tiles t + 1 and t + 2 are in flight while it
   // is computed (past the last tile the copy repeats the last one).
-  auto step = [&](SplitKvTile &cur, SplitKvTile &ahead, int kstart) __attribute__((always_inline)) {
+  auto step = [&](PairKvTile &cur, PairKvTile &ahead, int kstart) __attribute__((always_inline)) {
     const int keys = visible_end - kstart < kKeys ? visible_end - kstart : kKeys;
-    __builtin_amdgcn_s_waitcnt(6 | 0x0070);  // vmcnt(6) lgkmcnt(0): this tile's six copies
+    __builtin_amdgcn_s_waitcnt(4 | 0x0070);  // vmcnt(4) lgkmcnt(0): this tile's four copies
     plain_barrier();
     if (keys > 0 && keys < kKeys) {
-      // Last tile: clear the V slots of keys past the visible ones in every
-      // plane (p = 0 there, and 0 * V must stay finite).
-      for (int idx = tid; idx < 3 * 64 * 32; idx += 256) {
+      // Last tile: clear the V slots of keys past the visible ones in both
+      // planes (p = 0 there, and 0 * V must stay finite).
+      for (int idx = tid; idx < 2 * 64 * 32; idx += 256) {
         const int p = idx >> 11, rem = idx & 2047, dim = rem >> 5, slot = rem & 31;
         const int s2 = slot >> 4, hh = (slot >> 3) & 1, e = slot & 7;
         const int key = 16 * s2 + 4 * hh + 8 * (e >> 2) + (e & 3);
@@ -640,18 +753,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
       plain_barrier();
     }
     const int far = kstart + 2 * kKeys;
-    copy_split_tile(ahead, kp, vp, kplane, vplane, ktiles, (far < visible_end ? far : visible_end - 1) / kKeys, head,
-                    kv_head, wave, tid);
+    copy_pair_tile(ahead, kp, vp, kplane, vplane, ktiles, (far < visible_end ? far : visible_end - 1) / kKeys, head,
+                   kv_head, wave, tid);
     if (keys > 0 && w_queries > 0 && kstart < w_visible) {
       const bool full = keys == kKeys && (kstart + kKeys <= w_first + 1 ||
                                           (w_all_image && kstart >= a.image_start && kstart + kKeys <= a.image_end));
-      split_tile_step<STATIC, FAST>(a, cur, qb, o, run_max, den, kstart, keys, !full, h, l32, my_abs, my_image);
+      const int ke = kexp[head * ktiles + kstart / kKeys];
+      const float c = __builtin_ldexpf(cbase, qexp + ke - 33);
+      pair_tile_step<STATIC, FAST>(cur, qf, o, run_max, den, pexp, c, kstart, keys, !full, h, l32, my_abs, my_image,
+                                   a.image_start, a.image_end);
     }
   };
-  copy_split_tile(tile0, kp, vp, kplane, vplane, ktiles, key_begin / kKeys, head, kv_head, wave, tid);
-  copy_split_tile(tile1, kp, vp, kplane, vplane, ktiles,
-                  (key_begin + kKeys < visible_end ? key_begin + kKeys : visible_end - 1) / kKeys, head, kv_head, wave,
-                  tid);
+  copy_pair_tile(tile0, kp, vp, kplane, vplane, ktiles, key_begin / kKeys, head, kv_head, wave, tid);
+  copy_pair_tile(tile1, kp, vp, kplane, vplane, ktiles,
+                 (key_begin + kKeys < visible_end ? key_begin + kKeys : visible_end - 1) / kKeys, head, kv_head, wave,
+                 tid);
   for (int kstart = key_begin; kstart < visible_end; kstart += 3 * kKeys) {
     step(tile0, tile2, kstart);
     step(tile1, tile0, kstart + kKeys);
@@ -661,20 +777,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
   const float lse = STATIC ? logf_acc(den) : run_max + logf_acc(den);
   const float sink_scale = __fdiv_rn(1.0f, 1.0f + expf_acc(a.sinks[head] - lse));
   const bool split = parts > 1;
+  const int pshift = STATIC ? 15 - pexp : 14;
+  if (tid < 64) vexp[tid] = block_exp(__uint_as_float(vmax[kv_head * 64 + tid]));
   // The copies still in flight must land before the arrays are reused.
   __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
   __syncthreads();
   // Transpose through LDS (8 KB per wave): o[d][r] is output dim
-  // 32 d + 8(r/4) + 4h + r%4 of query l32.
+  // 32 d + 8(r/4) + 4h + r%4 of query l32, times 2^(pshift + 15 - e_dim).
   float4(*stage)[16] = reinterpret_cast<float4(*)[16]>(
-      wave == 0 ? &tile0.k[0][0] : wave == 1 ? &tile0.k[2][0] : wave == 2 ? &tile1.k[0][0] : &tile1.k[2][0]);
+      wave == 0 ? &tile0.k[0][0] : wave == 1 ? &tile0.v[0][0] : wave == 2 ? &tile1.k[0][0] : &tile1.v[0][0]);
 #pragma unroll
   for (int d = 0; d < 2; d++)
 #pragma unroll
     for (int r = 0; r < 16; r++) {
       const int dim = d * 32 + 8 * (r / 4) + 4 * h + (r % 4);
+      const float ov = __builtin_ldexpf(o[d][r], vexp[dim] - 15 - pshift);
       reinterpret_cast<float *>(&stage[l32][chunk(dim >> 2, l32)])[dim & 3] =
-          split ? o[d][r] : __fmul_rn(__fdiv_rn(o[d][r], den), sink_scale);
+          split ? ov : __fmul_rn(__fdiv_rn(ov, den), sink_scale);
     }
   __syncthreads();
   if (!split) {
@@ -784,7 +903,11 @@ int launch_attention_split(Ctx *ctx, const float *q, const float *k, const float
   FOCR_REQUIRE(query_len < (size_t(1) << 30) && n_heads < 65536, FOCR_E_SHAPE, "attention shape too large");
   const size_t ktiles = (query_len + kKeys - 1) / kKeys;
   const size_t kplane = n_heads * ktiles * 256, vplane = n_kv_heads * ktiles * 256;  // uint4 per plane
-  const size_t kv_bytes = 3 * (kplane + vplane) * sizeof(uint4);
+  // Scratch: K planes, V planes, the K tiles' exponents, the V dims' maxima.
+  const size_t planes_bytes = 2 * (kplane + vplane) * sizeof(uint4);
+  const size_t kexp_bytes = (n_heads * ktiles * sizeof(int) + 255) / 256 * 256;
+  const size_t vmax_bytes = (n_kv_heads * 64 * sizeof(unsigned) + 255) / 256 * 256;
+  const size_t kv_bytes = planes_bytes + kexp_bytes + vmax_bytes;
   AttnArgs a;
   a.prefix_k = k;
   a.generated_k = nullptr;
@@ -797,18 +920,29 @@ int launch_attention_split(Ctx *ctx, const float *q, const float *k, const float
   a.image_start = static_cast<int>(image_start);
   a.image_end = static_cast<int>(image_end);
   uint4 *kp = nullptr, *vp = nullptr;
-  auto split_kv = [&]() -> int {
-    kp = static_cast<uint4 *>(ctx->scratch);
-    vp = kp + 3 * kplane;
-    hipLaunchKernelGGL(split_kv_kernel, dim3(static_cast<unsigned>(ktiles), static_cast<unsigned>(n_heads)), dim3(256),
+  int *kexp = nullptr;
+  unsigned *vmax = nullptr;
+  auto pair_kv = [&]() -> int {
+    char *base = static_cast<char *>(ctx->scratch);
+    kp = reinterpret_cast<uint4 *>(base);
+    vp = kp + 2 * kplane;
+    kexp = reinterpret_cast<int *>(base + planes_bytes);
+    vmax = reinterpret_cast<unsigned *>(base + planes_bytes + kexp_bytes);
+    const int nv = static_cast<int>(n_kv_heads * 64);
+    hipLaunchKernelGGL(pair_zero_kernel, dim3(static_cast<unsigned>((nv + 63) / 64)), dim3(64), 0, ctx->stream, vmax, nv);
+    FOCR_HIP_CHECK(hipGetLastError());
+    hipLaunchKernelGGL(pair_vmax_kernel, dim3(static_cast<unsigned>(ktiles), static_cast<unsigned>(n_kv_heads)),
+                       dim3(256), 0, ctx->stream, v, static_cast<int>(query_len), static_cast<int>(n_kv_heads), vmax);
+    FOCR_HIP_CHECK(hipGetLastError());
+    hipLaunchKernelGGL(pair_kv_kernel, dim3(static_cast<unsigned>(ktiles), static_cast<unsigned>(n_heads)), dim3(256),
                        0, ctx->stream, k, v, static_cast<int>(query_len), static_cast<int>(n_heads),
-                       static_cast<int>(n_kv_heads), static_cast<int>(ktiles), kp, vp);
+                       static_cast<int>(n_kv_heads), static_cast<int>(ktiles), vmax, kp, vp, kexp);
     FOCR_HIP_CHECK(hipGetLastError());
     return FOCR_OK;
   };
   int rc = ensure_scratch(ctx, kv_bytes);
   if (rc != FOCR_OK) return rc;
-  rc = split_kv();
+  rc = pair_kv();
   if (rc != FOCR_OK) return rc;
   // Query rows in launches of at most kMaxTiles query tiles, each with its
   // split plan (parts of whole 32-key tiles) and merge.
@@ -829,12 +963,12 @@ int launch_attention_split(Ctx *ctx, const float *q, const float *k, const float
     a.part = nullptr;
     if (slots > 0) {
       const size_t part_bytes = static_cast<size_t>(slots) * n_heads * kQueries * 66 * sizeof(float);
-      // The split K/V stay at the front of the scratch; growing it would
-      // discard them, so grow first and split again.
+      // The planes stay at the front of the scratch; growing it would
+      // discard them, so grow first and write them again.
       if (ctx->scratch_bytes < kv_bytes + part_bytes) {
         rc = ensure_scratch(ctx, kv_bytes + part_bytes);
         if (rc != FOCR_OK) return rc;
-        rc = split_kv();
+        rc = pair_kv();
         if (rc != FOCR_OK) return rc;
       }
       a.part = reinterpret_cast<float *>(static_cast<char *>(ctx->scratch) + kv_bytes);
@@ -842,14 +976,14 @@ int launch_attention_split(Ctx *ctx, const float *q, const float *k, const float
     const dim3 grid(static_cast<unsigned>(items), static_cast<unsigned>(n_heads));
     const int kt = static_cast<int>(ktiles);
     if (softmax == FOCR_SOFTMAX_STATIC)
-      hipLaunchKernelGGL((attention_split_kernel<true, true>), grid, dim3(256), 0, ctx->stream, a, kp, vp, kplane,
-                         vplane, kt, plan);
+      hipLaunchKernelGGL((attention_pair_kernel<true, true>), grid, dim3(256), 0, ctx->stream, a, kp, vp, kexp, vmax,
+                         kplane, vplane, kt, plan);
     else if (exp_mode == FOCR_EXP_FAST)
-      hipLaunchKernelGGL((attention_split_kernel<false, true>), grid, dim3(256), 0, ctx->stream, a, kp, vp, kplane,
-                         vplane, kt, plan);
+      hipLaunchKernelGGL((attention_pair_kernel<false, true>), grid, dim3(256), 0, ctx->stream, a, kp, vp, kexp, vmax,
+                         kplane, vplane, kt, plan);
     else
-      hipLaunchKernelGGL((attention_split_kernel<false, false>), grid, dim3(256), 0, ctx->stream, a, kp, vp, kplane,
-                         vplane, kt, plan);
+      hipLaunchKernelGGL((attention_pair_kernel<false, false>), grid, dim3(256), 0, ctx->stream, a, kp, vp, kexp, vmax,
+                         kplane, vplane, kt, plan);
     FOCR_HIP_CHECK(hipGetLastError());
     if (slots > 0) {
       split::Args m;

@@ -394,9 +394,10 @@ class PrefillOptions:
     """attention/mod.rs:205-221: `softmax` is the BF16 kernels' softmax
     (static shift by default, as the reference's PrefillSoftmax), and
     `fp32_softmax` the FP32 tiles' one. `split_products` (a `hip` choice,
-    no reference counterpart) forms the FP32 tiles' products from exact
-    three-way BF16 splits on a pure prefill (focr_attention_prefill_split);
-    False keeps the FP32 matrix cores everywhere."""
+    no reference counterpart) forms the FP32 tiles' products on the FP16
+    matrix cores from power-of-two scaled FP16 pairs on a pure prefill
+    (focr_attention_prefill_split); False keeps the FP32 matrix cores
+    everywhere."""
 
     exp: ExpMode = ExpMode.FAST
     fp32_softmax: Softmax = Softmax.ONLINE
@@ -411,7 +412,7 @@ def attention_with(q, kv: CompactKv, query_len: int, geometry: Geometry, sinks, 
     As the reference dispatches (attention/mod.rs:271-311): fewer than 4
     queries, or up to 8 over a cache with generated keys (decode and draft
     verification), take the decode kernel; the rest the prefill tiles (their
-    products from exact BF16 splits on a pure prefill unless
+    products from FP16 pairs on a pure prefill unless
     `options.split_products` is False)."""
     torch = _torch()
     ctx = ctx or default_context()

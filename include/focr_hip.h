@@ -204,12 +204,14 @@ int focr_attention_prefill(focr_ctx *ctx, const float *q_dev, const float *prefi
 
 /* The same attention for a pure prefill (query_offset 0, every key a prefix
  * key, query_len == prefix_len == total_len), with every QK and PV product
- * formed from exact three-way BF16 splits of its FP32 operands (x = hi + mid
- * + lo with no rounding; the six largest part products, FP32 accumulation)
- * on the BF16 matrix cores: within the FP32 tolerance of the reference tiles,
- * like focr_attention_prefill, at about twice its speed. Other geometries
- * return FOCR_E_UNSUPPORTED and write nothing (focr_attention_prefill takes
- * them). Splits K and V into the context scratch first. */
+ * formed on the FP16 matrix cores from two-term FP16 expansions of its FP32
+ * operands scaled by powers of two (x 2^e = hi + lo to about 2^-22; the
+ * three largest part products, FP32 accumulation, exact descaling; scales
+ * per query row, per 32-key tile of K, per value dim, per tile or query of
+ * P): within the FP32 tolerance of the reference tiles, like
+ * focr_attention_prefill, at about twice its speed. Other geometries return
+ * FOCR_E_UNSUPPORTED and write nothing (focr_attention_prefill takes them).
+ * Writes K and V as FP16 pairs into the context scratch first. */
 int focr_attention_prefill_split(focr_ctx *ctx, const float *q_dev, const float *prefix_k_dev,
                                  const float *generated_k_dev, const float *v_dev, size_t query_len,
                                  size_t prefix_len, size_t total_len, size_t n_heads,

@@ -1,7 +1,7 @@
 """Prefill attention on the GPU against the oracle within the FP32 tolerance
 (src/kernels/attention/prefill64/tests.rs:36-84, static_shift/tests.rs).
 
-A pure prefill takes the products from exact BF16 splits by default
+A pure prefill takes the products from power-of-two scaled FP16 pairs by default
 (focr_attention_prefill_split); `split_products=False` and every prefill over
 generated keys take the FP32 matrix-core products (focr_attention_prefill).
 Both are held to the same bound."""
@@ -221,3 +221,40 @@ def test_split_products_take_pure_prefills_only(fh):
         assert rc == fh.FOCR_E_UNSUPPORTED
     torch.cuda.synchronize()
     assert bool(torch.all(out == 7.0))
+
+
+def test_split_products_power_of_two_scaling_is_exact(fh):
+    # The FP16 pairs scale every block by a power of two: Q x 2^-40 with
+    # K x 2^40 leaves every score exact, V x 2^-60 scales every output by
+    # exactly 2^-60, so the outputs are bitwise 2^-60 times the unscaled ones
+    # (online and static, one work item and split key ranges).
+    L, image = 1400, (0, 300)
+    q = gen.normal(L * 16 * 64, 1.0, 70)
+    k = gen.normal(L * 16 * 64, 1.0, 71)
+    v = gen.normal(L * 8 * 64, 1.0, 72)
+    sinks = gen.uniform(16, -2.0, 2.0, 73)
+    for static in (False, True):
+        if static:
+            q, k = gen.normalized(L * 16 * 64, 74), gen.normalized(L * 16 * 64, 75)
+        opts = fh.PrefillOptions(fp32_softmax=fh.Softmax.STATIC if static else fh.Softmax.ONLINE)
+        base = run(fh, q, k, v, sinks, L, (0, *image), opts)
+        scaled = run(fh, np.ldexp(q, -40), np.ldexp(k, 40), np.ldexp(v, -60), sinks, L, (0, *image), opts)
+        assert np.all(np.isfinite(base))
+        assert np.array_equal(np.ldexp(scaled, 60).view(np.uint32), base.view(np.uint32)), static
+
+
+def test_split_products_wide_magnitudes(fh):
+    # Rows of Q and K scaled by 2^u, u uniform in [-30, 0], and value dims by
+    # 2^w, w uniform in [-30, 30]: every output dim within 1e-5 of the
+    # oracle relative to that dim's largest output.
+    L, image = 600, (0, 128)
+    rng = np.random.default_rng(76)
+    q = (gen.normal((L, 16, 64), 1.0, 77) * np.ldexp(1.0, rng.integers(-30, 1, (L, 16, 1)))).astype(np.float32)
+    k = (gen.normal((L, 16, 64), 1.0, 78) * np.ldexp(1.0, rng.integers(-30, 1, (L, 16, 1)))).astype(np.float32)
+    v = (gen.normal((L, 8, 64), 1.0, 79) * np.ldexp(1.0, rng.integers(-30, 31, (1, 8, 64)))).astype(np.float32)
+    sinks = gen.uniform(16, -2.0, 2.0, 80)
+    q, k, v = q.ravel(), k.ravel(), v.ravel()
+    got = run(fh, q, k, v, sinks, L, (0, *image), fh.PrefillOptions())
+    want = oracle.attention_prefill(q, k, v, L, L, L, 16, 8, 0, *image, sinks, exp_fast=True).reshape(L, 16, 64)
+    scale = np.max(np.abs(want), axis=0, keepdims=True)
+    assert np.all(np.abs(got - want) <= 1e-5 * scale), float(np.max(np.abs(got - want) / scale))

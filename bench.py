@@ -45,7 +45,7 @@ FP32_MFMA_PEAK = 157.3  # TFLOP/s dense
 # 78.6 that 16 lanes x 2.4 GHz would allow, so the vector peak bounds them.
 FP32_VECTOR_PEAK = 157.3
 INT8_MFMA_PEAK = 5000.0  # TOP/s dense
-BF16_MFMA_PEAK = 2500.0  # TFLOP/s dense
+F16_MFMA_PEAK = 2500.0  # TFLOP/s dense, FP16 and BF16
 POOL_BYTES = 600 << 20  # > 2 x 256 MB Infinity Cache
 # Device clock cycles the stream sleeps (torch.cuda._sleep: a spin on the
 # clock, no memory traffic) while the host submits the timed replay whose
@@ -220,9 +220,9 @@ def bench_gemm(torch, fh, gen, np, reps, bits=32):
             peak = FP32_VECTOR_PEAK if tag == "chain" else FP32_MFMA_PEAK
             res[f"{name}_{tag}"] = {"ms": round(avg, 4), "tflops": round(tflops, 2), "frac": round(tflops / peak, 3)}
             if tag == "split":
-                # Six BF16 part products per FP32 product: the BF16 matrix-core
-                # work done, against the 2.5 PFLOP/s dense BF16 peak.
-                res[f"{name}_{tag}"]["bf16_frac"] = round(6 * tflops / BF16_MFMA_PEAK, 3)
+                # Three FP16 pair products per FP32 product: the FP16 matrix-
+                # core work done, against the 2.5 PFLOP/s dense FP16 peak.
+                res[f"{name}_{tag}"]["f16_frac"] = round(3 * tflops / F16_MFMA_PEAK, 3)
         lin.free()
     return res
 

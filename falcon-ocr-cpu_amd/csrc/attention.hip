@@ -395,38 +395,13 @@ union HalfFrag {
   half8 v;
 };
 
-// Exponents are kept in [-100, 127] so that 2^(15 - e) and 2^(e - 15) are
-// normal floats; a block whose largest magnitude is below 2^-101 keeps that
-// scale (its values then sit below 2^14).
-constexpr int kMinExp = -100;
-
-// The exponent e of a block's largest finite magnitude m (2^(e-1) <= m <
-// 2^e), clamped below at kMinExp (also for m = 0).
-__device__ __forceinline__ int block_exp(float m) {
-  const int e = m > 0.0f ? __builtin_amdgcn_frexp_expf(m) : kMinExp;
-  return e < kMinExp ? kMinExp : e;
-}
-
-// |x| for finite x, 0 otherwise (an infinity or NaN does not set the scale).
-__device__ __forceinline__ float finite_abs(float x) {
-  const float a = __builtin_fabsf(x);
-  return a <= 3.4028234663852886e38f ? a : 0.0f;
-}
-
-// Eight FP32 values times 2^shift as FP16 (hi, lo) fragments, hi and lo
-// rounded to nearest; an infinity or NaN travels in hi alone (lo = 0).
+// Eight FP32 values times 2^shift as FP16 (hi, lo) fragments (pair1).
 __device__ __forceinline__ void pair8(const float (&x)[8], int shift, uint4 &hi, uint4 &lo) {
-  HalfFrag h, l;
+  uint16_t h[8], l[8];
 #pragma unroll
-  for (int e = 0; e < 8; e++) {
-    const float xs = __builtin_ldexpf(x[e], shift);
-    const _Float16 a = static_cast<_Float16>(xs);
-    const bool finite = __builtin_fabsf(x[e]) <= 3.4028234663852886e38f;
-    h.v[e] = a;
-    l.v[e] = finite ? static_cast<_Float16>(xs - static_cast<float>(a)) : static_cast<_Float16>(0.0f);
-  }
-  hi = h.u;
-  lo = l.u;
+  for (int e = 0; e < 8; e++) pair1(x[e], shift, h[e], l[e]);
+  hi = make_uint4(h[0] | h[1] << 16, h[2] | h[3] << 16, h[4] | h[5] << 16, h[6] | h[7] << 16);
+  lo = make_uint4(l[0] | l[1] << 16, l[2] | l[3] << 16, l[4] | l[5] << 16, l[6] | l[7] << 16);
 }
 
 // Per (KV head, dim): the largest finite |v| over every key, as float bits
@@ -486,7 +461,7 @@ __global__ __launch_bounds__(256) void pair_kv_kernel(const float *__restrict__ 
     for (int off = 32; off >= 1; off >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, off));
     if ((t & 63) == 0) wmax[t >> 6] = m;
     __syncthreads();
-    const int ex = block_exp(__builtin_fmaxf(__builtin_fmaxf(wmax[0], wmax[1]), __builtin_fmaxf(wmax[2], wmax[3])));
+    const int ex = pair_exp(__builtin_fmaxf(__builtin_fmaxf(wmax[0], wmax[1]), __builtin_fmaxf(wmax[2], wmax[3])));
     if (t == 0) kexp[head * tiles + tile] = ex;
     uint4 hi, lo;
     pair8(val, 15 - ex, hi, lo);
@@ -505,7 +480,7 @@ __global__ __launch_bounds__(256) void pair_kv_kernel(const float *__restrict__ 
       val[e] = key < total ? v[(static_cast<size_t>(key) * n_kv_heads + head) * 64 + d] : 0.0f;
     }
     uint4 hi, lo;
-    pair8(val, 15 - block_exp(__uint_as_float(vmax[head * 64 + d])), hi, lo);
+    pair8(val, 15 - pair_exp(__uint_as_float(vmax[head * 64 + d])), hi, lo);
     const size_t i = (static_cast<size_t>(head) * tiles + tile) * 256 + d * 4 + (c ^ vs(d));
     vp[i] = hi;
     vp[vplane + i] = lo;
@@ -601,7 +576,7 @@ __device__ __forceinline__ void pair_tile_step(const PairKvTile &t, const HalfFr
     den = den + halves_sum(psum);
     // The running exponent of the largest P so far; the output follows it
     // by exact powers of two.
-    const int e = block_exp(halves_max(pmax));
+    const int e = pair_exp(halves_max(pmax));
     if (__builtin_amdgcn_ballot_w64(e > pexp)) {
       const float f = __builtin_ldexpf(1.0f, pexp - e);
       const bool up = e > pexp;
@@ -718,7 +693,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
 #pragma unroll
       for (int e = 0; e < 8; e++) m = __builtin_fmaxf(m, finite_abs(qv[s][e]));
     }
-    qexp = block_exp(halves_max(m));
+    qexp = pair_exp(halves_max(m));
 #pragma unroll
     for (int s = 0; s < 4; s++) pair8(qv[s], 15 - qexp, qf[0][s].u, qf[1][s].u);
   }
@@ -731,7 +706,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
 #pragma unroll
     for (int r = 0; r < 16; r++) o[d][r] = 0.0f;
   float run_max = -__builtin_inff(), den = 0.0f;
-  int pexp = kMinExp;
+  int pexp = kPairMinExp;
 
   // Tile t sits in array t % 3; tiles t + 1 and t + 2 are in flight while it
   // is computed (past the last tile the copy repeats the last one).
@@ -778,7 +753,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
   const float sink_scale = __fdiv_rn(1.0f, 1.0f + expf_acc(a.sinks[head] - lse));
   const bool split = parts > 1;
   const int pshift = STATIC ? 15 - pexp : 14;
-  if (tid < 64) vexp[tid] = block_exp(__uint_as_float(vmax[kv_head * 64 + tid]));
+  if (tid < 64) vexp[tid] = pair_exp(__uint_as_float(vmax[kv_head * 64 + tid]));
   // The copies still in flight must land before the arrays are reused.
   __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
   __syncthreads();

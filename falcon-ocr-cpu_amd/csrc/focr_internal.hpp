@@ -141,27 +141,36 @@ __device__ __forceinline__ float sdwa_cvt(uint32_t w) {
     asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:WORD_1" : "=v"(r) : "v"(w));
   return r;
 }
-// An FP32 value as three BF16 parts, x = hi + mid + lo exactly for every
-// finite x (bit patterns in the low 16 bits of each result): hi = x with the
-// low 16 bits of its pattern cleared (truncated to BF16), mid = (x - hi)
-// truncated, lo = x - hi - mid. Both differences are exact (they clear
-// leading bits of a value of the same sign and binade) and the last has at
-// most 8 significant bits, so no part rounds; |mid| < 2^-7 |x|, |lo| <
-// 2^-14 |x|. An infinity or NaN travels in hi alone (mid = lo = 0).
-__device__ __forceinline__ void split3(float x, uint32_t &hi, uint32_t &mid, uint32_t &lo) {
-  const uint32_t b = __float_as_uint(x);
-  if ((b & 0x7f800000u) == 0x7f800000u) {  // infinity or NaN
-    hi = (b & 0x007fffffu) ? 0x7fc0u : (b >> 16);
-    mid = lo = 0;
-    return;
-  }
-  const uint32_t h = b & 0xffff0000u;
-  const float r1 = x - __uint_as_float(h);
-  const uint32_t m = __float_as_uint(r1) & 0xffff0000u;
-  const float r2 = r1 - __uint_as_float(m);
-  hi = h >> 16;
-  mid = m >> 16;
-  lo = __float_as_uint(r2) >> 16;  // r2 fits 8 significant bits: no rounding
+// FP16 pairs of power-of-two scaled FP32 values (the split-product GEMM and
+// attention). A block of values (a row, a key tile, a value dim) takes the
+// exponent e of its largest finite magnitude m (2^(e-1) <= m < 2^e), and
+// each x becomes x' = x 2^(15 - e) (exact; |x'| < 2^15) and the pair
+// hi = fp16(x'), lo = fp16(x' - hi), both rounded to nearest: x' - hi is
+// exact in FP32, so x' = hi + lo to 2^-22 |x'| (to 2^-25 absolute once lo is
+// an FP16 subnormal, for |x'| below about 2^-3). An infinity or NaN travels
+// in hi alone (lo = 0) and does not set e. Exponents are clamped below at
+// kPairMinExp, so that 2^(15 - e) and 2^(e - 15) stay normal floats.
+constexpr int kPairMinExp = -100;
+
+__device__ __forceinline__ int pair_exp(float m) {
+  const int e = m > 0.0f ? __builtin_amdgcn_frexp_expf(m) : kPairMinExp;
+  return e < kPairMinExp ? kPairMinExp : e;
+}
+
+// |x| for finite x, 0 for an infinity or NaN.
+__device__ __forceinline__ float finite_abs(float x) {
+  const float a = __builtin_fabsf(x);
+  return a <= 3.4028234663852886e38f ? a : 0.0f;
+}
+
+// x 2^shift as an FP16 pair (bit patterns).
+__device__ __forceinline__ void pair1(float x, int shift, uint16_t &hi, uint16_t &lo) {
+  const float xs = __builtin_ldexpf(x, shift);
+  const _Float16 a = static_cast<_Float16>(xs);
+  const bool finite = __builtin_fabsf(x) <= 3.4028234663852886e38f;
+  const _Float16 b = finite ? static_cast<_Float16>(xs - static_cast<float>(a)) : static_cast<_Float16>(0.0f);
+  hi = __builtin_bit_cast(uint16_t, a);
+  lo = __builtin_bit_cast(uint16_t, b);
 }
 
 // squared_relu_glu, src/kernels/mod.rs:567-572.

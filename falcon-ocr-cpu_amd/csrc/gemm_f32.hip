@@ -910,30 +910,58 @@ void launch_one(bool chain, const GemmArgs &a, hipStream_t stream) {
   }
 }
 
-// ---- FP32 products on the BF16 matrix cores (FOCR_PROJ_F32_SPLIT) ---------
-// Every FP32 operand x is split into three BF16 parts, x = hi + mid + lo:
-// hi = x with the low 16 bits of its pattern cleared (x truncated to BF16),
-// mid = (x - hi) truncated, lo = (x - hi - mid). Both differences are exact
-// (they clear leading bits of a value of the same sign and binade), and the
-// last one has at most 8 significant bits, so lo is exact too: the split is
-// exact for every finite x (an infinity or NaN travels in hi alone). A
-// product is then the six largest of the nine part products,
-// hi.hi + hi.mid + mid.hi + hi.lo + lo.hi + mid.mid, each exact in FP32 and
-// summed by v_mfma_f32_32x32x16_bf16 in FP32; the three left out are below
-// 2^-21 |x y| together (|mid| < 2^-7 |x|, |lo| < 2^-14 |x|). Six BF16
-// products per 16 k cost 192 matrix-core cycles against 512 for eight
-// v_mfma_f32_32x32x2f32.
+// ---- FP32 products on the FP16 matrix cores (FOCR_PROJ_F32_SPLIT) ---------
+// Every row of A' = fl(x * row_scale) and of W is scaled by a power of two
+// that puts its largest finite magnitude in [2^14, 2^15) and written as FP16
+// pairs, x' = hi + lo to about 2^-22 |x'| (pair1). A product is then
+// hi.hi + hi.lo + lo.hi, summed by v_mfma_f32_32x32x16_f16 in FP32 (lo.lo,
+// left out, is below 2^-21 |x' y'|), and the output takes the exact
+// power-of-two descale 2^(e_row + e_col - 30). Three FP16 products per 16 k
+// cost 96 matrix-core cycles against 512 for eight v_mfma_f32_32x32x2f32.
 constexpr int kSplitBM = 128, kSplitBN = 128, kSplitBK = 16, kSplitKAlign = 32;
 
-// Three BF16 planes of fl(src * row_scale[row]) (or of src), zero past rows
-// and cols, stage-major: plane p, 16-k stage s, row r at
-// ((p * stages + s) * rows_pad + r) * 16, so that one stage of consecutive
-// rows is one contiguous run (the GEMM's copies read whole 1 KB pieces).
-// Thread (s, r, q) splits values 16 s + 4 q .. + 3 of row r: consecutive
-// threads write consecutive 8-byte pieces.
-__global__ __launch_bounds__(256) void split_planes_kernel(const float *__restrict__ src, int rows, int cols,
-                                                           const float *__restrict__ row_scale, bool vec,
-                                                           uint16_t *__restrict__ dst, int rows_pad, int cols_pad) {
+// exps[row] = the pair exponent of fl(src[row] * row_scale[row]) (of src[row]
+// without a row scale) for rows < rows, kPairMinExp for the padding rows up to
+// rows_pad: one wave per row.
+__global__ __launch_bounds__(256) void pair_rowexp_kernel(const float *__restrict__ src, int rows, int cols,
+                                                          const float *__restrict__ row_scale, bool vec,
+                                                          int *__restrict__ exps, int rows_pad) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (row >= rows_pad) return;
+  float m = 0.0f;
+  if (row < rows) {
+    const float *r = src + static_cast<size_t>(row) * cols;
+    const float sc = row_scale ? row_scale[row] : 1.0f;
+    if (vec) {
+      for (int c = 4 * lane; c < cols; c += 256) {
+        const float4 f = *reinterpret_cast<const float4 *>(r + c);
+        if (row_scale) {
+          m = __builtin_fmaxf(m, __builtin_fmaxf(__builtin_fmaxf(finite_abs(f.x * sc), finite_abs(f.y * sc)),
+                                                 __builtin_fmaxf(finite_abs(f.z * sc), finite_abs(f.w * sc))));
+        } else {
+          m = __builtin_fmaxf(m, __builtin_fmaxf(__builtin_fmaxf(finite_abs(f.x), finite_abs(f.y)),
+                                                 __builtin_fmaxf(finite_abs(f.z), finite_abs(f.w))));
+        }
+      }
+    } else {
+      for (int c = lane; c < cols; c += 64) m = __builtin_fmaxf(m, finite_abs(row_scale ? r[c] * sc : r[c]));
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, off));
+  if (lane == 0) exps[row] = pair_exp(m);
+}
+
+// Two FP16 planes (hi, lo) of fl(src * row_scale[row]) (or of src) scaled by
+// 2^(15 - exps[row]), zero past rows and cols, stage-major: plane p, 16-k
+// stage s, row r at ((p * stages + s) * rows_pad + r) * 16, so that one stage
+// of consecutive rows is one contiguous run (the GEMM's copies read whole
+// 1 KB pieces). Thread (s, r, q) converts values 16 s + 4 q .. + 3 of row r:
+// consecutive threads write consecutive 8-byte pieces.
+__global__ __launch_bounds__(256) void pair_planes_kernel(const float *__restrict__ src, int rows, int cols,
+                                                          const float *__restrict__ row_scale, bool vec,
+                                                          const int *__restrict__ exps, uint16_t *__restrict__ dst,
+                                                          int rows_pad, int cols_pad) {
   const int stages = cols_pad / 16;
   const long i = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
   if (i >= static_cast<long>(stages) * rows_pad * 4) return;
@@ -961,26 +989,26 @@ __global__ __launch_bounds__(256) void split_planes_kernel(const float *__restri
         if (c0 + e < cols) v[e] = v[e] * sc;
     }
   }
-  uint32_t hh[4], mm[4], ll[4];
+  const int shift = 15 - exps[row];
+  uint16_t hh[4], ll[4];
 #pragma unroll
-  for (int e = 0; e < 4; e++) split3(v[e], hh[e], mm[e], ll[e]);
+  for (int e = 0; e < 4; e++) pair1(v[e], shift, hh[e], ll[e]);
   const size_t plane = static_cast<size_t>(stages) * rows_pad * 16;
   const size_t off = (static_cast<size_t>(st) * rows_pad + row) * 16 + 4 * q;
   *reinterpret_cast<uint2 *>(dst + off) = make_uint2(hh[0] | hh[1] << 16, hh[2] | hh[3] << 16);
-  *reinterpret_cast<uint2 *>(dst + plane + off) = make_uint2(mm[0] | mm[1] << 16, mm[2] | mm[3] << 16);
-  *reinterpret_cast<uint2 *>(dst + 2 * plane + off) = make_uint2(ll[0] | ll[1] << 16, ll[2] | ll[3] << 16);
+  *reinterpret_cast<uint2 *>(dst + plane + off) = make_uint2(ll[0] | ll[1] << 16, ll[2] | ll[3] << 16);
 }
 
-typedef __bf16 split_bf16x8 __attribute__((ext_vector_type(8)));
-union SplitFrag {
+typedef _Float16 pair_half8 __attribute__((ext_vector_type(8)));
+union PairFrag {
   uint4 u;
-  split_bf16x8 v;
+  pair_half8 v;
 };
 
 // 128 x 128 outputs per workgroup, 4 waves in 2 x 2, each 64 x 64 in 32 x 32
-// blocks. Stages of 16 k: per operand three planes x 128 rows x 32 bytes
+// blocks. Stages of 16 k: per operand two planes x 128 rows x 32 bytes
 // (each plane's rows of a stage contiguous in memory), copied HBM -> LDS by
-// the LDS-DMA path (16 bytes per lane, three copies of 1 KB per wave and
+// the LDS-DMA path (16 bytes per lane, two copies of 1 KB per wave and
 // operand) into a ring of three stages, two stages ahead. A row's
 // two 16-byte chunks (k 0..7, 8..15) are stored swapped when (row / 8) is
 // odd: the 16 lanes a ds_read_b128 serves (rows r..r+15, one chunk) then hit
@@ -1006,12 +1034,14 @@ __device__ __forceinline__ void split_tile(int b, int row_tiles, int col_tiles, 
 
 template <int EPI>
 __global__ __launch_bounds__(256) void split_kernel(GemmArgs a, const uint16_t *__restrict__ ap,
-                                                    const uint16_t *__restrict__ bp, size_t a_plane, size_t b_plane,
+                                                    const uint16_t *__restrict__ bp, const int *__restrict__ aexp,
+                                                    const int *__restrict__ bexp, size_t a_plane, size_t b_plane,
                                                     int kp, int row_tiles, int col_tiles) {
   // The ring's three slots, each [A, B][plane * 256 + slot u], are separate
   // arrays and every step names its slots statically: the compiler then sees
   // that a step's fragment reads never touch the slot being copied into.
-  __shared__ uint4 ring0[2][3 * 256], ring1[2][3 * 256], ring2[2][3 * 256];
+  __shared__ uint4 ring0[2][2 * 256], ring1[2][2 * 256], ring2[2][2 * 256];
+  __shared__ int tile_exp[2][kSplitBM];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   int rt, ct;
@@ -1020,9 +1050,9 @@ __global__ __launch_bounds__(256) void split_kernel(GemmArgs a, const uint16_t *
   const int h = lane >> 5, l32 = lane & 31;
   // Copy t of operand o fills slots q = 64 (wave + 4 t) + lane: plane q / 256,
   // slot u = q % 256 = row u / 2, chunk (u % 2) ^ ((row / 8) % 2).
-  const char *src[2][3];
+  const char *src[2][2];
 #pragma unroll
-  for (int t = 0; t < 3; t++) {
+  for (int t = 0; t < 2; t++) {
     const int q = 64 * (wave + 4 * t) + lane, p = q >> 8, u = q & 255, r = u >> 1;
     const int c = (u & 1) ^ ((r >> 3) & 1);
     src[0][t] = reinterpret_cast<const char *>(ap + p * a_plane + static_cast<size_t>(m0 + r) * kSplitBK + 8 * c);
@@ -1031,31 +1061,31 @@ __global__ __launch_bounds__(256) void split_kernel(GemmArgs a, const uint16_t *
   const int stages = kp / kSplitBK;  // even
   // Stage-major planes: stage s of a plane starts rows_pad * 32 bytes after s - 1.
   const size_t a_step = a_plane / stages * 2, b_step = b_plane / stages * 2;  // bytes
-  auto issue = [&](uint4 (*slot)[3 * 256], int stage) __attribute__((always_inline)) {
+  auto issue = [&](uint4 (*slot)[2 * 256], int stage) __attribute__((always_inline)) {
 #pragma unroll
     for (int o = 0; o < 2; o++) {
       const size_t off = stage * (o == 0 ? a_step : b_step);
 #pragma unroll
-      for (int t = 0; t < 3; t++)
+      for (int t = 0; t < 2; t++)
         __builtin_amdgcn_global_load_lds((global_void *)(src[o][t] + off), (lds_void *)(&slot[o][64 * (wave + 4 * t)]),
                                          16, 0, 0);
     }
   };
-  // Fragments of a stage: A blocks i and B blocks j, planes 0..2.
-  auto read = [&](const uint4 (*slot)[3 * 256], SplitFrag (*fa)[3], SplitFrag (*fb)[3]) __attribute__((always_inline)) {
+  // Fragments of a stage: A blocks i and B blocks j, planes hi, lo.
+  auto read = [&](const uint4 (*slot)[2 * 256], PairFrag (*fa)[2], PairFrag (*fb)[2]) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 2; i++) {
       const int r = wm * 64 + 32 * i + l32;
       const int u = 2 * r + (h ^ ((r >> 3) & 1));
 #pragma unroll
-      for (int p = 0; p < 3; p++) fa[i][p].u = slot[0][p * 256 + u];
+      for (int p = 0; p < 2; p++) fa[i][p].u = slot[0][p * 256 + u];
     }
 #pragma unroll
     for (int j = 0; j < 2; j++) {
       const int r = wn * 64 + 32 * j + l32;
       const int u = 2 * r + (h ^ ((r >> 3) & 1));
 #pragma unroll
-      for (int p = 0; p < 3; p++) fb[j][p].u = slot[1][p * 256 + u];
+      for (int p = 0; p < 2; p++) fb[j][p].u = slot[1][p * 256 + u];
     }
   };
   v16f acc[2][2];
@@ -1065,29 +1095,28 @@ __global__ __launch_bounds__(256) void split_kernel(GemmArgs a, const uint16_t *
     for (int j = 0; j < 2; j++)
 #pragma unroll
       for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
-  // The six part products, smallest first: (mid, mid), (lo, hi), (hi, lo),
-  // (mid, hi), (hi, mid), (hi, hi).
-  auto products = [&](SplitFrag (*fa)[3], SplitFrag (*fb)[3]) __attribute__((always_inline)) {
-    constexpr int pa[6] = {1, 2, 0, 1, 0, 0}, pb[6] = {1, 0, 2, 0, 1, 0};
+  // The three pair products, smallest first: (lo, hi), (hi, lo), (hi, hi).
+  auto products = [&](PairFrag (*fa)[2], PairFrag (*fb)[2]) __attribute__((always_inline)) {
+    constexpr int pa[3] = {1, 0, 0}, pb[3] = {0, 1, 0};
 #pragma unroll
-    for (int q = 0; q < 6; q++)
+    for (int q = 0; q < 3; q++)
 #pragma unroll
       for (int i = 0; i < 2; i++)
 #pragma unroll
         for (int j = 0; j < 2; j++)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i][pa[q]].v, fb[j][pb[q]].v, acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i][pa[q]].v, fb[j][pb[q]].v, acc[i][j], 0, 0, 0);
   };
-  SplitFrag fa0[2][3], fb0[2][3], fa1[2][3], fb1[2][3];
+  PairFrag fa0[2][2], fb0[2][2], fa1[2][2], fb1[2][2];
   issue(ring0, 0);
   issue(ring1, 1);
   // Step st (stage st in slot st % 3): wait for this wave's copies of stage
-  // st (stage st + 1's six may still fly) and its earlier LDS reads, meet the
+  // st (stage st + 1's four may still fly) and its earlier LDS reads, meet the
   // other waves (nobody still reads stage st - 1's slot), start stage st + 2
   // there (past the last stage the copy repeats it, so the counts stay the
   // same), read stage st's fragments, then run stage st - 1's products.
-  auto step = [&](int st, const uint4 (*cur)[3 * 256], uint4 (*next)[3 * 256], SplitFrag (*ra)[3],
-                  SplitFrag (*rb)[3], SplitFrag (*pa)[3], SplitFrag (*pb)[3]) __attribute__((always_inline)) {
-    __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(6));
+  auto step = [&](int st, const uint4 (*cur)[2 * 256], uint4 (*next)[2 * 256], PairFrag (*ra)[2],
+                  PairFrag (*rb)[2], PairFrag (*pa)[2], PairFrag (*pb)[2]) __attribute__((always_inline)) {
+    __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(4));
     plain_barrier();
     issue(next, st + 2 < stages ? st + 2 : stages - 1);
     read(cur, ra, rb);
@@ -1112,21 +1141,30 @@ __global__ __launch_bounds__(256) void split_kernel(GemmArgs a, const uint16_t *
     }
   }
   products(fa1, fb1);
+  // The tile's row and column exponents (the planes are padded to whole
+  // tiles, and so are the exponent arrays).
+  if (tid < kSplitBM)
+    tile_exp[0][tid] = aexp[m0 + tid];
+  else
+    tile_exp[1][tid - kSplitBM] = bexp[n0 + tid - kSplitBM];
   // The repeated copies must land before the workgroup's LDS is released.
   __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
+  __syncthreads();
   // D layout of 32x32: column = lane % 32, row = 8 (r / 4) + 4 (lane / 32) + r % 4.
 #pragma unroll
   for (int i = 0; i < 2; i++)
 #pragma unroll
-    for (int j = 0; j < 2; j++)
+    for (int j = 0; j < 2; j++) {
+      const int lc = wn * 64 + j * 32 + l32;
+      const int ce = tile_exp[1][lc] - 30;
 #pragma unroll
       for (int r = 0; r < 16; r++) {
-        const int row = m0 + wm * 64 + i * 32 + 8 * (r / 4) + 4 * h + (r % 4);
-        const int col = n0 + wn * 64 + j * 32 + l32;
-        const float v = acc[i][j][r];
+        const int lr = wm * 64 + i * 32 + 8 * (r / 4) + 4 * h + (r % 4);
+        const float v = __builtin_ldexpf(acc[i][j][r], tile_exp[0][lr] + ce);
         const float partner = EPI == FOCR_EPI_GLU ? __shfl_xor(v, 1) : 0.0f;
-        emit<EPI>(a, row, col, v, partner);
+        emit<EPI>(a, m0 + lr, n0 + lc, v, partner);
       }
+    }
 }
 
 int launch_split(Ctx *ctx, const Linear *lin, const float *x, size_t rows, const float *row_scale, int epilogue,
@@ -1139,32 +1177,37 @@ int launch_split(Ctx *ctx, const Linear *lin, const float *x, size_t rows, const
   const size_t kp = (lin->k + kSplitKAlign - 1) / kSplitKAlign * kSplitKAlign;
   FOCR_REQUIRE(kp < (size_t(1) << 30) && n_pad < (size_t(1) << 30), FOCR_E_SHAPE, "prefill shape too large");
   const size_t a_plane = m_pad * kp, b_plane = n_pad * kp;
-  int rc = ensure_scratch(ctx, 3 * (a_plane + b_plane) * sizeof(uint16_t));
+  // Scratch: A's two planes, B's two planes, the row exponents of A and B.
+  const size_t planes_bytes = 2 * (a_plane + b_plane) * sizeof(uint16_t);
+  int rc = ensure_scratch(ctx, planes_bytes + (m_pad + n_pad) * sizeof(int));
   if (rc != FOCR_OK) return rc;
-  uint16_t *ap = static_cast<uint16_t *>(ctx->scratch), *bp = ap + 3 * a_plane;
+  uint16_t *ap = static_cast<uint16_t *>(ctx->scratch), *bp = ap + 2 * a_plane;
+  int *aexp = reinterpret_cast<int *>(static_cast<char *>(ctx->scratch) + planes_bytes), *bexp = aexp + m_pad;
   const float *w = static_cast<const float *>(lin->codes);
-  auto split = [&](const float *src, size_t r, size_t c, const float *rs, uint16_t *dst, size_t r_pad) {
+  auto pairs = [&](const float *src, size_t r, size_t c, const float *rs, int *exps, uint16_t *dst, size_t r_pad) {
     const bool vec = c % 4 == 0 && reinterpret_cast<uintptr_t>(src) % 16 == 0;
+    hipLaunchKernelGGL(pair_rowexp_kernel, dim3(static_cast<unsigned>(r_pad / 4)), dim3(256), 0, ctx->stream, src,
+                       static_cast<int>(r), static_cast<int>(c), rs, vec, exps, static_cast<int>(r_pad));
     const size_t threads = r_pad * (kp / 4);  // (kp / 16) stages x r_pad rows x 4
-    hipLaunchKernelGGL(split_planes_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0,
-                       ctx->stream, src, static_cast<int>(r), static_cast<int>(c), rs, vec, dst,
+    hipLaunchKernelGGL(pair_planes_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0,
+                       ctx->stream, src, static_cast<int>(r), static_cast<int>(c), rs, vec, exps, dst,
                        static_cast<int>(r_pad), static_cast<int>(kp));
   };
-  split(x, rows, lin->k, row_scale, ap, m_pad);
-  split(w, lin->n, lin->k, nullptr, bp, n_pad);
+  pairs(x, rows, lin->k, row_scale, aexp, ap, m_pad);
+  pairs(w, lin->n, lin->k, nullptr, bexp, bp, n_pad);
   GemmArgs a = make_args(lin, x, rows, row_scale, out);
   const int rtiles = static_cast<int>(m_pad / kSplitBM), ctiles = static_cast<int>(n_pad / kSplitBN);
   const dim3 grid(static_cast<unsigned>(rtiles * ctiles));
   const int k32 = static_cast<int>(kp);
   if (epilogue == FOCR_EPI_GLU)
-    hipLaunchKernelGGL((split_kernel<FOCR_EPI_GLU>), grid, dim3(256), 0, ctx->stream, a, ap, bp, a_plane, b_plane, k32,
-                       rtiles, ctiles);
+    hipLaunchKernelGGL((split_kernel<FOCR_EPI_GLU>), grid, dim3(256), 0, ctx->stream, a, ap, bp, aexp, bexp, a_plane,
+                       b_plane, k32, rtiles, ctiles);
   else if (epilogue == FOCR_EPI_ADD)
-    hipLaunchKernelGGL((split_kernel<FOCR_EPI_ADD>), grid, dim3(256), 0, ctx->stream, a, ap, bp, a_plane, b_plane, k32,
-                       rtiles, ctiles);
+    hipLaunchKernelGGL((split_kernel<FOCR_EPI_ADD>), grid, dim3(256), 0, ctx->stream, a, ap, bp, aexp, bexp, a_plane,
+                       b_plane, k32, rtiles, ctiles);
   else
-    hipLaunchKernelGGL((split_kernel<FOCR_EPI_STORE>), grid, dim3(256), 0, ctx->stream, a, ap, bp, a_plane, b_plane,
-                       k32, rtiles, ctiles);
+    hipLaunchKernelGGL((split_kernel<FOCR_EPI_STORE>), grid, dim3(256), 0, ctx->stream, a, ap, bp, aexp, bexp,
+                       a_plane, b_plane, k32, rtiles, ctiles);
   FOCR_HIP_CHECK(hipGetLastError());
   return FOCR_OK;
 }

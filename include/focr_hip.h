@@ -54,11 +54,12 @@ extern "C" {
                                  chain per output (bitwise PanelAvx2) */
 #define FOCR_PROJ_I16 2       /* INT16 activations x INT8 codes, exact INT32 group
                                  sums (bitwise PanelI16Vnni/PanelI16Avx2) */
-#define FOCR_PROJ_F32_SPLIT 3 /* FP32 weights: every FP32 operand split exactly
-                                 into three BF16 parts, six part products per
-                                 FP32 product on the BF16 matrix cores, FP32
-                                 accumulation (tolerance-matched like
-                                 FOCR_PROJ_F32_MFMA) */
+#define FOCR_PROJ_F32_SPLIT 3 /* FP32 weights: every row of both operands
+                                 scaled by a power of two and written as FP16
+                                 pairs (hi + lo), three pair products per FP32
+                                 product on the FP16 matrix cores, FP32
+                                 accumulation, exact descale (tolerance-matched
+                                 like FOCR_PROJ_F32_MFMA) */
 
 /* Prefill softmax (src/config.rs PrefillSoftmax) and exp (ExpMode). */
 #define FOCR_SOFTMAX_ONLINE 0
@@ -173,9 +174,9 @@ int focr_linear_decode_ex(focr_ctx *ctx, const focr_linear *lin, const float *x_
  * FOCR_PROJ_I16 needs 8-bit codes, group 64, out % 32 == 0, in % 64 == 0
  * (fits_i16_panels, src/quant/linear.rs:29-31); it uses a scratch buffer the
  * context owns and grows. FOCR_PROJ_F32_SPLIT needs FP32 weights
- * (FOCR_E_UNSUPPORTED for codes) and keeps the split operands, 6 bytes per
+ * (FOCR_E_UNSUPPORTED for codes) and keeps the FP16 pairs, 4 bytes per
  * element of x and of the weights (rows and out rounded up to 128, in to 32),
- * in the same scratch buffer. */
+ * and a row exponent each, in the same scratch buffer. */
 int focr_linear_prefill(focr_ctx *ctx, const focr_linear *lin, const float *x_dev, size_t rows,
                         const float *row_scale_dev, int epilogue, int kernel, float *out_dev);
 

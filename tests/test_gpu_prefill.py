@@ -1,7 +1,7 @@
 """Prefill projections on the GPU against the oracle:
 INT16 panels bitwise (src/kernels/panels/panel_i16/tests.rs), FP32 exact-order
-panels bitwise, and FP32 matrix cores and FP32 products from exact BF16 splits
-within the FP32 tolerance (src/kernels/panels/panel.rs:243-299)."""
+panels bitwise, and FP32 matrix cores and FP32 products from power-of-two
+scaled FP16 pairs within the FP32 tolerance (src/kernels/panels/panel.rs:243-299)."""
 import numpy as np
 import pytest
 
@@ -156,9 +156,10 @@ def test_f32_mfma_within_fp32_tolerance(fh, bits, m, k, n):
 
 @pytest.mark.parametrize("m,k,n", F32_SHAPES)
 def test_f32_split_within_fp32_tolerance(fh, m, k, n):
-    # FP32 weights split exactly into three BF16 parts, six part products per
-    # FP32 product on the BF16 matrix cores: the same tolerance as the FP32
-    # matrix cores; Glu and Add are the Store output passed through them.
+    # Rows of both operands as power-of-two scaled FP16 pairs, three pair
+    # products per FP32 product on the FP16 matrix cores: the same tolerance
+    # as the FP32 matrix cores; Glu and Add are the Store output passed
+    # through them.
     a = gen.matrix(m * k, 3).reshape(m, k)
     w = gen.matrix(n * k, 4).reshape(n, k)
     lin = fh.Linear.from_f32(w)
@@ -180,8 +181,9 @@ def test_f32_split_within_fp32_tolerance(fh, m, k, n):
 
 def test_f32_split_error_is_fp32_level(fh):
     # Against the exact (f64) product: the split kernel's error is of the
-    # FP32 matrix-core kernel's order (the three part products left out are
-    # below 2^-21 |a w| together, the FP32 sums' own rounding dominates).
+    # FP32 matrix-core kernel's order (each pair holds its value to 2^-22, the
+    # lo.lo product left out is below 2^-21 |a w|, the FP32 sums' own
+    # rounding dominates).
     m, k, n = 384, 2304, 256
     a = gen.normal((m, k), 1.0, 21)
     w = gen.normal((n, k), 0.02, 22)
@@ -194,6 +196,40 @@ def test_f32_split_error_is_fp32_level(fh):
         err[kern.name] = (float(np.max(np.abs(got - exact) / mag)), float(np.sqrt(np.mean(((got - exact) / mag) ** 2))))
     assert err["F32_SPLIT"][0] <= 2 * max(err["F32_MFMA"][0], err["F32_CHAIN"][0]), err
     assert err["F32_SPLIT"][1] <= 2 * max(err["F32_MFMA"][1], err["F32_CHAIN"][1]), err
+
+
+def test_f32_split_power_of_two_row_scaling_is_exact(fh):
+    # Each row of A and of W takes its own power-of-two scale, so scaling row
+    # i of A by 2^a_i and row j of W by 2^b_j scales output (i, j) by exactly
+    # 2^(a_i + b_j): bitwise, for exponents from -40 to 40.
+    m, k, n = 200, 1024, 160
+    rng = np.random.default_rng(31)
+    a = gen.normal((m, k), 1.0, 32)
+    w = gen.normal((n, k), 0.02, 33)
+    ea = rng.integers(-40, 41, m)
+    ew = rng.integers(-40, 41, n)
+    S = fh.PrefillProjection.F32_SPLIT
+    base = run_prefill(fh, fh.Linear.from_f32(w), a, m, None, fh.Epilogue.STORE, S)
+    scaled = run_prefill(fh, fh.Linear.from_f32(np.ldexp(w, ew[:, None]).astype(np.float32)),
+                         np.ldexp(a, ea[:, None]).astype(np.float32), m, None, fh.Epilogue.STORE, S)
+    back = np.ldexp(scaled, -(ea[:, None] + ew[None, :])).astype(np.float32)
+    assert np.array_equal(back.view(np.uint32), base.view(np.uint32))
+
+
+def test_f32_split_wide_row_magnitudes(fh):
+    # Rows of A spanning 2^-40 .. 2^40 and columns within a row spanning
+    # 2^-20 .. 1 of its largest: every output within 2 k eps of the
+    # magnitude sum against the exact product.
+    m, k, n = 128, 768, 192
+    rng = np.random.default_rng(34)
+    a = (gen.normal((m, k), 1.0, 35) * np.ldexp(1.0, rng.integers(-40, 41, (m, 1)))
+         * np.ldexp(1.0, rng.integers(-20, 1, (1, k)))).astype(np.float32)
+    w = gen.normal((n, k), 0.02, 36)
+    got = run_prefill(fh, fh.Linear.from_f32(w), a, m, None, fh.Epilogue.STORE,
+                      fh.PrefillProjection.F32_SPLIT).astype(np.float64)
+    exact = a.astype(np.float64) @ w.astype(np.float64).T
+    mag = np.abs(a.astype(np.float64)) @ np.abs(w.astype(np.float64)).T
+    assert np.all(np.abs(got - exact) <= 2 * k * EPS * mag), float(np.max(np.abs(got - exact) / mag))
 
 
 def test_f32_split_nonfinite_rows_stay_nonfinite_and_codes_are_refused(fh):

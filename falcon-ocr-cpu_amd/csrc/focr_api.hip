@@ -85,7 +85,8 @@ int upload_vector(const std::vector<T> &host, T **dev, size_t *total) {
 void free_linear(Linear *lin) {
   void *ptrs[] = {lin->codes,     lin->scales,      lin->exc_cols, lin->exc_vals,
                   lin->exc_index, lin->gemv_codes,  lin->gemv_scales,
-                  lin->i16_b,     lin->i16_wsum,    lin->i16_sw};
+                  lin->i16_b,     lin->i16_wsum,    lin->i16_sw,   lin->pair_w,
+                  lin->pair_wexp};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
 }
@@ -395,6 +396,8 @@ int focr_linear_upload(focr_ctx *handle, int bits, size_t n, size_t k, size_t gr
     if ((rc = upload_vector(wsum, &lin->i16_wsum, &total)) != FOCR_OK) return fail(rc);
     if ((rc = upload_vector(sw, &lin->i16_sw, &total)) != FOCR_OK) return fail(rc);
   }
+  // FP16 pairs of FP32 weights (FOCR_PROJ_F32_SPLIT's B operand).
+  if (bits == 32 && (rc = prepare_pairs(ctx, lin, &total)) != FOCR_OK) return fail(rc);
   lin->device_bytes = total;
   *out = reinterpret_cast<focr_linear *>(lin);
   return FOCR_OK;

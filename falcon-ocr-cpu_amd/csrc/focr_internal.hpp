@@ -76,6 +76,10 @@ struct Linear {
   int8_t *i16_b = nullptr;      // [groups][n/16][64 lanes][16 B]
   int32_t *i16_wsum = nullptr;  // [groups][n]  (128 * sum of the group's codes)
   float *i16_sw = nullptr;      // [groups][n]  scales, group-major
+  // FP16-pair operand of FOCR_PROJ_F32_SPLIT (bits 32): two stage-major
+  // planes of the rows (n rounded up to 128, k to 32) and a row exponent each.
+  uint16_t *pair_w = nullptr;   // [2][k_pad / 16][n_pad][16]
+  int *pair_wexp = nullptr;     // [n_pad]
   size_t device_bytes = 0;
 };
 
@@ -91,6 +95,9 @@ int launch_prefill_f32(Ctx *ctx, const Linear *lin, const float *x, size_t rows,
                        const float *row_scale, int epilogue, float *out);
 int launch_prefill_chain(Ctx *ctx, const Linear *lin, const float *x, size_t rows,
                          const float *row_scale, int epilogue, float *out);
+// Writes the FP16-pair operand of an FP32 matrix (Linear::pair_w, pair_wexp)
+// at upload; synchronous.
+int prepare_pairs(Ctx *ctx, Linear *lin, size_t *total);
 int launch_prefill_split(Ctx *ctx, const Linear *lin, const float *x, size_t rows,
                          const float *row_scale, int epilogue, float *out);
 int launch_prefill_i16(Ctx *ctx, const Linear *lin, const float *x, size_t rows,

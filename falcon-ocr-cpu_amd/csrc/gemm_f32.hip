@@ -1167,6 +1167,19 @@ __global__ __launch_bounds__(256) void split_kernel(GemmArgs a, const uint16_t *
     }
 }
 
+// The row exponents and FP16-pair planes of src [r][c] (rows padded to
+// r_pad, columns to kp).
+void pair_operand(hipStream_t stream, const float *src, size_t r, size_t c, const float *rs, int *exps, uint16_t *dst,
+                  size_t r_pad, size_t kp) {
+  const bool vec = c % 4 == 0 && reinterpret_cast<uintptr_t>(src) % 16 == 0;
+  hipLaunchKernelGGL(pair_rowexp_kernel, dim3(static_cast<unsigned>(r_pad / 4)), dim3(256), 0, stream, src,
+                     static_cast<int>(r), static_cast<int>(c), rs, vec, exps, static_cast<int>(r_pad));
+  const size_t threads = r_pad * (kp / 4);  // (kp / 16) stages x r_pad rows x 4
+  hipLaunchKernelGGL(pair_planes_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0, stream,
+                     src, static_cast<int>(r), static_cast<int>(c), rs, vec, exps, dst, static_cast<int>(r_pad),
+                     static_cast<int>(kp));
+}
+
 int launch_split(Ctx *ctx, const Linear *lin, const float *x, size_t rows, const float *row_scale, int epilogue,
                  float *out) {
   FOCR_REQUIRE(lin->bits == 32, FOCR_E_UNSUPPORTED,
@@ -1177,24 +1190,16 @@ int launch_split(Ctx *ctx, const Linear *lin, const float *x, size_t rows, const
   const size_t kp = (lin->k + kSplitKAlign - 1) / kSplitKAlign * kSplitKAlign;
   FOCR_REQUIRE(kp < (size_t(1) << 30) && n_pad < (size_t(1) << 30), FOCR_E_SHAPE, "prefill shape too large");
   const size_t a_plane = m_pad * kp, b_plane = n_pad * kp;
-  // Scratch: A's two planes, B's two planes, the row exponents of A and B.
-  const size_t planes_bytes = 2 * (a_plane + b_plane) * sizeof(uint16_t);
-  int rc = ensure_scratch(ctx, planes_bytes + (m_pad + n_pad) * sizeof(int));
+  FOCR_REQUIRE(lin->pair_w && lin->pair_wexp, FOCR_E_UNSUPPORTED, "FOCR_PROJ_F32_SPLIT: no FP16-pair weights");
+  // Scratch: A's two planes and row exponents (W's were written at upload).
+  const size_t planes_bytes = 2 * a_plane * sizeof(uint16_t);
+  int rc = ensure_scratch(ctx, planes_bytes + m_pad * sizeof(int));
   if (rc != FOCR_OK) return rc;
-  uint16_t *ap = static_cast<uint16_t *>(ctx->scratch), *bp = ap + 2 * a_plane;
-  int *aexp = reinterpret_cast<int *>(static_cast<char *>(ctx->scratch) + planes_bytes), *bexp = aexp + m_pad;
-  const float *w = static_cast<const float *>(lin->codes);
-  auto pairs = [&](const float *src, size_t r, size_t c, const float *rs, int *exps, uint16_t *dst, size_t r_pad) {
-    const bool vec = c % 4 == 0 && reinterpret_cast<uintptr_t>(src) % 16 == 0;
-    hipLaunchKernelGGL(pair_rowexp_kernel, dim3(static_cast<unsigned>(r_pad / 4)), dim3(256), 0, ctx->stream, src,
-                       static_cast<int>(r), static_cast<int>(c), rs, vec, exps, static_cast<int>(r_pad));
-    const size_t threads = r_pad * (kp / 4);  // (kp / 16) stages x r_pad rows x 4
-    hipLaunchKernelGGL(pair_planes_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0,
-                       ctx->stream, src, static_cast<int>(r), static_cast<int>(c), rs, vec, exps, dst,
-                       static_cast<int>(r_pad), static_cast<int>(kp));
-  };
-  pairs(x, rows, lin->k, row_scale, aexp, ap, m_pad);
-  pairs(w, lin->n, lin->k, nullptr, bexp, bp, n_pad);
+  uint16_t *ap = static_cast<uint16_t *>(ctx->scratch);
+  int *aexp = reinterpret_cast<int *>(static_cast<char *>(ctx->scratch) + planes_bytes);
+  const uint16_t *bp = lin->pair_w;
+  const int *bexp = lin->pair_wexp;
+  pair_operand(ctx->stream, x, rows, lin->k, row_scale, aexp, ap, m_pad, kp);
   GemmArgs a = make_args(lin, x, rows, row_scale, out);
   const int rtiles = static_cast<int>(m_pad / kSplitBM), ctiles = static_cast<int>(n_pad / kSplitBN);
   const dim3 grid(static_cast<unsigned>(rtiles * ctiles));
@@ -1254,6 +1259,21 @@ int launch_prefill_chain(Ctx *ctx, const Linear *lin, const float *x, size_t row
 int launch_prefill_split(Ctx *ctx, const Linear *lin, const float *x, size_t rows, const float *row_scale,
                          int epilogue, float *out) {
   return launch_split(ctx, lin, x, rows, row_scale, epilogue, out);
+}
+
+int prepare_pairs(Ctx *ctx, Linear *lin, size_t *total) {
+  const size_t n_pad = (lin->n + kSplitBN - 1) / kSplitBN * kSplitBN;
+  const size_t kp = (lin->k + kSplitKAlign - 1) / kSplitKAlign * kSplitKAlign;
+  FOCR_REQUIRE(kp < (size_t(1) << 30) && n_pad < (size_t(1) << 30), FOCR_E_SHAPE, "FP16-pair weights too large");
+  const size_t planes_bytes = 2 * n_pad * kp * sizeof(uint16_t), exp_bytes = n_pad * sizeof(int);
+  FOCR_HIP_CHECK(hipMalloc(reinterpret_cast<void **>(&lin->pair_w), planes_bytes));
+  FOCR_HIP_CHECK(hipMalloc(reinterpret_cast<void **>(&lin->pair_wexp), exp_bytes));
+  *total += planes_bytes + exp_bytes;
+  pair_operand(ctx->stream, static_cast<const float *>(lin->codes), lin->n, lin->k, nullptr, lin->pair_wexp,
+               lin->pair_w, n_pad, kp);
+  FOCR_HIP_CHECK(hipGetLastError());
+  FOCR_HIP_CHECK(hipStreamSynchronize(ctx->stream));
+  return FOCR_OK;
 }
 
 }  // namespace focr

@@ -551,10 +551,11 @@ __device__ __forceinline__ void pair_tile_step(const PairKvTile &t, const HalfFr
   for (int q = 0; q < 3; q++)
 #pragma unroll
     for (int s = 0; s < 4; s++) st = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[pa[q]][s].v, qf[pb[q]][s].v, st, 0, 0, 0);
-  // Register r holds key kstart + 8(r/4) + 4h + r%4; the descale is exact
-  // (a power of two; with log2(e), one rounding as in exp_hw's log2(e) * s).
-#pragma unroll
-  for (int r = 0; r < 16; r++) st[r] = st[r] * c;
+  // Register r holds key kstart + 8(r/4) + 4h + r%4. The descale c (> 0) is
+  // exact, a power of two; with log2(e) (static form) one rounding as in
+  // exp_hw's log2(e) * s. The online form applies it inside the max and the
+  // exp argument instead: c max(st) = max(c st) and fma(st, c, -m) =
+  // fl(c st - m), both exactly as with the scores descaled first.
   if (need_mask) {
 #pragma unroll
     for (int r = 0; r < 16; r++) {
@@ -568,7 +569,7 @@ __device__ __forceinline__ void pair_tile_step(const PairKvTile &t, const HalfFr
     float psum = 0.0f, pmax = 0.0f;
 #pragma unroll
     for (int r = 0; r < 16; r++) {
-      const float p = __builtin_amdgcn_exp2f(st[r]);  // exp_hw of the score; masked keys: +0
+      const float p = __builtin_amdgcn_exp2f(st[r] * c);  // exp_hw of the score; masked keys: +0
       st[r] = p;
       psum = psum + p;
       pmax = __builtin_fmaxf(pmax, p);
@@ -591,7 +592,7 @@ __device__ __forceinline__ void pair_tile_step(const PairKvTile &t, const HalfFr
     float tile_max = st[0];
 #pragma unroll
     for (int r = 1; r < 16; r++) tile_max = __builtin_fmaxf(tile_max, st[r]);
-    tile_max = halves_max(tile_max);
+    tile_max = halves_max(tile_max) * c;
     const float new_max = __builtin_fmaxf(tile_max, run_max);
     const bool skip = new_max == -__builtin_inff();
     const bool first = run_max == -__builtin_inff();
@@ -602,7 +603,7 @@ __device__ __forceinline__ void pair_tile_step(const PairKvTile &t, const HalfFr
     float psum = 0.0f;
 #pragma unroll
     for (int r = 0; r < 16; r++) {
-      const float x = st[r] - shift_max;
+      const float x = __builtin_fmaf(st[r], c, -shift_max);
       const float p = FAST ? exp_hw(x) : expf_acc(x);
       st[r] = p;
       psum = psum + p;
@@ -734,7 +735,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
       const bool full = keys == kKeys && (kstart + kKeys <= w_first + 1 ||
                                           (w_all_image && kstart >= a.image_start && kstart + kKeys <= a.image_end));
       const int ke = kexp[head * ktiles + kstart / kKeys];
-      const float c = __builtin_ldexpf(cbase, qexp + ke - 33);
+      // Kept a normal float (> 0) when the scores are below 2^-100 anyway.
+      const float c = __builtin_fmaxf(__builtin_ldexpf(cbase, qexp + ke - 33), 1.17549435e-38f);
       pair_tile_step<STATIC, FAST>(cur, qf, o, run_max, den, pexp, c, kstart, keys, !full, h, l32, my_abs, my_image,
                                    a.image_start, a.image_end);
     }

@@ -1032,65 +1032,77 @@ __device__ __forceinline__ void split_tile(int b, int row_tiles, int col_tiles, 
   rt = panel * kSplitPanel + rem % rows;
 }
 
-template <int EPI>
+template <int EPI, int BM>
 __global__ __launch_bounds__(256) void split_kernel(GemmArgs a, const uint16_t *__restrict__ ap,
                                                     const uint16_t *__restrict__ bp, const int *__restrict__ aexp,
                                                     const int *__restrict__ bexp, size_t a_plane, size_t b_plane,
                                                     int kp, int row_tiles, int col_tiles) {
-  // The ring's three slots, each [A, B][plane * 256 + slot u], are separate
-  // arrays and every step names its slots statically: the compiler then sees
-  // that a step's fragment reads never touch the slot being copied into.
-  __shared__ uint4 ring0[2][2 * 256], ring1[2][2 * 256], ring2[2][2 * 256];
-  __shared__ int tile_exp[2][kSplitBM];
+  // BM x 128 outputs (BM = 128 or 64). An A plane of a stage holds 2 BM
+  // slots of 16 bytes (AS), a B plane 256. The ring's three slots, each
+  // [A plane * AS + slot u | B plane * 256 + slot u], are separate arrays and
+  // every step names its slots statically: the compiler then sees that a
+  // step's fragment reads never touch the slot being copied into.
+  constexpr int AS = 2 * BM, AC = BM / 64;  // A slots per plane, A copies per wave and stage
+  constexpr int IB = BM / 64;               // 32-row blocks per wave
+  constexpr int RS = 2 * AS + 2 * 256;  // slots of one ring entry
+  __shared__ uint4 ring0[RS], ring1[RS], ring2[RS];
+  __shared__ int tile_exp[2][kSplitBN];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   int rt, ct;
   split_tile(blockIdx.x, row_tiles, col_tiles, rt, ct);
-  const int m0 = a.row0 + rt * kSplitBM, n0 = ct * kSplitBN;
+  const int m0 = a.row0 + rt * BM, n0 = ct * kSplitBN;
   const int h = lane >> 5, l32 = lane & 31;
-  // Copy t of operand o fills slots q = 64 (wave + 4 t) + lane: plane q / 256,
-  // slot u = q % 256 = row u / 2, chunk (u % 2) ^ ((row / 8) % 2).
+  // Copy t of operand o fills slots q = 64 (wave + 4 t) + lane: plane q / S,
+  // slot u = q % S = row u / 2, chunk (u % 2) ^ ((row / 8) % 2) (S = AS for
+  // A, 256 for B).
   const char *src[2][2];
 #pragma unroll
   for (int t = 0; t < 2; t++) {
-    const int q = 64 * (wave + 4 * t) + lane, p = q >> 8, u = q & 255, r = u >> 1;
-    const int c = (u & 1) ^ ((r >> 3) & 1);
-    src[0][t] = reinterpret_cast<const char *>(ap + p * a_plane + static_cast<size_t>(m0 + r) * kSplitBK + 8 * c);
-    src[1][t] = reinterpret_cast<const char *>(bp + p * b_plane + static_cast<size_t>(n0 + r) * kSplitBK + 8 * c);
+    const int q = 64 * (wave + 4 * t) + lane;
+    {
+      const int pa = q / AS, ua = q % AS, ra = ua >> 1;
+      const int ca = (ua & 1) ^ ((ra >> 3) & 1);
+      src[0][t] = reinterpret_cast<const char *>(ap + (pa < 2 ? pa : 1) * a_plane +
+                                                 static_cast<size_t>(m0 + ra) * kSplitBK + 8 * ca);
+    }
+    const int pb = q >> 8, ub = q & 255, rb = ub >> 1;
+    const int cb = (ub & 1) ^ ((rb >> 3) & 1);
+    src[1][t] = reinterpret_cast<const char *>(bp + pb * b_plane + static_cast<size_t>(n0 + rb) * kSplitBK + 8 * cb);
   }
   const int stages = kp / kSplitBK;  // even
   // Stage-major planes: stage s of a plane starts rows_pad * 32 bytes after s - 1.
   const size_t a_step = a_plane / stages * 2, b_step = b_plane / stages * 2;  // bytes
-  auto issue = [&](uint4 (*slot)[2 * 256], int stage) __attribute__((always_inline)) {
+  auto issue = [&](uint4 *slot, int stage) __attribute__((always_inline)) {
 #pragma unroll
-    for (int o = 0; o < 2; o++) {
-      const size_t off = stage * (o == 0 ? a_step : b_step);
+    for (int t = 0; t < AC; t++)
+      __builtin_amdgcn_global_load_lds((global_void *)(src[0][t] + stage * a_step),
+                                       (lds_void *)(&slot[64 * (wave + 4 * t)]), 16, 0, 0);
 #pragma unroll
-      for (int t = 0; t < 2; t++)
-        __builtin_amdgcn_global_load_lds((global_void *)(src[o][t] + off), (lds_void *)(&slot[o][64 * (wave + 4 * t)]),
-                                         16, 0, 0);
-    }
+    for (int t = 0; t < 2; t++)
+      __builtin_amdgcn_global_load_lds((global_void *)(src[1][t] + stage * b_step),
+                                       (lds_void *)(&slot[2 * AS + 64 * (wave + 4 * t)]), 16, 0, 0);
   };
   // Fragments of a stage: A blocks i and B blocks j, planes hi, lo.
-  auto read = [&](const uint4 (*slot)[2 * 256], PairFrag (*fa)[2], PairFrag (*fb)[2]) __attribute__((always_inline)) {
+  auto read = [&](const uint4 *slot, PairFrag (*fa)[2], PairFrag (*fb)[2]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-      const int r = wm * 64 + 32 * i + l32;
+    for (int i = 0; i < IB; i++) {
+      const int r = wm * 32 * IB + 32 * i + l32;
       const int u = 2 * r + (h ^ ((r >> 3) & 1));
 #pragma unroll
-      for (int p = 0; p < 2; p++) fa[i][p].u = slot[0][p * 256 + u];
+      for (int p = 0; p < 2; p++) fa[i][p].u = slot[p * AS + u];
     }
 #pragma unroll
     for (int j = 0; j < 2; j++) {
       const int r = wn * 64 + 32 * j + l32;
       const int u = 2 * r + (h ^ ((r >> 3) & 1));
 #pragma unroll
-      for (int p = 0; p < 2; p++) fb[j][p].u = slot[1][p * 256 + u];
+      for (int p = 0; p < 2; p++) fb[j][p].u = slot[2 * AS + p * 256 + u];
     }
   };
-  v16f acc[2][2];
+  v16f acc[IB][2];
 #pragma unroll
-  for (int i = 0; i < 2; i++)
+  for (int i = 0; i < IB; i++)
 #pragma unroll
     for (int j = 0; j < 2; j++)
 #pragma unroll
@@ -1101,22 +1113,22 @@ __global__ __launch_bounds__(256) void split_kernel(GemmArgs a, const uint16_t *
 #pragma unroll
     for (int q = 0; q < 3; q++)
 #pragma unroll
-      for (int i = 0; i < 2; i++)
+      for (int i = 0; i < IB; i++)
 #pragma unroll
         for (int j = 0; j < 2; j++)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[i][pa[q]].v, fb[j][pb[q]].v, acc[i][j], 0, 0, 0);
   };
-  PairFrag fa0[2][2], fb0[2][2], fa1[2][2], fb1[2][2];
+  PairFrag fa0[IB][2], fb0[2][2], fa1[IB][2], fb1[2][2];
   issue(ring0, 0);
   issue(ring1, 1);
   // Step st (stage st in slot st % 3): wait for this wave's copies of stage
-  // st (stage st + 1's four may still fly) and its earlier LDS reads, meet the
+  // st (stage st + 1's may still fly) and its earlier LDS reads, meet the
   // other waves (nobody still reads stage st - 1's slot), start stage st + 2
   // there (past the last stage the copy repeats it, so the counts stay the
   // same), read stage st's fragments, then run stage st - 1's products.
-  auto step = [&](int st, const uint4 (*cur)[2 * 256], uint4 (*next)[2 * 256], PairFrag (*ra)[2],
+  auto step = [&](int st, const uint4 *cur, uint4 *next, PairFrag (*ra)[2],
                   PairFrag (*rb)[2], PairFrag (*pa)[2], PairFrag (*pb)[2]) __attribute__((always_inline)) {
-    __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(4));
+    __builtin_amdgcn_s_waitcnt(wait_vm_lgkm0(AC + 2));
     plain_barrier();
     issue(next, st + 2 < stages ? st + 2 : stages - 1);
     read(cur, ra, rb);
@@ -1142,24 +1154,24 @@ __global__ __launch_bounds__(256) void split_kernel(GemmArgs a, const uint16_t *
   }
   products(fa1, fb1);
   // The tile's row and column exponents (the planes are padded to whole
-  // tiles, and so are the exponent arrays).
-  if (tid < kSplitBM)
+  // 128-row tiles, and so are the exponent arrays).
+  if (tid < BM)
     tile_exp[0][tid] = aexp[m0 + tid];
-  else
-    tile_exp[1][tid - kSplitBM] = bexp[n0 + tid - kSplitBM];
+  else if (tid >= 128)
+    tile_exp[1][tid - 128] = bexp[n0 + tid - 128];
   // The repeated copies must land before the workgroup's LDS is released.
   __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
   __syncthreads();
   // D layout of 32x32: column = lane % 32, row = 8 (r / 4) + 4 (lane / 32) + r % 4.
 #pragma unroll
-  for (int i = 0; i < 2; i++)
+  for (int i = 0; i < IB; i++)
 #pragma unroll
     for (int j = 0; j < 2; j++) {
       const int lc = wn * 64 + j * 32 + l32;
       const int ce = tile_exp[1][lc] - 30;
 #pragma unroll
       for (int r = 0; r < 16; r++) {
-        const int lr = wm * 64 + i * 32 + 8 * (r / 4) + 4 * h + (r % 4);
+        const int lr = wm * 32 * IB + i * 32 + 8 * (r / 4) + 4 * h + (r % 4);
         const float v = __builtin_ldexpf(acc[i][j][r], tile_exp[0][lr] + ce);
         const float partner = EPI == FOCR_EPI_GLU ? __shfl_xor(v, 1) : 0.0f;
         emit<EPI>(a, m0 + lr, n0 + lc, v, partner);
@@ -1201,18 +1213,49 @@ int launch_split(Ctx *ctx, const Linear *lin, const float *x, size_t rows, const
   const int *bexp = lin->pair_wexp;
   pair_operand(ctx->stream, x, rows, lin->k, row_scale, aexp, ap, m_pad, kp);
   GemmArgs a = make_args(lin, x, rows, row_scale, out);
-  const int rtiles = static_cast<int>(m_pad / kSplitBM), ctiles = static_cast<int>(n_pad / kSplitBN);
-  const dim3 grid(static_cast<unsigned>(rtiles * ctiles));
+  const int ctiles = static_cast<int>(n_pad / kSplitBN), rt128 = static_cast<int>(m_pad / kSplitBM);
   const int k32 = static_cast<int>(kp);
-  if (epilogue == FOCR_EPI_GLU)
-    hipLaunchKernelGGL((split_kernel<FOCR_EPI_GLU>), grid, dim3(256), 0, ctx->stream, a, ap, bp, aexp, bexp, a_plane,
-                       b_plane, k32, rtiles, ctiles);
-  else if (epilogue == FOCR_EPI_ADD)
-    hipLaunchKernelGGL((split_kernel<FOCR_EPI_ADD>), grid, dim3(256), 0, ctx->stream, a, ap, bp, aexp, bexp, a_plane,
-                       b_plane, k32, rtiles, ctiles);
-  else
-    hipLaunchKernelGGL((split_kernel<FOCR_EPI_STORE>), grid, dim3(256), 0, ctx->stream, a, ap, bp, aexp, bexp,
-                       a_plane, b_plane, k32, rtiles, ctiles);
+  auto launch = [&](int bm, int row0, int rtiles) {
+    a.row0 = row0;
+    const dim3 grid(static_cast<unsigned>(rtiles * ctiles));
+    if (bm == 128) {
+      if (epilogue == FOCR_EPI_GLU)
+        hipLaunchKernelGGL((split_kernel<FOCR_EPI_GLU, 128>), grid, dim3(256), 0, ctx->stream, a, ap, bp, aexp, bexp,
+                           a_plane, b_plane, k32, rtiles, ctiles);
+      else if (epilogue == FOCR_EPI_ADD)
+        hipLaunchKernelGGL((split_kernel<FOCR_EPI_ADD, 128>), grid, dim3(256), 0, ctx->stream, a, ap, bp, aexp, bexp,
+                           a_plane, b_plane, k32, rtiles, ctiles);
+      else
+        hipLaunchKernelGGL((split_kernel<FOCR_EPI_STORE, 128>), grid, dim3(256), 0, ctx->stream, a, ap, bp, aexp,
+                           bexp, a_plane, b_plane, k32, rtiles, ctiles);
+    } else {
+      if (epilogue == FOCR_EPI_GLU)
+        hipLaunchKernelGGL((split_kernel<FOCR_EPI_GLU, 64>), grid, dim3(256), 0, ctx->stream, a, ap, bp, aexp, bexp,
+                           a_plane, b_plane, k32, rtiles, ctiles);
+      else if (epilogue == FOCR_EPI_ADD)
+        hipLaunchKernelGGL((split_kernel<FOCR_EPI_ADD, 64>), grid, dim3(256), 0, ctx->stream, a, ap, bp, aexp, bexp,
+                           a_plane, b_plane, k32, rtiles, ctiles);
+      else
+        hipLaunchKernelGGL((split_kernel<FOCR_EPI_STORE, 64>), grid, dim3(256), 0, ctx->stream, a, ap, bp, aexp,
+                           bexp, a_plane, b_plane, k32, rtiles, ctiles);
+    }
+  };
+  // 128-row tiles fill 512 workgroup slots (two per compute unit, by VGPRs).
+  // Fewer tiles than that run as 64-row tiles (twice as many, half the
+  // work each); when the 128-row tiles' last round would be at most half
+  // full, whole rounds run as 128-row tiles and the rows left as 64-row tiles.
+  constexpr int kSlots = 512;
+  const int tiles = rt128 * ctiles, full = tiles / kSlots;
+  const int whole = full * kSlots / ctiles;  // 128-row tiles in whole rounds
+  if (full == 0) {
+    launch(64, 0, static_cast<int>((rows + 63) / 64));
+  } else if (whole < rt128 && (rt128 - whole) * ctiles <= kSlots / 2) {
+    launch(128, 0, whole);
+    FOCR_HIP_CHECK(hipGetLastError());
+    launch(64, whole * kSplitBM, static_cast<int>((rows - static_cast<size_t>(whole) * kSplitBM + 63) / 64));
+  } else {
+    launch(128, 0, rt128);
+  }
   FOCR_HIP_CHECK(hipGetLastError());
   return FOCR_OK;
 }

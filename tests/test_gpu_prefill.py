@@ -198,6 +198,28 @@ def test_f32_split_error_is_fp32_level(fh):
     assert err["F32_SPLIT"][1] <= 2 * max(err["F32_MFMA"][1], err["F32_CHAIN"][1]), err
 
 
+@pytest.mark.parametrize("m", [2048, 2176])
+def test_f32_split_tile_heights(fh, m):
+    # Launch shapes of the FP16-pair kernel: 2,048 rows x 4,096 outputs fill
+    # one whole round of 128-row tiles; 2,176 rows leave a last round at most
+    # half full, which runs as 64-row tiles after the whole rounds (the small
+    # shapes above run as 64-row tiles only). Every output within the FP32
+    # bound, Store and Add.
+    k, n = 256, 4096
+    oracle.set_threads(oracle_threads())
+    a = gen.normal((m, k), 1.0, 37)
+    w = gen.normal((n, k), 0.02, 38)
+    lin = fh.Linear.from_f32(w)
+    S = fh.PrefillProjection.F32_SPLIT
+    got = run_prefill(fh, lin, a, m, None, fh.Epilogue.STORE, S)
+    want = oracle.panel_gemm_fast(a, m, k, w, n)
+    mag = np.abs(a.astype(np.float64)) @ np.abs(w.astype(np.float64)).T
+    assert np.all(np.abs(got.astype(np.float64) - want) <= 2 * k * EPS * mag + 1e-30)
+    base = gen.matrix(m * n, 39).reshape(m, n)
+    add = run_prefill(fh, lin, a, m, None, fh.Epilogue.ADD, S, base=base)
+    assert_bitwise(add, (base + got).astype(np.float32), "add of store")
+
+
 def test_f32_split_power_of_two_row_scaling_is_exact(fh):
     # Each row of A and of W takes its own power-of-two scale, so scaling row
     # i of A by 2^a_i and row j of W by 2^b_j scales output (i, j) by exactly

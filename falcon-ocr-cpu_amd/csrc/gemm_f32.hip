@@ -920,83 +920,86 @@ void launch_one(bool chain, const GemmArgs &a, hipStream_t stream) {
 // cost 96 matrix-core cycles against 512 for eight v_mfma_f32_32x32x2f32.
 constexpr int kSplitBM = 128, kSplitBN = 128, kSplitBK = 16, kSplitKAlign = 32;
 
-// exps[row] = the pair exponent of fl(src[row] * row_scale[row]) (of src[row]
-// without a row scale) for rows < rows, kPairMinExp for the padding rows up to
-// rows_pad: one wave per row.
-__global__ __launch_bounds__(256) void pair_rowexp_kernel(const float *__restrict__ src, int rows, int cols,
-                                                          const float *__restrict__ row_scale, bool vec,
-                                                          int *__restrict__ exps, int rows_pad) {
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-  if (row >= rows_pad) return;
-  float m = 0.0f;
-  if (row < rows) {
-    const float *r = src + static_cast<size_t>(row) * cols;
-    const float sc = row_scale ? row_scale[row] : 1.0f;
-    if (vec) {
-      for (int c = 4 * lane; c < cols; c += 256) {
-        const float4 f = *reinterpret_cast<const float4 *>(r + c);
-        if (row_scale) {
-          m = __builtin_fmaxf(m, __builtin_fmaxf(__builtin_fmaxf(finite_abs(f.x * sc), finite_abs(f.y * sc)),
-                                                 __builtin_fmaxf(finite_abs(f.z * sc), finite_abs(f.w * sc))));
-        } else {
-          m = __builtin_fmaxf(m, __builtin_fmaxf(__builtin_fmaxf(finite_abs(f.x), finite_abs(f.y)),
-                                                 __builtin_fmaxf(finite_abs(f.z), finite_abs(f.w))));
+// The FP16-pair operand of src [rows][cols] (rows padded to rows_pad, a
+// multiple of 4; cols to cols_pad, a multiple of 32), one workgroup per 4
+// rows:
+//  - exps[row] = the pair exponent of fl(src[row] * row_scale[row]) (of
+//    src[row] without a row scale), kPairMinExp for padding rows: a wave per
+//    row;
+//  - two FP16 planes (hi, lo) of those values scaled by 2^(15 - exps[row]),
+//    zero past rows and cols, stage-major: plane p, 16-k stage s, row r at
+//    ((p * stages + s) * rows_pad + r) * 16, so that one stage of
+//    consecutive rows is one contiguous run (the GEMM's copies read whole
+//    1 KB pieces). Thread (s % 16, r, q) converts values 16 s + 4 q .. + 3 of
+//    row r; sixteen threads write one stage of the 4 rows, 128 contiguous
+//    bytes per plane. The second pass reads the rows the first one just read.
+__global__ __launch_bounds__(256) void pair_rows_kernel(const float *__restrict__ src, int rows, int cols,
+                                                        const float *__restrict__ row_scale, bool vec,
+                                                        int *__restrict__ exps, uint16_t *__restrict__ dst,
+                                                        int rows_pad, int cols_pad) {
+  __shared__ int row_exp[4];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int r0 = blockIdx.x * 4;
+  {
+    const int row = r0 + wave;
+    float m = 0.0f;
+    if (row < rows) {
+      const float *r = src + static_cast<size_t>(row) * cols;
+      const float sc = row_scale ? row_scale[row] : 1.0f;
+      if (vec) {
+        for (int c = 4 * lane; c < cols; c += 256) {
+          const float4 f = *reinterpret_cast<const float4 *>(r + c);
+          const float v0 = row_scale ? f.x * sc : f.x, v1 = row_scale ? f.y * sc : f.y;
+          const float v2 = row_scale ? f.z * sc : f.z, v3 = row_scale ? f.w * sc : f.w;
+          m = __builtin_fmaxf(m, __builtin_fmaxf(__builtin_fmaxf(finite_abs(v0), finite_abs(v1)),
+                                                 __builtin_fmaxf(finite_abs(v2), finite_abs(v3))));
         }
+      } else {
+        for (int c = lane; c < cols; c += 64) m = __builtin_fmaxf(m, finite_abs(row_scale ? r[c] * sc : r[c]));
       }
-    } else {
-      for (int c = lane; c < cols; c += 64) m = __builtin_fmaxf(m, finite_abs(row_scale ? r[c] * sc : r[c]));
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, off));
+    if (lane == 0) {
+      const int e = pair_exp(m);
+      row_exp[wave] = e;
+      exps[row] = e;
     }
   }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, off));
-  if (lane == 0) exps[row] = pair_exp(m);
-}
-
-// Two FP16 planes (hi, lo) of fl(src * row_scale[row]) (or of src) scaled by
-// 2^(15 - exps[row]), zero past rows and cols, stage-major: plane p, 16-k
-// stage s, row r at ((p * stages + s) * rows_pad + r) * 16, so that one stage
-// of consecutive rows is one contiguous run (the GEMM's copies read whole
-// 1 KB pieces). Thread (s, r, q) converts values 16 s + 4 q .. + 3 of row r:
-// consecutive threads write consecutive 8-byte pieces.
-__global__ __launch_bounds__(256) void pair_planes_kernel(const float *__restrict__ src, int rows, int cols,
-                                                          const float *__restrict__ row_scale, bool vec,
-                                                          const int *__restrict__ exps, uint16_t *__restrict__ dst,
-                                                          int rows_pad, int cols_pad) {
+  __syncthreads();
   const int stages = cols_pad / 16;
-  const long i = static_cast<long>(blockIdx.x) * 256 + threadIdx.x;
-  if (i >= static_cast<long>(stages) * rows_pad * 4) return;
-  const int q = static_cast<int>(i & 3);
-  const long sr = i >> 2;
-  const int row = static_cast<int>(sr % rows_pad), st = static_cast<int>(sr / rows_pad);
-  const int c0 = 16 * st + 4 * q;
-  float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  if (row < rows) {
-    const float *r = src + static_cast<size_t>(row) * cols;
-    if (vec && c0 + 3 < cols) {
-      const float4 f = *reinterpret_cast<const float4 *>(r + c0);
-      v[0] = f.x;
-      v[1] = f.y;
-      v[2] = f.z;
-      v[3] = f.w;
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; e++) v[e] = c0 + e < cols ? r[c0 + e] : 0.0f;
-    }
-    if (row_scale) {
-      const float sc = row_scale[row];
-#pragma unroll
-      for (int e = 0; e < 4; e++)
-        if (c0 + e < cols) v[e] = v[e] * sc;
-    }
-  }
-  const int shift = 15 - exps[row];
-  uint16_t hh[4], ll[4];
-#pragma unroll
-  for (int e = 0; e < 4; e++) pair1(v[e], shift, hh[e], ll[e]);
   const size_t plane = static_cast<size_t>(stages) * rows_pad * 16;
-  const size_t off = (static_cast<size_t>(st) * rows_pad + row) * 16 + 4 * q;
-  *reinterpret_cast<uint2 *>(dst + off) = make_uint2(hh[0] | hh[1] << 16, hh[2] | hh[3] << 16);
-  *reinterpret_cast<uint2 *>(dst + plane + off) = make_uint2(ll[0] | ll[1] << 16, ll[2] | ll[3] << 16);
+  const int q = threadIdx.x & 3, rl = (threadIdx.x >> 2) & 3, row = r0 + rl;
+  const int shift = 15 - row_exp[rl];
+  const float *rp = src + static_cast<size_t>(row < rows ? row : 0) * cols;
+  const float sc = row_scale && row < rows ? row_scale[row] : 1.0f;
+  for (int st = threadIdx.x >> 4; st < stages; st += 16) {
+    const int c0 = 16 * st + 4 * q;
+    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (row < rows) {
+      if (vec && c0 + 3 < cols) {
+        const float4 f = *reinterpret_cast<const float4 *>(rp + c0);
+        v[0] = f.x;
+        v[1] = f.y;
+        v[2] = f.z;
+        v[3] = f.w;
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; e++) v[e] = c0 + e < cols ? rp[c0 + e] : 0.0f;
+      }
+      if (row_scale) {
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+          if (c0 + e < cols) v[e] = v[e] * sc;
+      }
+    }
+    uint16_t hh[4], ll[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) pair1(v[e], shift, hh[e], ll[e]);
+    const size_t off = (static_cast<size_t>(st) * rows_pad + row) * 16 + 4 * q;
+    *reinterpret_cast<uint2 *>(dst + off) = make_uint2(hh[0] | hh[1] << 16, hh[2] | hh[3] << 16);
+    *reinterpret_cast<uint2 *>(dst + plane + off) = make_uint2(ll[0] | ll[1] << 16, ll[2] | ll[3] << 16);
+  }
 }
 
 typedef _Float16 pair_half8 __attribute__((ext_vector_type(8)));
@@ -1180,15 +1183,12 @@ __global__ __launch_bounds__(256) void split_kernel(GemmArgs a, const uint16_t *
 }
 
 // The row exponents and FP16-pair planes of src [r][c] (rows padded to
-// r_pad, columns to kp).
+// r_pad, a multiple of 128; columns to kp).
 void pair_operand(hipStream_t stream, const float *src, size_t r, size_t c, const float *rs, int *exps, uint16_t *dst,
                   size_t r_pad, size_t kp) {
   const bool vec = c % 4 == 0 && reinterpret_cast<uintptr_t>(src) % 16 == 0;
-  hipLaunchKernelGGL(pair_rowexp_kernel, dim3(static_cast<unsigned>(r_pad / 4)), dim3(256), 0, stream, src,
-                     static_cast<int>(r), static_cast<int>(c), rs, vec, exps, static_cast<int>(r_pad));
-  const size_t threads = r_pad * (kp / 4);  // (kp / 16) stages x r_pad rows x 4
-  hipLaunchKernelGGL(pair_planes_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0, stream,
-                     src, static_cast<int>(r), static_cast<int>(c), rs, vec, exps, dst, static_cast<int>(r_pad),
+  hipLaunchKernelGGL(pair_rows_kernel, dim3(static_cast<unsigned>(r_pad / 4)), dim3(256), 0, stream, src,
+                     static_cast<int>(r), static_cast<int>(c), rs, vec, exps, dst, static_cast<int>(r_pad),
                      static_cast<int>(kp));
 }
 

@@ -930,7 +930,7 @@ int launch_attention_split(Ctx *ctx, const float *q, const float *k, const float
     split::Plan plan;
     int slots = 0;
     const int items = split::make_plan(plan, tiles, n, static_cast<int>(q0), a.image_start, a.image_end, a.n_heads,
-                                       kKeys, split::kSplitItemsF32, &slots);
+                                       kKeys, split::kSplitItemsPair, &slots);
     a.q = q + q0 * n_heads * 64;
     a.out = out + q0 * n_heads * 64;
     a.query_len = n;

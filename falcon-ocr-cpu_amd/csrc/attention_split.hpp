@@ -23,9 +23,12 @@ constexpr int kMaxTiles = 256;  // plan table size: 32,768 query rows per launch
 // Target work items per call. The FP32 kernel's items are long (about 3 per
 // workgroup slot balance the tail); the BF16 kernel's are about five times
 // shorter, so fewer, larger parts (less partial-state traffic and merge
-// work) measure faster there.
+// work) measure faster there. The FP16-pair kernel's items are about half
+// as long as the FP32 kernel's; 2,048 to 4,096 items measured within noise
+// of each other at 6,544 and 16,320 rows (1,536: 5-15 % slower).
 constexpr long long kSplitItemsF32 = 3072;
 constexpr long long kSplitItemsBf16 = 1536;
+constexpr long long kSplitItemsPair = 3072;
 constexpr long long kMinChunkKeys = 1024;
 
 // Work plan (computed on the host, passed by value): query tiles in dispatch

@@ -405,23 +405,39 @@ __device__ __forceinline__ void pair8(const float (&x)[8], int shift, uint4 &hi,
 }
 
 // Per (KV head, dim): the largest finite |v| over every key, as float bits
-// (atomic unsigned max of non-negative floats). Block (tile, kv head):
-// thread = dim d, key quarter kq.
+// (atomic unsigned max of non-negative floats). Block (KV head, 128 keys):
+// thread = dims 4 d4 .. 4 d4 + 3 (d4 = t % 16) of keys kq, kq + 16, ...
+// (kq = t / 16): eight 16-byte loads in flight, sixteen threads per 256-byte
+// row; one atomic per dim and block. (A block per 32-key tile made four
+// times the atomics per address, 510 at 16,320 keys, and took 25 us there.)
 __global__ __launch_bounds__(256) void pair_vmax_kernel(const float *__restrict__ v, int total, int n_kv_heads,
                                                         unsigned *__restrict__ vmax) {
-  __shared__ float part[4][64];
-  const int tile = blockIdx.x, head = blockIdx.y, t = threadIdx.x;
-  const int d = t & 63, kq = t >> 6;
-  float m = 0.0f;
+  __shared__ float part[16][65];
+  const int head = blockIdx.x, t = threadIdx.x;
+  const int d4 = t & 15, kq = t >> 4;
+  const int k0 = blockIdx.y * 128;
+  float4 x[8];
 #pragma unroll
-  for (int e = 0; e < 8; e++) {
-    const int key = tile * kKeys + 8 * kq + e;
-    if (key < total) m = __builtin_fmaxf(m, finite_abs(v[(static_cast<size_t>(key) * n_kv_heads + head) * 64 + d]));
+  for (int j = 0; j < 8; j++) {
+    const int key = k0 + kq + 16 * j;
+    x[j] = key < total ? *reinterpret_cast<const float4 *>(v + (static_cast<size_t>(key) * n_kv_heads + head) * 64 + 4 * d4)
+                       : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   }
-  part[kq][d] = m;
+  float m[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    m[0] = __builtin_fmaxf(m[0], finite_abs(x[j].x));
+    m[1] = __builtin_fmaxf(m[1], finite_abs(x[j].y));
+    m[2] = __builtin_fmaxf(m[2], finite_abs(x[j].z));
+    m[3] = __builtin_fmaxf(m[3], finite_abs(x[j].w));
+  }
+#pragma unroll
+  for (int e = 0; e < 4; e++) part[kq][4 * d4 + e] = m[e];
   __syncthreads();
   if (t < 64) {
-    const float r = __builtin_fmaxf(__builtin_fmaxf(part[0][t], part[1][t]), __builtin_fmaxf(part[2][t], part[3][t]));
+    float r = part[0][t];
+#pragma unroll
+    for (int i = 1; i < 16; i++) r = __builtin_fmaxf(r, part[i][t]);
     atomicMax(vmax + head * 64 + t, __float_as_uint(r));
   }
 }
@@ -908,7 +924,7 @@ int launch_attention_split(Ctx *ctx, const float *q, const float *k, const float
     const int nv = static_cast<int>(n_kv_heads * 64);
     hipLaunchKernelGGL(pair_zero_kernel, dim3(static_cast<unsigned>((nv + 63) / 64)), dim3(64), 0, ctx->stream, vmax, nv);
     FOCR_HIP_CHECK(hipGetLastError());
-    hipLaunchKernelGGL(pair_vmax_kernel, dim3(static_cast<unsigned>(ktiles), static_cast<unsigned>(n_kv_heads)),
+    hipLaunchKernelGGL(pair_vmax_kernel, dim3(static_cast<unsigned>(n_kv_heads), static_cast<unsigned>((query_len + 127) / 128)),
                        dim3(256), 0, ctx->stream, v, static_cast<int>(query_len), static_cast<int>(n_kv_heads), vmax);
     FOCR_HIP_CHECK(hipGetLastError());
     hipLaunchKernelGGL(pair_kv_kernel, dim3(static_cast<unsigned>(ktiles), static_cast<unsigned>(n_heads)), dim3(256),

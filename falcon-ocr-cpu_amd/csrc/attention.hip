@@ -533,6 +533,10 @@ __device__ __forceinline__ void pair2_rtz(float x0, float x1, uint32_t &hi, uint
   lo = __builtin_bit_cast(uint32_t, l);
 }
 
+// How far the online softmax lets a tile's scores exceed the running maximum
+// before it moves the maximum: 2^14 e^1 = 44,536 < 65,504, the FP16 range.
+constexpr float kLazyMax = 1.0f;
+
 // One 32-key tile of one wave: tile_step's softmax with FP16-pair products.
 // c = the score factor (the Q, K and 1/8 descale, times log2(e) for the
 // static form's base-2 exp); pexp = the static form's running P exponent.
@@ -609,22 +613,33 @@ __device__ __forceinline__ void pair_tile_step(const PairKvTile &t, const HalfFr
 #pragma unroll
     for (int r = 1; r < 16; r++) tile_max = __builtin_fmaxf(tile_max, st[r]);
     tile_max = halves_max(tile_max) * c;
-    const float new_max = __builtin_fmaxf(tile_max, run_max);
+    // The running maximum moves only when the tile's exceeds it by more than
+    // kLazyMax (and at the first visible key): P = e^(s - max) then stays
+    // below e^kLazyMax, 2^14 P inside the FP16 range, and most tiles leave the
+    // output unscaled. Output and denominator always share the maximum, so
+    // their ratio is the softmax's.
+    const bool raise = tile_max > run_max + kLazyMax;
+    const float new_max = raise ? tile_max : run_max;
     const bool skip = new_max == -__builtin_inff();
     const bool first = run_max == -__builtin_inff();
     float rescale = FAST ? exp_hw(run_max - new_max) : expf_acc(run_max - new_max);
     rescale = first ? 0.0f : rescale;
-    rescale = skip ? 1.0f : rescale;
+    rescale = raise ? rescale : 1.0f;
     const float shift_max = skip ? 0.0f : new_max;
-    float psum = 0.0f;
+    float ps[16];
 #pragma unroll
     for (int r = 0; r < 16; r++) {
       const float x = __builtin_fmaf(st[r], c, -shift_max);
       const float p = FAST ? exp_hw(x) : expf_acc(x);
       st[r] = p;
-      psum = psum + p;
+      ps[r] = p;
     }
-    den = den * rescale + halves_sum(psum);
+    // The tile's sum as a pairwise tree (depth 4 instead of a 16-long chain).
+#pragma unroll
+    for (int w = 1; w < 16; w *= 2)
+#pragma unroll
+      for (int r = 0; r < 16; r += 2 * w) ps[r] = ps[r] + ps[r + w];
+    den = den * rescale + halves_sum(ps[0]);
     run_max = skip ? run_max : new_max;
     if (__builtin_amdgcn_ballot_w64(rescale != 1.0f)) {
 #pragma unroll
@@ -632,7 +647,7 @@ __device__ __forceinline__ void pair_tile_step(const PairKvTile &t, const HalfFr
 #pragma unroll
         for (int r = 0; r < 16; r++) o[d][r] = o[d][r] * rescale;
     }
-    shift = 14;  // P <= 1
+    shift = 14;  // P < e^kLazyMax
   }
   // O^T += V^T P^T: step s2 takes score registers 8 s2 .. 8 s2 + 7 (keys
   // 16 s2 + 4h + 8(e/4) + e%4) as the B operand, V^T slots 16 s2 + 8h .. of

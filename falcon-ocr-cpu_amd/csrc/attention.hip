@@ -224,12 +224,12 @@ __device__ __forceinline__ void tile_step(const AttnArgs &a, const KvTile &t, Wa
   }
 }
 
+// One work item of the plan on the FP32 matrix cores, through three LDS key
+// tiles (attention_kernel's, or the pair kernel's LDS when its pre-pass found
+// a non-finite K or V value).
 template <bool STATIC, bool FAST>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void attention_kernel(AttnArgs a,
-                                                                                                split::Plan plan) {
-  __shared__ KvTile tile0;
-  __shared__ KvTile tile1;
-  __shared__ KvTile tile2;
+__device__ __forceinline__ void attention_tiles(const AttnArgs &a, const split::Plan &plan, KvTile &tile0,
+                                                KvTile &tile1, KvTile &tile2) {
   const int head = blockIdx.y;
   const int kv_head = head / (a.n_heads / a.n_kv_heads);
   const int tid = threadIdx.x, lane = tid & 63;
@@ -362,6 +362,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void a
   }
 }
 
+template <bool STATIC, bool FAST>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void attention_kernel(AttnArgs a,
+                                                                                                split::Plan plan) {
+  __shared__ KvTile tiles[3];
+  attention_tiles<STATIC, FAST>(a, plan, tiles[0], tiles[1], tiles[2]);
+}
+
 // ---- FP32 products from FP16 pairs (focr_attention_prefill_split) --------
 // The same tiles, softmax, masks, sinks and work split as attention_kernel,
 // with every product of S^T = K Q^T and O^T = V^T P^T formed on
@@ -411,7 +418,7 @@ __device__ __forceinline__ void pair8(const float (&x)[8], int shift, uint4 &hi,
 // row; one atomic per dim and block. (A block per 32-key tile made four
 // times the atomics per address, 510 at 16,320 keys, and took 25 us there.)
 __global__ __launch_bounds__(256) void pair_vmax_kernel(const float *__restrict__ v, int total, int n_kv_heads,
-                                                        unsigned *__restrict__ vmax) {
+                                                        unsigned *__restrict__ vmax, unsigned *__restrict__ nonfinite) {
   __shared__ float part[16][65];
   const int head = blockIdx.x, t = threadIdx.x;
   const int d4 = t & 15, kq = t >> 4;
@@ -424,13 +431,16 @@ __global__ __launch_bounds__(256) void pair_vmax_kernel(const float *__restrict_
                        : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   }
   float m[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  bool bad = false;
 #pragma unroll
   for (int j = 0; j < 8; j++) {
     m[0] = __builtin_fmaxf(m[0], finite_abs(x[j].x));
     m[1] = __builtin_fmaxf(m[1], finite_abs(x[j].y));
     m[2] = __builtin_fmaxf(m[2], finite_abs(x[j].z));
     m[3] = __builtin_fmaxf(m[3], finite_abs(x[j].w));
+    bad = bad || !is_finite(x[j].x) || !is_finite(x[j].y) || !is_finite(x[j].z) || !is_finite(x[j].w);
   }
+  if (bad) atomicOr(nonfinite, 1u);
 #pragma unroll
   for (int e = 0; e < 4; e++) part[kq][4 * d4 + e] = m[e];
   __syncthreads();
@@ -454,7 +464,8 @@ __global__ __launch_bounds__(64) void pair_zero_kernel(unsigned *__restrict__ p,
 __global__ __launch_bounds__(256) void pair_kv_kernel(const float *__restrict__ k, const float *__restrict__ v,
                                                       int total, int n_heads, int n_kv_heads, int tiles,
                                                       const unsigned *__restrict__ vmax, uint4 *__restrict__ kp,
-                                                      uint4 *__restrict__ vp, int *__restrict__ kexp) {
+                                                      uint4 *__restrict__ vp, int *__restrict__ kexp,
+                                                      unsigned *__restrict__ nonfinite) {
   __shared__ float wmax[4];
   const int tile = blockIdx.x, head = blockIdx.y, t = threadIdx.x;
   const size_t kplane = static_cast<size_t>(n_heads) * tiles * 256, vplane = static_cast<size_t>(n_kv_heads) * tiles * 256;
@@ -471,8 +482,13 @@ __global__ __launch_bounds__(256) void pair_kv_kernel(const float *__restrict__ 
       val[4] = y.x; val[5] = y.y; val[6] = y.z; val[7] = y.w;
     }
     float m = 0.0f;
+    bool bad = false;
 #pragma unroll
-    for (int e = 0; e < 8; e++) m = __builtin_fmaxf(m, finite_abs(val[e]));
+    for (int e = 0; e < 8; e++) {
+      m = __builtin_fmaxf(m, finite_abs(val[e]));
+      bad = bad || !is_finite(val[e]);
+    }
+    if (bad) atomicOr(nonfinite, 1u);
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, off));
     if ((t & 63) == 0) wmax[t >> 6] = m;
@@ -676,11 +692,25 @@ __device__ __forceinline__ void pair_tile_step(const PairKvTile &t, const HalfFr
 template <bool STATIC, bool FAST>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void attention_pair_kernel(
     AttnArgs a, const uint4 *__restrict__ kp, const uint4 *__restrict__ vp, const int *__restrict__ kexp,
-    const unsigned *__restrict__ vmax, size_t kplane, size_t vplane, int ktiles, split::Plan plan) {
-  __shared__ PairKvTile tile0;
-  __shared__ PairKvTile tile1;
-  __shared__ PairKvTile tile2;
+    const unsigned *__restrict__ vmax, const unsigned *__restrict__ nonfinite, size_t kplane, size_t vplane,
+    int ktiles, split::Plan plan) {
+  static_assert(sizeof(PairKvTile) == sizeof(KvTile), "the two kernels' key tiles share the LDS");
+  __shared__ union {
+    PairKvTile pair[3];
+    KvTile f32[3];
+  } lds;
   __shared__ int vexp[64];
+  if (*nonfinite != 0u) {
+    // The pre-pass found a non-finite K or V value: an infinity in an FP16
+    // pair meets zero halves (0 * inf = NaN) where FP32 products give +-inf
+    // (a -inf score is a zero probability), so the whole call takes the FP32
+    // products, with the same plan and partial-state layout.
+    attention_tiles<STATIC, FAST>(a, plan, lds.f32[0], lds.f32[1], lds.f32[2]);
+    return;
+  }
+  PairKvTile &tile0 = lds.pair[0];
+  PairKvTile &tile1 = lds.pair[1];
+  PairKvTile &tile2 = lds.pair[2];
   const int head = blockIdx.y;
   const int kv_head = head / (a.n_heads / a.n_kv_heads);
   const int tid = threadIdx.x, lane = tid & 63;
@@ -911,10 +941,11 @@ int launch_attention_split(Ctx *ctx, const float *q, const float *k, const float
   FOCR_REQUIRE(query_len < (size_t(1) << 30) && n_heads < 65536, FOCR_E_SHAPE, "attention shape too large");
   const size_t ktiles = (query_len + kKeys - 1) / kKeys;
   const size_t kplane = n_heads * ktiles * 256, vplane = n_kv_heads * ktiles * 256;  // uint4 per plane
-  // Scratch: K planes, V planes, the K tiles' exponents, the V dims' maxima.
+  // Scratch: K planes, V planes, the K tiles' exponents, the V dims' maxima
+  // and the non-finite flag after them.
   const size_t planes_bytes = 2 * (kplane + vplane) * sizeof(uint4);
   const size_t kexp_bytes = (n_heads * ktiles * sizeof(int) + 255) / 256 * 256;
-  const size_t vmax_bytes = (n_kv_heads * 64 * sizeof(unsigned) + 255) / 256 * 256;
+  const size_t vmax_bytes = ((n_kv_heads * 64 + 1) * sizeof(unsigned) + 255) / 256 * 256;
   const size_t kv_bytes = planes_bytes + kexp_bytes + vmax_bytes;
   AttnArgs a;
   a.prefix_k = k;
@@ -929,7 +960,7 @@ int launch_attention_split(Ctx *ctx, const float *q, const float *k, const float
   a.image_end = static_cast<int>(image_end);
   uint4 *kp = nullptr, *vp = nullptr;
   int *kexp = nullptr;
-  unsigned *vmax = nullptr;
+  unsigned *vmax = nullptr, *nonfinite = nullptr;
   auto pair_kv = [&]() -> int {
     char *base = static_cast<char *>(ctx->scratch);
     kp = reinterpret_cast<uint4 *>(base);
@@ -937,14 +968,17 @@ int launch_attention_split(Ctx *ctx, const float *q, const float *k, const float
     kexp = reinterpret_cast<int *>(base + planes_bytes);
     vmax = reinterpret_cast<unsigned *>(base + planes_bytes + kexp_bytes);
     const int nv = static_cast<int>(n_kv_heads * 64);
-    hipLaunchKernelGGL(pair_zero_kernel, dim3(static_cast<unsigned>((nv + 63) / 64)), dim3(64), 0, ctx->stream, vmax, nv);
+    nonfinite = vmax + nv;
+    hipLaunchKernelGGL(pair_zero_kernel, dim3(static_cast<unsigned>((nv + 64) / 64)), dim3(64), 0, ctx->stream, vmax,
+                       nv + 1);
     FOCR_HIP_CHECK(hipGetLastError());
     hipLaunchKernelGGL(pair_vmax_kernel, dim3(static_cast<unsigned>(n_kv_heads), static_cast<unsigned>((query_len + 127) / 128)),
-                       dim3(256), 0, ctx->stream, v, static_cast<int>(query_len), static_cast<int>(n_kv_heads), vmax);
+                       dim3(256), 0, ctx->stream, v, static_cast<int>(query_len), static_cast<int>(n_kv_heads), vmax,
+                       nonfinite);
     FOCR_HIP_CHECK(hipGetLastError());
     hipLaunchKernelGGL(pair_kv_kernel, dim3(static_cast<unsigned>(ktiles), static_cast<unsigned>(n_heads)), dim3(256),
                        0, ctx->stream, k, v, static_cast<int>(query_len), static_cast<int>(n_heads),
-                       static_cast<int>(n_kv_heads), static_cast<int>(ktiles), vmax, kp, vp, kexp);
+                       static_cast<int>(n_kv_heads), static_cast<int>(ktiles), vmax, kp, vp, kexp, nonfinite);
     FOCR_HIP_CHECK(hipGetLastError());
     return FOCR_OK;
   };
@@ -985,13 +1019,13 @@ int launch_attention_split(Ctx *ctx, const float *q, const float *k, const float
     const int kt = static_cast<int>(ktiles);
     if (softmax == FOCR_SOFTMAX_STATIC)
       hipLaunchKernelGGL((attention_pair_kernel<true, true>), grid, dim3(256), 0, ctx->stream, a, kp, vp, kexp, vmax,
-                         kplane, vplane, kt, plan);
+                         nonfinite, kplane, vplane, kt, plan);
     else if (exp_mode == FOCR_EXP_FAST)
       hipLaunchKernelGGL((attention_pair_kernel<false, true>), grid, dim3(256), 0, ctx->stream, a, kp, vp, kexp, vmax,
-                         kplane, vplane, kt, plan);
+                         nonfinite, kplane, vplane, kt, plan);
     else
       hipLaunchKernelGGL((attention_pair_kernel<false, false>), grid, dim3(256), 0, ctx->stream, a, kp, vp, kexp, vmax,
-                         kplane, vplane, kt, plan);
+                         nonfinite, kplane, vplane, kt, plan);
     FOCR_HIP_CHECK(hipGetLastError());
     if (slots > 0) {
       split::Args m;

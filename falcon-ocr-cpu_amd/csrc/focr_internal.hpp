@@ -164,6 +164,9 @@ __device__ __forceinline__ int pair_exp(float m) {
   return e < kPairMinExp ? kPairMinExp : e;
 }
 
+// False for an infinity or NaN.
+__device__ __forceinline__ bool is_finite(float x) { return __builtin_fabsf(x) <= 3.4028234663852886e38f; }
+
 // |x| for finite x, 0 for an infinity or NaN.
 __device__ __forceinline__ float finite_abs(float x) {
   const float a = __builtin_fabsf(x);

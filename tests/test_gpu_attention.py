@@ -258,3 +258,64 @@ def test_split_products_wide_magnitudes(fh):
     want = oracle.attention_prefill(q, k, v, L, L, L, 16, 8, 0, *image, sinks, exp_fast=True).reshape(L, 16, 64)
     scale = np.max(np.abs(want), axis=0, keepdims=True)
     assert np.all(np.abs(got - want) <= 1e-5 * scale), float(np.max(np.abs(got - want) / scale))
+
+
+@pytest.mark.parametrize("static", [False, True])
+@pytest.mark.parametrize("products", ["split", "fp32"])
+def test_nan_key_propagates_as_the_reference(fh, static, products):
+    # static_shift/tests.rs:311-367 (nan_keys_propagate_in_masked_tiles): a
+    # NaN in head 0 of key 66, text after the image [3, 65): rows 66 to 69
+    # see it and are NaN in head 0; rows 64 and 65 mask it and stay finite,
+    # as does every other head.
+    L, image = 70, (3, 65)
+    q = gen.normalized(L * 16 * 64, 91)
+    k = gen.normalized(L * 16 * 64, 92)
+    v = gen.values(L * 8 * 64, 93, 3.0)
+    sinks = gen.values(16, 94, 2.0)
+    k[66 * 16 * 64] = np.nan
+    opts = fh.PrefillOptions(fp32_softmax=fh.Softmax.STATIC if static else fh.Softmax.ONLINE,
+                             split_products=products == "split")
+    got = run(fh, q, k, v, sinks, L, (0, *image), opts)
+    poisoned = np.zeros((L, 16), bool)
+    poisoned[66:, 0] = True
+    assert np.array_equal(np.isnan(got).all(axis=2), poisoned)
+    assert np.array_equal(np.isnan(got).any(axis=2), poisoned)
+    want = oracle.attention_prefill(q, k, v, L, L, L, 16, 8, 0, *image, sinks, static=static).reshape(L, 16, 64)
+    close(got[~poisoned], want[~poisoned])
+
+
+@pytest.mark.parametrize("case", ["k_neg_inf", "k_pos_inf", "v_inf"])
+def test_split_products_nonfinite_kv_take_the_fp32_products(fh, case):
+    # An infinity in an FP16 pair meets zero halves (0 * inf = NaN) where the
+    # FP32 products give +-inf, so a call whose K or V holds a non-finite
+    # value runs the FP32 products on the device: the outputs are bitwise the
+    # FP32 entry point's (the same plan), and for K under the online softmax
+    # the finite pattern and the finite values are the oracle's (a -inf score
+    # is a zero probability; the static softmax's exp takes finite scores
+    # only, exp_lanes in static_shift.rs). The next finite call takes the
+    # pairs again.
+    L, image = 300, (0, 100)
+    q = gen.normalized(L * 16 * 64, 95)
+    k = gen.normalized(L * 16 * 64, 96)
+    v = gen.values(L * 8 * 64, 97, 3.0)
+    sinks = gen.values(16, 98, 2.0)
+    clean = run(fh, q, k, v, sinks, L, (0, *image), fh.PrefillOptions())
+    bad_k, bad_v = k.copy(), v.copy()
+    if case == "v_inf":
+        bad_v[(150 * 8 + 3) * 64 + 7] = np.inf
+    else:
+        bad_k[(150 * 16 + 6) * 64] = -np.inf if case == "k_neg_inf" else np.inf
+    for static in (False, True):
+        opts = dict(fp32_softmax=fh.Softmax.STATIC if static else fh.Softmax.ONLINE)
+        split = run(fh, q, bad_k, bad_v, sinks, L, (0, *image), fh.PrefillOptions(**opts))
+        fp32 = run(fh, q, bad_k, bad_v, sinks, L, (0, *image), fh.PrefillOptions(split_products=False, **opts))
+        assert not np.all(np.isfinite(split))
+        assert np.array_equal(split, fp32, equal_nan=True), static
+        if case != "v_inf" and not static:
+            want = oracle.attention_prefill(q, bad_k, bad_v, L, L, L, 16, 8, 0, *image, sinks).reshape(L, 16, 64)
+            assert np.array_equal(np.isfinite(split), np.isfinite(want))
+            fin = np.isfinite(want)
+            assert np.any(fin[150:, 6]) and not np.all(fin[150:, 6])
+            close(split[fin], want[fin])
+    again = run(fh, q, k, v, sinks, L, (0, *image), fh.PrefillOptions())
+    assert np.array_equal(again.view(np.uint32), clean.view(np.uint32))

@@ -702,8 +702,8 @@ def cpu_prefill_page(np, gen, gpu_gemm, gpu_attention, facts, reps=2):
     if ghz:
         macs_cycle_core = round(m * 1024 * 4096 / (cpu["literal"] * 1e-3) / (cores * ghz * 1e9), 2)
     layer = ("qkv", "wo", "w13", "w2")
-    # The GPU side runs exact mode's plan: the FP32 projections from exact
-    # BF16 splits (hip-f32-split) and the online FP32 attention.
+    # The GPU side runs exact mode's plan: the FP32 projections from FP16
+    # pairs (hip-f32-split) and the online FP32 attention on FP16 pairs.
     gpu_literal = gpu_gemm["literal_split"]["ms"] + gpu_attention["online_fast"]["ms"]
     gpu_layer = sum(gpu_gemm[f"{s}_split"]["ms"] for s in layer) + gpu_attention["online_fast"]["ms"]
     cpu_literal = cpu["literal"] + cpu["attention"]

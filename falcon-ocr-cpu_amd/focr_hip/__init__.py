@@ -219,7 +219,7 @@ class PrefillProjection(enum.IntEnum):
     F32_MFMA = 0  # FP32 matrix cores, within FP32 tolerance of the panels
     F32_CHAIN = 1  # bitwise the FP32 panels (PanelAvx2)
     I16 = 2  # bitwise the INT16 panels (PanelI16Vnni / PanelI16Avx2)
-    F32_SPLIT = 3  # FP32 weights: exact three-way BF16 splits on the BF16 matrix cores, FP32 tolerance
+    F32_SPLIT = 3  # FP32 weights: power-of-two scaled FP16 pairs on the FP16 matrix cores, FP32 tolerance
 
 
 class Linear:

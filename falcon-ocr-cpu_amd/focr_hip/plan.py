@@ -15,8 +15,8 @@ mixes CPU and GPU records silently:
 kernels: an 8-bit body whose matrices the INT16 panels hold takes the INT16
 projections (bitwise the reference's INT16 panels) unless the tuning asks for
 FP32 ones; other quantized bodies take the bitwise FP32 chain
-(PanelAvx2's order); an FP32 body takes FP32 products from exact BF16 splits
-on the BF16 matrix cores (the reference's ``gemm`` crate order is not
+(PanelAvx2's order); an FP32 body takes FP32 products from power-of-two
+scaled FP16 pairs on the FP16 matrix cores (the reference's ``gemm`` crate order is not
 reproduced bitwise by any kernel; this one is the fastest within the FP32
 tolerance; ``hip-f32-mfma``, the FP32 matrix cores, stays a valid label).
 Attention: an 8-bit body takes BF16 attention unless ``prefill_bf16`` is off

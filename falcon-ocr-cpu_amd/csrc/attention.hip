@@ -79,6 +79,7 @@ __device__ __forceinline__ float halves_max(float x) {
 }
 
 constexpr float kLog2e = 1.44269504088896340736f;
+constexpr float kLn2 = 0.69314718055994530942f;
 
 // The hardware exp2 (v_exp_f32, 1 ulp) of log2(e) * x: e^x within a few ulp
 // of the reference's Cephes exp_poly, i.e. far inside the FP32 attention
@@ -379,9 +380,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void a
 // exact power-of-two descaling keep the result at the FP32 products' error.
 // The exponents put the largest magnitude of each scale block in
 // [2^14, 2^15): Q per query row (in the kernel), K per 32-key tile of a head,
-// V per (KV head, dim) over every key, P per tile by 2^14 (online softmax:
-// P <= 1) or per query by a running power-of-two maximum (static softmax:
-// P = e^s). Per 32-key tile a wave issues 12 + 12 FP16 products (32 matrix-
+// V per (KV head, dim) over every key; P by 2^14 (online softmax: P < e, the
+// running maximum moving lazily) or per query by a running power-of-two
+// maximum (static softmax: P = e^s), the scale folded into the exp argument
+// for the hardware exp2. Per 32-key tile a wave issues 12 + 12 FP16 products (32 matrix-
 // core cycles each) in place of 32 + 32 FP32 ones (64 cycles each).
 // A pre-pass writes the call's K and V as two FP16 planes of 32-key tiles
 // (zero past the last key), in the BF16 attention's tile layouts:
@@ -588,10 +590,9 @@ __device__ __forceinline__ void pair_tile_step(const PairKvTile &t, const HalfFr
 #pragma unroll
     for (int s = 0; s < 4; s++) st = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[pa[q]][s].v, qf[pb[q]][s].v, st, 0, 0, 0);
   // Register r holds key kstart + 8(r/4) + 4h + r%4. The descale c (> 0) is
-  // exact, a power of two; with log2(e) (static form) one rounding as in
-  // exp_hw's log2(e) * s. The online form applies it inside the max and the
-  // exp argument instead: c max(st) = max(c st) and fma(st, c, -m) =
-  // fl(c st - m), both exactly as with the scores descaled first.
+  // exact, a power of two, times log2(e) for the hardware exp2 (one rounding,
+  // as exp_hw's log2(e) * s). It is applied inside the max and the exp
+  // argument: c max(st) = max(c st), and fma(st, c, k) rounds c st + k once.
   if (need_mask) {
 #pragma unroll
     for (int r = 0; r < 16; r++) {
@@ -600,20 +601,18 @@ __device__ __forceinline__ void pair_tile_step(const PairKvTile &t, const HalfFr
       st[r] = hidden ? -__builtin_inff() : st[r];
     }
   }
-  int shift;  // P is scaled by 2^shift for its FP16 pair
+  // P enters its FP16 pair scaled by a power of two: the static form and the
+  // online form with the hardware exp fold it into the exp argument (an
+  // integer added inside the argument's one rounding, their c holding
+  // log2(e)); the online form with the platform exp scales P by 2^14 after.
+  int shift = 0;
   if constexpr (STATIC) {
-    float psum = 0.0f, pmax = 0.0f;
+    // The tile's largest P (exp2 is monotonic) moves the running exponent
+    // before any P is formed; the output follows it by exact powers of two.
+    float tmax = st[0];
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-      const float p = __builtin_amdgcn_exp2f(st[r] * c);  // exp_hw of the score; masked keys: +0
-      st[r] = p;
-      psum = psum + p;
-      pmax = __builtin_fmaxf(pmax, p);
-    }
-    den = den + halves_sum(psum);
-    // The running exponent of the largest P so far; the output follows it
-    // by exact powers of two.
-    const int e = pair_exp(halves_max(pmax));
+    for (int r = 1; r < 16; r++) tmax = __builtin_fmaxf(tmax, st[r]);
+    const int e = pair_exp(__builtin_amdgcn_exp2f(halves_max(tmax) * c));  // masked keys: +0
     if (__builtin_amdgcn_ballot_w64(e > pexp)) {
       const float f = __builtin_ldexpf(1.0f, pexp - e);
       const bool up = e > pexp;
@@ -623,8 +622,24 @@ __device__ __forceinline__ void pair_tile_step(const PairKvTile &t, const HalfFr
         for (int r = 0; r < 16; r++) o[d][r] = up ? o[d][r] * f : o[d][r];
       pexp = up ? e : pexp;
     }
-    shift = 15 - pexp;
+    // P' = 2^(15 - pexp) P <= 2^15; the denominator adds the unscaled P.
+    const float fs = static_cast<float>(15 - pexp);
+    float ps[16];
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(st[r], c, fs));
+      st[r] = p;
+      ps[r] = p;
+    }
+#pragma unroll
+    for (int w = 1; w < 16; w *= 2)
+#pragma unroll
+      for (int r = 0; r < 16; r += 2 * w) ps[r] = ps[r] + ps[r + w];
+    den = den + __builtin_ldexpf(halves_sum(ps[0]), pexp - 15);
   } else {
+    // Scores, maximum and the lazy threshold in log2 units with the hardware
+    // exp (FAST), natural units with the platform exp.
+    constexpr float lazy = FAST ? kLazyMax * kLog2e : kLazyMax;
     float tile_max = st[0];
 #pragma unroll
     for (int r = 1; r < 16; r++) tile_max = __builtin_fmaxf(tile_max, st[r]);
@@ -634,19 +649,20 @@ __device__ __forceinline__ void pair_tile_step(const PairKvTile &t, const HalfFr
     // below e^kLazyMax, 2^14 P inside the FP16 range, and most tiles leave the
     // output unscaled. Output and denominator always share the maximum, so
     // their ratio is the softmax's.
-    const bool raise = tile_max > run_max + kLazyMax;
+    const bool raise = tile_max > run_max + lazy;
     const float new_max = raise ? tile_max : run_max;
     const bool skip = new_max == -__builtin_inff();
     const bool first = run_max == -__builtin_inff();
-    float rescale = FAST ? exp_hw(run_max - new_max) : expf_acc(run_max - new_max);
+    float rescale = FAST ? __builtin_amdgcn_exp2f(run_max - new_max) : expf_acc(run_max - new_max);
     rescale = first ? 0.0f : rescale;
     rescale = raise ? rescale : 1.0f;
     const float shift_max = skip ? 0.0f : new_max;
+    const float off = FAST ? 14.0f - shift_max : -shift_max;  // FAST: P' = 2^14 P < 2^14 e
     float ps[16];
 #pragma unroll
     for (int r = 0; r < 16; r++) {
-      const float x = __builtin_fmaf(st[r], c, -shift_max);
-      const float p = FAST ? exp_hw(x) : expf_acc(x);
+      const float x = __builtin_fmaf(st[r], c, off);
+      const float p = FAST ? __builtin_amdgcn_exp2f(x) : expf_acc(x);
       st[r] = p;
       ps[r] = p;
     }
@@ -655,7 +671,8 @@ __device__ __forceinline__ void pair_tile_step(const PairKvTile &t, const HalfFr
     for (int w = 1; w < 16; w *= 2)
 #pragma unroll
       for (int r = 0; r < 16; r += 2 * w) ps[r] = ps[r] + ps[r + w];
-    den = den * rescale + halves_sum(ps[0]);
+    const float tsum = halves_sum(ps[0]);
+    den = den * rescale + (FAST ? __builtin_ldexpf(tsum, -14) : tsum);
     run_max = skip ? run_max : new_max;
     if (__builtin_amdgcn_ballot_w64(rescale != 1.0f)) {
 #pragma unroll
@@ -663,7 +680,7 @@ __device__ __forceinline__ void pair_tile_step(const PairKvTile &t, const HalfFr
 #pragma unroll
         for (int r = 0; r < 16; r++) o[d][r] = o[d][r] * rescale;
     }
-    shift = 14;  // P < e^kLazyMax
+    if constexpr (!FAST) shift = 14;  // P < e^kLazyMax
   }
   // O^T += V^T P^T: step s2 takes score registers 8 s2 .. 8 s2 + 7 (keys
   // 16 s2 + 4h + 8(e/4) + e%4) as the B operand, V^T slots 16 s2 + 8h .. of
@@ -674,8 +691,8 @@ __device__ __forceinline__ void pair_tile_step(const PairKvTile &t, const HalfFr
     uint32_t hw[4], lw[4];
 #pragma unroll
     for (int e = 0; e < 4; e++)
-      pair2_rtz(__builtin_ldexpf(st[8 * s2 + 2 * e], shift), __builtin_ldexpf(st[8 * s2 + 2 * e + 1], shift), hw[e],
-                lw[e]);
+      pair2_rtz(shift ? __builtin_ldexpf(st[8 * s2 + 2 * e], shift) : st[8 * s2 + 2 * e],
+                shift ? __builtin_ldexpf(st[8 * s2 + 2 * e + 1], shift) : st[8 * s2 + 2 * e + 1], hw[e], lw[e]);
     pf[0][s2].u = make_uint4(hw[0], hw[1], hw[2], hw[3]);
     pf[1][s2].u = make_uint4(lw[0], lw[1], lw[2], lw[3]);
   }
@@ -761,7 +778,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
   }
   // The score factor of a key tile with exponent ke: 2^(qexp + ke - 30) / 8,
   // times log2(e) for the static form.
-  const float cbase = STATIC ? kLog2e : 1.0f;
+  const float cbase = STATIC || FAST ? kLog2e : 1.0f;  // log2 units for the hardware exp2
   v16f o[2];
 #pragma unroll
   for (int d = 0; d < 2; d++)
@@ -812,7 +829,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
     step(tile2, tile1, kstart + 2 * kKeys);
   }
 
-  const float lse = STATIC ? logf_acc(den) : run_max + logf_acc(den);
+  // The running maximum in natural units (FAST keeps it in log2 units).
+  const float nat_max = FAST ? run_max * kLn2 : run_max;
+  const float lse = STATIC ? logf_acc(den) : nat_max + logf_acc(den);
   const float sink_scale = __fdiv_rn(1.0f, 1.0f + expf_acc(a.sinks[head] - lse));
   const bool split = parts > 1;
   const int pshift = STATIC ? 15 - pexp : 14;
@@ -852,7 +871,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
   }
   if (h == 0) {
     float *pmd = a.part + static_cast<size_t>(a.slots) * a.n_heads * kQueries * 64 + slot * kQueries * 2;
-    reinterpret_cast<float2 *>(pmd)[wave * 32 + l32] = make_float2(STATIC ? 0.0f : run_max, den);
+    reinterpret_cast<float2 *>(pmd)[wave * 32 + l32] = make_float2(STATIC ? 0.0f : nat_max, den);
   }
 }
 

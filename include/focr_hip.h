@@ -210,9 +210,11 @@ int focr_attention_prefill(focr_ctx *ctx, const float *q_dev, const float *prefi
  * three largest part products, FP32 accumulation, exact descaling; scales
  * per query row, per 32-key tile of K, per value dim, per tile or query of
  * P): within the FP32 tolerance of the reference tiles, like
- * focr_attention_prefill, at about twice its speed. Other geometries return
- * FOCR_E_UNSUPPORTED and write nothing (focr_attention_prefill takes them).
- * Writes K and V as FP16 pairs into the context scratch first. */
+ * focr_attention_prefill, at about twice its speed. A call whose K or V
+ * holds an infinity or NaN runs focr_attention_prefill's FP32 products on the
+ * device instead (its outputs bitwise that entry point's). Other geometries
+ * return FOCR_E_UNSUPPORTED and write nothing (focr_attention_prefill takes
+ * them). Writes K and V as FP16 pairs into the context scratch first. */
 int focr_attention_prefill_split(focr_ctx *ctx, const float *q_dev, const float *prefix_k_dev,
                                  const float *generated_k_dev, const float *v_dev, size_t query_len,
                                  size_t prefix_len, size_t total_len, size_t n_heads,

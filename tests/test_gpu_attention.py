@@ -319,3 +319,20 @@ def test_split_products_nonfinite_kv_take_the_fp32_products(fh, case):
             close(split[fin], want[fin])
     again = run(fh, q, k, v, sinks, L, (0, *image), fh.PrefillOptions())
     assert np.array_equal(again.view(np.uint32), clean.view(np.uint32))
+
+
+@pytest.mark.parametrize("n_heads,n_kv", [(16, 16), (16, 4), (4, 1)])
+@pytest.mark.parametrize("L,image", [(4, (0, 4)), (33, (1, 20)), (700, (0, 300))])
+@pytest.mark.parametrize("products", ["split", "fp32"])
+def test_gqa_groupings(fh, n_heads, n_kv, L, image, products):
+    # Head groupings other than the checkpoint's 16 / 8 (prefill64 takes any
+    # n_heads divisible by n_kv_heads), the smallest prefill the tiles take
+    # (4 rows) and a split plan; online, Fast exp.
+    q = gen.att_values(L * n_heads * 64, 111 + L, 3.0)
+    k = gen.att_values(L * n_heads * 64, 113 + L, 3.0)
+    v = gen.att_values(L * n_kv * 64, 117 + L, 3.0)
+    sinks = gen.att_values(n_heads, 119, 2.0)
+    opts = fh.PrefillOptions(split_products=products == "split")
+    got = run(fh, q, k, v, sinks, L, (0, *image), opts, n_heads=n_heads, n_kv=n_kv)
+    want = oracle.attention_prefill(q, k, v, L, L, L, n_heads, n_kv, 0, *image, sinks, exp_fast=True)
+    close(got, want.reshape(L, n_heads, 64))

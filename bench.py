@@ -381,6 +381,7 @@ def bench_layer(torch, fh, gen, np, steps=64):
                 "prefill_tflops": round((proj_flop + attn_flop) / (prefill_ms * 1e-3) / 1e12, 2),
                 "decode_us_per_step": round(decode_ms * 1e3 / steps, 2), "decode_bytes_per_step": int(step_bytes),
                 "decode_gbs": round(step_bytes / (decode_ms * 1e-3 / steps) / 1e9, 1),
+                "decode_frac_hbm": round(step_bytes / (decode_ms * 1e-3 / steps) / 1e9 / HBM_PEAK_GBS, 3),
                 "cache_bytes": int(cache_bytes), "decode_fast_exp": fast_exp}
 
     res = {"prefill_rows": P, "decode_steps": steps, "prefill_gflop": round((proj_flop + attn_flop) / 1e9, 2)}

@@ -225,20 +225,20 @@ __device__ __forceinline__ void tile_step(const AttnArgs &a, const KvTile &t, Wa
   }
 }
 
-// One work item of the plan on the FP32 matrix cores, through three LDS key
-// tiles (attention_kernel's, or the pair kernel's LDS when its pre-pass found
-// a non-finite K or V value).
-template <bool STATIC, bool FAST>
-__device__ __forceinline__ void attention_tiles(const AttnArgs &a, const split::Plan &plan, KvTile &tile0,
-                                                KvTile &tile1, KvTile &tile2) {
-  const int head = blockIdx.y;
+// Work item `item` of the plan for query head `head` on the FP32 matrix
+// cores, through a ring of RING LDS key tiles (3: two tiles in flight while
+// one is computed; 2: one).
+template <bool STATIC, bool FAST, int RING = 3>
+__device__ __forceinline__ void attention_tiles(const AttnArgs &a, const split::Plan &plan, int item, int head,
+                                                KvTile &tile0, KvTile &tile1, KvTile &tile2) {
+  static_assert(RING == 2 || RING == 3, "a ring of two or three tiles");
   const int kv_head = head / (a.n_heads / a.n_kv_heads);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int h = lane >> 5, l32 = lane & 31;
   // This workgroup's work item: part `it.part` of the tile `it.order` of the
   // plan (heavy, late tiles first).
-  const split::Item it = split::find_item(plan, a.tiles, blockIdx.x);
+  const split::Item it = split::find_item(plan, a.tiles, item);
   const int order = it.order, part = it.part, parts = it.parts;
   const int first_query = (a.tiles - 1 - order) * kQueries;
   const int wq0 = first_query + wave * 32;  // this wave's first query row
@@ -291,7 +291,10 @@ __device__ __forceinline__ void attention_tiles(const AttnArgs &a, const split::
     // This wave's copies into cur have landed and its reads of the previous
     // tile are done; after the barrier every wave's are, so the previous
     // tile's array (ahead) is free.
-    __builtin_amdgcn_s_waitcnt(4 | 0x0070);  // vmcnt(4) lgkmcnt(0)
+    if constexpr (RING == 3)
+      __builtin_amdgcn_s_waitcnt(4 | 0x0070);  // vmcnt(4) lgkmcnt(0)
+    else
+      __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
     plain_barrier();
     if (keys > 0 && keys < kKeys) {
       // Last tile: clear the V rows past the visible keys (p = 0 there, and
@@ -301,7 +304,7 @@ __device__ __forceinline__ void attention_tiles(const AttnArgs &a, const split::
       __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
       plain_barrier();
     }
-    const int far = kstart + 2 * kKeys;
+    const int far = kstart + (RING - 1) * kKeys;
     copy_tile(a, ahead, far < visible_end ? far : visible_end - 1, visible_end, head, kv_head, wave, lane);
     if (keys > 0 && w_queries > 0 && kstart < w_visible) {
       const bool full = keys == kKeys && (kstart + kKeys <= w_first + 1 ||
@@ -310,16 +313,23 @@ __device__ __forceinline__ void attention_tiles(const AttnArgs &a, const split::
     }
   };
   copy_tile(a, tile0, key_begin, visible_end, head, kv_head, wave, lane);
-  copy_tile(a, tile1, key_begin + kKeys < visible_end ? key_begin + kKeys : visible_end - 1, visible_end, head,
-            kv_head, wave, lane);
-  // Whole rounds of three steps (a step past the last tile only waits, meets
+  // Whole rounds of RING steps (a step past the last tile only waits, meets
   // the other waves and repeats a copy): the same straight-line code for
   // every round keeps the compiler's LDS-copy tracking exact, so it adds no
   // wait for the copies in flight before the reads of a landed tile.
-  for (int kstart = key_begin; kstart < visible_end; kstart += 3 * kKeys) {
-    step(tile0, tile2, kstart);
-    step(tile1, tile0, kstart + kKeys);
-    step(tile2, tile1, kstart + 2 * kKeys);
+  if constexpr (RING == 3) {
+    copy_tile(a, tile1, key_begin + kKeys < visible_end ? key_begin + kKeys : visible_end - 1, visible_end, head,
+              kv_head, wave, lane);
+    for (int kstart = key_begin; kstart < visible_end; kstart += 3 * kKeys) {
+      step(tile0, tile2, kstart);
+      step(tile1, tile0, kstart + kKeys);
+      step(tile2, tile1, kstart + 2 * kKeys);
+    }
+  } else {
+    for (int kstart = key_begin; kstart < visible_end; kstart += 2 * kKeys) {
+      step(tile0, tile1, kstart);
+      step(tile1, tile0, kstart + kKeys);
+    }
   }
 
   // Normalize and apply the sink (prefill64.rs:468-479); a split tile
@@ -367,7 +377,7 @@ template <bool STATIC, bool FAST>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) void attention_kernel(AttnArgs a,
                                                                                                 split::Plan plan) {
   __shared__ KvTile tiles[3];
-  attention_tiles<STATIC, FAST>(a, plan, tiles[0], tiles[1], tiles[2]);
+  attention_tiles<STATIC, FAST>(a, plan, blockIdx.x, blockIdx.y, tiles[0], tiles[1], tiles[2]);
 }
 
 // ---- FP32 products from FP16 pairs (focr_attention_prefill_split) --------
@@ -565,30 +575,19 @@ __device__ __forceinline__ void pair_tile_step(const PairKvTile &t, const HalfFr
                                                int image_start, int image_end) {
   // S^T = K Q^T: step s covers dims 16 s .. 16 s + 15 (lane half h: 8 h ..);
   // products (lo, hi), (hi, lo), (hi, hi).
-  HalfFrag kf[2][4];
-#pragma unroll
-  for (int p = 0; p < 2; p++)
-#pragma unroll
-    for (int s = 0; s < 4; s++) kf[p][s].u = t.k[p][l32 * 8 + ((2 * s + h) ^ ks(l32))];
-  // V^T fragments for the PV products below, read with K.
-  HalfFrag vf[2][2][2];
-#pragma unroll
-  for (int p = 0; p < 2; p++)
-#pragma unroll
-    for (int d = 0; d < 2; d++)
-#pragma unroll
-      for (int s2 = 0; s2 < 2; s2++) {
-        const int dim = l32 + 32 * d;
-        vf[p][d][s2].u = t.v[p][dim * 4 + ((2 * s2 + h) ^ vs(dim))];
-      }
+  // Fragments are read step by step (the registers hold four waves per SIMD).
   constexpr int pa[3] = {1, 0, 0}, pb[3] = {0, 1, 0};
   v16f st;
 #pragma unroll
   for (int r = 0; r < 16; r++) st[r] = 0.0f;
 #pragma unroll
-  for (int q = 0; q < 3; q++)
+  for (int s = 0; s < 4; s++) {
+    HalfFrag kf[2];
 #pragma unroll
-    for (int s = 0; s < 4; s++) st = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[pa[q]][s].v, qf[pb[q]][s].v, st, 0, 0, 0);
+    for (int p = 0; p < 2; p++) kf[p].u = t.k[p][l32 * 8 + ((2 * s + h) ^ ks(l32))];
+#pragma unroll
+    for (int q = 0; q < 3; q++) st = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[pa[q]].v, qf[pb[q]][s].v, st, 0, 0, 0);
+  }
   // Register r holds key kstart + 8(r/4) + 4h + r%4. The descale c (> 0) is
   // exact, a power of two, times log2(e) for the hardware exp2 (one rounding,
   // as exp_hw's log2(e) * s). It is applied inside the max and the exp
@@ -685,49 +684,58 @@ __device__ __forceinline__ void pair_tile_step(const PairKvTile &t, const HalfFr
   // O^T += V^T P^T: step s2 takes score registers 8 s2 .. 8 s2 + 7 (keys
   // 16 s2 + 4h + 8(e/4) + e%4) as the B operand, V^T slots 16 s2 + 8h .. of
   // dim l32 + 32 d as the A operand; products (lo, hi), (hi, lo), (hi, hi).
-  HalfFrag pf[2][2];
 #pragma unroll
   for (int s2 = 0; s2 < 2; s2++) {
-    uint32_t hw[4], lw[4];
+    HalfFrag pf[2];
+    {
+      uint32_t hw[4], lw[4];
 #pragma unroll
-    for (int e = 0; e < 4; e++)
-      pair2_rtz(shift ? __builtin_ldexpf(st[8 * s2 + 2 * e], shift) : st[8 * s2 + 2 * e],
-                shift ? __builtin_ldexpf(st[8 * s2 + 2 * e + 1], shift) : st[8 * s2 + 2 * e + 1], hw[e], lw[e]);
-    pf[0][s2].u = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-    pf[1][s2].u = make_uint4(lw[0], lw[1], lw[2], lw[3]);
-  }
+      for (int e = 0; e < 4; e++)
+        pair2_rtz(shift ? __builtin_ldexpf(st[8 * s2 + 2 * e], shift) : st[8 * s2 + 2 * e],
+                  shift ? __builtin_ldexpf(st[8 * s2 + 2 * e + 1], shift) : st[8 * s2 + 2 * e + 1], hw[e], lw[e]);
+      pf[0].u = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+      pf[1].u = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+    }
+    HalfFrag vf[2][2];
 #pragma unroll
-  for (int q = 0; q < 3; q++)
+    for (int p = 0; p < 2; p++)
 #pragma unroll
-    for (int s2 = 0; s2 < 2; s2++)
+      for (int d = 0; d < 2; d++) {
+        const int dim = l32 + 32 * d;
+        vf[p][d].u = t.v[p][dim * 4 + ((2 * s2 + h) ^ vs(dim))];
+      }
+#pragma unroll
+    for (int q = 0; q < 3; q++)
 #pragma unroll
       for (int d = 0; d < 2; d++)
-        o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[pa[q]][d][s2].v, pf[pb[q]][s2].v, o[d], 0, 0, 0);
+        o[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[pa[q]][d].v, pf[pb[q]].v, o[d], 0, 0, 0);
+  }
 }
 
 // Pure prefill only (every key a prefix key, queries = keys from position 0).
 template <bool STATIC, bool FAST>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void attention_pair_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void attention_pair_kernel(
     AttnArgs a, const uint4 *__restrict__ kp, const uint4 *__restrict__ vp, const int *__restrict__ kexp,
     const unsigned *__restrict__ vmax, const unsigned *__restrict__ nonfinite, size_t kplane, size_t vplane,
     int ktiles, split::Plan plan) {
-  static_assert(sizeof(PairKvTile) == sizeof(KvTile), "the two kernels' key tiles share the LDS");
+  static_assert(sizeof(PairKvTile) == sizeof(KvTile), "the two bodies' key tiles share the LDS");
   __shared__ union {
-    PairKvTile pair[3];
-    KvTile f32[3];
+    PairKvTile pair[2];
+    KvTile f32[2];
   } lds;
   __shared__ int vexp[64];
   if (*nonfinite != 0u) {
     // The pre-pass found a non-finite K or V value: an infinity in an FP16
     // pair meets zero halves (0 * inf = NaN) where FP32 products give +-inf
     // (a -inf score is a zero probability), so the whole call takes the FP32
-    // products, with the same plan and partial-state layout.
-    attention_tiles<STATIC, FAST>(a, plan, lds.f32[0], lds.f32[1], lds.f32[2]);
+    // products (attention_kernel's body on a ring of two tiles), with the
+    // same plan and partial-state layout. Its registers spill under this
+    // kernel's budget; it runs only for such calls.
+    attention_tiles<STATIC, FAST, 2>(a, plan, blockIdx.x, blockIdx.y, lds.f32[0], lds.f32[1], lds.f32[1]);
     return;
   }
   PairKvTile &tile0 = lds.pair[0];
   PairKvTile &tile1 = lds.pair[1];
-  PairKvTile &tile2 = lds.pair[2];
   const int head = blockIdx.y;
   const int kv_head = head / (a.n_heads / a.n_kv_heads);
   const int tid = threadIdx.x, lane = tid & 63;
@@ -787,11 +795,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
   float run_max = -__builtin_inff(), den = 0.0f;
   int pexp = kPairMinExp;
 
-  // Tile t sits in array t % 3; tiles t + 1 and t + 2 are in flight while it
-  // is computed (past the last tile the copy repeats the last one).
+  // Tile t sits in array t % 2; tile t + 1 is in flight while it is computed
+  // (past the last tile the copy repeats the last one). Two arrays (32 KB)
+  // and at most 128 VGPRs keep four waves per SIMD.
   auto step = [&](PairKvTile &cur, PairKvTile &ahead, int kstart) __attribute__((always_inline)) {
     const int keys = visible_end - kstart < kKeys ? visible_end - kstart : kKeys;
-    __builtin_amdgcn_s_waitcnt(4 | 0x0070);  // vmcnt(4) lgkmcnt(0): this tile's four copies
+    __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0): this tile's four copies
     plain_barrier();
     if (keys > 0 && keys < kKeys) {
       // Last tile: clear the V slots of keys past the visible ones in both
@@ -806,8 +815,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
       __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
       plain_barrier();
     }
-    const int far = kstart + 2 * kKeys;
-    copy_pair_tile(ahead, kp, vp, kplane, vplane, ktiles, (far < visible_end ? far : visible_end - 1) / kKeys, head,
+    const int next = kstart + kKeys;
+    copy_pair_tile(ahead, kp, vp, kplane, vplane, ktiles, (next < visible_end ? next : visible_end - 1) / kKeys, head,
                    kv_head, wave, tid);
     if (keys > 0 && w_queries > 0 && kstart < w_visible) {
       const bool full = keys == kKeys && (kstart + kKeys <= w_first + 1 ||
@@ -820,13 +829,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
     }
   };
   copy_pair_tile(tile0, kp, vp, kplane, vplane, ktiles, key_begin / kKeys, head, kv_head, wave, tid);
-  copy_pair_tile(tile1, kp, vp, kplane, vplane, ktiles,
-                 (key_begin + kKeys < visible_end ? key_begin + kKeys : visible_end - 1) / kKeys, head, kv_head, wave,
-                 tid);
-  for (int kstart = key_begin; kstart < visible_end; kstart += 3 * kKeys) {
-    step(tile0, tile2, kstart);
+  for (int kstart = key_begin; kstart < visible_end; kstart += 2 * kKeys) {
+    step(tile0, tile1, kstart);
     step(tile1, tile0, kstart + kKeys);
-    step(tile2, tile1, kstart + 2 * kKeys);
   }
 
   // The running maximum in natural units (FAST keeps it in log2 units).
@@ -1036,15 +1041,16 @@ int launch_attention_split(Ctx *ctx, const float *q, const float *k, const float
     }
     const dim3 grid(static_cast<unsigned>(items), static_cast<unsigned>(n_heads));
     const int kt = static_cast<int>(ktiles);
-    if (softmax == FOCR_SOFTMAX_STATIC)
+    if (softmax == FOCR_SOFTMAX_STATIC) {
       hipLaunchKernelGGL((attention_pair_kernel<true, true>), grid, dim3(256), 0, ctx->stream, a, kp, vp, kexp, vmax,
                          nonfinite, kplane, vplane, kt, plan);
-    else if (exp_mode == FOCR_EXP_FAST)
+    } else if (exp_mode == FOCR_EXP_FAST) {
       hipLaunchKernelGGL((attention_pair_kernel<false, true>), grid, dim3(256), 0, ctx->stream, a, kp, vp, kexp, vmax,
                          nonfinite, kplane, vplane, kt, plan);
-    else
+    } else {
       hipLaunchKernelGGL((attention_pair_kernel<false, false>), grid, dim3(256), 0, ctx->stream, a, kp, vp, kexp, vmax,
                          nonfinite, kplane, vplane, kt, plan);
+    }
     FOCR_HIP_CHECK(hipGetLastError());
     if (slots > 0) {
       split::Args m;

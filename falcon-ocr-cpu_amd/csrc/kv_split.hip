@@ -928,12 +928,18 @@ __global__ __launch_bounds__(256) void split_scan_kernel(SplitDecArgs a, int ite
 template <typename C, int M, bool ROW = false>
 int launch_split(Ctx *ctx, SplitDecArgs a, int rows, bool fast, const float *sinks, float *out, float *fixed,
                  size_t fixed_bytes) {
-  // Keys per workgroup task: about 1024 tasks over the chip (each serves two
-  // heads), at most kMaxChunks chunks, whole multiples of 64 keys (every
-  // wave of the task takes the same number of 16-key iterations).
+  // Keys per workgroup task, whole multiples of 64 keys (every wave of the
+  // task takes the same number of 16-key iterations), at most kMaxChunks
+  // chunks. Each task serves two heads. Up to 32,768 positions: about 512
+  // tasks (keys per task rounded to the nearest 64), which halves the
+  // partial states the combine reads; beyond: about 1024 tasks (rounded up),
+  // whose extra parallelism the longer cold scan needs. Measured one-row
+  // decode over Q8 records (cold): 16,384 positions 15.6 us with 512 tasks
+  // against 17.0 with 1,024; 65,536 positions 28.1 us with 1,024 tasks
+  // against 29.0 with 512; 4,160 positions 12.8 us with 520 tasks against
+  // 13.2 with 264.
   const long limit = a.last;
-  const long want = (limit * a.n_kv + 1023) / 1024;
-  long per = (want + 63) / 64 * 64;
+  long per = limit <= 32768 ? (limit * a.n_kv / 512 + 32) / 64 * 64 : ((limit * a.n_kv + 1023) / 1024 + 63) / 64 * 64;
   const long min_per = ((limit + kMaxChunks - 1) / kMaxChunks + 63) / 64 * 64;
   if (per < min_per) per = min_per;
   if (per < 64) per = 64;

@@ -933,6 +933,7 @@ constexpr int kSplitBM = 128, kSplitBN = 128, kSplitBK = 16, kSplitKAlign = 32;
 //    1 KB pieces). Thread (s % 16, r, q) converts values 16 s + 4 q .. + 3 of
 //    row r; sixteen threads write one stage of the 4 rows, 128 contiguous
 //    bytes per plane. The second pass reads the rows the first one just read.
+constexpr int kRowBatch = 4;
 __global__ __launch_bounds__(256) void pair_rows_kernel(const float *__restrict__ src, int rows, int cols,
                                                         const float *__restrict__ row_scale, bool vec,
                                                         int *__restrict__ exps, uint16_t *__restrict__ dst,
@@ -947,12 +948,21 @@ __global__ __launch_bounds__(256) void pair_rows_kernel(const float *__restrict_
       const float *r = src + static_cast<size_t>(row) * cols;
       const float sc = row_scale ? row_scale[row] : 1.0f;
       if (vec) {
-        for (int c = 4 * lane; c < cols; c += 256) {
-          const float4 f = *reinterpret_cast<const float4 *>(r + c);
-          const float v0 = row_scale ? f.x * sc : f.x, v1 = row_scale ? f.y * sc : f.y;
-          const float v2 = row_scale ? f.z * sc : f.z, v3 = row_scale ? f.w * sc : f.w;
-          m = __builtin_fmaxf(m, __builtin_fmaxf(__builtin_fmaxf(finite_abs(v0), finite_abs(v1)),
-                                                 __builtin_fmaxf(finite_abs(v2), finite_abs(v3))));
+        // kRowBatch loads in flight per lane before any is used.
+        for (int c0 = 4 * lane; c0 < cols; c0 += 256 * kRowBatch) {
+          float4 f[kRowBatch];
+#pragma unroll
+          for (int u = 0; u < kRowBatch; u++) {
+            const int c = c0 + 256 * u;
+            f[u] = c < cols ? *reinterpret_cast<const float4 *>(r + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+          }
+#pragma unroll
+          for (int u = 0; u < kRowBatch; u++) {
+            const float v0 = row_scale ? f[u].x * sc : f[u].x, v1 = row_scale ? f[u].y * sc : f[u].y;
+            const float v2 = row_scale ? f[u].z * sc : f[u].z, v3 = row_scale ? f[u].w * sc : f[u].w;
+            m = __builtin_fmaxf(m, __builtin_fmaxf(__builtin_fmaxf(finite_abs(v0), finite_abs(v1)),
+                                                   __builtin_fmaxf(finite_abs(v2), finite_abs(v3))));
+          }
         }
       } else {
         for (int c = lane; c < cols; c += 64) m = __builtin_fmaxf(m, finite_abs(row_scale ? r[c] * sc : r[c]));
@@ -973,32 +983,55 @@ __global__ __launch_bounds__(256) void pair_rows_kernel(const float *__restrict_
   const int shift = 15 - row_exp[rl];
   const float *rp = src + static_cast<size_t>(row < rows ? row : 0) * cols;
   const float sc = row_scale && row < rows ? row_scale[row] : 1.0f;
-  for (int st = threadIdx.x >> 4; st < stages; st += 16) {
-    const int c0 = 16 * st + 4 * q;
-    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (row < rows) {
-      if (vec && c0 + 3 < cols) {
-        const float4 f = *reinterpret_cast<const float4 *>(rp + c0);
-        v[0] = f.x;
-        v[1] = f.y;
-        v[2] = f.z;
-        v[3] = f.w;
-      } else {
+  // kRowBatch stages per thread and pass: their loads are all in flight
+  // before the first is converted.
+  for (int st0 = threadIdx.x >> 4; st0 < stages; st0 += 16 * kRowBatch) {
+    float v[kRowBatch][4];
+    if (vec) {
+      // cols % 4 == 0: a 4-value group is wholly in or past the row; the
+      // loads read an in-bounds group either way (branch-free, so none waits
+      // for another).
+      float4 f[kRowBatch];
 #pragma unroll
-        for (int e = 0; e < 4; e++) v[e] = c0 + e < cols ? rp[c0 + e] : 0.0f;
+      for (int u = 0; u < kRowBatch; u++) {
+        const int c0 = 16 * (st0 + 16 * u) + 4 * q;
+        const bool ok = row < rows && st0 + 16 * u < stages && c0 < cols;
+        f[u] = *reinterpret_cast<const float4 *>(rp + (ok ? c0 : 0));
+        f[u] = ok ? f[u] : make_float4(0.f, 0.f, 0.f, 0.f);
       }
-      if (row_scale) {
 #pragma unroll
-        for (int e = 0; e < 4; e++)
-          if (c0 + e < cols) v[e] = v[e] * sc;
+      for (int u = 0; u < kRowBatch; u++) {
+        v[u][0] = f[u].x;
+        v[u][1] = f[u].y;
+        v[u][2] = f[u].z;
+        v[u][3] = f[u].w;
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < kRowBatch; u++) {
+        const int c0 = 16 * (st0 + 16 * u) + 4 * q;
+        const bool ok = row < rows && st0 + 16 * u < stages;
+#pragma unroll
+        for (int e = 0; e < 4; e++) v[u][e] = ok && c0 + e < cols ? rp[c0 + e] : 0.0f;
       }
     }
-    uint16_t hh[4], ll[4];
 #pragma unroll
-    for (int e = 0; e < 4; e++) pair1(v[e], shift, hh[e], ll[e]);
-    const size_t off = (static_cast<size_t>(st) * rows_pad + row) * 16 + 4 * q;
-    *reinterpret_cast<uint2 *>(dst + off) = make_uint2(hh[0] | hh[1] << 16, hh[2] | hh[3] << 16);
-    *reinterpret_cast<uint2 *>(dst + plane + off) = make_uint2(ll[0] | ll[1] << 16, ll[2] | ll[3] << 16);
+    for (int u = 0; u < kRowBatch; u++) {
+      const int st = st0 + 16 * u;
+      if (st >= stages) break;
+      const int c0 = 16 * st + 4 * q;
+      if (row < rows && row_scale) {
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+          if (c0 + e < cols) v[u][e] = v[u][e] * sc;
+      }
+      uint16_t hh[4], ll[4];
+#pragma unroll
+      for (int e = 0; e < 4; e++) pair1(v[u][e], shift, hh[e], ll[e]);
+      const size_t off = (static_cast<size_t>(st) * rows_pad + row) * 16 + 4 * q;
+      *reinterpret_cast<uint2 *>(dst + off) = make_uint2(hh[0] | hh[1] << 16, hh[2] | hh[3] << 16);
+      *reinterpret_cast<uint2 *>(dst + plane + off) = make_uint2(ll[0] | ll[1] << 16, ll[2] | ll[3] << 16);
+    }
   }
 }
 

@@ -822,7 +822,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void a
       const bool full = keys == kKeys && (kstart + kKeys <= w_first + 1 ||
                                           (w_all_image && kstart >= a.image_start && kstart + kKeys <= a.image_end));
       const int ke = kexp[head * ktiles + kstart / kKeys];
-      // Kept a normal float (> 0) when the scores are below 2^-100 anyway.
+      // Kept a normal float (> 0): it is clamped only where every scaled
+      // score (|q'.k'| < 64 2^30) times the true factor is below 2^-89, so
+      // exp gives 1 with either factor.
       const float c = __builtin_fmaxf(__builtin_ldexpf(cbase, qexp + ke - 33), 1.17549435e-38f);
       pair_tile_step<STATIC, FAST>(cur, qf, o, run_max, den, pexp, c, kstart, keys, !full, h, l32, my_abs, my_image,
                                    a.image_start, a.image_end);

@@ -156,8 +156,11 @@ __device__ __forceinline__ float sdwa_cvt(uint32_t w) {
 // exact in FP32, so x' = hi + lo to 2^-22 |x'| (to 2^-25 absolute once lo is
 // an FP16 subnormal, for |x'| below about 2^-3). An infinity or NaN travels
 // in hi alone (lo = 0) and does not set e. Exponents are clamped below at
-// kPairMinExp, so that 2^(15 - e) and 2^(e - 15) stay normal floats.
-constexpr int kPairMinExp = -100;
+// kPairMinExp, the least e for which 2^(15 - e) and 2^(e - 15) are normal
+// floats: a block whose largest magnitude is below 2^-111 (tiny normals,
+// subnormals) is scaled by 2^126, so that even the least subnormal, 2^-149,
+// becomes 2^-23 and every subnormal (a multiple of 2^-149) is exactly hi + lo.
+constexpr int kPairMinExp = -111;
 
 __device__ __forceinline__ int pair_exp(float m) {
   const int e = m > 0.0f ? __builtin_amdgcn_frexp_expf(m) : kPairMinExp;

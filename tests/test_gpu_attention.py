@@ -262,6 +262,38 @@ def test_split_products_wide_magnitudes(fh):
 
 @pytest.mark.parametrize("static", [False, True])
 @pytest.mark.parametrize("products", ["split", "fp32"])
+def test_tiny_and_subnormal_magnitudes(fh, static, products):
+    # Q times 2^124 against K times 2^-124 (scores of order one from keys
+    # that are tiny normals and, one in five or so, subnormals), and value
+    # dims from 2^-145 to 2^20. Against the exact attention of these inputs
+    # (float64): every output within 1e-5 of its dim's largest output, plus,
+    # in the subnormal range, a few steps of 2^-149 for the FP16-pair products
+    # (the output's last roundings) and one step per key for the FP32 ones
+    # (their P V products round there one by one, as the reference's do).
+    L, image = 700, (0, 128)
+    if static:
+        q, k = gen.normalized(L * 16 * 64, 84), gen.normalized(L * 16 * 64, 85)
+    else:
+        q, k = gen.normal(L * 16 * 64, 1.0, 84), gen.normal(L * 16 * 64, 1.0, 85)
+    q = (q * np.float32(2.0 ** 124)).astype(np.float32)
+    k = (k * np.float32(2.0 ** -124)).astype(np.float32)
+    dims = np.ldexp(1.0, np.tile([0, -110, -120, -126, -130, -140, -145, 20], 8))
+    v = (gen.normal((L, 8, 64), 1.0, 86) * dims).astype(np.float32).ravel()
+    sinks = gen.uniform(16, -2.0, 2.0, 87)
+    assert np.all(np.isfinite(q)) and np.any((k != 0) & (np.abs(k) < 2.0 ** -126))
+    opts = fh.PrefillOptions(exp=fh.ExpMode.FAST if static else fh.ExpMode.EXACT,
+                             fp32_softmax=fh.Softmax.STATIC if static else fh.Softmax.ONLINE,
+                             split_products=products == "split")
+    got = run(fh, q, k, v, sinks, L, (0, *image), opts).astype(np.float64)
+    exact = attention_f64(q, k, v, L, 16, 8, image, sinks.astype(np.float64))
+    scale = np.max(np.abs(exact), axis=0, keepdims=True)
+    steps = 8 if products == "split" else L + 8
+    bound = 1e-5 * scale + steps * 2.0 ** -149
+    assert np.all(np.abs(got - exact) <= bound), float(np.max((np.abs(got - exact) - bound) / scale))
+
+
+@pytest.mark.parametrize("static", [False, True])
+@pytest.mark.parametrize("products", ["split", "fp32"])
 def test_nan_key_propagates_as_the_reference(fh, static, products):
     # static_shift/tests.rs:311-367 (nan_keys_propagate_in_masked_tiles): a
     # NaN in head 0 of key 66, text after the image [3, 65): rows 66 to 69

@@ -254,6 +254,36 @@ def test_f32_split_wide_row_magnitudes(fh):
     assert np.all(np.abs(got - exact) <= 2 * k * EPS * mag), float(np.max(np.abs(got - exact) / mag))
 
 
+def test_f32_split_zero_tiny_and_subnormal_rows(fh):
+    # Rows of A (and rows of W) that are zero, tiny normals or FP32
+    # subnormals: a zero row gives zero outputs, and every output is within
+    # 2 k eps of the magnitude sum plus one subnormal step (the final
+    # rounding into the subnormal range) of the exact product; against the
+    # reference's panels, whose products round one by one in the subnormal
+    # range, within twice that plus k steps.
+    m, k, n = 12, 64, 64
+    a = gen.normal((m, k), 1.0, 37)
+    scale = [0.0, 2.0 ** -100, 2.0 ** -110, 2.0 ** -118, 2.0 ** -124, 2.0 ** -126, 2.0 ** -130, 2.0 ** -140,
+             1.0, 1.0, 1.0, 2.0 ** 100]
+    a = (a * np.array(scale)[:, None]).astype(np.float32)
+    a[9, :] = 0.0
+    a[9, ::7] = np.float32(2.0 ** -149)  # the least subnormal, alone in a zero row
+    a[10, 0] = np.float32(2.0 ** -140)  # a subnormal among normal values
+    w = gen.normal((n, k), 0.02, 38)
+    w[5] *= np.float32(2.0 ** -120)
+    w[6] *= np.float32(2.0 ** -135)
+    w[7] = 0.0
+    got = run_prefill(fh, fh.Linear.from_f32(w), a, m, None, fh.Epilogue.STORE,
+                      fh.PrefillProjection.F32_SPLIT).astype(np.float64)
+    assert np.all(got[0] == 0.0) and np.all(got[:, 7] == 0.0)
+    exact = a.astype(np.float64) @ w.astype(np.float64).T
+    mag = np.abs(a.astype(np.float64)) @ np.abs(w.astype(np.float64)).T
+    bound = 2 * k * EPS * mag + 2.0 ** -149
+    assert np.all(np.abs(got - exact) <= bound), float(np.max((np.abs(got - exact) - bound) / np.maximum(mag, 1e-300)))
+    want = oracle.panel_gemm(a, m, k, w, n).astype(np.float64)
+    assert np.all(np.abs(got - want) <= 4 * k * EPS * mag + k * 2.0 ** -149)
+
+
 def test_f32_split_nonfinite_rows_stay_nonfinite_and_codes_are_refused(fh):
     # An infinite or NaN input reaches every output of its row as a
     # non-finite value (an infinity times a zero part is NaN where the FP32

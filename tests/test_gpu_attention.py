@@ -316,6 +316,39 @@ def test_nan_key_propagates_as_the_reference(fh, static, products):
     close(got[~poisoned], want[~poisoned])
 
 
+@pytest.mark.parametrize("static,exp", [(False, "fast"), (False, "exact"), (True, "fast")])
+@pytest.mark.parametrize("products", ["split", "fp32"])
+def test_nonfinite_query_poisons_its_row_and_head_only(fh, static, exp, products):
+    # An infinity or NaN in one query value makes that query's scores in its
+    # head infinite or NaN; the reference's output for that (row, head) is
+    # all NaN (exp(inf - inf), or 0 / 0 when every score is -inf), and no
+    # other output changes. Rows in and past the image, tiles split into
+    # several key ranges.
+    L, image = 2100, (0, 700)
+    q = gen.normalized(L * 16 * 64, 121) if static else gen.normal(L * 16 * 64, 1.0, 121)
+    k = gen.normalized(L * 16 * 64, 122) if static else gen.normal(L * 16 * 64, 1.0, 122)
+    v = gen.normal(L * 8 * 64, 1.0, 123)
+    sinks = gen.uniform(16, -2.0, 2.0, 124)
+    poisoned = np.zeros((L, 16), bool)
+    for r, h, d, val in ((40, 3, 5, np.inf), (600, 2, 63, -np.inf), (1800, 7, 0, np.nan), (2000, 11, 9, np.inf)):
+        q[(r * 16 + h) * 64 + d] = val
+        poisoned[r, h] = True
+    opts = fh.PrefillOptions(exp=fh.ExpMode.FAST if exp == "fast" else fh.ExpMode.EXACT,
+                             fp32_softmax=fh.Softmax.STATIC if static else fh.Softmax.ONLINE,
+                             split_products=products == "split")
+    got = run(fh, q, k, v, sinks, L, (0, *image), opts)
+    oracle.set_threads(oracle_threads())
+    if exp == "fast":
+        want = oracle.attention_prefill_fast(q, k, v, L, L, L, 16, 8, 0, *image, sinks, static=static)
+    else:
+        want = oracle.attention_prefill(q, k, v, L, L, L, 16, 8, 0, *image, sinks, exp_fast=False)
+    want = want.reshape(L, 16, 64)
+    assert np.array_equal(np.isnan(want).all(axis=2), poisoned) and np.all(np.isfinite(want[~poisoned]))
+    assert np.array_equal(np.isnan(got).all(axis=2), poisoned)
+    assert np.all(np.isfinite(got[~poisoned]))
+    close(got[~poisoned], want[~poisoned])
+
+
 @pytest.mark.parametrize("case", ["k_neg_inf", "k_pos_inf", "v_inf"])
 def test_split_products_nonfinite_kv_take_the_fp32_products(fh, case):
     # An infinity in an FP16 pair meets zero halves (0 * inf = NaN) where the

@@ -254,13 +254,9 @@ def test_f32_split_wide_row_magnitudes(fh):
     assert np.all(np.abs(got - exact) <= 2 * k * EPS * mag), float(np.max(np.abs(got - exact) / mag))
 
 
-def test_f32_split_zero_tiny_and_subnormal_rows(fh):
-    # Rows of A (and rows of W) that are zero, tiny normals or FP32
-    # subnormals: a zero row gives zero outputs, and every output is within
-    # 2 k eps of the magnitude sum plus one subnormal step (the final
-    # rounding into the subnormal range) of the exact product; against the
-    # reference's panels, whose products round one by one in the subnormal
-    # range, within twice that plus k steps.
+def tiny_rows():
+    """Rows of A (and of W) that are zero, tiny normals or FP32 subnormals,
+    beside ordinary ones (m, k, n = 12, 64, 64)."""
     m, k, n = 12, 64, 64
     a = gen.normal((m, k), 1.0, 37)
     scale = [0.0, 2.0 ** -100, 2.0 ** -110, 2.0 ** -118, 2.0 ** -124, 2.0 ** -126, 2.0 ** -130, 2.0 ** -140,
@@ -273,6 +269,16 @@ def test_f32_split_zero_tiny_and_subnormal_rows(fh):
     w[5] *= np.float32(2.0 ** -120)
     w[6] *= np.float32(2.0 ** -135)
     w[7] = 0.0
+    return a, w, m, k, n
+
+
+def test_f32_split_zero_tiny_and_subnormal_rows(fh):
+    # A zero row gives zero outputs, and every output is within 2 k eps of
+    # the magnitude sum plus one subnormal step (the final rounding into the
+    # subnormal range) of the exact product; against the reference's panels,
+    # whose products round one by one in the subnormal range, within twice
+    # that plus k steps.
+    a, w, m, k, n = tiny_rows()
     got = run_prefill(fh, fh.Linear.from_f32(w), a, m, None, fh.Epilogue.STORE,
                       fh.PrefillProjection.F32_SPLIT).astype(np.float64)
     assert np.all(got[0] == 0.0) and np.all(got[:, 7] == 0.0)
@@ -282,6 +288,23 @@ def test_f32_split_zero_tiny_and_subnormal_rows(fh):
     assert np.all(np.abs(got - exact) <= bound), float(np.max((np.abs(got - exact) - bound) / np.maximum(mag, 1e-300)))
     want = oracle.panel_gemm(a, m, k, w, n).astype(np.float64)
     assert np.all(np.abs(got - want) <= 4 * k * EPS * mag + k * 2.0 ** -149)
+
+
+def test_f32_chain_and_mfma_zero_tiny_and_subnormal_rows(fh):
+    # The same rows through the FP32 kernels: the exact-order chain bitwise
+    # the reference's panels (subnormal products and sums included), the FP32
+    # matrix cores within 2 k eps of the magnitude sum plus k subnormal steps
+    # of the panels.
+    a, w, m, k, n = tiny_rows()
+    lin = fh.Linear.from_f32(w)
+    want = oracle.panel_gemm(a, m, k, w, n)
+    chain = run_prefill(fh, lin, a, m, None, fh.Epilogue.STORE, fh.PrefillProjection.F32_CHAIN)
+    assert_bitwise(chain, want, "chain, tiny rows")
+    got = run_prefill(fh, lin, a, m, None, fh.Epilogue.STORE, fh.PrefillProjection.F32_MFMA).astype(np.float64)
+    mag = np.abs(a.astype(np.float64)) @ np.abs(w.astype(np.float64)).T
+    bound = 2 * k * EPS * mag + k * 2.0 ** -149
+    d = np.abs(got - want)
+    assert np.all(d <= bound), float(np.max((d - bound) / np.maximum(mag, 1e-300)))
 
 
 def test_f32_split_nonfinite_rows_stay_nonfinite_and_codes_are_refused(fh):

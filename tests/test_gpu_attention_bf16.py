@@ -138,3 +138,34 @@ def test_split_key_ranges_bf16(fh, softmax, L, image):
     want = oracle.attention_prefill_bf16(q, k, v, L, 16, 8, *image, sinks, static=softmax == "static")
     assert np.all(np.isfinite(got))
     assert max_rel(got, want) <= 2e-3
+
+
+@pytest.mark.parametrize("softmax", ["online", "static"])
+def test_nonfinite_inputs_poison_what_the_reference_poisons(fh, softmax):
+    # An infinity or NaN in one query value poisons that (row, head); a NaN
+    # key value poisons its head's rows that see the key (causal after it,
+    # and every image row for an image key); all of them all NaN, as the
+    # reference's BF16 tiles give, and every other output unchanged. Tiles
+    # split into several key ranges.
+    oracle.set_threads(8)
+    r = oracle.bf16_round
+    L, image = 2100, (0, 700)
+    q = r(gen.normalized(L * 16 * 64, 131))
+    k = r(gen.normalized(L * 16 * 64, 132))
+    v = r(gen.values(L * 8 * 64, 133, 3.0))
+    sinks = gen.values(16, 29, 2.0)
+    for row, h, d, val in ((40, 3, 5, np.inf), (1800, 7, 0, np.nan), (600, 2, 63, -np.inf)):
+        q[(row * 16 + h) * 64 + d] = val
+    k[(1500 * 16 + 9) * 64 + 4] = np.nan  # text key 1500, head 9
+    k[(650 * 16 + 12) * 64 + 1] = np.nan  # image key 650, head 12
+    poisoned = np.zeros((L, 16), bool)
+    poisoned[40, 3] = poisoned[1800, 7] = poisoned[600, 2] = True
+    poisoned[1500:, 9] = True
+    poisoned[:, 12] = True
+    static = softmax == "static"
+    got = run(fh, q, k, v, sinks, L, image, fh.Softmax.STATIC if static else fh.Softmax.ONLINE)
+    want = oracle.attention_prefill_bf16(q, k, v, L, 16, 8, *image, sinks, static=static).reshape(L, 16, 64)
+    assert np.array_equal(np.isnan(want).all(axis=2), poisoned) and np.all(np.isfinite(want[~poisoned]))
+    assert np.array_equal(np.isnan(got).all(axis=2), poisoned)
+    assert np.all(np.isfinite(got[~poisoned]))
+    assert max_rel(got[~poisoned], want[~poisoned]) <= 2e-3

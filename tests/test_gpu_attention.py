@@ -354,11 +354,14 @@ def test_split_products_nonfinite_kv_take_the_fp32_products(fh, case):
     # An infinity in an FP16 pair meets zero halves (0 * inf = NaN) where the
     # FP32 products give +-inf, so a call whose K or V holds a non-finite
     # value runs the FP32 products on the device: the outputs are bitwise the
-    # FP32 entry point's (the same plan), and for K under the online softmax
-    # the finite pattern and the finite values are the oracle's (a -inf score
-    # is a zero probability; the static softmax's exp takes finite scores
-    # only, exp_lanes in static_shift.rs). The next finite call takes the
-    # pairs again.
+    # FP32 entry point's (the same plan), and for V, and for K under the
+    # online softmax, the NaN and infinity patterns and the finite values are
+    # the oracle's (a -inf score is a zero probability; an infinite value
+    # reaches the rows that see its key as an infinity, and as a NaN, 0 * inf,
+    # the earlier rows of the 32-row group that multiply the key's masked zero
+    # probability; the static softmax's exp takes finite scores only,
+    # exp_lanes in static_shift.rs). The next finite call takes the pairs
+    # again.
     L, image = 300, (0, 100)
     q = gen.normalized(L * 16 * 64, 95)
     k = gen.normalized(L * 16 * 64, 96)
@@ -376,11 +379,13 @@ def test_split_products_nonfinite_kv_take_the_fp32_products(fh, case):
         fp32 = run(fh, q, bad_k, bad_v, sinks, L, (0, *image), fh.PrefillOptions(split_products=False, **opts))
         assert not np.all(np.isfinite(split))
         assert np.array_equal(split, fp32, equal_nan=True), static
-        if case != "v_inf" and not static:
-            want = oracle.attention_prefill(q, bad_k, bad_v, L, L, L, 16, 8, 0, *image, sinks).reshape(L, 16, 64)
-            assert np.array_equal(np.isfinite(split), np.isfinite(want))
+        if case == "v_inf" or not static:
+            want = oracle.attention_prefill(q, bad_k, bad_v, L, L, L, 16, 8, 0, *image, sinks,
+                                            static=static).reshape(L, 16, 64)
+            assert np.array_equal(np.isnan(split), np.isnan(want)) and np.array_equal(np.isinf(split), np.isinf(want))
             fin = np.isfinite(want)
-            assert np.any(fin[150:, 6]) and not np.all(fin[150:, 6])
+            if case != "v_inf":
+                assert np.any(fin[150:, 6]) and not np.all(fin[150:, 6])
             close(split[fin], want[fin])
     again = run(fh, q, k, v, sinks, L, (0, *image), fh.PrefillOptions())
     assert np.array_equal(again.view(np.uint32), clean.view(np.uint32))

@@ -59,6 +59,41 @@ def test_decode_exception_columns_in_ascending_order(fh, bits, n, k, group, colu
         assert_bitwise(got, want, f"exceptions bits {bits} rows {rows}")
 
 
+@pytest.mark.parametrize("bits", [8, 16, 32])
+def test_decode_nonfinite_activations(fh, bits):
+    # NaN and infinities in the activations travel as the reference's dot
+    # makes them (QuantLinear::linear takes them; only the scalar reference
+    # linear_f32 refuses them, linear.rs:289-291): bitwise, NaN by class,
+    # infinities by sign, through the plain and the GLU GEMVs, an exception
+    # column and zero weights included.
+    n, k, group = 38, 768, 64
+    columns = [5, 700]
+    if bits == 32:
+        w = gen.values(n * k, 41).reshape(n, k)
+        w[3, ::5] = 0.0
+        lin, args, kw = fh.Linear.from_f32(w), (32, w, None, n, k, 32), {}
+    else:
+        codes, scales, vals = quantized(bits, n, k, group, 43, exc=columns)
+        lin = fh.QuantLinear(bits, codes, scales, group, exc_cols=columns, exc_vals=vals)
+        args, kw = (bits, codes, scales, n, k, group), dict(exc_cols=columns, exc_vals=vals)
+    for rows in (1, 5, 8):
+        x = gen.values(rows * k, 47 + rows).reshape(rows, k)
+        x[0, 100] = np.nan
+        if rows > 1:
+            x[1, 5] = np.inf  # an exception column for the codes
+            x[2, 300] = -np.inf
+            x[3, 7], x[3, 9] = np.inf, -np.inf
+            x[4, 700] = np.nan
+        x = x.ravel()
+        got = host(lin.linear(to_dev(x), rows))
+        want = oracle.linear_decode(*args, x, rows, **kw)
+        assert not np.all(np.isfinite(want))
+        assert_bitwise(got, want, f"bits {bits} rows {rows}")
+        assert np.array_equal(np.isinf(got) & (got > 0), np.isinf(want) & (want > 0))
+        glu = host(lin.linear_glu(to_dev(x), rows))
+        assert_bitwise(glu, oracle.linear_decode_glu(*args, x, rows, **kw), f"glu bits {bits} rows {rows}")
+
+
 @pytest.mark.parametrize("in_dim,ffn", [(768, 2304), (65, 19), (1, 1), (1024, 64)])
 def test_fp32_decode_and_glu(fh, in_dim, ffn):
     # src/kernels/tests.rs:48-82 (NaN, signed zeros, negatives in the weights)

@@ -307,6 +307,37 @@ def test_f32_chain_and_mfma_zero_tiny_and_subnormal_rows(fh):
     assert np.all(d <= bound), float(np.max((d - bound) / np.maximum(mag, 1e-300)))
 
 
+def test_f32_chain_and_mfma_nonfinite_rows(fh):
+    # Infinite and NaN inputs: the exact-order chain bitwise the reference's
+    # panels (Store and Glu); the FP32 matrix cores with the panels' NaN and
+    # signed-infinity pattern (an infinity meets a zero weight as NaN, and
+    # opposite infinities cancel to NaN, in any order) and their finite
+    # values within the FP32 tolerance.
+    m, k, n = 20, 256, 64
+    a = gen.matrix(m * k, 25).reshape(m, k)
+    a[3, 17] = np.inf
+    a[4, 2], a[4, 9] = np.inf, -np.inf
+    a[6, 40] = -np.inf
+    a[7, 5] = np.nan
+    w = gen.matrix(n * k, 26).reshape(n, k)
+    w[::3, 17] = 0.0
+    w[:, 40] = np.abs(w[:, 40])
+    lin = fh.Linear.from_f32(w)
+    want = oracle.panel_gemm(a, m, k, w, n)
+    assert np.any(np.isnan(want[3])) and np.any(np.isinf(want[3])) and np.all(np.isinf(want[6]) & (want[6] < 0))
+    chain = run_prefill(fh, lin, a, m, None, fh.Epilogue.STORE, fh.PrefillProjection.F32_CHAIN)
+    assert_bitwise(chain, want, "chain, non-finite rows")
+    glu = run_prefill(fh, lin, a, m, None, fh.Epilogue.GLU, fh.PrefillProjection.F32_CHAIN)
+    assert_bitwise(glu, oracle.panel_gemm(a, m, k, w, n, epilogue=oracle.GLU), "chain glu, non-finite rows")
+    got = run_prefill(fh, lin, a, m, None, fh.Epilogue.STORE, fh.PrefillProjection.F32_MFMA)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    assert np.array_equal(np.isinf(got) & (got > 0), np.isinf(want) & (want > 0))
+    assert np.array_equal(np.isinf(got) & (got < 0), np.isinf(want) & (want < 0))
+    fin = np.isfinite(want)
+    mag = np.abs(np.where(np.isfinite(a), a, 0).astype(np.float64)) @ np.abs(w.astype(np.float64)).T
+    assert np.all(np.abs(got[fin].astype(np.float64) - want[fin]) <= 2 * k * EPS * mag[fin] + 1e-30)
+
+
 def test_f32_split_nonfinite_rows_stay_nonfinite_and_codes_are_refused(fh):
     # An infinite or NaN input reaches every output of its row as a
     # non-finite value (an infinity times a zero part is NaN where the FP32

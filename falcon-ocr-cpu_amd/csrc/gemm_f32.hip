@@ -918,13 +918,32 @@ void launch_one(bool chain, const GemmArgs &a, hipStream_t stream) {
 // left out, is below 2^-21 |x' y'|), and the output takes the exact
 // power-of-two descale 2^(e_row + e_col - 30). Three FP16 products per 16 k
 // cost 96 matrix-core cycles against 512 for eight v_mfma_f32_32x32x2f32.
+// A row of A' or of W that holds an infinity or NaN cannot go through the
+// pairs (an infinity in hi meets the other operand's zero lo: inf * 0 =
+// NaN, where FP32 products give the infinity): its exponent entry carries
+// kPairNonfinite on top of the exponent, and the outputs it reaches are
+// recomputed by the reference's FP32 chain (chain_output).
 constexpr int kSplitBM = 128, kSplitBN = 128, kSplitBK = 16, kSplitKAlign = 32;
+constexpr int kPairNonfinite = 1 << 16;
+
+// One output by the reference's FP32 panel order (panel.rs:154-172): an FMA
+// chain over k ascending from +0 on A' = fl(x * row_scale) and W, bitwise
+// the FP32 chain kernel's.
+__device__ __forceinline__ float chain_output(const GemmArgs &a, int row, int col) {
+  const float *x = a.x + static_cast<size_t>(row) * a.k;
+  const float *w = static_cast<const float *>(a.codes) + static_cast<size_t>(col) * a.k;
+  const float rs = a.row_scale ? a.row_scale[row] : 1.0f;
+  float acc = 0.0f;
+  for (int kk = 0; kk < a.k; kk++) acc = fmaf_(a.row_scale ? __fmul_rn(x[kk], rs) : x[kk], w[kk], acc);
+  return acc;
+}
 
 // The FP16-pair operand of src [rows][cols] (rows padded to rows_pad, a
 // multiple of 4; cols to cols_pad, a multiple of 32), one workgroup per 4
 // rows:
 //  - exps[row] = the pair exponent of fl(src[row] * row_scale[row]) (of
-//    src[row] without a row scale), kPairMinExp for padding rows: a wave per
+//    src[row] without a row scale), plus kPairNonfinite if one of those
+//    values is an infinity or NaN, kPairMinExp for padding rows: a wave per
 //    row;
 //  - two FP16 planes (hi, lo) of those values scaled by 2^(15 - exps[row]),
 //    zero past rows and cols, stage-major: plane p, 16-k stage s, row r at
@@ -944,6 +963,7 @@ __global__ __launch_bounds__(256) void pair_rows_kernel(const float *__restrict_
   {
     const int row = r0 + wave;
     float m = 0.0f;
+    bool nonfinite = false;
     if (row < rows) {
       const float *r = src + static_cast<size_t>(row) * cols;
       const float sc = row_scale ? row_scale[row] : 1.0f;
@@ -962,18 +982,24 @@ __global__ __launch_bounds__(256) void pair_rows_kernel(const float *__restrict_
             const float v2 = row_scale ? f[u].z * sc : f[u].z, v3 = row_scale ? f[u].w * sc : f[u].w;
             m = __builtin_fmaxf(m, __builtin_fmaxf(__builtin_fmaxf(finite_abs(v0), finite_abs(v1)),
                                                    __builtin_fmaxf(finite_abs(v2), finite_abs(v3))));
+            nonfinite |= !(is_finite(v0) && is_finite(v1) && is_finite(v2) && is_finite(v3));
           }
         }
       } else {
-        for (int c = lane; c < cols; c += 64) m = __builtin_fmaxf(m, finite_abs(row_scale ? r[c] * sc : r[c]));
+        for (int c = lane; c < cols; c += 64) {
+          const float v = row_scale ? r[c] * sc : r[c];
+          m = __builtin_fmaxf(m, finite_abs(v));
+          nonfinite |= !is_finite(v);
+        }
       }
     }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, off));
+    const bool flag = __builtin_amdgcn_ballot_w64(nonfinite) != 0;
     if (lane == 0) {
       const int e = pair_exp(m);
       row_exp[wave] = e;
-      exps[row] = e;
+      exps[row] = flag ? e + kPairNonfinite : e;
     }
   }
   __syncthreads();
@@ -1083,8 +1109,11 @@ __global__ __launch_bounds__(256) void split_kernel(GemmArgs a, const uint16_t *
   constexpr int RS = 2 * AS + 2 * 256;  // slots of one ring entry
   __shared__ uint4 ring0[RS], ring1[RS], ring2[RS];
   __shared__ int tile_exp[2][kSplitBN];
+  __shared__ bool tile_bad[2][kSplitBN];
+  __shared__ int tile_any;  // a flagged row or column in the tile
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
+  if (tid == 0) tile_any = 0;  // the main loop's barriers order it before the epilogue's writes
   int rt, ct;
   split_tile(blockIdx.x, row_tiles, col_tiles, rt, ct);
   const int m0 = a.row0 + rt * BM, n0 = ct * kSplitBN;
@@ -1190,29 +1219,58 @@ __global__ __launch_bounds__(256) void split_kernel(GemmArgs a, const uint16_t *
   }
   products(fa1, fb1);
   // The tile's row and column exponents (the planes are padded to whole
-  // 128-row tiles, and so are the exponent arrays).
-  if (tid < BM)
-    tile_exp[0][tid] = aexp[m0 + tid];
-  else if (tid >= 128)
-    tile_exp[1][tid - 128] = bexp[n0 + tid - 128];
+  // 128-row tiles, and so are the exponent arrays) and non-finite flags.
+  if (tid < BM || tid >= 128) {
+    const int o = tid < BM ? 0 : 1, t = tid & 127;
+    const int e = o == 0 ? aexp[m0 + t] : bexp[n0 + t];
+    const bool bad = e >= kPairNonfinite / 2;
+    tile_exp[o][t] = bad ? e - kPairNonfinite : e;
+    tile_bad[o][t] = bad;
+    if (bad) tile_any = 1;
+  }
   // The repeated copies must land before the workgroup's LDS is released.
   __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
   __syncthreads();
   // D layout of 32x32: column = lane % 32, row = 8 (r / 4) + 4 (lane / 32) + r % 4.
+  // With CHECKED, outputs a flagged row or column reaches (for Glu, either
+  // column of the pair) are left to the pass below.
+  auto store = [&](auto checked) __attribute__((always_inline)) {
+    constexpr bool CHECKED = decltype(checked)::value;
 #pragma unroll
-  for (int i = 0; i < IB; i++)
+    for (int i = 0; i < IB; i++)
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
-      const int lc = wn * 64 + j * 32 + l32;
-      const int ce = tile_exp[1][lc] - 30;
+      for (int j = 0; j < 2; j++) {
+        const int lc = wn * 64 + j * 32 + l32;
+        const int ce = tile_exp[1][lc] - 30;
+        const bool bad_col = CHECKED && (tile_bad[1][lc] || (EPI == FOCR_EPI_GLU && tile_bad[1][lc ^ 1]));
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int lr = wm * 32 * IB + i * 32 + 8 * (r / 4) + 4 * h + (r % 4);
-        const float v = __builtin_ldexpf(acc[i][j][r], tile_exp[0][lr] + ce);
-        const float partner = EPI == FOCR_EPI_GLU ? __shfl_xor(v, 1) : 0.0f;
-        emit<EPI>(a, m0 + lr, n0 + lc, v, partner);
+        for (int r = 0; r < 16; r++) {
+          const int lr = wm * 32 * IB + i * 32 + 8 * (r / 4) + 4 * h + (r % 4);
+          const float v = __builtin_ldexpf(acc[i][j][r], tile_exp[0][lr] + ce);
+          const float partner = EPI == FOCR_EPI_GLU ? __shfl_xor(v, 1) : 0.0f;
+          if (!CHECKED || !(bad_col || tile_bad[0][lr])) emit<EPI>(a, m0 + lr, n0 + lc, v, partner);
+        }
       }
+  };
+  if (tile_any == 0) {
+    store(std::false_type{});
+  } else {
+    store(std::true_type{});
+    // The flagged outputs (Glu: column pairs) by the FP32 chain. Thread t
+    // takes outputs u = (idx * 40503) mod N for idx = t, t + 256, ...: a
+    // bijection of the tile's N outputs that spreads a flagged row's or
+    // column's outputs over the workgroup.
+    constexpr int W = EPI == FOCR_EPI_GLU ? kSplitBN / 2 : kSplitBN, N = BM * W;
+    for (int idx = tid; idx < N; idx += 256) {
+      const int u = static_cast<int>((static_cast<unsigned>(idx) * 40503u) & (N - 1));
+      const int lr = u / W, lc = (u % W) * (EPI == FOCR_EPI_GLU ? 2 : 1);
+      const int row = m0 + lr, col = n0 + lc;
+      const bool hit = tile_bad[0][lr] || tile_bad[1][lc] || (EPI == FOCR_EPI_GLU && tile_bad[1][lc + 1]);
+      if (!hit || row >= a.m || col >= a.n) continue;
+      const float v = chain_output(a, row, col);
+      emit<EPI>(a, row, col, v, EPI == FOCR_EPI_GLU ? chain_output(a, row, col + 1) : 0.0f);
     }
+  }
 }
 
 // The row exponents and FP16-pair planes of src [r][c] (rows padded to

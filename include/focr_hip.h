@@ -59,7 +59,9 @@ extern "C" {
                                  pairs (hi + lo), three pair products per FP32
                                  product on the FP16 matrix cores, FP32
                                  accumulation, exact descale (tolerance-matched
-                                 like FOCR_PROJ_F32_MFMA) */
+                                 like FOCR_PROJ_F32_MFMA); outputs a row holding
+                                 an infinity or NaN reaches are the FP32 panel
+                                 chain's, bitwise */
 
 /* Prefill softmax (src/config.rs PrefillSoftmax) and exp (ExpMode). */
 #define FOCR_SOFTMAX_ONLINE 0

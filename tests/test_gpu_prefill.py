@@ -338,26 +338,71 @@ def test_f32_chain_and_mfma_nonfinite_rows(fh):
     assert np.all(np.abs(got[fin].astype(np.float64) - want[fin]) <= 2 * k * EPS * mag[fin] + 1e-30)
 
 
-def test_f32_split_nonfinite_rows_stay_nonfinite_and_codes_are_refused(fh):
-    # An infinite or NaN input reaches every output of its row as a
-    # non-finite value (an infinity times a zero part is NaN where the FP32
-    # panels give the infinity); the other rows are unaffected.
-    m, k, n = 20, 256, 64
+def test_f32_split_nonfinite_rows_are_the_panels_and_codes_are_refused(fh):
+    # A row of A' or of W holding an infinity or NaN cannot go through the
+    # FP16 pairs (inf * 0 = NaN against a zero half): every output it reaches
+    # is the reference's FP32 chain, bitwise the panels (their NaN and
+    # signed infinities), through Store, Glu and Add, with a row scale that
+    # overflows a finite input to an infinity; the other outputs within the
+    # FP32 tolerance and the tiles' other rows unaffected.
+    m, k, n = 150, 256, 192
     a = gen.matrix(m * k, 23).reshape(m, k)
     a[3, 17] = np.inf
+    a[4, 2], a[4, 9] = np.inf, -np.inf
     a[7, 5] = np.nan
+    a[140, 100] = np.float32(3e38)  # times the row scale 4: an infinity in A'
     w = gen.matrix(n * k, 24).reshape(n, k)
+    w[::3, 17] = 0.0
+    w[11, 30] = np.nan
+    w[64, 200] = -np.inf
+    w[130, 0] = np.inf
+    rs = np.ones(m, np.float32)
+    rs[140] = 4.0
     lin = fh.Linear.from_f32(w)
-    got = run_prefill(fh, lin, a, m, None, fh.Epilogue.STORE, fh.PrefillProjection.F32_SPLIT)
-    assert not np.any(np.isfinite(got[3])) and np.all(np.isnan(got[7]))
-    keep = [r for r in range(m) if r not in (3, 7)]
-    want = oracle.panel_gemm(a[keep], len(keep), k, w, n)
-    assert max_rel(got[keep], want) <= 1e-5
-    codes, scales = oracle.quantize_bits(w, n, k, 64, 8)
+    S = fh.PrefillProjection.F32_SPLIT
+    bad_rows, bad_cols = [3, 4, 7, 140], [11, 64, 130]
+    keep_r = [r for r in range(m) if r not in bad_rows]
+    keep_c = [c for c in range(n) if c not in bad_cols]
+    base = ((np.arange(m * n) % 17).astype(np.float32) - F32(8.0)).reshape(m, n)
+    for epi, o_epi in ((fh.Epilogue.STORE, oracle.STORE), (fh.Epilogue.GLU, oracle.GLU), (fh.Epilogue.ADD, oracle.ADD)):
+        got = run_prefill(fh, lin, a, m, rs, epi, S, base=base if o_epi == oracle.ADD else None)
+        want = oracle.panel_gemm(a, m, k, w, n, row_scale=rs, epilogue=o_epi, out=base if o_epi == oracle.ADD else None)
+        cols = keep_c if o_epi != oracle.GLU else [c for c in range(n // 2) if 2 * c not in bad_cols and 2 * c + 1 not in bad_cols]
+        hit = np.ones(got.shape, bool)
+        hit[np.ix_(keep_r, cols)] = False
+        assert_bitwise(got[hit], want[hit], f"flagged outputs {epi.name}")
+        assert not np.all(np.isfinite(want[hit]))
+        assert max_rel(got[np.ix_(keep_r, cols)], want[np.ix_(keep_r, cols)]) <= 1e-5, epi.name
+    codes, scales = oracle.quantize_bits(np.nan_to_num(w, posinf=0.0, neginf=0.0), n, k, 64, 8)
     q = fh.QuantLinear(8, codes, scales, 64)
     with pytest.raises(fh.FocrError) as e:
-        run_prefill(fh, q, a, m, None, fh.Epilogue.STORE, fh.PrefillProjection.F32_SPLIT)
+        run_prefill(fh, q, a, m, None, fh.Epilogue.STORE, S)
     assert e.value.code == fh.FOCR_E_UNSUPPORTED
+
+
+def test_f32_split_nonfinite_rows_in_128_row_tiles(fh):
+    # Enough tiles for the 128-row kernel: the flagged row and column are
+    # the panels' bitwise, and every other output is bitwise the call on the
+    # same inputs with the non-finite values replaced by zeros.
+    m, k, n = 6544, 256, 1280
+    a = gen.normal((m, k), 1.0, 27)
+    w = gen.normal((n, k), 0.02, 28)
+    bad_a, bad_w = a.copy(), w.copy()
+    bad_a[5000, 33] = np.inf
+    bad_a[77, 250] = np.nan
+    bad_w[700, 3] = -np.inf
+    S = fh.PrefillProjection.F32_SPLIT
+    got = run_prefill(fh, fh.Linear.from_f32(bad_w), bad_a, m, None, fh.Epilogue.STORE, S)
+    clean = run_prefill(fh, fh.Linear.from_f32(np.nan_to_num(bad_w, neginf=0.0)), np.nan_to_num(bad_a, nan=0.0, posinf=0.0),
+                        m, None, fh.Epilogue.STORE, S)
+    keep = np.ones((m, n), bool)
+    keep[[77, 5000], :] = False
+    keep[:, 700] = False
+    assert np.array_equal(got[keep].view(np.uint32), clean[keep].view(np.uint32))
+    for r in (77, 5000):
+        assert_bitwise(got[r], oracle.panel_gemm(bad_a[r:r + 1], 1, k, bad_w, n)[0], f"row {r}")
+    assert_bitwise(got[:, 700], oracle.panel_gemm(bad_a, m, k, bad_w[700:701], 1)[:, 0], "column 700")
+    assert not np.any(np.isfinite(got[:, 700])) and not np.any(np.isfinite(got[5000]))
 
 
 @pytest.mark.parametrize("bits", [16, 8])

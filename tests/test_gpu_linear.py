@@ -242,3 +242,41 @@ def test_long_rows_refill_the_weight_window(fh, bits, k):
         want = oracle.linear_decode(bits, codes, scales, n, k, group, x[:rows], rows, exc_cols=[k - 3], exc_vals=vals)
         assert_bitwise(host(lin.linear(to_dev(x[:rows]), rows)), want, f"bits {bits} k {k} rows {rows}")
     lin.free()
+
+
+@pytest.mark.parametrize("bits", [8, 16])
+def test_subnormal_scales_and_activations(fh, bits):
+    # Rows of subnormal or tiny values quantize to subnormal group scales
+    # (quantize_bits floors a nonzero scale at the least subnormal,
+    # linear.rs:140-201) and a zero group to a zero scale: the dequantized
+    # weights, the decode GEMVs (plain and GLU, with subnormal activations)
+    # and the prefill projections on the codes (the exact-order chain; for
+    # 8-bit codes the INT16-activation panels) are bitwise the reference's.
+    n, k, group = 64, 768, 64
+    w = gen.values(n * k, 51).reshape(n, k)
+    w[3] *= np.float32(1e-40)
+    w[4, :64] = 0.0
+    w[5, 64:128] *= np.float32(1e-38)
+    w[6] *= np.float32(2.0 ** -140)
+    codes, scales = oracle.quantize_bits(w, n, k, group, bits)
+    sc = np.asarray(scales)
+    assert np.any((sc > 0) & (sc < 2.0 ** -126)) and np.any(sc == 0)
+    lin = fh.QuantLinear(bits, codes, scales, group)
+    dense = oracle.dequantize(bits, codes, scales, n, k, group)
+    assert_bitwise(host(lin.dequantize()), dense, "dequant")
+    for rows in (1, 5, 8):
+        x = gen.values(rows * k, 53 + rows)
+        x[::7] *= np.float32(1e-39)
+        assert_bitwise(host(lin.linear(to_dev(x), rows)), oracle.linear_decode(bits, codes, scales, n, k, group, x, rows),
+                       f"decode rows {rows}")
+        assert_bitwise(host(lin.linear_glu(to_dev(x), rows)),
+                       oracle.linear_decode_glu(bits, codes, scales, n, k, group, x, rows), f"glu rows {rows}")
+    m = 37
+    a = gen.normal((m, k), 1.0, 57)
+    a[3] *= np.float32(1e-39)
+    a[9, ::5] = np.float32(2.0 ** -149)
+    got = host(lin.prefill(to_dev(a), m, kernel=fh.PrefillProjection.F32_CHAIN))
+    assert_bitwise(got, oracle.panel_gemm(a, m, k, dense, n), "chain on codes")
+    if bits == 8:
+        got = host(lin.prefill(to_dev(a), m, kernel=fh.PrefillProjection.I16))
+        assert_bitwise(got, oracle.i16_gemm(a, m, k, codes, scales, n), "INT16 panels")

@@ -60,6 +60,35 @@ def test_seal_and_append_are_bitwise_the_oracle(fh, bits, prefix_len):
     kv.free()
 
 
+@pytest.mark.parametrize("bits", [8, 16])
+def test_tiny_subnormal_and_zero_blocks_are_bitwise_the_oracle(fh, bits):
+    # Positions and tail blocks scaled into the tiny-normal and subnormal
+    # range, and zero ones: their steps (floored at the least subnormal, 0
+    # for a zero block) and codes are the oracle's: the decoded records are
+    # bitwise.
+    P = 70
+    k, v = pair_cache(P, N_KV, 31, 2.0)
+    for p, f in ((3, 1e-39), (4, 2.0 ** -140), (5, 0.0), (6, 1e-37), (50, 2.0 ** -149)):
+        k[p] *= np.float32(f)
+        v[p] *= np.float32(f)
+    cap = P + 6
+    tk = gen.normal((6, N_KV, 64), 1.5, 32)
+    tv = gen.normal((6, N_KV, 64), 1.5, 33)
+    tk[1] *= np.float32(1e-40)
+    tv[2, 3] *= np.float32(2.0 ** -135)
+    tk[4, 5] = 0.0
+    tv[5] = 0.0
+    kv = fh.KvSplit.seal(bits, to_dev(k), to_dev(v), P, cap, N_HEADS, N_KV)
+    kv.append(to_dev(tk), to_dev(tv), 6)
+    pk, vals, gk = (host(t) for t in kv.dequantize())
+    wpk, wvals, wgk = oracle_cache(bits, k, v, P, tk, tv, cap)
+    assert_bitwise(pk, wpk, "prefix keys")
+    assert_bitwise(vals, wvals, "values")
+    assert_bitwise(gk, wgk, "generated keys")
+    assert np.any((wvals != 0) & (np.abs(wvals) < 2.0 ** -126)) and np.all(wvals[5] == 0)
+    kv.free()
+
+
 def test_refusals(fh):
     P = 6
     k, v = pair_cache(P, N_KV, 21)

@@ -27,6 +27,28 @@ def test_row_scales_bitwise(fh, width):
     assert_bitwise(got, oracle.row_scales(h, width), f"width {width}")
 
 
+def test_row_scales_extreme_rows(fh):
+    # Rows whose squares underflow (subnormal and tiny values: the sum stays
+    # at or near 0 and the scale at 1 / sqrt(eps)), overflow (|x| ~ 1e20: an
+    # infinite sum, scale 0), a zero row, NaN and infinities: bitwise the
+    # reference's sum_squares_pairwise and rms_scale (mod.rs:531-553).
+    width = 768
+    rows = [gen.values(width, 61 + r) for r in range(10)]
+    rows[0] *= np.float32(1e-39)
+    rows[1] *= np.float32(1e-20)
+    rows[2] *= np.float32(1e20)
+    rows[3][:] = 0.0
+    rows[4][100] = np.nan
+    rows[5][7] = np.inf
+    rows[6][:] = np.float32(2.0 ** -149)
+    rows[7] *= np.float32(3e-23)
+    rows[8][::3] = np.float32(1.8e19)
+    h = np.concatenate(rows).astype(np.float32)
+    want = oracle.row_scales(h, width)
+    assert want[3] == want[0] and want[2] == 0.0 and np.isnan(want[4]) and want[5] == 0.0
+    assert_bitwise(host(fh.row_scales(to_dev(h), width)), want, "extreme rows")
+
+
 def test_row_scales_full_prefill(fh):
     m, width = 6544, 768
     h = gen.normal((m, width), 1.0, 30)

@@ -307,12 +307,14 @@ def test_f32_chain_and_mfma_zero_tiny_and_subnormal_rows(fh):
     assert np.all(d <= bound), float(np.max((d - bound) / np.maximum(mag, 1e-300)))
 
 
-def test_f32_chain_and_mfma_nonfinite_rows(fh):
+@pytest.mark.parametrize("bits", [32, 16, 8])
+def test_f32_chain_and_mfma_nonfinite_rows(fh, bits):
     # Infinite and NaN inputs: the exact-order chain bitwise the reference's
     # panels (Store and Glu); the FP32 matrix cores with the panels' NaN and
     # signed-infinity pattern (an infinity meets a zero weight as NaN, and
     # opposite infinities cancel to NaN, in any order) and their finite
-    # values within the FP32 tolerance.
+    # values within the FP32 tolerance; FP32 weights and code weights
+    # (fl(code * scale) formed in the kernels).
     m, k, n = 20, 256, 64
     a = gen.matrix(m * k, 25).reshape(m, k)
     a[3, 17] = np.inf
@@ -321,8 +323,13 @@ def test_f32_chain_and_mfma_nonfinite_rows(fh):
     a[7, 5] = np.nan
     w = gen.matrix(n * k, 26).reshape(n, k)
     w[::3, 17] = 0.0
-    w[:, 40] = np.abs(w[:, 40])
-    lin = fh.Linear.from_f32(w)
+    w[:, 40] = np.abs(w[:, 40]) + np.float32(0.5)
+    if bits == 32:
+        lin = fh.Linear.from_f32(w)
+    else:
+        codes, scales = oracle.quantize_bits(w, n, k, 64, bits)
+        lin = fh.QuantLinear(bits, codes, scales, 64)
+        w = oracle.dequantize(bits, codes, scales, n, k, 64)
     want = oracle.panel_gemm(a, m, k, w, n)
     assert np.any(np.isnan(want[3])) and np.any(np.isinf(want[3])) and np.all(np.isinf(want[6]) & (want[6] < 0))
     chain = run_prefill(fh, lin, a, m, None, fh.Epilogue.STORE, fh.PrefillProjection.F32_CHAIN)
